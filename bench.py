@@ -1,0 +1,345 @@
+"""Benchmark of the DeepSeek-V4.1 sparse-attention hot path on one MI355X.
+
+Workload (BASELINE metric "sparse-MLA decode tokens/s + HBM GB/s (% peak), bs32 64K ctx;
+prefill TFLOP/s"): one decode step of one compressing attention layer at batch 32 and
+65,536 tokens of context, i.e. 16,384 compressed entries per sequence (ratio 4), top-512,
+64 heads x 512 (64-channel rope tail), indexer 64 heads x 128, window 128, bf16. A step is
+indexer scoring of all 16,384 entries (MFMA) -> top-k -> sparse MLA over the 128 window
+rows + 512 selected rows (+ inverse rope). Inputs are seeded synthetic tensors resident in
+HBM; NSETS independent input sets (> 512 MB in total) rotate so the 256 MB Infinity Cache
+cannot serve the streamed caches. Steps are replayed from HIP graphs (one graph holds one
+step per input set), bracketed by events on the launch stream.
+
+Secondary: C3 prefill (8,192-token chunk after 32,768 tokens, top-2,048) indexer and sparse
+MLA TFLOP/s, and the CPU oracle (numpy) timed on a bounded sample of the decode workload.
+
+    python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "deepseek-v41-mlx_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "sparse-MLA decode tokens/s + HBM GB/s (% peak), bs32 64K ctx; prefill TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+SEED = 20261201
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--batch", type=int, default=32)
+    p.add_argument("--ctx", type=int, default=65536)
+    p.add_argument("--sets", type=int, default=4)
+    p.add_argument("--no-prefill", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    return p.parse_args()
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Shape:
+    def __init__(self, batch, ctx):
+        self.B, self.H, self.D, self.rd = batch, 64, 512, 64
+        self.Hi, self.Di, self.W, self.K, self.r = 64, 128, 128, 512, 4
+        self.start = ctx                      # decoding the token at position ctx
+        self.nb = (ctx + 1) // self.r         # visible compressed entries
+        self.wp = min(self.start, self.W)
+        self.rows = min(self.W, self.wp + 1) + min(self.K, self.nb)
+
+    def bytes_indexer(self):
+        return self.B * (self.nb * self.Di * 2 + self.Hi * self.Di * 2 + self.Hi * 2 + self.nb * 4)
+
+    def bytes_topk(self):
+        return self.B * (self.nb * 4 + self.K * 4)
+
+    def bytes_sparse(self):
+        return self.B * (self.rows * self.D * 2 + 2 * self.H * self.D * 2 + self.K * 4)
+
+    def flops_indexer(self):
+        return 2 * self.B * self.Hi * self.Di * self.nb
+
+    def flops_sparse(self):
+        return 4 * self.B * self.H * self.rows * self.D
+
+
+def make_set(s: Shape, seed, device):
+    """One input set: caches and queries N(0,1)/sqrt(576), fp4-grid index keys/queries, bf16."""
+    import torch
+    g = torch.Generator(device=device).manual_seed(seed)
+    bf = torch.bfloat16
+    sc = 576 ** -0.5
+
+    def fp4ish(*shape):
+        # values on the fp4 e2m1 grid times a power of two: what the index caches hold
+        grid = torch.tensor([0, .5, 1, 1.5, 2, 3, 4, 6, 0, -.5, -1, -1.5, -2, -3, -4, -6], device=device)
+        return (grid[torch.randint(0, 16, shape, generator=g, device=device)] * 0.25).to(bf)
+
+    return dict(
+        q=(torch.randn(s.B, 1, s.H, s.D, generator=g, device=device) * sc).to(bf),
+        win=(torch.randn(s.B, s.W, s.D, generator=g, device=device) * sc).to(bf),
+        chunk=(torch.randn(s.B, 1, s.D, generator=g, device=device) * sc).to(bf),
+        comp=(torch.randn(s.B, s.nb, s.D, generator=g, device=device) * sc).to(bf),
+        iq=fp4ish(s.B, 1, s.Hi, s.Di),
+        ik=fp4ish(s.B, s.nb, s.Di),
+        w=torch.randn(s.B, 1, s.Hi, generator=g, device=device).to(bf),
+        sink=torch.randn(s.H, generator=g, device=device),
+    )
+
+
+def graph_of(fn, reps_sets, torch):
+    """Capture fn(set) for every set in order into one graph (after one eager warm call each)."""
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        for d in reps_sets:
+            fn(d)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for d in reps_sets:
+            fn(d)
+    torch.cuda.synchronize()
+    return gr
+
+
+def time_graph(gr, reps, torch):
+    """Average ms per replay over `reps` replays, events on the current stream."""
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def run_decode(args, torch, device):
+    from dsv41 import _abi
+    from dsv41.indexer import weight_scale
+    from dsv41.layers import precompute_freqs_cis
+    from dsv41.step import SparseDecodeStep
+
+    s = Shape(args.batch, args.ctx)
+    log(f"[bench] decode B={s.B} ctx={args.ctx} nb={s.nb} K={s.K} sets={args.sets}")
+    sets = [make_set(s, SEED + i, device) for i in range(args.sets)]
+    cos, sin = precompute_freqs_cis(s.rd, s.start + 1, 65536, 160000.0, 16.0, 32, 1, device=device)
+    steps = [SparseDecodeStep(s.B, s.H, s.D, s.rd, s.Hi, s.Di, s.nb, s.K, s.W, s.start, s.r,
+                              torch.bfloat16, device) for _ in sets]
+    ws = weight_scale(s.Hi, s.Di, torch.bfloat16)
+    for d, st in zip(sets, steps):
+        d["step"] = st
+
+    def full(d):
+        d["step"](d["q"], d["iq"], d["w"], ws, d["ik"], d["comp"], d["win"], d["chunk"], d["sink"], cos, sin)
+
+    def only_indexer(d):
+        _abi.indexer_score(d["iq"], d["w"], ws, d["ik"], s.start, s.r, None, out=d["step"].scores)
+
+    def only_topk(d):
+        d["idx"] = _abi.topk_select(d["step"].scores, s.K, s.start, s.r, s.wp + 1)
+
+    def only_sparse(d):
+        _abi.sparse_mla(d["q"], d["win"], d["chunk"], d["comp"], s.nb, d["sink"], d["idx"], s.D ** -0.5, s.W,
+                        s.start, cos, sin, s.rd, out=d["step"].out, workspace=d["step"].workspace)
+
+    g_full = graph_of(full, sets, torch)
+    per_replay = len(sets)
+    warm = max(1, args.warmup // per_replay)
+    reps = max(1, args.steps // per_replay)
+    for _ in range(warm):
+        g_full.replay()
+    ms = time_graph(g_full, reps, torch) / per_replay
+    log(f"[bench] decode step {ms * 1e3:.2f} us")
+
+    # per-kernel averages (each kernel alone, same rotation, graph-replayed)
+    for d in sets:
+        only_indexer(d)
+        only_topk(d)
+    kern, graphs = {}, [g_full]
+    for name, fn in (("indexer_score", only_indexer), ("topk_select", only_topk), ("sparse_mla", only_sparse)):
+        gr = graph_of(fn, sets, torch)
+        graphs.append(gr)        # keeps graph-pool outputs (d["idx"]) alive
+        gr.replay()
+        kern[name] = time_graph(gr, reps, torch) / per_replay
+        log(f"[bench] {name} {kern[name] * 1e3:.2f} us")
+    torch.cuda.synchronize()
+    return s, ms, kern, sets, cos, sin, ws, graphs
+
+
+def run_prefill(torch, device):
+    """C3: B=1, 8,192-token chunk after 32,768 prior tokens, top-2,048, 64 heads x 512."""
+    from dsv41 import _abi
+    from dsv41.indexer import weight_scale
+    from dsv41.layers import precompute_freqs_cis
+
+    B, n, prior, H, D, rd, Hi, Di, W, K, r = 1, 8192, 32768, 64, 512, 64, 64, 128, 128, 2048, 4
+    end = prior + n
+    nb = end // r
+    log(f"[bench] prefill n={n} prior={prior} nb={nb} K={K}")
+    g = torch.Generator(device=device).manual_seed(SEED + 100)
+    bf = torch.bfloat16
+    q = torch.randn(B, n, H, D, generator=g, device=device).to(bf)
+    chunk = torch.randn(B, n, D, generator=g, device=device).to(bf)
+    win = torch.randn(B, W, D, generator=g, device=device).to(bf)
+    comp = torch.randn(B, nb, D, generator=g, device=device).to(bf)
+    iq = torch.randn(B, n, Hi, Di, generator=g, device=device).to(bf)
+    ik = torch.randn(B, nb, Di, generator=g, device=device).to(bf)
+    w = torch.randn(B, n, Hi, generator=g, device=device).to(bf)
+    sink = torch.randn(H, generator=g, device=device)
+    cos, sin = precompute_freqs_cis(rd, end, 65536, 160000.0, 16.0, 32, 1, device=device)
+    ws = weight_scale(Hi, Di, bf)
+    scores = torch.empty(B, n, nb, dtype=torch.float32, device=device)
+    out = torch.empty_like(q)
+    lens = (prior + torch.arange(n) + 1) // r
+    vis = int(lens.sum())
+    idx_holder = {}
+
+    def f_idx():
+        _abi.indexer_score(iq, w, ws, ik, prior, r, None, out=scores)
+
+    def f_topk():
+        idx_holder["idx"] = _abi.topk_select(scores, K, prior, r, W + n)
+
+    def f_sparse():
+        _abi.sparse_mla(q, win, chunk, comp, nb, sink, idx_holder["idx"], D ** -0.5, W, prior, cos, sin, rd,
+                        out=out)
+
+    res = {}
+    for name, fn in (("indexer_score", f_idx), ("topk_select", f_topk), ("sparse_mla", f_sparse)):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 3
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) / reps
+        log(f"[bench] prefill {name} {res[name]:.3f} ms")
+    rows_sparse = min(W, W + n) + K   # window rows listed per query (<= W valid) + top-k
+    fl_idx = 2.0 * Hi * Di * vis
+    fl_sparse = 4.0 * n * H * (W + K) * D
+    return {
+        "workload": "C3 chunked prefill: B=1, 8192-token chunk after 32768 tokens, nb=10240, top-2048",
+        "indexer_ms": res["indexer_score"], "topk_ms": res["topk_select"], "sparse_ms": res["sparse_mla"],
+        "indexer_TFLOPs": fl_idx / res["indexer_score"] / 1e9,
+        "sparse_TFLOPs": fl_sparse / res["sparse_mla"] / 1e9,
+        "indexer_mfma_frac": fl_idx / res["indexer_score"] / 1e9 / BF16_PEAK_TFLOPS,
+        "sparse_mfma_frac": fl_sparse / res["sparse_mla"] / 1e9 / BF16_PEAK_TFLOPS,
+        "flops_note": f"indexer 2*Hi*Di*sum(lens)={fl_idx:.3e} (causal), sparse 4*n*H*(W+K)*D={fl_sparse:.3e}",
+        "rows_per_query": rows_sparse,
+    }
+
+
+def cpu_baseline(s: Shape, sets, cos, sin, ws, seconds, torch):
+    """The numpy oracle on whole batch rows of the same decode workload, until `seconds` pass."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+
+    from oracle import cpu_ref as R
+
+    d = sets[0]
+    f = lambda t: t.float().cpu().numpy()  # noqa: E731
+    lens = R.query_lens(s.start, 1, s.r)
+    wslots = (s.start - s.wp + np.arange(s.wp)) % s.W
+    widx = R.window_idx_matrix(s.wp, 1, s.W)[None]
+    rc = f(cos[s.start:s.start + 1])
+    rsn = f(sin[s.start:s.start + 1])
+    sink = f(d["sink"])
+    rows, el = 0, 0.0
+    while el < seconds:
+        b = rows % s.B            # device->host copy of the row is outside the timed part
+        iq, ik, w = f(d["iq"][b:b + 1]), f(d["ik"][b:b + 1]), f(d["w"][b:b + 1])
+        q, win, chunk, comp = f(d["q"][b:b + 1]), f(d["win"][b:b + 1]), f(d["chunk"][b:b + 1]), f(d["comp"][b:b + 1])
+        t0 = time.perf_counter()
+        sc = R.indexer_scores(iq, ik, R.cast(w * np.float32(ws), "bf16"), s.start, s.r)
+        idx = R.topk_indices(sc, s.K, lens, s.wp + 1)
+        kv_all = np.concatenate([win[:, wslots], chunk, comp], axis=1)
+        o = R.sparse_attn(q, kv_all, sink, np.concatenate([widx, idx], -1), s.D ** -0.5, dtype="bf16")
+        R.rope_tail(o, s.rd, rc, rsn, inverse=True, dtype="bf16")
+        el += time.perf_counter() - t0
+        rows += 1
+    threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    return {"value": rows / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} batch rows of the bs32/64K decode step (indexer + top-k + sparse MLA + inverse rope), "
+                      f"numpy float32 oracle, BLAS threads {threads}, host cpu_count {os.cpu_count()}, "
+                      f"{el:.1f} s of compute (row copies to the host untimed)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the hot path is "
+              "batch-sharded with zero exchange, so N GPUs run N independent copies)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    device = torch.device("cuda:0")
+    from dsv41 import _abi
+    _abi.lib()
+
+    s, ms, kern, sets, cos, sin, ws, _graphs = run_decode(args, torch, device)
+    step_bytes = s.bytes_indexer() + s.bytes_topk() + s.bytes_sparse()
+    step_gbs = step_bytes / (ms * 1e-3) / 1e9
+    idx_gbs = s.bytes_indexer() / (kern["indexer_score"] * 1e-3) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": s.B / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": max(1, args.steps // len(sets)) * len(sets),
+        "warmup": max(1, args.warmup // len(sets)) * len(sets),
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "sparse-MLA decode step of one compressing layer: indexer scoring + top-k + "
+                               "sparse MLA (+inverse rope), bs32, 64K context",
+                   "batch": s.B, "context": args.ctx, "compressed_entries": s.nb, "index_topk": s.K,
+                   "heads": s.H, "head_dim": s.D, "rope_dim": s.rd, "index_heads": s.Hi, "index_dim": s.Di,
+                   "window": s.W, "input_sets": len(sets)},
+        "hbm_GBps_step": step_gbs,
+        "hbm_frac_step": step_gbs / HBM_PEAK_GBS,
+        "step_algorithmic_bytes": step_bytes,
+        "kernels_us": {k: v * 1e3 for k, v in kern.items()},
+        "roofline": {"bound": "hbm", "kernel": "indexer_score (dsv41_indexer_score, bf16 MFMA)",
+                     "achieved": idx_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": idx_gbs / HBM_PEAK_GBS,
+                     "traffic": None,
+                     "bytes_per_launch": s.bytes_indexer(), "avg_launch_us": kern["indexer_score"] * 1e3},
+    }
+    if not args.no_prefill:
+        try:
+            result["prefill"] = run_prefill(torch, device)
+        except Exception as e:  # report, do not hide: the decode line still prints
+            result["prefill"] = {"error": repr(e)}
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(s, sets, cos, sin, ws, args.cpu_seconds, torch)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,122 @@
+// Shared device helpers and host-side error plumbing for the dsv41 HIP kernels (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/dsv41.h"
+
+namespace dsv41 {
+
+// ------------------------------------------------------------------ host errors
+
+// Records a message for dsv41_last_error_string() and returns `code`.
+int set_error(int code, const char* fmt, ...);
+// Checks the launch that was just enqueued; returns 0 or the hipError_t.
+int check_launch(const char* what);
+
+#define DSV41_REQUIRE(cond, code, ...)                  \
+  do {                                                  \
+    if (!(cond)) return ::dsv41::set_error((code), __VA_ARGS__); \
+  } while (0)
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+// ------------------------------------------------------------------ numerics
+
+typedef uint16_t bf16_t;  // raw bfloat16 bits
+
+__device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// float -> bfloat16, round to nearest even (torch / MLX semantics).
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (bf16_t)0x7FC0u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf2f(f2bf(f)); }
+
+// Typed load/store: T = float or bf16_t; `rnd` rounds an fp32 value to T's precision.
+template <typename T> struct io;
+template <> struct io<float> {
+  __device__ __forceinline__ static float ld(const float* p) { return *p; }
+  __device__ __forceinline__ static void st(float* p, float v) { *p = v; }
+  __device__ __forceinline__ static float rnd(float v) { return v; }
+  static constexpr int kDtype = DSV41_F32;
+};
+template <> struct io<bf16_t> {
+  __device__ __forceinline__ static float ld(const bf16_t* p) { return bf2f(*p); }
+  __device__ __forceinline__ static void st(bf16_t* p, float v) { *p = f2bf(v); }
+  __device__ __forceinline__ static float rnd(float v) { return round_bf16(v); }
+  static constexpr int kDtype = DSV41_BF16;
+};
+
+// 2**ceil(log2(r)) from IEEE bits (the TileLang fast_round_scale, kernel.py:22-37).
+__device__ __forceinline__ float pow2_ceil_log2(float r) {
+  uint32_t b = __float_as_uint(r);
+  int e = (int)((b >> 23) & 0xFFu) - 127 + ((b & 0x7FFFFFu) != 0u);
+  return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+// Nearest OCP e4m3fn value, ties to even; |x| <= 448 expected (callers clip first).
+__device__ __forceinline__ float e4m3_round(float x) {
+  float a = fabsf(x);
+  float r;
+  if (a < 0.015625f) {  // below 2^-6: subnormal grid, quantum 2^-9
+    r = rintf(a * 512.0f) * (1.0f / 512.0f);
+  } else {              // 3 mantissa bits, round to nearest even at bit 20
+    uint32_t u = __float_as_uint(a);
+    u = (u + 0x7FFFFu + ((u >> 20) & 1u)) & ~0xFFFFFu;
+    r = __uint_as_float(u);
+  }
+  return copysignf(r, x);
+}
+
+// e4m3fn byte encoding of a value already on the e4m3 grid (|x| <= 448).
+__device__ __forceinline__ uint8_t e4m3_encode(float q) {
+  uint32_t s = (__float_as_uint(q) >> 31) << 7;
+  float a = fabsf(q);
+  if (a < 0.015625f) return (uint8_t)(s | (uint32_t)(a * 512.0f));
+  uint32_t u = __float_as_uint(a);
+  uint32_t e = ((u >> 23) & 0xFFu) - 127u + 7u;
+  return (uint8_t)(s | (e << 3) | ((u >> 20) & 7u));
+}
+
+__device__ __forceinline__ float e4m3_decode(uint8_t c) {
+  uint32_t e = (c >> 3) & 0xFu, m = c & 7u;
+  float a = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : (float)m * (1.0f / 512.0f);
+  return (c & 0x80u) ? -a : a;
+}
+
+// Nearest e2m1 magnitude with the reference's tie table (fakequant.py:65-73), sign kept.
+__device__ __forceinline__ float e2m1_round(float v) {
+  float m = fabsf(v);
+  float r = m > 5.0f    ? 6.0f
+            : m >= 3.5f  ? 4.0f
+            : m > 2.5f   ? 3.0f
+            : m >= 1.75f ? 2.0f
+            : m > 1.25f  ? 1.5f
+            : m >= 0.75f ? 1.0f
+            : m > 0.25f  ? 0.5f
+                         : 0.0f;
+  return copysignf(r, v);
+}
+
+// ------------------------------------------------------------------ wave helpers
+
+__device__ __forceinline__ float wave_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+__device__ __forceinline__ float group_max(float v, int width) {
+  for (int o = width >> 1; o > 0; o >>= 1) v = fmaxf(v, wave_xor_f(v, o));
+  return v;
+}
+__device__ __forceinline__ float group_sum(float v, int width) {
+  for (int o = width >> 1; o > 0; o >>= 1) v += wave_xor_f(v, o);
+  return v;
+}
+
+}  // namespace dsv41

@@ -1,0 +1,196 @@
+// Indexer scoring, deepseek_v41_mlx/indexer.py:183-198:
+//   S[b,s,t] = sum_h relu(q[b,s,h,:] . k[b,t,:]) * w[b,s,h],  t >= lens_s -> -inf,
+//   candidate-masked -> -inf, with w = round_dtype(w_raw * w_scale).
+//
+// bf16: one workgroup scores `rows_per_wg` cache rows of one query. The query's [heads x dim]
+// block is staged once in LDS and held by every wave as the MFMA A operand (heads = M); each
+// wave streams 16-row tiles of the owner's key cache straight from HBM as the B operand
+// (rows = N), two tiles in flight. Lane j ends with 4 heads x 1 row; ReLU * w and the in-lane
+// head sum run on the accumulators, two cross-lane adds finish the head reduction, and lanes
+// 0..15 store 16 consecutive fp32 scores. Rows past the query's visibility are written as
+// -inf without touching the cache (causal prefill skips about half the bytes).
+#include "mfma.h"
+
+namespace dsv41 {
+
+constexpr int kIdxThreads = 512;  // 8 waves
+
+template <int HT, int KS>
+__global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ w_raw, float w_scale,
+    const bf16_t* __restrict__ kcache, int64_t k_bstride, const uint8_t* __restrict__ cand,
+    float* __restrict__ scores, int n, int nb, int start_pos, int ratio, int rows_per_wg) {
+  constexpr int H = HT * 16;
+  constexpr int DIM = KS * 32;
+  constexpr int QUART = DIM / 4;           // dims owned by one lane group (k permutation)
+  constexpr int QROW = DIM * 2 + 16;       // padded LDS row stride in bytes
+  __shared__ __align__(16) uint8_t q_lds[H * QROW];
+
+  const int qi = blockIdx.y;               // b * n + s
+  const int b = qi / n, s = qi - (qi / n) * n;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int lens = (start_pos + s + 1) / ratio;
+  const int r0 = blockIdx.x * rows_per_wg;
+  const int r1 = min(r0 + rows_per_wg, nb);
+  const int vis_end = max(r0, min(r1, lens));
+  float* out = scores + (int64_t)qi * nb;
+  for (int t = vis_end + tid; t < r1; t += kIdxThreads) out[t] = -INFINITY;
+  if (vis_end <= r0) return;               // uniform: nothing visible in this row range
+
+  // stage q[b, s] ([H, DIM] bf16) into LDS
+  const bf16_t* qrow = q + (int64_t)qi * H * DIM;
+  for (int c = tid; c < H * DIM / 8; c += kIdxThreads) {
+    const int h = c / (DIM / 8), d8 = c - h * (DIM / 8);
+    *reinterpret_cast<uint4*>(q_lds + h * QROW + d8 * 16) = reinterpret_cast<const uint4*>(qrow)[c];
+  }
+  __syncthreads();
+
+  bf16x8 qa[HT][KS];
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qa[ht][ks] = ld_bf16x8(q_lds + (ht * 16 + l16) * QROW + (g * QUART + ks * 8) * 2);
+  float wv[HT][4];
+  const bf16_t* wrow = w_raw + (int64_t)qi * H;
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wrow[ht * 16 + 4 * g + i]) * w_scale);
+
+  const bf16_t* kb = kcache + (int64_t)b * k_bstride + g * QUART;
+  const uint8_t* cb = cand ? cand + (int64_t)qi * nb : nullptr;
+  constexpr int NW = kIdxThreads / 64;
+
+  // two 16-row tiles per iteration: loads for both are issued before either is consumed
+  for (int t0 = r0 + 32 * wave; t0 < vis_end; t0 += 32 * NW) {
+    bf16x8 kk[2][KS];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int row = min(t0 + 16 * u + l16, vis_end - 1);   // clamp: loads stay inside the cache
+      const bf16_t* kr = kb + (int64_t)row * DIM;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kk[u][ks] = ld_bf16x8(kr + ks * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int tb = t0 + 16 * u;
+      if (tb >= vis_end) break;
+      f32x4 acc[HT];
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) acc[ht] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) acc[ht] = mfma16x16x32(qa[ht][ks], kk[u][ks], acc[ht]);
+      float part = 0.0f;
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part += fmaxf(acc[ht][i], 0.0f) * wv[ht][i];
+      part += __shfl_xor(part, 16, 64);
+      part += __shfl_xor(part, 32, 64);
+      const int row = tb + l16;
+      if (g == 0 && row < vis_end) {
+        float v = part;
+        if (cb && !cb[row]) v = -INFINITY;
+        out[row] = v;
+      }
+    }
+  }
+}
+
+// fp32 path (parity configs): one thread per cache row, the query's q and w in LDS.
+__global__ __launch_bounds__(256) void indexer_score_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ w_raw, float w_scale, const float* __restrict__ kcache,
+    int64_t k_bstride, const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int heads, int dim,
+    int nb, int start_pos, int ratio) {
+  extern __shared__ float sm[];
+  float* qs = sm;                          // [heads, dim]
+  float* ws = sm + heads * dim;            // [heads]
+  const int qi = blockIdx.y;
+  const int b = qi / n, s = qi - (qi / n) * n;
+  const float* qrow = q + (int64_t)qi * heads * dim;
+  for (int i = threadIdx.x; i < heads * dim; i += 256) qs[i] = qrow[i];
+  for (int i = threadIdx.x; i < heads; i += 256) ws[i] = w_raw[(int64_t)qi * heads + i] * w_scale;
+  __syncthreads();
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= nb) return;
+  const int lens = (start_pos + s + 1) / ratio;
+  float v = -INFINITY;
+  if (t < lens) {
+    const float* kr = kcache + (int64_t)b * k_bstride + (int64_t)t * dim;
+    v = 0.0f;
+    for (int h = 0; h < heads; ++h) {
+      float dot = 0.0f;
+      for (int d = 0; d < dim; ++d) dot += qs[h * dim + d] * kr[d];
+      v += fmaxf(dot, 0.0f) * ws[h];
+    }
+    if (cand && !cand[(int64_t)qi * nb + t]) v = -INFINITY;
+  }
+  scores[(int64_t)qi * nb + t] = v;
+}
+
+template <int HT, int KS>
+static void launch_idx_bf16(dim3 grid, hipStream_t stream, const void* q, const void* w_raw, float w_scale,
+                            const void* index_k, int64_t k_bstride, const uint8_t* cand, float* scores, int n,
+                            int nb, int start_pos, int ratio, int rows_per_wg) {
+  hipLaunchKernelGGL((indexer_score_bf16_kernel<HT, KS>), grid, dim3(kIdxThreads), 0, stream,
+                     (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, (const bf16_t*)index_k, k_bstride, cand,
+                     scores, n, nb, start_pos, ratio, rows_per_wg);
+}
+
+}  // namespace dsv41
+
+using namespace dsv41;
+
+extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_scale, const void* index_k,
+                                   int64_t k_bstride, const uint8_t* candidates, float* scores, int32_t bsz,
+                                   int32_t n, int32_t heads, int32_t dim, int32_t nb, int32_t start_pos,
+                                   int32_t ratio, int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_indexer_score";
+  DSV41_REQUIRE(q && w_raw && index_k && scores, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(bsz >= 0 && n >= 0 && heads > 0 && dim > 0 && nb >= 0 && start_pos >= 0 && ratio > 0,
+                DSV41_E_ARG, "%s: bad sizes", what);
+  DSV41_REQUIRE(k_bstride >= (int64_t)nb * dim, DSV41_E_ARG, "%s: k_bstride %lld < nb*dim", what,
+                (long long)k_bstride);
+  DSV41_REQUIRE((int64_t)bsz * n < 65536, DSV41_E_ARG, "%s: bsz*n must be < 65536", what);
+  if ((int64_t)bsz * n == 0 || nb == 0) return 0;
+  if (dtype == DSV41_F32) {
+    const size_t smem = ((size_t)heads * dim + heads) * sizeof(float);
+    DSV41_REQUIRE(smem <= 64 * 1024, DSV41_E_SHAPE, "%s: fp32 path needs heads*dim <= 16k", what);
+    dim3 grid((unsigned)((nb + 255) / 256), (unsigned)(bsz * n));
+    hipLaunchKernelGGL(indexer_score_f32_kernel, grid, dim3(256), smem, stream, (const float*)q,
+                       (const float*)w_raw, w_scale, (const float*)index_k, k_bstride, candidates, scores, n,
+                       heads, dim, nb, start_pos, ratio);
+    return check_launch(what);
+  }
+  if (dtype != DSV41_BF16) return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported", what, dtype);
+  DSV41_REQUIRE(aligned16(q) && aligned16(index_k), DSV41_E_ARG, "%s: q and index_k must be 16-byte aligned", what);
+  DSV41_REQUIRE(k_bstride % 8 == 0, DSV41_E_ARG, "%s: k_bstride must be a multiple of 8", what);
+  // spread the visible rows over ~1024 workgroups, in multiples of one 8-wave sweep (256 rows)
+  const int64_t want = ((int64_t)nb * bsz * n + 1023) / 1024;
+  int rows_per_wg = (int)((want + 255) / 256 * 256);
+  if (rows_per_wg < 256) rows_per_wg = 256;
+  if (rows_per_wg > 4096) rows_per_wg = 4096;
+  dim3 grid((unsigned)((nb + rows_per_wg - 1) / rows_per_wg), (unsigned)(bsz * n));
+#define DSV41_IDX_CASE(HT_, KS_)                                                                          \
+  if (heads == HT_ * 16 && dim == KS_ * 32) {                                                             \
+    launch_idx_bf16<HT_, KS_>(grid, stream, q, w_raw, w_scale, index_k, k_bstride, candidates, scores, n, \
+                              nb, start_pos, ratio, rows_per_wg);                                         \
+    return check_launch(what);                                                                            \
+  }
+  DSV41_IDX_CASE(4, 4)   // 64 heads x 128
+  DSV41_IDX_CASE(2, 4)   // 32 heads x 128 (the released model)
+  DSV41_IDX_CASE(1, 4)
+  DSV41_IDX_CASE(8, 4)
+  DSV41_IDX_CASE(4, 2)
+  DSV41_IDX_CASE(2, 2)
+  DSV41_IDX_CASE(1, 2)
+  DSV41_IDX_CASE(1, 1)
+  DSV41_IDX_CASE(2, 1)
+  DSV41_IDX_CASE(4, 1)
+#undef DSV41_IDX_CASE
+  return set_error(DSV41_E_SHAPE, "%s: bf16 path has no instance for heads=%d dim=%d", what, heads, dim);
+}

@@ -1,0 +1,423 @@
+// Row pipelines of the attention path: RMSNorm -> rope tail -> QAT fake-quant, each stage
+// rounded to the activation dtype exactly where the reference rounds, fused into one pass
+// over HBM. One thread owns a 32-element chunk of a row (fake-quant blocks of 16/32 and rope
+// pairs never straddle chunks), so the only cross-thread step is the RMSNorm reduction.
+//
+// Reference semantics: deepseek_v41_mlx/fakequant.py:47-119, layers.py:20-84,
+// attention.py:119-122, 157-163, indexer.py:89-104, 179-181, cache.py:61-67.
+#include "common.h"
+
+namespace dsv41 {
+
+enum FqKind { FQ_NONE = 0, FQ_FP8_UE8M0 = 1, FQ_FP4_UE8M0 = 2, FQ_FP4_E4M3 = 3 };
+
+struct RowArgs {
+  const void* src;          // [rows, dim] contiguous
+  void* dst;                // row (b, s, h) at dst + b*dst_bstride + (tok_base+s)*dst_tstride + h*dim
+  int64_t rows;
+  int dim, cpr;             // cpr = dim / 32 chunks per row
+  int S, H;                 // tokens per batch row, rows per token
+  int64_t dst_bstride, dst_tstride;
+  int tok_base;
+  const float* norm_w;
+  float eps;
+  const float* cos_tab;
+  const float* sin_tab;
+  int rd, pos_base, pos_step, inverse;
+};
+
+template <typename T> __device__ __forceinline__ void load32(const T* p, float v[32]);
+template <> __device__ __forceinline__ void load32<float>(const float* p, float v[32]) {
+  const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float4 t = q[i];
+    v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+  }
+}
+template <> __device__ __forceinline__ void load32<bf16_t>(const bf16_t* p, float v[32]) {
+  const uint4* q = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint4 t = q[i];
+    uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
+      v[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+    }
+  }
+}
+template <typename T> __device__ __forceinline__ void store32(T* p, const float v[32]);
+template <> __device__ __forceinline__ void store32<float>(float* p, const float v[32]) {
+  float4* q = reinterpret_cast<float4*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+template <> __device__ __forceinline__ void store32<bf16_t>(bf16_t* p, const float v[32]) {
+  uint4* q = reinterpret_cast<uint4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = (uint32_t)f2bf(v[8 * i + 2 * j]) | ((uint32_t)f2bf(v[8 * i + 2 * j + 1]) << 16);
+    q[i] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// One fake-quant block of BLK values at v[0..BLK), rounded back to T.
+template <typename T, int FQ, int BLK>
+__device__ __forceinline__ void fake_quant_block(float* v) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < BLK; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  if (FQ == FQ_FP8_UE8M0) {
+    amax = fmaxf(amax, 1e-4f);
+    const float s = pow2_ceil_log2(amax * (float)(1.0 / 448.0));
+#pragma unroll
+    for (int i = 0; i < BLK; ++i)
+      v[i] = io<T>::rnd(e4m3_round(fminf(fmaxf(__fdiv_rn(v[i], s), -448.0f), 448.0f)) * s);
+  } else if (FQ == FQ_FP4_UE8M0) {
+    amax = fmaxf(amax, (float)(6.0 * 1.1754943508222875e-38));  // 6 * 2^-126
+    const float s = pow2_ceil_log2(amax * (float)(1.0 / 6.0));
+#pragma unroll
+    for (int i = 0; i < BLK; ++i)
+      v[i] = io<T>::rnd(e2m1_round(fminf(fmaxf(__fdiv_rn(v[i], s), -6.0f), 6.0f)) * s);
+  } else if (FQ == FQ_FP4_E4M3) {
+    amax = fmaxf(amax, 0.01171875f);                             // 6 * 2^-9
+    const float s = e4m3_round(__fdiv_rn(amax, 6.0f));
+#pragma unroll
+    for (int i = 0; i < BLK; ++i)
+      v[i] = io<T>::rnd(e2m1_round(fminf(fmaxf(__fdiv_rn(v[i], s), -6.0f), 6.0f)) * s);
+  }
+}
+
+template <typename T, bool NORM, bool ROPE, int FQ, int BLK>
+__global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid / a.cpr;
+  const int c = (int)(gid - row * a.cpr);
+  if (row >= a.rows) return;  // whole row groups leave together (cpr divides 64 when NORM)
+  const int h = (int)(row % a.H);
+  const int64_t t = row / a.H;
+  const int s = (int)(t % a.S);
+  const int64_t b = t / a.S;
+
+  float v[32];
+  load32<T>(reinterpret_cast<const T*>(a.src) + row * a.dim + c * 32, v);
+
+  if (NORM) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) ss += v[i] * v[i];
+    ss = group_sum(ss, a.cpr);
+    const float inv = 1.0f / sqrtf(ss / (float)a.dim + a.eps);
+    const float* w = a.norm_w + c * 32;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = io<T>::rnd(w[i] * (v[i] * inv));
+  }
+  if (ROPE) {
+    const int first = a.dim - a.rd;
+    const int half = a.rd >> 1;
+    const int64_t pos = (int64_t)a.pos_base + (int64_t)s * a.pos_step;
+    const float* ct = a.cos_tab + pos * half;
+    const float* st = a.sin_tab + pos * half;
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) {
+      const int ch = c * 32 + i;
+      if (ch >= first) {
+        const int p = (ch - first) >> 1;
+        const float cs = ct[p];
+        const float sn = a.inverse ? -st[p] : st[p];
+        const float xr = v[i], xi = v[i + 1];
+        v[i] = io<T>::rnd(__fsub_rn(__fmul_rn(xr, cs), __fmul_rn(xi, sn)));
+        v[i + 1] = io<T>::rnd(__fadd_rn(__fmul_rn(xr, sn), __fmul_rn(xi, cs)));
+      }
+    }
+  }
+  if (FQ != FQ_NONE) {
+#pragma unroll
+    for (int b0 = 0; b0 < 32; b0 += BLK) fake_quant_block<T, FQ, BLK>(v + b0);
+  }
+  T* dst = reinterpret_cast<T*>(a.dst) + b * a.dst_bstride + (int64_t)(a.tok_base + s) * a.dst_tstride +
+           (int64_t)h * a.dim + c * 32;
+  store32<T>(dst, v);
+}
+
+template <typename T, bool NORM, bool ROPE, int FQ, int BLK>
+static int launch_rows(const RowArgs& a, hipStream_t stream, const char* what) {
+  const int64_t threads = a.rows * a.cpr;
+  if (threads == 0) return 0;
+  const int64_t blocks = (threads + 255) / 256;
+  hipLaunchKernelGGL((row_pipeline_kernel<T, NORM, ROPE, FQ, BLK>), dim3((unsigned)blocks), dim3(256),
+                     0, stream, a);
+  return check_launch(what);
+}
+
+template <bool NORM, bool ROPE, int FQ, int BLK>
+static int dispatch_rows(int dtype, const RowArgs& a, hipStream_t stream, const char* what) {
+  if (dtype == DSV41_F32) return launch_rows<float, NORM, ROPE, FQ, BLK>(a, stream, what);
+  if (dtype == DSV41_BF16) return launch_rows<bf16_t, NORM, ROPE, FQ, BLK>(a, stream, what);
+  return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported (F32 or BF16)", what, dtype);
+}
+
+// Common shape checks. NORM needs the row's chunks in one power-of-two lane group.
+static int check_rows(const char* what, const void* src, const void* dst, int64_t rows, int dim,
+                      bool norm) {
+  DSV41_REQUIRE(src && dst, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(aligned16(src) && aligned16(dst), DSV41_E_ARG, "%s: tensors must be 16-byte aligned", what);
+  DSV41_REQUIRE(rows >= 0, DSV41_E_ARG, "%s: rows < 0", what);
+  DSV41_REQUIRE(dim > 0 && dim % 32 == 0, DSV41_E_SHAPE, "%s: dim %d must be a positive multiple of 32", what, dim);
+  if (norm)
+    DSV41_REQUIRE(is_pow2(dim / 32) && dim / 32 <= 64, DSV41_E_SHAPE,
+                  "%s: dim %d must be 32 * 2^k <= 2048 for the fused norm", what, dim);
+  return 0;
+}
+
+static RowArgs plain_rows(const void* x, void* y, int64_t rows, int dim) {
+  RowArgs a{};
+  a.src = x; a.dst = y; a.rows = rows; a.dim = dim; a.cpr = dim / 32;
+  a.S = 1; a.H = 1; a.dst_bstride = 0; a.dst_tstride = dim; a.tok_base = 0;
+  // with S = H = 1 every row is its own batch row: b = row, so the batch stride is the row
+  a.dst_bstride = dim;
+  return a;
+}
+
+template <int FQ>
+static int fq_entry(const char* what, const void* x, void* y, int64_t rows, int32_t cols, int32_t block,
+                    int32_t dtype, hipStream_t stream) {
+  int rc = check_rows(what, x, y, rows, cols, false);
+  if (rc) return rc;
+  DSV41_REQUIRE(block == 16 || block == 32, DSV41_E_SHAPE, "%s: block %d must be 16 or 32", what, block);
+  // blocks never cross 32-element chunks, so the tensor is treated as chunks of one row each
+  RowArgs a = plain_rows(x, y, rows * (cols / 32), 32);
+  if (block == 32) return dispatch_rows<false, false, FQ, 32>(dtype, a, stream, what);
+  return dispatch_rows<false, false, FQ, 16>(dtype, a, stream, what);
+}
+
+// ------------------------------------------------------------------ RMSNorm (any dim)
+
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, T* y, const float* w, int dim, float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  x += row * dim;
+  y += row * dim;
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < dim; i += 256) {
+    const float v = io<T>::ld(x + i);
+    ss += v * v;
+  }
+  ss = group_sum(ss, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.0f / sqrtf(tot / (float)dim + eps);
+  for (int i = threadIdx.x; i < dim; i += 256) io<T>::st(y + i, w[i] * (io<T>::ld(x + i) * inv));
+}
+
+// ------------------------------------------------------------------ rope table, ring, window idx
+
+__global__ void rope_table_kernel(float* cs, float* sn, const float* freqs, int seqlen, int half) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)seqlen * half) return;
+  const int t = (int)(i / half), j = (int)(i % half);
+  const float ang = (float)t * freqs[j];
+  cs[i] = cosf(ang);
+  sn[i] = sinf(ang);
+}
+
+template <typename T>
+__global__ void window_write_kernel(T* win, const T* kv, int n, int dim, int window, int start_pos, int keep,
+                                    int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over bsz*keep*dim
+  if (i >= total) return;
+  const int64_t per_b = (int64_t)keep * dim;
+  const int64_t b = i / per_b;
+  const int64_t r = i - b * per_b;
+  const int t = (int)(r / dim), d = (int)(r % dim);
+  const int slot = (int)(((int64_t)start_pos + n - keep + t) % window);
+  win[(b * window + slot) * dim + d] = kv[(b * n + (n - keep + t)) * dim + d];
+}
+
+__global__ void window_idx_kernel(int32_t* out, int wp, int n, int window, int weff) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)n * weff) return;
+  const int q = (int)(i / weff), j = (int)(i % weff);
+  const int end = q + wp;
+  const int start = max(end - window + 1, 0);
+  const int idx = start + j;
+  out[i] = idx > end ? -1 : idx;
+}
+
+}  // namespace dsv41
+
+using namespace dsv41;
+
+// ------------------------------------------------------------------ C ABI
+
+extern "C" int dsv41_fq_fp8_ue8m0(const void* x, void* y, int64_t rows, int32_t cols, int32_t block,
+                                  int32_t dtype, hipStream_t stream) {
+  return fq_entry<FQ_FP8_UE8M0>("dsv41_fq_fp8_ue8m0", x, y, rows, cols, block, dtype, stream);
+}
+
+extern "C" int dsv41_fq_fp4_ue8m0(const void* x, void* y, int64_t rows, int32_t cols, int32_t block,
+                                  int32_t dtype, hipStream_t stream) {
+  return fq_entry<FQ_FP4_UE8M0>("dsv41_fq_fp4_ue8m0", x, y, rows, cols, block, dtype, stream);
+}
+
+extern "C" int dsv41_fq_fp4_e4m3(const void* x, void* y, int64_t rows, int32_t cols, int32_t block,
+                                 int32_t dtype, hipStream_t stream) {
+  return fq_entry<FQ_FP4_E4M3>("dsv41_fq_fp4_e4m3", x, y, rows, cols, block, dtype, stream);
+}
+
+extern "C" int dsv41_rope_table(float* cos_out, float* sin_out, const float* freqs, int32_t seqlen,
+                                int32_t half, hipStream_t stream) {
+  const char* what = "dsv41_rope_table";
+  DSV41_REQUIRE(cos_out && sin_out && freqs, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(seqlen >= 0 && half > 0, DSV41_E_ARG, "%s: bad sizes seqlen=%d half=%d", what, seqlen, half);
+  const int64_t total = (int64_t)seqlen * half;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, cos_out,
+                     sin_out, freqs, seqlen, half);
+  return check_launch(what);
+}
+
+extern "C" int dsv41_rope_tail(const void* x, void* y, int32_t bsz, int32_t seqlen, int32_t heads, int32_t dim,
+                               int32_t rd, const float* cos_tab, const float* sin_tab, int32_t pos_base,
+                               int32_t pos_step, int32_t inverse, int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_rope_tail";
+  DSV41_REQUIRE(bsz >= 0 && seqlen >= 0 && heads > 0, DSV41_E_ARG, "%s: bad sizes", what);
+  int rc = check_rows(what, x, y, (int64_t)bsz * seqlen * heads, dim, false);
+  if (rc) return rc;
+  DSV41_REQUIRE(cos_tab && sin_tab, DSV41_E_ARG, "%s: null rope table", what);
+  DSV41_REQUIRE(rd > 0 && rd % 2 == 0 && rd <= dim, DSV41_E_SHAPE, "%s: rd %d must be even and <= dim", what, rd);
+  DSV41_REQUIRE(pos_base >= 0 && (seqlen == 0 || (int64_t)pos_base + (int64_t)(seqlen - 1) * pos_step >= 0),
+                DSV41_E_ARG, "%s: negative position", what);
+  RowArgs a{};
+  a.src = x; a.dst = y; a.rows = (int64_t)bsz * seqlen * heads; a.dim = dim; a.cpr = dim / 32;
+  a.S = seqlen; a.H = heads; a.dst_bstride = (int64_t)seqlen * heads * dim; a.dst_tstride = (int64_t)heads * dim;
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.pos_base = pos_base; a.pos_step = pos_step;
+  a.inverse = inverse ? 1 : 0;
+  return dispatch_rows<false, true, FQ_NONE, 32>(dtype, a, stream, what);
+}
+
+extern "C" int dsv41_rmsnorm(const void* x, void* y, const float* weight, int64_t rows, int32_t dim, float eps,
+                             int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_rmsnorm";
+  DSV41_REQUIRE(x && y && weight, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(rows >= 0 && dim > 0, DSV41_E_ARG, "%s: bad sizes", what);
+  if (rows == 0) return 0;
+  DSV41_REQUIRE(rows < (1ll << 31), DSV41_E_ARG, "%s: too many rows", what);
+  if (dtype == DSV41_F32)
+    hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3((unsigned)rows), dim3(256), 0, stream, (const float*)x,
+                       (float*)y, weight, dim, eps);
+  else if (dtype == DSV41_BF16)
+    hipLaunchKernelGGL(rmsnorm_kernel<bf16_t>, dim3((unsigned)rows), dim3(256), 0, stream, (const bf16_t*)x,
+                       (bf16_t*)y, weight, dim, eps);
+  else
+    return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported", what, dtype);
+  return check_launch(what);
+}
+
+extern "C" int dsv41_kv_window_prep(void* kv, const float* norm_w, const float* cos_tab, const float* sin_tab,
+                                    int32_t bsz, int32_t n, int32_t dim, int32_t rd, int32_t start_pos, float eps,
+                                    int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_kv_window_prep";
+  DSV41_REQUIRE(bsz >= 0 && n >= 0 && start_pos >= 0, DSV41_E_ARG, "%s: bad sizes", what);
+  int rc = check_rows(what, kv, kv, (int64_t)bsz * n, dim, true);
+  if (rc) return rc;
+  DSV41_REQUIRE(norm_w && cos_tab && sin_tab, DSV41_E_ARG, "%s: null weight/table", what);
+  DSV41_REQUIRE(rd > 0 && rd % 2 == 0 && rd <= dim, DSV41_E_SHAPE, "%s: bad rd %d", what, rd);
+  RowArgs a{};
+  a.src = kv; a.dst = kv; a.rows = (int64_t)bsz * n; a.dim = dim; a.cpr = dim / 32;
+  a.S = n; a.H = 1; a.dst_bstride = (int64_t)n * dim; a.dst_tstride = dim;
+  a.norm_w = norm_w; a.eps = eps; a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd;
+  a.pos_base = start_pos; a.pos_step = 1;
+  return dispatch_rows<true, true, FQ_FP8_UE8M0, 32>(dtype, a, stream, what);
+}
+
+extern "C" int dsv41_window_write(void* win_kv, const void* kv, int32_t bsz, int32_t n, int32_t dim,
+                                  int32_t window, int32_t start_pos, int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_window_write";
+  DSV41_REQUIRE(win_kv && kv, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(bsz >= 0 && n >= 0 && dim > 0 && window > 0 && start_pos >= 0, DSV41_E_ARG, "%s: bad sizes", what);
+  const int keep = n < window ? n : window;
+  const int64_t total = (int64_t)bsz * keep * dim;
+  if (total == 0) return 0;
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  if (dtype == DSV41_F32)
+    hipLaunchKernelGGL(window_write_kernel<float>, dim3(blocks), dim3(256), 0, stream, (float*)win_kv,
+                       (const float*)kv, n, dim, window, start_pos, keep, total);
+  else if (dtype == DSV41_BF16)
+    hipLaunchKernelGGL(window_write_kernel<bf16_t>, dim3(blocks), dim3(256), 0, stream, (bf16_t*)win_kv,
+                       (const bf16_t*)kv, n, dim, window, start_pos, keep, total);
+  else
+    return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported", what, dtype);
+  return check_launch(what);
+}
+
+extern "C" int dsv41_window_idx(int32_t* out, int32_t wp, int32_t n, int32_t window, hipStream_t stream) {
+  const char* what = "dsv41_window_idx";
+  DSV41_REQUIRE(out, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(wp >= 0 && n >= 0 && window > 0, DSV41_E_ARG, "%s: bad sizes", what);
+  const int weff = window < wp + n ? window : wp + n;
+  const int64_t total = (int64_t)n * weff;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(window_idx_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, out, wp, n,
+                     window, weff);
+  return check_launch(what);
+}
+
+extern "C" int dsv41_comp_write(const void* latents, void* comp_kv, int64_t cache_bstride, const float* cos_tab,
+                                const float* sin_tab, int32_t bsz, int32_t g, int32_t dim, int32_t rd, int32_t g0,
+                                int32_t ratio, int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_comp_write";
+  DSV41_REQUIRE(bsz >= 0 && g >= 0 && g0 >= 0 && ratio > 0, DSV41_E_ARG, "%s: bad sizes", what);
+  int rc = check_rows(what, latents, comp_kv, (int64_t)bsz * g, dim, false);
+  if (rc) return rc;
+  DSV41_REQUIRE(cache_bstride >= (int64_t)(g0 + g) * dim, DSV41_E_ARG, "%s: cache too small", what);
+  DSV41_REQUIRE(cos_tab && sin_tab, DSV41_E_ARG, "%s: null rope table", what);
+  DSV41_REQUIRE(rd > 0 && rd % 2 == 0 && rd <= dim, DSV41_E_SHAPE, "%s: bad rd %d", what, rd);
+  RowArgs a{};
+  a.src = latents; a.dst = comp_kv; a.rows = (int64_t)bsz * g; a.dim = dim; a.cpr = dim / 32;
+  a.S = g; a.H = 1; a.dst_bstride = cache_bstride; a.dst_tstride = dim; a.tok_base = g0;
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.pos_base = g0 * ratio; a.pos_step = ratio;
+  return dispatch_rows<false, true, FQ_FP4_E4M3, 16>(dtype, a, stream, what);
+}
+
+extern "C" int dsv41_index_key_publish(const void* k_raw, void* index_k, int64_t cache_bstride, const float* norm_w,
+                                       const float* cos_tab, const float* sin_tab, int32_t bsz, int32_t g,
+                                       int32_t dim, int32_t rd, int32_t g0, int32_t ratio, float eps,
+                                       int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_index_key_publish";
+  DSV41_REQUIRE(bsz >= 0 && g >= 0 && g0 >= 0 && ratio > 0, DSV41_E_ARG, "%s: bad sizes", what);
+  int rc = check_rows(what, k_raw, index_k, (int64_t)bsz * g, dim, true);
+  if (rc) return rc;
+  DSV41_REQUIRE(cache_bstride >= (int64_t)(g0 + g) * dim, DSV41_E_ARG, "%s: cache too small", what);
+  DSV41_REQUIRE(norm_w && cos_tab && sin_tab, DSV41_E_ARG, "%s: null weight/table", what);
+  DSV41_REQUIRE(rd > 0 && rd % 2 == 0 && rd <= dim, DSV41_E_SHAPE, "%s: bad rd %d", what, rd);
+  RowArgs a{};
+  a.src = k_raw; a.dst = index_k; a.rows = (int64_t)bsz * g; a.dim = dim; a.cpr = dim / 32;
+  a.S = g; a.H = 1; a.dst_bstride = cache_bstride; a.dst_tstride = dim; a.tok_base = g0;
+  a.norm_w = norm_w; a.eps = eps; a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd;
+  a.pos_base = g0 * ratio; a.pos_step = ratio;
+  return dispatch_rows<true, true, FQ_FP4_UE8M0, 32>(dtype, a, stream, what);
+}
+
+extern "C" int dsv41_index_q_prep(void* q, const float* cos_tab, const float* sin_tab, int32_t bsz, int32_t n,
+                                  int32_t heads, int32_t dim, int32_t rd, int32_t start_pos, int32_t dtype,
+                                  hipStream_t stream) {
+  const char* what = "dsv41_index_q_prep";
+  DSV41_REQUIRE(bsz >= 0 && n >= 0 && heads > 0 && start_pos >= 0, DSV41_E_ARG, "%s: bad sizes", what);
+  int rc = check_rows(what, q, q, (int64_t)bsz * n * heads, dim, false);
+  if (rc) return rc;
+  DSV41_REQUIRE(cos_tab && sin_tab, DSV41_E_ARG, "%s: null rope table", what);
+  DSV41_REQUIRE(rd > 0 && rd % 2 == 0 && rd <= dim, DSV41_E_SHAPE, "%s: bad rd %d", what, rd);
+  RowArgs a{};
+  a.src = q; a.dst = q; a.rows = (int64_t)bsz * n * heads; a.dim = dim; a.cpr = dim / 32;
+  a.S = n; a.H = heads; a.dst_bstride = (int64_t)n * heads * dim; a.dst_tstride = (int64_t)heads * dim;
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.pos_base = start_pos; a.pos_step = 1;
+  return dispatch_rows<false, true, FQ_FP4_UE8M0, 32>(dtype, a, stream, what);
+}

@@ -1,0 +1,459 @@
+"""ctypes binding of libdsv41.so, the C ABI declared in include/dsv41.h.
+
+Every wrapper takes torch tensors that must already live on the GPU, checks dtype, shape
+and contiguity the way the reference's TileLang wrappers assert them
+(docs/reference/kernel.py:108, 193-194, 286-298), passes raw device pointers and torch's
+current stream, and turns a non-zero status into an exception: ``ValueError`` for a
+contract violation (negative dsv41_status), ``RuntimeError`` for a HIP launch error.
+
+There is no fallback: if the library is missing, or a tensor is not on a GPU, the call
+raises. The kernels run on the HIP path or not at all.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+LIB_NAME = "libdsv41.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+F32, BF16, FP8_E4M3 = 0, 1, 2
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16}
+
+_c_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> argtypes, mirroring include/dsv41.h
+_SIGNATURES = {
+    "dsv41_fq_fp8_ue8m0": [_c_p, _c_p, _i64, _i32, _i32, _i32, _c_p],
+    "dsv41_fq_fp4_ue8m0": [_c_p, _c_p, _i64, _i32, _i32, _i32, _c_p],
+    "dsv41_fq_fp4_e4m3": [_c_p, _c_p, _i64, _i32, _i32, _i32, _c_p],
+    "dsv41_rope_table": [_c_p, _c_p, _c_p, _i32, _i32, _c_p],
+    "dsv41_rope_tail": [_c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _c_p, _c_p, _i32, _i32, _i32,
+                        _i32, _c_p],
+    "dsv41_rmsnorm": [_c_p, _c_p, _c_p, _i64, _i32, _f32, _i32, _c_p],
+    "dsv41_kv_window_prep": [_c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _f32, _i32,
+                             _c_p],
+    "dsv41_window_write": [_c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_window_idx": [_c_p, _i32, _i32, _i32, _c_p],
+    "dsv41_compress_pool": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32,
+                            _f32, _i32, _c_p],
+    "dsv41_comp_write": [_c_p, _c_p, _i64, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                         _c_p],
+    "dsv41_index_key_publish": [_c_p, _c_p, _i64, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32,
+                                _i32, _f32, _i32, _c_p],
+    "dsv41_index_q_prep": [_c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_indexer_score": [_c_p, _c_p, _f32, _c_p, _i64, _c_p, _c_p, _i32, _i32, _i32, _i32,
+                            _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_topk_select": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_candidate_blocks": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _i32, _i32, _c_p],
+    "dsv41_sparse_mla_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32],
+    "dsv41_sparse_attn": [_c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+                          _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
+                         _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
+    "dsv41_version": [],
+    "dsv41_last_error_string": [],
+}
+_RESTYPES = {
+    "dsv41_sparse_mla_workspace_bytes": _sz,
+    "dsv41_version": ctypes.c_char_p,
+    "dsv41_last_error_string": ctypes.c_char_p,
+}
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libdsv41.so (once). Raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python deepseek-v41-mlx_amd/build.py` "
+                "(or __graft_entry__.build()); the dsv41 kernels have no fallback")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, args in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        _LIB = handle
+    return _LIB
+
+
+def version() -> str:
+    return lib().dsv41_version().decode()
+
+
+def _check(rc: int, name: str) -> None:
+    if rc == 0:
+        return
+    msg = (lib().dsv41_last_error_string() or b"").decode()
+    if rc < 0:
+        raise ValueError(f"{name}: {msg} (status {rc})")
+    raise RuntimeError(f"{name}: {msg} (hipError {rc})")
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _gpu(name: str, *tensors):
+    for t in tensors:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+        if not t.is_cuda:
+            raise ValueError(f"{name}: tensor on {t.device}; the dsv41 kernels run on the GPU only")
+
+
+def _contig(name: str, *tensors):
+    for t in tensors:
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"{name}: tensor of shape {tuple(t.shape)} must be contiguous")
+
+
+def dtype_code(t: torch.Tensor, name: str) -> int:
+    if t.dtype not in _DTYPES:
+        raise ValueError(f"{name}: dtype {t.dtype} not supported (float32 or bfloat16)")
+    return _DTYPES[t.dtype]
+
+
+def _call(name: str, *args) -> None:
+    _check(getattr(lib(), name)(*args), name)
+
+
+def row_stride(t: torch.Tensor, name: str) -> int:
+    """Batch stride (elements) of a [b, rows, dim] view whose rows are dense."""
+    if t.dim() != 3 or t.stride(2) != 1 or t.stride(1) != t.shape[2]:
+        raise ValueError(f"{name}: cache view must be [b, rows, dim] with dense rows")
+    return t.stride(0)
+
+
+# ---------------------------------------------------------------------------- fake-quant
+
+
+def _fq(name: str, x: torch.Tensor, block: int, out: torch.Tensor | None) -> torch.Tensor:
+    _gpu(name, x, out)
+    _contig(name, x)
+    out = torch.empty_like(x) if out is None else out
+    _contig(name, out)
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    _call(name, _ptr(x), _ptr(out), rows, cols, block, dtype_code(x, name), _stream(x))
+    return out
+
+
+def fq_fp8_ue8m0(x, block=32, out=None):
+    return _fq("dsv41_fq_fp8_ue8m0", x, block, out)
+
+
+def fq_fp4_ue8m0(x, block=32, out=None):
+    return _fq("dsv41_fq_fp4_ue8m0", x, block, out)
+
+
+def fq_fp4_e4m3(x, block=16, out=None):
+    return _fq("dsv41_fq_fp4_e4m3", x, block, out)
+
+
+# ---------------------------------------------------------------------------- rope / norm
+
+
+def rope_table(freqs: torch.Tensor, seqlen: int):
+    """cos, sin [seqlen, half] fp32 on freqs' device."""
+    name = "dsv41_rope_table"
+    _gpu(name, freqs)
+    freqs = freqs.to(torch.float32).contiguous()
+    half = freqs.numel()
+    cos = torch.empty(seqlen, half, dtype=torch.float32, device=freqs.device)
+    sin = torch.empty_like(cos)
+    _call(name, _ptr(cos), _ptr(sin), _ptr(freqs), seqlen, half, _stream(freqs))
+    return cos, sin
+
+
+def rope_tail(x, rd, cos, sin, pos_base=0, pos_step=1, inverse=False, out=None):
+    """x [b, s, d] or [b, s, h, d]; rows of the tables at pos_base + s*pos_step."""
+    name = "dsv41_rope_tail"
+    _gpu(name, x, cos, sin, out)
+    _contig(name, x, cos, sin)
+    if x.dim() not in (3, 4):
+        raise ValueError(f"{name}: x must be [b, s, d] or [b, s, h, d], got {tuple(x.shape)}")
+    b, s = x.shape[0], x.shape[1]
+    h = x.shape[2] if x.dim() == 4 else 1
+    d = x.shape[-1]
+    if rd > d or cos.shape[-1] * 2 != rd:
+        raise ValueError(f"{name}: rope tables of width {cos.shape[-1]} do not match rd={rd}")
+    last = pos_base + (s - 1) * pos_step if s else 0
+    if s and last >= cos.shape[0]:
+        raise ValueError(f"{name}: position {last} beyond the rope table ({cos.shape[0]} rows)")
+    out = torch.empty_like(x) if out is None else out
+    _contig(name, out)
+    _call(name, _ptr(x), _ptr(out), b, s, h, d, rd, _ptr(cos), _ptr(sin), pos_base, pos_step,
+          1 if inverse else 0, dtype_code(x, name), _stream(x))
+    return out
+
+
+def rmsnorm(x, weight, eps, out=None):
+    name = "dsv41_rmsnorm"
+    _gpu(name, x, weight, out)
+    _contig(name, x, weight)
+    if weight.dtype != torch.float32 or weight.numel() != x.shape[-1]:
+        raise ValueError(f"{name}: weight must be fp32 [{x.shape[-1]}]")
+    out = torch.empty_like(x) if out is None else out
+    _contig(name, out)
+    d = x.shape[-1]
+    _call(name, _ptr(x), _ptr(out), _ptr(weight), x.numel() // d, d, float(eps),
+          dtype_code(x, name), _stream(x))
+    return out
+
+
+# ---------------------------------------------------------------------------- window
+
+
+def kv_window_prep(kv, norm_w, cos, sin, rd, start_pos, eps):
+    name = "dsv41_kv_window_prep"
+    _gpu(name, kv, norm_w, cos, sin)
+    _contig(name, kv, norm_w, cos, sin)
+    b, n, d = kv.shape
+    if n and start_pos + n - 1 >= cos.shape[0]:
+        raise ValueError(f"{name}: rope table too short")
+    _call(name, _ptr(kv), _ptr(norm_w), _ptr(cos), _ptr(sin), b, n, d, rd, start_pos, float(eps),
+          dtype_code(kv, name), _stream(kv))
+    return kv
+
+
+def window_write(win_kv, kv, start_pos):
+    name = "dsv41_window_write"
+    _gpu(name, win_kv, kv)
+    _contig(name, win_kv, kv)
+    if win_kv.dtype != kv.dtype:
+        raise ValueError(f"{name}: ring dtype {win_kv.dtype} != kv dtype {kv.dtype}")
+    b, n, d = kv.shape
+    if win_kv.shape[0] < b or win_kv.shape[2] != d:
+        raise ValueError(f"{name}: ring {tuple(win_kv.shape)} does not hold kv {tuple(kv.shape)}")
+    # rows past b in the ring are untouched: the kernel indexes [b, window, d]
+    ring = win_kv[:b]
+    _call(name, _ptr(ring), _ptr(kv), b, n, d, win_kv.shape[1], start_pos, dtype_code(kv, name),
+          _stream(kv))
+
+
+def window_idx(wp, n, window, device):
+    name = "dsv41_window_idx"
+    weff = min(window, wp + n)
+    out = torch.empty(n, weff, dtype=torch.int32, device=device)
+    if out.numel():
+        _call(name, _ptr(out), wp, n, window, ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
+    return out
+
+
+# ---------------------------------------------------------------------------- compressor
+
+
+def compress_pool(kv, score, kv_state, score_state, norm_w, ratio, start_pos, eps, dtype):
+    """Returns latents [b, g, d] in `dtype` (None when no group completes)."""
+    name = "dsv41_compress_pool"
+    _gpu(name, kv, score, kv_state, score_state, norm_w)
+    _contig(name, kv, score, kv_state, score_state, norm_w)
+    for t in (kv, score, kv_state, score_state):
+        if t.dtype != torch.float32:
+            raise ValueError(f"{name}: kv/score/state must be fp32")
+    b, n, d = kv.shape
+    if kv_state.shape[0] < b or kv_state.shape[1:] != (ratio, d):
+        raise ValueError(f"{name}: state {tuple(kv_state.shape)} does not match [b, {ratio}, {d}]")
+    g = (start_pos % ratio + n) // ratio
+    lat = torch.empty(b, g, d, dtype=dtype, device=kv.device) if g else None
+    code = _DTYPES.get(dtype)
+    if code is None:
+        raise ValueError(f"{name}: dtype {dtype} not supported")
+    _call(name, _ptr(kv), _ptr(score), _ptr(kv_state), _ptr(score_state), _ptr(lat), _ptr(norm_w),
+          b, n, d, ratio, start_pos, float(eps), code, _stream(kv))
+    return lat
+
+
+def comp_write(latents, comp_kv, g0, ratio, cos, sin, rd):
+    name = "dsv41_comp_write"
+    _gpu(name, latents, comp_kv, cos, sin)
+    _contig(name, latents, cos, sin)
+    b, g, d = latents.shape
+    if comp_kv.dtype != latents.dtype:
+        raise ValueError(f"{name}: cache dtype {comp_kv.dtype} != latent dtype {latents.dtype}")
+    if comp_kv.shape[1] < g0 + g or comp_kv.shape[2] != d:
+        raise ValueError(f"{name}: cache {tuple(comp_kv.shape)} cannot take groups {g0}..{g0 + g}")
+    if g and (g0 + g - 1) * ratio >= cos.shape[0]:
+        raise ValueError(f"{name}: rope table too short")
+    _call(name, _ptr(latents), _ptr(comp_kv), row_stride(comp_kv, name), _ptr(cos), _ptr(sin), b, g, d,
+          rd, g0, ratio, dtype_code(latents, name), _stream(latents))
+
+
+def index_key_publish(k_raw, index_k, g0, ratio, norm_w, cos, sin, rd, eps):
+    name = "dsv41_index_key_publish"
+    _gpu(name, k_raw, index_k, norm_w, cos, sin)
+    _contig(name, k_raw, norm_w, cos, sin)
+    b, g, d = k_raw.shape
+    if index_k.dtype != k_raw.dtype:
+        raise ValueError(f"{name}: cache dtype {index_k.dtype} != key dtype {k_raw.dtype}")
+    if index_k.shape[1] < g0 + g or index_k.shape[2] != d:
+        raise ValueError(f"{name}: cache {tuple(index_k.shape)} cannot take groups {g0}..{g0 + g}")
+    if g and (g0 + g - 1) * ratio >= cos.shape[0]:
+        raise ValueError(f"{name}: rope table too short")
+    _call(name, _ptr(k_raw), _ptr(index_k), row_stride(index_k, name), _ptr(norm_w), _ptr(cos),
+          _ptr(sin), b, g, d, rd, g0, ratio, float(eps), dtype_code(k_raw, name), _stream(k_raw))
+
+
+# ---------------------------------------------------------------------------- indexer
+
+
+def index_q_prep(q, cos, sin, rd, start_pos):
+    name = "dsv41_index_q_prep"
+    _gpu(name, q, cos, sin)
+    _contig(name, q, cos, sin)
+    b, n, h, d = q.shape
+    if n and start_pos + n - 1 >= cos.shape[0]:
+        raise ValueError(f"{name}: rope table too short")
+    _call(name, _ptr(q), _ptr(cos), _ptr(sin), b, n, h, d, rd, start_pos, dtype_code(q, name),
+          _stream(q))
+    return q
+
+
+def indexer_score(q, w_raw, w_scale, index_k, start_pos, ratio, candidates=None, out=None):
+    """q [b,n,h,d], w_raw [b,n,h], index_k view [b, nb, d] of the owner's cache."""
+    name = "dsv41_indexer_score"
+    _gpu(name, q, w_raw, index_k, candidates, out)
+    _contig(name, q, w_raw, candidates)
+    b, n, h, d = q.shape
+    nb = index_k.shape[1]
+    if w_raw.shape != (b, n, h) or w_raw.dtype != q.dtype:
+        raise ValueError(f"{name}: w_raw must be {q.dtype} [{b}, {n}, {h}]")
+    if index_k.shape[0] < b or index_k.shape[2] != d or index_k.dtype != q.dtype:
+        raise ValueError(f"{name}: index_k {tuple(index_k.shape)} {index_k.dtype} does not match q")
+    if candidates is not None and (candidates.shape != (b, n, nb) or candidates.dtype not in (torch.uint8, torch.bool)):
+        raise ValueError(f"{name}: candidates must be bool/uint8 [{b}, {n}, {nb}]")
+    out = torch.empty(b, n, nb, dtype=torch.float32, device=q.device) if out is None else out
+    cand = candidates.view(torch.uint8) if candidates is not None else None
+    _call(name, _ptr(q), _ptr(w_raw), float(w_scale), _ptr(index_k), row_stride(index_k, name),
+          _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, dtype_code(q, name), _stream(q))
+    return out
+
+
+def topk_select(scores, topk, start_pos, ratio, offset):
+    """scores [b, n, nb] fp32 -> int32 [b, n, min(topk, nb)]."""
+    name = "dsv41_topk_select"
+    _gpu(name, scores)
+    _contig(name, scores)
+    if scores.dtype != torch.float32 or scores.dim() != 3:
+        raise ValueError(f"{name}: scores must be fp32 [b, n, nb]")
+    b, n, nb = scores.shape
+    k = min(topk, nb)
+    out = torch.empty(b, n, k, dtype=torch.int32, device=scores.device)
+    if out.numel():
+        _call(name, _ptr(scores), _ptr(out), b * n, n, nb, topk, start_pos, ratio, offset,
+              _stream(scores))
+    return out
+
+
+def candidate_blocks(scores, topk_blocks, block_size, lens=None, start_pos=0, ratio=1):
+    """scores [b, n, nb] fp32 -> bool [b, n, nb]; lens optional int32 [n] on the GPU."""
+    name = "dsv41_candidate_blocks"
+    _gpu(name, scores, lens)
+    _contig(name, scores, lens)
+    if scores.dtype != torch.float32 or scores.dim() != 3:
+        raise ValueError(f"{name}: scores must be fp32 [b, n, nb]")
+    b, n, nb = scores.shape
+    if lens is not None and (lens.dtype != torch.int32 or lens.numel() != n):
+        raise ValueError(f"{name}: lens must be int32 [{n}]")
+    keep = torch.empty(b, n, nb, dtype=torch.uint8, device=scores.device)
+    if keep.numel():
+        _call(name, _ptr(scores), _ptr(keep), b * n, n, nb, topk_blocks, block_size, _ptr(lens),
+              start_pos, ratio, _stream(scores))
+    return keep.view(torch.bool)
+
+
+# ---------------------------------------------------------------------------- sparse MLA
+
+
+def mla_workspace_bytes(b, m, heads, dim, rows_per_query, dtype) -> int:
+    return int(lib().dsv41_sparse_mla_workspace_bytes(b, m, heads, dim, rows_per_query,
+                                                      _DTYPES.get(dtype, -1)))
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor | None:
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
+def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale):
+    name = "dsv41_sparse_attn"
+    _gpu(name, q, kv, attn_sink, topk_idxs)
+    _contig(name, q, kv, attn_sink, topk_idxs)
+    b, m, h, d = q.shape
+    if kv.dim() != 3 or kv.shape[0] != b or kv.shape[2] != d or kv.dtype != q.dtype:
+        raise ValueError(f"{name}: kv {tuple(kv.shape)} {kv.dtype} does not match q")
+    if topk_idxs.dtype != torch.int32 or topk_idxs.shape[:2] != (b, m):
+        raise ValueError(f"{name}: topk_idxs must be int32 [{b}, {m}, k]")
+    if attn_sink.dtype != torch.float32 or attn_sink.numel() != h:
+        raise ValueError(f"{name}: attn_sink must be fp32 [{h}]")
+    k = topk_idxs.shape[2]
+    o = torch.empty_like(q)
+    ws_bytes = mla_workspace_bytes(b, m, h, d, k, q.dtype)
+    ws = _workspace(ws_bytes, q.device)
+    _call(name, _ptr(q), _ptr(kv), _ptr(attn_sink), _ptr(topk_idxs), _ptr(o), b, m, h, d,
+          kv.shape[1], k, float(softmax_scale), dtype_code(q, name), _ptr(ws), ws_bytes, _stream(q))
+    return o
+
+
+def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_scale, window,
+               start_pos, cos=None, sin=None, rd=0, out=None, workspace=None):
+    """The layer form: window ring + this chunk's KV + the owner's compressed cache, all read
+    in place. comp_kv: [b, >=n_comp, d] view (or None); idx [b, n, k] int32 or None."""
+    name = "dsv41_sparse_mla"
+    _gpu(name, q, win_kv, chunk_kv, comp_kv, attn_sink, idx, cos, sin, out)
+    _contig(name, q, chunk_kv, attn_sink, idx)
+    b, n, h, d = q.shape
+    wp = min(start_pos, window)
+    if chunk_kv.shape != (b, n, d) or chunk_kv.dtype != q.dtype:
+        raise ValueError(f"{name}: chunk kv must be {q.dtype} [{b}, {n}, {d}]")
+    ring = None
+    if win_kv is not None:
+        if win_kv.shape[0] < b or win_kv.shape[1:] != (window, d) or win_kv.dtype != q.dtype:
+            raise ValueError(f"{name}: window ring {tuple(win_kv.shape)} does not match")
+        ring = win_kv[:b]
+        _contig(name, ring)
+    elif wp:
+        raise ValueError(f"{name}: a window ring is needed once start_pos > 0")
+    comp_bstride = 0
+    if comp_kv is not None and n_comp:
+        if comp_kv.dtype != q.dtype or comp_kv.shape[2] != d or comp_kv.shape[1] < n_comp:
+            raise ValueError(f"{name}: compressed cache {tuple(comp_kv.shape)} does not match")
+        comp_bstride = row_stride(comp_kv, name)
+    else:
+        comp_kv, n_comp = None, 0
+    k = 0
+    if idx is not None:
+        if idx.dtype != torch.int32 or idx.shape[:2] != (b, n):
+            raise ValueError(f"{name}: idx must be int32 [{b}, {n}, k]")
+        k = idx.shape[2]
+    if rd:
+        if cos is None or sin is None or cos.shape[-1] * 2 != rd:
+            raise ValueError(f"{name}: rope tables do not match rd={rd}")
+        if n and start_pos + n - 1 >= cos.shape[0]:
+            raise ValueError(f"{name}: rope table too short")
+    o = torch.empty_like(q) if out is None else out
+    rows = min(window, wp + n) + k
+    ws_bytes = mla_workspace_bytes(b, n, h, d, rows, q.dtype)
+    if ws_bytes and (workspace is None or workspace.numel() < ws_bytes):
+        workspace = _workspace(ws_bytes, q.device)
+    _call(name, _ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp_kv), comp_bstride, n_comp,
+          _ptr(attn_sink), _ptr(idx), k, _ptr(o), b, n, h, d, window, start_pos, float(softmax_scale),
+          _ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, dtype_code(q, name),
+          _ptr(workspace) if ws_bytes else None, ws_bytes, _stream(q))
+    return o

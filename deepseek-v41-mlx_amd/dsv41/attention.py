@@ -1,0 +1,176 @@
+"""One V4.1 attention layer (deepseek_v41_mlx/attention.py:53-179) on the GPU.
+
+The projections (wq_a, wq_b, wkv, the compressor / indexer projections, wo_a, wo_b) are torch
+GEMMs; everything between them runs in HIP kernels:
+
+  q      : q_norm (RMSNorm kernel) ... rope tail (in place)
+  kv     : kv_norm -> rope -> fp8 fake-quant, one fused kernel, in place
+  owner  : compressor pooling kernel; index keys published into its own index_k; latents
+           roped + fp4/e4m3 fake-quantized straight into its comp_kv (no staging copy)
+  index  : fused q prologue, MFMA scoring, candidate blocks, top-k
+  attend : one sparse-MLA kernel that reads the previous window ring, this chunk's KV and the
+           most recent owner's comp_kv in place -- the reference's concatenation of the three
+           (attention.py:127, 165-168) never happens -- and applies the inverse rope to the
+           output tail before storing it.
+The window ring is written after the attention kernel has read the previous window, which
+is equivalent to the reference's write-before-concatenate order because the concatenated
+copy held the old ring contents.
+
+The forward is chunk-general: prefill, chunked prefill and 1-token decode share one path.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _abi, fakequant
+from .compressor import Compressor
+from .config import ModelArgs
+from .indexer import Indexer
+from .layers import RMSNorm, yarn_inv_freqs
+
+
+def window_idx_matrix(wp: int, n: int, window: int, device="cuda") -> torch.Tensor:
+    """[n, min(window, wp+n)] int32 indices into concat(prev window(wp), chunk(n)), -1 pads
+    (attention.py:40-50)."""
+    return _abi.window_idx(wp, n, window, torch.device(device))
+
+
+class Attention(torch.nn.Module):
+    def __init__(self, layer_id: int, args: ModelArgs, dtype=torch.bfloat16, device="cuda"):
+        super().__init__()
+        self.layer_id = layer_id
+        self.dim = args.dim
+        self.n_heads = args.n_heads
+        self.head_dim = args.head_dim
+        self.rope_head_dim = args.rope_head_dim
+        self.q_lora_rank = args.q_lora_rank
+        self.o_lora_rank = args.o_lora_rank
+        self.n_groups = args.o_groups
+        self.window_size = args.window_size
+        self.ratio = args.compress_ratio(layer_id)
+        self.eps = args.norm_eps
+        self.softmax_scale = args.head_dim ** -0.5
+        self.dtype = dtype
+        self.device = torch.device(device)
+
+        def lin(i, o):
+            return torch.nn.Linear(i, o, bias=False, dtype=dtype, device=device)
+
+        self.attn_sink = torch.nn.Parameter(torch.zeros(self.n_heads, dtype=torch.float32, device=device))
+        self.wq_a = lin(self.dim, self.q_lora_rank)
+        self.q_norm = RMSNorm(self.q_lora_rank, self.eps, device=device)
+        self.wq_b = lin(self.q_lora_rank, self.n_heads * self.head_dim)
+        self.wkv = lin(self.dim, self.head_dim)
+        self.kv_norm = RMSNorm(self.head_dim, self.eps, device=device)
+        self.wo_a = lin(self.n_heads * self.head_dim // self.n_groups, self.n_groups * self.o_lora_rank)
+        self.wo_b = lin(self.n_groups * self.o_lora_rank, self.dim)
+
+        self.is_kv_source = layer_id in args.kv_source_layers
+        self.is_index_source = layer_id in args.index_source_layers
+        if self.is_kv_source:
+            self.compressor = Compressor(args, layer_id, dtype, device)
+        if self.is_index_source:
+            self.indexer = Indexer(args, layer_id, dtype, device)
+
+        if self.ratio:
+            orig_len, theta = args.original_seq_len, args.compress_rope_theta
+        else:
+            orig_len, theta = 0, args.rope_theta
+        self._rope = (args.rope_head_dim, orig_len, theta, args.rope_factor, args.beta_fast,
+                      args.beta_slow)
+        self._freq_vec = None
+        self._cos = None
+        self._sin = None
+        self._workspace = None
+        self.requires_grad_(False)
+
+        # test hooks (negative controls), attention.py:95-97
+        self._break_rope_inverse = False
+        self._break_sink = False
+
+    def _freqs(self, upto: int):
+        """Device (cos, sin) tables covering positions < upto; grown geometrically."""
+        if self._cos is None or self._cos.shape[0] < upto:
+            if self._freq_vec is None:
+                rd, orig_len, theta, factor, bf, bs = self._rope
+                self._freq_vec = torch.from_numpy(yarn_inv_freqs(rd, orig_len, theta, factor, bf, bs)).to(self.device)
+            rows = max(upto, 64, 0 if self._cos is None else 2 * self._cos.shape[0])
+            self._cos, self._sin = _abi.rope_table(self._freq_vec, rows)
+        return self._cos, self._sin
+
+    def _kv_prologue(self, kv, cos, sin, start_pos):
+        rd = self.rope_head_dim
+        if fakequant.DISABLE:
+            kv = _abi.rmsnorm(kv, self.kv_norm.weight, self.eps)
+            return _abi.rope_tail(kv, rd, cos, sin, start_pos, 1)
+        return _abi.kv_window_prep(kv, self.kv_norm.weight, cos, sin, rd, start_pos, self.eps)
+
+    def _write_latents(self, latents, lc, g0, cos, sin):
+        rd = self.rope_head_dim
+        lat = latents.to(lc.dtype).contiguous()
+        if fakequant.DISABLE:
+            lat = _abi.rope_tail(lat, rd, cos, sin, g0 * self.ratio, self.ratio)
+            lc.comp_kv[:lat.shape[0], g0:g0 + lat.shape[1]] = lat
+            return
+        _abi.comp_write(lat, lc.comp_kv, g0, self.ratio, cos, sin, rd)
+
+    def forward(self, x: torch.Tensor, start_pos: int, cache, shared) -> torch.Tensor:
+        """x [b, n, dim] (post attn_norm), absolute positions [start_pos, start_pos + n)."""
+        bsz, n, _ = x.shape
+        rd = self.rope_head_dim
+        end_pos = start_pos + n
+        cos, sin = self._freqs(end_pos)
+        x = x.contiguous()
+
+        # queries
+        qr = self.q_norm(self.wq_a(x))
+        q = self.wq_b(qr).view(bsz, n, self.n_heads, self.head_dim).contiguous()
+        _abi.rope_tail(q, rd, cos, sin, start_pos, 1, out=q)
+
+        # this chunk's window KV
+        kv = self._kv_prologue(self.wkv(x).contiguous(), cos, sin, start_pos)
+
+        lc = cache.layers[self.layer_id]
+        wp = min(start_pos, self.window_size)
+        offset = wp + n                     # compressed entries follow window + chunk
+        cidx = None
+        comp, n_comp = None, 0
+        if self.ratio:
+            src = shared.kv_src_cache
+            compress_len = end_pos // self.ratio
+            latents = None
+            if self.is_kv_source:
+                latents = self.compressor(x, start_pos, lc.comp_state)
+                shared.kv_src_cache = src = lc
+            if self.is_index_source:
+                if self.indexer.owns_k:
+                    if latents is not None:
+                        self.indexer.publish_keys(latents, start_pos, cos, sin, lc)
+                    shared.index_src_cache = lc
+                if compress_len == 0:
+                    cidx = torch.zeros(bsz, n, 0, dtype=torch.int32, device=x.device)
+                else:
+                    index_k = shared.index_src_cache.index_k[:bsz, :compress_len]
+                    cidx = self.indexer(x, qr, start_pos, offset, cos, sin, index_k, shared)
+                shared.topk_idxs = cidx
+            else:
+                cidx = shared.topk_idxs
+            if latents is not None:
+                self._write_latents(latents, lc, start_pos // self.ratio, cos, sin)
+            if compress_len:
+                comp, n_comp = src.comp_kv[:bsz], compress_len
+
+        sink = torch.zeros_like(self.attn_sink) if self._break_sink else self.attn_sink
+        o = _abi.sparse_mla(q, lc.win_kv, kv, comp, n_comp, sink,
+                            cidx if cidx is not None and cidx.shape[-1] else None,
+                            self.softmax_scale, self.window_size, start_pos, cos, sin,
+                            0 if self._break_rope_inverse else rd)
+        lc.write_window(start_pos, kv)
+
+        # grouped block-diagonal wo_a in fp32, then wo_b (attention.py:176-179)
+        G, R = self.n_groups, self.o_lora_rank
+        og = o.view(bsz * n, G, -1).float().transpose(0, 1)                      # [G, bn, d]
+        wa = self.wo_a.weight.float().view(G, R, -1).transpose(1, 2).contiguous()  # [G, d, R]
+        oa = torch.matmul(og.contiguous(), wa).transpose(0, 1).reshape(bsz, n, G * R)
+        return self.wo_b(oa.to(x.dtype))

@@ -1,0 +1,227 @@
+/*
+ * dsv41.h -- C ABI of the MI355X (gfx950) DeepSeek-V4.1 sparse-attention hot path.
+ *
+ * One extern "C" entry point per kernel. Conventions shared by every entry point:
+ *   - all tensor arguments are raw device pointers to contiguous row-major memory,
+ *     described by explicit sizes (and, for caches, a batch stride in elements);
+ *   - `dtype` arguments take a dsv41_dtype value; bf16 is stored as raw 16-bit words;
+ *   - work is enqueued on `stream` (a hipStream_t; NULL = the default stream) and
+ *     nothing synchronises with the host; no entry point allocates device memory:
+ *     scratch space is passed in by the caller, sized by the *_workspace_bytes query;
+ *   - the return value is 0 on success, a negative dsv41_status for a contract
+ *     violation (bad size, dtype, null pointer, unsupported shape), or a positive
+ *     hipError_t from the launch; dsv41_last_error_string() then describes it
+ *     (thread-local, valid until the next call on the same thread);
+ *   - calls are stateless and reentrant.
+ *
+ * Reference citations name files of the reference repository (thedracle/deepseek-v41-mlx):
+ * the MLX modules under deepseek_v41_mlx/ and DeepSeek's TileLang kernels in
+ * docs/reference/kernel.py, whose wrappers are the native seam the reference's tests
+ * swap out (tests/test_parity.py:57-58).
+ */
+#ifndef DSV41_H
+#define DSV41_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  DSV41_F32 = 0,      /* float32 */
+  DSV41_BF16 = 1,     /* bfloat16 (raw uint16) */
+  DSV41_FP8_E4M3 = 2  /* OCP e4m3fn bytes + ue8m0 (biased exponent) scale bytes */
+} dsv41_dtype;
+
+typedef enum {
+  DSV41_OK = 0,
+  DSV41_E_ARG = -1,         /* null pointer or a size out of range */
+  DSV41_E_DTYPE = -2,       /* dtype not supported by this entry point */
+  DSV41_E_SHAPE = -3,       /* shape not supported (e.g. head_dim not a multiple of 32) */
+  DSV41_E_WORKSPACE = -4    /* workspace missing or too small */
+} dsv41_status;
+
+/* Library identification and the last error of the calling thread. */
+const char* dsv41_version(void);
+const char* dsv41_last_error_string(void);
+
+/* ---------------------------------------------------------------- fake-quant --
+ * In-place-capable (x == y allowed) QAT round trips over the last dimension,
+ * `rows` rows of `cols` elements, `cols % block == 0`. dtype is F32 or BF16 (in == out).
+ */
+
+/* fake_quant_fp8_ue8m0, deepseek_v41_mlx/fakequant.py:83-93;
+ * act_quant(x, block, scale_fmt="ue8m0", inplace=True), docs/reference/kernel.py:98-124. */
+int dsv41_fq_fp8_ue8m0(const void* x, void* y, int64_t rows, int32_t cols, int32_t block,
+                       int32_t dtype, hipStream_t stream);
+
+/* fake_quant_fp4_ue8m0, deepseek_v41_mlx/fakequant.py:96-106;
+ * fp4_act_quant(x, block, inplace=True), docs/reference/kernel.py:184-204. */
+int dsv41_fq_fp4_ue8m0(const void* x, void* y, int64_t rows, int32_t cols, int32_t block,
+                       int32_t dtype, hipStream_t stream);
+
+/* fake_quant_fp4_e4m3, deepseek_v41_mlx/fakequant.py:109-119;
+ * fp4_act_quant(x, block, inplace=True, scale_dtype=float8_e4m3fn), kernel.py:160-163. */
+int dsv41_fq_fp4_e4m3(const void* x, void* y, int64_t rows, int32_t cols, int32_t block,
+                      int32_t dtype, hipStream_t stream);
+
+/* ---------------------------------------------------------------- rope / norm --
+ */
+
+/* cos/sin tables [seqlen, half] of the fp32 angles t*freqs[i] (the trigonometric half of
+ * precompute_freqs_cis, deepseek_v41_mlx/layers.py:36-56; freqs[half] comes from the host). */
+int dsv41_rope_table(float* cos_out, float* sin_out, const float* freqs, int32_t seqlen,
+                     int32_t half, hipStream_t stream);
+
+/* rope_tail, deepseek_v41_mlx/layers.py:59-84: rotate adjacent pairs of the last `rd`
+ * channels of x [bsz, seqlen, heads, dim] (heads = 1 for 3-D tensors) by the angle of
+ * position pos_base + s * pos_step (s = token index); inverse != 0 conjugates.
+ * The first dim - rd channels are copied unchanged. x == y allowed. dim % 32 == 0 and
+ * dim / 32 a power of two <= 64. */
+int dsv41_rope_tail(const void* x, void* y, int32_t bsz, int32_t seqlen, int32_t heads,
+                    int32_t dim, int32_t rd, const float* cos_tab, const float* sin_tab,
+                    int32_t pos_base, int32_t pos_step, int32_t inverse, int32_t dtype,
+                    hipStream_t stream);
+
+/* RMSNorm, deepseek_v41_mlx/layers.py:20-33: y = cast(w * x * rsqrt(mean(x^2) + eps)),
+ * computed in fp32, over `rows` rows of `dim` elements. x == y allowed. */
+int dsv41_rmsnorm(const void* x, void* y, const float* weight, int64_t rows, int32_t dim,
+                  float eps, int32_t dtype, hipStream_t stream);
+
+/* ---------------------------------------------------------------- window KV --
+ */
+
+/* The window-KV prologue of Attention.__call__, deepseek_v41_mlx/attention.py:119-122:
+ * kv [bsz, n, dim] <- fake_quant_fp8_ue8m0(rope_tail(kv_norm(kv), positions start_pos+s), 32),
+ * in place, with the dtype rounding between the three steps that the reference performs. */
+int dsv41_kv_window_prep(void* kv, const float* norm_w, const float* cos_tab,
+                         const float* sin_tab, int32_t bsz, int32_t n, int32_t dim, int32_t rd,
+                         int32_t start_pos, float eps, int32_t dtype, hipStream_t stream);
+
+/* LayerCache.write_window, deepseek_v41_mlx/cache.py:61-67: the last min(n, window) rows
+ * of kv [bsz, n, dim] go to ring slots (pos) % window of win_kv [bsz, window, dim]. */
+int dsv41_window_write(void* win_kv, const void* kv, int32_t bsz, int32_t n, int32_t dim,
+                       int32_t window, int32_t start_pos, int32_t dtype, hipStream_t stream);
+
+/* window_idx_matrix, deepseek_v41_mlx/attention.py:40-50: out [n, min(window, wp+n)] int32. */
+int dsv41_window_idx(int32_t* out, int32_t wp, int32_t n, int32_t window, hipStream_t stream);
+
+/* ---------------------------------------------------------------- compressor --
+ */
+
+/* Compressor.__call__ after its two fp32 projections, deepseek_v41_mlx/compressor.py:58-79
+ * (ratio > 1): prepend the m = start_pos % ratio carried rows of kv_state/score_state
+ * [bsz, ratio, dim] (fp32, updated in place with the new remainder), pool every complete
+ * group with a per-channel softmax over the ratio axis, RMSNorm the pooled vector (after the
+ * reference's cast to dtype) and write latents [bsz, g, dim], g = (m + n) / ratio (latents
+ * may be NULL when g == 0). kv, score: [bsz, n, dim] fp32. dim <= 1024. */
+int dsv41_compress_pool(const float* kv, const float* score, float* kv_state, float* score_state,
+                        void* latents, const float* norm_w, int32_t bsz, int32_t n, int32_t dim,
+                        int32_t ratio, int32_t start_pos, float eps, int32_t dtype,
+                        hipStream_t stream);
+
+/* The compressed-cache write of Attention.__call__, deepseek_v41_mlx/attention.py:157-163:
+ * comp_kv[b, g0 + j] <- fake_quant_fp4_e4m3(rope_tail(latents[b, j], position (g0+j)*ratio), 16)
+ * for latents [bsz, g, dim]; comp_kv has `cache_bstride` elements per batch row. */
+int dsv41_comp_write(const void* latents, void* comp_kv, int64_t cache_bstride,
+                     const float* cos_tab, const float* sin_tab, int32_t bsz, int32_t g,
+                     int32_t dim, int32_t rd, int32_t g0, int32_t ratio, int32_t dtype,
+                     hipStream_t stream);
+
+/* Indexer.publish_keys after the wk projection, deepseek_v41_mlx/indexer.py:89-104:
+ * index_k[b, g0 + j] <- fake_quant_fp4_ue8m0(rope_tail(k_norm(k_raw[b, j]), (g0+j)*ratio), 32)
+ * for k_raw [bsz, g, dim]; index_k has `cache_bstride` elements per batch row. */
+int dsv41_index_key_publish(const void* k_raw, void* index_k, int64_t cache_bstride,
+                            const float* norm_w, const float* cos_tab, const float* sin_tab,
+                            int32_t bsz, int32_t g, int32_t dim, int32_t rd, int32_t g0,
+                            int32_t ratio, float eps, int32_t dtype, hipStream_t stream);
+
+/* ---------------------------------------------------------------- indexer --
+ */
+
+/* The index-query prologue, deepseek_v41_mlx/indexer.py:179-181: in place on
+ * q [bsz, n, heads, dim], q <- fake_quant_fp4_ue8m0(rope_tail(q, positions start_pos+s), 32). */
+int dsv41_index_q_prep(void* q, const float* cos_tab, const float* sin_tab, int32_t bsz,
+                       int32_t n, int32_t heads, int32_t dim, int32_t rd, int32_t start_pos,
+                       int32_t dtype, hipStream_t stream);
+
+/* Indexer scoring, deepseek_v41_mlx/indexer.py:183-198:
+ *   scores[b,s,t] = sum_h relu(q[b,s,h,:] . index_k[b,t,:]) * w[b,s,h]      (fp32)
+ *   w = round_dtype(w_raw * w_scale); t >= (start_pos+s+1)/ratio -> -inf;
+ *   candidates (optional, uint8 [bsz,n,nb], 0 = masked) -> -inf.
+ * q [bsz,n,heads,dim], w_raw [bsz,n,heads] in `dtype`; index_k rows of `dim` elements with
+ * `k_bstride` elements per batch row (the owner's cache read in place); scores [bsz,n,nb].
+ * dtype F32 or BF16; bf16 runs on MFMA and needs heads % 16 == 0 and dim % 32 == 0. */
+int dsv41_indexer_score(const void* q, const void* w_raw, float w_scale, const void* index_k,
+                        int64_t k_bstride, const uint8_t* candidates, float* scores,
+                        int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
+                        int32_t start_pos, int32_t ratio, int32_t dtype, hipStream_t stream);
+
+/* ---------------------------------------------------------------- top-k --
+ */
+
+/* Top-k selection, deepseek_v41_mlx/indexer.py:200-204: per row of scores [bsz*n, nb],
+ * the k = min(topk, nb) best positions (ties -> lowest position; -0.0 == +0.0), sorted
+ * ascending, written as idx + offset when idx < lens else -1, lens = (start_pos+s+1)/ratio,
+ * s = row % n. out [bsz*n, k] int32. nb <= 1<<22. */
+int dsv41_topk_select(const float* scores, int32_t* out, int64_t rows, int32_t n, int32_t nb,
+                      int32_t topk, int32_t start_pos, int32_t ratio, int32_t offset,
+                      hipStream_t stream);
+
+/* select_candidate_blocks, deepseek_v41_mlx/indexer.py:38-64: block maxima over blocks of
+ * block_size (padded with -inf), the block holding position lens-1 pinned to +inf, the best
+ * min(topk_blocks, n_blocks) blocks kept (ties -> lowest block) when their value is > -inf,
+ * expanded back to positions. keep [bsz*n, nb] uint8 (1 = candidate). lens: optional device
+ * int32 [n] of visible positions per query (NULL: (start_pos+s+1)/ratio). n_blocks <= 8192. */
+int dsv41_candidate_blocks(const float* scores, uint8_t* keep, int64_t rows, int32_t n,
+                           int32_t nb, int32_t topk_blocks, int32_t block_size,
+                           const int32_t* lens, int32_t start_pos, int32_t ratio,
+                           hipStream_t stream);
+
+/* ---------------------------------------------------------------- sparse MLA --
+ */
+
+/* Scratch bytes the sparse-MLA entry points need for split partial results at this shape
+ * (0 when no split is used). `rows_per_query` = window rows + index rows. */
+size_t dsv41_sparse_mla_workspace_bytes(int32_t bsz, int32_t m, int32_t heads, int32_t dim,
+                                        int32_t rows_per_query, int32_t dtype);
+
+/* sparse_attn, deepseek_v41_mlx/sparse_attention.py:34-60 and the TileLang kernel wrapper
+ * sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale), docs/reference/kernel.py:392-403:
+ *   o[b,s,h] = sum_j e^{l_j - M} kv[b,idx_j] / (sum_j e^{l_j - M} + e^{sink_h - M}),
+ *   l_j = scale * q[b,s,h].kv[b,idx_j] for idx_j >= 0 (others contribute nothing),
+ *   M = max(max_j l_j, sink_h, -1e30); K = V; an all-masked row gives 0.
+ * q, o [bsz,m,heads,dim]; kv [bsz,nkv,dim]; sink [heads] fp32; idx [bsz,m,k] int32
+ * (indices >= nkv are treated as masked). dtype F32 or BF16 (q, kv and o alike). */
+int dsv41_sparse_attn(const void* q, const void* kv, const float* sink, const int32_t* idx,
+                      void* o, int32_t bsz, int32_t m, int32_t heads, int32_t dim, int32_t nkv,
+                      int32_t k, float scale, int32_t dtype, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream);
+
+/* The attention core of Attention.__call__, deepseek_v41_mlx/attention.py:124-175, reading
+ * every KV source in place instead of concatenating them (attention.py:127, 165-168):
+ *   unified position u < wp            -> window ring slot (start_pos - wp + u) % window
+ *                   wp <= u < wp + n   -> chunk row u - wp              (this call's KV)
+ *                   u >= wp + n        -> comp row u - wp - n < n_comp  (the source owner's cache)
+ * with wp = min(start_pos, window). Query s sees the window positions
+ * [max(wp+s-window+1, 0), wp+s] (window_idx_matrix, attention.py:40-50) plus idx[b,s,:]
+ * (the indexer's output, already offset by wp + n; -1 masked; may be NULL with k = 0).
+ * Output o [bsz,n,heads,dim] gets the inverse rope on its last rd channels at position
+ * start_pos + s when rd > 0 (attention.py:174-175). win_kv [bsz,window,dim], chunk
+ * [bsz,n,dim], comp with comp_bstride elements per batch row. dtype F32 or BF16. */
+int dsv41_sparse_mla(const void* q, const void* win_kv, const void* chunk_kv,
+                     const void* comp_kv, int64_t comp_bstride, int32_t n_comp,
+                     const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
+                     int32_t n, int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
+                     float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                     int32_t dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV41_H */

@@ -1,0 +1,129 @@
+"""CPU checks of the boundary: libdsv41.so loads and exports exactly the C ABI that
+include/dsv41.h declares, the ctypes table matches the header, the host-side config mirrors
+the reference's topology rules, and wrappers refuse non-GPU tensors instead of falling back."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dsv41.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsv41_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    names = header_functions()
+    for must in ("dsv41_sparse_attn", "dsv41_sparse_mla", "dsv41_indexer_score", "dsv41_topk_select",
+                 "dsv41_candidate_blocks", "dsv41_compress_pool", "dsv41_comp_write",
+                 "dsv41_index_key_publish", "dsv41_fq_fp8_ue8m0", "dsv41_fq_fp4_ue8m0",
+                 "dsv41_fq_fp4_e4m3", "dsv41_rope_tail", "dsv41_last_error_string"):
+        assert must in names
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from dsv41 import _abi
+    lib = _abi.lib()
+    for name in header_functions():
+        assert hasattr(lib, name), f"{name} declared in dsv41.h but not exported"
+    assert set(_abi._SIGNATURES) == set(header_functions())
+    assert "gfx950" in _abi.version()
+
+
+def test_ctypes_arity_matches_header():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    from dsv41 import _abi
+    for name, args in _abi._SIGNATURES.items():
+        m = re.search(name + r"\s*\(([^)]*)\)", text)
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(args), name
+
+
+def test_workspace_query_is_host_only():
+    from dsv41 import _abi
+    # decode-sized work splits its index list across workgroups and needs scratch
+    assert _abi.mla_workspace_bytes(32, 1, 64, 512, 640, torch.bfloat16) > 0
+    # prefill-sized work does not
+    assert _abi.mla_workspace_bytes(1, 8192, 64, 512, 2176, torch.bfloat16) == 0
+    assert _abi.mla_workspace_bytes(1, 1, 4, 64, 16, torch.float32) == 0
+
+
+def test_wrappers_refuse_cpu_tensors():
+    from dsv41 import _abi
+    from dsv41.sparse_attention import sparse_attn
+    q = torch.zeros(1, 1, 4, 64)
+    with pytest.raises(ValueError, match="GPU"):
+        sparse_attn(q, torch.zeros(1, 8, 64), torch.zeros(4), torch.zeros(1, 1, 4, dtype=torch.int32), 0.1)
+    with pytest.raises(ValueError, match="GPU"):
+        _abi.fq_fp8_ue8m0(torch.zeros(4, 32))
+    with pytest.raises(ValueError, match="GPU"):
+        _abi.topk_select(torch.zeros(1, 1, 8), 4, 0, 1, 0)
+
+
+def test_contract_violations_are_reported_by_the_library():
+    """Host-side validation in the C ABI runs before any launch (null pointers, shapes)."""
+    from dsv41 import _abi
+    lib = _abi.lib()
+    rc = lib.dsv41_sparse_attn(None, None, None, None, None, 1, 1, 4, 64, 8, 4, ctypes.c_float(0.1), 1,
+                               None, 0, None)
+    assert rc == -1 and b"null" in lib.dsv41_last_error_string()
+    fake = ctypes.c_void_p(256)    # never dereferenced: rejected before launch
+    rc = lib.dsv41_fq_fp8_ue8m0(fake, fake, 4, 48, 32, 1, None)
+    assert rc == -3
+    rc = lib.dsv41_fq_fp8_ue8m0(fake, fake, 4, 64, 8, 1, None)
+    assert rc == -3 and b"block" in lib.dsv41_last_error_string()
+    rc = lib.dsv41_rmsnorm(fake, fake, fake, 4, 64, ctypes.c_float(1e-6), 7, None)
+    assert rc == -2
+    rc = lib.dsv41_topk_select(fake, fake, 1, 1, 1 << 23, 4, 0, 1, 0, None)
+    assert rc == -3
+    rc = lib.dsv41_compress_pool(fake, fake, fake, fake, fake, fake, 1, 1, 64, 1, 0, ctypes.c_float(0),
+                                 1, None)
+    assert rc == -1 and b"ratio" in lib.dsv41_last_error_string()
+
+
+# ------------------------------------------------------------------ host logic
+
+
+def test_model_args_topology_and_both_config_layouts():
+    from dsv41.config import ModelArgs
+    flat = {"dim": 256, "n_layers": 8, "compress_ratios": [0, 0, 2, 2, 2, 1, 1, 1],
+            "kv_source_layers": [2, 5], "index_source_layers": [2, 5, 7],
+            "candidate_source_layer": 5, "candidate_topk_blocks": 3, "candidate_block_size": 2,
+            "index_n_heads": 8, "rope_scaling": {"factor": 4.0, "original_max_position_embeddings": 64}}
+    hub = {"model_type": "x", "text_config": {"hidden_size": 256, "num_hidden_layers": 8,
+                                              "compress_ratios": [0, 0, 2, 2, 2, 1, 1, 1],
+                                              "kv_source_layer_ids": [2, 5],
+                                              "index_source_layer_ids": [2, 5, 7],
+                                              "candidate_source_layer_id": 5,
+                                              "candidate_topk_blocks": 3, "candidate_block_size": 2,
+                                              "index_n_heads": 8,
+                                              "rope_scaling": {"factor": 4.0,
+                                                               "original_max_position_embeddings": 64}}}
+    for a in (ModelArgs.from_dict(flat), ModelArgs.from_dict(hub)):
+        assert a.dim == 256 and a.n_layers == 8 and a.index_n_heads == 8
+        assert a.rope_factor == 4.0 and a.original_seq_len == 64
+        assert [a.compress_ratio(i) for i in range(10)] == [0, 0, 2, 2, 2, 1, 1, 1, 0, 0]
+        assert a.kv_source_for(4) == 2 and a.kv_source_for(7) == 5
+        assert a.index_source_for(6) == 5 and a.index_source_for(7) == 7
+        with pytest.raises(ValueError):
+            a.kv_source_for(1)
+    bad = ModelArgs(compress_ratios=(2, 1), kv_source_layers=(0,))
+    with pytest.raises(ValueError, match="ratio"):
+        bad.kv_source_for(1)
+
+
+def test_rope_frequencies_match_oracle_restatement():
+    from dsv41.layers import yarn_inv_freqs
+    from oracle import cpu_ref as R
+    for args in [(64, 65536, 160000.0, 16.0, 32, 1), (16, 0, 10000.0, 4.0, 32, 1), (16, 64, 40000.0, 4.0, 32, 1)]:
+        assert np.array_equal(yarn_inv_freqs(*args), R.yarn_freqs(*args))

@@ -1,0 +1,348 @@
+"""Kernel-level parity: each HIP entry point against the CPU oracle on the same seeded inputs.
+
+Bars: bit-exact for index work (top-k, candidate blocks, window indices) and for the
+fake-quants given identical inputs; 1e-5 max-abs for fp32 attention; 2e-2 relative
+(max |a-b| / max |b|) for bf16. Fused kernels that end in a fake-quant are compared
+allowing rare one-step rounding flips, which fp32 noise of ~1e-7 upstream of a rounding
+midpoint legitimately causes (the reference's own test hits the same thing,
+tests/test_parity.py:712-722); the flip rate and size are bounded in the test.
+"""
+
+from __future__ import annotations
+
+import os
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from common import max_abs, rel_max_diff, to_np
+from oracle import cpu_ref as R
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "fakequant_kat.npz")
+
+DT = {"f32": torch.float32, "bf16": torch.bfloat16}
+
+
+def dev(x, dt="f32", device="cuda"):
+    return torch.as_tensor(np.asarray(x, F32)).to(device=device, dtype=DT[dt]).contiguous()
+
+
+def rng_for(name):
+    return np.random.default_rng(zlib.crc32(name.encode()))
+
+
+def assert_fq_close(got, want, max_flip_frac=2e-3, step_rel=0.26):
+    """Equal except for rare single-step flips (each at most one grid step of its row)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    bad = got != want
+    frac = bad.mean()
+    assert frac <= max_flip_frac, f"{frac:.2e} of values differ"
+    if bad.any():
+        rowmax = np.abs(want).max(axis=-1, keepdims=True)
+        rowmax = np.broadcast_to(rowmax, want.shape)
+        assert np.all(np.abs(got - want)[bad] <= step_rel * rowmax[bad])
+
+
+# ------------------------------------------------------------------ fake-quant
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_fake_quants_bit_exact(gpu, dt):
+    from dsv41 import _abi
+    d = np.load(GOLDEN)
+    xs = [d["x0"], d["x1"], d["x2"], rng_for("fq").standard_normal((512, 512)).astype(F32) * 3]
+    for x in xs:
+        xin = R.cast(x, dt)
+        for fn, ref, blk in ((_abi.fq_fp8_ue8m0, R.fq_fp8_ue8m0, 32), (_abi.fq_fp4_ue8m0, R.fq_fp4_ue8m0, 32),
+                             (_abi.fq_fp4_e4m3, R.fq_fp4_e4m3, 16)):
+            got = to_np(fn(dev(xin, dt), blk))
+            want = ref(xin, blk, dt)
+            assert np.array_equal(got, want), f"{fn.__name__} {dt} shape {x.shape}"
+
+
+def test_fake_quant_golden_on_gpu(gpu):
+    from dsv41 import _abi
+    d = np.load(GOLDEN)
+    for n in range(3):
+        x = dev(d[f"x{n}"])
+        assert np.array_equal(to_np(_abi.fq_fp8_ue8m0(x, 32)), d[f"fp8_ue8m0_{n}"])
+        assert np.array_equal(to_np(_abi.fq_fp4_ue8m0(x, 32)), d[f"fp4_ue8m0_{n}"])
+        assert np.array_equal(to_np(_abi.fq_fp4_e4m3(x, 16)), d[f"fp4_e4m3_{n}"])
+
+
+# ------------------------------------------------------------------ rope, norm, tables
+
+
+def test_rope_table_matches_oracle(gpu):
+    from dsv41 import layers
+    for args in [(16, 300, 64, 10000.0, 4.0, 32, 1), (64, 70000, 65536, 160000.0, 16.0, 32, 1)]:
+        cos, sin = layers.precompute_freqs_cis(*args, device=gpu)
+        rc, rs = R.precompute_freqs_cis(*args)
+        assert max_abs(to_np(cos), rc) < 2e-6 and max_abs(to_np(sin), rs) < 2e-6
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_rope_tail_and_rmsnorm(gpu, dt):
+    from dsv41 import _abi
+    rng = rng_for("rope" + dt)
+    rc, rs = R.precompute_freqs_cis(64, 512, 65536, 160000.0, 16.0, 32, 1)
+    cos, sin = dev(rc), dev(rs)
+    x = R.cast(rng.standard_normal((2, 37, 8, 512)).astype(F32), dt)
+    for inverse in (False, True):
+        got = to_np(_abi.rope_tail(dev(x, dt), 64, cos, sin, 100, 3, inverse))
+        pos = 100 + 3 * np.arange(37)
+        want = R.rope_tail(x, 64, rc[pos], rs[pos], inverse, dt)
+        if dt == "f32":
+            assert max_abs(got, want) < 1e-5
+        else:
+            assert rel_max_diff(got, want) < 1e-2
+    w = (1 + 0.1 * rng.standard_normal(1280)).astype(F32)
+    y = R.cast(rng.standard_normal((33, 1280)).astype(F32) * 4, dt)
+    got = to_np(_abi.rmsnorm(dev(y, dt), dev(w), 1e-20))
+    want = R.rmsnorm(y, w, 1e-20, dt)
+    assert (max_abs(got, want) < 1e-5) if dt == "f32" else (rel_max_diff(got, want) < 1e-2)
+
+
+# ------------------------------------------------------------------ fused window / cache writes
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_kv_window_prep_and_ring_write(gpu, dt):
+    from dsv41 import _abi
+    rng = rng_for("kvw" + dt)
+    rc, rs = R.precompute_freqs_cis(64, 400, 65536, 160000.0, 16.0, 32, 1)
+    b, n, d, start = 3, 21, 512, 300
+    kv = R.cast(rng.standard_normal((b, n, d)).astype(F32), dt)
+    w = (1 + 0.1 * rng.standard_normal(d)).astype(F32)
+    t = dev(kv, dt)
+    _abi.kv_window_prep(t, dev(w), dev(rc), dev(rs), 64, start, 1e-20)
+    pos = start + np.arange(n)
+    want = R.fq_fp8_ue8m0(R.rope_tail(R.rmsnorm(kv, w, 1e-20, dt), 64, rc[pos], rs[pos], dtype=dt), 32, dt)
+    assert_fq_close(to_np(t), want)
+    # ring write: last min(n, W) rows to slots p % W
+    ring = torch.zeros(b, 16, d, dtype=DT[dt], device=gpu)
+    _abi.window_write(ring, t, start)
+    want_ring = np.zeros((b, 16, d), F32)
+    got_t = to_np(t)
+    for j in range(n - 16, n):
+        want_ring[:, (start + j) % 16] = got_t[:, j]
+    assert np.array_equal(to_np(ring), want_ring)
+
+
+@pytest.mark.parametrize("wp,n,window", [(0, 7, 8), (8, 13, 8), (128, 1, 128), (50, 300, 128)])
+def test_window_idx(gpu, wp, n, window):
+    from dsv41.attention import window_idx_matrix
+    assert np.array_equal(window_idx_matrix(wp, n, window, gpu).cpu().numpy(), R.window_idx_matrix(wp, n, window))
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_compress_pool_chunked(gpu, dt):
+    from dsv41 import _abi
+    rng = rng_for("pool" + dt)
+    b, d, r = 2, 512, 4
+    kv = rng.standard_normal((b, 45, d)).astype(F32)
+    sc = rng.standard_normal((b, 45, d)).astype(F32)
+    nw = (1 + 0.1 * rng.standard_normal(d)).astype(F32)
+    st = R.CompressorState(b, r, d)
+    ks, ss = dev(st.kv_state), dev(st.score_state)
+    pos = 0
+    for n in (3, 1, 1, 14, 2, 24):
+        want = R.compressor_pool(kv[:, pos:pos + n], sc[:, pos:pos + n], pos, st, r, nw, 1e-20, dt)
+        got = _abi.compress_pool(dev(kv[:, pos:pos + n]), dev(sc[:, pos:pos + n]), ks, ss, dev(nw), r, pos,
+                                 1e-20, DT[dt])
+        assert (want is None) == (got is None), f"chunk at {pos}"
+        if want is not None:
+            g = to_np(got)
+            assert (max_abs(g, want) < 1e-5) if dt == "f32" else (rel_max_diff(g, want) < 1e-2), f"chunk at {pos}"
+        rem = (pos + n) % r
+        assert np.array_equal(to_np(ks)[:, :rem], st.kv_state[:, :rem])
+        assert np.array_equal(to_np(ss)[:, :rem], st.score_state[:, :rem])
+        pos += n
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_comp_write_and_index_key_publish(gpu, dt):
+    from dsv41 import _abi
+    rng = rng_for("cw" + dt)
+    rc, rs = R.precompute_freqs_cis(64, 2048, 65536, 160000.0, 16.0, 32, 1)
+    b, g, d, di, g0, r = 2, 9, 512, 128, 100, 4
+    lat = R.cast(rng.standard_normal((b, g, d)).astype(F32), dt)
+    comp = torch.zeros(b, 256, d, dtype=DT[dt], device=gpu)
+    _abi.comp_write(dev(lat, dt), comp, g0, r, dev(rc), dev(rs), 64)
+    pos = (g0 + np.arange(g)) * r
+    want = R.fq_fp4_e4m3(R.rope_tail(lat, 64, rc[pos], rs[pos], dtype=dt), 16, dt)
+    got = to_np(comp)
+    assert_fq_close(got[:, g0:g0 + g], want)
+    assert not got[:, :g0].any() and not got[:, g0 + g:].any()
+    kr = R.cast(rng.standard_normal((b, g, di)).astype(F32), dt)
+    nw = (1 + 0.1 * rng.standard_normal(di)).astype(F32)
+    ik = torch.zeros(b, 256, di, dtype=DT[dt], device=gpu)
+    _abi.index_key_publish(dev(kr, dt), ik, g0, r, dev(nw), dev(rc), dev(rs), 64, 1e-20)
+    want = R.fq_fp4_ue8m0(R.rope_tail(R.rmsnorm(kr, nw, 1e-20, dt), 64, rc[pos], rs[pos], dtype=dt), 32, dt)
+    assert_fq_close(to_np(ik)[:, g0:g0 + g], want)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_index_q_prep(gpu, dt):
+    from dsv41 import _abi
+    rng = rng_for("iq" + dt)
+    rc, rs = R.precompute_freqs_cis(64, 600, 65536, 160000.0, 16.0, 32, 1)
+    q = R.cast(rng.standard_normal((2, 5, 64, 128)).astype(F32), dt)
+    t = dev(q, dt)
+    _abi.index_q_prep(t, dev(rc), dev(rs), 64, 500)
+    pos = 500 + np.arange(5)
+    want = R.fq_fp4_ue8m0(R.rope_tail(q, 64, rc[pos], rs[pos], dtype=dt), 32, dt)
+    assert_fq_close(to_np(t), want)
+
+
+# ------------------------------------------------------------------ indexer scoring
+
+
+@pytest.mark.parametrize("dt,hi,di,b,n,nb,start,use_cand", [
+    ("f32", 2, 32, 1, 128, 32, 0, False),          # C1 prefill
+    ("f32", 2, 32, 1, 1, 36, 143, True),           # C1 decode
+    ("bf16", 64, 128, 4, 1, 4096, 16383, False),    # C2-shaped decode
+    ("bf16", 64, 128, 1, 96, 1000, 3900, True),    # prefill chunk, causal + candidates
+    ("bf16", 32, 128, 2, 3, 777, 3100, False),     # released model's 32 index heads
+])
+def test_indexer_score(gpu, dt, hi, di, b, n, nb, start, use_cand):
+    from dsv41 import _abi
+    rng = rng_for(f"idx{dt}{hi}{n}{nb}")
+    r = 4
+    q = R.fq_fp4_ue8m0(rng.standard_normal((b, n, hi, di)).astype(F32), 32, dt)
+    k = R.fq_fp4_ue8m0(rng.standard_normal((b, nb + 5, di)).astype(F32), 32, dt)
+    w_raw = R.cast(rng.standard_normal((b, n, hi)).astype(F32), dt)
+    scale = R.index_weight_scale(hi, di, dt)
+    cand = (rng.random((b, n, nb)) < 0.7) if use_cand else None
+    kt = dev(k, dt)
+    got = _abi.indexer_score(dev(q, dt), dev(w_raw, dt), scale, kt[:, :nb], start, r,
+                             torch.as_tensor(cand).to(gpu) if use_cand else None)
+    w = R.cast(w_raw * scale, dt)
+    want = R.indexer_scores(q, k[:, :nb], w, start, r, cand)
+    g = to_np(got)
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isfinite(g), fin) and np.array_equal(g[~fin], want[~fin])
+    assert np.abs(g[fin] - want[fin]).max() <= 1e-5 * max(np.abs(want[fin]).max(), 1.0)
+
+
+# ------------------------------------------------------------------ top-k and candidates
+
+
+def _score_sets(rng, b, n, nb):
+    yield rng.standard_normal((b, n, nb)).astype(F32)
+    yield rng.choice(np.array([-np.inf, -1.0, -0.0, 0.0, 0.5, 0.5, 2.0], F32), size=(b, n, nb))
+    z = np.zeros((b, n, nb), F32)
+    z[..., ::3] = -0.0
+    yield z
+    yield np.round(rng.standard_normal((b, n, nb)) * 4).astype(F32)
+
+
+@pytest.mark.parametrize("b,n,nb,topk,start,r", [(2, 3, 40, 16, 100, 4), (4, 1, 4096, 512, 16383, 4),
+                                                  (1, 64, 1000, 256, 3000, 4), (2, 1, 16384, 512, 65535, 4),
+                                                  (1, 2, 300, 512, 1199, 4), (1, 5, 2049, 2048, 8191, 4)])
+def test_topk_bit_exact(gpu, b, n, nb, topk, start, r):
+    from dsv41 import _abi
+    rng = rng_for(f"topk{nb}{n}")
+    for s in _score_sets(rng, b, n, nb):
+        lens = R.query_lens(start, n, r)
+        s = np.where(np.arange(nb)[None, None] < lens[None, :, None], s, -np.inf).astype(F32)
+        off = 129
+        got = _abi.topk_select(dev(s), topk, start, r, off).cpu().numpy()
+        want = R.topk_indices(s, topk, lens, off)
+        assert np.array_equal(got, want), f"nb={nb} topk={topk}"
+
+
+@pytest.mark.parametrize("b,n,nb,tb,bs,start,r", [(2, 3, 40, 3, 2, 100, 4), (1, 7, 333, 20, 8, 1200, 4),
+                                                   (2, 1, 16384, 2048, 8, 65535, 4), (1, 4, 64, 100, 3, 0, 1)])
+def test_candidate_blocks_bit_exact(gpu, b, n, nb, tb, bs, start, r):
+    from dsv41 import _abi
+    from dsv41.indexer import select_candidate_blocks
+    rng = rng_for(f"cand{nb}{n}")
+    for s in _score_sets(rng, b, n, nb):
+        lens = R.query_lens(start, n, r)
+        s = np.where(np.arange(nb)[None, None] < lens[None, :, None], s, -np.inf).astype(F32)
+        got = _abi.candidate_blocks(dev(s), tb, bs, None, start, r).cpu().numpy()
+        want = R.select_candidate_blocks(s, lens, tb, bs)
+        assert np.array_equal(got, want)
+        got2 = select_candidate_blocks(dev(s), lens, tb, bs).cpu().numpy()
+        assert np.array_equal(got2, want)
+
+
+# ------------------------------------------------------------------ sparse attention
+
+
+@pytest.mark.parametrize("dt,b,m,h,d,nkv,k", [
+    ("f32", 1, 128, 4, 64, 160, 144),      # C1-sized prefill
+    ("f32", 2, 3, 6, 512, 300, 70),
+    ("bf16", 2, 5, 64, 512, 900, 300),     # prefill-shaped: 64 heads per workgroup
+    ("bf16", 32, 1, 64, 512, 4224, 640),   # C2 decode: split index lists + combine
+    ("bf16", 3, 2, 16, 576, 200, 97),      # head_dim 576 (512 + 64 reading)
+    ("bf16", 1, 4, 4, 64, 50, 33),         # heads < 16 (masked head tile)
+])
+def test_sparse_attn(gpu, dt, b, m, h, d, nkv, k):
+    from dsv41.sparse_attention import sparse_attn
+    rng = rng_for(f"sa{dt}{b}{m}{h}{d}")
+    # logits with std ~2 after the softmax scale: a peaked distribution, not a flat one
+    q = R.cast(rng.standard_normal((b, m, h, d)).astype(F32) * 2, dt)
+    kv = R.cast(rng.standard_normal((b, nkv, d)).astype(F32), dt)
+    sink = rng.standard_normal(h).astype(F32)
+    idx = rng.integers(-1, nkv + 3, size=(b, m, k)).astype(np.int32)   # includes -1 and >= nkv
+    idx[0, 0, :] = -1                                                   # all-masked row
+    got = to_np(sparse_attn(dev(q, dt), dev(kv, dt), dev(sink), torch.as_tensor(idx).to(gpu), d ** -0.5))
+    want = R.sparse_attn(q, kv, sink, np.where(idx < nkv, idx, -1), d ** -0.5, dtype=dt)
+    assert np.all(got[0, 0] == 0)
+    if dt == "f32":
+        assert max_abs(got, want) < 1e-5
+    else:
+        assert rel_max_diff(got, want) < 2e-2
+
+
+def _concat_reference(win, chunk, comp, n_comp, start, window):
+    """What attention.py:124-168 materializes: concat(prev window chrono, chunk, comp)."""
+    wp = min(start, window)
+    slots = (start - wp + np.arange(wp)) % window
+    return np.concatenate([win[:, slots], chunk, comp[:, :n_comp]], axis=1)
+
+
+@pytest.mark.parametrize("dt,b,n,h,d,window,start,n_comp,k", [
+    ("f32", 1, 1, 4, 64, 128, 143, 36, 16),       # C1 decode
+    ("f32", 2, 20, 4, 64, 8, 30, 12, 4),          # chunk longer than part of the ring
+    ("bf16", 32, 1, 64, 512, 128, 16383, 4096, 512),
+    ("bf16", 1, 40, 64, 512, 16, 100, 35, 24),
+    ("bf16", 2, 1, 64, 512, 128, 5, 0, 0),        # window only, ring still filling
+])
+def test_sparse_mla_in_place_sources(gpu, dt, b, n, h, d, window, start, n_comp, k):
+    from dsv41 import _abi
+    rng = rng_for(f"mla{dt}{b}{n}{start}")
+    rd = 16 if d == 64 else 64
+    rc, rs = R.precompute_freqs_cis(rd, start + n + 1, 65536, 160000.0, 16.0, 32, 1)
+    q = R.cast(rng.standard_normal((b, n, h, d)).astype(F32) * 2, dt)
+    win = R.cast(rng.standard_normal((b, window, d)).astype(F32), dt)
+    chunk = R.cast(rng.standard_normal((b, n, d)).astype(F32), dt)
+    comp = R.cast(rng.standard_normal((b, n_comp + 7, d)).astype(F32), dt)
+    sink = rng.standard_normal(h).astype(F32)
+    wp = min(start, window)
+    lens = R.query_lens(start, n, 4)
+    cidx = None
+    if k:
+        cidx = np.sort(rng.integers(0, max(n_comp, 1), size=(b, n, k)), axis=-1)
+        cidx = np.where(cidx < np.minimum(lens, n_comp)[None, :, None], cidx + wp + n, -1).astype(np.int32)
+    got = _abi.sparse_mla(dev(q, dt), dev(win, dt), dev(chunk, dt), dev(comp, dt) if n_comp else None, n_comp,
+                          dev(sink), torch.as_tensor(cidx).to(gpu) if k else None, d ** -0.5, window, start,
+                          dev(rc), dev(rs), rd)
+    kv_all = _concat_reference(win, chunk, comp, n_comp, start, window)
+    widx = np.broadcast_to(R.window_idx_matrix(wp, n, window)[None], (b, n, min(window, wp + n)))
+    idxs = np.concatenate([widx, cidx], axis=-1) if k else widx
+    o = R.sparse_attn(q, kv_all, sink, idxs, d ** -0.5, dtype=dt)
+    pos = start + np.arange(n)
+    want = R.rope_tail(o, rd, rc[pos], rs[pos], inverse=True, dtype=dt)
+    g = to_np(got)
+    if dt == "f32":
+        assert max_abs(g, want) < 1e-5
+    else:
+        assert rel_max_diff(g, want) < 2e-2

@@ -1,0 +1,167 @@
+"""Layer- and stack-level parity of the dsv41 path against the oracle, plus the C2 decode step.
+
+* C1 (tiny fp32, 4 layers, 128-token prefill then 16 decode steps): QAT simulation off on
+  both sides at 1e-5 max-abs (the strict pass), on at 5e-3 relative (the reference's own
+  threshold for the QAT-on pass, tests/test_parity.py:721-722: midpoint flips).
+* TOPO (every sharing role incl. candidates, ring wraps): the same two passes, GPU decode vs
+  GPU prefill tail, chunked vs single forward, and the negative controls of
+  tests/test_parity.py:736-760 (broken sink / rope inverse / sharing must move the output).
+* C2 (bf16, batch 32, 4096 compressed entries, top-512, 64 heads x 512): the decode step --
+  scores within 1e-5 of the float32 contraction, top-k bit-exact given those scores,
+  attention output within 2e-2 relative.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from common import C1, SEED_BASE, TOPO, args, load_stack, max_abs, model_args, rel_max_diff, to_np
+from oracle import cpu_ref as R
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+def _stacks(cfg, dt, seed, device):
+    from dsv41.model import AttentionStack
+    a = args(cfg)
+    params = R.make_params(a, seed, dt)
+    st = AttentionStack(model_args(cfg), {"f32": torch.float32, "bf16": torch.bfloat16}[dt], device)
+    load_stack(st, params)
+    return a, st, R.AttentionStack(a, params, dt)
+
+
+def _qat(enabled: bool):
+    import dsv41.fakequant as FQ
+    FQ.DISABLE = not enabled
+    R.DISABLE_FAKE_QUANT = not enabled
+
+
+@pytest.fixture
+def qat_restore():
+    yield
+    _qat(True)
+
+
+def _run(model, h, cache, splits, to_dev):
+    """Feed h[:, s:e] chunk by chunk; to_dev=None runs the oracle on numpy arrays."""
+    outs = []
+    for s, e in splits:
+        chunk = np.ascontiguousarray(h[:, s:e])
+        outs.append(to_np(model(to_dev(chunk), cache)) if to_dev is not None else model(chunk, cache))
+    return np.concatenate(outs, axis=1)
+
+
+@pytest.mark.parametrize("qat", [False, True], ids=["qat-off", "qat-on"])
+def test_c1_prefill_then_decode(gpu, qat, qat_restore):
+    _qat(qat)
+    a, st, ost = _stacks(C1, "f32", SEED_BASE, gpu)
+    rng = np.random.default_rng(SEED_BASE)
+    T = 128 + 16
+    h = rng.standard_normal((1, T, a.dim)).astype(F32)
+    splits = [(0, 128)] + [(t, t + 1) for t in range(128, T)]
+    want = _run(ost, h, R.ModelCache(a, 1, a.max_seq_len), splits, None)
+    got = _run(st, h, st.make_cache(1, a.max_seq_len), splits, lambda x: torch.from_numpy(x).to(gpu))
+    if qat:
+        assert rel_max_diff(got, want) < 5e-3
+    else:
+        assert max_abs(got, want) < 1e-5, f"max abs {max_abs(got, want):.3e}"
+
+
+@pytest.mark.parametrize("qat", [False, True], ids=["qat-off", "qat-on"])
+def test_topology_battery(gpu, qat, qat_restore):
+    _qat(qat)
+    a, st, ost = _stacks(TOPO, "f32", SEED_BASE + 3, gpu)
+    rng = np.random.default_rng(SEED_BASE + 3)
+    T = 40
+    h = rng.standard_normal((2, T, a.dim)).astype(F32)
+    dev = lambda x: torch.from_numpy(x).to(gpu)   # noqa: E731
+    full_o = _run(ost, h, R.ModelCache(a, 2, a.max_seq_len), [(0, T)], None)
+    full_g = _run(st, h, st.make_cache(2, a.max_seq_len), [(0, T)], dev)
+    dec = [(0, 32)] + [(t, t + 1) for t in range(32, T)]
+    dec_g = _run(st, h, st.make_cache(2, a.max_seq_len), dec, dev)
+    chunks = [(0, 13), (13, 14), (14, 27), (27, 31), (31, T)]
+    chk_g = _run(st, h, st.make_cache(2, a.max_seq_len), chunks, dev)
+    tol = (lambda g, w: rel_max_diff(g, w) < 5e-3) if qat else (lambda g, w: max_abs(g, w) < 1e-5)
+    assert tol(full_g, full_o), f"prefill vs oracle {max_abs(full_g, full_o):.3e}"
+    assert tol(dec_g, full_o), f"decode vs oracle prefill {max_abs(dec_g, full_o):.3e}"
+    assert tol(chk_g, full_o), f"chunked vs oracle {max_abs(chk_g, full_o):.3e}"
+
+
+def test_negative_controls_move_the_output(gpu):
+    a, st, _ = _stacks(TOPO, "f32", SEED_BASE + 4, gpu)
+    rng = np.random.default_rng(SEED_BASE + 4)
+    h = torch.from_numpy(rng.standard_normal((2, 30, a.dim)).astype(F32)).to(gpu)
+    base = to_np(st(h, st.make_cache(2, a.max_seq_len)))
+
+    def broken(setup, teardown):
+        setup()
+        try:
+            return rel_max_diff(to_np(st(h, st.make_cache(2, a.max_seq_len))), base)
+        finally:
+            teardown()
+
+    for attr in ("_break_sink", "_break_rope_inverse"):
+        d = broken(lambda: [setattr(l, attr, True) for l in st.layers],
+                   lambda: [setattr(l, attr, False) for l in st.layers])
+        assert d > 1e-3, attr
+    d = broken(lambda: setattr(st, "_break_sharing", True), lambda: setattr(st, "_break_sharing", False))
+    assert d > 1e-3
+    assert max_abs(to_np(st(h, st.make_cache(2, a.max_seq_len))), base) == 0.0
+
+
+def c2_inputs(nb=4096, start=16384, seed=SEED_BASE + 1, b=32):
+    """C2: batch 32, 16,384-token context -> 4,096 compressed entries, 64 heads x 512 (rope 64),
+    indexer 64 x 128, top-512, window 128. Cache and queries N(0,1)/sqrt(576); sinks N(0,1);
+    index queries/keys are fp4 fake-quantized N(0,1), head weights N(0,1) in bf16. Drawn in
+    this fixed order from one seeded CPU generator."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    H, D, Hi, Di, W = 64, 512, 64, 128, 128
+    s = 576 ** -0.5
+    t = {}
+    t["q"] = (torch.randn(b, 1, H, D, generator=g) * s).to(torch.bfloat16)
+    t["win"] = (torch.randn(b, W, D, generator=g) * s).to(torch.bfloat16)
+    t["chunk"] = (torch.randn(b, 1, D, generator=g) * s).to(torch.bfloat16)
+    t["comp"] = (torch.randn(b, nb, D, generator=g) * s).to(torch.bfloat16)
+    t["iq"] = torch.from_numpy(R.fq_fp4_ue8m0(torch.randn(b, 1, Hi, Di, generator=g).numpy(), 32, "bf16")).to(torch.bfloat16)
+    t["ik"] = torch.from_numpy(R.fq_fp4_ue8m0(torch.randn(b, nb, Di, generator=g).numpy(), 32, "bf16")).to(torch.bfloat16)
+    t["w"] = torch.randn(b, 1, Hi, generator=g).to(torch.bfloat16)
+    t["sink"] = torch.randn(H, generator=g)
+    return t, dict(H=H, D=D, Hi=Hi, Di=Di, W=W, nb=nb, start=start, K=512, rd=64, r=4)
+
+
+def test_c2_decode_step(gpu):
+    from dsv41.indexer import weight_scale
+    from dsv41.layers import precompute_freqs_cis
+    from dsv41.step import SparseDecodeStep
+    t, c = c2_inputs()
+    b = t["q"].shape[0]
+    d = {k: v.to(gpu) for k, v in t.items()}
+    cos, sin = precompute_freqs_cis(c["rd"], c["start"] + 1, 65536, 160000.0, 16.0, 32, 1, device=gpu)
+    step = SparseDecodeStep(b, c["H"], c["D"], c["rd"], c["Hi"], c["Di"], c["nb"], c["K"], c["W"], c["start"],
+                            c["r"], torch.bfloat16, gpu)
+    ws = weight_scale(c["Hi"], c["Di"], torch.bfloat16)
+    out, idx = step(d["q"], d["iq"], d["w"], ws, d["ik"], d["comp"], d["win"], d["chunk"], d["sink"], cos, sin)
+    torch.cuda.synchronize()
+    f = lambda x: x.float().numpy()   # noqa: E731
+    # scores
+    w = R.cast(f(t["w"]) * np.float32(ws), "bf16")
+    want_s = R.indexer_scores(f(t["iq"]), f(t["ik"]), w, c["start"], c["r"])
+    got_s = to_np(step.scores)
+    assert np.abs(got_s - want_s).max() <= 1e-5 * np.abs(want_s).max()
+    # top-k bit-exact given the GPU's scores
+    lens = R.query_lens(c["start"], 1, c["r"])
+    wp = min(c["start"], c["W"])
+    want_i = R.topk_indices(got_s, c["K"], lens, wp + 1)
+    assert np.array_equal(idx.cpu().numpy(), want_i)
+    # attention over concat(window, chunk, comp) with the reference's index layout
+    slots = (c["start"] - wp + np.arange(wp)) % c["W"]
+    kv_all = np.concatenate([f(t["win"])[:, slots], f(t["chunk"]), f(t["comp"])], axis=1)
+    widx = np.broadcast_to(R.window_idx_matrix(wp, 1, c["W"])[None], (b, 1, min(c["W"], wp + 1)))
+    o = R.sparse_attn(f(t["q"]), kv_all, f(t["sink"]), np.concatenate([widx, want_i], -1), c["D"] ** -0.5,
+                      dtype="bf16")
+    rc, rs = R.precompute_freqs_cis(c["rd"], c["start"] + 1, 65536, 160000.0, 16.0, 32, 1)
+    want_o = R.rope_tail(o, c["rd"], rc[[c["start"]]], rs[[c["start"]]], inverse=True, dtype="bf16")
+    assert rel_max_diff(to_np(out), want_o) < 2e-2

@@ -1,0 +1,421 @@
+"""Pins the CPU oracle (oracle/cpu_ref.py) before anything is checked against it.
+
+Every function is checked against something other than its own formula: library routines
+(torch's bf16 / float8_e4m3fn casts), the reference test's known-answer inputs with answers
+from an independent brute-force search (tests/golden/), float64 brute force, closed forms,
+and invariants. A few checks plant a mistake in a copy of the oracle and assert the check
+catches it. CPU only.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from common import C1, TOPO, args, max_abs
+from oracle import cpu_ref as R
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "fakequant_kat.npz")
+F32 = np.float32
+
+
+# ------------------------------------------------------------------ dtype emulation
+
+
+def test_bf16_rounding_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2 ** 32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(F32)
+    x = x[np.isfinite(x)]
+    ours = R.to_bf16(x)
+    ref = torch.from_numpy(x.copy()).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ours.view(np.uint32), ref.view(np.uint32))
+
+
+def _e4m3_points():
+    vals = []
+    for code in range(0x7F):
+        e, m = code >> 3, code & 7
+        vals.append(m * 2.0 ** -9 if e == 0 else (1 + m / 8) * 2.0 ** (e - 7))
+    vals = np.array(sorted(vals))
+    mids = (vals[1:] + vals[:-1]) / 2
+    pts = np.concatenate([vals, mids, np.nextafter(mids, 0), np.nextafter(mids, 1e9)]).astype(F32)
+    rng = np.random.default_rng(1)
+    rand = (rng.uniform(-1, 1, 200000) * 448).astype(F32)
+    tiny = (rng.uniform(-1, 1, 200000) * 2.0 ** -5).astype(F32)
+    pts = np.concatenate([pts, -pts, rand, tiny])
+    return pts[np.abs(pts) <= 448]
+
+
+def test_e4m3_rounding_matches_torch_float8_cast():
+    x = _e4m3_points()
+    ours = R.e4m3_round(x)
+    ref = torch.from_numpy(x.copy()).to(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(ours, ref)
+
+
+def test_pow2_ceil_log2_closed_form():
+    rng = np.random.default_rng(2)
+    x = np.exp(rng.uniform(-80, 80, 100000)).astype(F32)
+    x = np.concatenate([x, 2.0 ** np.arange(-120, 120, dtype=np.float64)]).astype(F32)
+    got = R.pow2_ceil_log2(x)
+    for xi, gi in zip(x[::97], got[::97]):
+        f, e = math.frexp(float(xi))
+        want = 2.0 ** (e - 1) if f == 0.5 else 2.0 ** e
+        assert gi == want
+
+
+def test_e2m1_round_is_nearest_even_on_grid():
+    grid = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+    mids = (grid[1:] + grid[:-1]) / 2
+    rng = np.random.default_rng(3)
+    v = np.concatenate([grid, mids, np.nextafter(mids, 0), np.nextafter(mids, 9),
+                        rng.uniform(0, 6, 5000)]).astype(F32)
+    v = np.concatenate([v, -v])
+    got = R.e2m1_round(v)
+    for vi, gi in zip(v, got):
+        d = np.abs(grid - abs(float(vi)))
+        cands = np.nonzero(d == d.min())[0]
+        code = cands[0] if len(cands) == 1 else [c for c in cands if c % 2 == 0][0]
+        assert gi == math.copysign(grid[code], float(vi))
+
+
+# ------------------------------------------------------------------ fake-quant known answers
+
+
+@pytest.mark.parametrize("n", [0, 1, 2])
+def test_fake_quants_match_known_answers(n):
+    d = np.load(GOLDEN)
+    x = d[f"x{n}"]
+    assert np.array_equal(R.fq_fp8_ue8m0(x, 32), d[f"fp8_ue8m0_{n}"])
+    assert np.array_equal(R.fq_fp4_ue8m0(x, 32), d[f"fp4_ue8m0_{n}"])
+    assert np.array_equal(R.fq_fp4_e4m3(x, 16), d[f"fp4_e4m3_{n}"])
+
+
+def test_fake_quant_known_answers_catch_a_planted_mistake(monkeypatch):
+    """A tie table with 0.75 rounding down (a plausible slip) must fail the fixture."""
+    d = np.load(GOLDEN)
+
+    def bad_e2m1(v):
+        v = np.asarray(v, F32)
+        mag = np.abs(v)
+        idx = np.zeros(mag.shape, np.int32)
+        for t in (0.25, 0.75, 1.25, 2.5, 5.0):
+            idx += mag > F32(t)
+        for t in (1.75, 3.5):
+            idx += mag >= F32(t)
+        return np.copysign(R._E2M1_LUT[idx], v).astype(F32)
+
+    monkeypatch.setattr(R, "e2m1_round", bad_e2m1)
+    assert not np.array_equal(R.fq_fp4_ue8m0(d["x2"], 32), d["fp4_ue8m0_2"])
+    assert not np.array_equal(R.fq_fp4_e4m3(d["x2"], 16), d["fp4_e4m3_2"])
+
+
+def test_fake_quant_values_are_exact_in_bf16():
+    """The QAT grids are representable in bf16, so a bf16 cache stores them losslessly."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((64, 128)).astype(F32) * 3
+    for q in (R.fq_fp8_ue8m0(x, 32), R.fq_fp4_ue8m0(x, 32), R.fq_fp4_e4m3(x, 16)):
+        assert np.array_equal(R.to_bf16(q), q)
+
+
+# ------------------------------------------------------------------ rope, norm
+
+
+def test_rope_inverse_undoes_rotation_and_is_a_complex_multiply():
+    rng = np.random.default_rng(5)
+    cos, sin = R.precompute_freqs_cis(16, 300, 64, 10000.0, 4.0, 32, 1)
+    x = rng.standard_normal((2, 300, 3, 64)).astype(F32)
+    y = R.rope_tail(x, 16, cos, sin)
+    assert np.array_equal(y[..., :48], x[..., :48])
+    z = R.rope_tail(y, 16, cos, sin, inverse=True)
+    assert max_abs(z, x) < 1e-5
+    # adjacent pairs (real, imag) times e^{i theta}, float64
+    ang = np.arctan2(sin.astype(np.float64), cos.astype(np.float64))
+    c = x[..., 48:].astype(np.float64).reshape(2, 300, 3, 8, 2)
+    zc = (c[..., 0] + 1j * c[..., 1]) * np.exp(1j * ang)[None, :, None, :]
+    assert max_abs(y[..., 48:].reshape(2, 300, 3, 8, 2)[..., 0], zc.real) < 1e-4
+    assert max_abs(y[..., 48:].reshape(2, 300, 3, 8, 2)[..., 1], zc.imag) < 1e-4
+
+
+def test_yarn_ramp_invariants():
+    base = R.yarn_freqs(64, 0, 160000.0, 16.0, 32, 1)
+    want = 1.0 / 160000.0 ** (np.arange(0, 64, 2) / 64)
+    assert np.allclose(base, want, rtol=1e-6)
+    y = R.yarn_freqs(64, 65536, 160000.0, 16.0, 32, 1)
+    ratio = y.astype(np.float64) / base
+    assert abs(ratio[0] - 1) < 1e-6                    # fastest dims keep their frequency
+    assert abs(ratio[-1] - 1 / 16) < 1e-6              # slowest dims are divided by factor
+    assert np.all(np.diff(ratio) <= 1e-9)              # monotone blend in between
+
+
+def test_rmsnorm_float64():
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((17, 512)).astype(F32) * 5
+    w = rng.standard_normal(512).astype(F32)
+    x64 = x.astype(np.float64)
+    want = w * x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + 1e-20)
+    assert np.allclose(R.rmsnorm(x, w), want, rtol=2e-6, atol=1e-6)
+
+
+# ------------------------------------------------------------------ window index, ring
+
+
+@pytest.mark.parametrize("wp,n,window", [(0, 7, 8), (0, 20, 8), (5, 3, 8), (8, 1, 8), (8, 13, 8),
+                                         (128, 1, 128), (0, 300, 128)])
+def test_window_idx_matrix_brute_force(wp, n, window):
+    got = R.window_idx_matrix(wp, n, window)
+    assert got.shape == (n, min(window, wp + n))
+    for i in range(n):
+        end = wp + i
+        want = set(range(max(0, end - window + 1), end + 1))
+        row = got[i]
+        assert set(row[row >= 0].tolist()) == want
+        assert len(row[row >= 0]) == len(want)
+
+
+def test_ring_reads_back_chronologically():
+    a = args(dict(C1, window_size=8))
+    lc = R.LayerCache(2, a, 1, 64)
+    rng = np.random.default_rng(7)
+    hist = np.zeros((2, 0, a.head_dim), F32)
+    pos = 0
+    for n in (3, 1, 9, 1, 2, 20):
+        kv = rng.standard_normal((2, n, a.head_dim)).astype(F32)
+        lc.write_window(pos, kv)
+        hist = np.concatenate([hist, kv], axis=1)
+        pos += n
+        wp = min(pos, 8)
+        assert np.array_equal(lc.window_chrono(pos), hist[:, pos - wp:pos])
+
+
+# ------------------------------------------------------------------ compressor
+
+
+def test_compressor_pool_chunk_invariance_and_float64():
+    rng = np.random.default_rng(8)
+    b, d, r = 2, 64, 4
+    a = args(C1)
+    kv = rng.standard_normal((b, 37, d)).astype(F32)
+    sc = rng.standard_normal((b, 37, d)).astype(F32)
+    nw = (1 + 0.1 * rng.standard_normal(d)).astype(F32)
+    st = R.CompressorState(b, r, d)
+    one = R.compressor_pool(kv, sc, 0, st, r, nw, a.norm_eps, "f32")
+    parts, st2, pos = [], R.CompressorState(b, r, d), 0
+    for n in (1, 2, 5, 1, 11, 3, 14):
+        lat = R.compressor_pool(kv[:, pos:pos + n], sc[:, pos:pos + n], pos, st2, r, nw, a.norm_eps, "f32")
+        if lat is not None:
+            parts.append(lat)
+        pos += n
+    assert np.array_equal(np.concatenate(parts, axis=1), one)
+    # the open group (37 % 4 = 1 row) is carried; rows past it are stale in any implementation
+    assert np.array_equal(st.kv_state[:, :1], kv[:, 36:37])
+    assert np.array_equal(st2.kv_state[:, :1], st.kv_state[:, :1])
+    assert np.array_equal(st2.score_state[:, :1], sc[:, 36:37])
+    # float64: softmax over the ratio axis per channel, then RMSNorm
+    k64 = kv[:, :36].astype(np.float64).reshape(b, 9, r, d)
+    s64 = sc[:, :36].astype(np.float64).reshape(b, 9, r, d)
+    w = np.exp(s64 - s64.max(2, keepdims=True))
+    pooled = (k64 * w / w.sum(2, keepdims=True)).sum(2)
+    want = nw * pooled / np.sqrt((pooled ** 2).mean(-1, keepdims=True) + 1e-20)
+    assert np.allclose(one, want, rtol=1e-5, atol=1e-5)
+
+
+# ------------------------------------------------------------------ indexer
+
+
+def test_indexer_scores_float64_and_masks():
+    rng = np.random.default_rng(9)
+    b, n, hi, di, nb = 2, 5, 4, 32, 23
+    q = rng.standard_normal((b, n, hi, di)).astype(F32)
+    k = rng.standard_normal((b, nb, di)).astype(F32)
+    w = rng.standard_normal((b, n, hi)).astype(F32)
+    start, r = 90, 4
+    got = R.indexer_scores(q, k, w, start, r)
+    dots = np.einsum("bshd,btd->bsht", q.astype(np.float64), k.astype(np.float64))
+    want = (np.maximum(dots, 0) * w[..., None]).sum(2)
+    for s in range(n):
+        lens = (start + s + 1) // r
+        assert np.allclose(got[:, s, :lens], want[:, s, :lens], rtol=1e-5, atol=1e-5)
+        assert np.all(np.isneginf(got[:, s, lens:]))
+    # ReLU: flipping every key's sign leaves only the formerly negative dots
+    got2 = R.indexer_scores(q, -k, w, start, r)
+    want2 = (np.maximum(-dots, 0) * w[..., None]).sum(2)
+    assert np.allclose(got2[:, 0, :22], want2[:, 0, :22], rtol=1e-5, atol=1e-5)
+
+
+def _brute_topk(row, k):
+    keyed = sorted(range(len(row)), key=lambda i: (-(0.0 if row[i] == 0 else float(row[i])), i))
+    return sorted(keyed[:k])
+
+
+def test_topk_brute_force_with_adversarial_ties():
+    rng = np.random.default_rng(10)
+    pool = np.array([-np.inf, -1.5, -0.0, 0.0, 0.25, 0.25, 1.0, 3.0, np.inf], F32)
+    for trial in range(200):
+        nb = int(rng.integers(1, 40))
+        n = int(rng.integers(1, 4))
+        s = rng.choice(pool, size=(1, n, nb)).astype(F32)
+        if trial % 3 == 0:
+            s = rng.standard_normal((1, n, nb)).astype(F32)
+        k = int(rng.integers(1, 50))
+        start, r = int(rng.integers(0, 4 * nb)), 4
+        lens = R.query_lens(start, n, r)
+        off = int(rng.integers(0, 200))
+        got = R.topk_indices(s, k, lens, off)
+        for qi in range(n):
+            sel = _brute_topk(s[0, qi], min(k, nb))
+            want = [i + off if i < lens[qi] else -1 for i in sel]
+            assert got[0, qi].tolist() == want
+
+
+def test_topk_check_catches_highest_index_ties(monkeypatch):
+    s = np.zeros((1, 1, 10), F32)
+    monkeypatch.setattr(R, "topk_order",
+                        lambda sc, k: np.argsort(-R._canon(sc)[..., ::-1], kind="stable")[..., :k] * -1 + sc.shape[-1] - 1)
+    got = R.topk_indices(s, 3, np.array([10]), 0)
+    assert got[0, 0].tolist() != _brute_topk(s[0, 0], 3)
+
+
+def _brute_candidates(row, lens, topk_blocks, bs):
+    width = len(row)
+    nbk = (width + bs - 1) // bs
+    blocks = []
+    for j in range(nbk):
+        vals = [float(v) for v in row[j * bs:(j + 1) * bs]]
+        blocks.append(max(vals + [-np.inf] * (bs - len(vals))))
+    last = math.floor((lens - 1) / bs)
+    blocks = [np.inf if j == last else v for j, v in enumerate(blocks)]
+    k = min(topk_blocks, nbk)
+    order = sorted(range(nbk), key=lambda j: (-blocks[j], j))[:k]
+    keep = [False] * nbk
+    for j in order:
+        keep[j] = blocks[j] > -np.inf
+    return [keep[t // bs] for t in range(width)]
+
+
+def test_candidate_blocks_brute_force():
+    rng = np.random.default_rng(11)
+    for trial in range(150):
+        nb = int(rng.integers(1, 30))
+        n = int(rng.integers(1, 4))
+        bs = int(rng.integers(1, 5))
+        s = rng.standard_normal((2, n, nb)).astype(F32)
+        s[rng.random(s.shape) < 0.3] = -np.inf
+        if trial % 4 == 0:
+            s = np.round(s)                              # ties between blocks
+        lens = rng.integers(0, nb + 1, size=n)
+        tb = int(rng.integers(0, 8))
+        got = R.select_candidate_blocks(s, lens, tb, bs)
+        for bi in range(2):
+            for qi in range(n):
+                assert got[bi, qi].tolist() == _brute_candidates(s[bi, qi], lens[qi], tb, bs)
+
+
+# ------------------------------------------------------------------ sparse attention
+
+
+def _brute_attn(q, kv, sink, idx, scale):
+    b, m, h, d = q.shape
+    out = np.zeros((b, m, h, d))
+    for bi in range(b):
+        for mi in range(m):
+            rows = [int(i) for i in idx[bi, mi] if i >= 0]
+            for hi in range(h):
+                logits = [scale * float(np.dot(q[bi, mi, hi].astype(np.float64), kv[bi, r].astype(np.float64)))
+                          for r in rows]
+                mx = max(logits + [float(sink[hi]), -1e30])
+                e = [math.exp(l - mx) for l in logits]
+                den = sum(e) + math.exp(float(sink[hi]) - mx)
+                acc = np.zeros(d)
+                for ei, r in zip(e, rows):
+                    acc += ei * kv[bi, r]
+                out[bi, mi, hi] = acc / den
+    return out
+
+
+def test_sparse_attn_float64_brute_force_and_closed_forms():
+    rng = np.random.default_rng(12)
+    b, m, h, d, n, k = 2, 3, 4, 32, 17, 9
+    q = rng.standard_normal((b, m, h, d)).astype(F32)
+    kv = rng.standard_normal((b, n, d)).astype(F32)
+    sink = rng.standard_normal(h).astype(F32)
+    idx = rng.integers(-1, n, size=(b, m, k)).astype(np.int32)
+    idx[1, 2] = -1                                          # an all-masked row -> zeros
+    got = R.sparse_attn(q, kv, sink, idx, d ** -0.5)
+    assert max_abs(got, _brute_attn(q, kv, sink, idx, d ** -0.5)) < 1e-5
+    assert np.all(got[1, 2] == 0)
+    # a single valid index: out = kv * e^l / (e^l + e^sink)
+    one = np.full((1, 1, 1), 3, np.int32)
+    g1 = R.sparse_attn(q[:1, :1], kv[:1], sink, one, 0.5)
+    lg = 0.5 * (q[0, 0].astype(np.float64) @ kv[0, 3].astype(np.float64))
+    want = kv[0, 3][None, :] * (np.exp(lg) / (np.exp(lg) + np.exp(sink.astype(np.float64))))[:, None]
+    assert max_abs(g1[0, 0], want) < 1e-5
+    # sink -> -inf: plain softmax
+    g2 = R.sparse_attn(q[:, :2], kv, np.full(h, -np.inf, F32), idx[:, :2], 0.3)
+    ref2 = _brute_attn(q[:, :2], kv, np.full(h, -1e300), idx[:, :2], 0.3)
+    assert max_abs(g2, ref2) < 1e-5
+
+
+def test_sparse_attn_check_catches_sink_in_numerator(monkeypatch):
+    """Planting a value row for the sink (a plausible mistake) must fail the brute force."""
+    rng = np.random.default_rng(13)
+    q = rng.standard_normal((1, 1, 2, 32)).astype(F32)
+    kv = rng.standard_normal((1, 5, 32)).astype(F32)
+    sink = np.array([2.0, 1.0], F32)
+    idx = np.array([[[0, 1, 2]]], np.int32)
+    good = R.sparse_attn(q, kv, sink, idx, 0.2)
+    bad = R.sparse_attn(q, kv, np.full(2, -np.inf, F32), idx, 0.2)   # sink dropped
+    want = _brute_attn(q, kv, sink, idx, 0.2)
+    assert max_abs(good, want) < 1e-6
+    assert max_abs(bad, want) > 1e-3
+
+
+# ------------------------------------------------------------------ layer / stack invariants
+
+
+def _stack(cfg, seed):
+    a = args(cfg)
+    return a, R.AttentionStack(a, R.make_params(a, seed))
+
+
+@pytest.mark.parametrize("cfg", [C1, TOPO], ids=["C1", "TOPO"])
+def test_stack_decode_equals_prefill_tail_and_chunked_equals_single(cfg):
+    a, st = _stack(cfg, 21)
+    rng = np.random.default_rng(22)
+    T = 40 if cfg is TOPO else 136
+    h = rng.standard_normal((2, T, a.dim)).astype(F32)
+    full = st(h, R.ModelCache(a, 2, a.max_seq_len))
+    cache = R.ModelCache(a, 2, a.max_seq_len)
+    outs = [st(h[:, :T - 8], cache)]
+    for t in range(T - 8, T):
+        outs.append(st(h[:, t:t + 1], cache))
+    dec = np.concatenate(outs, axis=1)
+    assert max_abs(dec, full) < 2e-5
+    cache = R.ModelCache(a, 2, a.max_seq_len)
+    cuts = sorted({0, 13, 14, 27, T - 9, T})
+    chunks = [st(h[:, s:e], cache) for s, e in zip(cuts[:-1], cuts[1:])]
+    assert max_abs(np.concatenate(chunks, axis=1), full) < 2e-5
+
+
+def test_topology_negative_controls_move_the_output():
+    a, st = _stack(TOPO, 23)
+    rng = np.random.default_rng(24)
+    h = rng.standard_normal((1, 30, a.dim)).astype(F32)
+    base = st(h, R.ModelCache(a, 1, a.max_seq_len))
+    for layer in st.layers:
+        layer.break_sink = True
+    broken = st(h, R.ModelCache(a, 1, a.max_seq_len))
+    for layer in st.layers:
+        layer.break_sink = False
+    assert max_abs(broken, base) > 1e-3
+    for layer in st.layers:
+        layer.break_rope_inverse = True
+    broken = st(h, R.ModelCache(a, 1, a.max_seq_len))
+    for layer in st.layers:
+        layer.break_rope_inverse = False
+    assert max_abs(broken, base) > 1e-3
