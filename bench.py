@@ -45,6 +45,8 @@ def parse():
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--eager", action="store_true",
+                   help="launch the decode kernels without HIP graphs (for counter-collecting profilers)")
     return p.parse_args()
 
 
@@ -160,8 +162,23 @@ def run_decode(args, torch, device):
         _abi.sparse_mla(d["q"], d["win"], d["chunk"], d["comp"], s.nb, d["sink"], d["idx"], s.D ** -0.5, s.W,
                         s.start, cos, sin, s.rd, out=d["step"].out, workspace=d["step"].workspace)
 
-    g_full = graph_of(full, sets, torch)
     per_replay = len(sets)
+    if args.eager:
+        # plain launches: each step's three kernels issued from Python (host overhead included)
+        for i in range(args.warmup):
+            full(sets[i % per_replay])
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(args.steps):
+            full(sets[i % per_replay])
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        log(f"[bench] eager decode step {ms * 1e3:.2f} us (host-bound timing)")
+        kern = {"indexer_score": float("nan"), "topk_select": float("nan"), "sparse_mla": float("nan")}
+        return s, ms, kern, sets, cos, sin, ws, []
+    g_full = graph_of(full, sets, torch)
     warm = max(1, args.warmup // per_replay)
     reps = max(1, args.steps // per_replay)
     for _ in range(warm):

@@ -5,7 +5,7 @@
 // bf16: one workgroup scores `rows_per_wg` cache rows of one query. The query's [heads x dim]
 // block is staged once in LDS and held by every wave as the MFMA A operand (heads = M); each
 // wave streams 16-row tiles of the owner's key cache straight from HBM as the B operand
-// (rows = N), two tiles in flight. Lane j ends with 4 heads x 1 row; ReLU * w and the in-lane
+// (rows = N), four tiles in flight. Lane j ends with 4 heads x 1 row; ReLU * w and the in-lane
 // head sum run on the accumulators, two cross-lane adds finish the head reduction, and lanes
 // 0..15 store 16 consecutive fp32 scores. Rows past the query's visibility are written as
 // -inf without touching the cache (causal prefill skips about half the bytes).
@@ -63,18 +63,19 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
   const uint8_t* cb = cand ? cand + (int64_t)qi * nb : nullptr;
   constexpr int NW = kIdxThreads / 64;
 
-  // two 16-row tiles per iteration: loads for both are issued before either is consumed
-  for (int t0 = r0 + 32 * wave; t0 < vis_end; t0 += 32 * NW) {
-    bf16x8 kk[2][KS];
+  // four 16-row tiles per iteration: every load of the four is issued before any is consumed
+  constexpr int U = 4;
+  for (int t0 = r0 + 16 * U * wave; t0 < vis_end; t0 += 16 * U * NW) {
+    bf16x8 kk[U][KS];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int row = min(t0 + 16 * u + l16, vis_end - 1);   // clamp: loads stay inside the cache
       const bf16_t* kr = kb + (int64_t)row * DIM;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) kk[u][ks] = ld_bf16x8(kr + ks * 8);
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int tb = t0 + 16 * u;
       if (tb >= vis_end) break;
       f32x4 acc[HT];
@@ -169,10 +170,11 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
   if (dtype != DSV41_BF16) return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported", what, dtype);
   DSV41_REQUIRE(aligned16(q) && aligned16(index_k), DSV41_E_ARG, "%s: q and index_k must be 16-byte aligned", what);
   DSV41_REQUIRE(k_bstride % 8 == 0, DSV41_E_ARG, "%s: k_bstride must be a multiple of 8", what);
-  // spread the visible rows over ~1024 workgroups, in multiples of one 8-wave sweep (256 rows)
-  const int64_t want = ((int64_t)nb * bsz * n + 1023) / 1024;
-  int rows_per_wg = (int)((want + 255) / 256 * 256);
-  if (rows_per_wg < 256) rows_per_wg = 256;
+  // ~256 workgroups over all rows (one per CU), in multiples of one 8-wave sweep of four tiles
+  // (512 rows): long-lived workgroups amortize staging the query block
+  const int64_t want = ((int64_t)nb * bsz * n + 255) / 256;
+  int rows_per_wg = (int)((want + 511) / 512 * 512);
+  if (rows_per_wg < 512) rows_per_wg = 512;
   if (rows_per_wg > 4096) rows_per_wg = 4096;
   dim3 grid((unsigned)((nb + rows_per_wg - 1) / rows_per_wg), (unsigned)(bsz * n));
 #define DSV41_IDX_CASE(HT_, KS_)                                                                          \

@@ -11,10 +11,42 @@
 namespace dsv41 {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_f32_16x16x16_bf16: 4 bf16 per lane, lane group g owns k = 4g..4g+3.
+__device__ __forceinline__ f32x4 mfma16x16x16(i16x4 a, i16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void gbl_void;
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i returns element (i % 4) of the 8-byte
+// reads of lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12. If lane r of a group reads 4 consecutive
+// 16-bit values of row (r / 4) at column 4 * (r % 4), lane i receives column i of those 4 rows:
+// a 4 x 16 block comes back transposed, one column per lane.
+__device__ __forceinline__ i16x4 lds_read_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p));
+}
+
+// One 16-byte-per-lane global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes land at
+// lds_base + 16 * l; lds_base must be wave-uniform. Completion is tracked by vmcnt only.
+__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((gbl_void*)src, (lds_void*)lds_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ i16x4 pack_bf16x4(const float* v) {
+  i16x4 r;
+  r[0] = (short)f2bf(v[0]);
+  r[1] = (short)f2bf(v[1]);
+  r[2] = (short)f2bf(v[2]);
+  r[3] = (short)f2bf(v[3]);
+  return r;
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }

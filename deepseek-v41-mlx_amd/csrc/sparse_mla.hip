@@ -4,20 +4,18 @@
 // K = V: one shared [dim] row per selected position serves all heads of a query, so a query is
 // a small GEMM of its [heads x dim] q block against the gathered [rows x dim] block.
 //
-// bf16 kernel (MFMA 16x16x32, fp32 accumulate), one workgroup = one query x (NHT*16) heads x one
-// split of its index list; 4 waves share every gathered 32-row tile through LDS and split the
-// head dimension between them:
-//   S^T[rows x heads] = K[rows x d] Q^T[d x heads]: each wave contracts a quarter of d; the four
-//     partial tiles meet in LDS and every wave sums them in the same order;
-//   online softmax in log2 units, the sink seeding the running max and denominator of split 0
-//     (sink in the denominator only, no value row); masked rows contribute nothing;
-//   O^T[d x heads] += V^T P^T: each wave owns a quarter of d; P^T comes straight from the S^T
-//     accumulators (same lane layout), V^T is read from the row-major LDS tile.
-// Rows are gathered with one 1 KB coalesced read per wave per row (d = 512) and the next tile's
-// reads are in flight while the current one is computed. Queries with too little parallelism
-// (decode) split their index list across workgroups and a combine kernel merges the partial
-// (max, denominator, numerator) triples. The epilogue divides, rounds to bf16 as the reference
-// does, then applies the inverse rope to the last rd channels (attention.py:174-175).
+// bf16 kernels (MFMA, fp32 accumulate). A wave owns 16 heads of one query:
+//   S^T[rows x heads] = K[rows x d] Q^T[d x heads]   (16x16x32, K rows from LDS, Q^T in registers)
+//   online softmax in log2 units with lazy rescaling; the sink seeds the running max and the
+//     denominator once per head (sink in the denominator only, no value row); masked rows give 0;
+//   O^T[d x heads] += V^T P^T   (P^T straight from the S^T accumulators -- same lane layout --
+//     V^T through the LDS transpose read ds_read_b64_tr_b16).
+// Selected rows are gathered with global_load_lds_dwordx4 (one 1 KB row per wave instruction at
+// d = 512) into LDS ring buffers, so several tiles are in flight without staging registers.
+// Decode (few queries) splits each query's index list across workgroups; a combine kernel
+// merges the partial (max, denominator, numerator) triples. The epilogue divides, rounds to bf16
+// as the reference does, then applies the inverse rope to the last rd channels
+// (attention.py:174-175).
 //
 // fp32 kernel: a plain FMA implementation for the 1e-5 parity configs.
 #include "mfma.h"
@@ -94,16 +92,79 @@ __device__ __forceinline__ void rope_inv_pair(const MlaArgs& a, int D, int qs, i
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegFloor = -1e30f;
 
-template <int D, int NHT>
-__global__ __launch_bounds__(256) void mla_bf16_kernel(MlaArgs a) {
+// Masked list entries gather this zero row, so every chunk issues the same number of DMA loads
+// (their count is what s_waitcnt vmcnt waits on) and padded LDS rows hold finite zeros.
+__device__ __align__(16) uint4 g_zero_row[128] = {};
+
+constexpr float kRescale = 8.0f;       // lazy softmax rescaling threshold (log2 units)
+constexpr int kDecChunk = 16;          // rows per wave chunk (decode kernel)
+constexpr int kMaxSplitList = 1024;    // list entries one decode split stages in LDS
+constexpr int kPreTile = 32;           // rows per shared tile (prefill kernel)
+constexpr int kMaxPreList = 2304;      // list entries the prefill kernel stages in LDS
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N == 0 || N == 8 || N == 16 || N == 32, "vmcnt immediate");
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+}
+
+__device__ __forceinline__ bf16x8 join_bf16x8(i16x4 lo, i16x4 hi) {
+  struct P { i16x4 a, b; } p{lo, hi};
+  return __builtin_bit_cast(bf16x8, p);
+}
+
+// The 64-bit value lane `r` holds as (lo, hi). readlane returns a signed int: both halves are
+// widened through uint32_t so the low word never sign-extends into the high one.
+__device__ __forceinline__ uint64_t lane_u64(uint32_t lo, uint32_t hi, int r) {
+  const uint32_t l = (uint32_t)__builtin_amdgcn_readlane((int)lo, r);
+  const uint32_t h = (uint32_t)__builtin_amdgcn_readlane((int)hi, r);
+  return ((uint64_t)h << 32) | (uint64_t)l;
+}
+
+// DMA one KV row (or the zero row) of D bf16 into LDS at `dst` (wave-uniform).
+template <int D>
+__device__ __forceinline__ void dma_row(const bf16_t* p, uint8_t* dst, int lane) {
+  constexpr int CPR = D / 8, IPR = (CPR + 63) / 64;
+  const uint8_t* src = p ? reinterpret_cast<const uint8_t*>(p) : reinterpret_cast<const uint8_t*>(g_zero_row);
+#pragma unroll
+  for (int ii = 0; ii < IPR; ++ii) {
+    const int ch = ii * 64 + lane;
+    if (CPR % 64 == 0 || ch < CPR) dma16(src + ch * 16, dst + ii * 1024);
+  }
+}
+
+// Store 4 consecutive output channels d0..d0+3 of one head: divide, round to bf16 (the
+// reference's cast at the end of sparse_attn), inverse rope, round again, 8-byte store.
+__device__ __forceinline__ void store_out4(const MlaArgs& a, int D, int qs, bf16_t* orow, int d0, f32x4 o, float den) {
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = round_bf16(o[i] / den);
+  rope_inv_pair(a, D, qs, d0, v[0], v[1], true);
+  rope_inv_pair(a, D, qs, d0 + 2, v[2], v[3], true);
+  uint2 st;
+  st.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+  st.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+  *reinterpret_cast<uint2*>(orow + d0) = st;
+}
+
+// Decode: few queries. Workgroup = (query, 16 heads, split of the index list); each of the 4
+// waves walks its own 16-row chunks of the split (chunks w, w+4, ...), gathering rows straight
+// into a private double-buffered LDS slot with global_load_lds; the waves merge in LDS at the end.
+template <int D>
+__global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
   constexpr int KS = D / 32, DT = D / 16;
-  constexpr int KSW = (KS + 3) / 4, DTW = (DT + 3) / 4;
-  constexpr int RS = D * 2 + 16;   // padded LDS row stride, bytes
-  constexpr int CPR = D / 8;       // 16-byte chunks per row
-  constexpr int CPT = D / 64;      // chunks per thread per 32-row tile
-  __shared__ __align__(16) uint8_t kv_lds[32 * RS];
-  __shared__ __align__(16) f32x4 xch[4][NHT][2][64];
-  __shared__ uint32_t vmask_sh;
+  constexpr int RS = D * 2 + 16;
+  constexpr int IPR = (D / 8 + 63) / 64;
+  constexpr int NL = kDecChunk * IPR;           // DMA instructions per chunk
+  constexpr int BUF = kDecChunk * RS;
+  static_assert(DT % 4 == 0, "head_dim must be a multiple of 64");
+  static_assert(4 * DT * 64 * 16 <= 4 * 2 * BUF, "merge buffer must fit in the chunk buffers");
+  __shared__ __align__(16) uint8_t lds[4 * 2 * BUF];
+  __shared__ uint64_t rows[kMaxSplitList];      // resolved row addresses, 0 = masked
+  __shared__ float2 ml_x[4][64];
 
   const KvSrc& S = a.src;
   const int unit = blockIdx.x, hg = blockIdx.y, sp = blockIdx.z;
@@ -112,197 +173,256 @@ __global__ __launch_bounds__(256) void mla_bf16_kernel(MlaArgs a) {
   const int wc = window_count(S, qs);
   const int L = wc + S.k;
   const int e_begin = sp * a.per_split;
-  const int e_end = min(e_begin + a.per_split, L);
-  const int ks0 = (KS * wave) / 4, ks1 = (KS * (wave + 1)) / 4;
-  const int dt0 = (DT * wave) / 4, dt1 = (DT * (wave + 1)) / 4;
-  const int hbase = hg * NHT * 16;
-  const float sl2 = a.scale * kLog2e;
+  const int cnt = max(min(e_begin + a.per_split, L) - e_begin, 0);
+  // resolve every entry of the split once (segment, ring slot, batch row): the gather loop then
+  // spends a few instructions per row
+  for (int e = tid; e < cnt; e += 256)
+    rows[e] = reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, list_pos(S, b, a.m, qs, e_begin + e, wc), D));
+  __syncthreads();
 
-  // Q^T as the MFMA B operand: lane -> head (hbase + ht*16 + l16), k-chunk 8g of k-step ks
-  bf16x8 qb[NHT][KSW];
-  const bf16_t* qrow = reinterpret_cast<const bf16_t*>(a.q) + (int64_t)unit * a.heads * D;
-  float m_run[NHT], l_run[NHT];
+  const int h = hg * 16 + l16;
+  const bool hok = h < a.heads;
+  bf16x8 qb[KS];
+  {
+    const bf16_t* qrow = reinterpret_cast<const bf16_t*>(a.q) + ((int64_t)unit * a.heads + (hok ? h : 0)) * D;
 #pragma unroll
-  for (int ht = 0; ht < NHT; ++ht) {
-    const int h = hbase + ht * 16 + l16;
-#pragma unroll
-    for (int kk = 0; kk < KSW; ++kk) {
-      const int ks = ks0 + kk;
-      qb[ht][kk] = (h < a.heads && ks < ks1) ? ld_bf16x8(qrow + (int64_t)h * D + ks * 32 + 8 * g) : zero_bf16x8();
-    }
-    if (sp == 0 && h < a.heads) {
-      const float s2 = a.sink[h] * kLog2e;
-      m_run[ht] = fmaxf(s2, kNegFloor);
-      l_run[ht] = exp2f(s2 - m_run[ht]);
-    } else {
-      m_run[ht] = kNegFloor;
-      l_run[ht] = 0.0f;
-    }
+    for (int ks = 0; ks < KS; ++ks) qb[ks] = hok ? ld_bf16x8(qrow + ks * 32 + 8 * g) : zero_bf16x8();
   }
-  f32x4 acc_o[NHT][DTW];
+  const float sl2 = a.scale * kLog2e;
+  float m_run = kNegFloor, l_run = 0.0f;   // m_run: the exponent reference of acc and l_run
+  if (sp == 0 && wave == 0 && hok) {
+    const float s2 = a.sink[h] * kLog2e;
+    m_run = fmaxf(s2, kNegFloor);
+    l_run = exp2f(s2 - m_run);
+  }
+  f32x4 acc[DT];
 #pragma unroll
-  for (int ht = 0; ht < NHT; ++ht)
-#pragma unroll
-    for (int dd = 0; dd < DTW; ++dd) acc_o[ht][dd] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  uint4 pf[CPT];
-  auto load_tile = [&](int e0) {
+  uint8_t* wbuf = lds + wave * (2 * BUF);
+  const int nchunk = (cnt + kDecChunk - 1) / kDecChunk;
+  auto issue = [&](int c, int slot) -> uint32_t {
+    uint8_t* dst = wbuf + slot * BUF;
+    const int mine = c * kDecChunk + (lane & (kDecChunk - 1));      // one LDS read for the chunk
+    const uint64_t mp = mine < cnt ? rows[mine] : 0ull;
+    const uint32_t vm = (uint32_t)__ballot(mp != 0ull) & ((1u << kDecChunk) - 1u);
+    const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int ci = tid + 256 * c;
-      const int r = ci / CPR, col = ci - (ci / CPR) * CPR;
-      const int e = e0 + r;
-      const bf16_t* p = e < e_end ? row_ptr<bf16_t>(S, b, list_pos(S, b, a.m, qs, e, wc), D) : nullptr;
-      pf[c] = p ? *reinterpret_cast<const uint4*>(p + col * 8) : make_uint4(0, 0, 0, 0);
+    for (int r = 0; r < kDecChunk; ++r) {
+      dma_row<D>(reinterpret_cast<const bf16_t*>(lane_u64(lo, hi, r)), dst + r * RS, lane);
     }
+    return vm;
   };
 
-  if (e_begin < e_end) load_tile(e_begin);
-  for (int e0 = e_begin; e0 < e_end; e0 += 32) {
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int ci = tid + 256 * c;
-      const int r = ci / CPR, col = ci - (ci / CPR) * CPR;
-      *reinterpret_cast<uint4*>(kv_lds + r * RS + col * 16) = pf[c];
+  int slot = 0;
+  uint32_t vm_cur = wave < nchunk ? issue(wave, 0) : 0u;
+  for (int c = wave; c < nchunk; c += 4) {
+    uint32_t vm_nxt = 0u;
+    if (c + 4 < nchunk) {
+      vm_nxt = issue(c + 4, slot ^ 1);
+      wait_vmcnt<NL>();
+    } else {
+      wait_vmcnt<0>();
     }
-    if (wave == 0) {
-      bool v = false;
-      if (lane < 32) {
-        const int e = e0 + lane;
-        v = e < e_end && row_ptr<bf16_t>(S, b, list_pos(S, b, a.m, qs, e, wc), D) != nullptr;
-      }
-      const uint64_t bal = __ballot(v);
-      if (lane == 0) vmask_sh = (uint32_t)bal;
+    const uint8_t* buf = wbuf + slot * BUF;
+    f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;      // two independent MFMA chains
+#pragma unroll
+    for (int ks = 0; ks < KS; ks += 2) {
+      s0 = mfma16x16x32(ld_bf16x8(buf + l16 * RS + (ks * 32 + 8 * g) * 2), qb[ks], s0);
+      s1 = mfma16x16x32(ld_bf16x8(buf + l16 * RS + (ks * 32 + 32 + 8 * g) * 2), qb[ks + 1], s1);
     }
-    __syncthreads();
-    const uint32_t vmask = vmask_sh;
-    if (e0 + 32 < e_end) load_tile(e0 + 32);
-
-    // partial S^T over this wave's share of d
-    f32x4 sacc[NHT][2];
+    const f32x4 sacc = s0 + s1;
+    float p[4];
+    float tmax = kNegFloor;
 #pragma unroll
-    for (int ht = 0; ht < NHT; ++ht) sacc[ht][0] = sacc[ht][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < KSW; ++kk) {
-      const int ks = ks0 + kk;
-      if (ks < ks1) {
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-          const bf16x8 A = ld_bf16x8(kv_lds + (rt * 16 + l16) * RS + (ks * 32 + 8 * g) * 2);
-#pragma unroll
-          for (int ht = 0; ht < NHT; ++ht) sacc[ht][rt] = mfma16x16x32(A, qb[ht][kk], sacc[ht][rt]);
-        }
-      }
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = (vm_cur >> (4 * g + i)) & 1u;
+      const float l2 = sacc[i] * sl2;
+      p[i] = ok ? l2 : -INFINITY;
+      if (ok) tmax = fmaxf(tmax, l2);
     }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const bool grow = tmax > m_run + kRescale;
+    if (__any(grow)) {
+      const float alpha = grow ? exp2f(m_run - tmax) : 1.0f;
 #pragma unroll
-    for (int ht = 0; ht < NHT; ++ht) {
-      xch[wave][ht][0][lane] = sacc[ht][0];
-      xch[wave][ht][1][lane] = sacc[ht][1];
+      for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+      l_run *= alpha;
+      m_run = grow ? tmax : m_run;
     }
-    __syncthreads();
-
-    bf16x8 pb[NHT];
+    float psum = 0.0f;
 #pragma unroll
-    for (int ht = 0; ht < NHT; ++ht) {
-      float p[8];
-      float tmax = kNegFloor;
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        const f32x4 s4 = ((xch[0][ht][rt][lane] + xch[1][ht][rt][lane]) + xch[2][ht][rt][lane]) + xch[3][ht][rt][lane];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = rt * 16 + 4 * g + i;
-          const bool ok = (vmask >> r) & 1u;
-          const float l2 = s4[i] * sl2;
-          p[rt * 4 + i] = ok ? l2 : -INFINITY;
-          if (ok) tmax = fmaxf(tmax, l2);
-        }
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float mnew = fmaxf(m_run[ht], tmax);
-      const float alpha = exp2f(m_run[ht] - mnew);
-      float psum = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        p[e] = exp2f(p[e] - mnew);
-        psum += p[e];
-      }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
-      l_run[ht] = l_run[ht] * alpha + psum;
-      m_run[ht] = mnew;
-#pragma unroll
-      for (int dd = 0; dd < DTW; ++dd) acc_o[ht][dd] *= alpha;
-      pb[ht] = pack_bf16x8(p);
+    for (int i = 0; i < 4; ++i) {
+      p[i] = exp2f(p[i] - m_run);
+      psum += p[i];
     }
-
-    // O^T += V^T P^T over this wave's share of d
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    l_run += psum;
+    const i16x4 pb = pack_bf16x4(p);
 #pragma unroll
-    for (int dd = 0; dd < DTW; ++dd) {
-      const int dt = dt0 + dd;
-      if (dt < dt1) {
-        const uint8_t* col = kv_lds + (dt * 16 + l16) * 2;
-        uint32_t w4[4];
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-          const int r = rt * 16 + 4 * g;
-          const uint32_t v0 = *reinterpret_cast<const uint16_t*>(col + (r + 0) * RS);
-          const uint32_t v1 = *reinterpret_cast<const uint16_t*>(col + (r + 1) * RS);
-          const uint32_t v2 = *reinterpret_cast<const uint16_t*>(col + (r + 2) * RS);
-          const uint32_t v3 = *reinterpret_cast<const uint16_t*>(col + (r + 3) * RS);
-          w4[rt * 2 + 0] = v0 | (v1 << 16);
-          w4[rt * 2 + 1] = v2 | (v3 << 16);
-        }
-        const bf16x8 A = as_bf16x8(make_uint4(w4[0], w4[1], w4[2], w4[3]));
-#pragma unroll
-        for (int ht = 0; ht < NHT; ++ht) acc_o[ht][dd] = mfma16x16x32(A, pb[ht], acc_o[ht][dd]);
-      }
+    for (int dt = 0; dt < DT; ++dt) {
+      const i16x4 va = lds_read_tr16(buf + (4 * g + (l16 >> 2)) * RS + (dt * 16 + 4 * (l16 & 3)) * 2);
+      acc[dt] = mfma16x16x16(va, pb, acc[dt]);
     }
-    __syncthreads();
+    vm_cur = vm_nxt;
+    slot ^= 1;
   }
 
-  if (a.splits == 1) {
+  // merge the four waves' (m, l, O) in LDS; wave w then owns dim tiles [w*DT/4, (w+1)*DT/4)
+  __syncthreads();
+  float* xo = reinterpret_cast<float*>(lds);
 #pragma unroll
-    for (int ht = 0; ht < NHT; ++ht) {
-      const int h = hbase + ht * 16 + l16;
-      if (h >= a.heads) continue;
-      const float den = l_run[ht];
-      bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + h) * D;
+  for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(xo + ((wave * DT + dt) * 64 + lane) * 4) = acc[dt];
+  ml_x[wave][lane] = make_float2(m_run, l_run);
+  __syncthreads();
+  float M = kNegFloor;
 #pragma unroll
-      for (int dd = 0; dd < DTW; ++dd) {
-        const int dt = dt0 + dd;
-        if (dt >= dt1) continue;
-        const int d0 = dt * 16 + 4 * g;
-        float v[4];
+  for (int w = 0; w < 4; ++w) M = fmaxf(M, ml_x[w][lane].x);
+  float wsc[4], den = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = round_bf16(acc_o[ht][dd][i] / den);
-        rope_inv_pair(a, D, qs, d0, v[0], v[1], true);
-        rope_inv_pair(a, D, qs, d0 + 2, v[2], v[3], true);
-        uint2 st;
-        st.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-        st.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-        *reinterpret_cast<uint2*>(orow + d0) = st;
-      }
+  for (int w = 0; w < 4; ++w) {
+    wsc[w] = exp2f(ml_x[w][lane].x - M);
+    den += ml_x[w][lane].y * wsc[w];
+  }
+  if (!hok) return;
+  const int64_t slot_id = ((int64_t)unit * a.splits + sp) * a.heads + h;
+  bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + h) * D;
+#pragma unroll
+  for (int dd = 0; dd < DT / 4; ++dd) {
+    const int dt = wave * (DT / 4) + dd;
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o += *reinterpret_cast<const f32x4*>(xo + ((w * DT + dt) * 64 + lane) * 4) * wsc[w];
+    const int d0 = dt * 16 + 4 * g;
+    if (a.splits == 1) store_out4(a, D, qs, orow, d0, o, den);
+    else *reinterpret_cast<f32x4*>(a.part_o + slot_id * D + d0) = o;
+  }
+  if (a.splits > 1 && wave == 0 && g == 0) {
+    a.part_ml[slot_id * 2 + 0] = M;
+    a.part_ml[slot_id * 2 + 1] = den;
+  }
+}
+
+// Prefill: many queries. Workgroup = (query, 64 heads); wave w owns heads 16w..16w+15 over the
+// query's whole index list. 32-row tiles are gathered cooperatively (8 rows per wave) into a
+// triple-buffered LDS ring: one barrier per tile, two tiles in flight behind the one computed.
+template <int D>
+__global__ __launch_bounds__(256) void mla_prefill_kernel(MlaArgs a) {
+  constexpr int KS = D / 32, DT = D / 16;
+  constexpr int RS = D * 2 + 16;
+  constexpr int IPR = (D / 8 + 63) / 64;
+  constexpr int RPW = kPreTile / 4;             // rows each wave gathers per tile
+  constexpr int NL = RPW * IPR;                 // DMA instructions per wave per tile
+  constexpr int BUF = kPreTile * RS;
+  __shared__ __align__(16) uint8_t lds[3 * BUF];
+  __shared__ uint8_t vrow[3][kPreTile];
+  __shared__ uint64_t rows[kMaxPreList];        // resolved row addresses, 0 = masked
+
+  const KvSrc& S = a.src;
+  const int unit = blockIdx.x, hg = blockIdx.y;
+  const int b = unit / a.m, qs = unit - (unit / a.m) * a.m;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
+  const int wc = window_count(S, qs);
+  const int L = min(wc + S.k, kMaxPreList);     // the planner keeps whole lists within the limit
+  const int ntile = (L + kPreTile - 1) / kPreTile;
+  // resolve the list once: no global reads are left inside the DMA pipeline (vmcnt retires in
+  // order) and the gather loop spends a few instructions per row
+  for (int e = tid; e < L; e += 256)
+    rows[e] = reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, list_pos(S, b, a.m, qs, e, wc), D));
+  __syncthreads();
+
+  const int h = hg * 64 + wave * 16 + l16;
+  const bool hok = h < a.heads;
+  bf16x8 qb[KS];
+  {
+    const bf16_t* qrow = reinterpret_cast<const bf16_t*>(a.q) + ((int64_t)unit * a.heads + (hok ? h : 0)) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qb[ks] = hok ? ld_bf16x8(qrow + ks * 32 + 8 * g) : zero_bf16x8();
+  }
+  const float sl2 = a.scale * kLog2e;
+  float m_run = kNegFloor, l_run = 0.0f;
+  if (hok) {
+    const float s2 = a.sink[h] * kLog2e;
+    m_run = fmaxf(s2, kNegFloor);
+    l_run = exp2f(s2 - m_run);
+  }
+  f32x4 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto issue = [&](int t, int bi) {
+    uint8_t* dst = lds + bi * BUF;
+    const int mine = t * kPreTile + wave * RPW + (lane & (RPW - 1));
+    const uint64_t mp = mine < L ? rows[mine] : 0ull;
+    if (lane < RPW) vrow[bi][wave * RPW + lane] = mp != 0ull ? 1 : 0;
+    const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) {
+      dma_row<D>(reinterpret_cast<const bf16_t*>(lane_u64(lo, hi, rr)), dst + (wave * RPW + rr) * RS, lane);
     }
-  } else {
-    const int64_t slot = ((int64_t)unit * a.splits + sp) * a.heads;
+  };
+  if (ntile > 0) issue(0, 0);
+  if (ntile > 1) issue(1, 1);
+  for (int t = 0; t < ntile; ++t) {
+    if (t + 1 < ntile) wait_vmcnt<NL>();
+    else wait_vmcnt<0>();
+    __syncthreads();               // tile t is in LDS; every wave is done with tile t-1
+    if (t + 2 < ntile) issue(t + 2, (t + 2) % 3);
+    const int bi = t % 3;
+    const uint8_t* buf = lds + bi * BUF;
+    f32x4 sacc[2];
+    sacc[0] = sacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ht = 0; ht < NHT; ++ht) {
-      const int h = hbase + ht * 16 + l16;
-      if (h >= a.heads) continue;
-      float* po = a.part_o + (slot + h) * D;
+    for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-      for (int dd = 0; dd < DTW; ++dd) {
-        const int dt = dt0 + dd;
-        if (dt < dt1) *reinterpret_cast<f32x4*>(po + dt * 16 + 4 * g) = acc_o[ht][dd];
+      for (int rt = 0; rt < 2; ++rt)
+        sacc[rt] = mfma16x16x32(ld_bf16x8(buf + (rt * 16 + l16) * RS + (ks * 32 + 8 * g) * 2), qb[ks], sacc[rt]);
+    }
+    float p[8];
+    float tmax = kNegFloor;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = vrow[bi][rt * 16 + 4 * g + i] != 0;
+        const float l2 = sacc[rt][i] * sl2;
+        p[rt * 4 + i] = ok ? l2 : -INFINITY;
+        if (ok) tmax = fmaxf(tmax, l2);
       }
-      if (wave == 0 && g == 0) {
-        a.part_ml[(slot + h) * 2 + 0] = m_run[ht];
-        a.part_ml[(slot + h) * 2 + 1] = l_run[ht];
-      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const bool grow = tmax > m_run + kRescale;
+    if (__any(grow)) {
+      const float alpha = grow ? exp2f(m_run - tmax) : 1.0f;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+      l_run *= alpha;
+      m_run = grow ? tmax : m_run;
+    }
+    float psum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      p[e] = exp2f(p[e] - m_run);
+      psum += p[e];
+    }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    l_run += psum;
+    const bf16x8 pb = pack_bf16x8(p);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint8_t* col = buf + (dt * 16 + 4 * (l16 & 3)) * 2;
+      const i16x4 lo = lds_read_tr16(col + (4 * g + (l16 >> 2)) * RS);
+      const i16x4 hi = lds_read_tr16(col + (16 + 4 * g + (l16 >> 2)) * RS);
+      acc[dt] = mfma16x16x32(join_bf16x8(lo, hi), pb, acc[dt]);
     }
   }
+  if (!hok) return;
+  bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + h) * D;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) store_out4(a, D, qs, orow, dt * 16 + 4 * g, acc[dt], l_run);
 }
 
 // Merges split partials (log2-domain max, denominator, numerator) of one (query, head).
@@ -451,30 +571,37 @@ __global__ __launch_bounds__(256) void mla_f32_kernel(MlaArgs a) {
 // ------------------------------------------------------------------ host planning
 
 struct MlaPlan {
-  int nht, hgroups, splits, per_split;
+  bool prefill;
+  int hgroups, splits, per_split;
 };
 
+// Enough queries to fill the chip with (query, 64-head) workgroups -> prefill kernel; otherwise
+// the decode kernel over (query, 16-head, split) workgroups, splitting each index list until
+// ~256 workgroups exist (a split stages at most kMaxSplitList entries).
 static MlaPlan plan_bf16(int64_t units, int heads, int list_max) {
-  const int hg16 = (heads + 15) / 16;
   MlaPlan p{};
-  p.nht = hg16 >= 4 ? 4 : (hg16 >= 2 ? 2 : 1);
-  p.hgroups = (hg16 + p.nht - 1) / p.nht;
-  p.splits = 1;
-  if (units * p.hgroups < 256) {
-    p.nht = 1;
-    p.hgroups = hg16;
-    const int64_t wgs = units * p.hgroups;
-    if (wgs < 256) {
-      int want = (int)((256 + wgs - 1) / wgs);
-      int cap = list_max / 64;
-      if (cap < 1) cap = 1;
-      if (want > cap) want = cap;
-      if (want > 16) want = 16;
-      p.splits = want;
-    }
-  }
   const int lm = list_max > 0 ? list_max : 1;
-  p.per_split = ((lm + p.splits - 1) / p.splits + 31) / 32 * 32;
+  const int hg64 = (heads + 63) / 64;
+  if (units * hg64 >= 512 && lm <= kMaxPreList) {
+    p.prefill = true;
+    p.hgroups = hg64;
+    p.splits = 1;
+    p.per_split = lm;
+    return p;
+  }
+  p.prefill = false;
+  p.hgroups = (heads + 15) / 16;
+  const int64_t wgs = units * p.hgroups;
+  int want = wgs < 256 ? (int)((256 + wgs - 1) / wgs) : 1;
+  int cap = (lm + 63) / 64;
+  if (want > cap) want = cap;
+  if (want > 16) want = 16;
+  if (want < 1) want = 1;
+  p.per_split = ((lm + want - 1) / want + 63) / 64 * 64;
+  while (p.per_split > kMaxSplitList) {
+    ++want;
+    p.per_split = ((lm + want - 1) / want + 63) / 64 * 64;
+  }
   p.splits = (lm + p.per_split - 1) / p.per_split;
   return p;
 }
@@ -491,10 +618,11 @@ static bool bf16_dim_supported(int d) { return d == 64 || d == 128 || d == 256 |
 
 template <int D>
 static void launch_bf16_d(const MlaArgs& a, const MlaPlan& p, int64_t units, hipStream_t stream) {
-  dim3 grid((unsigned)units, (unsigned)p.hgroups, (unsigned)p.splits);
-  if (p.nht == 4) hipLaunchKernelGGL((mla_bf16_kernel<D, 4>), grid, dim3(256), 0, stream, a);
-  else if (p.nht == 2) hipLaunchKernelGGL((mla_bf16_kernel<D, 2>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((mla_bf16_kernel<D, 1>), grid, dim3(256), 0, stream, a);
+  if (p.prefill)
+    hipLaunchKernelGGL(mla_prefill_kernel<D>, dim3((unsigned)units, (unsigned)p.hgroups, 1), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(mla_decode_kernel<D>, dim3((unsigned)units, (unsigned)p.hgroups, (unsigned)p.splits), dim3(256),
+                       0, stream, a);
 }
 
 static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int dtype, void* workspace,

@@ -8,9 +8,10 @@
 // One 1024-thread workgroup per score row. A 4-pass, 8-bit MSD radix select over
 // order-preserving 32-bit keys finds the k-th best key T and how many T-valued keys to keep
 // (per-wave histograms in LDS keep atomics uncontended); one ordered compaction pass then
-// writes every key > T plus the first `need` keys == T, in position order, with a block-wide
-// scan of packed (greater, equal) counts -- so the output comes out sorted and ties resolve to
-// the lowest positions by construction.
+// writes every key > T plus the first `need` keys == T, in position order (wave ballots and
+// popcounts give each selected key its rank) -- so the output comes out sorted and ties
+// resolve to the lowest positions by construction. Rows up to 32k scores keep their keys in
+// registers for the whole selection.
 #include "common.h"
 
 namespace dsv41 {
@@ -123,6 +124,145 @@ __device__ void ordered_select(SelShared& sh, KeyFn key, int count, uint32_t T, 
   }
 }
 
+// Histogram add where many lanes share a digit (the leading radix passes see most keys in a
+// few bins): the two most common digits of the wave are added with one atomic each, the
+// remaining lanes individually, so no LDS address takes more than a few atomics per instruction.
+__device__ __forceinline__ void hist_add(uint32_t* h, uint32_t digit, bool active, int lane) {
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const uint64_t act = __ballot(active);
+    if (act == 0ull) return;
+    const int leader = __ffsll((unsigned long long)act) - 1;
+    const uint32_t ld = (uint32_t)__shfl((int)digit, leader, 64);
+    const uint64_t peers = __ballot(active && digit == ld);
+    if (lane == leader) atomicAdd(&h[ld], (uint32_t)__popcll(peers));
+    if (digit == ld) active = false;
+  }
+  if (active) atomicAdd(&h[digit], 1u);
+}
+
+// Rows of up to J*1024 scores: every thread holds its J keys in registers (one batched
+// load), so the four radix passes and the compaction touch memory only for histograms.
+template <int J>
+__global__ __launch_bounds__(kSelThreads) void topk_reg_kernel(const float* __restrict__ scores,
+                                                               int32_t* __restrict__ out, int n, int nb, int k,
+                                                               int start_pos, int ratio, int offset) {
+  constexpr int E = J * kSelWaves;               // (chunk, wave) count entries
+  constexpr int EL = (E + 63) / 64;              // entries per lane of wave 0 in the base scan
+  __shared__ uint32_t hist[kSelWaves][256];
+  __shared__ uint32_t cnt[2][E];                 // gt / eq counts, then exclusive bases
+  __shared__ uint32_t pick[2];
+  const int64_t row = blockIdx.x;
+  const float* x = scores + row * nb;
+  int32_t* o = out + row * k;
+  const int s = (int)(row % n);
+  const int lens = (start_pos + s + 1) / ratio;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  uint32_t key[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int i = tid + j * kSelThreads;
+    key[j] = i < nb ? order_key(x[i]) : 0u;
+  }
+  uint32_t T = 0u;
+  int need = k;
+  if (k < nb) {
+    uint32_t prefix = 0u, pmask = 0u;
+    int kk = k;
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = 24 - 8 * pass;
+      // a wave clears and fills only its own histogram row: no barrier before the atomics
+      for (int d = lane; d < 256; d += 64) hist[wave][d] = 0u;
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        hist_add(hist[wave], (key[j] >> shift) & 255u, tid + j * kSelThreads < nb && (key[j] & pmask) == prefix,
+                 lane);
+      __syncthreads();
+      if (wave == 0) {
+        // lane l owns digits 255-4l .. 252-4l; scan from the highest digit down
+        uint32_t c[4], sum = 0u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int d = 255 - 4 * lane - q;
+          uint32_t t = 0u;
+#pragma unroll
+          for (int w = 0; w < kSelWaves; ++w) t += hist[w][d];
+          c[q] = t;
+          sum += t;
+        }
+        uint32_t above = wave_incl_scan(sum, lane) - sum;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (above < (uint32_t)kk && (uint32_t)kk <= above + c[q]) {
+            pick[0] = (uint32_t)(255 - 4 * lane - q);
+            pick[1] = above;
+          }
+          above += c[q];
+        }
+      }
+      __syncthreads();
+      prefix |= pick[0] << shift;
+      pmask |= 255u << shift;
+      kk -= (int)pick[1];
+    }
+    T = prefix;
+    need = kk;
+  }
+  // ordered compaction: keys > T, then the first `need` keys == T, in position order
+  const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int i = tid + j * kSelThreads;
+    const bool ok = i < nb && k < nb;
+    const uint64_t bg = __ballot(ok && key[j] > T);
+    const uint64_t be = __ballot(ok && key[j] == T);
+    if (lane == 0) {
+      cnt[0][j * kSelWaves + wave] = (uint32_t)__popcll(bg);
+      cnt[1][j * kSelWaves + wave] = (uint32_t)__popcll(be);
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      uint32_t v[EL], sum = 0u;
+#pragma unroll
+      for (int q = 0; q < EL; ++q) {
+        const int e = lane * EL + q;
+        v[q] = e < E ? cnt[f][e] : 0u;
+        sum += v[q];
+      }
+      uint32_t base = wave_incl_scan(sum, lane) - sum;
+#pragma unroll
+      for (int q = 0; q < EL; ++q) {
+        const int e = lane * EL + q;
+        if (e < E) cnt[f][e] = base;
+        base += v[q];
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int i = tid + j * kSelThreads;
+    if (k >= nb) {                       // everything selected, in order
+      if (i < nb) o[i] = i < lens ? i + offset : -1;
+      continue;
+    }
+    const bool ok = i < nb;
+    const bool gt = ok && key[j] > T, eq = ok && key[j] == T;
+    const uint64_t bg = __ballot(gt), be = __ballot(eq);
+    const uint32_t gt_before = cnt[0][j * kSelWaves + wave] + (uint32_t)__popcll(bg & below);
+    const uint32_t eq_before = cnt[1][j * kSelWaves + wave] + (uint32_t)__popcll(be & below);
+    if (gt || (eq && eq_before < (uint32_t)need)) {
+      const uint32_t pos = gt_before + min(eq_before, (uint32_t)need);
+      if (pos < (uint32_t)k) o[pos] = i < lens ? i + offset : -1;
+    }
+  }
+}
+
+// Rows longer than 32k scores: keys are re-read from memory in every pass.
 __global__ __launch_bounds__(kSelThreads) void topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out,
                                                            int n, int nb, int k, int start_pos, int ratio,
                                                            int offset) {
@@ -196,8 +336,17 @@ extern "C" int dsv41_topk_select(const float* scores, int32_t* out, int64_t rows
   DSV41_REQUIRE(rows < (1ll << 31), DSV41_E_ARG, "%s: too many rows", what);
   const int k = topk < nb ? topk : nb;
   if (rows == 0 || k == 0) return 0;
-  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)rows), dim3(kSelThreads), 0, stream, scores, out, n, nb, k,
-                     start_pos, ratio, offset);
+  const dim3 grid((unsigned)rows), block(kSelThreads);
+  if (nb <= 4 * kSelThreads)
+    hipLaunchKernelGGL(topk_reg_kernel<4>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset);
+  else if (nb <= 8 * kSelThreads)
+    hipLaunchKernelGGL(topk_reg_kernel<8>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset);
+  else if (nb <= 16 * kSelThreads)
+    hipLaunchKernelGGL(topk_reg_kernel<16>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset);
+  else if (nb <= 32 * kSelThreads)
+    hipLaunchKernelGGL(topk_reg_kernel<32>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset);
+  else
+    hipLaunchKernelGGL(topk_kernel, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset);
   return check_launch(what);
 }
 

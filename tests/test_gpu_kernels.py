@@ -283,6 +283,8 @@ def test_candidate_blocks_bit_exact(gpu, b, n, nb, tb, bs, start, r):
     ("bf16", 32, 1, 64, 512, 4224, 640),   # C2 decode: split index lists + combine
     ("bf16", 3, 2, 16, 576, 200, 97),      # head_dim 576 (512 + 64 reading)
     ("bf16", 1, 4, 4, 64, 50, 33),         # heads < 16 (masked head tile)
+    ("bf16", 1, 640, 64, 512, 2000, 96),   # >= 512 queries: the prefill kernel
+    ("bf16", 2, 300, 48, 128, 700, 130),   # prefill kernel, partial 64-head group
 ])
 def test_sparse_attn(gpu, dt, b, m, h, d, nkv, k):
     from dsv41.sparse_attention import sparse_attn
@@ -346,3 +348,29 @@ def test_sparse_mla_in_place_sources(gpu, dt, b, n, h, d, window, start, n_comp,
         assert max_abs(g, want) < 1e-5
     else:
         assert rel_max_diff(g, want) < 2e-2
+
+
+def test_reference_kernel_module_seam(gpu):
+    """dsv41.kernel stands in for the reference model's native `kernel` module."""
+    import dsv41.kernel as K
+    rng = rng_for("seam")
+    x = rng.standard_normal((64, 128)).astype(F32) * 2
+    t = dev(x)
+    K.act_quant(t, 32, "ue8m0", None, True)
+    assert np.array_equal(to_np(t), R.fq_fp8_ue8m0(x, 32))
+    t = dev(x)
+    K.fp4_act_quant(t, 32, True)
+    assert np.array_equal(to_np(t), R.fq_fp4_ue8m0(x, 32))
+    t = dev(x)
+    K.fp4_act_quant(t, 16, True, torch.float8_e4m3fn)
+    assert np.array_equal(to_np(t), R.fq_fp4_e4m3(x, 16))
+    q = rng.standard_normal((1, 3, 4, 64)).astype(F32)
+    kv = rng.standard_normal((1, 20, 64)).astype(F32)
+    sink = rng.standard_normal(4).astype(F32)
+    idx = rng.integers(-1, 20, size=(1, 3, 7)).astype(np.int32)
+    got = to_np(K.sparse_attn(dev(q), dev(kv), dev(sink), torch.as_tensor(idx).to(gpu), 0.125))
+    assert max_abs(got, R.sparse_attn(q, kv, sink, idx, 0.125)) < 1e-5
+    with pytest.raises(NotImplementedError):
+        K.act_quant(dev(x), 32)
+    with pytest.raises(RuntimeError):
+        K.fp8_gemm()
