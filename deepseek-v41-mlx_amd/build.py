@@ -29,8 +29,12 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC)")
 
 
+# -packed-fp32-ops: no v_pk_*_f32 generation. -amdgpu-mfma-vgpr-form: MFMA accumulators in
+# VGPRs -- with a one-workgroup-per-CU LDS footprint the default heuristic parks them in AGPRs
+# and copies them around every VALU use.
 FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def _compile(src: str, obj: str) -> None:

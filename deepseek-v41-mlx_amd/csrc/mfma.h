@@ -40,6 +40,21 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_base) {
   __builtin_amdgcn_global_load_lds((gbl_void*)src, (lds_void*)lds_base, 16, 0, 0);
 }
 
+// Same copy, issued as inline asm (saddr form: `base` wave-uniform, `voff` per lane, LDS byte
+// offset `lds` in M0). The compiler's wait-count pass cannot see an LDS write behind it, so it
+// never adds a full vmcnt(0) drain in front of LDS reads that it cannot prove disjoint from the
+// copies in flight; completion is tracked only by the caller's explicit vmcnt waits. M0 carries
+// no other value in the kernels that use it.
+__device__ __forceinline__ void dma16_sgpr(uint64_t base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+
+// LDS byte offset of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 __device__ __forceinline__ i16x4 pack_bf16x4(const float* v) {
   i16x4 r;
   r[0] = (short)f2bf(v[0]);
@@ -66,5 +81,17 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(const float* v) {
   u.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
   return as_bf16x8(u);
 }
+
+// 8 floats -> MFMA operand with the hardware round-to-nearest-even convert (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ bf16x8 cvt_bf16x8(const float* v) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (__bf16)v[i];
+  return r;
+}
+
+// 2^x with the bare v_exp_f32 (no denormal-range fix-up). Used for softmax weights 2^(s - m) with
+// s - m <= the lazy-rescale threshold: results below 2^-126 are zero for the sum anyway.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 }  // namespace dsv41

@@ -40,10 +40,19 @@ struct MlaArgs {
   const float* cos_tab;
   const float* sin_tab;
   int rd, start_pos;
-  int splits, per_split;
+  int hgroups, splits, per_split;
   float* part_o;
   float* part_ml;
 };
+
+// Workgroups are dispatched to the 8 XCDs round-robin by linear id and each XCD has its own L2.
+// Renumber so that consecutive logical tiles run on one XCD: the head groups of one query (and
+// neighbouring queries of a prefill chunk) gather the same KV rows and then share that L2.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_tile(int bid, int total) {
+  if (total % kXcds) return bid;
+  return (bid % kXcds) * (total / kXcds) + bid / kXcds;
+}
 
 // Entry e of query qs's list -> unified position (-1 = none). wc = window entries of qs.
 __device__ __forceinline__ int list_pos(const KvSrc& s, int b, int m, int qs, int e, int wc) {
@@ -92,23 +101,28 @@ __device__ __forceinline__ void rope_inv_pair(const MlaArgs& a, int D, int qs, i
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegFloor = -1e30f;
 
-// Masked list entries gather this zero row, so every chunk issues the same number of DMA loads
+// Masked list entries gather this zero row, so every step issues the same number of copies
 // (their count is what s_waitcnt vmcnt waits on) and padded LDS rows hold finite zeros.
 __device__ __align__(16) uint4 g_zero_row[128] = {};
 
 constexpr float kRescale = 8.0f;       // lazy softmax rescaling threshold (log2 units)
-constexpr int kDecChunk = 16;          // rows per wave chunk (decode kernel)
-constexpr int kMaxSplitList = 1024;    // list entries one decode split stages in LDS
-constexpr int kPreTile = 32;           // rows per shared tile (prefill kernel)
-constexpr int kMaxPreList = 2304;      // list entries the prefill kernel stages in LDS
+constexpr int kStepRows = 32;          // rows per pipeline step (two 16-row MFMA tiles)
+constexpr int kMaxList = 2304;         // list entries one workgroup stages in LDS
+constexpr int kLdsBudget = 160 * 1024;
+constexpr int kMaxRing = 4;            // ring slots: steps in flight + the one computed
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N == 0 || N == 8 || N == 16 || N == 32, "vmcnt immediate");
-  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else if constexpr (N == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Wait until at most `after` steps of NL copies each are still in flight (after < kMaxRing).
+template <int NL>
+__device__ __forceinline__ void wait_steps(int after) {
+  if (after >= 3) wait_vmcnt<3 * NL>();
+  else if (after == 2) wait_vmcnt<2 * NL>();
+  else if (after == 1) wait_vmcnt<NL>();
+  else wait_vmcnt<0>();
 }
 
 __device__ __forceinline__ bf16x8 join_bf16x8(i16x4 lo, i16x4 hi) {
@@ -124,15 +138,16 @@ __device__ __forceinline__ uint64_t lane_u64(uint32_t lo, uint32_t hi, int r) {
   return ((uint64_t)h << 32) | (uint64_t)l;
 }
 
-// DMA one KV row (or the zero row) of D bf16 into LDS at `dst` (wave-uniform).
+// Copy one KV row (address `p`, wave-uniform; 0 = masked -> the zero row) of D bf16 into LDS at
+// byte offset `dst`: one 1 KB wave instruction per 512 channels.
 template <int D>
-__device__ __forceinline__ void dma_row(const bf16_t* p, uint8_t* dst, int lane) {
+__device__ __forceinline__ void dma_row(uint64_t p, uint32_t dst, int lane) {
   constexpr int CPR = D / 8, IPR = (CPR + 63) / 64;
-  const uint8_t* src = p ? reinterpret_cast<const uint8_t*>(p) : reinterpret_cast<const uint8_t*>(g_zero_row);
+  const uint64_t src = p ? p : reinterpret_cast<uint64_t>(g_zero_row);
 #pragma unroll
   for (int ii = 0; ii < IPR; ++ii) {
     const int ch = ii * 64 + lane;
-    if (CPR % 64 == 0 || ch < CPR) dma16(src + ch * 16, dst + ii * 1024);
+    if (CPR % 64 == 0 || ch < CPR) dma16_sgpr(src, (uint32_t)ch * 16u, dst + ii * 1024);
   }
 }
 
@@ -150,243 +165,131 @@ __device__ __forceinline__ void store_out4(const MlaArgs& a, int D, int qs, bf16
   *reinterpret_cast<uint2*>(orow + d0) = st;
 }
 
-// Decode: few queries. Workgroup = (query, 16 heads, split of the index list); each of the 4
-// waves walks its own 16-row chunks of the split (chunks w, w+4, ...), gathering rows straight
-// into a private double-buffered LDS slot with global_load_lds; the waves merge in LDS at the end.
-template <int D>
-__global__ __launch_bounds__(256) void mla_decode_kernel(MlaArgs a) {
-  constexpr int KS = D / 32, DT = D / 16;
-  constexpr int RS = D * 2 + 16;
+template <int D, int NW>
+struct MlaLds {
+  static constexpr int RS = D * 2 + 16;                   // padded row stride (bytes)
+  static constexpr int SLOT = kStepRows * RS;
+  static constexpr int XS = NW * 2 * 64 * 16;             // partial-score exchange
+  static constexpr int FIXED = XS + kMaxList * 8 + kMaxRing * kStepRows + 256;
+  static constexpr int NS = (kLdsBudget - FIXED) / SLOT < kMaxRing ? (kLdsBudget - FIXED) / SLOT : kMaxRing;
+  static_assert(NS >= 2, "ring needs two slots");
+};
+
+// Workgroup = (query, HT*16 heads, split of the index list), one wave per (head tile ht, dim
+// slice dh) -- HT*DS waves. Per 32-row step:
+//   every wave gathers 32/(HT*DS) rows into the step's ring slot (global_load_lds);
+//   QK: wave (ht, dh) forms the partial S^T over its D/DS channels (Q^T slice in registers) and
+//     the DS partials of a head tile are summed through LDS in a fixed order, so all DS waves of
+//     the tile hold bit-identical scores and therefore identical softmax state;
+//   PV: each wave accumulates O^T only for its own channel slice (D/DS x 16 heads).
+// Register footprint per wave: Q^T slice D/DS/8 + accumulators D/DS/4 VGPRs.
+// (__launch_bounds__'s second argument asks for 2 waves per SIMD: a 256-register budget, which
+// keeps the accumulators in VGPRs instead of AGPR copies around every MFMA block.)
+template <int D, int HT, int DS>
+__global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
+  constexpr int NW = HT * DS, NT = 64 * NW;
+  constexpr int DSL = D / DS, KSS = DSL / 32, DTS = DSL / 16;
+  static_assert(DSL % 32 == 0, "dim slice must be a multiple of 32 channels");
+  constexpr int R = kStepRows;
+  static_assert(R % NW == 0, "rows per step must split evenly over the waves");
+  constexpr int RPW = R / NW;
   constexpr int IPR = (D / 8 + 63) / 64;
-  constexpr int NL = kDecChunk * IPR;           // DMA instructions per chunk
-  constexpr int BUF = kDecChunk * RS;
-  static_assert(DT % 4 == 0, "head_dim must be a multiple of 64");
-  static_assert(4 * DT * 64 * 16 <= 4 * 2 * BUF, "merge buffer must fit in the chunk buffers");
-  __shared__ __align__(16) uint8_t lds[4 * 2 * BUF];
-  __shared__ uint64_t rows[kMaxSplitList];      // resolved row addresses, 0 = masked
-  __shared__ float2 ml_x[4][64];
+  constexpr int NL = RPW * IPR;                 // copies each wave issues per step
+  using Lds = MlaLds<D, NW>;
+  constexpr int RS = Lds::RS, SLOT = Lds::SLOT, NS = Lds::NS;
+  __shared__ __align__(16) uint8_t ring[NS * SLOT];
+  __shared__ __align__(16) f32x4 xs[NW][2][64];
+  __shared__ uint64_t rows[kMaxList];           // resolved row addresses, 0 = masked
+  __shared__ __align__(4) uint8_t vrow[NS][R];
 
   const KvSrc& S = a.src;
-  const int unit = blockIdx.x, hg = blockIdx.y, sp = blockIdx.z;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);   // (unit, split, head group), head group fastest
+  const int hg = tile % a.hgroups;
+  const int sp = (tile / a.hgroups) % a.splits;
+  const int unit = tile / (a.hgroups * a.splits);
   const int b = unit / a.m, qs = unit - (unit / a.m) * a.m;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar address math
+  const int ht = wave % HT, dh = wave / HT;
   const int wc = window_count(S, qs);
   const int L = wc + S.k;
   const int e_begin = sp * a.per_split;
-  const int cnt = max(min(e_begin + a.per_split, L) - e_begin, 0);
-  // resolve every entry of the split once (segment, ring slot, batch row): the gather loop then
-  // spends a few instructions per row
-  for (int e = tid; e < cnt; e += 256)
+  const int cnt = min(max(min(e_begin + a.per_split, L) - e_begin, 0), kMaxList);  // planner: <= kMaxList
+  // resolve the split's list once (segment, ring slot, batch row): no global reads are left
+  // inside the copy pipeline and a step spends a few instructions per row
+  for (int e = tid; e < cnt; e += NT)
     rows[e] = reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, list_pos(S, b, a.m, qs, e_begin + e, wc), D));
-  __syncthreads();
 
-  const int h = hg * 16 + l16;
+  const int h = hg * (HT * 16) + ht * 16 + l16;
   const bool hok = h < a.heads;
-  bf16x8 qb[KS];
+  bf16x8 qb[KSS];
   {
-    const bf16_t* qrow = reinterpret_cast<const bf16_t*>(a.q) + ((int64_t)unit * a.heads + (hok ? h : 0)) * D;
+    const bf16_t* qrow =
+        reinterpret_cast<const bf16_t*>(a.q) + ((int64_t)unit * a.heads + (hok ? h : 0)) * D + dh * DSL;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qb[ks] = hok ? ld_bf16x8(qrow + ks * 32 + 8 * g) : zero_bf16x8();
+    for (int ks = 0; ks < KSS; ++ks) qb[ks] = hok ? ld_bf16x8(qrow + ks * 32 + 8 * g) : zero_bf16x8();
   }
   const float sl2 = a.scale * kLog2e;
   float m_run = kNegFloor, l_run = 0.0f;   // m_run: the exponent reference of acc and l_run
-  if (sp == 0 && wave == 0 && hok) {
+  if (sp == 0 && hok) {
     const float s2 = a.sink[h] * kLog2e;
     m_run = fmaxf(s2, kNegFloor);
     l_run = exp2f(s2 - m_run);
   }
-  f32x4 acc[DT];
+  f32x4 acc[DTS];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int dt = 0; dt < DTS; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  __syncthreads();                         // rows[] complete
 
-  uint8_t* wbuf = lds + wave * (2 * BUF);
-  const int nchunk = (cnt + kDecChunk - 1) / kDecChunk;
-  auto issue = [&](int c, int slot) -> uint32_t {
-    uint8_t* dst = wbuf + slot * BUF;
-    const int mine = c * kDecChunk + (lane & (kDecChunk - 1));      // one LDS read for the chunk
+  const int nsteps = (cnt + R - 1) / R;
+  const uint32_t ring_base = lds_offset(ring);
+  auto issue = [&](int t) {
+    const int slot = t % NS;
+    const int mine = t * R + wave * RPW + (lane % RPW);
     const uint64_t mp = mine < cnt ? rows[mine] : 0ull;
-    const uint32_t vm = (uint32_t)__ballot(mp != 0ull) & ((1u << kDecChunk) - 1u);
+    if (lane < RPW) vrow[slot][wave * RPW + lane] = mp != 0ull ? 1 : 0;
     const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
+    const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_base + (uint32_t)(slot * SLOT + wave * RPW * RS));
 #pragma unroll
-    for (int r = 0; r < kDecChunk; ++r) {
-      dma_row<D>(reinterpret_cast<const bf16_t*>(lane_u64(lo, hi, r)), dst + r * RS, lane);
-    }
-    return vm;
+    for (int rr = 0; rr < RPW; ++rr) dma_row<D>(lane_u64(lo, hi, rr), dst + rr * RS, lane);
   };
+  for (int t = 0; t < nsteps && t < NS - 1; ++t) issue(t);
 
-  int slot = 0;
-  uint32_t vm_cur = wave < nchunk ? issue(wave, 0) : 0u;
-  for (int c = wave; c < nchunk; c += 4) {
-    uint32_t vm_nxt = 0u;
-    if (c + 4 < nchunk) {
-      vm_nxt = issue(c + 4, slot ^ 1);
-      wait_vmcnt<NL>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    const uint8_t* buf = wbuf + slot * BUF;
-    f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = s0;      // two independent MFMA chains
-#pragma unroll
-    for (int ks = 0; ks < KS; ks += 2) {
-      s0 = mfma16x16x32(ld_bf16x8(buf + l16 * RS + (ks * 32 + 8 * g) * 2), qb[ks], s0);
-      s1 = mfma16x16x32(ld_bf16x8(buf + l16 * RS + (ks * 32 + 32 + 8 * g) * 2), qb[ks + 1], s1);
-    }
-    const f32x4 sacc = s0 + s1;
-    float p[4];
-    float tmax = kNegFloor;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool ok = (vm_cur >> (4 * g + i)) & 1u;
-      const float l2 = sacc[i] * sl2;
-      p[i] = ok ? l2 : -INFINITY;
-      if (ok) tmax = fmaxf(tmax, l2);
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const bool grow = tmax > m_run + kRescale;
-    if (__any(grow)) {
-      const float alpha = grow ? exp2f(m_run - tmax) : 1.0f;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
-      l_run *= alpha;
-      m_run = grow ? tmax : m_run;
-    }
-    float psum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      p[i] = exp2f(p[i] - m_run);
-      psum += p[i];
-    }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l_run += psum;
-    const i16x4 pb = pack_bf16x4(p);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const i16x4 va = lds_read_tr16(buf + (4 * g + (l16 >> 2)) * RS + (dt * 16 + 4 * (l16 & 3)) * 2);
-      acc[dt] = mfma16x16x16(va, pb, acc[dt]);
-    }
-    vm_cur = vm_nxt;
-    slot ^= 1;
-  }
-
-  // merge the four waves' (m, l, O) in LDS; wave w then owns dim tiles [w*DT/4, (w+1)*DT/4)
-  __syncthreads();
-  float* xo = reinterpret_cast<float*>(lds);
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(xo + ((wave * DT + dt) * 64 + lane) * 4) = acc[dt];
-  ml_x[wave][lane] = make_float2(m_run, l_run);
-  __syncthreads();
-  float M = kNegFloor;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) M = fmaxf(M, ml_x[w][lane].x);
-  float wsc[4], den = 0.0f;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    wsc[w] = exp2f(ml_x[w][lane].x - M);
-    den += ml_x[w][lane].y * wsc[w];
-  }
-  if (!hok) return;
-  const int64_t slot_id = ((int64_t)unit * a.splits + sp) * a.heads + h;
-  bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + h) * D;
-#pragma unroll
-  for (int dd = 0; dd < DT / 4; ++dd) {
-    const int dt = wave * (DT / 4) + dd;
-    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int w = 0; w < 4; ++w) o += *reinterpret_cast<const f32x4*>(xo + ((w * DT + dt) * 64 + lane) * 4) * wsc[w];
-    const int d0 = dt * 16 + 4 * g;
-    if (a.splits == 1) store_out4(a, D, qs, orow, d0, o, den);
-    else *reinterpret_cast<f32x4*>(a.part_o + slot_id * D + d0) = o;
-  }
-  if (a.splits > 1 && wave == 0 && g == 0) {
-    a.part_ml[slot_id * 2 + 0] = M;
-    a.part_ml[slot_id * 2 + 1] = den;
-  }
-}
-
-// Prefill: many queries. Workgroup = (query, 64 heads); wave w owns heads 16w..16w+15 over the
-// query's whole index list. 32-row tiles are gathered cooperatively (8 rows per wave) into a
-// triple-buffered LDS ring: one barrier per tile, two tiles in flight behind the one computed.
-template <int D>
-__global__ __launch_bounds__(256) void mla_prefill_kernel(MlaArgs a) {
-  constexpr int KS = D / 32, DT = D / 16;
-  constexpr int RS = D * 2 + 16;
-  constexpr int IPR = (D / 8 + 63) / 64;
-  constexpr int RPW = kPreTile / 4;             // rows each wave gathers per tile
-  constexpr int NL = RPW * IPR;                 // DMA instructions per wave per tile
-  constexpr int BUF = kPreTile * RS;
-  __shared__ __align__(16) uint8_t lds[3 * BUF];
-  __shared__ uint8_t vrow[3][kPreTile];
-  __shared__ uint64_t rows[kMaxPreList];        // resolved row addresses, 0 = masked
-
-  const KvSrc& S = a.src;
-  const int unit = blockIdx.x, hg = blockIdx.y;
-  const int b = unit / a.m, qs = unit - (unit / a.m) * a.m;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
-  const int wc = window_count(S, qs);
-  const int L = min(wc + S.k, kMaxPreList);     // the planner keeps whole lists within the limit
-  const int ntile = (L + kPreTile - 1) / kPreTile;
-  // resolve the list once: no global reads are left inside the DMA pipeline (vmcnt retires in
-  // order) and the gather loop spends a few instructions per row
-  for (int e = tid; e < L; e += 256)
-    rows[e] = reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, list_pos(S, b, a.m, qs, e, wc), D));
-  __syncthreads();
-
-  const int h = hg * 64 + wave * 16 + l16;
-  const bool hok = h < a.heads;
-  bf16x8 qb[KS];
-  {
-    const bf16_t* qrow = reinterpret_cast<const bf16_t*>(a.q) + ((int64_t)unit * a.heads + (hok ? h : 0)) * D;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qb[ks] = hok ? ld_bf16x8(qrow + ks * 32 + 8 * g) : zero_bf16x8();
-  }
-  const float sl2 = a.scale * kLog2e;
-  float m_run = kNegFloor, l_run = 0.0f;
-  if (hok) {
-    const float s2 = a.sink[h] * kLog2e;
-    m_run = fmaxf(s2, kNegFloor);
-    l_run = exp2f(s2 - m_run);
-  }
-  f32x4 acc[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  auto issue = [&](int t, int bi) {
-    uint8_t* dst = lds + bi * BUF;
-    const int mine = t * kPreTile + wave * RPW + (lane & (RPW - 1));
-    const uint64_t mp = mine < L ? rows[mine] : 0ull;
-    if (lane < RPW) vrow[bi][wave * RPW + lane] = mp != 0ull ? 1 : 0;
-    const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
-#pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      dma_row<D>(reinterpret_cast<const bf16_t*>(lane_u64(lo, hi, rr)), dst + (wave * RPW + rr) * RS, lane);
-    }
-  };
-  if (ntile > 0) issue(0, 0);
-  if (ntile > 1) issue(1, 1);
-  for (int t = 0; t < ntile; ++t) {
-    if (t + 1 < ntile) wait_vmcnt<NL>();
-    else wait_vmcnt<0>();
-    __syncthreads();               // tile t is in LDS; every wave is done with tile t-1
-    if (t + 2 < ntile) issue(t + 2, (t + 2) % 3);
-    const int bi = t % 3;
-    const uint8_t* buf = lds + bi * BUF;
+  for (int t = 0; t < nsteps; ++t) {
+    wait_steps<NL>(min(nsteps - 1 - t, NS - 2));
+    __syncthreads();                       // step t landed; every wave is done with step t-1
+    if (t + NS - 1 < nsteps) issue(t + NS - 1);
+    const int slot = t % NS;
+    const uint8_t* buf = ring + slot * SLOT;
     f32x4 sacc[2];
     sacc[0] = sacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
+    for (int ks = 0; ks < KSS; ++ks)
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
-        sacc[rt] = mfma16x16x32(ld_bf16x8(buf + (rt * 16 + l16) * RS + (ks * 32 + 8 * g) * 2), qb[ks], sacc[rt]);
+        sacc[rt] = mfma16x16x32(ld_bf16x8(buf + (rt * 16 + l16) * RS + (dh * DSL + ks * 32 + 8 * g) * 2), qb[ks],
+                                sacc[rt]);
+    if constexpr (DS > 1) {
+      xs[wave][0][lane] = sacc[0];
+      xs[wave][1][lane] = sacc[1];
+      __syncthreads();
+      sacc[0] = xs[ht][0][lane];
+      sacc[1] = xs[ht][1][lane];
+#pragma unroll
+      for (int d2 = 1; d2 < DS; ++d2) {
+        sacc[0] += xs[ht + HT * d2][0][lane];
+        sacc[1] += xs[ht + HT * d2][1][lane];
+      }
     }
+    const uint32_t v0 = *reinterpret_cast<const uint32_t*>(&vrow[slot][4 * g]);
+    const uint32_t v1 = *reinterpret_cast<const uint32_t*>(&vrow[slot][16 + 4 * g]);
     float p[8];
     float tmax = kNegFloor;
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const bool ok = vrow[bi][rt * 16 + 4 * g + i] != 0;
+        const bool ok = (((rt ? v1 : v0) >> (8 * i)) & 0xFFu) != 0u;
         const float l2 = sacc[rt][i] * sl2;
         p[rt * 4 + i] = ok ? l2 : -INFINITY;
         if (ok) tmax = fmaxf(tmax, l2);
@@ -395,65 +298,85 @@ __global__ __launch_bounds__(256) void mla_prefill_kernel(MlaArgs a) {
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const bool grow = tmax > m_run + kRescale;
     if (__any(grow)) {
-      const float alpha = grow ? exp2f(m_run - tmax) : 1.0f;
+      const float alpha = grow ? fast_exp2(m_run - tmax) : 1.0f;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+      for (int dt = 0; dt < DTS; ++dt) acc[dt] *= alpha;
       l_run *= alpha;
       m_run = grow ? tmax : m_run;
     }
     float psum = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      p[e] = exp2f(p[e] - m_run);
+      p[e] = fast_exp2(p[e] - m_run);
       psum += p[e];
     }
     psum += __shfl_xor(psum, 16, 64);
     psum += __shfl_xor(psum, 32, 64);
     l_run += psum;
-    const bf16x8 pb = pack_bf16x8(p);
+    const bf16x8 pb = cvt_bf16x8(p);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const uint8_t* col = buf + (dt * 16 + 4 * (l16 & 3)) * 2;
+    for (int dt = 0; dt < DTS; ++dt) {
+      const uint8_t* col = buf + (dh * DSL + dt * 16 + 4 * (l16 & 3)) * 2;
       const i16x4 lo = lds_read_tr16(col + (4 * g + (l16 >> 2)) * RS);
       const i16x4 hi = lds_read_tr16(col + (16 + 4 * g + (l16 >> 2)) * RS);
       acc[dt] = mfma16x16x32(join_bf16x8(lo, hi), pb, acc[dt]);
     }
   }
-  if (!hok) return;
+
+  if (!hok) return;                        // no barrier follows
+  const int64_t slot_id = ((int64_t)unit * a.splits + sp) * a.heads + h;
   bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + h) * D;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) store_out4(a, D, qs, orow, dt * 16 + 4 * g, acc[dt], l_run);
+  for (int dt = 0; dt < DTS; ++dt) {
+    const int d0 = dh * DSL + dt * 16 + 4 * g;
+    if (a.splits == 1) store_out4(a, D, qs, orow, d0, acc[dt], l_run);
+    else *reinterpret_cast<f32x4*>(a.part_o + slot_id * D + d0) = acc[dt];
+  }
+  if (a.splits > 1 && dh == 0 && g == 0) {
+    a.part_ml[slot_id * 2 + 0] = m_run;
+    a.part_ml[slot_id * 2 + 1] = l_run;
+  }
 }
 
-// Merges split partials (log2-domain max, denominator, numerator) of one (query, head).
+// Merges split partials (log2-domain max, denominator, numerator) of one query: one wave per
+// head, 4 heads per workgroup. Lane s reads split s's (max, denominator); the weights reach every
+// lane by readlane, and the numerator slices of all splits are loaded together (no load waits on
+// another). Splits are at most 64 (the planner's bound).
 template <typename T>
-__global__ __launch_bounds__(128) void mla_combine_kernel(MlaArgs a) {
-  const int unit = blockIdx.x, h = blockIdx.y;
-  const int D = a.dim;
-  const int qs = unit % a.m;
-  const int64_t slot0 = (int64_t)unit * a.splits * a.heads;
-  float M = kNegFloor;
-  for (int sp = 0; sp < a.splits; ++sp) M = fmaxf(M, a.part_ml[(slot0 + (int64_t)sp * a.heads + h) * 2]);
-  float den = 0.0f;
-  for (int sp = 0; sp < a.splits; ++sp) {
-    const float* ml = a.part_ml + (slot0 + (int64_t)sp * a.heads + h) * 2;
-    den += ml[1] * exp2f(ml[0] - M);
+__global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
+  const int unit = blockIdx.x;
+  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (h >= a.heads) return;
+  const int D = a.dim, qs = unit % a.m, ns = a.splits;
+  const int64_t slot0 = (int64_t)unit * ns * a.heads + h;     // split s: slot0 + s * heads
+  float mk = kNegFloor, dk = 0.0f;
+  if (lane < ns) {
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (slot0 + (int64_t)lane * a.heads) * 2);
+    mk = ml.x;
+    dk = ml.y;
   }
+  float M = mk;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  const float wk = lane < ns ? exp2f(mk - M) : 0.0f;
+  float den = dk * wk;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
   T* orow = reinterpret_cast<T*>(a.o) + ((int64_t)unit * a.heads + h) * D;
-  for (int p = threadIdx.x; p < D / 2; p += 128) {
-    float x0 = 0.0f, x1 = 0.0f;
-    for (int sp = 0; sp < a.splits; ++sp) {
-      const int64_t slot = slot0 + (int64_t)sp * a.heads + h;
-      const float wgt = exp2f(a.part_ml[slot * 2] - M);
-      const float* po = a.part_o + slot * D + 2 * p;
-      x0 += po[0] * wgt;
-      x1 += po[1] * wgt;
+  for (int d = 4 * lane; d < D; d += 256) {
+    f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < ns; ++s) {
+      const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), s));
+      x += *reinterpret_cast<const f32x4*>(a.part_o + (slot0 + (int64_t)s * a.heads) * D + d) * w;
     }
-    x0 = io<T>::rnd(x0 / den);
-    x1 = io<T>::rnd(x1 / den);
-    rope_inv_pair(a, D, qs, 2 * p, x0, x1, false);
-    io<T>::st(orow + 2 * p, x0);
-    io<T>::st(orow + 2 * p + 1, x1);
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = io<T>::rnd(x[i] / den);
+    rope_inv_pair(a, D, qs, d, v[0], v[1], false);
+    rope_inv_pair(a, D, qs, d + 2, v[2], v[3], false);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) io<T>::st(orow + d + i, v[i]);
   }
 }
 
@@ -571,37 +494,36 @@ __global__ __launch_bounds__(256) void mla_f32_kernel(MlaArgs a) {
 // ------------------------------------------------------------------ host planning
 
 struct MlaPlan {
-  bool prefill;
+  bool wide;                     // 64-head workgroups of 8 waves (else 32-head, 4 waves)
   int hgroups, splits, per_split;
 };
 
-// Enough queries to fill the chip with (query, 64-head) workgroups -> prefill kernel; otherwise
-// the decode kernel over (query, 16-head, split) workgroups, splitting each index list until
-// ~256 workgroups exist (a split stages at most kMaxSplitList entries).
+// Many queries (prefill): one workgroup per (query, head group) over the whole list, 64 heads
+// per workgroup when there are more than 32. Few queries (decode): (query, 32-head, split)
+// workgroups, the list split in whole 32-row steps until about 256 workgroups exist (one per
+// CU: each holds a ~160 KB LDS ring). A workgroup stages at most kMaxList list entries.
 static MlaPlan plan_bf16(int64_t units, int heads, int list_max) {
   MlaPlan p{};
   const int lm = list_max > 0 ? list_max : 1;
-  const int hg64 = (heads + 63) / 64;
-  if (units * hg64 >= 512 && lm <= kMaxPreList) {
-    p.prefill = true;
-    p.hgroups = hg64;
+  const int hg32 = (heads + 31) / 32;
+  if (units * hg32 >= 512 && lm <= kMaxList) {
+    p.wide = heads > 32;
+    p.hgroups = p.wide ? (heads + 63) / 64 : hg32;
     p.splits = 1;
     p.per_split = lm;
     return p;
   }
-  p.prefill = false;
-  p.hgroups = (heads + 15) / 16;
+  p.wide = false;
+  p.hgroups = hg32;
   const int64_t wgs = units * p.hgroups;
   int want = wgs < 256 ? (int)((256 + wgs - 1) / wgs) : 1;
-  int cap = (lm + 63) / 64;
+  const int cap = (lm + kStepRows - 1) / kStepRows;
   if (want > cap) want = cap;
   if (want > 16) want = 16;
   if (want < 1) want = 1;
-  p.per_split = ((lm + want - 1) / want + 63) / 64 * 64;
-  while (p.per_split > kMaxSplitList) {
-    ++want;
-    p.per_split = ((lm + want - 1) / want + 63) / 64 * 64;
-  }
+  auto per = [&](int w) { return ((lm + w - 1) / w + kStepRows - 1) / kStepRows * kStepRows; };
+  p.per_split = per(want);
+  while (p.per_split > kMaxList) p.per_split = per(++want);
   p.splits = (lm + p.per_split - 1) / p.per_split;
   return p;
 }
@@ -618,11 +540,11 @@ static bool bf16_dim_supported(int d) { return d == 64 || d == 128 || d == 256 |
 
 template <int D>
 static void launch_bf16_d(const MlaArgs& a, const MlaPlan& p, int64_t units, hipStream_t stream) {
-  if (p.prefill)
-    hipLaunchKernelGGL(mla_prefill_kernel<D>, dim3((unsigned)units, (unsigned)p.hgroups, 1), dim3(256), 0, stream, a);
+  const unsigned wgs = (unsigned)(units * p.hgroups * p.splits);
+  if (p.wide)
+    hipLaunchKernelGGL((mla_bf16_kernel<D, 4, 2>), dim3(wgs), dim3(512), 0, stream, a);
   else
-    hipLaunchKernelGGL(mla_decode_kernel<D>, dim3((unsigned)units, (unsigned)p.hgroups, (unsigned)p.splits), dim3(256),
-                       0, stream, a);
+    hipLaunchKernelGGL((mla_bf16_kernel<D, 2, 2>), dim3(wgs), dim3(256), 0, stream, a);
 }
 
 static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int dtype, void* workspace,
@@ -643,6 +565,10 @@ static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int
   DSV41_REQUIRE(bf16_dim_supported(a.dim), DSV41_E_SHAPE, "%s: bf16 path supports dim 64/128/256/512/576, got %d",
                 what, a.dim);
   const MlaPlan p = plan_bf16(units, a.heads, list_max);
+  DSV41_REQUIRE(units * p.hgroups * p.splits < (1ll << 31), DSV41_E_ARG, "%s: too many workgroups", what);
+  DSV41_REQUIRE(p.splits <= 64, DSV41_E_SHAPE, "%s: index list of %d entries is too long for the decode path", what,
+                list_max);
+  a.hgroups = p.hgroups;
   a.splits = p.splits;
   a.per_split = p.per_split;
   const size_t need = workspace_for(p, units, a.heads, a.dim);
@@ -663,7 +589,8 @@ static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int
   }
   int rc = check_launch(what);
   if (rc || p.splits == 1) return rc;
-  hipLaunchKernelGGL(mla_combine_kernel<bf16_t>, dim3((unsigned)units, (unsigned)a.heads), dim3(128), 0, stream, a);
+  hipLaunchKernelGGL(mla_combine_kernel<bf16_t>, dim3((unsigned)units, (unsigned)((a.heads + 3) / 4)), dim3(256), 0,
+                     stream, a);
   return check_launch(what);
 }
 

@@ -124,33 +124,23 @@ __device__ void ordered_select(SelShared& sh, KeyFn key, int count, uint32_t T, 
   }
 }
 
-// Histogram add where many lanes share a digit (the leading radix passes see most keys in a
-// few bins): the two most common digits of the wave are added with one atomic each, the
-// remaining lanes individually, so no LDS address takes more than a few atomics per instruction.
-__device__ __forceinline__ void hist_add(uint32_t* h, uint32_t digit, bool active, int lane) {
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const uint64_t act = __ballot(active);
-    if (act == 0ull) return;
-    const int leader = __ffsll((unsigned long long)act) - 1;
-    const uint32_t ld = (uint32_t)__shfl((int)digit, leader, 64);
-    const uint64_t peers = __ballot(active && digit == ld);
-    if (lane == leader) atomicAdd(&h[ld], (uint32_t)__popcll(peers));
-    if (digit == ld) active = false;
-  }
-  if (active) atomicAdd(&h[digit], 1u);
-}
-
-// Rows of up to J*1024 scores: every thread holds its J keys in registers (one batched
-// load), so the four radix passes and the compaction touch memory only for histograms.
+// Rows of up to J*1024 scores: thread t holds the J consecutive positions t*J .. t*J+J-1 in
+// registers (float4 loads), so the radix passes and the compaction touch memory only for
+// histograms and the output. Digits are 11, 11 and 10 bits wide: an 11-bit leading digit (sign,
+// exponent, two mantissa bits) spreads realistic score rows over enough bins that plain LDS
+// atomics stay cheap, and the later passes count only keys sharing the chosen prefix.
+// Histograms alternate between two buffers, so clearing the next one needs no extra barrier.
+// Compaction: one block scan of the packed per-thread (greater, equal) counts gives every thread
+// the number of selected positions before its own; it then walks its keys in position order.
 template <int J>
 __global__ __launch_bounds__(kSelThreads) void topk_reg_kernel(const float* __restrict__ scores,
                                                                int32_t* __restrict__ out, int n, int nb, int k,
-                                                               int start_pos, int ratio, int offset) {
-  constexpr int E = J * kSelWaves;               // (chunk, wave) count entries
-  constexpr int EL = (E + 63) / 64;              // entries per lane of wave 0 in the base scan
-  __shared__ uint32_t hist[kSelWaves][256];
-  __shared__ uint32_t cnt[2][E];                 // gt / eq counts, then exclusive bases
+                                                               int start_pos, int ratio, int offset, int vec) {
+  static_assert(J % 4 == 0, "keys are loaded as float4");
+  constexpr int NBIN = 2048;
+  static_assert(NBIN == 2 * kSelThreads, "each thread owns two bins in the suffix scan");
+  __shared__ uint32_t hist[2][NBIN];
+  __shared__ uint32_t wsum[kSelWaves];
   __shared__ uint32_t pick[2];
   const int64_t row = blockIdx.x;
   const float* x = scores + row * nb;
@@ -158,106 +148,105 @@ __global__ __launch_bounds__(kSelThreads) void topk_reg_kernel(const float* __re
   const int s = (int)(row % n);
   const int lens = (start_pos + s + 1) / ratio;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i0 = tid * J;
+  const int nvalid = min(max(nb - i0, 0), J);   // keys j < nvalid are real positions
 
+  if (k >= nb) {                                 // everything is selected, in order
+    for (int j = 0; j < nvalid; ++j) o[i0 + j] = i0 + j < lens ? i0 + j + offset : -1;
+    return;
+  }
   uint32_t key[J];
+  if (vec) {                                     // row 16-byte aligned, nb % 4 == 0
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int i = tid + j * kSelThreads;
-    key[j] = i < nb ? order_key(x[i]) : 0u;
-  }
-  uint32_t T = 0u;
-  int need = k;
-  if (k < nb) {
-    uint32_t prefix = 0u, pmask = 0u;
-    int kk = k;
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
-      // a wave clears and fills only its own histogram row: no barrier before the atomics
-      for (int d = lane; d < 256; d += 64) hist[wave][d] = 0u;
-#pragma unroll
-      for (int j = 0; j < J; ++j)
-        hist_add(hist[wave], (key[j] >> shift) & 255u, tid + j * kSelThreads < nb && (key[j] & pmask) == prefix,
-                 lane);
-      __syncthreads();
-      if (wave == 0) {
-        // lane l owns digits 255-4l .. 252-4l; scan from the highest digit down
-        uint32_t c[4], sum = 0u;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int d = 255 - 4 * lane - q;
-          uint32_t t = 0u;
-#pragma unroll
-          for (int w = 0; w < kSelWaves; ++w) t += hist[w][d];
-          c[q] = t;
-          sum += t;
-        }
-        uint32_t above = wave_incl_scan(sum, lane) - sum;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (above < (uint32_t)kk && (uint32_t)kk <= above + c[q]) {
-            pick[0] = (uint32_t)(255 - 4 * lane - q);
-            pick[1] = above;
-          }
-          above += c[q];
-        }
-      }
-      __syncthreads();
-      prefix |= pick[0] << shift;
-      pmask |= 255u << shift;
-      kk -= (int)pick[1];
+    for (int q = 0; q < J / 4; ++q) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (4 * q < nvalid) v = *reinterpret_cast<const float4*>(x + i0 + 4 * q);
+      key[4 * q + 0] = order_key(v.x);
+      key[4 * q + 1] = order_key(v.y);
+      key[4 * q + 2] = order_key(v.z);
+      key[4 * q + 3] = order_key(v.w);
     }
-    T = prefix;
-    need = kk;
-  }
-  // ordered compaction: keys > T, then the first `need` keys == T, in position order
-  const uint64_t below = (1ull << lane) - 1ull;
+  } else {
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int i = tid + j * kSelThreads;
-    const bool ok = i < nb && k < nb;
-    const uint64_t bg = __ballot(ok && key[j] > T);
-    const uint64_t be = __ballot(ok && key[j] == T);
-    if (lane == 0) {
-      cnt[0][j * kSelWaves + wave] = (uint32_t)__popcll(bg);
-      cnt[1][j * kSelWaves + wave] = (uint32_t)__popcll(be);
-    }
+    for (int j = 0; j < J; ++j) key[j] = j < nvalid ? order_key(x[i0 + j]) : 0u;
+  }
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi) {
+    hist[bi][tid] = 0u;
+    hist[bi][tid + kSelThreads] = 0u;
   }
   __syncthreads();
-  if (wave == 0) {
+
+  // exclusive prefix of the per-wave totals in wsum, for wave `wave` (all 16 reads in flight)
+  auto wave_base = [&]() {
+    uint32_t base = 0u;
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-      uint32_t v[EL], sum = 0u;
-#pragma unroll
-      for (int q = 0; q < EL; ++q) {
-        const int e = lane * EL + q;
-        v[q] = e < E ? cnt[f][e] : 0u;
-        sum += v[q];
-      }
-      uint32_t base = wave_incl_scan(sum, lane) - sum;
-#pragma unroll
-      for (int q = 0; q < EL; ++q) {
-        const int e = lane * EL + q;
-        if (e < E) cnt[f][e] = base;
-        base += v[q];
-      }
+    for (int w = 0; w < kSelWaves; ++w) {
+      const uint32_t v = wsum[w];
+      base += w < wave ? v : 0u;
     }
+    return base;
+  };
+
+  uint32_t prefix = 0u, pmask = 0u;
+  int kk = k;
+#pragma unroll
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const uint32_t dmask = pass == 2 ? 1023u : 2047u;
+    uint32_t* h = hist[pass & 1];
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (j < nvalid && (key[j] & pmask) == prefix) atomicAdd(&h[(key[j] >> shift) & dmask], 1u);
+    __syncthreads();                             // histogram complete
+    if (pass < 2) {                              // the other buffer was last read before the previous barrier
+      hist[(pass & 1) ^ 1][tid] = 0u;
+      hist[(pass & 1) ^ 1][tid + kSelThreads] = 0u;
+    }
+    // suffix scan from the highest digit down: thread t owns digits 2047-2t and 2046-2t
+    const uint32_t c0 = h[NBIN - 1 - 2 * tid], c1 = h[NBIN - 2 - 2 * tid];
+    const uint32_t pair = c0 + c1;
+    const uint32_t incl = wave_incl_scan(pair, lane);
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    const uint32_t above = wave_base() + incl - pair;
+    if (above < (uint32_t)kk && (uint32_t)kk <= above + c0) {
+      pick[0] = (uint32_t)(NBIN - 1 - 2 * tid);
+      pick[1] = above;
+    } else if (above + c0 < (uint32_t)kk && (uint32_t)kk <= above + pair) {
+      pick[0] = (uint32_t)(NBIN - 2 - 2 * tid);
+      pick[1] = above + c0;
+    }
+    __syncthreads();
+    prefix |= pick[0] << shift;
+    pmask |= dmask << shift;
+    kk -= (int)pick[1];
   }
-  __syncthreads();
+  const uint32_t T = prefix;
+  const uint32_t need = (uint32_t)kk;            // keys == T to take, lowest positions first
+
+  uint32_t cg = 0u, ce = 0u;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int i = tid + j * kSelThreads;
-    if (k >= nb) {                       // everything selected, in order
-      if (i < nb) o[i] = i < lens ? i + offset : -1;
-      continue;
-    }
-    const bool ok = i < nb;
-    const bool gt = ok && key[j] > T, eq = ok && key[j] == T;
-    const uint64_t bg = __ballot(gt), be = __ballot(eq);
-    const uint32_t gt_before = cnt[0][j * kSelWaves + wave] + (uint32_t)__popcll(bg & below);
-    const uint32_t eq_before = cnt[1][j * kSelWaves + wave] + (uint32_t)__popcll(be & below);
-    if (gt || (eq && eq_before < (uint32_t)need)) {
-      const uint32_t pos = gt_before + min(eq_before, (uint32_t)need);
-      if (pos < (uint32_t)k) o[pos] = i < lens ? i + offset : -1;
+    cg += (j < nvalid && key[j] > T) ? 1u : 0u;
+    ce += (j < nvalid && key[j] == T) ? 1u : 0u;
+  }
+  const uint32_t packed = (cg << 16) | ce;       // counts <= 32768: no carry between halves
+  const uint32_t incl = wave_incl_scan(packed, lane);
+  if (lane == 63) wsum[wave] = incl;             // last read before the final pass barrier
+  __syncthreads();
+  const uint32_t excl = wave_base() + incl - packed;
+  uint32_t gt_before = excl >> 16, eq_before = excl & 0xFFFFu;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    if (j >= nvalid) break;
+    const int i = i0 + j;
+    if (key[j] > T) {
+      o[gt_before + min(eq_before, need)] = i < lens ? i + offset : -1;
+      ++gt_before;
+    } else if (key[j] == T) {
+      if (eq_before < need) o[gt_before + eq_before] = i < lens ? i + offset : -1;
+      ++eq_before;
     }
   }
 }
@@ -337,14 +326,17 @@ extern "C" int dsv41_topk_select(const float* scores, int32_t* out, int64_t rows
   const int k = topk < nb ? topk : nb;
   if (rows == 0 || k == 0) return 0;
   const dim3 grid((unsigned)rows), block(kSelThreads);
+  const int vec = (nb % 4 == 0 && aligned16(scores)) ? 1 : 0;
   if (nb <= 4 * kSelThreads)
-    hipLaunchKernelGGL(topk_reg_kernel<4>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset);
+    hipLaunchKernelGGL(topk_reg_kernel<4>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset, vec);
   else if (nb <= 8 * kSelThreads)
-    hipLaunchKernelGGL(topk_reg_kernel<8>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset);
+    hipLaunchKernelGGL(topk_reg_kernel<8>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset, vec);
   else if (nb <= 16 * kSelThreads)
-    hipLaunchKernelGGL(topk_reg_kernel<16>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset);
+    hipLaunchKernelGGL(topk_reg_kernel<16>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset,
+                       vec);
   else if (nb <= 32 * kSelThreads)
-    hipLaunchKernelGGL(topk_reg_kernel<32>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset);
+    hipLaunchKernelGGL(topk_reg_kernel<32>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset,
+                       vec);
   else
     hipLaunchKernelGGL(topk_kernel, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset);
   return check_launch(what);

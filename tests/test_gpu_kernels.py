@@ -244,7 +244,9 @@ def _score_sets(rng, b, n, nb):
 
 @pytest.mark.parametrize("b,n,nb,topk,start,r", [(2, 3, 40, 16, 100, 4), (4, 1, 4096, 512, 16383, 4),
                                                   (1, 64, 1000, 256, 3000, 4), (2, 1, 16384, 512, 65535, 4),
-                                                  (1, 2, 300, 512, 1199, 4), (1, 5, 2049, 2048, 8191, 4)])
+                                                  (1, 2, 300, 512, 1199, 4), (1, 5, 2049, 2048, 8191, 4),
+                                                  (1, 2, 32768, 2048, 131071, 4), (1, 3, 5001, 700, 20003, 4),
+                                                  (1, 1, 40000, 1000, 159999, 4)])
 def test_topk_bit_exact(gpu, b, n, nb, topk, start, r):
     from dsv41 import _abi
     rng = rng_for(f"topk{nb}{n}")
