@@ -22,7 +22,6 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
     float* __restrict__ scores, int n, int nb, int start_pos, int ratio, int rows_per_wg) {
   constexpr int H = HT * 16;
   constexpr int DIM = KS * 32;
-  constexpr int QUART = DIM / 4;           // dims owned by one lane group (k permutation)
   constexpr int QROW = DIM * 2 + 16;       // padded LDS row stride in bytes
   __shared__ __align__(16) uint8_t q_lds[H * QROW];
 
@@ -51,7 +50,7 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
   for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      qa[ht][ks] = ld_bf16x8(q_lds + (ht * 16 + l16) * QROW + (g * QUART + ks * 8) * 2);
+      qa[ht][ks] = ld_bf16x8(q_lds + (ht * 16 + l16) * QROW + (ks * 32 + g * 8) * 2);
   float wv[HT][4];
   const bf16_t* wrow = w_raw + (int64_t)qi * H;
 #pragma unroll
@@ -59,25 +58,34 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wrow[ht * 16 + 4 * g + i]) * w_scale);
 
-  const bf16_t* kb = kcache + (int64_t)b * k_bstride + g * QUART;
+  // natural MFMA k order (k = 32 ks + 8 g + i): one load instruction reads a contiguous 64-byte
+  // span of each of its 16 rows
+  const bf16_t* kb = kcache + (int64_t)b * k_bstride + g * 8;
   const uint8_t* cb = cand ? cand + (int64_t)qi * nb : nullptr;
   constexpr int NW = kIdxThreads / 64;
 
-  // four 16-row tiles per iteration: every load of the four is issued before any is consumed
-  constexpr int U = 4;
-  for (int t0 = r0 + 16 * U * wave; t0 < vis_end; t0 += 16 * U * NW) {
-    bf16x8 kk[U][KS];
+  // Four 16-row tiles per batch; the next batch is always in flight while the current one is
+  // computed (two register sets). Loads are unconditional -- rows past the visible range are
+  // clamped onto its last row -- so every batch issues the same number of loads and the
+  // compiler's wait counts stay exact across iterations.
+  constexpr int U = HT >= 8 ? 2 : 4;       // 128 heads: the query block alone takes 128 VGPRs
+  constexpr int STRIDE = 16 * U * NW;
+  // candidate flags of a batch travel with its key loads, so no load is issued behind the batch
+  // that is waited on before it
+  auto load = [&](bf16x8 (&kk)[U][KS], uint32_t (&cf)[U], int t0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int row = min(t0 + 16 * u + l16, vis_end - 1);   // clamp: loads stay inside the cache
       const bf16_t* kr = kb + (int64_t)row * DIM;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kk[u][ks] = ld_bf16x8(kr + ks * 8);
+      for (int ks = 0; ks < KS; ++ks) kk[u][ks] = ld_bf16x8(kr + ks * 32);
+      cf[u] = cb ? (uint32_t)cb[row] : 1u;
     }
+  };
+  auto compute = [&](const bf16x8 (&kk)[U][KS], const uint32_t (&cf)[U], int t0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int tb = t0 + 16 * u;
-      if (tb >= vis_end) break;
       f32x4 acc[HT];
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) acc[ht] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -94,11 +102,24 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
       part += __shfl_xor(part, 32, 64);
       const int row = tb + l16;
       if (g == 0 && row < vis_end) {
-        float v = part;
-        if (cb && !cb[row]) v = -INFINITY;
-        out[row] = v;
+        out[row] = cf[u] ? part : -INFINITY;
       }
     }
+  };
+  int t0 = r0 + 16 * U * wave;
+  if (t0 >= vis_end) return;
+  bf16x8 ka[U][KS], kb2[U][KS];
+  uint32_t ca[U], cb2[U];
+  load(ka, ca, t0);
+  for (;;) {
+    load(kb2, cb2, t0 + STRIDE);
+    compute(ka, ca, t0);
+    t0 += STRIDE;
+    if (t0 >= vis_end) break;
+    load(ka, ca, t0 + STRIDE);
+    compute(kb2, cb2, t0);
+    t0 += STRIDE;
+    if (t0 >= vis_end) break;
   }
 }
 

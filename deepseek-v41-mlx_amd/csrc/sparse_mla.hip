@@ -230,11 +230,14 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
     for (int ks = 0; ks < KSS; ++ks) qb[ks] = hok ? ld_bf16x8(qrow + ks * 32 + 8 * g) : zero_bf16x8();
   }
   const float sl2 = a.scale * kLog2e;
-  float m_run = kNegFloor, l_run = 0.0f;   // m_run: the exponent reference of acc and l_run
+  // m_run: the exponent reference of acc and l_run, shared by the 4 lane groups of a head.
+  // l_run: this lane's share of the denominator (its own rows); the lane groups are summed once
+  // after the loop, so the sink term is seeded in lane group 0 only.
+  float m_run = kNegFloor, l_run = 0.0f;
   if (sp == 0 && hok) {
     const float s2 = a.sink[h] * kLog2e;
     m_run = fmaxf(s2, kNegFloor);
-    l_run = exp2f(s2 - m_run);
+    l_run = g == 0 ? exp2f(s2 - m_run) : 0.0f;
   }
   f32x4 acc[DTS];
 #pragma unroll
@@ -258,17 +261,22 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   for (int t = 0; t < nsteps; ++t) {
     wait_steps<NL>(min(nsteps - 1 - t, NS - 2));
     __syncthreads();                       // step t landed; every wave is done with step t-1
-    if (t + NS - 1 < nsteps) issue(t + NS - 1);
     const int slot = t % NS;
     const uint8_t* buf = ring + slot * SLOT;
-    f32x4 sacc[2];
-    sacc[0] = sacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // four independent MFMA chains (row tile x k parity)
+    f32x4 sq[2][2];
+    sq[0][0] = sq[0][1] = sq[1][0] = sq[1][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KSS; ++ks)
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt)
-        sacc[rt] = mfma16x16x32(ld_bf16x8(buf + (rt * 16 + l16) * RS + (dh * DSL + ks * 32 + 8 * g) * 2), qb[ks],
-                                sacc[rt]);
+        sq[rt][ks & 1] = mfma16x16x32(ld_bf16x8(buf + (rt * 16 + l16) * RS + (dh * DSL + ks * 32 + 8 * g) * 2),
+                                      qb[ks], sq[rt][ks & 1]);
+    // the next copies go out while the MFMAs drain (slot (t-1) % NS is free past the barrier)
+    if (t + NS - 1 < nsteps) issue(t + NS - 1);
+    f32x4 sacc[2];
+    sacc[0] = sq[0][0] + sq[0][1];
+    sacc[1] = sq[1][0] + sq[1][1];
     if constexpr (DS > 1) {
       xs[wave][0][lane] = sacc[0];
       xs[wave][1][lane] = sacc[1];
@@ -294,25 +302,23 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
         p[rt * 4 + i] = ok ? l2 : -INFINITY;
         if (ok) tmax = fmaxf(tmax, l2);
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const bool grow = tmax > m_run + kRescale;
-    if (__any(grow)) {
-      const float alpha = grow ? fast_exp2(m_run - tmax) : 1.0f;
+    // lazy rescale: only when some lane's rows exceed the shared reference by kRescale is the
+    // head's exact maximum over its 4 lane groups formed (two shuffles) and the reference moved
+    if (__any(tmax > m_run + kRescale)) {
+      float gmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      gmax = fmaxf(gmax, __shfl_xor(gmax, 32, 64));
+      const bool grow = gmax > m_run + kRescale;
+      const float alpha = grow ? fast_exp2(m_run - gmax) : 1.0f;
 #pragma unroll
       for (int dt = 0; dt < DTS; ++dt) acc[dt] *= alpha;
       l_run *= alpha;
-      m_run = grow ? tmax : m_run;
+      m_run = grow ? gmax : m_run;
     }
-    float psum = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       p[e] = fast_exp2(p[e] - m_run);
-      psum += p[e];
+      l_run += p[e];
     }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l_run += psum;
     const bf16x8 pb = cvt_bf16x8(p);
 #pragma unroll
     for (int dt = 0; dt < DTS; ++dt) {
@@ -323,6 +329,8 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
     }
   }
 
+  l_run += __shfl_xor(l_run, 16, 64);      // denominator: sum of the 4 lane groups
+  l_run += __shfl_xor(l_run, 32, 64);
   if (!hok) return;                        // no barrier follows
   const int64_t slot_id = ((int64_t)unit * a.splits + sp) * a.heads + h;
   bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + h) * D;

@@ -414,7 +414,9 @@ def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale):
 def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_scale, window,
                start_pos, cos=None, sin=None, rd=0, out=None, workspace=None):
     """The layer form: window ring + this chunk's KV + the owner's compressed cache, all read
-    in place. comp_kv: [b, >=n_comp, d] view (or None); idx [b, n, k] int32 or None."""
+    in place. comp_kv: [b, >=n_comp, d] view (or None); idx [b, n, k] int32 or None.
+    workspace: a uint8 scratch tensor of at least mla_workspace_bytes(...) bytes, allocated
+    when it is omitted or too small."""
     name = "dsv41_sparse_mla"
     _gpu(name, q, win_kv, chunk_kv, comp_kv, attn_sink, idx, cos, sin, out)
     _contig(name, q, chunk_kv, attn_sink, idx)

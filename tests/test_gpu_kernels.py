@@ -352,6 +352,40 @@ def test_sparse_mla_in_place_sources(gpu, dt, b, n, h, d, window, start, n_comp,
         assert rel_max_diff(g, want) < 2e-2
 
 
+def test_sparse_mla_split_lists_reuse_workspace(gpu):
+    """Decode lists split 14 ways and merged: one workspace serves consecutive calls (different
+    data, then a smaller batch)."""
+    from dsv41 import _abi
+    d, h, window, start, rd = 512, 64, 128, 40000, 64
+    rc, rs = R.precompute_freqs_cis(rd, start + 2, 65536, 160000.0, 16.0, 32, 1)
+    n_comp, k = 9000, 2000                    # 2128 rows per query: 16 splits at batch 8
+    ws = None
+    for call, b in enumerate((8, 8, 3)):
+        rng = rng_for(f"mlaws{call}")
+        q = R.cast(rng.standard_normal((b, 1, h, d)).astype(F32) * 2, "bf16")
+        win = R.cast(rng.standard_normal((b, window, d)).astype(F32), "bf16")
+        chunk = R.cast(rng.standard_normal((b, 1, d)).astype(F32), "bf16")
+        comp = R.cast(rng.standard_normal((b, n_comp, d)).astype(F32), "bf16")
+        sink = rng.standard_normal(h).astype(F32)
+        cidx = np.sort(rng.integers(0, n_comp, size=(b, 1, k)), axis=-1)
+        cidx[:, :, ::7] = -1
+        cidx = np.where(cidx >= 0, cidx + window + 1, -1).astype(np.int32)
+        nbytes = _abi.mla_workspace_bytes(b, 1, h, d, window + k, torch.bfloat16)
+        assert nbytes > 0
+        if ws is None:
+            ws = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+        assert ws.numel() >= nbytes
+        got = _abi.sparse_mla(dev(q, "bf16"), dev(win, "bf16"), dev(chunk, "bf16"), dev(comp, "bf16"), n_comp,
+                              dev(sink), torch.as_tensor(cidx).to(gpu), d ** -0.5, window, start, dev(rc), dev(rs),
+                              rd, workspace=ws)
+        torch.cuda.synchronize()
+        kv_all = _concat_reference(win, chunk, comp, n_comp, start, window)
+        widx = np.broadcast_to(R.window_idx_matrix(window, 1, window)[None], (b, 1, window))
+        o = R.sparse_attn(q, kv_all, sink, np.concatenate([widx, cidx], axis=-1), d ** -0.5, dtype="bf16")
+        want = R.rope_tail(o, rd, rc[[start]], rs[[start]], inverse=True, dtype="bf16")
+        assert rel_max_diff(to_np(got), want) < 2e-2, f"call {call}"
+
+
 def test_reference_kernel_module_seam(gpu):
     """dsv41.kernel stands in for the reference model's native `kernel` module."""
     import dsv41.kernel as K
