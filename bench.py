@@ -47,7 +47,27 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--eager", action="store_true",
                    help="launch the decode kernels without HIP graphs (for counter-collecting profilers)")
+    p.add_argument("--calib-mb", type=int, default=0,
+                   help="eager mode: also run a plain streaming copy of this many MB (read and write), "
+                        "the reference kernel for scaling HBM byte counters")
     return p.parse_args()
+
+
+# HBM bytes per indexer launch, from two rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE)
+# scaled by the same counters over a copy of known size; the summary names its commands.
+TRAFFIC_FILE = "profiles/indexer_score_bs32_ctx64k_hbm_traffic.md"
+
+
+def measured_traffic():
+    path = os.path.join(ROOT, TRAFFIC_FILE)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg):
@@ -176,6 +196,15 @@ def run_decode(args, torch, device):
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / args.steps
         log(f"[bench] eager decode step {ms * 1e3:.2f} us (host-bound timing)")
+        if args.calib_mb:
+            # plain streaming copy (elementwise kernel: N MB read, N MB written) for counter scaling
+            n = args.calib_mb << 20
+            src = torch.ones(n // 2, dtype=torch.bfloat16, device=device)
+            dst = torch.empty_like(src)
+            for _ in range(4):
+                torch.neg(src, out=dst)
+            torch.cuda.synchronize()
+            log(f"[bench] calibration copy of {args.calib_mb} MB x4 done")
         kern = {"indexer_score": float("nan"), "topk_select": float("nan"), "sparse_mla": float("nan")}
         return s, ms, kern, sets, cos, sin, ws, []
     g_full = graph_of(full, sets, torch)
@@ -344,7 +373,8 @@ def main():
         "kernels_us": {k: v * 1e3 for k, v in kern.items()},
         "roofline": {"bound": "hbm", "kernel": "indexer_score (dsv41_indexer_score, bf16 MFMA)",
                      "achieved": idx_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": idx_gbs / HBM_PEAK_GBS,
-                     "traffic": None,
+                     "traffic": measured_traffic(),
+                     "traffic_source": TRAFFIC_FILE,
                      "bytes_per_launch": s.bytes_indexer(), "avg_launch_us": kern["indexer_score"] * 1e3},
     }
     if not args.no_prefill:
