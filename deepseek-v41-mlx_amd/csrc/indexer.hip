@@ -15,11 +15,30 @@ namespace dsv41 {
 
 constexpr int kIdxThreads = 512;  // 8 waves
 
-template <int HT, int KS>
+// One batch of U 16-row key tiles in the MFMA B-operand layout: bf16 rows, or (F8) e4m3 codes
+// with the row block's ue8m0 scale bytes (one per 32 channels), dequantized to bf16 at use.
+template <bool F8, int U, int KS> struct KeyBatch;
+template <int U, int KS> struct KeyBatch<false, U, KS> {
+  bf16x8 k[U][KS];
+  uint32_t cf[U];
+  __device__ __forceinline__ bf16x8 op(int u, int ks) const { return k[u][ks]; }
+};
+template <int U, int KS> struct KeyBatch<true, U, KS> {
+  uint2 k[U][KS];
+  uint32_t sc[U];
+  uint32_t cf[U];
+  __device__ __forceinline__ bf16x8 op(int u, int ks) const {
+    return dequant_e4m3x8(k[u][ks].x, k[u][ks].y, e8m0_to_float((sc[u] >> (8 * ks)) & 255u));
+  }
+};
+
+template <int HT, int KS, bool F8>
 __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ w_raw, float w_scale,
-    const bf16_t* __restrict__ kcache, int64_t k_bstride, const uint8_t* __restrict__ cand,
-    float* __restrict__ scores, int n, int nb, int start_pos, int ratio, int rows_per_wg) {
+    const void* __restrict__ kcache, int64_t k_bstride, const uint8_t* __restrict__ kscale, int64_t ks_bstride,
+    int ks_rb, const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int nb, int start_pos, int ratio,
+    int rows_per_wg) {
+  static_assert(!F8 || KS == 4, "fp8 keys: 128 channels (four scale bytes per row block)");
   constexpr int H = HT * 16;
   constexpr int DIM = KS * 32;
   constexpr int QROW = DIM * 2 + 16;       // padded LDS row stride in bytes
@@ -59,8 +78,10 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
     for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wrow[ht * 16 + 4 * g + i]) * w_scale);
 
   // natural MFMA k order (k = 32 ks + 8 g + i): one load instruction reads a contiguous 64-byte
-  // span of each of its 16 rows
-  const bf16_t* kb = kcache + (int64_t)b * k_bstride + g * 8;
+  // (fp8: 32-byte) span of each of its 16 rows
+  const bf16_t* kb = reinterpret_cast<const bf16_t*>(kcache) + (int64_t)b * k_bstride + g * 8;
+  const uint8_t* kb8 = reinterpret_cast<const uint8_t*>(kcache) + (int64_t)b * k_bstride + g * 8;
+  const uint8_t* ksb = F8 ? kscale + (int64_t)b * ks_bstride : nullptr;
   const uint8_t* cb = cand ? cand + (int64_t)qi * nb : nullptr;
   constexpr int NW = kIdxThreads / 64;
 
@@ -72,17 +93,25 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
   constexpr int STRIDE = 16 * U * NW;
   // candidate flags of a batch travel with its key loads, so no load is issued behind the batch
   // that is waited on before it
-  auto load = [&](bf16x8 (&kk)[U][KS], uint32_t (&cf)[U], int t0) {
+  using Batch = KeyBatch<F8, U, KS>;
+  auto load = [&](Batch& kk, int t0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int row = min(t0 + 16 * u + l16, vis_end - 1);   // clamp: loads stay inside the cache
-      const bf16_t* kr = kb + (int64_t)row * DIM;
+      if constexpr (F8) {
+        const uint8_t* kr = kb8 + (int64_t)row * DIM;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kk[u][ks] = ld_bf16x8(kr + ks * 32);
-      cf[u] = cb ? (uint32_t)cb[row] : 1u;
+        for (int ks = 0; ks < KS; ++ks) kk.k[u][ks] = *reinterpret_cast<const uint2*>(kr + ks * 32);
+        kk.sc[u] = *reinterpret_cast<const uint32_t*>(ksb + (int64_t)(row / ks_rb) * 4);
+      } else {
+        const bf16_t* kr = kb + (int64_t)row * DIM;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kk.k[u][ks] = ld_bf16x8(kr + ks * 32);
+      }
+      kk.cf[u] = cb ? (uint32_t)cb[row] : 1u;
     }
   };
-  auto compute = [&](const bf16x8 (&kk)[U][KS], const uint32_t (&cf)[U], int t0) {
+  auto compute = [&](const Batch& kk, int t0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int tb = t0 + 16 * u;
@@ -90,9 +119,11 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) acc[ht] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 kop = kk.op(u, ks);
 #pragma unroll
-        for (int ht = 0; ht < HT; ++ht) acc[ht] = mfma16x16x32(qa[ht][ks], kk[u][ks], acc[ht]);
+        for (int ht = 0; ht < HT; ++ht) acc[ht] = mfma16x16x32(qa[ht][ks], kop, acc[ht]);
+      }
       float part = 0.0f;
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht)
@@ -102,22 +133,21 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
       part += __shfl_xor(part, 32, 64);
       const int row = tb + l16;
       if (g == 0 && row < vis_end) {
-        out[row] = cf[u] ? part : -INFINITY;
+        out[row] = kk.cf[u] ? part : -INFINITY;
       }
     }
   };
   int t0 = r0 + 16 * U * wave;
   if (t0 >= vis_end) return;
-  bf16x8 ka[U][KS], kb2[U][KS];
-  uint32_t ca[U], cb2[U];
-  load(ka, ca, t0);
+  Batch ka, kb2;
+  load(ka, t0);
   for (;;) {
-    load(kb2, cb2, t0 + STRIDE);
-    compute(ka, ca, t0);
+    load(kb2, t0 + STRIDE);
+    compute(ka, t0);
     t0 += STRIDE;
     if (t0 >= vis_end) break;
-    load(ka, ca, t0 + STRIDE);
-    compute(kb2, cb2, t0);
+    load(ka, t0 + STRIDE);
+    compute(kb2, t0);
     t0 += STRIDE;
     if (t0 >= vis_end) break;
   }
@@ -154,13 +184,25 @@ __global__ __launch_bounds__(256) void indexer_score_f32_kernel(
   scores[(int64_t)qi * nb + t] = v;
 }
 
-template <int HT, int KS>
+template <int HT, int KS, bool F8>
 static void launch_idx_bf16(dim3 grid, hipStream_t stream, const void* q, const void* w_raw, float w_scale,
-                            const void* index_k, int64_t k_bstride, const uint8_t* cand, float* scores, int n,
-                            int nb, int start_pos, int ratio, int rows_per_wg) {
-  hipLaunchKernelGGL((indexer_score_bf16_kernel<HT, KS>), grid, dim3(kIdxThreads), 0, stream,
-                     (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, (const bf16_t*)index_k, k_bstride, cand,
-                     scores, n, nb, start_pos, ratio, rows_per_wg);
+                            const void* index_k, int64_t k_bstride, const uint8_t* kscale, int64_t ks_bstride,
+                            int ks_rb, const uint8_t* cand, float* scores, int n, int nb, int start_pos, int ratio,
+                            int rows_per_wg) {
+  hipLaunchKernelGGL((indexer_score_bf16_kernel<HT, KS, F8>), grid, dim3(kIdxThreads), 0, stream,
+                     (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, index_k, k_bstride, kscale, ks_bstride, ks_rb,
+                     cand, scores, n, nb, start_pos, ratio, rows_per_wg);
+}
+
+// ~256 workgroups over all rows (one per CU), in multiples of one 8-wave sweep of four tiles
+// (512 rows): long-lived workgroups amortize staging the query block
+static dim3 idx_grid(int64_t rows_total, int nb, int bn, int* rows_per_wg) {
+  const int64_t want = (rows_total + 255) / 256;
+  int r = (int)((want + 511) / 512 * 512);
+  if (r < 512) r = 512;
+  if (r > 4096) r = 4096;
+  *rows_per_wg = r;
+  return dim3((unsigned)((nb + r - 1) / r), (unsigned)bn);
 }
 
 }  // namespace dsv41
@@ -191,18 +233,13 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
   if (dtype != DSV41_BF16) return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported", what, dtype);
   DSV41_REQUIRE(aligned16(q) && aligned16(index_k), DSV41_E_ARG, "%s: q and index_k must be 16-byte aligned", what);
   DSV41_REQUIRE(k_bstride % 8 == 0, DSV41_E_ARG, "%s: k_bstride must be a multiple of 8", what);
-  // ~256 workgroups over all rows (one per CU), in multiples of one 8-wave sweep of four tiles
-  // (512 rows): long-lived workgroups amortize staging the query block
-  const int64_t want = ((int64_t)nb * bsz * n + 255) / 256;
-  int rows_per_wg = (int)((want + 511) / 512 * 512);
-  if (rows_per_wg < 512) rows_per_wg = 512;
-  if (rows_per_wg > 4096) rows_per_wg = 4096;
-  dim3 grid((unsigned)((nb + rows_per_wg - 1) / rows_per_wg), (unsigned)(bsz * n));
-#define DSV41_IDX_CASE(HT_, KS_)                                                                          \
-  if (heads == HT_ * 16 && dim == KS_ * 32) {                                                             \
-    launch_idx_bf16<HT_, KS_>(grid, stream, q, w_raw, w_scale, index_k, k_bstride, candidates, scores, n, \
-                              nb, start_pos, ratio, rows_per_wg);                                         \
-    return check_launch(what);                                                                            \
+  int rows_per_wg = 0;
+  const dim3 grid = idx_grid((int64_t)nb * bsz * n, nb, bsz * n, &rows_per_wg);
+#define DSV41_IDX_CASE(HT_, KS_)                                                                             \
+  if (heads == HT_ * 16 && dim == KS_ * 32) {                                                                \
+    launch_idx_bf16<HT_, KS_, false>(grid, stream, q, w_raw, w_scale, index_k, k_bstride, nullptr, 0, 1,     \
+                                     candidates, scores, n, nb, start_pos, ratio, rows_per_wg);              \
+    return check_launch(what);                                                                               \
   }
   DSV41_IDX_CASE(4, 4)   // 64 heads x 128
   DSV41_IDX_CASE(2, 4)   // 32 heads x 128 (the released model)
@@ -216,4 +253,39 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
   DSV41_IDX_CASE(4, 1)
 #undef DSV41_IDX_CASE
   return set_error(DSV41_E_SHAPE, "%s: bf16 path has no instance for heads=%d dim=%d", what, heads, dim);
+}
+
+extern "C" int dsv41_indexer_score_fp8(const void* q, const void* w_raw, float w_scale, const uint8_t* index_k,
+                                       int64_t k_bstride, const uint8_t* k_scale, int64_t ks_bstride, int32_t ks_rb,
+                                       const uint8_t* candidates, float* scores, int32_t bsz, int32_t n,
+                                       int32_t heads, int32_t dim, int32_t nb, int32_t start_pos, int32_t ratio,
+                                       hipStream_t stream) {
+  const char* what = "dsv41_indexer_score_fp8";
+  DSV41_REQUIRE(q && w_raw && index_k && k_scale && scores, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(bsz >= 0 && n >= 0 && heads > 0 && nb >= 0 && start_pos >= 0 && ratio > 0, DSV41_E_ARG,
+                "%s: bad sizes", what);
+  DSV41_REQUIRE(dim == 128, DSV41_E_SHAPE, "%s: fp8 index keys support dim 128, got %d", what, dim);
+  DSV41_REQUIRE(ks_rb == 1 || ks_rb == 32, DSV41_E_ARG, "%s: scale row block must be 1 or 32", what);
+  DSV41_REQUIRE(k_bstride >= (int64_t)nb * dim, DSV41_E_ARG, "%s: k_bstride too small", what);
+  DSV41_REQUIRE(ks_bstride >= (int64_t)((nb + ks_rb - 1) / ks_rb) * (dim / 32), DSV41_E_ARG,
+                "%s: ks_bstride too small", what);
+  DSV41_REQUIRE((int64_t)bsz * n < 65536, DSV41_E_ARG, "%s: bsz*n must be < 65536", what);
+  DSV41_REQUIRE(aligned16(q) && aligned16(index_k) && (reinterpret_cast<uintptr_t>(k_scale) & 3u) == 0,
+                DSV41_E_ARG, "%s: q and index_k must be 16-byte aligned, k_scale 4-byte aligned", what);
+  DSV41_REQUIRE(k_bstride % 16 == 0 && ks_bstride % 4 == 0, DSV41_E_ARG,
+                "%s: k_bstride must be a multiple of 16 bytes, ks_bstride of 4", what);
+  if ((int64_t)bsz * n == 0 || nb == 0) return 0;
+  int rows_per_wg = 0;
+  const dim3 grid = idx_grid((int64_t)nb * bsz * n, nb, bsz * n, &rows_per_wg);
+#define DSV41_IDX8_CASE(HT_)                                                                                   \
+  if (heads == HT_ * 16) {                                                                                     \
+    launch_idx_bf16<HT_, 4, true>(grid, stream, q, w_raw, w_scale, index_k, k_bstride, k_scale, ks_bstride,  \
+                                  ks_rb, candidates, scores, n, nb, start_pos, ratio, rows_per_wg);            \
+    return check_launch(what);                                                                                 \
+  }
+  DSV41_IDX8_CASE(4)   // 64 heads
+  DSV41_IDX8_CASE(2)   // 32 heads
+  DSV41_IDX8_CASE(1)
+#undef DSV41_IDX8_CASE
+  return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
 }

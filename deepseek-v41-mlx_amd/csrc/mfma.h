@@ -50,6 +50,13 @@ __device__ __forceinline__ void dma16_sgpr(uint64_t base, uint32_t voff, uint32_
                : "memory", "m0");
 }
 
+// Same copy with a per-lane 64-bit address (vaddr form): lanes may read from different
+// buffers, e.g. a row's data and its block scales in one instruction.
+__device__ __forceinline__ void dma16_vaddr(uint64_t addr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(addr), "s"(lds)
+               : "memory", "m0");
+}
+
 // LDS byte offset of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
@@ -93,5 +100,23 @@ __device__ __forceinline__ bf16x8 cvt_bf16x8(const float* v) {
 // 2^x with the bare v_exp_f32 (no denormal-range fix-up). Used for softmax weights 2^(s - m) with
 // s - m <= the lazy-rescale threshold: results below 2^-126 are zero for the sum anyway.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ue8m0 scale byte -> float 2^(e-127) (e = 0 is 2^-127, a subnormal; 255 is NaN).
+__device__ __forceinline__ float e8m0_to_float(uint32_t e) {
+  return e == 0u ? __uint_as_float(0x00400000u) : (e == 255u ? __uint_as_float(0x7fc00000u) : __uint_as_float(e << 23));
+}
+
+// 8 e4m3fn codes (two dwords) times a power-of-two scale -> MFMA operand. Exact: e4m3 values
+// scaled by 2^k are bf16-representable within bf16's exponent range. v_cvt_pk_f32_fp8 decodes
+// OCP e4m3fn on gfx950, subnormals included.
+__device__ __forceinline__ bf16x8 dequant_e4m3x8(uint32_t lo, uint32_t hi, float scale) {
+  typedef __attribute__((ext_vector_type(2))) float f2;
+  float v[8];
+  const f2 a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+  const f2 c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+  v[0] = a[0] * scale; v[1] = a[1] * scale; v[2] = b[0] * scale; v[3] = b[1] * scale;
+  v[4] = c[0] * scale; v[5] = c[1] * scale; v[6] = d[0] * scale; v[7] = d[1] * scale;
+  return cvt_bf16x8(v);
+}
 
 }  // namespace dsv41

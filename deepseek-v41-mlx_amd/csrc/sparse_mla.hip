@@ -26,6 +26,9 @@ struct KvSrc {
   const void* ring;  int64_t ring_bstride;  int window, wp, ring_first;
   const void* chunk; int64_t chunk_bstride; int n_chunk;
   const void* comp;  int64_t comp_bstride;  int n_comp;
+  // fp8 compressed cache (F8 kernels): e4m3 rows, one ue8m0 byte per 32 channels for every
+  // block of comp_scale_rb rows (1 or 32), comp_scale_bstride bytes per batch row
+  const uint8_t* comp_scale; int64_t comp_scale_bstride; int comp_scale_rb;
   const int32_t* idx; int k;
   int win_implicit;
 };
@@ -185,7 +188,11 @@ struct MlaLds {
 // Register footprint per wave: Q^T slice D/DS/8 + accumulators D/DS/4 VGPRs.
 // (__launch_bounds__'s second argument asks for 2 waves per SIMD: a 256-register budget, which
 // keeps the accumulators in VGPRs instead of AGPR copies around every MFMA block.)
-template <int D, int HT, int DS>
+// F8: the compressed cache is fp8 (e4m3 + ue8m0 block scales). Such a row and its scale bytes
+// arrive in the second half of its bf16 slot row ([D, 2D) data, [2D, 2D + D/32) scales -- the
+// row padding) with one copy instruction, so copy counts and waits are unchanged; after its own
+// copies land, the issuing wave dequantizes the row in place to bf16, before the step barrier.
+template <int D, int HT, int DS, bool F8>
 __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   constexpr int NW = HT * DS, NT = 64 * NW;
   constexpr int DSL = D / DS, KSS = DSL / 32, DTS = DSL / 16;
@@ -217,8 +224,14 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   const int cnt = min(max(min(e_begin + a.per_split, L) - e_begin, 0), kMaxList);  // planner: <= kMaxList
   // resolve the split's list once (segment, ring slot, batch row): no global reads are left
   // inside the copy pipeline and a step spends a few instructions per row
-  for (int e = tid; e < cnt; e += NT)
-    rows[e] = reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, list_pos(S, b, a.m, qs, e_begin + e, wc), D));
+  // (F8: a compressed-cache entry is stored as (row << 1) | 1 and addressed at issue time)
+  static_assert(!F8 || D == 512, "fp8 cache rows: 512 channels (one copy instruction with their scales)");
+  for (int e = tid; e < cnt; e += NT) {
+    const int u = list_pos(S, b, a.m, qs, e_begin + e, wc);
+    const int ci = u - S.wp - S.n_chunk;
+    rows[e] = (F8 && u >= 0 && ci >= 0 && ci < S.n_comp) ? (((uint64_t)ci << 1) | 1ull)
+                                                          : reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, u, D));
+  }
 
   const int h = hg * (HT * 16) + ht * 16 + l16;
   const bool hok = h < a.heads;
@@ -246,6 +259,8 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
 
   const int nsteps = (cnt + R - 1) / R;
   const uint32_t ring_base = lds_offset(ring);
+  const uint64_t comp8 = F8 ? reinterpret_cast<uint64_t>(S.comp) + (uint64_t)b * (uint64_t)S.comp_bstride : 0ull;
+  const uint64_t scal8 = F8 ? reinterpret_cast<uint64_t>(S.comp_scale) + (uint64_t)b * (uint64_t)S.comp_scale_bstride : 0ull;
   auto issue = [&](int t) {
     const int slot = t % NS;
     const int mine = t * R + wave * RPW + (lane % RPW);
@@ -254,12 +269,40 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
     const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
     const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_base + (uint32_t)(slot * SLOT + wave * RPW * RS));
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) dma_row<D>(lane_u64(lo, hi, rr), dst + rr * RS, lane);
+    for (int rr = 0; rr < RPW; ++rr) {
+      const uint64_t ent = lane_u64(lo, hi, rr);
+      if (F8 && (ent & 1ull)) {
+        // lanes 0..31: the row's 512 fp8 bytes; lane 32: its 16 scale bytes
+        const uint64_t ci = ent >> 1;
+        const uint64_t src = lane < D / 16 ? comp8 + ci * D + (uint64_t)lane * 16u
+                                           : scal8 + (ci / (uint64_t)S.comp_scale_rb) * (D / 32);
+        if (lane <= D / 16) dma16_vaddr(src, dst + rr * RS + D);
+      } else {
+        dma_row<D>(ent, dst + rr * RS, lane);
+      }
+    }
   };
   for (int t = 0; t < nsteps && t < NS - 1; ++t) issue(t);
 
   for (int t = 0; t < nsteps; ++t) {
     wait_steps<NL>(min(nsteps - 1 - t, NS - 2));
+    if constexpr (F8) {
+      // this wave's own fp8 rows of step t have landed: dequantize them in place. One read of
+      // the whole row precedes the writes (a single wave converts a row), so the bf16 output
+      // may overlap the fp8 bytes it came from.
+      uint8_t* sb = ring + (t % NS) * SLOT;
+#pragma unroll
+      for (int rr = 0; rr < RPW; ++rr) {
+        const int ei = t * R + wave * RPW + rr;
+        const uint64_t ent = ei < cnt ? rows[ei] : 0ull;
+        if (ent & 1ull) {
+          uint8_t* row = sb + (wave * RPW + rr) * RS;
+          const uint2 c8 = *reinterpret_cast<const uint2*>(row + D + lane * 8);
+          const float sc = e8m0_to_float(row[2 * D + (lane >> 2)]);
+          *reinterpret_cast<bf16x8*>(row + lane * 16) = dequant_e4m3x8(c8.x, c8.y, sc);
+        }
+      }
+    }
     __syncthreads();                       // step t landed; every wave is done with step t-1
     const int slot = t % NS;
     const uint8_t* buf = ring + slot * SLOT;
@@ -546,17 +589,19 @@ static size_t workspace_for(const MlaPlan& p, int64_t units, int heads, int dim)
 
 static bool bf16_dim_supported(int d) { return d == 64 || d == 128 || d == 256 || d == 512 || d == 576; }
 
-template <int D>
+template <int D, bool F8>
 static void launch_bf16_d(const MlaArgs& a, const MlaPlan& p, int64_t units, hipStream_t stream) {
   const unsigned wgs = (unsigned)(units * p.hgroups * p.splits);
   if (p.wide)
-    hipLaunchKernelGGL((mla_bf16_kernel<D, 4, 2>), dim3(wgs), dim3(512), 0, stream, a);
+    hipLaunchKernelGGL((mla_bf16_kernel<D, 4, 2, F8>), dim3(wgs), dim3(512), 0, stream, a);
   else
-    hipLaunchKernelGGL((mla_bf16_kernel<D, 2, 2>), dim3(wgs), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((mla_bf16_kernel<D, 2, 2, F8>), dim3(wgs), dim3(256), 0, stream, a);
 }
 
+// fp8_comp: the compressed source is an e4m3 cache with ue8m0 block scales (q, o and the other
+// sources are bf16; head_dim 512).
 static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int dtype, void* workspace,
-                   size_t workspace_bytes, hipStream_t stream) {
+                   size_t workspace_bytes, hipStream_t stream, bool fp8_comp = false) {
   if (units == 0) return 0;
   DSV41_REQUIRE(units < (1ll << 31), DSV41_E_ARG, "%s: too many queries", what);
   if (dtype == DSV41_F32) {
@@ -588,12 +633,17 @@ static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int
     a.part_o = reinterpret_cast<float*>(workspace);
     a.part_ml = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + align256(slots * a.dim * sizeof(float)));
   }
-  switch (a.dim) {
-    case 64: launch_bf16_d<64>(a, p, units, stream); break;
-    case 128: launch_bf16_d<128>(a, p, units, stream); break;
-    case 256: launch_bf16_d<256>(a, p, units, stream); break;
-    case 512: launch_bf16_d<512>(a, p, units, stream); break;
-    default: launch_bf16_d<576>(a, p, units, stream); break;
+  if (fp8_comp) {
+    DSV41_REQUIRE(a.dim == 512, DSV41_E_SHAPE, "%s: the fp8 cache path supports dim 512, got %d", what, a.dim);
+    launch_bf16_d<512, true>(a, p, units, stream);
+  } else {
+    switch (a.dim) {
+      case 64: launch_bf16_d<64, false>(a, p, units, stream); break;
+      case 128: launch_bf16_d<128, false>(a, p, units, stream); break;
+      case 256: launch_bf16_d<256, false>(a, p, units, stream); break;
+      case 512: launch_bf16_d<512, false>(a, p, units, stream); break;
+      default: launch_bf16_d<576, false>(a, p, units, stream); break;
+    }
   }
   int rc = check_launch(what);
   if (rc || p.splits == 1) return rc;
@@ -660,4 +710,43 @@ extern "C" int dsv41_sparse_mla(const void* q, const void* win_kv, const void* c
   a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.start_pos = start_pos;
   const int weff = window < wp + n ? window : wp + n;
   return run_mla(what, a, (int64_t)bsz * n, weff + k, dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dsv41_sparse_mla_fp8(const void* q, const void* win_kv, const void* chunk_kv, const uint8_t* comp_kv,
+                                    int64_t comp_bstride, int32_t n_comp, const uint8_t* comp_scale,
+                                    int64_t comp_scale_bstride, int32_t comp_scale_rb, const float* sink,
+                                    const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads,
+                                    int32_t dim, int32_t window, int32_t start_pos, float scale,
+                                    const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream) {
+  const char* what = "dsv41_sparse_mla_fp8";
+  const int wp = start_pos < window ? start_pos : window;
+  DSV41_REQUIRE(q && chunk_kv && sink && o && (idx || k == 0) && (win_kv || wp == 0) &&
+                    ((comp_kv && comp_scale) || n_comp == 0),
+                DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(bsz >= 0 && n >= 0 && heads > 0 && window > 0 && start_pos >= 0 && k >= 0 && n_comp >= 0,
+                DSV41_E_ARG, "%s: bad sizes", what);
+  DSV41_REQUIRE(dim == 512, DSV41_E_SHAPE, "%s: the fp8 cache path supports dim 512, got %d", what, dim);
+  DSV41_REQUIRE(comp_scale_rb == 1 || comp_scale_rb == 32, DSV41_E_ARG, "%s: scale row block must be 1 or 32", what);
+  DSV41_REQUIRE(n_comp == 0 || comp_bstride >= (int64_t)n_comp * dim, DSV41_E_ARG, "%s: comp_bstride too small", what);
+  DSV41_REQUIRE(n_comp == 0 || comp_scale_bstride >= (int64_t)((n_comp + comp_scale_rb - 1) / comp_scale_rb) * (dim / 32),
+                DSV41_E_ARG, "%s: comp_scale_bstride too small", what);
+  DSV41_REQUIRE(aligned16(q) && aligned16(chunk_kv) && aligned16(o) && (!win_kv || aligned16(win_kv)) &&
+                    (!comp_kv || (aligned16(comp_kv) && aligned16(comp_scale))),
+                DSV41_E_ARG, "%s: tensors must be 16-byte aligned", what);
+  DSV41_REQUIRE(comp_bstride % 16 == 0 && comp_scale_bstride % 16 == 0, DSV41_E_ARG,
+                "%s: comp_bstride and comp_scale_bstride must be multiples of 16 bytes", what);
+  DSV41_REQUIRE(rd == 0 || (cos_tab && sin_tab && rd % 2 == 0 && rd <= dim), DSV41_E_ARG, "%s: bad rope tail", what);
+  MlaArgs a{};
+  a.q = q; a.o = o; a.sink = sink;
+  a.src.ring = win_kv; a.src.ring_bstride = (int64_t)window * dim; a.src.window = window; a.src.wp = wp;
+  a.src.ring_first = (start_pos - wp) % window;
+  a.src.chunk = chunk_kv; a.src.chunk_bstride = (int64_t)n * dim; a.src.n_chunk = n;
+  a.src.comp = comp_kv; a.src.comp_bstride = comp_bstride; a.src.n_comp = n_comp;
+  a.src.comp_scale = comp_scale; a.src.comp_scale_bstride = comp_scale_bstride; a.src.comp_scale_rb = comp_scale_rb;
+  a.src.idx = idx; a.src.k = k; a.src.win_implicit = 1;
+  a.m = n; a.heads = heads; a.dim = dim; a.scale = scale;
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.start_pos = start_pos;
+  const int weff = window < wp + n ? window : wp + n;
+  return run_mla(what, a, (int64_t)bsz * n, weff + k, DSV41_BF16, workspace, workspace_bytes, stream, true);
 }

@@ -51,6 +51,8 @@ _SIGNATURES = {
     "dsv41_index_q_prep": [_c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_indexer_score": [_c_p, _c_p, _f32, _c_p, _i64, _c_p, _c_p, _i32, _i32, _i32, _i32,
                             _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_indexer_score_fp8": [_c_p, _c_p, _f32, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32,
+                                _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_topk_select": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_candidate_blocks": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _i32, _i32, _c_p],
     "dsv41_sparse_mla_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32],
@@ -58,6 +60,9 @@ _SIGNATURES = {
                           _i32, _c_p, _sz, _c_p],
     "dsv41_sparse_mla": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
                          _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla_fp8": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _i64, _i32, _c_p, _c_p, _i32,
+                             _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p,
+                             _sz, _c_p],
     "dsv41_version": [],
     "dsv41_last_error_string": [],
 }
@@ -346,6 +351,33 @@ def indexer_score(q, w_raw, w_scale, index_k, start_pos, ratio, candidates=None,
     return out
 
 
+def indexer_score_fp8(q, w_raw, w_scale, index_k8, k_scale, scale_rb, nb, start_pos, ratio, candidates=None,
+                      out=None):
+    """indexer_score with fp8 keys: index_k8 uint8 [b, >=nb, 128] e4m3fn codes, k_scale uint8
+    [b, >=ceil(nb / scale_rb), 4] ue8m0 exponents (one per 32 channels, every scale_rb = 1 or 32
+    rows). q [b,n,h,128] and w_raw [b,n,h] bf16."""
+    name = "dsv41_indexer_score_fp8"
+    _gpu(name, q, w_raw, index_k8, k_scale, candidates, out)
+    _contig(name, q, w_raw, candidates)
+    b, n, h, d = q.shape
+    if q.dtype != torch.bfloat16 or d != 128:
+        raise ValueError(f"{name}: q must be bf16 with 128 channels")
+    if w_raw.shape != (b, n, h) or w_raw.dtype != q.dtype:
+        raise ValueError(f"{name}: w_raw must be {q.dtype} [{b}, {n}, {h}]")
+    if index_k8.dtype != torch.uint8 or index_k8.shape[0] < b or index_k8.shape[2] != d or index_k8.shape[1] < nb:
+        raise ValueError(f"{name}: fp8 keys {tuple(index_k8.shape)} {index_k8.dtype} do not match")
+    if (k_scale.dtype != torch.uint8 or k_scale.shape[0] < b or k_scale.shape[2] != d // 32
+            or k_scale.shape[1] < -(-nb // scale_rb)):
+        raise ValueError(f"{name}: key scales {tuple(k_scale.shape)} do not match")
+    if candidates is not None and (candidates.shape != (b, n, nb) or candidates.dtype not in (torch.uint8, torch.bool)):
+        raise ValueError(f"{name}: candidates must be bool/uint8 [{b}, {n}, {nb}]")
+    out = torch.empty(b, n, nb, dtype=torch.float32, device=q.device) if out is None else out
+    cand = candidates.view(torch.uint8) if candidates is not None else None
+    _call(name, _ptr(q), _ptr(w_raw), float(w_scale), _ptr(index_k8), row_stride(index_k8, name), _ptr(k_scale),
+          row_stride(k_scale, name), scale_rb, _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, _stream(q))
+    return out
+
+
 def topk_select(scores, topk, start_pos, ratio, offset):
     """scores [b, n, nb] fp32 -> int32 [b, n, min(topk, nb)]."""
     name = "dsv41_topk_select"
@@ -457,5 +489,61 @@ def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_sca
     _call(name, _ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp_kv), comp_bstride, n_comp,
           _ptr(attn_sink), _ptr(idx), k, _ptr(o), b, n, h, d, window, start_pos, float(softmax_scale),
           _ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, dtype_code(q, name),
+          _ptr(workspace) if ws_bytes else None, ws_bytes, _stream(q))
+    return o
+
+
+def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, attn_sink, idx, softmax_scale,
+                   window, start_pos, cos=None, sin=None, rd=0, out=None, workspace=None):
+    """sparse_mla with an fp8 compressed cache: comp8 uint8 [b, >=n_comp, 512] e4m3fn codes,
+    comp_scale uint8 [b, >=ceil(n_comp / scale_rb), 16] ue8m0 exponents (one per 32 channels
+    for every scale_rb = 1 or 32 rows). q, the window ring, chunk and output are bf16."""
+    name = "dsv41_sparse_mla_fp8"
+    _gpu(name, q, win_kv, chunk_kv, comp8, comp_scale, attn_sink, idx, cos, sin, out)
+    _contig(name, q, chunk_kv, attn_sink, idx)
+    b, n, h, d = q.shape
+    if q.dtype != torch.bfloat16 or d != 512:
+        raise ValueError(f"{name}: q must be bf16 with 512 channels")
+    wp = min(start_pos, window)
+    if chunk_kv.shape != (b, n, d) or chunk_kv.dtype != q.dtype:
+        raise ValueError(f"{name}: chunk kv must be {q.dtype} [{b}, {n}, {d}]")
+    ring = None
+    if win_kv is not None:
+        if win_kv.shape[0] < b or win_kv.shape[1:] != (window, d) or win_kv.dtype != q.dtype:
+            raise ValueError(f"{name}: window ring {tuple(win_kv.shape)} does not match")
+        ring = win_kv[:b]
+        _contig(name, ring)
+    elif wp:
+        raise ValueError(f"{name}: a window ring is needed once start_pos > 0")
+    comp_bstride = sc_bstride = 0
+    if comp8 is not None and n_comp:
+        if comp8.dtype != torch.uint8 or comp8.shape[2] != d or comp8.shape[1] < n_comp or comp8.shape[0] < b:
+            raise ValueError(f"{name}: fp8 cache {tuple(comp8.shape)} {comp8.dtype} does not match")
+        nblk = -(-n_comp // scale_rb)
+        if (comp_scale is None or comp_scale.dtype != torch.uint8 or comp_scale.shape[2] != d // 32
+                or comp_scale.shape[1] < nblk or comp_scale.shape[0] < b):
+            raise ValueError(f"{name}: scale tensor does not match the cache")
+        comp_bstride = row_stride(comp8, name)
+        sc_bstride = row_stride(comp_scale, name)
+    else:
+        comp8, comp_scale, n_comp = None, None, 0
+    k = 0
+    if idx is not None:
+        if idx.dtype != torch.int32 or idx.shape[:2] != (b, n):
+            raise ValueError(f"{name}: idx must be int32 [{b}, {n}, k]")
+        k = idx.shape[2]
+    if rd:
+        if cos is None or sin is None or cos.shape[-1] * 2 != rd:
+            raise ValueError(f"{name}: rope tables do not match rd={rd}")
+        if n and start_pos + n - 1 >= cos.shape[0]:
+            raise ValueError(f"{name}: rope table too short")
+    o = torch.empty_like(q) if out is None else out
+    rows = min(window, wp + n) + k
+    ws_bytes = mla_workspace_bytes(b, n, h, d, rows, q.dtype)
+    if ws_bytes and (workspace is None or workspace.numel() < ws_bytes):
+        workspace = _workspace(ws_bytes, q.device)
+    _call(name, _ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp8), comp_bstride, n_comp, _ptr(comp_scale),
+          sc_bstride, scale_rb, _ptr(attn_sink), _ptr(idx), k, _ptr(o), b, n, h, d, window, start_pos,
+          float(softmax_scale), _ptr(cos) if rd else None, _ptr(sin) if rd else None, rd,
           _ptr(workspace) if ws_bytes else None, ws_bytes, _stream(q))
     return o

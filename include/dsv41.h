@@ -164,6 +164,18 @@ int dsv41_indexer_score(const void* q, const void* w_raw, float w_scale, const v
 /* ---------------------------------------------------------------- top-k --
  */
 
+/* dsv41_indexer_score with fp8 index keys: the packed, lossless form of the fp4/ue8m0-QAT keys
+ * publish_keys stores (indexer.py:89-104) or of the fp8 cache variant. index_k holds e4m3fn
+ * bytes [bsz, >=nb, 128] (k_bstride bytes per batch row); k_scale holds one ue8m0 byte per 32
+ * channels for every ks_rb rows (1 or 32): [bsz, ceil(nb / ks_rb), 4], ks_bstride bytes per
+ * batch row. Keys are dequantized to bf16 in-kernel (exact), so scores equal
+ * dsv41_indexer_score's on the dequantized keys. q and w_raw are bf16; dim is 128. */
+int dsv41_indexer_score_fp8(const void* q, const void* w_raw, float w_scale, const uint8_t* index_k,
+                            int64_t k_bstride, const uint8_t* k_scale, int64_t ks_bstride,
+                            int32_t ks_rb, const uint8_t* candidates, float* scores, int32_t bsz,
+                            int32_t n, int32_t heads, int32_t dim, int32_t nb, int32_t start_pos,
+                            int32_t ratio, hipStream_t stream);
+
 /* Top-k selection, deepseek_v41_mlx/indexer.py:200-204: per row of scores [bsz*n, nb],
  * the k = min(topk, nb) best positions (ties -> lowest position; -0.0 == +0.0), sorted
  * ascending, written as idx + offset when idx < lens else -1, lens = (start_pos+s+1)/ratio,
@@ -219,6 +231,23 @@ int dsv41_sparse_mla(const void* q, const void* win_kv, const void* chunk_kv,
                      int32_t n, int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
                      float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
                      int32_t dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* dsv41_sparse_mla with the compressed source stored as fp8: the packed, lossless form of the
+ * QAT values that attention.py:157-163 writes into the cache (e4m3 code times a power-of-two
+ * block scale, the ue8m0 convention of fakequant.py:83-93). comp_kv holds e4m3fn bytes
+ * [bsz, >=n_comp, 512] (comp_bstride bytes per batch row); comp_scale holds one ue8m0 byte
+ * (scale 2^(e-127)) per 32 channels for every comp_scale_rb rows (1 or 32):
+ * [bsz, ceil(n_comp / rb), 16] with comp_scale_bstride bytes per batch row. Rows are
+ * dequantized to bf16 in-kernel, exactly (e4m3 x 2^k is bf16-representable), so the result
+ * equals dsv41_sparse_mla's on the dequantized cache. q, win_kv, chunk_kv and o are bf16;
+ * dim is 512; the workspace is sized by dsv41_sparse_mla_workspace_bytes(..., DSV41_BF16). */
+int dsv41_sparse_mla_fp8(const void* q, const void* win_kv, const void* chunk_kv,
+                         const uint8_t* comp_kv, int64_t comp_bstride, int32_t n_comp,
+                         const uint8_t* comp_scale, int64_t comp_scale_bstride, int32_t comp_scale_rb,
+                         const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
+                         int32_t n, int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
+                         float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

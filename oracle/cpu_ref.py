@@ -15,6 +15,7 @@ reference repository root).
 
 Pinning status (what checks each function; see tests/test_oracle.py):
   * bf16/e4m3 rounding        -- torch's own casts over exhaustive grids (library routines)
+  * e4m3 decode / fp8 cache   -- torch's float8_e4m3fn over all 256 codes; per-element loop
   * fake-quants (a1-a3)       -- known-answer vectors (reference test inputs, rng 3 +
                                  midpoint vector) with answers from an independent
                                  brute-force nearest-grid search; closed-form scales
@@ -95,6 +96,27 @@ def e4m3_round(x) -> np.ndarray:
 DISABLE_FAKE_QUANT = False
 
 _E2M1_LUT = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], dtype=F32)
+
+
+def e4m3_decode(codes) -> np.ndarray:
+    """float32 values of e4m3fn codes (uint8): sign, 4-bit exponent (bias 7), 3-bit mantissa;
+    exponent 0 is subnormal (m * 2^-9); 0x7F / 0xFF are NaN. The byte form of the values
+    e4m3_round produces (the fp8 QAT of fakequant.py:83-93 stores exactly these)."""
+    c = np.asarray(codes, np.uint8).astype(np.int32)
+    s, e, m = (c >> 7) & 1, (c >> 3) & 15, c & 7
+    v = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    v = np.where((e == 15) & (m == 7), np.nan, v)
+    return np.where(s == 1, -v, v).astype(F32)
+
+
+def dequant_fp8_cache(codes, scales, rb: int) -> np.ndarray:
+    """An fp8 cache [b, rows, D] of e4m3 codes with ue8m0 block scales [b, ceil(rows/rb), D/32]
+    (scale 2^(e-127) for every rb rows x 32 channels) -> float32 values."""
+    v = e4m3_decode(codes)
+    b, rows, d = v.shape
+    sc = np.ldexp(np.ones(np.shape(scales), F32), np.asarray(scales, np.int32) - 127).astype(F32)
+    sc_rows = np.repeat(sc, rb, axis=1)[:, :rows]
+    return (v * np.repeat(sc_rows, 32, axis=2)).astype(F32)
 
 
 def pow2_ceil_log2(r) -> np.ndarray:

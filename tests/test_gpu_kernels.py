@@ -230,6 +230,34 @@ def test_indexer_score(gpu, dt, hi, di, b, n, nb, start, use_cand):
     assert np.abs(g[fin] - want[fin]).max() <= 1e-5 * max(np.abs(want[fin]).max(), 1.0)
 
 
+@pytest.mark.parametrize("b,n,h,nb,start,rb", [(16, 1, 64, 32768, 131071, 32), (3, 5, 32, 1000, 3990, 1),
+                                               (2, 40, 16, 700, 2700, 32)])
+def test_indexer_score_fp8_keys(gpu, b, n, h, nb, start, rb):
+    """fp8 index keys dequantized in-kernel: bit-identical to the bf16 path on the dequantized
+    keys, and within the bf16 path's tolerance of the oracle."""
+    from dsv41 import _abi
+    from dsv41.indexer import weight_scale
+    rng = rng_for(f"idx8{b}{n}{nb}")
+    d, r = 128, 4
+    q = R.cast(rng.standard_normal((b, n, h, d)).astype(F32) * 0.3, "bf16")
+    w_raw = R.cast(rng.standard_normal((b, n, h)).astype(F32), "bf16")
+    codes = rng.integers(0, 256, size=(b, nb + 3, d), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] ^= 0x01
+    scales = rng.integers(123, 132, size=(b, -(-(nb + 3) // rb), d // 32), dtype=np.uint8)
+    keys = R.dequant_fp8_cache(codes, scales, rb)
+    scale = weight_scale(h, d, torch.bfloat16)
+    got8 = _abi.indexer_score_fp8(dev(q, "bf16"), dev(w_raw, "bf16"), scale, torch.as_tensor(codes).to(gpu),
+                                  torch.as_tensor(scales).to(gpu), rb, nb, start, r)
+    got16 = _abi.indexer_score(dev(q, "bf16"), dev(w_raw, "bf16"), scale, dev(keys[:, :nb], "bf16"), start, r)
+    assert torch.equal(got8, got16)
+    w = R.cast(w_raw * scale, "bf16")
+    want = R.indexer_scores(q, keys[:, :nb], w, start, r)
+    g = to_np(got8)
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isfinite(g), fin)
+    assert np.abs(g[fin] - want[fin]).max() <= 1e-5 * max(np.abs(want[fin]).max(), 1.0)
+
+
 # ------------------------------------------------------------------ top-k and candidates
 
 
@@ -384,6 +412,53 @@ def test_sparse_mla_split_lists_reuse_workspace(gpu):
         o = R.sparse_attn(q, kv_all, sink, np.concatenate([widx, cidx], axis=-1), d ** -0.5, dtype="bf16")
         want = R.rope_tail(o, rd, rc[[start]], rs[[start]], inverse=True, dtype="bf16")
         assert rel_max_diff(to_np(got), want) < 2e-2, f"call {call}"
+
+
+def _fp8_cache(rng, b, rows, d, rb):
+    """e4m3 codes (the two NaN codes avoided) and ue8m0 block scales 2^-4 .. 2^4."""
+    codes = rng.integers(0, 256, size=(b, rows, d), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] ^= 0x01
+    scales = rng.integers(123, 132, size=(b, -(-rows // rb), d // 32), dtype=np.uint8)
+    return codes, scales
+
+
+@pytest.mark.parametrize("b,n,window,start,n_comp,k,rb", [
+    (8, 1, 128, 40000, 9000, 1000, 32),     # decode, split index lists, 32x32-block scales
+    (16, 1, 128, 131071, 4000, 1024, 32),   # the fp8-cache decode shape (batch 16, top-1024), smaller cache
+    (1, 600, 16, 200, 150, 64, 1),          # >= 512 queries: the 64-head plan; per-row scales
+])
+def test_sparse_mla_fp8_cache_equals_bf16_on_dequantized_cache(gpu, b, n, window, start, n_comp, k, rb):
+    """fp8 compressed cache dequantized in-kernel: bit-identical to the bf16 path on the
+    dequantized cache (e4m3 x 2^k is exact in bf16) and within the bf16 tolerance of the oracle."""
+    from dsv41 import _abi
+    rng = rng_for(f"mla8{b}{n}{start}")
+    h, d, rd = 64, 512, 64
+    rc, rs = R.precompute_freqs_cis(rd, start + n + 1, 65536, 160000.0, 16.0, 32, 1)
+    q = R.cast(rng.standard_normal((b, n, h, d)).astype(F32) * 2, "bf16")
+    win = R.cast(rng.standard_normal((b, window, d)).astype(F32), "bf16")
+    chunk = R.cast(rng.standard_normal((b, n, d)).astype(F32), "bf16")
+    codes, scales = _fp8_cache(rng, b, n_comp + 5, d, rb)
+    comp = R.dequant_fp8_cache(codes, scales, rb)
+    assert np.array_equal(R.cast(comp, "bf16"), comp)
+    sink = rng.standard_normal(h).astype(F32)
+    wp = min(start, window)
+    lens = R.query_lens(start, n, 4)
+    cidx = np.sort(rng.integers(0, n_comp, size=(b, n, k)), axis=-1)
+    cidx = np.where(cidx < np.minimum(lens, n_comp)[None, :, None], cidx + wp + n, -1).astype(np.int32)
+    cidx[:, :, ::5] = -1
+    idx_t = torch.as_tensor(cidx).to(gpu)
+    args = (d ** -0.5, window, start, dev(rc), dev(rs), rd)
+    got8 = _abi.sparse_mla_fp8(dev(q, "bf16"), dev(win, "bf16"), dev(chunk, "bf16"), torch.as_tensor(codes).to(gpu),
+                               torch.as_tensor(scales).to(gpu), rb, n_comp, dev(sink), idx_t, *args)
+    got16 = _abi.sparse_mla(dev(q, "bf16"), dev(win, "bf16"), dev(chunk, "bf16"), dev(comp, "bf16"), n_comp,
+                            dev(sink), idx_t, *args)
+    assert torch.equal(got8, got16)
+    kv_all = _concat_reference(win, chunk, comp, n_comp, start, window)
+    widx = np.broadcast_to(R.window_idx_matrix(wp, n, window)[None], (b, n, min(window, wp + n)))
+    o = R.sparse_attn(q, kv_all, sink, np.concatenate([widx, cidx], axis=-1), d ** -0.5, dtype="bf16")
+    pos = start + np.arange(n)
+    want = R.rope_tail(o, rd, rc[pos], rs[pos], inverse=True, dtype="bf16")
+    assert rel_max_diff(to_np(got8), want) < 2e-2
 
 
 def test_reference_kernel_module_seam(gpu):

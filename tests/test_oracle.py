@@ -58,6 +58,31 @@ def test_e4m3_rounding_matches_torch_float8_cast():
     assert np.array_equal(ours, ref)
 
 
+def test_e4m3_decode_matches_torch_on_every_code():
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).float().numpy()
+    got = R.e4m3_decode(codes)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan) and nan.sum() == 2
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))   # bitwise, -0 included
+
+
+def test_fp8_cache_dequant_per_element():
+    rng = np.random.default_rng(11)
+    b, rows, d = 2, 70, 64
+    codes = rng.integers(0, 256, size=(b, rows, d), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x3C                       # no NaN codes
+    for rb in (1, 32):
+        scales = rng.integers(123, 132, size=(b, -(-rows // rb), d // 32), dtype=np.uint8)
+        got = R.dequant_fp8_cache(codes, scales, rb)
+        for i in range(b):
+            for r in range(rows):
+                for c in range(0, d, 7):
+                    v = float(torch.tensor(int(codes[i, r, c]), dtype=torch.uint8).view(torch.float8_e4m3fn).float())
+                    want = v * 2.0 ** (int(scales[i, r // rb, c // 32]) - 127)
+                    assert got[i, r, c] == np.float32(want)
+
+
 def test_pow2_ceil_log2_closed_form():
     rng = np.random.default_rng(2)
     x = np.exp(rng.uniform(-80, 80, 100000)).astype(F32)
