@@ -11,9 +11,11 @@ cannot serve the streamed caches. Steps are replayed from HIP graphs (one graph 
 step per input set), bracketed by events on the launch stream.
 
 Secondary: C3 prefill (8,192-token chunk after 32,768 tokens, top-2,048) indexer and sparse
-MLA TFLOP/s, and the CPU oracle (numpy) timed on a bounded sample of the decode workload.
+MLA TFLOP/s; the fp8-cache decode step (batch 16, 131,072 tokens, top-1,024, e4m3 caches with
+ue8m0 block scales dequantized in-kernel); and the CPU oracle (numpy) timed on a bounded sample
+of the decode workload.
 
-    python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-fp8] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -44,6 +46,7 @@ def parse():
     p.add_argument("--sets", type=int, default=4)
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-fp8", action="store_true", help="skip the fp8-cache decode line")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--eager", action="store_true",
                    help="launch the decode kernels without HIP graphs (for counter-collecting profilers)")
@@ -296,6 +299,96 @@ def run_prefill(torch, device):
     }
 
 
+def run_fp8_decode(args, torch, device):
+    """fp8-cache decode (batch 16, 131,072-token context -> 32,768 compressed entries, top-1,024):
+    compressed KV and index keys stored as e4m3 with ue8m0 scales per 32 x 32 block (2^-4..2^4),
+    dequantized in-kernel; the 128-row window ring and this token's KV stay bf16. Same step as
+    the bf16 decode line (indexer -> top-k -> sparse MLA), 4 rotating input sets."""
+    from dsv41 import _abi
+    from dsv41.indexer import weight_scale
+    from dsv41.layers import precompute_freqs_cis
+
+    B, ctx, H, D, rd, Hi, Di, W, K, r = 16, 131072, 64, 512, 64, 64, 128, 128, 1024, 4
+    start, nb = ctx, (ctx + 1) // 4
+    wp, rb = min(ctx, W), 32
+    rows = min(W, wp + 1) + K
+    log(f"[bench] fp8-cache decode B={B} ctx={ctx} nb={nb} K={K}")
+    bf = torch.bfloat16
+
+    def codes(g, *shape):
+        c = torch.randint(0, 256, shape, generator=g, device=device, dtype=torch.int32)
+        c = torch.where((c & 0x7F) == 0x7F, c ^ 1, c)          # no NaN codes
+        return c.to(torch.uint8)
+
+    def scales(g, *shape):
+        return torch.randint(123, 132, shape, generator=g, device=device, dtype=torch.int32).to(torch.uint8)
+
+    sets = []
+    for i in range(args.sets):
+        g = torch.Generator(device=device).manual_seed(SEED + 200 + i)
+        sc = 576 ** -0.5
+        sets.append(dict(
+            q=(torch.randn(B, 1, H, D, generator=g, device=device) * sc).to(bf),
+            win=(torch.randn(B, W, D, generator=g, device=device) * sc).to(bf),
+            chunk=(torch.randn(B, 1, D, generator=g, device=device) * sc).to(bf),
+            comp8=codes(g, B, nb, D), comp_sc=scales(g, B, nb // rb, D // 32),
+            iq=(torch.randn(B, 1, Hi, Di, generator=g, device=device) * 0.3).to(bf),
+            ik8=codes(g, B, nb, Di), ik_sc=scales(g, B, nb // rb, Di // 32),
+            w=torch.randn(B, 1, Hi, generator=g, device=device).to(bf),
+            sink=torch.randn(H, generator=g, device=device),
+            scores=torch.empty(B, 1, nb, dtype=torch.float32, device=device),
+            out=torch.empty(B, 1, H, D, dtype=bf, device=device),
+            ws=torch.empty(max(_abi.mla_workspace_bytes(B, 1, H, D, rows, bf), 1), dtype=torch.uint8,
+                           device=device)))
+    cos, sin = precompute_freqs_cis(rd, start + 1, 65536, 160000.0, 16.0, 32, 1, device=device)
+    wsc = weight_scale(Hi, Di, bf)
+
+    def f_idx(d):
+        _abi.indexer_score_fp8(d["iq"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, out=d["scores"])
+
+    def f_topk(d):
+        d["idx"] = _abi.topk_select(d["scores"], K, start, r, wp + 1)
+
+    def f_sparse(d):
+        _abi.sparse_mla_fp8(d["q"], d["win"], d["chunk"], d["comp8"], d["comp_sc"], rb, nb, d["sink"], d["idx"],
+                            D ** -0.5, W, start, cos, sin, rd, out=d["out"], workspace=d["ws"])
+
+    def full(d):
+        f_idx(d)
+        f_topk(d)
+        f_sparse(d)
+
+    per = len(sets)
+    reps = max(1, args.steps // per)
+    g_full = graph_of(full, sets, torch)
+    for _ in range(max(1, args.warmup // per)):
+        g_full.replay()
+    step_ms = time_graph(g_full, reps, torch) / per
+    kern, graphs = {}, [g_full]
+    for name, fn in (("indexer_score", f_idx), ("topk_select", f_topk), ("sparse_mla", f_sparse)):
+        gr = graph_of(fn, sets, torch)
+        graphs.append(gr)
+        gr.replay()
+        kern[name] = time_graph(gr, reps, torch) / per
+        log(f"[bench] fp8 {name} {kern[name] * 1e3:.2f} us")
+    torch.cuda.synchronize()
+    b_idx = B * (nb * Di + (nb // rb) * (Di // 32) + Hi * Di * 2 + Hi * 2 + nb * 4)
+    b_topk = B * (nb * 4 + K * 4)
+    b_sparse = B * (K * (D + D // 32) + (rows - K) * D * 2 + 2 * H * D * 2 + K * 4)
+    step_bytes = b_idx + b_topk + b_sparse
+    log(f"[bench] fp8-cache decode step {step_ms * 1e3:.2f} us")
+    return {
+        "workload": "fp8-cache decode step: B=16, 131072-token context (nb=32768), top-1024; compressed KV and "
+                    "index keys e4m3 with ue8m0 32x32-block scales, dequantized in-kernel; window ring bf16",
+        "step_us": step_ms * 1e3, "tokens_per_s": B / (step_ms * 1e-3),
+        "kernels_us": {k: v * 1e3 for k, v in kern.items()},
+        "step_algorithmic_bytes": step_bytes,
+        "hbm_GBps_step": step_bytes / (step_ms * 1e-3) / 1e9,
+        "indexer_GBps": b_idx / (kern["indexer_score"] * 1e-3) / 1e9,
+        "sparse_GBps": b_sparse / (kern["sparse_mla"] * 1e-3) / 1e9,
+    }
+
+
 def cpu_baseline(s: Shape, sets, cos, sin, ws, seconds, torch):
     """The numpy oracle on whole batch rows of the same decode workload, until `seconds` pass."""
     import numpy as np
@@ -382,6 +475,11 @@ def main():
             result["prefill"] = run_prefill(torch, device)
         except Exception as e:  # report, do not hide: the decode line still prints
             result["prefill"] = {"error": repr(e)}
+    if not args.no_fp8:
+        try:
+            result["fp8_cache_decode"] = run_fp8_decode(args, torch, device)
+        except Exception as e:
+            result["fp8_cache_decode"] = {"error": repr(e)}
     if not args.no_cpu:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(s, sets, cos, sin, ws, args.cpu_seconds, torch)
