@@ -32,12 +32,15 @@ struct SelShared {
   uint32_t pick[2];
 };
 
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t t = __shfl_up(v, o, 64);
-    if (lane >= o) v += t;
-  }
+// Inclusive scan over the 64 lanes of a wave with DPP moves (no LDS round trips): shifts by 1,
+// 2, 4, 8 within each 16-lane row, then row 15 -> row 1 and 3, lane 31 -> rows 2 and 3.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);   // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);   // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);   // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);   // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);  // row_bcast:31
   return v;
 }
 
@@ -237,17 +240,18 @@ __global__ __launch_bounds__(kSelThreads) void topk_reg_kernel(const float* __re
   __syncthreads();
   const uint32_t excl = wave_base() + incl - packed;
   uint32_t gt_before = excl >> 16, eq_before = excl & 0xFFFFu;
+  // branch-free walk in position order: a key > T goes to gt_before + min(eq_before, need), a
+  // key == T to gt_before + eq_before while eq_before < need
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    if (j >= nvalid) break;
     const int i = i0 + j;
-    if (key[j] > T) {
-      o[gt_before + min(eq_before, need)] = i < lens ? i + offset : -1;
-      ++gt_before;
-    } else if (key[j] == T) {
-      if (eq_before < need) o[gt_before + eq_before] = i < lens ? i + offset : -1;
-      ++eq_before;
-    }
+    const bool ok = j < nvalid;
+    const bool gt = ok && key[j] > T, eq = ok && key[j] == T;
+    const bool take = gt || (eq && eq_before < need);
+    const uint32_t pos = gt_before + min(eq_before, need);
+    if (take) o[pos] = i < lens ? i + offset : -1;
+    gt_before += gt ? 1u : 0u;
+    eq_before += eq ? 1u : 0u;
   }
 }
 
