@@ -56,26 +56,8 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
   for (int t = vis_end + tid; t < r1; t += kIdxThreads) out[t] = -INFINITY;
   if (vis_end <= r0) return;               // uniform: nothing visible in this row range
 
-  // stage q[b, s] ([H, DIM] bf16) into LDS
-  const bf16_t* qrow = q + (int64_t)qi * H * DIM;
-  for (int c = tid; c < H * DIM / 8; c += kIdxThreads) {
-    const int h = c / (DIM / 8), d8 = c - h * (DIM / 8);
-    *reinterpret_cast<uint4*>(q_lds + h * QROW + d8 * 16) = reinterpret_cast<const uint4*>(qrow)[c];
-  }
-  __syncthreads();
-
-  bf16x8 qa[HT][KS];
-#pragma unroll
-  for (int ht = 0; ht < HT; ++ht)
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qa[ht][ks] = ld_bf16x8(q_lds + (ht * 16 + l16) * QROW + (ks * 32 + g * 8) * 2);
-  float wv[HT][4];
-  const bf16_t* wrow = w_raw + (int64_t)qi * H;
-#pragma unroll
-  for (int ht = 0; ht < HT; ++ht)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wrow[ht * 16 + 4 * g + i]) * w_scale);
+  bf16x8 qa[HT][KS];                       // the query block as the MFMA A operand (heads = M)
+  float wv[HT][4];                         // head weights of this lane's 4 heads per head tile
 
   // natural MFMA k order (k = 32 ks + 8 g + i): one load instruction reads a contiguous 64-byte
   // (fp8: 32-byte) span of each of its 16 rows
@@ -138,9 +120,41 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
     }
   };
   int t0 = r0 + 16 * U * wave;
-  if (t0 >= vis_end) return;
+  // Stage q[b, s] ([H, DIM] bf16) through LDS, with the first key batch already in flight: the
+  // query's global loads go out first, then every wave's first batch (unconditional and clamped,
+  // so the wait counts stay exact), then the LDS store and the barrier.
+  constexpr int QN = (H * DIM / 8 + kIdxThreads - 1) / kIdxThreads;
+  const uint4* qrow = reinterpret_cast<const uint4*>(q + (int64_t)qi * H * DIM);
+  uint4 qv[QN];
+#pragma unroll
+  for (int c = 0; c < QN; ++c) {
+    const int e = tid + c * kIdxThreads;
+    qv[c] = e < H * DIM / 8 ? qrow[e] : make_uint4(0u, 0u, 0u, 0u);
+  }
   Batch ka, kb2;
-  load(ka, t0);
+  load(ka, min(t0, vis_end - 1));
+#pragma unroll
+  for (int c = 0; c < QN; ++c) {
+    const int e = tid + c * kIdxThreads;
+    if (e < H * DIM / 8) {
+      const int h = e / (DIM / 8), d8 = e - h * (DIM / 8);
+      *reinterpret_cast<uint4*>(q_lds + h * QROW + d8 * 16) = qv[c];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qa[ht][ks] = ld_bf16x8(q_lds + (ht * 16 + l16) * QROW + (ks * 32 + g * 8) * 2);
+  {
+    const bf16_t* wrow = w_raw + (int64_t)qi * H;
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wrow[ht * 16 + 4 * g + i]) * w_scale);
+  }
+  if (t0 >= vis_end) return;
   for (;;) {
     load(kb2, t0 + STRIDE);
     compute(ka, t0);
