@@ -44,8 +44,8 @@ struct MlaArgs {
   const float* sin_tab;
   int rd, start_pos;
   int hgroups, splits, per_split;
-  float* part_o;
-  float* part_ml;
+  bf16_t* part_o;     // split partials: numerator / denominator, rounded to bf16 [slot][dim]
+  float* part_ml;     // split partials: (log2-domain max, denominator) [slot][2]
 };
 
 // Workgroups are dispatched to the 8 XCDs round-robin by linear id and each XCD has its own L2.
@@ -83,18 +83,31 @@ __device__ __forceinline__ int window_count(const KvSrc& s, int qs) {
   return s.win_implicit ? min(s.window, s.wp + qs + 1) : 0;
 }
 
-// inverse rope of one adjacent pair at channel d (even) of a head_dim-D row
-__device__ __forceinline__ void rope_inv_pair(const MlaArgs& a, int D, int qs, int d, float& x0, float& x1,
-                                              bool round) {
-  if (a.rd <= 0 || d < D - a.rd) return;
+// inverse rope: rotate the adjacent pair (x0, x1) by the conjugate of (cs, sn)
+__device__ __forceinline__ void rope_inv_apply(float cs, float sn_neg, float& x0, float& x1) {
+  const float xr = x0, xi = x1;
+  x0 = __fsub_rn(__fmul_rn(xr, cs), __fmul_rn(xi, sn_neg));
+  x1 = __fadd_rn(__fmul_rn(xr, sn_neg), __fmul_rn(xi, cs));
+}
+
+__device__ __forceinline__ bool in_rope_tail(const MlaArgs& a, int D, int d) { return a.rd > 0 && d >= D - a.rd; }
+
+// (cos, -sin) of the pair at channel d (even) of query qs, when d lies in the rope tail
+__device__ __forceinline__ void rope_inv_load(const MlaArgs& a, int D, int qs, int d, float& cs, float& sn_neg) {
   const int half = a.rd >> 1;
   const int p = (d - (D - a.rd)) >> 1;
   const int64_t pos = (int64_t)a.start_pos + qs;
-  const float cs = a.cos_tab[pos * half + p];
-  const float sn = -a.sin_tab[pos * half + p];
-  const float xr = x0, xi = x1;
-  x0 = __fsub_rn(__fmul_rn(xr, cs), __fmul_rn(xi, sn));
-  x1 = __fadd_rn(__fmul_rn(xr, sn), __fmul_rn(xi, cs));
+  cs = a.cos_tab[pos * half + p];
+  sn_neg = -a.sin_tab[pos * half + p];
+}
+
+// inverse rope of one adjacent pair at channel d (even) of a head_dim-D row
+__device__ __forceinline__ void rope_inv_pair(const MlaArgs& a, int D, int qs, int d, float& x0, float& x1,
+                                              bool round) {
+  if (!in_rope_tail(a, D, d)) return;
+  float cs, sn;
+  rope_inv_load(a, D, qs, d, cs, sn);
+  rope_inv_apply(cs, sn, x0, x1);
   if (round) {
     x0 = round_bf16(x0);
     x1 = round_bf16(x1);
@@ -377,11 +390,20 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   if (!hok) return;                        // no barrier follows
   const int64_t slot_id = ((int64_t)unit * a.splits + sp) * a.heads + h;
   bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + h) * D;
+  // a split's partial is stored normalized (numerator / its own denominator) in bf16; a split
+  // whose rows are all masked (denominator 0) stores zeros, which the combine weighs by 0
+  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
 #pragma unroll
   for (int dt = 0; dt < DTS; ++dt) {
     const int d0 = dh * DSL + dt * 16 + 4 * g;
-    if (a.splits == 1) store_out4(a, D, qs, orow, d0, acc[dt], l_run);
-    else *reinterpret_cast<f32x4*>(a.part_o + slot_id * D + d0) = acc[dt];
+    if (a.splits == 1) {
+      store_out4(a, D, qs, orow, d0, acc[dt], l_run);
+    } else {
+      uint2 st;
+      st.x = (uint32_t)f2bf(acc[dt][0] * inv) | ((uint32_t)f2bf(acc[dt][1] * inv) << 16);
+      st.y = (uint32_t)f2bf(acc[dt][2] * inv) | ((uint32_t)f2bf(acc[dt][3] * inv) << 16);
+      *reinterpret_cast<uint2*>(a.part_o + slot_id * D + d0) = st;
+    }
   }
   if (a.splits > 1 && dh == 0 && g == 0) {
     a.part_ml[slot_id * 2 + 0] = m_run;
@@ -389,11 +411,13 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   }
 }
 
-// Merges split partials (log2-domain max, denominator, numerator) of one query: one wave per
-// head, 4 heads per workgroup. Lane s reads split s's (max, denominator); the weights reach every
-// lane by readlane, and the numerator slices of all splits are loaded together (no load waits on
-// another). Splits are at most 64 (the planner's bound).
-template <typename T>
+// Merges split partials of one query: one wave per head, 4 heads per workgroup. Split s holds
+// (m_s, l_s, o_s) = (log2-domain max, denominator, numerator / l_s in bf16); the merged row is
+// sum_s w_s o_s / sum_s w_s with w_s = l_s 2^(m_s - M). Lane s reads split s's (m_s, l_s); the
+// weights reach every lane by readlane. NB numerator rows (splits clamped to the last one, whose
+// weight past ns is 0) are loaded together before any weight is formed; splits beyond NB are
+// streamed. Each lane covers 8 channels per 512. Splits are at most 64 (the planner's bound).
+template <typename T, int NB>
 __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
   const int unit = blockIdx.x;
   const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
@@ -401,34 +425,76 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
   if (h >= a.heads) return;
   const int D = a.dim, qs = unit % a.m, ns = a.splits;
   const int64_t slot0 = (int64_t)unit * ns * a.heads + h;     // split s: slot0 + s * heads
-  float mk = kNegFloor, dk = 0.0f;
-  if (lane < ns) {
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (slot0 + (int64_t)lane * a.heads) * 2);
-    mk = ml.x;
-    dk = ml.y;
-  }
-  float M = mk;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-  const float wk = lane < ns ? exp2f(mk - M) : 0.0f;
-  float den = dk * wk;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
   T* orow = reinterpret_cast<T*>(a.o) + ((int64_t)unit * a.heads + h) * D;
-  for (int d = 4 * lane; d < D; d += 256) {
-    f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < ns; ++s) {
-      const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), s));
-      x += *reinterpret_cast<const f32x4*>(a.part_o + (slot0 + (int64_t)s * a.heads) * D + d) * w;
+  auto part = [&](int s, int d) {
+    return *reinterpret_cast<const uint4*>(a.part_o + (slot0 + (int64_t)s * a.heads) * D + d);
+  };
+  for (int d = 8 * lane; d < D; d += 512) {
+    // the inverse-rope factors of this lane's pairs are fetched with the partials (unpredicated:
+    // a pair outside the tail reads the table's first pair of its row and ignores it)
+    float cs[4] = {0.f, 0.f, 0.f, 0.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.rd > 0) {
+      const int64_t row = ((int64_t)a.start_pos + qs) * (a.rd >> 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int p = max(d + 2 * j - (D - a.rd), 0) >> 1;
+        cs[j] = a.cos_tab[row + p];
+        sn[j] = a.sin_tab[row + p];
+      }
     }
-    float v[4];
+    uint4 pv[NB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = io<T>::rnd(x[i] / den);
-    rope_inv_pair(a, D, qs, d, v[0], v[1], false);
-    rope_inv_pair(a, D, qs, d + 2, v[2], v[3], false);
+    for (int s = 0; s < NB; ++s) pv[s] = part(s < ns ? s : ns - 1, d);
+    float mk = kNegFloor, lk = 0.0f;
+    if (lane < ns) {
+      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (slot0 + (int64_t)lane * a.heads) * 2);
+      mk = ml.x;
+      lk = ml.y;
+    }
+    float M = mk;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) io<T>::st(orow + d + i, v[i]);
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    const float wk = lane < ns ? lk * exp2f(mk - M) : 0.0f;
+    float den = wk;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+    float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    auto add = [&](int s, const uint4& v) {
+      const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), s));
+      const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[2 * i] += w * __uint_as_float(wd[i] << 16);
+        x[2 * i + 1] += w * __uint_as_float(wd[i] & 0xFFFF0000u);
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < NB; ++s) add(s, pv[s]);
+    for (int s = NB; s < ns; ++s) add(s, part(s, d));
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = io<T>::rnd(x[i] / den);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (in_rope_tail(a, D, d + 2 * j)) rope_inv_apply(cs[j], -sn[j], v[2 * j], v[2 * j + 1]);
+    if constexpr (sizeof(T) == 2) {
+      uint4 st;
+      st.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+      st.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+      st.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
+      st.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+      *reinterpret_cast<uint4*>(orow + d) = st;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) io<T>::st(orow + d + i, v[i]);
+    }
   }
+}
+
+template <int NB>
+static void launch_combine(const MlaArgs& a, int64_t units, hipStream_t stream) {
+  hipLaunchKernelGGL((mla_combine_kernel<bf16_t, NB>), dim3((unsigned)units, (unsigned)((a.heads + 3) / 4)), dim3(256),
+                     0, stream, a);
 }
 
 // fp32: 4 heads x 16 rows per step, plain FMA, natural-log softmax with the reference's form.
@@ -584,7 +650,7 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 static size_t workspace_for(const MlaPlan& p, int64_t units, int heads, int dim) {
   if (p.splits <= 1) return 0;
   const size_t slots = (size_t)units * p.splits * heads;
-  return align256(slots * dim * sizeof(float)) + align256(slots * 2 * sizeof(float));
+  return align256(slots * dim * sizeof(bf16_t)) + align256(slots * 2 * sizeof(float));
 }
 
 static bool bf16_dim_supported(int d) { return d == 64 || d == 128 || d == 256 || d == 512 || d == 576; }
@@ -630,8 +696,8 @@ static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int
                   what, need);
     DSV41_REQUIRE(aligned16(workspace), DSV41_E_ARG, "%s: workspace must be 16-byte aligned", what);
     const size_t slots = (size_t)units * p.splits * a.heads;
-    a.part_o = reinterpret_cast<float*>(workspace);
-    a.part_ml = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + align256(slots * a.dim * sizeof(float)));
+    a.part_o = reinterpret_cast<bf16_t*>(workspace);
+    a.part_ml = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + align256(slots * a.dim * sizeof(bf16_t)));
   }
   if (fp8_comp) {
     DSV41_REQUIRE(a.dim == 512, DSV41_E_SHAPE, "%s: the fp8 cache path supports dim 512, got %d", what, a.dim);
@@ -647,8 +713,10 @@ static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int
   }
   int rc = check_launch(what);
   if (rc || p.splits == 1) return rc;
-  hipLaunchKernelGGL(mla_combine_kernel<bf16_t>, dim3((unsigned)units, (unsigned)((a.heads + 3) / 4)), dim3(256), 0,
-                     stream, a);
+  if (p.splits <= 2) launch_combine<2>(a, units, stream);
+  else if (p.splits <= 4) launch_combine<4>(a, units, stream);
+  else if (p.splits <= 8) launch_combine<8>(a, units, stream);
+  else launch_combine<16>(a, units, stream);
   return check_launch(what);
 }
 
