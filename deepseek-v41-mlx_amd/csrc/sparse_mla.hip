@@ -127,6 +127,9 @@ constexpr int kMaxList = 2304;         // list entries one workgroup stages in L
 constexpr int kLdsBudget = 160 * 1024;
 constexpr int kMaxRing = 4;            // ring slots: steps in flight + the one computed
 
+// s_waitcnt immediate (gfx9 encoding): vmcnt 0, expcnt 7 and lgkmcnt 15 (no wait on those)
+constexpr int kWaitVmcnt0 = 0x0F70;
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -232,20 +235,47 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar address math
   const int ht = wave % HT, dh = wave / HT;
   const int wc = window_count(S, qs);
-  const int L = wc + S.k;
-  const int e_begin = sp * a.per_split;
-  const int cnt = min(max(min(e_begin + a.per_split, L) - e_begin, 0), kMaxList);  // planner: <= kMaxList
-  // resolve the split's list once (segment, ring slot, batch row): no global reads are left
-  // inside the copy pipeline and a step spends a few instructions per row
-  // (F8: a compressed-cache entry is stored as (row << 1) | 1 and addressed at issue time)
-  static_assert(!F8 || D == 512, "fp8 cache rows: 512 channels (one copy instruction with their scales)");
-  for (int e = tid; e < cnt; e += NT) {
-    const int u = list_pos(S, b, a.m, qs, e_begin + e, wc);
+  // The split's entries: its share of the window rows, then its share of the index list (one
+  // split takes the whole list). Window rows need no index read, so a split whose first step is
+  // all window rows issues that step before its index entries arrive.
+  const int ws = (wc + a.splits - 1) / a.splits, ks = (S.k + a.splits - 1) / a.splits;
+  const int w0 = min(sp * ws, wc), nw = min(w0 + ws, wc) - w0;
+  const int k0 = min(sp * ks, S.k), nk = min(k0 + ks, S.k) - k0;
+  const int cnt = min(nw + nk, kMaxList);       // planner: nw + nk <= kMaxList
+  auto entry_row = [&](int e) {                  // split entry -> row address (0 = masked)
+    const int u = list_pos(S, b, a.m, qs, e < nw ? w0 + e : wc + k0 + (e - nw), wc);
     const int ci = u - S.wp - S.n_chunk;
-    rows[e] = (F8 && u >= 0 && ci >= 0 && ci < S.n_comp) ? (((uint64_t)ci << 1) | 1ull)
-                                                          : reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, u, D));
-  }
+    // F8: a compressed-cache entry is encoded as (row << 1) | 1 and addressed at issue time
+    return (F8 && u >= 0 && ci >= 0 && ci < S.n_comp) ? (((uint64_t)ci << 1) | 1ull)
+                                                       : reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, u, D));
+  };
+  static_assert(!F8 || D == 512, "fp8 cache rows: 512 channels (one copy instruction with their scales)");
 
+  const int nsteps = (cnt + R - 1) / R;
+  const uint32_t ring_base = lds_offset(ring);
+  const uint64_t comp8 = F8 ? reinterpret_cast<uint64_t>(S.comp) + (uint64_t)b * (uint64_t)S.comp_bstride : 0ull;
+  const uint64_t scal8 = F8 ? reinterpret_cast<uint64_t>(S.comp_scale) + (uint64_t)b * (uint64_t)S.comp_scale_bstride : 0ull;
+  auto issue = [&](int t, bool direct) {
+    const int slot = t % NS;
+    const int mine = t * R + wave * RPW + (lane % RPW);
+    const uint64_t mp = mine < cnt ? (direct ? entry_row(mine) : rows[mine]) : 0ull;
+    if (lane < RPW) vrow[slot][wave * RPW + lane] = mp != 0ull ? 1 : 0;
+    const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
+    const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_base + (uint32_t)(slot * SLOT + wave * RPW * RS));
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) {
+      const uint64_t ent = lane_u64(lo, hi, rr);
+      if (F8 && (ent & 1ull)) {
+        // lanes 0..31: the row's 512 fp8 bytes; lane 32: its 16 scale bytes
+        const uint64_t ci = ent >> 1;
+        const uint64_t src = lane < D / 16 ? comp8 + ci * D + (uint64_t)lane * 16u
+                                           : scal8 + (ci / (uint64_t)S.comp_scale_rb) * (D / 32);
+        if (lane <= D / 16) dma16_vaddr(src, dst + rr * RS + D);
+      } else {
+        dma_row<D>(ent, dst + rr * RS, lane);
+      }
+    }
+  };
   const int h = hg * (HT * 16) + ht * 16 + l16;
   const bool hok = h < a.heads;
   bf16x8 qb[KSS];
@@ -265,37 +295,22 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
     m_run = fmaxf(s2, kNegFloor);
     l_run = g == 0 ? exp2f(s2 - m_run) : 0.0f;
   }
+  const bool early = nw >= R;                   // step 0: window rows only
+  if (early) issue(0, true);
+  // resolve the split's list once (segment, ring slot, batch row): no global reads are left
+  // inside the copy pipeline and a step spends a few instructions per row
+  for (int e = tid; e < cnt; e += NT) rows[e] = entry_row(e);
+
   f32x4 acc[DTS];
 #pragma unroll
   for (int dt = 0; dt < DTS; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // The query, sink and list loads are complete on every path before the step loop. Without a
+  // wait the compiler can see, it waits for the query registers at their first use inside the
+  // loop -- vmcnt(0) at every step, which also drains the copies in flight.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();                         // rows[] complete
 
-  const int nsteps = (cnt + R - 1) / R;
-  const uint32_t ring_base = lds_offset(ring);
-  const uint64_t comp8 = F8 ? reinterpret_cast<uint64_t>(S.comp) + (uint64_t)b * (uint64_t)S.comp_bstride : 0ull;
-  const uint64_t scal8 = F8 ? reinterpret_cast<uint64_t>(S.comp_scale) + (uint64_t)b * (uint64_t)S.comp_scale_bstride : 0ull;
-  auto issue = [&](int t) {
-    const int slot = t % NS;
-    const int mine = t * R + wave * RPW + (lane % RPW);
-    const uint64_t mp = mine < cnt ? rows[mine] : 0ull;
-    if (lane < RPW) vrow[slot][wave * RPW + lane] = mp != 0ull ? 1 : 0;
-    const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
-    const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_base + (uint32_t)(slot * SLOT + wave * RPW * RS));
-#pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      const uint64_t ent = lane_u64(lo, hi, rr);
-      if (F8 && (ent & 1ull)) {
-        // lanes 0..31: the row's 512 fp8 bytes; lane 32: its 16 scale bytes
-        const uint64_t ci = ent >> 1;
-        const uint64_t src = lane < D / 16 ? comp8 + ci * D + (uint64_t)lane * 16u
-                                           : scal8 + (ci / (uint64_t)S.comp_scale_rb) * (D / 32);
-        if (lane <= D / 16) dma16_vaddr(src, dst + rr * RS + D);
-      } else {
-        dma_row<D>(ent, dst + rr * RS, lane);
-      }
-    }
-  };
-  for (int t = 0; t < nsteps && t < NS - 1; ++t) issue(t);
+  for (int t = early ? 1 : 0; t < nsteps && t < NS - 1; ++t) issue(t, false);
 
   for (int t = 0; t < nsteps; ++t) {
     wait_steps<NL>(min(nsteps - 1 - t, NS - 2));
@@ -329,7 +344,7 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
         sq[rt][ks & 1] = mfma16x16x32(ld_bf16x8(buf + (rt * 16 + l16) * RS + (dh * DSL + ks * 32 + 8 * g) * 2),
                                       qb[ks], sq[rt][ks & 1]);
     // the next copies go out while the MFMAs drain (slot (t-1) % NS is free past the barrier)
-    if (t + NS - 1 < nsteps) issue(t + NS - 1);
+    if (t + NS - 1 < nsteps) issue(t + NS - 1, false);
     f32x4 sacc[2];
     sacc[0] = sq[0][0] + sq[0][1];
     sacc[1] = sq[1][0] + sq[1][1];
@@ -640,7 +655,8 @@ static MlaPlan plan_bf16(int64_t units, int heads, int list_max) {
   if (want < 1) want = 1;
   auto per = [&](int w) { return ((lm + w - 1) / w + kStepRows - 1) / kStepRows * kStepRows; };
   p.per_split = per(want);
-  while (p.per_split > kMaxList) p.per_split = per(++want);
+  // a split holds ceil(window / splits) + ceil(k / splits) <= per_split + 1 entries
+  while (p.per_split + 1 > kMaxList) p.per_split = per(++want);
   p.splits = (lm + p.per_split - 1) / p.per_split;
   return p;
 }
