@@ -12,10 +12,11 @@ step per input set), bracketed by events on the launch stream.
 
 Secondary: C3 prefill (8,192-token chunk after 32,768 tokens, top-2,048) indexer and sparse
 MLA TFLOP/s; the fp8-cache decode step (batch 16, 131,072 tokens, top-1,024, e4m3 caches with
-ue8m0 block scales dequantized in-kernel); and the CPU oracle (numpy) timed on a bounded sample
+ue8m0 block scales dequantized in-kernel); the 40-layer decode step of the C4 sharing topology
+(batch 64, 65,536 tokens, kernels only); and the CPU oracle (numpy) timed on a bounded sample
 of the decode workload.
 
-    python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-fp8] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-fp8] [--no-c4] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -47,6 +48,7 @@ def parse():
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-fp8", action="store_true", help="skip the fp8-cache decode line")
+    p.add_argument("--no-c4", action="store_true", help="skip the 40-layer decode line")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--eager", action="store_true",
                    help="launch the decode kernels without HIP graphs (for counter-collecting profilers)")
@@ -389,6 +391,104 @@ def run_fp8_decode(args, torch, device):
     }
 
 
+def c4_model_args():
+    """The 40-layer attention-only stack: layers 0-1 window only, ratio 4 elsewhere; owners
+    2/8/14/20; index sources 2/8/14/20/24/28/32/36 (24-36 score against layer 20's keys under
+    its candidate mask: blocks of 8, top 2,048 blocks); 64 heads x 512, indexer 64 x 128, top-512."""
+    from dsv41.config import ModelArgs
+    return ModelArgs(n_layers=40, compress_ratios=(0, 0) + (4,) * 38, kv_source_layers=(2, 8, 14, 20),
+                     index_source_layers=(2, 8, 14, 20, 24, 28, 32, 36), candidate_source_layer=20,
+                     candidate_topk_blocks=2048, candidate_block_size=8, index_n_heads=64, index_head_dim=128,
+                     index_topk=512, window_size=128, n_heads=64, head_dim=512, rope_head_dim=64,
+                     compress_rope_theta=160000.0, original_seq_len=65536, rope_factor=16.0, max_seq_len=65536)
+
+
+def c4_step_bytes(a, B, start_pos):
+    """Algorithmic HBM bytes of one 40-layer decode step (bf16 caches): per layer the sparse
+    MLA gather (window + top-k rows), q and o; per index source the key stream, its queries
+    and the score write; top-k score reads and index writes; the candidate mask write and
+    reads; the window / latent / key writes of this token."""
+    H, D, Hi, Di, W, K = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim, a.window_size, a.index_topk
+    wp = min(start_pos, W)
+    total = 0
+    for l in range(a.n_layers):
+        r = a.compress_ratio(l)
+        rows = min(W, wp + 1)
+        total += B * D * 2                                   # window write
+        if r:
+            nb = (start_pos + 1) // r
+            k = min(K, nb)
+            rows += k
+            total += B * k * 4                               # index list read
+            if l in a.index_source_layers:
+                total += B * (nb * Di * 2 + Hi * Di * 2 + Hi * 2 + nb * 4)   # indexer
+                total += B * (nb * 4 + k * 4)                               # top-k
+                if l == a.candidate_source_layer:
+                    total += B * (nb * 4 + nb)                              # block max + mask write
+                elif 0 <= a.candidate_source_layer < l:
+                    total += B * nb                                         # mask read
+            if l in a.kv_source_layers:
+                total += B * D * 2 * 2 + (B * Di * 2 * 2 if l in a.index_source_layers else 0)
+        total += B * (rows * D * 2 + 2 * H * D * 2)          # sparse MLA gather, q, o
+    return total
+
+
+def run_c4(args, torch, device):
+    """C4: one decode token through the 40-layer stack at batch 64 and 65,536 tokens of context
+    (16,384 compressed entries per sequence), kernels only: window writes, owner latent / key
+    writes (the token completes a group), indexer + top-k at the 8 index sources (candidate
+    blocks at layer 20, applied at 24-36), sparse MLA at every layer. Caches (about 5.7 GB)
+    exceed the Infinity Cache, so one input set suffices."""
+    from dsv41 import _abi
+    from dsv41.cache import ModelCache
+    from dsv41.indexer import weight_scale
+    from dsv41.step import StackDecodeStep
+
+    a = c4_model_args()
+    B, start = 64, 65535
+    bf = torch.bfloat16
+    log(f"[bench] C4 40-layer decode B={B} start_pos={start}")
+    g = torch.Generator(device=device).manual_seed(SEED + 300)
+    sc = 576 ** -0.5
+    cache = ModelCache(a, B, start + 1, bf, device)
+    for lc in cache.layers:
+        for t in (lc.win_kv, lc.comp_kv):
+            if t is not None:
+                t.copy_(torch.randn(t.shape, generator=g, device=device) * sc)
+        if lc.index_k is not None:
+            lc.index_k.copy_(torch.randn(lc.index_k.shape, generator=g, device=device))
+            _abi.fq_fp4_ue8m0(lc.index_k, out=lc.index_k)
+    H, D, Hi, Di = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim
+    rn = lambda *shape: torch.randn(*shape, generator=g, device=device)   # noqa: E731
+    ins = []
+    for l in range(a.n_layers):
+        x = dict(q=(rn(B, 1, H, D) * sc).to(bf), kv=(rn(B, 1, D) * sc).to(bf), sink=rn(H))
+        if a.compress_ratio(l) and l in a.index_source_layers:
+            x.update(index_q=_abi.fq_fp4_ue8m0(rn(B, 1, Hi, Di).to(bf)), w_raw=rn(B, 1, Hi).to(bf),
+                     w_scale=weight_scale(Hi, Di, bf))
+        if l in a.kv_source_layers:
+            x["latent"] = rn(B, 1, D).to(bf)
+            if l in a.index_source_layers:
+                x.update(k_raw=rn(B, 1, Di).to(bf), k_norm=torch.ones(Di, device=device))
+        ins.append(x)
+    step = StackDecodeStep(a, B, start, bf, device)
+    gr = graph_of(lambda _: step(cache, ins), [None], torch)
+    for _ in range(max(1, args.warmup // 4)):
+        gr.replay()
+    reps = max(4, args.steps // 8)
+    ms = time_graph(gr, reps, torch)
+    nbytes = c4_step_bytes(a, B, start)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] C4 step {ms:.3f} ms, {B / (ms * 1e-3):.0f} tokens/s, {gbs:.0f} GB/s")
+    del gr
+    return {
+        "workload": "C4: 40-layer attention-only decode step (kernels only), B=64, 65536-token context "
+                    "(nb=16384), ratio 4, top-512; owners 2/8/14/20, index sources 2..36, candidate source 20",
+        "step_ms": ms, "tokens_per_s": B / (ms * 1e-3), "steps": reps,
+        "step_algorithmic_bytes": nbytes, "hbm_GBps_step": gbs, "hbm_frac_step": gbs / HBM_PEAK_GBS,
+    }
+
+
 def cpu_baseline(s: Shape, sets, cos, sin, ws, seconds, torch):
     """The numpy oracle on whole batch rows of the same decode workload, until `seconds` pass."""
     import numpy as np
@@ -480,6 +580,12 @@ def main():
             result["fp8_cache_decode"] = run_fp8_decode(args, torch, device)
         except Exception as e:
             result["fp8_cache_decode"] = {"error": repr(e)}
+    if not args.no_c4:
+        try:
+            result["c4_stack_decode"] = run_c4(args, torch, device)
+        except Exception as e:
+            result["c4_stack_decode"] = {"error": repr(e)}
+        torch.cuda.empty_cache()
     if not args.no_cpu:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(s, sets, cos, sin, ws, args.cpu_seconds, torch)

@@ -46,3 +46,107 @@ class SparseDecodeStep:
                         self.window, self.start_pos, cos, sin, self.rd, out=self.out,
                         workspace=self.workspace)
         return self.out, idx
+
+
+class _LayerPlan:
+    __slots__ = ("layer_id", "ratio", "kv_source", "index_source", "owns_k", "candidate_source",
+                 "uses_candidates", "cos", "sin", "out", "idx")
+
+
+class StackDecodeStep:
+    """One decode token through every layer of an attention-only stack, kernels only.
+
+    Per layer this is the kernel sequence of attention.py:106-175 with the projections left
+    out (as in ``SparseDecodeStep``): the owners store the token's completed group (latent ->
+    rope -> fp4/e4m3 fake-quant into comp_kv; key -> k_norm -> rope -> fp4/ue8m0 into
+    index_k), index sources score their queries against the most recent key owner's cache
+    (layers after the candidate source with its block mask applied) and select the top-k, and
+    every layer attends over its window ring, this token's KV and the most recent owner's
+    comp_kv in place, then writes the token into its ring. The sharing follows the layer loop
+    of model.py:141-154: the most recent kv source, key owner, top-k selection and candidate
+    mask are handed down the stack.
+
+    ``inputs[l]`` holds layer l's per-token tensors: ``q`` [b,1,H,D] (roped), ``kv`` [b,1,D]
+    (the window KV after its prologue), ``sink`` [H]; index sources add ``index_q``
+    [b,1,Hi,Di] (roped, fake-quantized), ``w_raw`` [b,1,Hi] and ``w_scale``; kv sources add
+    ``latent`` [b,1,D] (pre-rope); key owners add ``k_raw`` [b,1,Di] and ``k_norm`` [Di].
+    Outputs (``out`` per layer) and scratch are allocated once, so a step can be captured in
+    a HIP graph.
+    """
+
+    def __init__(self, args, bsz: int, start_pos: int, dtype=torch.bfloat16, device="cuda"):
+        from .layers import yarn_inv_freqs
+
+        self.args, self.bsz, self.start_pos, self.dtype = args, bsz, start_pos, dtype
+        dev = torch.device(device)
+        self.end_pos = start_pos + 1
+        self.window = args.window_size
+        self.wp = min(start_pos, self.window)
+        self.offset = self.wp + 1
+        self.scale = args.head_dim ** -0.5
+        tables = {}
+
+        def table(ratio):
+            key = bool(ratio)
+            if key not in tables:
+                orig, theta = (args.original_seq_len, args.compress_rope_theta) if ratio else (0, args.rope_theta)
+                f = torch.from_numpy(yarn_inv_freqs(args.rope_head_dim, orig, theta, args.rope_factor,
+                                                    args.beta_fast, args.beta_slow)).to(dev)
+                tables[key] = _abi.rope_table(f, self.end_pos)
+            return tables[key]
+
+        self.plan = []
+        max_rows, max_nb = 1, 1
+        for l in range(args.n_layers):
+            p = _LayerPlan()
+            p.layer_id = l
+            p.ratio = args.compress_ratio(l)
+            p.kv_source = l in args.kv_source_layers
+            p.index_source = p.ratio > 0 and l in args.index_source_layers
+            p.owns_k = p.index_source and p.kv_source
+            p.candidate_source = p.index_source and l == args.candidate_source_layer
+            p.uses_candidates = p.index_source and 0 <= args.candidate_source_layer < l
+            p.cos, p.sin = table(p.ratio)
+            p.out = torch.empty(bsz, 1, args.n_heads, args.head_dim, dtype=dtype, device=dev)
+            p.idx = None                                   # an index source's last selection
+            if p.ratio:
+                max_nb = max(max_nb, self.end_pos // p.ratio)
+                max_rows = max(max_rows, min(self.window, self.wp + 1) + min(args.index_topk, self.end_pos // p.ratio))
+            self.plan.append(p)
+        self.scores = torch.empty(bsz * max_nb, dtype=torch.float32, device=dev)   # [b, 1, nb] per layer
+        ws = _abi.mla_workspace_bytes(bsz, 1, args.n_heads, args.head_dim, max_rows, dtype)
+        self.workspace = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
+
+    def __call__(self, cache, inputs):
+        """cache: a ``ModelCache`` for ``bsz`` rows; returns the per-layer outputs."""
+        a, sp, b = self.args, self.start_pos, self.bsz
+        kv_src = key_src = topk = cand = None
+        for p in self.plan:
+            x = inputs[p.layer_id]
+            lc = cache.layers[p.layer_id]
+            comp, n_comp, idx = None, 0, None
+            if p.ratio:
+                nb = self.end_pos // p.ratio
+                emits = self.end_pos % p.ratio == 0       # this token completes group nb - 1
+                if p.kv_source:
+                    kv_src = lc
+                if p.index_source:
+                    if p.owns_k:
+                        if emits:
+                            _abi.index_key_publish(x["k_raw"], lc.index_k, nb - 1, p.ratio, x["k_norm"],
+                                                   p.cos, p.sin, a.rope_head_dim, a.norm_eps)
+                        key_src = lc
+                    scores = self.scores[:b * nb].view(b, 1, nb)
+                    _abi.indexer_score(x["index_q"], x["w_raw"], x["w_scale"], key_src.index_k[:b, :nb], sp,
+                                       p.ratio, cand if p.uses_candidates else None, out=scores)
+                    if p.candidate_source:
+                        cand = _abi.candidate_blocks(scores, a.candidate_topk_blocks, a.candidate_block_size,
+                                                     None, sp, p.ratio)
+                    topk = p.idx = _abi.topk_select(scores, a.index_topk, sp, p.ratio, self.offset)
+                if p.kv_source and emits:
+                    _abi.comp_write(x["latent"], lc.comp_kv, nb - 1, p.ratio, p.cos, p.sin, a.rope_head_dim)
+                comp, n_comp, idx = kv_src.comp_kv[:b], nb, topk
+            _abi.sparse_mla(x["q"], lc.win_kv, x["kv"], comp, n_comp, x["sink"], idx, self.scale, self.window, sp,
+                            p.cos, p.sin, a.rope_head_dim, out=p.out, workspace=self.workspace)
+            lc.write_window(sp, x["kv"])
+        return [p.out for p in self.plan]

@@ -27,6 +27,16 @@ TOPO = dict(dim=64, n_layers=6, n_heads=4, head_dim=64, rope_head_dim=16, q_lora
             index_topk=4, rope_theta=10000.0, compress_rope_theta=40000.0, original_seq_len=64,
             rope_factor=4.0, max_seq_len=128)
 
+# The 40-layer sharing topology of the C4 decode config at toy sizes: window-only layers 0-1,
+# owners 2/8/14/20, index sources 2..36 (24-36 score against layer 20's keys under its
+# candidate mask, which keeps 3 of 5 blocks here), ratio 4, window 8 (the ring wraps).
+C4_TOY = dict(dim=64, n_layers=40, n_heads=4, head_dim=64, rope_head_dim=16, q_lora_rank=32,
+              o_lora_rank=16, o_groups=2, window_size=8, compress_ratios=(0, 0) + (4,) * 38,
+              kv_source_layers=(2, 8, 14, 20), index_source_layers=(2, 8, 14, 20, 24, 28, 32, 36),
+              candidate_source_layer=20, candidate_topk_blocks=3, candidate_block_size=2,
+              index_n_heads=16, index_head_dim=32, index_topk=4, rope_theta=10000.0,
+              compress_rope_theta=40000.0, original_seq_len=64, rope_factor=4.0, max_seq_len=128)
+
 
 def args(cfg: dict) -> R.Args:
     return R.Args(**cfg)

@@ -1,0 +1,213 @@
+"""The 40-layer decode step (dsv41.step.StackDecodeStep) of the C4 sharing topology.
+
+* Toy size: the kernels-only step reproduces, bit for bit, every per-layer attention output
+  and every cache write of the full ``AttentionStack`` forward (projections included) for the
+  same decode token -- the per-layer kernel inputs are recorded from that forward.
+* Full size (batch 64, 65,536-token context -> 16,384 entries, 64 heads x 512, indexer
+  64 x 128, top-512, 40 layers): sampled rows of a window-only layer, the last index source
+  (layer 36: its own queries against layer 20's keys under layer 20's candidate mask) and a
+  consumer (layer 39) against the oracle -- scores within 1e-5 of max |S|, top-k bit-exact
+  given those scores, outputs within 2e-2 relative.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from common import C4_TOY, SEED_BASE, args, load_stack, model_args, rel_max_diff, to_np
+from oracle import cpu_ref as R
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+def _clone_cache(cache):
+    import copy
+    c = copy.copy(cache)
+    c.layers = []
+    for lc in cache.layers:
+        n = copy.copy(lc)
+        for name in ("win_kv", "comp_kv", "index_k"):
+            t = getattr(lc, name)
+            setattr(n, name, None if t is None else t.clone())
+        c.layers.append(n)
+    return c
+
+
+def _record_decode(stack, h, cache):
+    """Run one forward of the stack and record the kernel inputs of each layer."""
+    from dsv41 import _abi
+    recs = [dict() for _ in stack.layers]
+    layer = [0]
+    orig = {n: getattr(_abi, n) for n in ("sparse_mla", "indexer_score", "comp_write", "index_key_publish")}
+
+    def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, *a, **k):
+        r = recs[layer[0]]
+        r.update(q=q.clone(), kv=chunk_kv.clone(), sink=attn_sink.clone())
+        o = orig["sparse_mla"](q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, *a, **k)
+        r["out"] = o.clone()
+        layer[0] += 1
+        return o
+
+    def indexer_score(q, w_raw, w_scale, *a, **k):
+        recs[layer[0]].update(index_q=q.clone(), w_raw=w_raw.clone(), w_scale=w_scale)
+        return orig["indexer_score"](q, w_raw, w_scale, *a, **k)
+
+    def comp_write(latents, *a, **k):
+        recs[layer[0]]["latent"] = latents.clone()
+        return orig["comp_write"](latents, *a, **k)
+
+    def index_key_publish(k_raw, index_k, g0, ratio, norm_w, *a, **k):
+        recs[layer[0]].update(k_raw=k_raw.clone(), k_norm=norm_w.clone())
+        return orig["index_key_publish"](k_raw, index_k, g0, ratio, norm_w, *a, **k)
+
+    for n, f in (("sparse_mla", sparse_mla), ("indexer_score", indexer_score), ("comp_write", comp_write),
+                 ("index_key_publish", index_key_publish)):
+        setattr(_abi, n, f)
+    try:
+        stack(h, cache)
+    finally:
+        for n, f in orig.items():
+            setattr(_abi, n, f)
+    assert layer[0] == len(stack.layers)
+    return recs
+
+
+def test_stack_step_reproduces_attention_stack(gpu):
+    """Toy C4 topology in bf16: 39 prefill tokens, then the decode token at position 39, which
+    completes group 9 (owners write a latent and a key)."""
+    from dsv41.model import AttentionStack
+    from dsv41.step import StackDecodeStep
+    a = args(C4_TOY)
+    st = AttentionStack(model_args(C4_TOY), torch.bfloat16, gpu)
+    load_stack(st, R.make_params(a, SEED_BASE + 40, "bf16"))
+    rng = np.random.default_rng(SEED_BASE + 40)
+    b, T = 2, 40
+    h = torch.from_numpy(rng.standard_normal((b, T, a.dim)).astype(F32)).to(gpu).to(torch.bfloat16)
+    cache = st.make_cache(b, a.max_seq_len)
+    st(h[:, :T - 1], cache)
+    before = _clone_cache(cache)
+    recs = _record_decode(st, h[:, T - 1:], cache)
+    step = StackDecodeStep(model_args(C4_TOY), b, T - 1, torch.bfloat16, gpu)
+    outs = step(before, recs)
+    torch.cuda.synchronize()
+    for l, (o, r) in enumerate(zip(outs, recs)):
+        assert torch.equal(o, r["out"]), f"layer {l} output"
+    for l, (g, w) in enumerate(zip(before.layers, cache.layers)):
+        for name in ("win_kv", "comp_kv", "index_k"):
+            x, y = getattr(g, name), getattr(w, name)
+            assert (x is None) == (y is None)
+            if x is not None:
+                assert torch.equal(x, y), f"layer {l} {name}"
+    # the candidate mask is live at this size: layers after 20 use it, and it drops blocks
+    assert step.plan[20].candidate_source and step.plan[24].uses_candidates
+
+
+def c4_args(**over):
+    from dsv41.config import ModelArgs
+    cfg = dict(n_layers=40, compress_ratios=(0, 0) + (4,) * 38, kv_source_layers=(2, 8, 14, 20),
+               index_source_layers=(2, 8, 14, 20, 24, 28, 32, 36), candidate_source_layer=20,
+               candidate_topk_blocks=2048, candidate_block_size=8, index_n_heads=64, index_head_dim=128,
+               index_topk=512, window_size=128, n_heads=64, head_dim=512, rope_head_dim=64,
+               compress_rope_theta=160000.0, original_seq_len=65536, rope_factor=16.0, max_seq_len=65536)
+    cfg.update(over)
+    return ModelArgs(**cfg)
+
+
+def c4_inputs(a, b, gen, device):
+    """Per-layer decode inputs of the C4 config: q / kv N(0,1)/sqrt(576) bf16, sinks N(0,1),
+    index queries fp4-fake-quantized N(0,1), head weights N(0,1) bf16, owner latents and raw
+    keys N(0,1)."""
+    from dsv41 import _abi
+    from dsv41.indexer import weight_scale
+    s = 576 ** -0.5
+    bf = torch.bfloat16
+    H, D, Hi, Di = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim
+    rn = lambda *shape: torch.randn(*shape, generator=gen, device=device)   # noqa: E731
+    ins = []
+    for l in range(a.n_layers):
+        x = dict(q=(rn(b, 1, H, D) * s).to(bf), kv=(rn(b, 1, D) * s).to(bf), sink=rn(H))
+        if a.compress_ratio(l) and l in a.index_source_layers:
+            x["index_q"] = _abi.fq_fp4_ue8m0(rn(b, 1, Hi, Di).to(bf))
+            x["w_raw"] = rn(b, 1, Hi).to(bf)
+            x["w_scale"] = weight_scale(Hi, Di, bf)
+        if l in a.kv_source_layers:
+            x["latent"] = rn(b, 1, D).to(bf)
+            if l in a.index_source_layers:
+                x["k_raw"] = rn(b, 1, Di).to(bf)
+                x["k_norm"] = torch.ones(Di, device=device)
+        ins.append(x)
+    return ins
+
+
+def c4_fill_cache(cache, gen):
+    """Window rings and compressed caches N(0,1)/sqrt(576), index keys fp4-fake-quantized N(0,1)."""
+    from dsv41 import _abi
+    s = 576 ** -0.5
+    for lc in cache.layers:
+        for t in (lc.win_kv, lc.comp_kv):
+            if t is not None:
+                t.copy_(torch.randn(t.shape, generator=gen, device=t.device) * s)
+        if lc.index_k is not None:
+            lc.index_k.copy_(torch.randn(lc.index_k.shape, generator=gen, device=lc.index_k.device))
+            _abi.fq_fp4_ue8m0(lc.index_k, out=lc.index_k)
+
+
+def _oracle_layer_out(a, q_row, win_before, kv_row, comp_row, idx_row, sink, start_pos, ratio):
+    """Oracle attention output of one batch row: concat(window chrono, chunk, comp), then the
+    inverse rope of the layer's table."""
+    W = a.window_size
+    wp = min(start_pos, W)
+    slots = (start_pos - wp + np.arange(wp)) % W
+    parts = [win_before[slots], kv_row]
+    if comp_row is not None:
+        parts.append(comp_row)
+    kv_all = np.concatenate(parts, axis=0)[None]
+    widx = R.window_idx_matrix(wp, 1, W)[None]
+    full = widx if idx_row is None else np.concatenate([widx, idx_row[None, None]], -1)
+    o = R.sparse_attn(q_row[None, None], kv_all, sink, full, a.head_dim ** -0.5, dtype="bf16")
+    orig, theta = (a.original_seq_len, a.compress_rope_theta) if ratio else (0, a.rope_theta)
+    rc, rs = R.precompute_freqs_cis(a.rope_head_dim, start_pos + 1, orig, theta, a.rope_factor, a.beta_fast,
+                                    a.beta_slow)
+    return R.rope_tail(o, a.rope_head_dim, rc[[start_pos]], rs[[start_pos]], inverse=True, dtype="bf16")[0, 0]
+
+
+def test_c4_full_size_sampled_rows(gpu):
+    from dsv41.cache import ModelCache
+    from dsv41.step import StackDecodeStep
+    a = c4_args()
+    B, sp, r = 64, 65535, 4
+    gen = torch.Generator(device=gpu).manual_seed(SEED_BASE + 4)
+    cache = ModelCache(a, B, 65536, torch.bfloat16, gpu)
+    c4_fill_cache(cache, gen)
+    ins = c4_inputs(a, B, gen, gpu)
+    rows = (0, 37, 63)
+    layers = (0, 36, 39)
+    win_before = {(l, b): to_np(cache.layers[l].win_kv[b]) for l in layers for b in rows}
+    step = StackDecodeStep(a, B, sp, torch.bfloat16, gpu)
+    outs = step(cache, ins)
+    torch.cuda.synchronize()
+    nb = (sp + 1) // r
+    lens = R.query_lens(sp, 1, r)
+    f = lambda t: t.float().cpu().numpy()   # noqa: E731
+    got_s = to_np(step.scores[:B * nb].view(B, 1, nb))    # the last index source's (layer 36)
+    idx36 = step.plan[36].idx.cpu().numpy()
+    for b in rows:
+        keys20 = f(cache.layers[20].index_k[b, :nb])[None]
+        w20 = R.cast(f(ins[20]["w_raw"][b:b + 1]) * F32(ins[20]["w_scale"]), "bf16")
+        s20 = R.indexer_scores(f(ins[20]["index_q"][b:b + 1]), keys20, w20, sp, r)
+        cand = R.select_candidate_blocks(s20, lens, a.candidate_topk_blocks, a.candidate_block_size)
+        w36 = R.cast(f(ins[36]["w_raw"][b:b + 1]) * F32(ins[36]["w_scale"]), "bf16")
+        want = R.indexer_scores(f(ins[36]["index_q"][b:b + 1]), keys20, w36, sp, r, cand)
+        assert np.abs(got_s[b:b + 1] - want).max() <= 1e-5 * np.abs(want).max(), f"scores row {b}"
+        want_i = R.topk_indices(got_s[b:b + 1], a.index_topk, lens, min(sp, a.window_size) + 1)
+        assert np.array_equal(idx36[b:b + 1], want_i), f"top-k row {b}"
+        comp20 = f(cache.layers[20].comp_kv[b, :nb])
+        for l in layers:
+            ratio = a.compress_ratio(l)
+            o = _oracle_layer_out(a, f(ins[l]["q"][b, 0]), win_before[(l, b)], f(ins[l]["kv"][b]),
+                                  comp20 if ratio else None, idx36[b, 0] if ratio else None, f(ins[l]["sink"]),
+                                  sp, ratio)
+            assert rel_max_diff(to_np(outs[l][b, 0]), o) < 2e-2, f"layer {l} row {b}"
