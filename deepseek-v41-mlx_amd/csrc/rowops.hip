@@ -75,15 +75,17 @@ __device__ __forceinline__ void fake_quant_block(float* v) {
   if (FQ == FQ_FP8_UE8M0) {
     amax = fmaxf(amax, 1e-4f);
     const float s = pow2_ceil_log2(amax * (float)(1.0 / 448.0));
+    const float inv = __fdiv_rn(1.0f, s);   // s is a power of two: x * (1/s) rounds as x / s does
 #pragma unroll
     for (int i = 0; i < BLK; ++i)
-      v[i] = io<T>::rnd(e4m3_round(fminf(fmaxf(__fdiv_rn(v[i], s), -448.0f), 448.0f)) * s);
+      v[i] = io<T>::rnd(e4m3_round(fminf(fmaxf(v[i] * inv, -448.0f), 448.0f)) * s);
   } else if (FQ == FQ_FP4_UE8M0) {
     amax = fmaxf(amax, (float)(6.0 * 1.1754943508222875e-38));  // 6 * 2^-126
     const float s = pow2_ceil_log2(amax * (float)(1.0 / 6.0));
+    const float inv = __fdiv_rn(1.0f, s);   // s is a power of two: x * (1/s) rounds as x / s does
 #pragma unroll
     for (int i = 0; i < BLK; ++i)
-      v[i] = io<T>::rnd(e2m1_round(fminf(fmaxf(__fdiv_rn(v[i], s), -6.0f), 6.0f)) * s);
+      v[i] = io<T>::rnd(e2m1_round(fminf(fmaxf(v[i] * inv, -6.0f), 6.0f)) * s);
   } else if (FQ == FQ_FP4_E4M3) {
     amax = fmaxf(amax, 0.01171875f);                             // 6 * 2^-9
     const float s = e4m3_round(__fdiv_rn(amax, 6.0f));
@@ -93,17 +95,63 @@ __device__ __forceinline__ void fake_quant_block(float* v) {
   }
 }
 
-template <typename T, bool NORM, bool ROPE, int FQ, int BLK>
-__global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t row = gid / a.cpr;
-  const int c = (int)(gid - row * a.cpr);
-  if (row >= a.rows) return;  // whole row groups leave together (cpr divides 64 when NORM)
-  const int h = (int)(row % a.H);
-  const int64_t t = row / a.H;
-  const int s = (int)(t % a.S);
-  const int64_t b = t / a.S;
+// Row coordinates of thread gid: (row, chunk c, head h, token s, batch row b). Launches with
+// fewer than 2^32 threads (the common case) use 32-bit division, a short sequence where the
+// 64-bit one is a long software routine.
+struct RowPos {
+  int64_t row, b;
+  int c, h, s;
+};
 
+template <bool WIDE>
+__device__ __forceinline__ RowPos row_pos(const RowArgs& a) {
+  RowPos p;
+  if (WIDE) {
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    p.row = gid / a.cpr;
+    p.c = (int)(gid - p.row * a.cpr);
+    p.h = (int)(p.row % a.H);
+    const int64_t t = p.row / a.H;
+    p.s = (int)(t % a.S);
+    p.b = t / a.S;
+  } else {
+    const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t row = gid / (uint32_t)a.cpr;
+    p.c = (int)(gid - row * (uint32_t)a.cpr);
+    const uint32_t t = row / (uint32_t)a.H;
+    p.h = (int)(row - t * (uint32_t)a.H);
+    const uint32_t bb = t / (uint32_t)a.S;
+    p.s = (int)(t - bb * (uint32_t)a.S);
+    p.row = row;
+    p.b = bb;
+  }
+  return p;
+}
+
+template <typename T, bool NORM, bool ROPE, int FQ, int BLK, bool WIDE>
+__global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
+  const RowPos rp = row_pos<WIDE>(a);
+  const int64_t row = rp.row, b = rp.b;
+  const int c = rp.c, h = rp.h, s = rp.s;
+  if (row >= a.rows) return;  // whole row groups leave together (cpr divides 64 when NORM)
+
+  // rope factors of this chunk's pairs, requested before the row itself so the two loads
+  // overlap (a pair ahead of the tail reads the first entry and is left unrotated)
+  const int first = a.dim - a.rd;
+  const bool rope = ROPE && a.rd > 0 && c * 32 + 32 > first;   // the chunk meets the rope tail
+  float cs[16], sn[16];
+  if (rope) {
+    const int half = a.rd >> 1;
+    const int64_t pos = (int64_t)a.pos_base + (int64_t)s * a.pos_step;
+    const float* ct = a.cos_tab + pos * half;
+    const float* st = a.sin_tab + pos * half;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int p = max(c * 32 + 2 * j - first, 0) >> 1;
+      cs[j] = ct[p];
+      sn[j] = st[p];
+    }
+  }
   float v[32];
   load32<T>(reinterpret_cast<const T*>(a.src) + row * a.dim + c * 32, v);
 
@@ -117,22 +165,14 @@ __global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) v[i] = io<T>::rnd(w[i] * (v[i] * inv));
   }
-  if (ROPE) {
-    const int first = a.dim - a.rd;
-    const int half = a.rd >> 1;
-    const int64_t pos = (int64_t)a.pos_base + (int64_t)s * a.pos_step;
-    const float* ct = a.cos_tab + pos * half;
-    const float* st = a.sin_tab + pos * half;
+  if (rope) {
 #pragma unroll
-    for (int i = 0; i < 32; i += 2) {
-      const int ch = c * 32 + i;
-      if (ch >= first) {
-        const int p = (ch - first) >> 1;
-        const float cs = ct[p];
-        const float sn = a.inverse ? -st[p] : st[p];
-        const float xr = v[i], xi = v[i + 1];
-        v[i] = io<T>::rnd(__fsub_rn(__fmul_rn(xr, cs), __fmul_rn(xi, sn)));
-        v[i + 1] = io<T>::rnd(__fadd_rn(__fmul_rn(xr, sn), __fmul_rn(xi, cs)));
+    for (int j = 0; j < 16; ++j) {
+      if (c * 32 + 2 * j >= first) {
+        const float s_ = a.inverse ? -sn[j] : sn[j];
+        const float xr = v[2 * j], xi = v[2 * j + 1];
+        v[2 * j] = io<T>::rnd(__fsub_rn(__fmul_rn(xr, cs[j]), __fmul_rn(xi, s_)));
+        v[2 * j + 1] = io<T>::rnd(__fadd_rn(__fmul_rn(xr, s_), __fmul_rn(xi, cs[j])));
       }
     }
   }
@@ -150,8 +190,12 @@ static int launch_rows(const RowArgs& a, hipStream_t stream, const char* what) {
   const int64_t threads = a.rows * a.cpr;
   if (threads == 0) return 0;
   const int64_t blocks = (threads + 255) / 256;
-  hipLaunchKernelGGL((row_pipeline_kernel<T, NORM, ROPE, FQ, BLK>), dim3((unsigned)blocks), dim3(256),
-                     0, stream, a);
+  if (blocks * 256 <= (int64_t)UINT32_MAX)
+    hipLaunchKernelGGL((row_pipeline_kernel<T, NORM, ROPE, FQ, BLK, false>), dim3((unsigned)blocks), dim3(256),
+                       0, stream, a);
+  else
+    hipLaunchKernelGGL((row_pipeline_kernel<T, NORM, ROPE, FQ, BLK, true>), dim3((unsigned)blocks), dim3(256),
+                       0, stream, a);
   return check_launch(what);
 }
 

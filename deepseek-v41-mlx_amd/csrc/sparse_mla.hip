@@ -46,7 +46,21 @@ struct MlaArgs {
   int hgroups, splits, per_split;
   bf16_t* part_o;     // split partials: numerator / denominator, rounded to bf16 [slot][dim]
   float* part_ml;     // split partials: (log2-domain max, denominator) [slot][2]
+  void* ring_w;       // one-token decode: also store the token's KV row in its ring slot (or null)
 };
+
+// One-token decode: copy batch row b's KV row into ring slot start_pos % window. The slot holds
+// position start_pos - window, which has just left the window, so no entry of the launch reads
+// it; one wave per batch row does the copy, at its start.
+template <typename T>
+__device__ __forceinline__ void ring_store(const MlaArgs& a, int b, int lane, int lanes) {
+  const KvSrc& S = a.src;
+  const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const T*>(S.chunk) + (int64_t)b * S.chunk_bstride);
+  uint4* dst = reinterpret_cast<uint4*>(reinterpret_cast<T*>(a.ring_w) + (int64_t)b * S.ring_bstride +
+                                        (int64_t)(a.start_pos % S.window) * a.dim);
+  const int n16 = a.dim * (int)sizeof(T) / 16;
+  for (int c = lane; c < n16; c += lanes) dst[c] = src[c];
+}
 
 // Workgroups are dispatched to the 8 XCDs round-robin by linear id and each XCD has its own L2.
 // Renumber so that consecutive logical tiles run on one XCD: the head groups of one query (and
@@ -234,6 +248,7 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar address math
   const int ht = wave % HT, dh = wave / HT;
+  if (a.ring_w && hg == 0 && sp == 0 && wave == 0) ring_store<bf16_t>(a, b, lane, 64);
   const int wc = window_count(S, qs);
   // The split's entries: its share of the window rows, then its share of the index list (one
   // split takes the whole list). Window rows need no index read, so a split whose first step is
@@ -529,6 +544,7 @@ __global__ __launch_bounds__(256) void mla_f32_kernel(MlaArgs a) {
   const int unit = blockIdx.x, hbase = blockIdx.y * kF32Heads;
   const int b = unit / a.m, qs = unit - (unit / a.m) * a.m;
   const int tid = threadIdx.x;
+  if (a.ring_w && blockIdx.y == 0) ring_store<float>(a, b, tid, 256);
   const int wc = window_count(S, qs);
   const int L = wc + S.k;
   const float* qrow = reinterpret_cast<const float*>(a.q) + (int64_t)unit * a.heads * D;
@@ -765,12 +781,12 @@ extern "C" int dsv41_sparse_attn(const void* q, const void* kv, const float* sin
   return run_mla(what, a, (int64_t)bsz * m, k, dtype, workspace, workspace_bytes, stream);
 }
 
-extern "C" int dsv41_sparse_mla(const void* q, const void* win_kv, const void* chunk_kv, const void* comp_kv,
-                                int64_t comp_bstride, int32_t n_comp, const float* sink, const int32_t* idx, int32_t k,
-                                void* o, int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t window,
-                                int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
-                                int32_t dtype, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  const char* what = "dsv41_sparse_mla";
+static int sparse_mla_layer(const char* what, const void* q, const void* win_kv, const void* chunk_kv,
+                            const void* comp_kv, int64_t comp_bstride, int32_t n_comp, const float* sink,
+                            const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads, int32_t dim,
+                            int32_t window, int32_t start_pos, float scale, const float* cos_tab,
+                            const float* sin_tab, int32_t rd, int32_t dtype, void* workspace, size_t workspace_bytes,
+                            bool write_ring, hipStream_t stream) {
   const int wp = start_pos < window ? start_pos : window;
   DSV41_REQUIRE(q && chunk_kv && sink && o && (idx || k == 0) && (win_kv || wp == 0) && (comp_kv || n_comp == 0),
                 DSV41_E_ARG, "%s: null tensor", what);
@@ -792,8 +808,33 @@ extern "C" int dsv41_sparse_mla(const void* q, const void* win_kv, const void* c
   a.src.idx = idx; a.src.k = k; a.src.win_implicit = 1;
   a.m = n; a.heads = heads; a.dim = dim; a.scale = scale;
   a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.start_pos = start_pos;
+  if (write_ring) {
+    DSV41_REQUIRE(n == 1 && win_kv, DSV41_E_ARG, "%s: the ring store needs one token per row and a ring", what);
+    a.ring_w = const_cast<void*>(win_kv);
+  }
   const int weff = window < wp + n ? window : wp + n;
   return run_mla(what, a, (int64_t)bsz * n, weff + k, dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dsv41_sparse_mla(const void* q, const void* win_kv, const void* chunk_kv, const void* comp_kv,
+                                int64_t comp_bstride, int32_t n_comp, const float* sink, const int32_t* idx, int32_t k,
+                                void* o, int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t window,
+                                int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                                int32_t dtype, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return sparse_mla_layer("dsv41_sparse_mla", q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp, sink, idx, k, o, bsz,
+                          n, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, dtype, workspace,
+                          workspace_bytes, false, stream);
+}
+
+extern "C" int dsv41_sparse_mla_decode(const void* q, void* win_kv, const void* chunk_kv, const void* comp_kv,
+                                       int64_t comp_bstride, int32_t n_comp, const float* sink, const int32_t* idx,
+                                       int32_t k, void* o, int32_t bsz, int32_t heads, int32_t dim, int32_t window,
+                                       int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab,
+                                       int32_t rd, int32_t dtype, void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream) {
+  return sparse_mla_layer("dsv41_sparse_mla_decode", q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp, sink, idx, k,
+                          o, bsz, 1, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, dtype, workspace,
+                          workspace_bytes, true, stream);
 }
 
 extern "C" int dsv41_sparse_mla_fp8(const void* q, const void* win_kv, const void* chunk_kv, const uint8_t* comp_kv,

@@ -60,6 +60,8 @@ _SIGNATURES = {
                           _i32, _c_p, _sz, _c_p],
     "dsv41_sparse_mla": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
                          _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
+                                _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_sparse_mla_fp8": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _i64, _i32, _c_p, _c_p, _i32,
                              _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p,
                              _sz, _c_p],
@@ -444,12 +446,13 @@ def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale):
 
 
 def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_scale, window,
-               start_pos, cos=None, sin=None, rd=0, out=None, workspace=None):
+               start_pos, cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False):
     """The layer form: window ring + this chunk's KV + the owner's compressed cache, all read
     in place. comp_kv: [b, >=n_comp, d] view (or None); idx [b, n, k] int32 or None.
     workspace: a uint8 scratch tensor of at least mla_workspace_bytes(...) bytes, allocated
-    when it is omitted or too small."""
-    name = "dsv41_sparse_mla"
+    when it is omitted or too small. write_ring (one token per row): the same launch also
+    stores chunk_kv into its ring slot, as LayerCache.write_window would afterwards."""
+    name = "dsv41_sparse_mla_decode" if write_ring else "dsv41_sparse_mla"
     _gpu(name, q, win_kv, chunk_kv, comp_kv, attn_sink, idx, cos, sin, out)
     _contig(name, q, chunk_kv, attn_sink, idx)
     b, n, h, d = q.shape
@@ -486,10 +489,16 @@ def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_sca
     ws_bytes = mla_workspace_bytes(b, n, h, d, rows, q.dtype)
     if ws_bytes and (workspace is None or workspace.numel() < ws_bytes):
         workspace = _workspace(ws_bytes, q.device)
-    _call(name, _ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp_kv), comp_bstride, n_comp,
-          _ptr(attn_sink), _ptr(idx), k, _ptr(o), b, n, h, d, window, start_pos, float(softmax_scale),
-          _ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, dtype_code(q, name),
-          _ptr(workspace) if ws_bytes else None, ws_bytes, _stream(q))
+    tail = (_ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, dtype_code(q, name),
+            _ptr(workspace) if ws_bytes else None, ws_bytes, _stream(q))
+    if write_ring:
+        if n != 1 or ring is None:
+            raise ValueError(f"{name}: the ring store needs one token per row and a window ring")
+        _call(name, _ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp_kv), comp_bstride, n_comp, _ptr(attn_sink),
+              _ptr(idx), k, _ptr(o), b, h, d, window, start_pos, float(softmax_scale), *tail)
+    else:
+        _call(name, _ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp_kv), comp_bstride, n_comp, _ptr(attn_sink),
+              _ptr(idx), k, _ptr(o), b, n, h, d, window, start_pos, float(softmax_scale), *tail)
     return o
 
 

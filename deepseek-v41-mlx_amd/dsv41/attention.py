@@ -162,11 +162,15 @@ class Attention(torch.nn.Module):
                 comp, n_comp = src.comp_kv[:bsz], compress_len
 
         sink = torch.zeros_like(self.attn_sink) if self._break_sink else self.attn_sink
+        # one-token decode: the attention launch also writes the token into the ring (the slot it
+        # takes is outside the token's window); a chunk writes its ring after the attention
+        decode = n == 1
         o = _abi.sparse_mla(q, lc.win_kv, kv, comp, n_comp, sink,
                             cidx if cidx is not None and cidx.shape[-1] else None,
                             self.softmax_scale, self.window_size, start_pos, cos, sin,
-                            0 if self._break_rope_inverse else rd)
-        lc.write_window(start_pos, kv)
+                            0 if self._break_rope_inverse else rd, write_ring=decode)
+        if not decode:
+            lc.write_window(start_pos, kv)
 
         # grouped block-diagonal wo_a in fp32, then wo_b (attention.py:176-179)
         G, R = self.n_groups, self.o_lora_rank

@@ -62,9 +62,9 @@ class StackDecodeStep:
     index_k), index sources score their queries against the most recent key owner's cache
     (layers after the candidate source with its block mask applied) and select the top-k, and
     every layer attends over its window ring, this token's KV and the most recent owner's
-    comp_kv in place, then writes the token into its ring. The sharing follows the layer loop
-    of model.py:141-154: the most recent kv source, key owner, top-k selection and candidate
-    mask are handed down the stack.
+    comp_kv in place and, in the same launch, writes the token into its ring. The sharing
+    follows the layer loop of model.py:141-154: the most recent kv source, key owner, top-k
+    selection and candidate mask are handed down the stack.
 
     ``inputs[l]`` holds layer l's per-token tensors: ``q`` [b,1,H,D] (roped), ``kv`` [b,1,D]
     (the window KV after its prologue), ``sink`` [H]; index sources add ``index_q``
@@ -146,7 +146,7 @@ class StackDecodeStep:
                 if p.kv_source and emits:
                     _abi.comp_write(x["latent"], lc.comp_kv, nb - 1, p.ratio, p.cos, p.sin, a.rope_head_dim)
                 comp, n_comp, idx = kv_src.comp_kv[:b], nb, topk
+            # attention + this token's ring write in one launch
             _abi.sparse_mla(x["q"], lc.win_kv, x["kv"], comp, n_comp, x["sink"], idx, self.scale, self.window, sp,
-                            p.cos, p.sin, a.rope_head_dim, out=p.out, workspace=self.workspace)
-            lc.write_window(sp, x["kv"])
+                            p.cos, p.sin, a.rope_head_dim, out=p.out, workspace=self.workspace, write_ring=True)
         return [p.out for p in self.plan]

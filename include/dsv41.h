@@ -232,6 +232,19 @@ int dsv41_sparse_mla(const void* q, const void* win_kv, const void* chunk_kv,
                      float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
                      int32_t dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* One-token decode form of dsv41_sparse_mla (n = 1) that also performs the ring write of
+ * LayerCache.write_window, deepseek_v41_mlx/cache.py:61-67 (attention.py:131): chunk_kv's row
+ * is stored into win_kv slot start_pos % window within the same launch. That slot holds
+ * position start_pos - window, which has left the token's window, so the attention reads are
+ * unaffected; the output equals dsv41_sparse_mla's and the ring equals what the separate
+ * write produces. */
+int dsv41_sparse_mla_decode(const void* q, void* win_kv, const void* chunk_kv,
+                            const void* comp_kv, int64_t comp_bstride, int32_t n_comp,
+                            const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
+                            int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
+                            float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                            int32_t dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* dsv41_sparse_mla with the compressed source stored as fp8: the packed, lossless form of the
  * QAT values that attention.py:157-163 writes into the cache (e4m3 code times a power-of-two
  * block scale, the ue8m0 convention of fakequant.py:83-93). comp_kv holds e4m3fn bytes

@@ -486,3 +486,35 @@ def test_reference_kernel_module_seam(gpu):
         K.act_quant(dev(x), 32)
     with pytest.raises(RuntimeError):
         K.fp8_gemm()
+
+
+@pytest.mark.parametrize("dt,b,h,d,window,start,n_comp,k", [
+    ("bf16", 32, 64, 512, 128, 16383, 4096, 512),   # split lists + combine
+    ("bf16", 600, 64, 512, 128, 700, 175, 64),     # one workgroup per 64 heads, no split
+    ("bf16", 3, 16, 576, 128, 5, 1, 1),            # ring still filling
+    ("f32", 2, 4, 64, 8, 37, 9, 4),                # fp32 kernel, wrapped ring
+])
+def test_sparse_mla_decode_writes_the_ring(gpu, dt, b, h, d, window, start, n_comp, k):
+    """dsv41_sparse_mla_decode: same output as dsv41_sparse_mla, and the ring afterwards equals
+    what the separate window write produces."""
+    from dsv41 import _abi
+    rng = rng_for(f"mlad{dt}{b}{d}")
+    rd = 16 if d == 64 else 64
+    rc, rs = R.precompute_freqs_cis(rd, start + 2, 65536, 160000.0, 16.0, 32, 1)
+    q = dev(R.cast(rng.standard_normal((b, 1, h, d)).astype(F32), dt), dt)
+    win = dev(R.cast(rng.standard_normal((b, window, d)).astype(F32), dt), dt)
+    chunk = dev(R.cast(rng.standard_normal((b, 1, d)).astype(F32), dt), dt)
+    comp = dev(R.cast(rng.standard_normal((b, n_comp, d)).astype(F32), dt), dt)
+    sink = dev(rng.standard_normal(h).astype(F32))
+    cidx = np.sort(rng.integers(0, n_comp, size=(b, 1, k)), axis=-1)
+    cidx[:, :, ::5] = -1
+    wp = min(start, window)
+    idx = torch.as_tensor(np.where(cidx >= 0, cidx + wp + 1, -1).astype(np.int32)).to(gpu)
+    args = (comp, n_comp, sink, idx, d ** -0.5, window, start, dev(rc), dev(rs), rd)
+    ring_a, ring_b = win.clone(), win.clone()
+    want = _abi.sparse_mla(q, ring_a, chunk, *args)
+    _abi.window_write(ring_a, chunk, start)
+    got = _abi.sparse_mla(q, ring_b, chunk, *args, write_ring=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(ring_b, ring_a)
