@@ -49,6 +49,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-fp8", action="store_true", help="skip the fp8-cache decode line")
     p.add_argument("--no-c4", action="store_true", help="skip the 40-layer decode line")
+    p.add_argument("--no-mx", action="store_true", help="skip the MXFP4-index decode line")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--eager", action="store_true",
                    help="launch the decode kernels without HIP graphs (for counter-collecting profilers)")
@@ -233,6 +234,84 @@ def run_decode(args, torch, device):
         log(f"[bench] {name} {kern[name] * 1e3:.2f} us")
     torch.cuda.synchronize()
     return s, ms, kern, sets, cos, sin, ws, graphs
+
+
+def run_mx_decode(args, torch, device):
+    """The bs32 / 64K decode step with the index cache in MXFP4 (e2m1 codes + ue8m0 scales per
+    32 channels, 68 bytes per key instead of 256): the packed form of the fp4 fake-quantized
+    keys the indexer stores; the index query arrives in the same form from its prologue (as the
+    bf16 line's query arrives roped and quantized); scored with block-scaled fp4 MFMA.
+    Everything else as the bf16 line (same shapes, 4 rotating input sets)."""
+    from dsv41 import _abi
+    from dsv41.indexer import weight_scale
+    from dsv41.layers import precompute_freqs_cis
+
+    s = Shape(args.batch, args.ctx)
+    log(f"[bench] MXFP4-index decode B={s.B} ctx={args.ctx} nb={s.nb} K={s.K}")
+    sets = []
+    for i in range(args.sets):
+        d = make_set(s, SEED + 400 + i, device)
+        g = torch.Generator(device=device).manual_seed(SEED + 450 + i)
+        del d["ik"], d["iq"]
+        d["qc"] = torch.randint(0, 256, (s.B, 1, s.Hi, s.Di // 2), generator=g, device=device,
+                                dtype=torch.int32).to(torch.uint8)
+        d["qs"] = torch.randint(123, 132, (s.B, 1, s.Hi, s.Di // 32), generator=g, device=device,
+                                dtype=torch.int32).to(torch.uint8)
+        d["kc"] = torch.randint(0, 256, (s.B, s.nb, s.Di // 2), generator=g, device=device,
+                                dtype=torch.int32).to(torch.uint8)
+        d["ks"] = torch.randint(123, 132, (s.B, s.nb, s.Di // 32), generator=g, device=device,
+                                dtype=torch.int32).to(torch.uint8)
+        d["scores"] = torch.empty(s.B, 1, s.nb, dtype=torch.float32, device=device)
+        d["out"] = torch.empty(s.B, 1, s.H, s.D, dtype=torch.bfloat16, device=device)
+        d["ws"] = torch.empty(max(_abi.mla_workspace_bytes(s.B, 1, s.H, s.D, s.rows, torch.bfloat16), 1),
+                              dtype=torch.uint8, device=device)
+        sets.append(d)
+    cos, sin = precompute_freqs_cis(s.rd, s.start + 1, 65536, 160000.0, 16.0, 32, 1, device=device)
+    ws = weight_scale(s.Hi, s.Di, torch.bfloat16)
+
+    def f_idx(d):
+        _abi.indexer_score_mxfp4((d["qc"], d["qs"]), d["w"], ws, d["kc"], d["ks"], s.nb, s.start, s.r, out=d["scores"])
+
+    def f_topk(d):
+        d["idx"] = _abi.topk_select(d["scores"], s.K, s.start, s.r, s.wp + 1)
+
+    def f_sparse(d):
+        _abi.sparse_mla(d["q"], d["win"], d["chunk"], d["comp"], s.nb, d["sink"], d["idx"], s.D ** -0.5, s.W,
+                        s.start, cos, sin, s.rd, out=d["out"], workspace=d["ws"])
+
+    def full(d):
+        f_idx(d)
+        f_topk(d)
+        f_sparse(d)
+
+    per = len(sets)
+    reps = max(1, args.steps // per)
+    g_full = graph_of(full, sets, torch)
+    for _ in range(max(1, args.warmup // per)):
+        g_full.replay()
+    step_ms = time_graph(g_full, reps, torch) / per
+    kern, graphs = {}, [g_full]
+    for name, fn in (("indexer_score", f_idx), ("topk_select", f_topk), ("sparse_mla", f_sparse)):
+        gr = graph_of(fn, sets, torch)
+        graphs.append(gr)
+        gr.replay()
+        kern[name] = time_graph(gr, reps, torch) / per
+        log(f"[bench] mxfp4 {name} {kern[name] * 1e3:.2f} us")
+    torch.cuda.synchronize()
+    b_idx = s.B * (s.nb * (s.Di // 2 + s.Di // 32) + s.Hi * (s.Di // 2 + s.Di // 32) + s.Hi * 2 + s.nb * 4)
+    step_bytes = b_idx + s.bytes_topk() + s.bytes_sparse()
+    log(f"[bench] MXFP4-index decode step {step_ms * 1e3:.2f} us")
+    return {
+        "workload": "bs32 / 64K decode step with an MXFP4 index cache (e2m1 codes + ue8m0 block scales, 68 B per "
+                    "128-channel key) scored by block-scaled fp4 MFMA; KV caches bf16 as in the main line",
+        "step_us": step_ms * 1e3, "tokens_per_s": s.B / (step_ms * 1e-3),
+        "kernels_us": {k: v * 1e3 for k, v in kern.items()},
+        "step_algorithmic_bytes": step_bytes,
+        "hbm_GBps_step": step_bytes / (step_ms * 1e-3) / 1e9,
+        "indexer_bytes_per_launch": b_idx,
+        "indexer_GBps": b_idx / (kern["indexer_score"] * 1e-3) / 1e9,
+        "indexer_hbm_frac": b_idx / (kern["indexer_score"] * 1e-3) / 1e9 / HBM_PEAK_GBS,
+    }
 
 
 def run_prefill(torch, device):
@@ -570,6 +649,11 @@ def main():
                      "traffic_source": TRAFFIC_FILE,
                      "bytes_per_launch": s.bytes_indexer(), "avg_launch_us": kern["indexer_score"] * 1e3},
     }
+    if not args.no_mx:
+        try:
+            result["mxfp4_index_decode"] = run_mx_decode(args, torch, device)
+        except Exception as e:
+            result["mxfp4_index_decode"] = {"error": repr(e)}
     if not args.no_prefill:
         try:
             result["prefill"] = run_prefill(torch, device)

@@ -167,6 +167,124 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
   }
 }
 
+// MXFP4 keys: the index cache holds each 128-channel key as fp4 e2m1 codes (64 bytes; byte p
+// carries channels 2p and 2p+1, the even one in the low nibble) plus one ue8m0 scale byte per
+// 32 channels (4 bytes) -- the lossless packed form of the fake_quant_fp4_ue8m0 keys that
+// indexer.py:100-104 stores. The query comes in the same form (its prologue, indexer.py:119-121,
+// quantizes it), so each lane loads its A operand -- 16 code bytes and a scale of one
+// (head, 32-channel block) -- straight into registers: no staging, no barrier. Each 16-head x
+// 16-row tile is one block-scaled fp4 MFMA over all 128 channels (16x16x128, e8m0 scales per
+// 32-channel block on both operands, fp32 accumulate). The products are exact and the sums are
+// fp32, as in the bf16 kernel; the epilogue (ReLU * w, head sum, masks) is the same.
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+
+__device__ __forceinline__ f32x4 mfma_mxfp4(uint4 a, int sa, uint4 b, int sb) {
+  const i32x8 av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+  const i32x8 bv = {(int)b.x, (int)b.y, (int)b.z, (int)b.w, 0, 0, 0, 0};
+  // cbsz = blgp = 4: both operands fp4 e2m1; scale bytes in byte 0 (opsel 0)
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, f32x4{0.f, 0.f, 0.f, 0.f}, 4, 4, 0, sa, 0, sb);
+}
+
+template <int U> struct MxBatch {
+  uint4 k[U];
+  uint32_t sc[U];
+  uint32_t cf[U];
+};
+
+constexpr int kMxThreads = 512;  // 8 waves
+
+template <int HT>
+__global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
+    const uint8_t* __restrict__ qcodes, const uint8_t* __restrict__ qscales, const bf16_t* __restrict__ w_raw,
+    float w_scale,
+    const uint8_t* __restrict__ kcodes, int64_t kc_bstride, const uint8_t* __restrict__ kscales, int64_t ks_bstride,
+    const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int nb, int start_pos, int ratio,
+    int rows_per_wg) {
+  constexpr int H = HT * 16;
+  constexpr int DIM = 128;
+
+  const int qi = blockIdx.y;               // b * n + s
+  const int b = qi / n, s = qi - (qi / n) * n;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int lens = (start_pos + s + 1) / ratio;
+  const int r0 = blockIdx.x * rows_per_wg;
+  const int r1 = min(r0 + rows_per_wg, nb);
+  const int vis_end = max(r0, min(r1, lens));
+  float* out = scores + (int64_t)qi * nb;
+  for (int t = vis_end + tid; t < r1; t += kMxThreads) out[t] = -INFINITY;
+  if (vis_end <= r0) return;               // uniform: nothing visible in this row range
+
+  // lane (l16, g) of a tile loads row l16's 32-channel block g: 16 code bytes and its scale
+  const uint8_t* kcb = kcodes + (int64_t)b * kc_bstride + g * 16;
+  const uint8_t* ksb = kscales + (int64_t)b * ks_bstride;
+  const uint8_t* cb = cand ? cand + (int64_t)qi * nb : nullptr;
+  constexpr int NW = kMxThreads / 64;
+  constexpr int U = 4;
+  constexpr int NBUF = 2;
+  constexpr int STRIDE = 16 * U * NW;
+  using Batch = MxBatch<U>;
+  auto load = [&](Batch& kk, int t0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = min(t0 + 16 * u + l16, vis_end - 1);   // clamp: loads stay inside the cache
+      kk.k[u] = *reinterpret_cast<const uint4*>(kcb + (int64_t)row * (DIM / 2));
+      kk.sc[u] = *reinterpret_cast<const uint32_t*>(ksb + (int64_t)row * (DIM / 32));
+      kk.cf[u] = cb ? (uint32_t)cb[row] : 1u;
+    }
+  };
+  uint4 qa[HT];
+  int qsa[HT];
+  float wv[HT][4];
+  auto compute = [&](const Batch& kk, int t0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int sb = (int)((kk.sc[u] >> (8 * g)) & 0xFFu);
+      float part = 0.0f;
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) {
+        const f32x4 acc = mfma_mxfp4(qa[ht], qsa[ht], kk.k[u], sb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part += fmaxf(acc[i], 0.0f) * wv[ht][i];
+      }
+      part += __shfl_xor(part, 16, 64);
+      part += __shfl_xor(part, 32, 64);
+      const int row = t0 + 16 * u + l16;
+      if (g == 0 && row < vis_end) out[row] = kk.cf[u] ? part : -INFINITY;
+    }
+  };
+  int t0 = r0 + 16 * U * wave;
+  // a ring of NBUF register batches: NBUF - 1 are in flight while one is computed; the first
+  // ones go out before the query operands are loaded
+  Batch buf[NBUF];
+#pragma unroll
+  for (int j = 0; j < NBUF - 1; ++j) load(buf[j], t0 + j * STRIDE);
+  // the query's A operands: lane (l16, g) of head tile ht holds head ht*16 + l16, block g
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht) {
+    const int64_t hq = (int64_t)qi * H + ht * 16 + l16;
+    qa[ht] = *reinterpret_cast<const uint4*>(qcodes + hq * (DIM / 2) + g * 16);
+    qsa[ht] = (int)qscales[hq * (DIM / 32) + g];
+  }
+  {
+    const bf16_t* wrow = w_raw + (int64_t)qi * H;
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wrow[ht * 16 + 4 * g + i]) * w_scale);
+  }
+  if (t0 >= vis_end) return;
+  for (;;) {
+#pragma unroll
+    for (int j = 0; j < NBUF; ++j) {
+      load(buf[(j + NBUF - 1) % NBUF], t0 + (NBUF - 1) * STRIDE);
+      compute(buf[j], t0);
+      t0 += STRIDE;
+      if (t0 >= vis_end) return;
+    }
+  }
+}
+
 // fp32 path (parity configs): one thread per cache row, the query's q and w in LDS.
 __global__ __launch_bounds__(256) void indexer_score_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ w_raw, float w_scale, const float* __restrict__ kcache,
@@ -301,5 +419,39 @@ extern "C" int dsv41_indexer_score_fp8(const void* q, const void* w_raw, float w
   DSV41_IDX8_CASE(2)   // 32 heads
   DSV41_IDX8_CASE(1)
 #undef DSV41_IDX8_CASE
+  return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
+}
+
+extern "C" int dsv41_indexer_score_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
+                                         float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                                         const uint8_t* k_scales, int64_t ks_bstride, const uint8_t* candidates,
+                                         float* scores, int32_t bsz, int32_t n, int32_t heads, int32_t dim,
+                                         int32_t nb, int32_t start_pos, int32_t ratio, hipStream_t stream) {
+  const char* what = "dsv41_indexer_score_mxfp4";
+  DSV41_REQUIRE(q_codes && q_scales && w_raw && k_codes && k_scales && scores, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(bsz >= 0 && n >= 0 && heads > 0 && nb >= 0 && start_pos >= 0 && ratio > 0, DSV41_E_ARG,
+                "%s: bad sizes", what);
+  DSV41_REQUIRE(dim == 128, DSV41_E_SHAPE, "%s: MXFP4 index keys support dim 128, got %d", what, dim);
+  DSV41_REQUIRE(kc_bstride >= (int64_t)nb * (dim / 2) && ks_bstride >= (int64_t)nb * (dim / 32), DSV41_E_ARG,
+                "%s: batch strides too small", what);
+  DSV41_REQUIRE((int64_t)bsz * n < 65536, DSV41_E_ARG, "%s: bsz*n must be < 65536", what);
+  DSV41_REQUIRE(aligned16(q_codes) && aligned16(k_codes) && (reinterpret_cast<uintptr_t>(k_scales) & 3u) == 0,
+                DSV41_E_ARG, "%s: q_codes and k_codes must be 16-byte aligned, k_scales 4-byte aligned", what);
+  DSV41_REQUIRE(kc_bstride % 16 == 0 && ks_bstride % 4 == 0, DSV41_E_ARG,
+                "%s: kc_bstride must be a multiple of 16 bytes, ks_bstride of 4", what);
+  if ((int64_t)bsz * n == 0 || nb == 0) return 0;
+  int rows_per_wg = 0;
+  const dim3 grid = idx_grid((int64_t)nb * bsz * n, nb, bsz * n, &rows_per_wg);
+#define DSV41_IDXMX_CASE(HT_)                                                                                 \
+  if (heads == HT_ * 16) {                                                                                    \
+    hipLaunchKernelGGL((indexer_score_mx_kernel<HT_>), grid, dim3(kMxThreads), 0, stream, q_codes, q_scales, \
+                       (const bf16_t*)w_raw, w_scale, k_codes, kc_bstride, k_scales, ks_bstride, candidates,  \
+                       scores, n, nb, start_pos, ratio, rows_per_wg);                                        \
+    return check_launch(what);                                                                                \
+  }
+  DSV41_IDXMX_CASE(4)   // 64 heads
+  DSV41_IDXMX_CASE(2)   // 32 heads
+  DSV41_IDXMX_CASE(1)
+#undef DSV41_IDXMX_CASE
   return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
 }

@@ -9,7 +9,8 @@
 
 namespace dsv41 {
 
-enum FqKind { FQ_NONE = 0, FQ_FP8_UE8M0 = 1, FQ_FP4_UE8M0 = 2, FQ_FP4_E4M3 = 3 };
+// FQ_FP4_MX: the FQ_FP4_UE8M0 values stored packed (MXFP4 codes + ue8m0 scale bytes)
+enum FqKind { FQ_NONE = 0, FQ_FP8_UE8M0 = 1, FQ_FP4_UE8M0 = 2, FQ_FP4_E4M3 = 3, FQ_FP4_MX = 4 };
 
 struct RowArgs {
   const void* src;          // [rows, dim] contiguous
@@ -24,6 +25,10 @@ struct RowArgs {
   const float* cos_tab;
   const float* sin_tab;
   int rd, pos_base, pos_step, inverse;
+  // FQ_FP4_MX: dst takes dim/2 code bytes per row and dst2 dim/32 scale bytes; all four
+  // strides in bytes
+  uint8_t* dst2;
+  int64_t dst2_bstride, dst2_tstride;
 };
 
 template <typename T> __device__ __forceinline__ void load32(const T* p, float v[32]);
@@ -175,6 +180,16 @@ __global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
         v[2 * j + 1] = io<T>::rnd(__fadd_rn(__fmul_rn(xr, s_), __fmul_rn(xi, cs[j])));
       }
     }
+  }
+  if (FQ == FQ_FP4_MX) {
+    uint32_t cw[4];
+    const uint32_t sc = mxfp4_block(v, cw);
+    uint8_t* cdst = reinterpret_cast<uint8_t*>(a.dst) + b * a.dst_bstride + (int64_t)(a.tok_base + s) * a.dst_tstride +
+                    (int64_t)h * (a.dim / 2) + c * 16;
+    *reinterpret_cast<uint4*>(cdst) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+    a.dst2[b * a.dst2_bstride + (int64_t)(a.tok_base + s) * a.dst2_tstride + (int64_t)h * (a.dim / 32) + c] =
+        (uint8_t)sc;
+    return;
   }
   if (FQ != FQ_NONE) {
 #pragma unroll
@@ -448,6 +463,48 @@ extern "C" int dsv41_index_key_publish(const void* k_raw, void* index_k, int64_t
   a.norm_w = norm_w; a.eps = eps; a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd;
   a.pos_base = g0 * ratio; a.pos_step = ratio;
   return dispatch_rows<true, true, FQ_FP4_UE8M0, 32>(dtype, a, stream, what);
+}
+
+extern "C" int dsv41_index_key_publish_mxfp4(const void* k_raw, uint8_t* k_codes, int64_t kc_bstride,
+                                             uint8_t* k_scales, int64_t ks_bstride, const float* norm_w,
+                                             const float* cos_tab, const float* sin_tab, int32_t bsz, int32_t g,
+                                             int32_t dim, int32_t rd, int32_t g0, int32_t ratio, float eps,
+                                             int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_index_key_publish_mxfp4";
+  DSV41_REQUIRE(bsz >= 0 && g >= 0 && g0 >= 0 && ratio > 0, DSV41_E_ARG, "%s: bad sizes", what);
+  int rc = check_rows(what, k_raw, k_codes, (int64_t)bsz * g, dim, true);
+  if (rc) return rc;
+  DSV41_REQUIRE(k_scales, DSV41_E_ARG, "%s: null scale cache", what);
+  DSV41_REQUIRE(kc_bstride >= (int64_t)(g0 + g) * (dim / 2) && ks_bstride >= (int64_t)(g0 + g) * (dim / 32),
+                DSV41_E_ARG, "%s: cache too small", what);
+  DSV41_REQUIRE(kc_bstride % 16 == 0, DSV41_E_ARG, "%s: kc_bstride must be a multiple of 16 bytes", what);
+  DSV41_REQUIRE(norm_w && cos_tab && sin_tab, DSV41_E_ARG, "%s: null weight/table", what);
+  DSV41_REQUIRE(rd > 0 && rd % 2 == 0 && rd <= dim, DSV41_E_SHAPE, "%s: bad rd %d", what, rd);
+  RowArgs a{};
+  a.src = k_raw; a.dst = k_codes; a.rows = (int64_t)bsz * g; a.dim = dim; a.cpr = dim / 32;
+  a.S = g; a.H = 1; a.dst_bstride = kc_bstride; a.dst_tstride = dim / 2; a.tok_base = g0;
+  a.dst2 = k_scales; a.dst2_bstride = ks_bstride; a.dst2_tstride = dim / 32;
+  a.norm_w = norm_w; a.eps = eps; a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd;
+  a.pos_base = g0 * ratio; a.pos_step = ratio;
+  return dispatch_rows<true, true, FQ_FP4_MX, 32>(dtype, a, stream, what);
+}
+
+extern "C" int dsv41_index_q_prep_mxfp4(const void* q, uint8_t* q_codes, uint8_t* q_scales, const float* cos_tab,
+                                        const float* sin_tab, int32_t bsz, int32_t n, int32_t heads, int32_t dim,
+                                        int32_t rd, int32_t start_pos, int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_index_q_prep_mxfp4";
+  DSV41_REQUIRE(bsz >= 0 && n >= 0 && heads > 0 && start_pos >= 0, DSV41_E_ARG, "%s: bad sizes", what);
+  int rc = check_rows(what, q, q_codes, (int64_t)bsz * n * heads, dim, false);
+  if (rc) return rc;
+  DSV41_REQUIRE(q_scales && cos_tab && sin_tab, DSV41_E_ARG, "%s: null scales or rope table", what);
+  DSV41_REQUIRE(rd > 0 && rd % 2 == 0 && rd <= dim, DSV41_E_SHAPE, "%s: bad rd %d", what, rd);
+  RowArgs a{};
+  a.src = q; a.dst = q_codes; a.rows = (int64_t)bsz * n * heads; a.dim = dim; a.cpr = dim / 32;
+  a.S = n; a.H = heads;
+  a.dst_bstride = (int64_t)n * heads * (dim / 2); a.dst_tstride = (int64_t)heads * (dim / 2);
+  a.dst2 = q_scales; a.dst2_bstride = (int64_t)n * heads * (dim / 32); a.dst2_tstride = (int64_t)heads * (dim / 32);
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.pos_base = start_pos; a.pos_step = 1;
+  return dispatch_rows<false, true, FQ_FP4_MX, 32>(dtype, a, stream, what);
 }
 
 extern "C" int dsv41_index_q_prep(void* q, const float* cos_tab, const float* sin_tab, int32_t bsz, int32_t n,

@@ -48,11 +48,17 @@ _SIGNATURES = {
                          _c_p],
     "dsv41_index_key_publish": [_c_p, _c_p, _i64, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32,
                                 _i32, _f32, _i32, _c_p],
+    "dsv41_index_key_publish_mxfp4": [_c_p, _c_p, _i64, _c_p, _i64, _c_p, _c_p, _c_p, _i32, _i32, _i32,
+                                      _i32, _i32, _i32, _f32, _i32, _c_p],
     "dsv41_index_q_prep": [_c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_indexer_score": [_c_p, _c_p, _f32, _c_p, _i64, _c_p, _c_p, _i32, _i32, _i32, _i32,
                             _i32, _i32, _i32, _i32, _c_p],
     "dsv41_indexer_score_fp8": [_c_p, _c_p, _f32, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32,
                                 _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_index_q_prep_mxfp4": [_c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                 _c_p],
+    "dsv41_indexer_score_mxfp4": [_c_p, _c_p, _c_p, _f32, _c_p, _i64, _c_p, _i64, _c_p, _c_p, _i32, _i32,
+                                  _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_topk_select": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_candidate_blocks": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _i32, _i32, _c_p],
     "dsv41_sparse_mla_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32],
@@ -318,6 +324,24 @@ def index_key_publish(k_raw, index_k, g0, ratio, norm_w, cos, sin, rd, eps):
           _ptr(sin), b, g, d, rd, g0, ratio, float(eps), dtype_code(k_raw, name), _stream(k_raw))
 
 
+def index_key_publish_mxfp4(k_raw, k_codes, k_scales, g0, ratio, norm_w, cos, sin, rd, eps):
+    """index_key_publish into an MXFP4 index cache: k_codes uint8 [b, >=g0+g, d/2] e2m1 codes,
+    k_scales uint8 [b, >=g0+g, d/32] ue8m0 exponents."""
+    name = "dsv41_index_key_publish_mxfp4"
+    _gpu(name, k_raw, k_codes, k_scales, norm_w, cos, sin)
+    _contig(name, k_raw, norm_w, cos, sin)
+    b, g, d = k_raw.shape
+    if k_codes.dtype != torch.uint8 or k_codes.shape[0] < b or k_codes.shape[2] != d // 2 or k_codes.shape[1] < g0 + g:
+        raise ValueError(f"{name}: code cache {tuple(k_codes.shape)} cannot take groups {g0}..{g0 + g}")
+    if k_scales.dtype != torch.uint8 or k_scales.shape[0] < b or k_scales.shape[2] != d // 32 or k_scales.shape[1] < g0 + g:
+        raise ValueError(f"{name}: scale cache {tuple(k_scales.shape)} cannot take groups {g0}..{g0 + g}")
+    if g and (g0 + g - 1) * ratio >= cos.shape[0]:
+        raise ValueError(f"{name}: rope table too short")
+    _call(name, _ptr(k_raw), _ptr(k_codes), row_stride(k_codes, name), _ptr(k_scales), row_stride(k_scales, name),
+          _ptr(norm_w), _ptr(cos), _ptr(sin), b, g, d, rd, g0, ratio, float(eps), dtype_code(k_raw, name),
+          _stream(k_raw))
+
+
 # ---------------------------------------------------------------------------- indexer
 
 
@@ -377,6 +401,56 @@ def indexer_score_fp8(q, w_raw, w_scale, index_k8, k_scale, scale_rb, nb, start_
     cand = candidates.view(torch.uint8) if candidates is not None else None
     _call(name, _ptr(q), _ptr(w_raw), float(w_scale), _ptr(index_k8), row_stride(index_k8, name), _ptr(k_scale),
           row_stride(k_scale, name), scale_rb, _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, _stream(q))
+    return out
+
+
+def index_q_prep_mxfp4(q, cos, sin, rd, start_pos, out=None):
+    """index_q_prep into MXFP4 form: q [b,n,h,d] (read only) -> (codes uint8 [b,n,h,d/2],
+    scales uint8 [b,n,h,d/32]) of fake_quant_fp4_ue8m0(rope_tail(q))."""
+    name = "dsv41_index_q_prep_mxfp4"
+    _gpu(name, q, cos, sin)
+    _contig(name, q, cos, sin)
+    b, n, h, d = q.shape
+    if n and start_pos + n - 1 >= cos.shape[0]:
+        raise ValueError(f"{name}: rope table too short")
+    if out is None:
+        out = (torch.empty(b, n, h, d // 2, dtype=torch.uint8, device=q.device),
+               torch.empty(b, n, h, d // 32, dtype=torch.uint8, device=q.device))
+    codes, scales = out
+    if codes.shape != (b, n, h, d // 2) or scales.shape != (b, n, h, d // 32):
+        raise ValueError(f"{name}: outputs must be [{b}, {n}, {h}, {d // 2}] and [{b}, {n}, {h}, {d // 32}] uint8")
+    _gpu(name, codes, scales)
+    _contig(name, codes, scales)
+    _call(name, _ptr(q), _ptr(codes), _ptr(scales), _ptr(cos), _ptr(sin), b, n, h, d, rd, start_pos,
+          dtype_code(q, name), _stream(q))
+    return codes, scales
+
+
+def indexer_score_mxfp4(q_mx, w_raw, w_scale, k_codes, k_scales, nb, start_pos, ratio, candidates=None, out=None):
+    """indexer_score with query and keys in MXFP4 form: q_mx = (codes uint8 [b,n,h,64], scales
+    uint8 [b,n,h,4]) from index_q_prep_mxfp4; k_codes uint8 [b, >=nb, 64], k_scales uint8
+    [b, >=nb, 4]; w_raw [b,n,h] bf16."""
+    name = "dsv41_indexer_score_mxfp4"
+    q_codes, q_scales = q_mx
+    _gpu(name, q_codes, q_scales, w_raw, k_codes, k_scales, candidates, out)
+    _contig(name, q_codes, q_scales, w_raw, candidates)
+    b, n, h, d2 = q_codes.shape
+    d = d2 * 2
+    if q_codes.dtype != torch.uint8 or d != 128 or q_scales.shape != (b, n, h, d // 32) or q_scales.dtype != torch.uint8:
+        raise ValueError(f"{name}: query must be uint8 codes [b, n, h, 64] with scales [b, n, h, 4]")
+    if w_raw.shape != (b, n, h) or w_raw.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: w_raw must be bf16 [{b}, {n}, {h}]")
+    if k_codes.dtype != torch.uint8 or k_codes.shape[0] < b or k_codes.shape[2] != d // 2 or k_codes.shape[1] < nb:
+        raise ValueError(f"{name}: key codes {tuple(k_codes.shape)} {k_codes.dtype} do not match")
+    if k_scales.dtype != torch.uint8 or k_scales.shape[0] < b or k_scales.shape[2] != d // 32 or k_scales.shape[1] < nb:
+        raise ValueError(f"{name}: key scales {tuple(k_scales.shape)} do not match")
+    if candidates is not None and (candidates.shape != (b, n, nb) or candidates.dtype not in (torch.uint8, torch.bool)):
+        raise ValueError(f"{name}: candidates must be bool/uint8 [{b}, {n}, {nb}]")
+    out = torch.empty(b, n, nb, dtype=torch.float32, device=w_raw.device) if out is None else out
+    cand = candidates.view(torch.uint8) if candidates is not None else None
+    _call(name, _ptr(q_codes), _ptr(q_scales), _ptr(w_raw), float(w_scale), _ptr(k_codes), row_stride(k_codes, name),
+          _ptr(k_scales), row_stride(k_scales, name), _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio,
+          _stream(w_raw))
     return out
 
 

@@ -140,6 +140,18 @@ int dsv41_index_key_publish(const void* k_raw, void* index_k, int64_t cache_bstr
                             int32_t bsz, int32_t g, int32_t dim, int32_t rd, int32_t g0,
                             int32_t ratio, float eps, int32_t dtype, hipStream_t stream);
 
+/* dsv41_index_key_publish into an MXFP4 index cache, the lossless packed form of the same
+ * fake_quant_fp4_ue8m0 keys (indexer.py:100-104): per 32-channel block one ue8m0 scale byte
+ * (scale 2^(e-127), the block's fake-quant scale) and 16 bytes of e2m1 codes (byte p holds
+ * channels 2p, 2p+1 of the block, the even one in the low nibble). k_codes [bsz, >=g0+g, dim/2]
+ * and k_scales [bsz, >=g0+g, dim/32] bytes with kc_bstride / ks_bstride bytes per batch row.
+ * Decoding e2m1(code) * scale gives exactly dsv41_index_key_publish's values. */
+int dsv41_index_key_publish_mxfp4(const void* k_raw, uint8_t* k_codes, int64_t kc_bstride,
+                                  uint8_t* k_scales, int64_t ks_bstride, const float* norm_w,
+                                  const float* cos_tab, const float* sin_tab, int32_t bsz, int32_t g,
+                                  int32_t dim, int32_t rd, int32_t g0, int32_t ratio, float eps,
+                                  int32_t dtype, hipStream_t stream);
+
 /* ---------------------------------------------------------------- indexer --
  */
 
@@ -175,6 +187,27 @@ int dsv41_indexer_score_fp8(const void* q, const void* w_raw, float w_scale, con
                             int32_t ks_rb, const uint8_t* candidates, float* scores, int32_t bsz,
                             int32_t n, int32_t heads, int32_t dim, int32_t nb, int32_t start_pos,
                             int32_t ratio, hipStream_t stream);
+
+/* dsv41_index_q_prep writing the query in MXFP4 form (the layout of
+ * dsv41_index_key_publish_mxfp4): q [bsz, n, heads, dim] is read, not modified;
+ * q_codes [bsz, n, heads, dim/2] and q_scales [bsz, n, heads, dim/32] bytes receive
+ * fake_quant_fp4_ue8m0(rope_tail(q)) losslessly packed (indexer.py:119-121). */
+int dsv41_index_q_prep_mxfp4(const void* q, uint8_t* q_codes, uint8_t* q_scales,
+                             const float* cos_tab, const float* sin_tab, int32_t bsz, int32_t n,
+                             int32_t heads, int32_t dim, int32_t rd, int32_t start_pos,
+                             int32_t dtype, hipStream_t stream);
+
+/* dsv41_indexer_score with query and keys in MXFP4 form (dsv41_index_q_prep_mxfp4 and
+ * dsv41_index_key_publish_mxfp4 layouts; dim 128: 64 code bytes and 4 scale bytes per head
+ * or key). Each 16-head x 16-key tile is one block-scaled fp4 MFMA over the 128 channels
+ * (exact products, fp32 sums), so the scores equal dsv41_indexer_score's on the decoded
+ * values up to fp32 summation order. w_raw bf16; heads 16, 32 or 64; k_codes / k_scales with
+ * kc_bstride / ks_bstride bytes per batch row. */
+int dsv41_indexer_score_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
+                              float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                              const uint8_t* k_scales, int64_t ks_bstride, const uint8_t* candidates,
+                              float* scores, int32_t bsz, int32_t n, int32_t heads, int32_t dim,
+                              int32_t nb, int32_t start_pos, int32_t ratio, hipStream_t stream);
 
 /* Top-k selection, deepseek_v41_mlx/indexer.py:200-204: per row of scores [bsz*n, nb],
  * the k = min(topk, nb) best positions (ties -> lowest position; -0.0 == +0.0), sorted

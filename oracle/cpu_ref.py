@@ -16,6 +16,9 @@ reference repository root).
 Pinning status (what checks each function; see tests/test_oracle.py):
   * bf16/e4m3 rounding        -- torch's own casts over exhaustive grids (library routines)
   * e4m3 decode / fp8 cache   -- torch's float8_e4m3fn over all 256 codes; per-element loop
+  * MXFP4 encode / decode     -- decode(encode(x)) == fq_fp4_ue8m0(x) bit for bit (signed zeros
+                                 included) on the fake-quant known-answer inputs; every code's
+                                 value against the e2m1 grid definition
   * fake-quants (a1-a3)       -- known-answer vectors (reference test inputs, rng 3 +
                                  midpoint vector) with answers from an independent
                                  brute-force nearest-grid search; closed-form scales
@@ -169,6 +172,33 @@ def fq_fp4_ue8m0(x, block: int = 32, dtype: str = "f32") -> np.ndarray:
     s = pow2_ceil_log2(amax * FP4_MAX_INV)
     q = e2m1_round(np.clip(xb / s, -FP4_MAX, FP4_MAX)) * s
     return cast(q.reshape(shape), dtype)
+
+
+def mxfp4_encode(x):
+    """MXFP4 form of fake_quant_fp4_ue8m0(x, 32) over the last dim (d % 32 == 0): the block
+    scale s of fakequant.py:96-106 as a ue8m0 byte (log2(s) + 127) and each x/s rounded by
+    e2m1_round as a 4-bit code (sign in bit 3, magnitude index into 0, .5, 1, 1.5, 2, 3, 4, 6),
+    two per byte, the even channel in the low nibble. Returns (codes [..., d/2], scales
+    [..., d/32]) uint8."""
+    xb = _blockify(x, 32)
+    amax = np.maximum(np.abs(xb).max(axis=-1, keepdims=True), F32(6.0 * 2.0 ** -126))
+    s = pow2_ceil_log2(amax * FP4_MAX_INV)
+    r = e2m1_round(np.clip(xb / s, -FP4_MAX, FP4_MAX))
+    mag = np.searchsorted(_E2M1_LUT, np.abs(r)).astype(np.uint8)          # exact grid values
+    code = mag | (np.signbit(r).astype(np.uint8) << 3)
+    code = code.reshape(*np.shape(x)[:-1], -1)
+    codes = (code[..., 0::2] | (code[..., 1::2] << 4)).astype(np.uint8)
+    scales = ((s.view(np.uint32) >> 23) & 0xFF).astype(np.uint8)[..., 0]
+    return codes, scales
+
+
+def mxfp4_decode(codes, scales) -> np.ndarray:
+    """float32 values of an MXFP4 encoding (mxfp4_encode's layout): e2m1(code) * 2^(scale-127)."""
+    c = np.asarray(codes, np.uint8)
+    nib = np.stack([c & 15, c >> 4], axis=-1).reshape(*c.shape[:-1], -1)
+    v = _E2M1_LUT[nib & 7] * np.where(nib & 8, F32(-1.0), F32(1.0))
+    sc = np.ldexp(np.ones(np.shape(scales), F32), np.asarray(scales, np.int32) - 127).astype(F32)
+    return (v * np.repeat(sc, 32, axis=-1)).astype(F32)
 
 
 def fq_fp4_e4m3(x, block: int = 16, dtype: str = "f32") -> np.ndarray:

@@ -258,6 +258,81 @@ def test_indexer_score_fp8_keys(gpu, b, n, h, nb, start, rb):
     assert np.abs(g[fin] - want[fin]).max() <= 1e-5 * max(np.abs(want[fin]).max(), 1.0)
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_index_key_publish_mxfp4_decodes_to_the_dense_publish(gpu, dt):
+    """The MXFP4 key writer stores the dense writer's values losslessly: decoded, its bytes
+    equal dsv41_index_key_publish's output bit for bit; untouched groups stay zero."""
+    from dsv41 import _abi
+    rng = rng_for("kmx" + dt)
+    rc, rs = R.precompute_freqs_cis(64, 2048, 65536, 160000.0, 16.0, 32, 1)
+    b, g, di, g0, r = 3, 11, 128, 70, 4
+    kr = R.cast(rng.standard_normal((b, g, di)).astype(F32) * 2, dt)
+    nw = (1 + 0.1 * rng.standard_normal(di)).astype(F32)
+    dense = torch.zeros(b, 128, di, dtype=DT[dt], device=gpu)
+    _abi.index_key_publish(dev(kr, dt), dense, g0, r, dev(nw), dev(rc), dev(rs), 64, 1e-20)
+    codes = torch.zeros(b, 128, di // 2, dtype=torch.uint8, device=gpu)
+    scales = torch.zeros(b, 128, di // 32, dtype=torch.uint8, device=gpu)
+    _abi.index_key_publish_mxfp4(dev(kr, dt), codes, scales, g0, r, dev(nw), dev(rc), dev(rs), 64, 1e-20)
+    torch.cuda.synchronize()
+    c, sc = codes.cpu().numpy(), scales.cpu().numpy()
+    got = R.mxfp4_decode(c[:, g0:g0 + g], sc[:, g0:g0 + g])
+    want = to_np(dense)[:, g0:g0 + g]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert not c[:, :g0].any() and not c[:, g0 + g:].any() and not sc[:, g0 + g:].any()
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_index_q_prep_mxfp4_decodes_to_the_dense_prep(gpu, dt):
+    """The MXFP4 query prologue holds exactly dsv41_index_q_prep's values, and leaves q as is."""
+    from dsv41 import _abi
+    rng = rng_for("qmx" + dt)
+    b, n, h, d, rd, start = 2, 5, 32, 128, 64, 3000
+    rc, rs = R.precompute_freqs_cis(rd, start + n, 65536, 160000.0, 16.0, 32, 1)
+    q = dev(R.cast(rng.standard_normal((b, n, h, d)).astype(F32) * 3, dt), dt)
+    keep = q.clone()
+    codes, scales = _abi.index_q_prep_mxfp4(q, dev(rc), dev(rs), rd, start)
+    assert torch.equal(q, keep)
+    dense = _abi.index_q_prep(q.clone(), dev(rc), dev(rs), rd, start)
+    got = R.mxfp4_decode(codes.cpu().numpy(), scales.cpu().numpy())
+    assert np.array_equal(got.view(np.uint32), to_np(dense).view(np.uint32))
+
+
+@pytest.mark.parametrize("b,n,h,nb,start,use_cand", [
+    (32, 1, 64, 16384, 65536, False),    # the bs32 / 64K decode shape
+    (4, 1, 64, 4096, 16383, True),
+    (1, 96, 64, 1000, 3900, True),       # prefill chunk: causal + candidates
+    (2, 3, 32, 777, 3100, False),        # 32 index heads
+    (3, 2, 16, 333, 1300, False),
+])
+def test_indexer_score_mxfp4(gpu, b, n, h, nb, start, use_cand):
+    """MXFP4 query and keys, block-scaled fp4 MFMA: within 1e-5 of max |S| of the oracle (and of
+    the bf16 kernel) on the same fake-quantized values; masks and -inf identical."""
+    from dsv41 import _abi
+    from dsv41.indexer import weight_scale
+    rng = rng_for(f"idxmx{b}{n}{h}{nb}")
+    d, r = 128, 4
+    q = R.fq_fp4_ue8m0(rng.standard_normal((b, n, h, d)).astype(F32), 32, "bf16")
+    k = R.fq_fp4_ue8m0(rng.standard_normal((b, nb + 5, d)).astype(F32) * 3, 32, "bf16")
+    qc, qs = R.mxfp4_encode(q)
+    kc, ks = R.mxfp4_encode(k)
+    assert np.array_equal(R.mxfp4_decode(kc, ks), k) and np.array_equal(R.mxfp4_decode(qc, qs), q)
+    w_raw = R.cast(rng.standard_normal((b, n, h)).astype(F32), "bf16")
+    scale = weight_scale(h, d, torch.bfloat16)
+    cand = (rng.random((b, n, nb)) < 0.7) if use_cand else None
+    ct = torch.as_tensor(cand).to(gpu) if use_cand else None
+    t = lambda a: torch.as_tensor(a).to(gpu)   # noqa: E731
+    got = _abi.indexer_score_mxfp4((t(qc), t(qs)), dev(w_raw, "bf16"), scale, t(kc), t(ks), nb, start, r, ct)
+    w = R.cast(w_raw * scale, "bf16")
+    want = R.indexer_scores(q, k[:, :nb], w, start, r, cand)
+    g = to_np(got)
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isfinite(g), fin) and np.array_equal(g[~fin], want[~fin])
+    tol = 1e-5 * max(np.abs(want[fin]).max(), 1.0)
+    assert np.abs(g[fin] - want[fin]).max() <= tol
+    dense = to_np(_abi.indexer_score(dev(q, "bf16"), dev(w_raw, "bf16"), scale, dev(k[:, :nb], "bf16"), start, r, ct))
+    assert np.array_equal(np.isfinite(dense), fin) and np.abs(dense[fin] - g[fin]).max() <= tol
+
+
 # ------------------------------------------------------------------ top-k and candidates
 
 

@@ -140,6 +140,45 @@ def test_fake_quant_known_answers_catch_a_planted_mistake(monkeypatch):
     assert not np.array_equal(R.fq_fp4_e4m3(d["x2"], 16), d["fp4_e4m3_2"])
 
 
+@pytest.mark.parametrize("n", [0, 1, 2])
+def test_mxfp4_decodes_to_the_fp4_fake_quant_known_answers(n):
+    """MXFP4 (codes + ue8m0 bytes) is a lossless form of fake_quant_fp4_ue8m0: decoding the
+    encoding of the known-answer inputs gives the known answers bit for bit, signed zeros
+    included."""
+    d = np.load(GOLDEN)
+    x = d[f"x{n}"]
+    x = x[..., : x.shape[-1] // 32 * 32]
+    want = R.fq_fp4_ue8m0(x, 32)
+    codes, scales = R.mxfp4_encode(x)
+    got = R.mxfp4_decode(codes, scales)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the known answers themselves re-encode to the same bytes (the encoding is idempotent)
+    c2, s2 = R.mxfp4_encode(got)
+    assert np.array_equal(R.mxfp4_decode(c2, s2).view(np.uint32), want.view(np.uint32))
+
+
+def test_mxfp4_code_values_and_nibble_order():
+    """Every code's value from the e2m1 definition (sign, 2-bit exponent with bias 1,
+    1-bit mantissa, exponent 0 subnormal), the scale byte as 2^(e-127), and the packing:
+    channel 2p in the low nibble of byte p."""
+    codes = np.arange(16, dtype=np.uint8)
+    packed = (codes[0::2] | (codes[1::2] << 4)).astype(np.uint8)          # 8 bytes, 16 channels
+    packed = np.concatenate([packed, np.zeros(8, np.uint8)])[None]        # one 32-channel block
+    for e in (120, 127, 131):
+        v = R.mxfp4_decode(packed, np.array([[e]], np.uint8))[0, :16]
+        for c in range(16):
+            s, ex, m = c >> 3, (c >> 1) & 3, c & 1
+            mag = m * 0.5 if ex == 0 else (1 + m / 2) * 2.0 ** (ex - 1)
+            want = (-mag if s else mag) * 2.0 ** (e - 127)
+            assert v[c] == want and math.copysign(1.0, v[c]) == (-1.0 if s else 1.0)
+    x = np.zeros((1, 32), F32)
+    x[0, 1] = 1.0                                                         # channel 1 only
+    c, s = R.mxfp4_encode(x)
+    # amax 1 -> scale 2^ceil(log2(1/6)) = 0.25, so 1.0 is 4.0 (code 6) in the high nibble
+    assert c[0, 0] == 0x60 and not c[0, 1:].any()
+    assert s[0, 0] == 127 - 2
+
+
 def test_fake_quant_values_are_exact_in_bf16():
     """The QAT grids are representable in bf16, so a bf16 cache stores them losslessly."""
     rng = np.random.default_rng(4)
