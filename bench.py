@@ -482,12 +482,13 @@ def c4_model_args():
                      compress_rope_theta=160000.0, original_seq_len=65536, rope_factor=16.0, max_seq_len=65536)
 
 
-def c4_step_bytes(a, B, start_pos):
+def c4_step_bytes(a, B, start_pos, index_format="dense"):
     """Algorithmic HBM bytes of one 40-layer decode step (bf16 caches): per layer the sparse
     MLA gather (window + top-k rows), q and o; per index source the key stream, its queries
     and the score write; top-k score reads and index writes; the candidate mask write and
     reads; the window / latent / key writes of this token."""
     H, D, Hi, Di, W, K = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim, a.window_size, a.index_topk
+    kb = Di // 2 + Di // 32 if index_format == "mxfp4" else Di * 2   # bytes per index key / query head
     wp = min(start_pos, W)
     total = 0
     for l in range(a.n_layers):
@@ -500,24 +501,25 @@ def c4_step_bytes(a, B, start_pos):
             rows += k
             total += B * k * 4                               # index list read
             if l in a.index_source_layers:
-                total += B * (nb * Di * 2 + Hi * Di * 2 + Hi * 2 + nb * 4)   # indexer
+                total += B * (nb * kb + Hi * kb + Hi * 2 + nb * 4)          # indexer
                 total += B * (nb * 4 + k * 4)                               # top-k
                 if l == a.candidate_source_layer:
                     total += B * (nb * 4 + nb)                              # block max + mask write
                 elif 0 <= a.candidate_source_layer < l:
                     total += B * nb                                         # mask read
             if l in a.kv_source_layers:
-                total += B * D * 2 * 2 + (B * Di * 2 * 2 if l in a.index_source_layers else 0)
+                total += B * D * 2 * 2 + (B * (Di * 2 + kb) if l in a.index_source_layers else 0)
         total += B * (rows * D * 2 + 2 * H * D * 2)          # sparse MLA gather, q, o
     return total
 
 
-def run_c4(args, torch, device):
+def run_c4(args, torch, device, index_format="dense"):
     """C4: one decode token through the 40-layer stack at batch 64 and 65,536 tokens of context
     (16,384 compressed entries per sequence), kernels only: window writes, owner latent / key
     writes (the token completes a group), indexer + top-k at the 8 index sources (candidate
     blocks at layer 20, applied at 24-36), sparse MLA at every layer. Caches (about 5.7 GB)
-    exceed the Infinity Cache, so one input set suffices."""
+    exceed the Infinity Cache, so one input set suffices. index_format "mxfp4": the index
+    caches and index queries in packed fp4 form (codes + ue8m0 scales, random valid bytes)."""
     from dsv41 import _abi
     from dsv41.cache import ModelCache
     from dsv41.indexer import weight_scale
@@ -526,10 +528,15 @@ def run_c4(args, torch, device):
     a = c4_model_args()
     B, start = 64, 65535
     bf = torch.bfloat16
-    log(f"[bench] C4 40-layer decode B={B} start_pos={start}")
+    log(f"[bench] C4 40-layer decode B={B} start_pos={start} index={index_format}")
     g = torch.Generator(device=device).manual_seed(SEED + 300)
     sc = 576 ** -0.5
-    cache = ModelCache(a, B, start + 1, bf, device)
+    mx = index_format == "mxfp4"
+    cache = ModelCache(a, B, start + 1, bf, device, index_format)
+
+    def rbytes(lo, hi, *shape):
+        return torch.randint(lo, hi, shape, generator=g, device=device, dtype=torch.int32).to(torch.uint8)
+
     for lc in cache.layers:
         for t in (lc.win_kv, lc.comp_kv):
             if t is not None:
@@ -537,14 +544,20 @@ def run_c4(args, torch, device):
         if lc.index_k is not None:
             lc.index_k.copy_(torch.randn(lc.index_k.shape, generator=g, device=device))
             _abi.fq_fp4_ue8m0(lc.index_k, out=lc.index_k)
+        if lc.index_k4 is not None:
+            lc.index_k4.copy_(rbytes(0, 256, *lc.index_k4.shape))
+            lc.index_ks.copy_(rbytes(123, 132, *lc.index_ks.shape))
     H, D, Hi, Di = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim
     rn = lambda *shape: torch.randn(*shape, generator=g, device=device)   # noqa: E731
     ins = []
     for l in range(a.n_layers):
         x = dict(q=(rn(B, 1, H, D) * sc).to(bf), kv=(rn(B, 1, D) * sc).to(bf), sink=rn(H))
         if a.compress_ratio(l) and l in a.index_source_layers:
-            x.update(index_q=_abi.fq_fp4_ue8m0(rn(B, 1, Hi, Di).to(bf)), w_raw=rn(B, 1, Hi).to(bf),
-                     w_scale=weight_scale(Hi, Di, bf))
+            x.update(w_raw=rn(B, 1, Hi).to(bf), w_scale=weight_scale(Hi, Di, bf))
+            if mx:
+                x["index_q_mx"] = (rbytes(0, 256, B, 1, Hi, Di // 2), rbytes(123, 132, B, 1, Hi, Di // 32))
+            else:
+                x["index_q"] = _abi.fq_fp4_ue8m0(rn(B, 1, Hi, Di).to(bf))
         if l in a.kv_source_layers:
             x["latent"] = rn(B, 1, D).to(bf)
             if l in a.index_source_layers:
@@ -556,13 +569,14 @@ def run_c4(args, torch, device):
         gr.replay()
     reps = max(4, args.steps // 8)
     ms = time_graph(gr, reps, torch)
-    nbytes = c4_step_bytes(a, B, start)
+    nbytes = c4_step_bytes(a, B, start, index_format)
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] C4 step {ms:.3f} ms, {B / (ms * 1e-3):.0f} tokens/s, {gbs:.0f} GB/s")
     del gr
     return {
         "workload": "C4: 40-layer attention-only decode step (kernels only), B=64, 65536-token context "
-                    "(nb=16384), ratio 4, top-512; owners 2/8/14/20, index sources 2..36, candidate source 20",
+                    "(nb=16384), ratio 4, top-512; owners 2/8/14/20, index sources 2..36, candidate source 20; "
+                    f"index caches {index_format}",
         "step_ms": ms, "tokens_per_s": B / (ms * 1e-3), "steps": reps,
         "step_algorithmic_bytes": nbytes, "hbm_GBps_step": gbs, "hbm_frac_step": gbs / HBM_PEAK_GBS,
     }
@@ -670,6 +684,12 @@ def main():
         except Exception as e:
             result["c4_stack_decode"] = {"error": repr(e)}
         torch.cuda.empty_cache()
+        if not args.no_mx:
+            try:
+                result["c4_stack_decode_mxfp4_index"] = run_c4(args, torch, device, "mxfp4")
+            except Exception as e:
+                result["c4_stack_decode_mxfp4_index"] = {"error": repr(e)}
+            torch.cuda.empty_cache()
     if not args.no_cpu:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(s, sets, cos, sin, ws, args.cpu_seconds, torch)

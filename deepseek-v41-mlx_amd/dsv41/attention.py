@@ -151,7 +151,7 @@ class Attention(torch.nn.Module):
                 if compress_len == 0:
                     cidx = torch.zeros(bsz, n, 0, dtype=torch.int32, device=x.device)
                 else:
-                    index_k = shared.index_src_cache.index_k[:bsz, :compress_len]
+                    index_k = shared.index_src_cache.index_keys(bsz, compress_len)
                     cidx = self.indexer(x, qr, start_pos, offset, cos, sin, index_k, shared)
                 shared.topk_idxs = cidx
             else:

@@ -8,7 +8,10 @@ Per layer:
   ``SharedState.kv_src_cache``;
 * ``comp_state`` -- ratio > 1 owners: the fp32 kv/score rows of the open group;
 * ``index_k`` -- owners that are also index sources: the indexer's key cache, read in place
-  by every index source below them.
+  by every index source below them. With ``index_format="mxfp4"`` the keys -- fp4
+  fake-quantized by construction (indexer.py:100-104) -- are held losslessly packed instead:
+  ``index_k4`` (e2m1 codes, [b, n, Di/2] bytes) and ``index_ks`` (ue8m0 block scales,
+  [b, n, Di/32] bytes), and ``index_k`` is None.
 
 All buffers are plain torch device tensors with the reference's attribute names, so callers
 that snapshot and restore them (generate.py:18-44) work unchanged. The attention kernels
@@ -24,9 +27,14 @@ from .compressor import CompressorState
 from .config import ModelArgs
 
 
+INDEX_FORMATS = ("dense", "mxfp4")
+
+
 class LayerCache:
     def __init__(self, bsz: int, args: ModelArgs, layer_id: int, max_seq_len: int,
-                 dtype=torch.float32, device="cuda"):
+                 dtype=torch.float32, device="cuda", index_format: str = "dense"):
+        if index_format not in INDEX_FORMATS:
+            raise ValueError(f"index_format must be one of {INDEX_FORMATS}, got {index_format!r}")
         self.window = args.window_size
         self.ratio = args.compress_ratio(layer_id)
         self.is_kv_source = layer_id in args.kv_source_layers
@@ -35,14 +43,27 @@ class LayerCache:
         self.comp_kv = None
         self.comp_state = None
         self.index_k = None
+        self.index_k4 = None
+        self.index_ks = None
         if self.is_kv_source:
             n_comp = max_seq_len // self.ratio
             self.comp_kv = torch.zeros(bsz, n_comp, args.head_dim, dtype=dtype, device=device)
             if self.ratio > 1:
                 self.comp_state = CompressorState(bsz, self.ratio, args.head_dim, device)
             if layer_id in args.index_source_layers:
-                self.index_k = torch.zeros(bsz, n_comp, args.index_head_dim, dtype=dtype,
-                                           device=device)
+                di = args.index_head_dim
+                if index_format == "mxfp4":
+                    self.index_k4 = torch.zeros(bsz, n_comp, di // 2, dtype=torch.uint8, device=device)
+                    self.index_ks = torch.zeros(bsz, n_comp, di // 32, dtype=torch.uint8, device=device)
+                else:
+                    self.index_k = torch.zeros(bsz, n_comp, di, dtype=dtype, device=device)
+
+    def index_keys(self, bsz: int, n: int):
+        """The first n keys of rows [:bsz] in the form the indexer takes: a dense view, or
+        the (codes, scales) views of an MXFP4 cache."""
+        if self.index_k4 is not None:
+            return self.index_k4[:bsz, :n], self.index_ks[:bsz, :n]
+        return self.index_k[:bsz, :n]
 
     def window_chrono(self, pos: int) -> torch.Tensor:
         """The ring in chronological order: positions [pos - Wp, pos), Wp = min(pos, window)."""
@@ -58,9 +79,9 @@ class LayerCache:
 
 class ModelCache:
     def __init__(self, args: ModelArgs, bsz: int = 1, max_seq_len: int | None = None,
-                 dtype=torch.float32, device="cuda"):
+                 dtype=torch.float32, device="cuda", index_format: str = "dense"):
         self.max_seq_len = max_seq_len or min(args.max_seq_len, 4096)
         self.offset = 0
-        self.layers = [LayerCache(bsz, args, i, self.max_seq_len, dtype, device)
+        self.layers = [LayerCache(bsz, args, i, self.max_seq_len, dtype, device, index_format)
                        for i in range(args.n_layers)]
         self.engram_ids = None

@@ -71,10 +71,17 @@ class Indexer(torch.nn.Module):
         self.requires_grad_(False)
 
     def publish_keys(self, latents: torch.Tensor, start_pos: int, cos, sin, cache) -> None:
-        """Index keys of this chunk's pre-RoPE latents into cache.index_k (indexer.py:89-104)."""
+        """Index keys of this chunk's pre-RoPE latents into cache.index_k (indexer.py:89-104),
+        or packed into an MXFP4 cache (index_k4 / index_ks)."""
         g0 = start_pos // self.ratio
         rd = self.rope_head_dim
         k_raw = self.wk(latents).contiguous()
+        if cache.index_k4 is not None:
+            if fakequant.DISABLE:
+                raise ValueError("an MXFP4 index cache holds fp4 fake-quantized keys; QAT is disabled")
+            _abi.index_key_publish_mxfp4(k_raw, cache.index_k4, cache.index_ks, g0, self.ratio, self.k_norm.weight,
+                                         cos, sin, rd, self.k_norm.eps)
+            return
         if fakequant.DISABLE:
             k = _abi.rmsnorm(k_raw, self.k_norm.weight, self.k_norm.eps)
             k = _abi.rope_tail(k, rd, cos, sin, g0 * self.ratio, self.ratio)
@@ -85,21 +92,30 @@ class Indexer(torch.nn.Module):
 
     def forward(self, x: torch.Tensor, qr: torch.Tensor, start_pos: int, offset: int,
                 cos, sin, index_k: torch.Tensor, shared) -> torch.Tensor:
-        """x [b,n,dim], qr [b,n,q_lora]; index_k [b, nb, Di] (the owner's cache, in place).
+        """x [b,n,dim], qr [b,n,q_lora]; index_k [b, nb, Di] (the owner's cache, in place), or
+        the (codes, scales) views of an MXFP4 cache (LayerCache.index_keys).
         Returns [b, n, min(index_topk, nb)] int32 indices, -1 masked."""
         bsz, n, _ = x.shape
         rd = self.rope_head_dim
         q = self.wq_b(qr).view(bsz, n, self.n_heads, self.head_dim).contiguous()
-        if fakequant.DISABLE:
-            q = _abi.rope_tail(q, rd, cos, sin, start_pos, 1)
-        else:
-            _abi.index_q_prep(q, cos, sin, rd, start_pos)
         w_raw = self.weights_proj(x).contiguous()
         w_scale = weight_scale(self.n_heads, self.head_dim, x.dtype)
         cand = None
         if not self.is_candidate_source and self.uses_candidates and shared.candidates is not None:
             cand = shared.candidates
-        scores = _abi.indexer_score(q, w_raw, w_scale, index_k, start_pos, self.ratio, cand)
+        if isinstance(index_k, tuple):
+            if fakequant.DISABLE:
+                raise ValueError("an MXFP4 index cache holds fp4 fake-quantized keys; QAT is disabled")
+            codes, scales = index_k
+            q_mx = _abi.index_q_prep_mxfp4(q, cos, sin, rd, start_pos)
+            scores = _abi.indexer_score_mxfp4(q_mx, w_raw, w_scale, codes, scales, codes.shape[1], start_pos,
+                                              self.ratio, cand)
+        else:
+            if fakequant.DISABLE:
+                q = _abi.rope_tail(q, rd, cos, sin, start_pos, 1)
+            else:
+                _abi.index_q_prep(q, cos, sin, rd, start_pos)
+            scores = _abi.indexer_score(q, w_raw, w_scale, index_k, start_pos, self.ratio, cand)
         if self.is_candidate_source:
             shared.candidates = _abi.candidate_blocks(scores, self.candidate_topk_blocks,
                                                       self.candidate_block_size, None, start_pos,

@@ -68,8 +68,10 @@ class StackDecodeStep:
 
     ``inputs[l]`` holds layer l's per-token tensors: ``q`` [b,1,H,D] (roped), ``kv`` [b,1,D]
     (the window KV after its prologue), ``sink`` [H]; index sources add ``index_q``
-    [b,1,Hi,Di] (roped, fake-quantized), ``w_raw`` [b,1,Hi] and ``w_scale``; kv sources add
-    ``latent`` [b,1,D] (pre-rope); key owners add ``k_raw`` [b,1,Di] and ``k_norm`` [Di].
+    [b,1,Hi,Di] (roped, fake-quantized) -- or, when the key owners' caches are MXFP4,
+    ``index_q_mx`` (its codes and scales from dsv41_index_q_prep_mxfp4) --, ``w_raw`` [b,1,Hi]
+    and ``w_scale``; kv sources add ``latent`` [b,1,D] (pre-rope); key owners add ``k_raw``
+    [b,1,Di] and ``k_norm`` [Di].
     Outputs (``out`` per layer) and scratch are allocated once, so a step can be captured in
     a HIP graph.
     """
@@ -132,13 +134,21 @@ class StackDecodeStep:
                     kv_src = lc
                 if p.index_source:
                     if p.owns_k:
-                        if emits:
+                        if emits and lc.index_k4 is not None:
+                            _abi.index_key_publish_mxfp4(x["k_raw"], lc.index_k4, lc.index_ks, nb - 1, p.ratio,
+                                                         x["k_norm"], p.cos, p.sin, a.rope_head_dim, a.norm_eps)
+                        elif emits:
                             _abi.index_key_publish(x["k_raw"], lc.index_k, nb - 1, p.ratio, x["k_norm"],
                                                    p.cos, p.sin, a.rope_head_dim, a.norm_eps)
                         key_src = lc
                     scores = self.scores[:b * nb].view(b, 1, nb)
-                    _abi.indexer_score(x["index_q"], x["w_raw"], x["w_scale"], key_src.index_k[:b, :nb], sp,
-                                       p.ratio, cand if p.uses_candidates else None, out=scores)
+                    keys = key_src.index_keys(b, nb)
+                    c = cand if p.uses_candidates else None
+                    if isinstance(keys, tuple):
+                        _abi.indexer_score_mxfp4(x["index_q_mx"], x["w_raw"], x["w_scale"], keys[0], keys[1], nb, sp,
+                                                 p.ratio, c, out=scores)
+                    else:
+                        _abi.indexer_score(x["index_q"], x["w_raw"], x["w_scale"], keys, sp, p.ratio, c, out=scores)
                     if p.candidate_source:
                         cand = _abi.candidate_blocks(scores, a.candidate_topk_blocks, a.candidate_block_size,
                                                      None, sp, p.ratio)
