@@ -285,6 +285,126 @@ __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
   }
 }
 
+// Prefill (many queries per batch row, no candidate mask): a workgroup scores 8 consecutive
+// queries of one batch row -- one per wave -- against a range of kPfRows keys. The keys stream
+// through an LDS ring in 64-row chunks with global_load_lds, so each key row is read from HBM
+// once per workgroup instead of once per query; a wave holds its query's [heads x 128] block
+// as MFMA A operands in registers and reads every chunk's B operands from LDS. Rows are stored
+// with their 16-byte column chunks XOR-swizzled by (row % 16), so the 16 rows one B-operand read
+// touches fall in distinct banks. Per chunk a wave runs 4 tiles x 4 k-steps x HT head tiles of
+// 16x16x32 MFMA and the same epilogue as the decode kernel; queries mask rows past their own
+// causal length, rows past the group's longest one are written as -inf without compute.
+constexpr int kPfThreads = 512;        // 8 waves = 8 queries
+constexpr int kPfChunk = 64;           // key rows per ring slot (16 KB at 128 channels)
+constexpr int kPfSlots = 3;            // ring slots: 2 chunks in flight (48 KB: two workgroups per CU)
+constexpr int kPfRows = 2048;          // key rows per workgroup
+
+// (__launch_bounds__'s second argument, 4 waves per SIMD, caps VGPRs at 128 so that two
+// workgroups share a CU)
+template <int HT>
+__global__ __launch_bounds__(kPfThreads, 4) void indexer_prefill_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ w_raw, float w_scale, const bf16_t* __restrict__ kcache,
+    int64_t k_bstride, float* __restrict__ scores, int n, int nb, int start_pos, int ratio) {
+  constexpr int H = HT * 16, DIM = 128, KS = 4;
+  constexpr int ROWB = DIM * 2;                          // 256 bytes per key row
+  constexpr int CHUNKB = kPfChunk * ROWB;
+  constexpr int NL = CHUNKB / 1024 / (kPfThreads / 64);  // copies per wave per chunk
+  static_assert(NL * 1024 * (kPfThreads / 64) == CHUNKB, "a chunk splits evenly into 1 KB copies per wave");
+  __shared__ __align__(16) uint8_t ring[kPfSlots * CHUNKB];
+
+  const int groups = (n + 7) / 8;
+  const int b = blockIdx.y / groups, sg = blockIdx.y - (blockIdx.y / groups) * groups;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int s = sg * 8 + wave;
+  const bool qok = s < n;
+  const int s_last = min(sg * 8 + 7, n - 1);
+  const int lens_max = (start_pos + s_last + 1) / ratio;
+  const int lens = (start_pos + min(s, n - 1) + 1) / ratio;
+  const int r0 = blockIdx.x * kPfRows, r1 = min(r0 + kPfRows, nb);
+  const int vis_end = max(r0, min(r1, lens_max));
+  float* out = scores + ((int64_t)b * n + min(s, n - 1)) * nb;
+  // rows past the group's visibility: -inf for each of its queries
+  {
+    const int span = r1 - vis_end;
+    for (int e = tid; e < 8 * span; e += kPfThreads) {
+      const int qq = e / span, row = vis_end + (e - qq * span);
+      if (sg * 8 + qq < n) scores[((int64_t)b * n + sg * 8 + qq) * nb + row] = -INFINITY;
+    }
+  }
+  if (vis_end <= r0) return;               // uniform: nothing visible in this row range
+  const int nchunks = (vis_end - r0 + kPfChunk - 1) / kPfChunk;
+  const uint8_t* kb = reinterpret_cast<const uint8_t*>(kcache + (int64_t)b * k_bstride);
+  const uint32_t ring_base = lds_offset(ring);
+  // chunk c -> slot c % kPfSlots; copy i (1 KB = 4 rows) goes to wave i / NL. Lane l of a copy
+  // lands at row 4i + l/16, position l%16, and so loads column chunk (l%16) ^ (row % 16).
+  auto issue = [&](int c) {
+    const int slot = c % kPfSlots;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int ins = wave * NL + j;
+      const int rloc = ins * 4 + (lane >> 4);
+      const int row = min(r0 + c * kPfChunk + rloc, vis_end - 1);    // clamp: stays in the cache
+      const int col = (lane & 15) ^ (rloc & 15);
+      const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_base + (uint32_t)(slot * CHUNKB + ins * 1024));
+      dma16_vaddr(reinterpret_cast<uint64_t>(kb + (int64_t)row * ROWB + col * 16), dst);
+    }
+  };
+  issue(0);
+  // the query's A operands and head weights (an idle wave takes the last query and stores nothing)
+  const int64_t qi = (int64_t)b * n + min(s, n - 1);
+  bf16x8 qa[HT][KS];
+  float wv[HT][4];
+  {
+    const bf16_t* qrow = q + qi * H * DIM;
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qa[ht][ks] = ld_bf16x8(qrow + (ht * 16 + l16) * DIM + ks * 32 + g * 8);
+    const bf16_t* wrow = w_raw + qi * H;
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wrow[ht * 16 + 4 * g + i]) * w_scale);
+  }
+  // query, weights and chunk 0 complete (a wait the compiler sees: no drain inside the loop)
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  for (int c = 1; c < nchunks && c < kPfSlots - 1; ++c) issue(c);
+
+  for (int c = 0; c < nchunks; ++c) {
+    const int after = min(nchunks - 1 - c, kPfSlots - 2);   // younger chunks allowed in flight
+    static_assert(kPfSlots <= 4, "waits below cover at most 2 younger chunks");
+    if (after >= 2) wait_vmcnt<2 * NL>();
+    else if (after == 1) wait_vmcnt<NL>();
+    else wait_vmcnt<0>();
+    __syncthreads();                       // chunk c landed for every wave; chunk c-1 consumed
+    if (c + kPfSlots - 1 < nchunks) issue(c + kPfSlots - 1);
+    const uint8_t* buf = ring + (c % kPfSlots) * CHUNKB;
+#pragma unroll
+    for (int kt = 0; kt < kPfChunk / 16; ++kt) {
+      f32x4 acc[HT];
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) acc[ht] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const uint8_t* rowp = buf + (kt * 16 + l16) * ROWB;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 kop = ld_bf16x8(rowp + (((ks * 4 + g) ^ l16) * 16));
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) acc[ht] = mfma16x16x32(qa[ht][ks], kop, acc[ht]);
+      }
+      float part = 0.0f;
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part += fmaxf(acc[ht][i], 0.0f) * wv[ht][i];
+      part += __shfl_xor(part, 16, 64);
+      part += __shfl_xor(part, 32, 64);
+      const int row = r0 + c * kPfChunk + kt * 16 + l16;
+      if (qok && g == 0 && row < vis_end) out[row] = row < lens ? part : -INFINITY;
+    }
+  }
+}
+
 // fp32 path (parity configs): one thread per cache row, the query's q and w in LDS.
 __global__ __launch_bounds__(256) void indexer_score_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ w_raw, float w_scale, const float* __restrict__ kcache,
@@ -365,6 +485,21 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
   if (dtype != DSV41_BF16) return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported", what, dtype);
   DSV41_REQUIRE(aligned16(q) && aligned16(index_k), DSV41_E_ARG, "%s: q and index_k must be 16-byte aligned", what);
   DSV41_REQUIRE(k_bstride % 8 == 0, DSV41_E_ARG, "%s: k_bstride must be a multiple of 8", what);
+  if (n >= 8 && !candidates && dim == 128 && (heads == 64 || heads == 32 || heads == 16) &&
+      (int64_t)bsz * ((n + 7) / 8) < 65536) {
+    const dim3 pgrid((unsigned)((nb + kPfRows - 1) / kPfRows), (unsigned)(bsz * ((n + 7) / 8)));
+#define DSV41_PF_CASE(HT_)                                                                                  \
+    if (heads == HT_ * 16) {                                                                                 \
+      hipLaunchKernelGGL((indexer_prefill_kernel<HT_>), pgrid, dim3(kPfThreads), 0, stream, (const bf16_t*)q, \
+                         (const bf16_t*)w_raw, w_scale, (const bf16_t*)index_k, k_bstride, scores, n, nb,      \
+                         start_pos, ratio);                                                                  \
+      return check_launch(what);                                                                             \
+    }
+    DSV41_PF_CASE(4)
+    DSV41_PF_CASE(2)
+    DSV41_PF_CASE(1)
+#undef DSV41_PF_CASE
+  }
   int rows_per_wg = 0;
   const dim3 grid = idx_grid((int64_t)nb * bsz * n, nb, bsz * n, &rows_per_wg);
 #define DSV41_IDX_CASE(HT_, KS_)                                                                             \

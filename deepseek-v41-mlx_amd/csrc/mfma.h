@@ -57,6 +57,17 @@ __device__ __forceinline__ void dma16_vaddr(uint64_t addr, uint32_t lds) {
                : "memory", "m0");
 }
 
+// s_waitcnt immediate (gfx9 encoding): vmcnt 0, expcnt 7 and lgkmcnt 15 (no wait on those).
+// As __builtin_amdgcn_s_waitcnt it is visible to the compiler's wait-count pass.
+constexpr int kWaitVmcnt0 = 0x0F70;
+
+// Wait until at most N vector-memory operations of this wave are outstanding (asm: invisible
+// to the wait-count pass; used for the LDS copies it does not track).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // LDS byte offset of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;

@@ -141,13 +141,6 @@ constexpr int kMaxList = 2304;         // list entries one workgroup stages in L
 constexpr int kLdsBudget = 160 * 1024;
 constexpr int kMaxRing = 4;            // ring slots: steps in flight + the one computed
 
-// s_waitcnt immediate (gfx9 encoding): vmcnt 0, expcnt 7 and lgkmcnt 15 (no wait on those)
-constexpr int kWaitVmcnt0 = 0x0F70;
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 // Wait until at most `after` steps of NL copies each are still in flight (after < kMaxRing).
 template <int NL>

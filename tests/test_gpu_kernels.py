@@ -209,6 +209,9 @@ def test_index_q_prep(gpu, dt):
     ("bf16", 64, 128, 4, 1, 4096, 16383, False),    # C2-shaped decode
     ("bf16", 64, 128, 1, 96, 1000, 3900, True),    # prefill chunk, causal + candidates
     ("bf16", 32, 128, 2, 3, 777, 3100, False),     # released model's 32 index heads
+    ("bf16", 64, 128, 2, 40, 3000, 11000, False),  # prefill kernel: 8 queries per workgroup, 2 row ranges
+    ("bf16", 32, 128, 1, 13, 700, 2500, False),    # prefill kernel: a partial query group (idle waves)
+    ("bf16", 16, 128, 3, 9, 300, 100, False),      # prefill kernel: most rows past visibility
 ])
 def test_indexer_score(gpu, dt, hi, di, b, n, nb, start, use_cand):
     from dsv41 import _abi
