@@ -9,8 +9,9 @@
 
 namespace dsv41 {
 
-// FQ_FP4_MX: the FQ_FP4_UE8M0 values stored packed (MXFP4 codes + ue8m0 scale bytes)
-enum FqKind { FQ_NONE = 0, FQ_FP8_UE8M0 = 1, FQ_FP4_UE8M0 = 2, FQ_FP4_E4M3 = 3, FQ_FP4_MX = 4 };
+// FQ_FP4_MX: the FQ_FP4_UE8M0 values stored packed (MXFP4 codes + ue8m0 scale bytes);
+// FQ_FP8_PACK: the FQ_FP8_UE8M0 values stored packed (e4m3fn codes + ue8m0 scale bytes)
+enum FqKind { FQ_NONE = 0, FQ_FP8_UE8M0 = 1, FQ_FP4_UE8M0 = 2, FQ_FP4_E4M3 = 3, FQ_FP4_MX = 4, FQ_FP8_PACK = 5 };
 
 struct RowArgs {
   const void* src;          // [rows, dim] contiguous
@@ -25,8 +26,8 @@ struct RowArgs {
   const float* cos_tab;
   const float* sin_tab;
   int rd, pos_base, pos_step, inverse;
-  // FQ_FP4_MX: dst takes dim/2 code bytes per row and dst2 dim/32 scale bytes; all four
-  // strides in bytes
+  // packed stores (FQ_FP4_MX, FQ_FP8_PACK): dst takes dim/2 (fp4) or dim (fp8) code bytes per
+  // row and dst2 dim/32 scale bytes; all four strides in bytes
   uint8_t* dst2;
   int64_t dst2_bstride, dst2_tstride;
 };
@@ -189,6 +190,31 @@ __global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
     *reinterpret_cast<uint4*>(cdst) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
     a.dst2[b * a.dst2_bstride + (int64_t)(a.tok_base + s) * a.dst2_tstride + (int64_t)h * (a.dim / 32) + c] =
         (uint8_t)sc;
+    return;
+  }
+  if (FQ == FQ_FP8_PACK) {
+    // fake_quant_fp8_ue8m0's scale and rounding (fake_quant_block, FQ_FP8_UE8M0), stored as codes
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, 1e-4f);
+    const float sc = pow2_ceil_log2(amax * (float)(1.0 / 448.0));
+    const float inv = __fdiv_rn(1.0f, sc);   // exact: sc is a power of two
+    uint32_t cw[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      uint32_t word = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        word |= (uint32_t)e4m3_encode(e4m3_round(fminf(fmaxf(v[4 * w + i] * inv, -448.0f), 448.0f))) << (8 * i);
+      cw[w] = word;
+    }
+    uint8_t* cdst = reinterpret_cast<uint8_t*>(a.dst) + b * a.dst_bstride + (int64_t)(a.tok_base + s) * a.dst_tstride +
+                    (int64_t)h * a.dim + c * 32;
+    reinterpret_cast<uint4*>(cdst)[0] = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+    reinterpret_cast<uint4*>(cdst)[1] = make_uint4(cw[4], cw[5], cw[6], cw[7]);
+    a.dst2[b * a.dst2_bstride + (int64_t)(a.tok_base + s) * a.dst2_tstride + (int64_t)h * (a.dim / 32) + c] =
+        (uint8_t)((__float_as_uint(sc) >> 23) & 0xFFu);
     return;
   }
   if (FQ != FQ_NONE) {
@@ -487,6 +513,52 @@ extern "C" int dsv41_index_key_publish_mxfp4(const void* k_raw, uint8_t* k_codes
   a.norm_w = norm_w; a.eps = eps; a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd;
   a.pos_base = g0 * ratio; a.pos_step = ratio;
   return dispatch_rows<true, true, FQ_FP4_MX, 32>(dtype, a, stream, what);
+}
+
+// Shared checks and set-up of the packed fp8 writers: codes [bsz, >=g0+g, dim] and scales
+// [bsz, >=g0+g, dim/32] bytes, batch strides in bytes, one scale per 32 channels of each row.
+static int fp8_rows(const char* what, const void* src, uint8_t* codes, int64_t c_bstride, uint8_t* scales,
+                    int64_t s_bstride, int32_t bsz, int32_t g, int32_t dim, int32_t rd, int32_t g0, int32_t ratio,
+                    bool norm, RowArgs* a) {
+  DSV41_REQUIRE(bsz >= 0 && g >= 0 && g0 >= 0 && ratio > 0, DSV41_E_ARG, "%s: bad sizes", what);
+  int rc = check_rows(what, src, codes, (int64_t)bsz * g, dim, norm);
+  if (rc) return rc;
+  DSV41_REQUIRE(scales, DSV41_E_ARG, "%s: null scale cache", what);
+  DSV41_REQUIRE(c_bstride >= (int64_t)(g0 + g) * dim && s_bstride >= (int64_t)(g0 + g) * (dim / 32), DSV41_E_ARG,
+                "%s: cache too small", what);
+  DSV41_REQUIRE(c_bstride % 16 == 0, DSV41_E_ARG, "%s: code batch stride must be a multiple of 16 bytes", what);
+  DSV41_REQUIRE(rd > 0 && rd % 2 == 0 && rd <= dim, DSV41_E_SHAPE, "%s: bad rd %d", what, rd);
+  a->src = src; a->dst = codes; a->rows = (int64_t)bsz * g; a->dim = dim; a->cpr = dim / 32;
+  a->S = g; a->H = 1; a->dst_bstride = c_bstride; a->dst_tstride = dim; a->tok_base = g0;
+  a->dst2 = scales; a->dst2_bstride = s_bstride; a->dst2_tstride = dim / 32;
+  a->rd = rd; a->pos_base = g0 * ratio; a->pos_step = ratio;
+  return 0;
+}
+
+extern "C" int dsv41_comp_write_fp8(const void* latents, uint8_t* codes, int64_t c_bstride, uint8_t* scales,
+                                    int64_t s_bstride, const float* cos_tab, const float* sin_tab, int32_t bsz,
+                                    int32_t g, int32_t dim, int32_t rd, int32_t g0, int32_t ratio, int32_t dtype,
+                                    hipStream_t stream) {
+  const char* what = "dsv41_comp_write_fp8";
+  RowArgs a{};
+  int rc = fp8_rows(what, latents, codes, c_bstride, scales, s_bstride, bsz, g, dim, rd, g0, ratio, false, &a);
+  if (rc) return rc;
+  DSV41_REQUIRE(cos_tab && sin_tab, DSV41_E_ARG, "%s: null rope table", what);
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab;
+  return dispatch_rows<false, true, FQ_FP8_PACK, 32>(dtype, a, stream, what);
+}
+
+extern "C" int dsv41_index_key_publish_fp8(const void* k_raw, uint8_t* codes, int64_t c_bstride, uint8_t* scales,
+                                           int64_t s_bstride, const float* norm_w, const float* cos_tab,
+                                           const float* sin_tab, int32_t bsz, int32_t g, int32_t dim, int32_t rd,
+                                           int32_t g0, int32_t ratio, float eps, int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_index_key_publish_fp8";
+  RowArgs a{};
+  int rc = fp8_rows(what, k_raw, codes, c_bstride, scales, s_bstride, bsz, g, dim, rd, g0, ratio, true, &a);
+  if (rc) return rc;
+  DSV41_REQUIRE(norm_w && cos_tab && sin_tab, DSV41_E_ARG, "%s: null weight/table", what);
+  a.norm_w = norm_w; a.eps = eps; a.cos_tab = cos_tab; a.sin_tab = sin_tab;
+  return dispatch_rows<true, true, FQ_FP8_PACK, 32>(dtype, a, stream, what);
 }
 
 extern "C" int dsv41_index_q_prep_mxfp4(const void* q, uint8_t* q_codes, uint8_t* q_scales, const float* cos_tab,

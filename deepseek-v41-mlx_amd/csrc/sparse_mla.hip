@@ -830,14 +830,13 @@ extern "C" int dsv41_sparse_mla_decode(const void* q, void* win_kv, const void* 
                           workspace_bytes, true, stream);
 }
 
-extern "C" int dsv41_sparse_mla_fp8(const void* q, const void* win_kv, const void* chunk_kv, const uint8_t* comp_kv,
-                                    int64_t comp_bstride, int32_t n_comp, const uint8_t* comp_scale,
-                                    int64_t comp_scale_bstride, int32_t comp_scale_rb, const float* sink,
-                                    const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads,
-                                    int32_t dim, int32_t window, int32_t start_pos, float scale,
-                                    const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
-                                    size_t workspace_bytes, hipStream_t stream) {
-  const char* what = "dsv41_sparse_mla_fp8";
+static int sparse_mla_fp8_layer(const char* what, const void* q, const void* win_kv, const void* chunk_kv,
+                                const uint8_t* comp_kv, int64_t comp_bstride, int32_t n_comp,
+                                const uint8_t* comp_scale, int64_t comp_scale_bstride, int32_t comp_scale_rb,
+                                const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n,
+                                int32_t heads, int32_t dim, int32_t window, int32_t start_pos, float scale,
+                                const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
+                                size_t workspace_bytes, bool write_ring, hipStream_t stream) {
   const int wp = start_pos < window ? start_pos : window;
   DSV41_REQUIRE(q && chunk_kv && sink && o && (idx || k == 0) && (win_kv || wp == 0) &&
                     ((comp_kv && comp_scale) || n_comp == 0),
@@ -865,6 +864,34 @@ extern "C" int dsv41_sparse_mla_fp8(const void* q, const void* win_kv, const voi
   a.src.idx = idx; a.src.k = k; a.src.win_implicit = 1;
   a.m = n; a.heads = heads; a.dim = dim; a.scale = scale;
   a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.start_pos = start_pos;
+  if (write_ring) {
+    DSV41_REQUIRE(n == 1 && win_kv, DSV41_E_ARG, "%s: the ring store needs one token per row and a ring", what);
+    a.ring_w = const_cast<void*>(win_kv);
+  }
   const int weff = window < wp + n ? window : wp + n;
   return run_mla(what, a, (int64_t)bsz * n, weff + k, DSV41_BF16, workspace, workspace_bytes, stream, true);
+}
+
+extern "C" int dsv41_sparse_mla_fp8(const void* q, const void* win_kv, const void* chunk_kv, const uint8_t* comp_kv,
+                                    int64_t comp_bstride, int32_t n_comp, const uint8_t* comp_scale,
+                                    int64_t comp_scale_bstride, int32_t comp_scale_rb, const float* sink,
+                                    const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads,
+                                    int32_t dim, int32_t window, int32_t start_pos, float scale,
+                                    const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream) {
+  return sparse_mla_fp8_layer("dsv41_sparse_mla_fp8", q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp, comp_scale,
+                              comp_scale_bstride, comp_scale_rb, sink, idx, k, o, bsz, n, heads, dim, window,
+                              start_pos, scale, cos_tab, sin_tab, rd, workspace, workspace_bytes, false, stream);
+}
+
+extern "C" int dsv41_sparse_mla_fp8_decode(const void* q, void* win_kv, const void* chunk_kv, const uint8_t* comp_kv,
+                                           int64_t comp_bstride, int32_t n_comp, const uint8_t* comp_scale,
+                                           int64_t comp_scale_bstride, int32_t comp_scale_rb, const float* sink,
+                                           const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t heads,
+                                           int32_t dim, int32_t window, int32_t start_pos, float scale,
+                                           const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
+                                           size_t workspace_bytes, hipStream_t stream) {
+  return sparse_mla_fp8_layer("dsv41_sparse_mla_fp8_decode", q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp,
+                              comp_scale, comp_scale_bstride, comp_scale_rb, sink, idx, k, o, bsz, 1, heads, dim,
+                              window, start_pos, scale, cos_tab, sin_tab, rd, workspace, workspace_bytes, true, stream);
 }

@@ -71,6 +71,12 @@ _SIGNATURES = {
     "dsv41_sparse_mla_fp8": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _i64, _i32, _c_p, _c_p, _i32,
                              _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p,
                              _sz, _c_p],
+    "dsv41_sparse_mla_fp8_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _i64, _i32, _c_p, _c_p, _i32,
+                                    _c_p, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
+    "dsv41_comp_write_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                             _c_p],
+    "dsv41_index_key_publish_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32,
+                                    _i32, _f32, _i32, _c_p],
     "dsv41_version": [],
     "dsv41_last_error_string": [],
 }
@@ -322,6 +328,42 @@ def index_key_publish(k_raw, index_k, g0, ratio, norm_w, cos, sin, rd, eps):
         raise ValueError(f"{name}: rope table too short")
     _call(name, _ptr(k_raw), _ptr(index_k), row_stride(index_k, name), _ptr(norm_w), _ptr(cos),
           _ptr(sin), b, g, d, rd, g0, ratio, float(eps), dtype_code(k_raw, name), _stream(k_raw))
+
+
+def _fp8_rows(name, src, codes, scales, g0):
+    b, g, d = src.shape
+    if codes.dtype != torch.uint8 or codes.shape[0] < b or codes.shape[2] != d or codes.shape[1] < g0 + g:
+        raise ValueError(f"{name}: code cache {tuple(codes.shape)} cannot take groups {g0}..{g0 + g}")
+    if scales.dtype != torch.uint8 or scales.shape[0] < b or scales.shape[2] != d // 32 or scales.shape[1] < g0 + g:
+        raise ValueError(f"{name}: scale cache {tuple(scales.shape)} cannot take groups {g0}..{g0 + g}")
+    return b, g, d
+
+
+def comp_write_fp8(latents, codes, scales, g0, ratio, cos, sin, rd):
+    """comp_write into an fp8 cache: codes uint8 [b, >=g0+g, d] e4m3fn, scales uint8
+    [b, >=g0+g, d/32] ue8m0 (one per 32 channels of each row), values fq_fp8_ue8m0(rope(latent))."""
+    name = "dsv41_comp_write_fp8"
+    _gpu(name, latents, codes, scales, cos, sin)
+    _contig(name, latents, cos, sin)
+    b, g, d = _fp8_rows(name, latents, codes, scales, g0)
+    if g and (g0 + g - 1) * ratio >= cos.shape[0]:
+        raise ValueError(f"{name}: rope table too short")
+    _call(name, _ptr(latents), _ptr(codes), row_stride(codes, name), _ptr(scales), row_stride(scales, name), _ptr(cos),
+          _ptr(sin), b, g, d, rd, g0, ratio, dtype_code(latents, name), _stream(latents))
+
+
+def index_key_publish_fp8(k_raw, codes, scales, g0, ratio, norm_w, cos, sin, rd, eps):
+    """index_key_publish into an fp8 index cache (layout of comp_write_fp8), values
+    fq_fp8_ue8m0(rope(k_norm(k_raw)))."""
+    name = "dsv41_index_key_publish_fp8"
+    _gpu(name, k_raw, codes, scales, norm_w, cos, sin)
+    _contig(name, k_raw, norm_w, cos, sin)
+    b, g, d = _fp8_rows(name, k_raw, codes, scales, g0)
+    if g and (g0 + g - 1) * ratio >= cos.shape[0]:
+        raise ValueError(f"{name}: rope table too short")
+    _call(name, _ptr(k_raw), _ptr(codes), row_stride(codes, name), _ptr(scales), row_stride(scales, name),
+          _ptr(norm_w), _ptr(cos), _ptr(sin), b, g, d, rd, g0, ratio, float(eps), dtype_code(k_raw, name),
+          _stream(k_raw))
 
 
 def index_key_publish_mxfp4(k_raw, k_codes, k_scales, g0, ratio, norm_w, cos, sin, rd, eps):
@@ -577,11 +619,12 @@ def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_sca
 
 
 def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, attn_sink, idx, softmax_scale,
-                   window, start_pos, cos=None, sin=None, rd=0, out=None, workspace=None):
+                   window, start_pos, cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False):
     """sparse_mla with an fp8 compressed cache: comp8 uint8 [b, >=n_comp, 512] e4m3fn codes,
     comp_scale uint8 [b, >=ceil(n_comp / scale_rb), 16] ue8m0 exponents (one per 32 channels
-    for every scale_rb = 1 or 32 rows). q, the window ring, chunk and output are bf16."""
-    name = "dsv41_sparse_mla_fp8"
+    for every scale_rb = 1 or 32 rows). q, the window ring, chunk and output are bf16.
+    write_ring (one token per row): the launch also stores chunk_kv into its ring slot."""
+    name = "dsv41_sparse_mla_fp8_decode" if write_ring else "dsv41_sparse_mla_fp8"
     _gpu(name, q, win_kv, chunk_kv, comp8, comp_scale, attn_sink, idx, cos, sin, out)
     _contig(name, q, chunk_kv, attn_sink, idx)
     b, n, h, d = q.shape
@@ -625,8 +668,16 @@ def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, att
     ws_bytes = mla_workspace_bytes(b, n, h, d, rows, q.dtype)
     if ws_bytes and (workspace is None or workspace.numel() < ws_bytes):
         workspace = _workspace(ws_bytes, q.device)
-    _call(name, _ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp8), comp_bstride, n_comp, _ptr(comp_scale),
-          sc_bstride, scale_rb, _ptr(attn_sink), _ptr(idx), k, _ptr(o), b, n, h, d, window, start_pos,
-          float(softmax_scale), _ptr(cos) if rd else None, _ptr(sin) if rd else None, rd,
-          _ptr(workspace) if ws_bytes else None, ws_bytes, _stream(q))
+    tail = (_ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, _ptr(workspace) if ws_bytes else None,
+            ws_bytes, _stream(q))
+    if write_ring:
+        if n != 1 or ring is None:
+            raise ValueError(f"{name}: the ring store needs one token per row and a window ring")
+        _call(name, _ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp8), comp_bstride, n_comp, _ptr(comp_scale),
+              sc_bstride, scale_rb, _ptr(attn_sink), _ptr(idx), k, _ptr(o), b, h, d, window, start_pos,
+              float(softmax_scale), *tail)
+    else:
+        _call(name, _ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp8), comp_bstride, n_comp, _ptr(comp_scale),
+              sc_bstride, scale_rb, _ptr(attn_sink), _ptr(idx), k, _ptr(o), b, n, h, d, window, start_pos,
+              float(softmax_scale), *tail)
     return o

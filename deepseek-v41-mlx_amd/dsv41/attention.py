@@ -108,6 +108,10 @@ class Attention(torch.nn.Module):
 
     def _write_latents(self, latents, lc, g0, cos, sin):
         rd = self.rope_head_dim
+        if lc.comp_kv8 is not None:           # fp8 cache variant: fp8 QAT, stored packed
+            _abi.comp_write_fp8(latents.to(self.dtype).contiguous(), lc.comp_kv8, lc.comp_ks, g0, self.ratio, cos,
+                                sin, rd)
+            return
         lat = latents.to(lc.dtype).contiguous()
         if fakequant.DISABLE:
             lat = _abi.rope_tail(lat, rd, cos, sin, g0 * self.ratio, self.ratio)
@@ -159,16 +163,20 @@ class Attention(torch.nn.Module):
             if latents is not None:
                 self._write_latents(latents, lc, start_pos // self.ratio, cos, sin)
             if compress_len:
-                comp, n_comp = src.comp_kv[:bsz], compress_len
+                comp, n_comp = (src.comp_kv8 if src.comp_kv8 is not None else src.comp_kv)[:bsz], compress_len
 
         sink = torch.zeros_like(self.attn_sink) if self._break_sink else self.attn_sink
         # one-token decode: the attention launch also writes the token into the ring (the slot it
         # takes is outside the token's window); a chunk writes its ring after the attention
         decode = n == 1
-        o = _abi.sparse_mla(q, lc.win_kv, kv, comp, n_comp, sink,
-                            cidx if cidx is not None and cidx.shape[-1] else None,
-                            self.softmax_scale, self.window_size, start_pos, cos, sin,
-                            0 if self._break_rope_inverse else rd, write_ring=decode)
+        sel = cidx if cidx is not None and cidx.shape[-1] else None
+        rdo = 0 if self._break_rope_inverse else rd
+        if comp is not None and comp.dtype == torch.uint8:      # the fp8 cache variant
+            o = _abi.sparse_mla_fp8(q, lc.win_kv, kv, comp, src.comp_ks[:bsz], 1, n_comp, sink, sel,
+                                    self.softmax_scale, self.window_size, start_pos, cos, sin, rdo, write_ring=decode)
+        else:
+            o = _abi.sparse_mla(q, lc.win_kv, kv, comp, n_comp, sink, sel, self.softmax_scale, self.window_size,
+                                start_pos, cos, sin, rdo, write_ring=decode)
         if not decode:
             lc.write_window(start_pos, kv)
 

@@ -13,6 +13,12 @@ Per layer:
   ``index_k4`` (e2m1 codes, [b, n, Di/2] bytes) and ``index_ks`` (ue8m0 block scales,
   [b, n, Di/32] bytes), and ``index_k`` is None.
 
+``cache_format="fp8"`` is the fp8 cache variant: the compressed KV and the index keys are
+stored as e4m3fn codes with one ue8m0 scale byte per 32 channels of each row (``comp_kv8`` /
+``comp_ks``, ``index_k8`` / ``index_k8s``; ``comp_kv`` and ``index_k`` are None), written with
+fake_quant_fp8_ue8m0's formula in place of the reference's fp4 QAT at those two stores and
+dequantized in-kernel. The window ring stays in ``dtype``.
+
 All buffers are plain torch device tensors with the reference's attribute names, so callers
 that snapshot and restore them (generate.py:18-44) work unchanged. The attention kernels
 require ``dtype`` to equal the activation dtype.
@@ -28,13 +34,29 @@ from .config import ModelArgs
 
 
 INDEX_FORMATS = ("dense", "mxfp4")
+CACHE_FORMATS = ("dense", "fp8")
+
+
+class PackedKeys:
+    """Index keys of a packed cache as the indexer takes them: kind "mxfp4" or "fp8", the code
+    and scale views of rows [:bsz, :n]."""
+
+    def __init__(self, kind: str, codes: torch.Tensor, scales: torch.Tensor):
+        self.kind, self.codes, self.scales = kind, codes, scales
+
+    @property
+    def shape(self):
+        return self.codes.shape
 
 
 class LayerCache:
     def __init__(self, bsz: int, args: ModelArgs, layer_id: int, max_seq_len: int,
-                 dtype=torch.float32, device="cuda", index_format: str = "dense"):
+                 dtype=torch.float32, device="cuda", index_format: str = "dense", cache_format: str = "dense"):
         if index_format not in INDEX_FORMATS:
             raise ValueError(f"index_format must be one of {INDEX_FORMATS}, got {index_format!r}")
+        if cache_format not in CACHE_FORMATS:
+            raise ValueError(f"cache_format must be one of {CACHE_FORMATS}, got {cache_format!r}")
+        fp8 = cache_format == "fp8"
         self.window = args.window_size
         self.ratio = args.compress_ratio(layer_id)
         self.is_kv_source = layer_id in args.kv_source_layers
@@ -45,24 +67,35 @@ class LayerCache:
         self.index_k = None
         self.index_k4 = None
         self.index_ks = None
+        self.comp_kv8 = self.comp_ks = self.index_k8 = self.index_k8s = None
         if self.is_kv_source:
             n_comp = max_seq_len // self.ratio
-            self.comp_kv = torch.zeros(bsz, n_comp, args.head_dim, dtype=dtype, device=device)
+            d = args.head_dim
+            if fp8:
+                self.comp_kv8 = torch.zeros(bsz, n_comp, d, dtype=torch.uint8, device=device)
+                self.comp_ks = torch.zeros(bsz, n_comp, d // 32, dtype=torch.uint8, device=device)
+            else:
+                self.comp_kv = torch.zeros(bsz, n_comp, d, dtype=dtype, device=device)
             if self.ratio > 1:
                 self.comp_state = CompressorState(bsz, self.ratio, args.head_dim, device)
             if layer_id in args.index_source_layers:
                 di = args.index_head_dim
-                if index_format == "mxfp4":
+                if fp8:
+                    self.index_k8 = torch.zeros(bsz, n_comp, di, dtype=torch.uint8, device=device)
+                    self.index_k8s = torch.zeros(bsz, n_comp, di // 32, dtype=torch.uint8, device=device)
+                elif index_format == "mxfp4":
                     self.index_k4 = torch.zeros(bsz, n_comp, di // 2, dtype=torch.uint8, device=device)
                     self.index_ks = torch.zeros(bsz, n_comp, di // 32, dtype=torch.uint8, device=device)
                 else:
                     self.index_k = torch.zeros(bsz, n_comp, di, dtype=dtype, device=device)
 
     def index_keys(self, bsz: int, n: int):
-        """The first n keys of rows [:bsz] in the form the indexer takes: a dense view, or
-        the (codes, scales) views of an MXFP4 cache."""
+        """The first n keys of rows [:bsz] in the form the indexer takes: a dense view, or the
+        PackedKeys of an MXFP4 or fp8 cache."""
         if self.index_k4 is not None:
-            return self.index_k4[:bsz, :n], self.index_ks[:bsz, :n]
+            return PackedKeys("mxfp4", self.index_k4[:bsz, :n], self.index_ks[:bsz, :n])
+        if self.index_k8 is not None:
+            return PackedKeys("fp8", self.index_k8[:bsz, :n], self.index_k8s[:bsz, :n])
         return self.index_k[:bsz, :n]
 
     def window_chrono(self, pos: int) -> torch.Tensor:
@@ -79,9 +112,9 @@ class LayerCache:
 
 class ModelCache:
     def __init__(self, args: ModelArgs, bsz: int = 1, max_seq_len: int | None = None,
-                 dtype=torch.float32, device="cuda", index_format: str = "dense"):
+                 dtype=torch.float32, device="cuda", index_format: str = "dense", cache_format: str = "dense"):
         self.max_seq_len = max_seq_len or min(args.max_seq_len, 4096)
         self.offset = 0
-        self.layers = [LayerCache(bsz, args, i, self.max_seq_len, dtype, device, index_format)
+        self.layers = [LayerCache(bsz, args, i, self.max_seq_len, dtype, device, index_format, cache_format)
                        for i in range(args.n_layers)]
         self.engram_ids = None

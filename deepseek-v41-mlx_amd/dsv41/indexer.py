@@ -76,6 +76,10 @@ class Indexer(torch.nn.Module):
         g0 = start_pos // self.ratio
         rd = self.rope_head_dim
         k_raw = self.wk(latents).contiguous()
+        if cache.index_k8 is not None:
+            _abi.index_key_publish_fp8(k_raw, cache.index_k8, cache.index_k8s, g0, self.ratio, self.k_norm.weight,
+                                       cos, sin, rd, self.k_norm.eps)
+            return
         if cache.index_k4 is not None:
             if fakequant.DISABLE:
                 raise ValueError("an MXFP4 index cache holds fp4 fake-quantized keys; QAT is disabled")
@@ -93,7 +97,7 @@ class Indexer(torch.nn.Module):
     def forward(self, x: torch.Tensor, qr: torch.Tensor, start_pos: int, offset: int,
                 cos, sin, index_k: torch.Tensor, shared) -> torch.Tensor:
         """x [b,n,dim], qr [b,n,q_lora]; index_k [b, nb, Di] (the owner's cache, in place), or
-        the (codes, scales) views of an MXFP4 cache (LayerCache.index_keys).
+        the PackedKeys of an MXFP4 or fp8 cache (LayerCache.index_keys).
         Returns [b, n, min(index_topk, nb)] int32 indices, -1 masked."""
         bsz, n, _ = x.shape
         rd = self.rope_head_dim
@@ -103,13 +107,19 @@ class Indexer(torch.nn.Module):
         cand = None
         if not self.is_candidate_source and self.uses_candidates and shared.candidates is not None:
             cand = shared.candidates
-        if isinstance(index_k, tuple):
+        if getattr(index_k, "kind", None) == "mxfp4":
             if fakequant.DISABLE:
                 raise ValueError("an MXFP4 index cache holds fp4 fake-quantized keys; QAT is disabled")
-            codes, scales = index_k
             q_mx = _abi.index_q_prep_mxfp4(q, cos, sin, rd, start_pos)
-            scores = _abi.indexer_score_mxfp4(q_mx, w_raw, w_scale, codes, scales, codes.shape[1], start_pos,
-                                              self.ratio, cand)
+            scores = _abi.indexer_score_mxfp4(q_mx, w_raw, w_scale, index_k.codes, index_k.scales,
+                                              index_k.codes.shape[1], start_pos, self.ratio, cand)
+        elif getattr(index_k, "kind", None) == "fp8":
+            if fakequant.DISABLE:
+                q = _abi.rope_tail(q, rd, cos, sin, start_pos, 1)
+            else:
+                _abi.index_q_prep(q, cos, sin, rd, start_pos)
+            scores = _abi.indexer_score_fp8(q, w_raw, w_scale, index_k.codes, index_k.scales, 1,
+                                            index_k.codes.shape[1], start_pos, self.ratio, cand)
         else:
             if fakequant.DISABLE:
                 q = _abi.rope_tail(q, rd, cos, sin, start_pos, 1)

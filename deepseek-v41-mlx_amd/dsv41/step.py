@@ -71,7 +71,9 @@ class StackDecodeStep:
     [b,1,Hi,Di] (roped, fake-quantized) -- or, when the key owners' caches are MXFP4,
     ``index_q_mx`` (its codes and scales from dsv41_index_q_prep_mxfp4) --, ``w_raw`` [b,1,Hi]
     and ``w_scale``; kv sources add ``latent`` [b,1,D] (pre-rope); key owners add ``k_raw``
-    [b,1,Di] and ``k_norm`` [Di].
+    [b,1,Di] and ``k_norm`` [Di]. Caches may be dense, carry MXFP4 index keys, or be the fp8
+    variant (cache_format "fp8": fp8 compressed KV and index keys); each layer takes the kernels
+    that read and write its owners' format.
     Outputs (``out`` per layer) and scratch are allocated once, so a step can be captured in
     a HIP graph.
     """
@@ -134,7 +136,10 @@ class StackDecodeStep:
                     kv_src = lc
                 if p.index_source:
                     if p.owns_k:
-                        if emits and lc.index_k4 is not None:
+                        if emits and lc.index_k8 is not None:
+                            _abi.index_key_publish_fp8(x["k_raw"], lc.index_k8, lc.index_k8s, nb - 1, p.ratio,
+                                                       x["k_norm"], p.cos, p.sin, a.rope_head_dim, a.norm_eps)
+                        elif emits and lc.index_k4 is not None:
                             _abi.index_key_publish_mxfp4(x["k_raw"], lc.index_k4, lc.index_ks, nb - 1, p.ratio,
                                                          x["k_norm"], p.cos, p.sin, a.rope_head_dim, a.norm_eps)
                         elif emits:
@@ -144,19 +149,32 @@ class StackDecodeStep:
                     scores = self.scores[:b * nb].view(b, 1, nb)
                     keys = key_src.index_keys(b, nb)
                     c = cand if p.uses_candidates else None
-                    if isinstance(keys, tuple):
-                        _abi.indexer_score_mxfp4(x["index_q_mx"], x["w_raw"], x["w_scale"], keys[0], keys[1], nb, sp,
-                                                 p.ratio, c, out=scores)
+                    kind = getattr(keys, "kind", None)
+                    if kind == "mxfp4":
+                        _abi.indexer_score_mxfp4(x["index_q_mx"], x["w_raw"], x["w_scale"], keys.codes, keys.scales,
+                                                 nb, sp, p.ratio, c, out=scores)
+                    elif kind == "fp8":
+                        _abi.indexer_score_fp8(x["index_q"], x["w_raw"], x["w_scale"], keys.codes, keys.scales, 1, nb,
+                                               sp, p.ratio, c, out=scores)
                     else:
                         _abi.indexer_score(x["index_q"], x["w_raw"], x["w_scale"], keys, sp, p.ratio, c, out=scores)
                     if p.candidate_source:
                         cand = _abi.candidate_blocks(scores, a.candidate_topk_blocks, a.candidate_block_size,
                                                      None, sp, p.ratio)
                     topk = p.idx = _abi.topk_select(scores, a.index_topk, sp, p.ratio, self.offset)
-                if p.kv_source and emits:
+                if p.kv_source and emits and lc.comp_kv8 is not None:
+                    _abi.comp_write_fp8(x["latent"], lc.comp_kv8, lc.comp_ks, nb - 1, p.ratio, p.cos, p.sin,
+                                        a.rope_head_dim)
+                elif p.kv_source and emits:
                     _abi.comp_write(x["latent"], lc.comp_kv, nb - 1, p.ratio, p.cos, p.sin, a.rope_head_dim)
-                comp, n_comp, idx = kv_src.comp_kv[:b], nb, topk
+                comp, n_comp, idx = (kv_src.comp_kv8 if kv_src.comp_kv8 is not None else kv_src.comp_kv)[:b], nb, topk
             # attention + this token's ring write in one launch
-            _abi.sparse_mla(x["q"], lc.win_kv, x["kv"], comp, n_comp, x["sink"], idx, self.scale, self.window, sp,
-                            p.cos, p.sin, a.rope_head_dim, out=p.out, workspace=self.workspace, write_ring=True)
+            if comp is not None and comp.dtype == torch.uint8:
+                _abi.sparse_mla_fp8(x["q"], lc.win_kv, x["kv"], comp, kv_src.comp_ks[:b], 1, n_comp, x["sink"], idx,
+                                    self.scale, self.window, sp, p.cos, p.sin, a.rope_head_dim, out=p.out,
+                                    workspace=self.workspace, write_ring=True)
+            else:
+                _abi.sparse_mla(x["q"], lc.win_kv, x["kv"], comp, n_comp, x["sink"], idx, self.scale, self.window,
+                                sp, p.cos, p.sin, a.rope_head_dim, out=p.out, workspace=self.workspace,
+                                write_ring=True)
         return [p.out for p in self.plan]

@@ -140,6 +140,22 @@ int dsv41_index_key_publish(const void* k_raw, void* index_k, int64_t cache_bstr
                             int32_t bsz, int32_t g, int32_t dim, int32_t rd, int32_t g0,
                             int32_t ratio, float eps, int32_t dtype, hipStream_t stream);
 
+/* The writers of the fp8 cache variant: the compressed-cache write (attention.py:157-163) and
+ * the index-key publish (indexer.py:89-104) with the row's values -- rope(latent), resp.
+ * rope(k_norm(k_raw)), in dtype -- quantized by fake_quant_fp8_ue8m0's formula
+ * (fakequant.py:83-93) and stored packed: e4m3fn codes [bsz, >=g0+g, dim] and one ue8m0 scale
+ * byte per 32 channels of each row [bsz, >=g0+g, dim/32] (the scale row block 1 of
+ * dsv41_sparse_mla_fp8 / dsv41_indexer_score_fp8), batch strides in bytes. This replaces the
+ * reference's fp4 QAT at these two stores; decoding gives fake_quant_fp8_ue8m0(value). */
+int dsv41_comp_write_fp8(const void* latents, uint8_t* codes, int64_t c_bstride, uint8_t* scales,
+                         int64_t s_bstride, const float* cos_tab, const float* sin_tab, int32_t bsz,
+                         int32_t g, int32_t dim, int32_t rd, int32_t g0, int32_t ratio, int32_t dtype,
+                         hipStream_t stream);
+int dsv41_index_key_publish_fp8(const void* k_raw, uint8_t* codes, int64_t c_bstride, uint8_t* scales,
+                                int64_t s_bstride, const float* norm_w, const float* cos_tab,
+                                const float* sin_tab, int32_t bsz, int32_t g, int32_t dim, int32_t rd,
+                                int32_t g0, int32_t ratio, float eps, int32_t dtype, hipStream_t stream);
+
 /* dsv41_index_key_publish into an MXFP4 index cache, the lossless packed form of the same
  * fake_quant_fp4_ue8m0 keys (indexer.py:100-104): per 32-channel block one ue8m0 scale byte
  * (scale 2^(e-127), the block's fake-quant scale) and 16 bytes of e2m1 codes (byte p holds
@@ -294,6 +310,16 @@ int dsv41_sparse_mla_fp8(const void* q, const void* win_kv, const void* chunk_kv
                          int32_t n, int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
                          float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
                          void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* dsv41_sparse_mla_fp8 for one token per row (n = 1) that also performs the ring write of
+ * LayerCache.write_window, deepseek_v41_mlx/cache.py:61-67, as dsv41_sparse_mla_decode does. */
+int dsv41_sparse_mla_fp8_decode(const void* q, void* win_kv, const void* chunk_kv,
+                                const uint8_t* comp_kv, int64_t comp_bstride, int32_t n_comp,
+                                const uint8_t* comp_scale, int64_t comp_scale_bstride,
+                                int32_t comp_scale_rb, const float* sink, const int32_t* idx, int32_t k,
+                                void* o, int32_t bsz, int32_t heads, int32_t dim, int32_t window,
+                                int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab,
+                                int32_t rd, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

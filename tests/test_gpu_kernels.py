@@ -262,6 +262,38 @@ def test_indexer_score_fp8_keys(gpu, b, n, h, nb, start, rb):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_fp8_cache_writers(gpu, dt):
+    """The fp8-variant writers store fake_quant_fp8_ue8m0 of the roped latent (and of the normed,
+    roped key) packed: decoded, bit-equal to the GPU's own rope + fp8 fake-quant, and within the
+    fake-quant flip tolerance of the oracle; untouched rows stay zero."""
+    from dsv41 import _abi
+    rng = rng_for("w8" + dt)
+    rc, rs = R.precompute_freqs_cis(64, 2048, 65536, 160000.0, 16.0, 32, 1)
+    b, g, d, di, g0, r = 2, 7, 512, 128, 90, 4
+    pos = (g0 + np.arange(g)) * r
+    lat = R.cast(rng.standard_normal((b, g, d)).astype(F32) * 2, dt)
+    codes = torch.zeros(b, 128, d, dtype=torch.uint8, device=gpu)
+    scales = torch.zeros(b, 128, d // 32, dtype=torch.uint8, device=gpu)
+    _abi.comp_write_fp8(dev(lat, dt), codes, scales, g0, r, dev(rc), dev(rs), 64)
+    roped = _abi.rope_tail(dev(lat, dt), 64, dev(rc), dev(rs), g0 * r, r)     # positions (g0 + j) * r
+    dense = to_np(_abi.fq_fp8_ue8m0(roped))
+    torch.cuda.synchronize()
+    c, sc = codes.cpu().numpy(), scales.cpu().numpy()
+    got = R.dequant_fp8_cache(c[:, g0:g0 + g], sc[:, g0:g0 + g], 1)
+    assert np.array_equal(got.view(np.uint32), dense.view(np.uint32))
+    assert_fq_close(got, R.fq_fp8_ue8m0(R.rope_tail(lat, 64, rc[pos], rs[pos], dtype=dt), 32, dt))
+    assert not c[:, :g0].any() and not c[:, g0 + g:].any() and not sc[:, g0 + g:].any()
+    kr = R.cast(rng.standard_normal((b, g, di)).astype(F32), dt)
+    nw = (1 + 0.1 * rng.standard_normal(di)).astype(F32)
+    kc = torch.zeros(b, 128, di, dtype=torch.uint8, device=gpu)
+    ks = torch.zeros(b, 128, di // 32, dtype=torch.uint8, device=gpu)
+    _abi.index_key_publish_fp8(dev(kr, dt), kc, ks, g0, r, dev(nw), dev(rc), dev(rs), 64, 1e-20)
+    want = R.fq_fp8_ue8m0(R.rope_tail(R.rmsnorm(kr, nw, 1e-20, dt), 64, rc[pos], rs[pos], dtype=dt), 32, dt)
+    got = R.dequant_fp8_cache(kc.cpu().numpy()[:, g0:g0 + g], ks.cpu().numpy()[:, g0:g0 + g], 1)
+    assert_fq_close(got, want)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_index_key_publish_mxfp4_decodes_to_the_dense_publish(gpu, dt):
     """The MXFP4 key writer stores the dense writer's values losslessly: decoded, its bytes
     equal dsv41_index_key_publish's output bit for bit; untouched groups stay zero."""

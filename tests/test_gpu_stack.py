@@ -29,7 +29,8 @@ def _clone_cache(cache):
     c.layers = []
     for lc in cache.layers:
         n = copy.copy(lc)
-        for name in ("win_kv", "comp_kv", "index_k", "index_k4", "index_ks"):
+        for name in ("win_kv", "comp_kv", "index_k", "index_k4", "index_ks", "comp_kv8", "comp_ks", "index_k8",
+                     "index_k8s"):
             t = getattr(lc, name)
             setattr(n, name, None if t is None else t.clone())
         c.layers.append(n)
@@ -42,7 +43,8 @@ def _record_decode(stack, h, cache):
     recs = [dict() for _ in stack.layers]
     layer = [0]
     orig = {n: getattr(_abi, n) for n in ("sparse_mla", "indexer_score", "comp_write", "index_key_publish",
-                                          "indexer_score_mxfp4", "index_key_publish_mxfp4")}
+                                          "indexer_score_mxfp4", "index_key_publish_mxfp4", "sparse_mla_fp8",
+                                          "indexer_score_fp8", "comp_write_fp8", "index_key_publish_fp8")}
 
     def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, *a, **k):
         r = recs[layer[0]]
@@ -55,6 +57,26 @@ def _record_decode(stack, h, cache):
     def indexer_score(q, w_raw, w_scale, *a, **k):
         recs[layer[0]].update(index_q=q.clone(), w_raw=w_raw.clone(), w_scale=w_scale)
         return orig["indexer_score"](q, w_raw, w_scale, *a, **k)
+
+    def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, attn_sink, idx, *a, **k):
+        r = recs[layer[0]]
+        r.update(q=q.clone(), kv=chunk_kv.clone(), sink=attn_sink.clone())
+        o = orig["sparse_mla_fp8"](q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, attn_sink, idx, *a, **k)
+        r["out"] = o.clone()
+        layer[0] += 1
+        return o
+
+    def indexer_score_fp8(q, w_raw, w_scale, *a, **k):
+        recs[layer[0]].update(index_q=q.clone(), w_raw=w_raw.clone(), w_scale=w_scale)
+        return orig["indexer_score_fp8"](q, w_raw, w_scale, *a, **k)
+
+    def comp_write_fp8(latents, *a, **k):
+        recs[layer[0]]["latent"] = latents.clone()
+        return orig["comp_write_fp8"](latents, *a, **k)
+
+    def index_key_publish_fp8(k_raw, codes, scales, g0, ratio, norm_w, *a, **k):
+        recs[layer[0]].update(k_raw=k_raw.clone(), k_norm=norm_w.clone())
+        return orig["index_key_publish_fp8"](k_raw, codes, scales, g0, ratio, norm_w, *a, **k)
 
     def indexer_score_mxfp4(q_mx, w_raw, w_scale, *a, **k):
         recs[layer[0]].update(index_q_mx=tuple(t.clone() for t in q_mx), w_raw=w_raw.clone(), w_scale=w_scale)
@@ -74,7 +96,9 @@ def _record_decode(stack, h, cache):
 
     for n, f in (("sparse_mla", sparse_mla), ("indexer_score", indexer_score), ("comp_write", comp_write),
                  ("index_key_publish", index_key_publish), ("indexer_score_mxfp4", indexer_score_mxfp4),
-                 ("index_key_publish_mxfp4", index_key_publish_mxfp4)):
+                 ("index_key_publish_mxfp4", index_key_publish_mxfp4), ("sparse_mla_fp8", sparse_mla_fp8),
+                 ("indexer_score_fp8", indexer_score_fp8), ("comp_write_fp8", comp_write_fp8),
+                 ("index_key_publish_fp8", index_key_publish_fp8)):
         setattr(_abi, n, f)
     try:
         stack(h, cache)
@@ -85,21 +109,27 @@ def _record_decode(stack, h, cache):
     return recs
 
 
-@pytest.mark.parametrize("index_format", ["dense", "mxfp4"])
+@pytest.mark.parametrize("index_format", ["dense", "mxfp4", "fp8"])
 def test_stack_step_reproduces_attention_stack(gpu, index_format):
     """Toy C4 topology in bf16: 39 prefill tokens, then the decode token at position 39, which
-    completes group 9 (owners write a latent and a key); dense or MXFP4 index caches (the
-    latter with 128-channel index keys, the only width its kernels take)."""
+    completes group 9 (owners write a latent and a key); dense or MXFP4 index caches, or the
+    fp8 cache variant (fp8 compressed KV and index keys). The packed formats use the widths
+    their kernels take (128-channel index keys; fp8 latents of 512)."""
     from dsv41.model import AttentionStack
     from dsv41.step import StackDecodeStep
     cfg = dict(C4_TOY, index_head_dim=128) if index_format == "mxfp4" else C4_TOY
+    if index_format == "fp8":
+        cfg = dict(C4_TOY, index_head_dim=128, head_dim=512, rope_head_dim=64)
     a = args(cfg)
     st = AttentionStack(model_args(cfg), torch.bfloat16, gpu)
     load_stack(st, R.make_params(a, SEED_BASE + 40, "bf16"))
     rng = np.random.default_rng(SEED_BASE + 40)
     b, T = 2, 40
     h = torch.from_numpy(rng.standard_normal((b, T, a.dim)).astype(F32)).to(gpu).to(torch.bfloat16)
-    cache = st.make_cache(b, a.max_seq_len, index_format)
+    if index_format == "fp8":
+        cache = st.make_cache(b, a.max_seq_len, cache_format="fp8")
+    else:
+        cache = st.make_cache(b, a.max_seq_len, index_format)
     st(h[:, :T - 1], cache)
     before = _clone_cache(cache)
     recs = _record_decode(st, h[:, T - 1:], cache)
@@ -109,7 +139,8 @@ def test_stack_step_reproduces_attention_stack(gpu, index_format):
     for l, (o, r) in enumerate(zip(outs, recs)):
         assert torch.equal(o, r["out"]), f"layer {l} output"
     for l, (g, w) in enumerate(zip(before.layers, cache.layers)):
-        for name in ("win_kv", "comp_kv", "index_k", "index_k4", "index_ks"):
+        for name in ("win_kv", "comp_kv", "index_k", "index_k4", "index_ks", "comp_kv8", "comp_ks", "index_k8",
+                     "index_k8s"):
             x, y = getattr(g, name), getattr(w, name)
             assert (x is None) == (y is None)
             if x is not None:
