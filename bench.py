@@ -470,25 +470,31 @@ def run_fp8_decode(args, torch, device):
     }
 
 
-def c4_model_args():
+def c4_model_args(**over):
     """The 40-layer attention-only stack: layers 0-1 window only, ratio 4 elsewhere; owners
     2/8/14/20; index sources 2/8/14/20/24/28/32/36 (24-36 score against layer 20's keys under
     its candidate mask: blocks of 8, top 2,048 blocks); 64 heads x 512, indexer 64 x 128, top-512."""
     from dsv41.config import ModelArgs
-    return ModelArgs(n_layers=40, compress_ratios=(0, 0) + (4,) * 38, kv_source_layers=(2, 8, 14, 20),
-                     index_source_layers=(2, 8, 14, 20, 24, 28, 32, 36), candidate_source_layer=20,
-                     candidate_topk_blocks=2048, candidate_block_size=8, index_n_heads=64, index_head_dim=128,
-                     index_topk=512, window_size=128, n_heads=64, head_dim=512, rope_head_dim=64,
-                     compress_rope_theta=160000.0, original_seq_len=65536, rope_factor=16.0, max_seq_len=65536)
+    cfg = dict(n_layers=40, compress_ratios=(0, 0) + (4,) * 38, kv_source_layers=(2, 8, 14, 20),
+               index_source_layers=(2, 8, 14, 20, 24, 28, 32, 36), candidate_source_layer=20,
+               candidate_topk_blocks=2048, candidate_block_size=8, index_n_heads=64, index_head_dim=128,
+               index_topk=512, window_size=128, n_heads=64, head_dim=512, rope_head_dim=64,
+               compress_rope_theta=160000.0, original_seq_len=65536, rope_factor=16.0, max_seq_len=65536)
+    cfg.update(over)
+    return ModelArgs(**cfg)
 
 
 def c4_step_bytes(a, B, start_pos, index_format="dense"):
+    """index_format "dense", "mxfp4" (packed index keys) or "fp8" (the fp8 cache variant:
+    e4m3 + ue8m0 per 32 channels for the compressed rows and the index keys)."""
     """Algorithmic HBM bytes of one 40-layer decode step (bf16 caches): per layer the sparse
     MLA gather (window + top-k rows), q and o; per index source the key stream, its queries
     and the score write; top-k score reads and index writes; the candidate mask write and
     reads; the window / latent / key writes of this token."""
     H, D, Hi, Di, W, K = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim, a.window_size, a.index_topk
-    kb = Di // 2 + Di // 32 if index_format == "mxfp4" else Di * 2   # bytes per index key / query head
+    kb = {"mxfp4": Di // 2 + Di // 32, "fp8": Di + Di // 32}.get(index_format, Di * 2)   # per index key
+    qb = Di // 2 + Di // 32 if index_format == "mxfp4" else Di * 2   # per index-query head
+    cb = D + D // 32 if index_format == "fp8" else D * 2              # per compressed KV row
     wp = min(start_pos, W)
     total = 0
     for l in range(a.n_layers):
@@ -501,19 +507,22 @@ def c4_step_bytes(a, B, start_pos, index_format="dense"):
             rows += k
             total += B * k * 4                               # index list read
             if l in a.index_source_layers:
-                total += B * (nb * kb + Hi * kb + Hi * 2 + nb * 4)          # indexer
+                total += B * (nb * kb + Hi * qb + Hi * 2 + nb * 4)          # indexer
                 total += B * (nb * 4 + k * 4)                               # top-k
                 if l == a.candidate_source_layer:
                     total += B * (nb * 4 + nb)                              # block max + mask write
                 elif 0 <= a.candidate_source_layer < l:
                     total += B * nb                                         # mask read
             if l in a.kv_source_layers:
-                total += B * D * 2 * 2 + (B * (Di * 2 + kb) if l in a.index_source_layers else 0)
-        total += B * (rows * D * 2 + 2 * H * D * 2)          # sparse MLA gather, q, o
+                total += B * (D * 2 + cb) + (B * (Di * 2 + kb) if l in a.index_source_layers else 0)
+            total += B * (rows - k) * D * 2 + B * k * cb     # sparse MLA gather: window rows + selected rows
+        else:
+            total += B * rows * D * 2
+        total += B * 2 * H * D * 2                           # q, o
     return total
 
 
-def run_c4(args, torch, device, index_format="dense"):
+def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=512):
     """C4: one decode token through the 40-layer stack at batch 64 and 65,536 tokens of context
     (16,384 compressed entries per sequence), kernels only: window writes, owner latent / key
     writes (the token completes a group), indexer + top-k at the 8 index sources (candidate
@@ -525,14 +534,15 @@ def run_c4(args, torch, device, index_format="dense"):
     from dsv41.indexer import weight_scale
     from dsv41.step import StackDecodeStep
 
-    a = c4_model_args()
-    B, start = 64, 65535
+    a = c4_model_args(index_topk=topk, max_seq_len=start + 1)
     bf = torch.bfloat16
-    log(f"[bench] C4 40-layer decode B={B} start_pos={start} index={index_format}")
+    log(f"[bench] 40-layer decode B={B} start_pos={start} top-{topk} index={index_format}")
     g = torch.Generator(device=device).manual_seed(SEED + 300)
     sc = 576 ** -0.5
     mx = index_format == "mxfp4"
-    cache = ModelCache(a, B, start + 1, bf, device, index_format)
+    fp8 = index_format == "fp8"
+    cache = (ModelCache(a, B, start + 1, bf, device, cache_format="fp8") if fp8
+             else ModelCache(a, B, start + 1, bf, device, index_format))
 
     def rbytes(lo, hi, *shape):
         return torch.randint(lo, hi, shape, generator=g, device=device, dtype=torch.int32).to(torch.uint8)
@@ -547,6 +557,11 @@ def run_c4(args, torch, device, index_format="dense"):
         if lc.index_k4 is not None:
             lc.index_k4.copy_(rbytes(0, 256, *lc.index_k4.shape))
             lc.index_ks.copy_(rbytes(123, 132, *lc.index_ks.shape))
+        for codes, scales in ((lc.comp_kv8, lc.comp_ks), (lc.index_k8, lc.index_k8s)):
+            if codes is not None:                  # e4m3 codes without the two NaN patterns
+                c = rbytes(0, 256, *codes.shape)
+                codes.copy_(torch.where((c & 0x7F) == 0x7F, c ^ 1, c))
+                scales.copy_(rbytes(123, 132, *scales.shape))
     H, D, Hi, Di = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim
     rn = lambda *shape: torch.randn(*shape, generator=g, device=device)   # noqa: E731
     ins = []
@@ -573,10 +588,12 @@ def run_c4(args, torch, device, index_format="dense"):
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] C4 step {ms:.3f} ms, {B / (ms * 1e-3):.0f} tokens/s, {gbs:.0f} GB/s")
     del gr
+    name = "C5" if fp8 else "C4"
     return {
-        "workload": "C4: 40-layer attention-only decode step (kernels only), B=64, 65536-token context "
-                    "(nb=16384), ratio 4, top-512; owners 2/8/14/20, index sources 2..36, candidate source 20; "
-                    f"index caches {index_format}",
+        "workload": f"{name}: 40-layer attention-only decode step (kernels only), B={B}, {start + 1}-token context "
+                    f"(nb={(start + 1) // 4}), ratio 4, top-{topk}; owners 2/8/14/20, index sources 2..36, candidate "
+                    f"source 20; " + ("fp8 caches (e4m3 + ue8m0 per 32 channels of each row) for compressed KV and "
+                                      "index keys, window ring bf16" if fp8 else f"index caches {index_format}"),
         "step_ms": ms, "tokens_per_s": B / (ms * 1e-3), "steps": reps,
         "step_algorithmic_bytes": nbytes, "hbm_GBps_step": gbs, "hbm_frac_step": gbs / HBM_PEAK_GBS,
     }
@@ -689,6 +706,12 @@ def main():
                 result["c4_stack_decode_mxfp4_index"] = run_c4(args, torch, device, "mxfp4")
             except Exception as e:
                 result["c4_stack_decode_mxfp4_index"] = {"error": repr(e)}
+            torch.cuda.empty_cache()
+        if not args.no_fp8:
+            try:
+                result["c5_stack_decode_fp8"] = run_c4(args, torch, device, "fp8", B=16, start=131071, topk=1024)
+            except Exception as e:
+                result["c5_stack_decode_fp8"] = {"error": repr(e)}
             torch.cuda.empty_cache()
     if not args.no_cpu:
         log("[bench] cpu baseline")
