@@ -142,27 +142,6 @@ __device__ __forceinline__ uint32_t mxfp4_block(const float* v, uint32_t codes[4
   return (__float_as_uint(s) >> 23) & 0xFFu;
 }
 
-// mxfp4_block split over an adjacent lane pair (lanes 2i, 2i+1 of a wave): each lane holds 16
-// of the block's 32 values (the even lane the first half) and writes their codes into cw[2];
-// the block maximum is exchanged across the pair, so both return the same scale byte.
-__device__ __forceinline__ uint32_t mxfp4_half_block(const float* v, uint32_t cw[2]) {
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  amax = fmaxf(amax, (float)(6.0 * 1.1754943508222875e-38));  // 6 * 2^-126
-  const float s = pow2_ceil_log2(amax * (float)(1.0 / 6.0));
-  const float inv = __fdiv_rn(1.0f, s);                       // exact: s is a power of two
-#pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    uint32_t c = 0u;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) c |= e2m1_code(fminf(fmaxf(v[8 * w + i] * inv, -6.0f), 6.0f)) << (4 * i);
-    cw[w] = c;
-  }
-  return (__float_as_uint(s) >> 23) & 0xFFu;
-}
-
 // ------------------------------------------------------------------ wave helpers
 
 __device__ __forceinline__ float wave_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }

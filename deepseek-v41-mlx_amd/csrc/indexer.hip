@@ -111,8 +111,7 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
       for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
         for (int i = 0; i < 4; ++i) part += fmaxf(acc[ht][i], 0.0f) * wv[ht][i];
-      part += __shfl_xor(part, 16, 64);
-      part += __shfl_xor(part, 32, 64);
+      part = sum_rows4(part);
       const int row = tb + l16;
       if (g == 0 && row < vis_end) {
         out[row] = kk.cf[u] ? part : -INFINITY;
@@ -247,8 +246,7 @@ __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) part += fmaxf(acc[i], 0.0f) * wv[ht][i];
       }
-      part += __shfl_xor(part, 16, 64);
-      part += __shfl_xor(part, 32, 64);
+      part = sum_rows4(part);
       const int row = t0 + 16 * u + l16;
       if (g == 0 && row < vis_end) out[row] = kk.cf[u] ? part : -INFINITY;
     }
@@ -397,8 +395,7 @@ __global__ __launch_bounds__(kPfThreads, 4) void indexer_prefill_kernel(
       for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
         for (int i = 0; i < 4; ++i) part += fmaxf(acc[ht][i], 0.0f) * wv[ht][i];
-      part += __shfl_xor(part, 16, 64);
-      part += __shfl_xor(part, 32, 64);
+      part = sum_rows4(part);
       const int row = r0 + c * kPfChunk + kt * 16 + l16;
       if (qok && g == 0 && row < vis_end) out[row] = row < lens ? part : -INFINITY;
     }

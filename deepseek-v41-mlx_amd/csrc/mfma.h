@@ -68,6 +68,20 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Sum of v over the four 16-lane rows of the wave (lanes l, l^16, l^32, l^48), in every lane:
+// (v[l] + v[l^16]) + (v[l^32] + v[l^48]), the additions of v + shfl_xor(v, 16) followed by
+// + shfl_xor(., 32), but with gfx950's row-swap permutes (VALU) instead of LDS-routed shuffles.
+// permlane16_swap(x, x) returns (x[l], x[l^16]) in row-pair order and permlane32_swap(x, x)
+// (x[l], x[l^32]) (checked lane by lane on the hardware).
+__device__ __forceinline__ float sum_rows4(float v) {
+  const uint32_t b = __float_as_uint(v);
+  const auto s16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  const float y = __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
+  const uint32_t c = __float_as_uint(y);
+  const auto s32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+  return __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+}
+
 // LDS byte offset of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
