@@ -166,6 +166,130 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
   }
 }
 
+// bf16 keys of 128 channels, the decode shape (few queries, long cache): the same scores as
+// indexer_score_bf16_kernel, with the key stream moved by LDS copies. Wave w of the workgroup
+// takes 16-row tiles w, w + 8, w + 16, ... of the row range; each tile is four 1 KB
+// global_load_lds copies (4 whole rows each, non-temporal) into the wave's private ring of
+// kDecSlots tiles, read back in the MFMA operand layout. Lane l of copy k lands at tile row
+// 4k + l/16, position l%16, and fetches column chunk (l%16) ^ row, so the operand reads (16 rows,
+// one chunk each) hit 16 different bank groups. The query block and the head weights arrive the
+// same way, the scores collect in LDS and leave in one coalesced pass at the end (candidate mask
+// and -inf past visibility applied there): between the first copy and the last wait the wave
+// issues no other vector-memory operation, so its vmcnt waits count exactly its own copies.
+constexpr int kDecSlots = 3;             // ring depth per wave: two tiles in flight
+constexpr int kDecTile = 16 * 256;       // one 16-row tile of 128 bf16 channels
+constexpr int kIdxMaxRows = 4096;        // rows per workgroup (idx_grid's bound)
+
+template <int HT>
+__global__ __launch_bounds__(kIdxThreads) void indexer_decode_kernel(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ w_raw, float w_scale, const bf16_t* __restrict__ kcache,
+    int64_t k_bstride, const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int nb, int start_pos,
+    int ratio, int rows_per_wg) {
+  constexpr int H = HT * 16, DIM = 128, KS = 4, ROWB = DIM * 2;
+  constexpr int NW = kIdxThreads / 64;
+  constexpr int QCOPIES = H * ROWB / 1024;                 // 1 KB copies of the query block
+  constexpr int QPW = (QCOPIES + NW - 1) / NW;             // per wave (waves past the block issue none)
+  static_assert(H * 2 % 16 == 0, "the head-weight row is whole 16-byte chunks");
+  __shared__ __align__(16) uint8_t ring[NW * kDecSlots * kDecTile];
+  __shared__ __align__(16) uint8_t q_lds[H * ROWB];
+  __shared__ __align__(16) uint8_t w_lds[1024];
+  __shared__ __align__(16) float sc_lds[kIdxMaxRows];
+
+  const int qi = blockIdx.y;               // b * n + s
+  const int b = qi / n, s = qi - (qi / n) * n;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lens = (start_pos + s + 1) / ratio;
+  const int r0 = blockIdx.x * rows_per_wg;
+  const int r1 = min(r0 + rows_per_wg, nb);
+  const int vis_end = max(r0, min(r1, lens));
+  float* out = scores + (int64_t)qi * nb;
+  if (vis_end <= r0) {                     // uniform: nothing visible in this row range
+    for (int t = r0 + tid; t < r1; t += kIdxThreads) out[t] = -INFINITY;
+    return;
+  }
+  const int nt = (vis_end - r0 + 16 * NW - 1) / (16 * NW);   // tiles per wave (the last ones clamped)
+  const uint8_t* kb = reinterpret_cast<const uint8_t*>(kcache + (int64_t)b * k_bstride);
+  const uint32_t ring_w = lds_offset(ring) + (uint32_t)(wave * kDecSlots * kDecTile);
+  auto issue = [&](int i) {                // tile i of this wave into slot i % kDecSlots: 4 copies
+    const int ti = min(i, nt - 1);
+    const int slot = i % kDecSlots;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int rloc = 4 * k + (lane >> 4);
+      const int row = min(r0 + 16 * (NW * ti + wave) + rloc, vis_end - 1);   // clamp: stays in the cache
+      const int col = (lane & 15) ^ rloc;
+      const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_w + (uint32_t)(slot * kDecTile + k * 1024));
+      dma16_vaddr_nt(reinterpret_cast<uint64_t>(kb + (int64_t)row * ROWB + col * 16), dst);
+    }
+  };
+  {
+    const uint8_t* qb = reinterpret_cast<const uint8_t*>(q + (int64_t)qi * H * DIM);
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+      const int c = wave * QPW + j;        // uniform
+      if (c < QCOPIES) {
+        const int rloc = c * 4 + (lane >> 4);
+        const int col = (lane & 15) ^ (rloc & 15);
+        dma16_vaddr(reinterpret_cast<uint64_t>(qb + rloc * ROWB + col * 16),
+                    (uint32_t)__builtin_amdgcn_readfirstlane(lds_offset(q_lds) + (uint32_t)(c * 1024)));
+      }
+    }
+    if (wave == NW - 1) {                  // the H-entry weight row: lanes past it re-read its last chunk
+      const uint8_t* wb = reinterpret_cast<const uint8_t*>(w_raw + (int64_t)qi * H);
+      dma16_vaddr(reinterpret_cast<uint64_t>(wb + min(lane, H * 2 / 16 - 1) * 16),
+                  (uint32_t)__builtin_amdgcn_readfirstlane(lds_offset(w_lds)));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kDecSlots - 1; ++i) issue(i);
+  wait_vmcnt<4 * (kDecSlots - 1)>();       // this wave's query / weight copies landed
+  __syncthreads();                         // ... and every other wave's
+  bf16x8 qa[HT][KS];
+  float wv[HT][4];
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qa[ht][ks] = ld_bf16x8(q_lds + (ht * 16 + l16) * ROWB + (((ks * 4 + g) ^ l16) * 16));
+  {
+    const bf16_t* wl = reinterpret_cast<const bf16_t*>(w_lds);
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wl[ht * 16 + 4 * g + i]) * w_scale);
+  }
+  for (int i = 0; i < nt; ++i) {
+    issue(i + kDecSlots - 1);              // past the last tile: a clamped re-read, so counts stay exact
+    wait_vmcnt<4 * (kDecSlots - 1)>();     // tile i landed
+    const uint8_t* rowp = ring + (wave * kDecSlots + i % kDecSlots) * kDecTile + l16 * ROWB;
+    f32x4 acc[HT];
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) acc[ht] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const bf16x8 kop = ld_bf16x8(rowp + (((ks * 4 + g) ^ l16) * 16));
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) acc[ht] = mfma16x16x32(qa[ht][ks], kop, acc[ht]);
+    }
+    float part = 0.0f;
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+      for (int i2 = 0; i2 < 4; ++i2) part += fmaxf(acc[ht][i2], 0.0f) * wv[ht][i2];
+    part = sum_rows4(part);
+    if (g == 0) sc_lds[16 * (NW * i + wave) + l16] = part;
+  }
+  wait_vmcnt<0>();                         // no copy may land in LDS after the workgroup ends
+  __syncthreads();                         // every score of the range is in LDS
+  const uint8_t* cb = cand ? cand + (int64_t)qi * nb : nullptr;
+  for (int t = tid; t < r1 - r0; t += kIdxThreads) {
+    float v = -INFINITY;
+    if (t < vis_end - r0 && (!cb || cb[r0 + t])) v = sc_lds[t];
+    out[r0 + t] = v;
+  }
+}
+
 // MXFP4 keys: the index cache holds each 128-channel key as fp4 e2m1 codes (64 bytes; byte p
 // carries channels 2p and 2p+1, the even one in the low nibble) plus one ue8m0 scale byte per
 // 32 channels (4 bytes) -- the lossless packed form of the fake_quant_fp4_ue8m0 keys that
@@ -499,7 +623,20 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
   }
   int rows_per_wg = 0;
   const dim3 grid = idx_grid((int64_t)nb * bsz * n, nb, bsz * n, &rows_per_wg);
-#define DSV41_IDX_CASE(HT_, KS_)                                                                             \
+  if (dim == 128 && (heads == 64 || heads == 32 || heads == 16) && aligned16(w_raw) && rows_per_wg <= kIdxMaxRows) {
+#define DSV41_DEC_CASE(HT_)                                                                                   \
+    if (heads == HT_ * 16) {                                                                                  \
+      hipLaunchKernelGGL((indexer_decode_kernel<HT_>), grid, dim3(kIdxThreads), 0, stream, (const bf16_t*)q,  \
+                         (const bf16_t*)w_raw, w_scale, (const bf16_t*)index_k, k_bstride, candidates, scores, \
+                         n, nb, start_pos, ratio, rows_per_wg);                                               \
+      return check_launch(what);                                                                              \
+    }
+    DSV41_DEC_CASE(4)
+    DSV41_DEC_CASE(2)
+    DSV41_DEC_CASE(1)
+#undef DSV41_DEC_CASE
+  }
+#define DSV41_IDX_CASE(HT_, KS_)                                                                          \
   if (heads == HT_ * 16 && dim == KS_ * 32) {                                                                \
     launch_idx_bf16<HT_, KS_, false>(grid, stream, q, w_raw, w_scale, index_k, k_bstride, nullptr, 0, 1,     \
                                      candidates, scores, n, nb, start_pos, ratio, rows_per_wg);              \

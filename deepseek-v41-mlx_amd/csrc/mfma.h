@@ -57,6 +57,13 @@ __device__ __forceinline__ void dma16_vaddr(uint64_t addr, uint32_t lds) {
                : "memory", "m0");
 }
 
+// The vaddr-form copy with the non-temporal hint: for data read once (streamed key caches), so
+// that it does not displace what later kernels read from L2 and the Infinity Cache.
+__device__ __forceinline__ void dma16_vaddr_nt(uint64_t addr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(addr), "s"(lds)
+               : "memory", "m0");
+}
+
 // s_waitcnt immediate (gfx9 encoding): vmcnt 0, expcnt 7 and lgkmcnt 15 (no wait on those).
 // As __builtin_amdgcn_s_waitcnt it is visible to the compiler's wait-count pass.
 constexpr int kWaitVmcnt0 = 0x0F70;

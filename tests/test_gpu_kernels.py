@@ -212,6 +212,9 @@ def test_index_q_prep(gpu, dt):
     ("bf16", 64, 128, 2, 40, 3000, 11000, False),  # prefill kernel: 8 queries per workgroup, 2 row ranges
     ("bf16", 32, 128, 1, 13, 700, 2500, False),    # prefill kernel: a partial query group (idle waves)
     ("bf16", 16, 128, 3, 9, 300, 100, False),      # prefill kernel: most rows past visibility
+    ("bf16", 64, 128, 2, 1, 50, 199, False),       # decode kernel: fewer rows than one 8-wave sweep
+    ("bf16", 16, 128, 3, 2, 3000, 4000, True),     # decode kernel: workgroups wholly past visibility
+    ("bf16", 32, 128, 5, 1, 20000, 79999, True),   # decode kernel: 40 row ranges, candidates
 ])
 def test_indexer_score(gpu, dt, hi, di, b, n, nb, start, use_cand):
     from dsv41 import _abi
