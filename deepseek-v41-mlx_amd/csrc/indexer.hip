@@ -176,24 +176,26 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
 // same way, the scores collect in LDS and leave in one coalesced pass at the end (candidate mask
 // and -inf past visibility applied there): between the first copy and the last wait the wave
 // issues no other vector-memory operation, so its vmcnt waits count exactly its own copies.
-constexpr int kDecSlots = 3;             // ring depth per wave: two tiles in flight
+constexpr int kDecSlots = 2;             // ring depth per wave: one tile in flight while one is scored
 constexpr int kDecTile = 16 * 256;       // one 16-row tile of 128 bf16 channels
 constexpr int kIdxMaxRows = 4096;        // rows per workgroup (idx_grid's bound)
+constexpr int kDecWaves = 8;
 
-template <int HT>
-__global__ __launch_bounds__(kIdxThreads) void indexer_decode_kernel(
+template <int HT, int NW>
+__global__ __launch_bounds__(NW * 64) void indexer_decode_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ w_raw, float w_scale, const bf16_t* __restrict__ kcache,
     int64_t k_bstride, const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int nb, int start_pos,
     int ratio, int rows_per_wg) {
   constexpr int H = HT * 16, DIM = 128, KS = 4, ROWB = DIM * 2;
-  constexpr int NW = kIdxThreads / 64;
   constexpr int QCOPIES = H * ROWB / 1024;                 // 1 KB copies of the query block
   constexpr int QPW = (QCOPIES + NW - 1) / NW;             // per wave (waves past the block issue none)
+  constexpr int QSC = H * ROWB > kIdxMaxRows * 4 ? H * ROWB : kIdxMaxRows * 4;
   static_assert(H * 2 % 16 == 0, "the head-weight row is whole 16-byte chunks");
   __shared__ __align__(16) uint8_t ring[NW * kDecSlots * kDecTile];
-  __shared__ __align__(16) uint8_t q_lds[H * ROWB];
-  __shared__ __align__(16) uint8_t w_lds[1024];
-  __shared__ __align__(16) float sc_lds[kIdxMaxRows];
+  __shared__ __align__(16) uint8_t q_lds[QSC];   // the query block; then, once every wave holds it, the scores
+  // the head-weight row lands in the last wave's last ring slot, which no tile uses before the loop
+  const uint8_t* w_lds = ring + ((NW - 1) * kDecSlots + kDecSlots - 1) * kDecTile;
+  float* sc_lds = reinterpret_cast<float*>(q_lds);
 
   const int qi = blockIdx.y;               // b * n + s
   const int b = qi / n, s = qi - (qi / n) * n;
@@ -205,7 +207,7 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_decode_kernel(
   const int vis_end = max(r0, min(r1, lens));
   float* out = scores + (int64_t)qi * nb;
   if (vis_end <= r0) {                     // uniform: nothing visible in this row range
-    for (int t = r0 + tid; t < r1; t += kIdxThreads) out[t] = -INFINITY;
+    for (int t = r0 + tid; t < r1; t += NW * 64) out[t] = -INFINITY;
     return;
   }
   const int nt = (vis_end - r0 + 16 * NW - 1) / (16 * NW);   // tiles per wave (the last ones clamped)
@@ -238,7 +240,7 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_decode_kernel(
     if (wave == NW - 1) {                  // the H-entry weight row: lanes past it re-read its last chunk
       const uint8_t* wb = reinterpret_cast<const uint8_t*>(w_raw + (int64_t)qi * H);
       dma16_vaddr(reinterpret_cast<uint64_t>(wb + min(lane, H * 2 / 16 - 1) * 16),
-                  (uint32_t)__builtin_amdgcn_readfirstlane(lds_offset(w_lds)));
+                  (uint32_t)__builtin_amdgcn_readfirstlane(ring_w + (uint32_t)((kDecSlots - 1) * kDecTile)));
     }
   }
 #pragma unroll
@@ -259,6 +261,8 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_decode_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wl[ht * 16 + 4 * g + i]) * w_scale);
   }
+  __syncthreads();                         // every wave holds its query operands and weights: q_lds takes
+                                           // scores, the last ring slot its first tile
   for (int i = 0; i < nt; ++i) {
     issue(i + kDecSlots - 1);              // past the last tile: a clamped re-read, so counts stay exact
     wait_vmcnt<4 * (kDecSlots - 1)>();     // tile i landed
@@ -283,7 +287,7 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_decode_kernel(
   wait_vmcnt<0>();                         // no copy may land in LDS after the workgroup ends
   __syncthreads();                         // every score of the range is in LDS
   const uint8_t* cb = cand ? cand + (int64_t)qi * nb : nullptr;
-  for (int t = tid; t < r1 - r0; t += kIdxThreads) {
+  for (int t = tid; t < r1 - r0; t += NW * 64) {
     float v = -INFINITY;
     if (t < vis_end - r0 && (!cb || cb[r0 + t])) v = sc_lds[t];
     out[r0 + t] = v;
@@ -626,7 +630,8 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
   if (dim == 128 && (heads == 64 || heads == 32 || heads == 16) && aligned16(w_raw) && rows_per_wg <= kIdxMaxRows) {
 #define DSV41_DEC_CASE(HT_)                                                                                   \
     if (heads == HT_ * 16) {                                                                                  \
-      hipLaunchKernelGGL((indexer_decode_kernel<HT_>), grid, dim3(kIdxThreads), 0, stream, (const bf16_t*)q,  \
+      hipLaunchKernelGGL((indexer_decode_kernel<HT_, kDecWaves>), grid, dim3(kDecWaves * 64), 0, stream,      \
+                         (const bf16_t*)q,                                                                    \
                          (const bf16_t*)w_raw, w_scale, (const bf16_t*)index_k, k_bstride, candidates, scores, \
                          n, nb, start_pos, ratio, rows_per_wg);                                               \
       return check_launch(what);                                                                              \
