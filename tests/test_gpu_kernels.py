@@ -387,7 +387,7 @@ def _score_sets(rng, b, n, nb):
                                                   (1, 64, 1000, 256, 3000, 4), (2, 1, 16384, 512, 65535, 4),
                                                   (1, 2, 300, 512, 1199, 4), (1, 5, 2049, 2048, 8191, 4),
                                                   (1, 2, 32768, 2048, 131071, 4), (1, 3, 5001, 700, 20003, 4),
-                                                  (1, 1, 40000, 1000, 159999, 4)])
+                                                  (1, 1, 40000, 1000, 159999, 4), (1, 1, 20000, 5000, 79999, 4)])
 def test_topk_bit_exact(gpu, b, n, nb, topk, start, r):
     from dsv41 import _abi
     rng = rng_for(f"topk{nb}{n}")
