@@ -166,35 +166,51 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
   }
 }
 
-// bf16 keys of 128 channels, the decode shape (few queries, long cache): the same scores as
+// 128-channel keys, the decode shape (few queries, long cache): the same scores as
 // indexer_score_bf16_kernel, with the key stream moved by LDS copies. Wave w of the workgroup
-// takes 16-row tiles w, w + 8, w + 16, ... of the row range; each tile is four 1 KB
-// global_load_lds copies (4 whole rows each, non-temporal) into the wave's private ring of
-// kDecSlots tiles, read back in the MFMA operand layout. Lane l of copy k lands at tile row
-// 4k + l/16, position l%16, and fetches column chunk (l%16) ^ row, so the operand reads (16 rows,
-// one chunk each) hit 16 different bank groups. The query block and the head weights arrive the
-// same way, the scores collect in LDS and leave in one coalesced pass at the end (candidate mask
-// and -inf past visibility applied there): between the first copy and the last wait the wave
-// issues no other vector-memory operation, so its vmcnt waits count exactly its own copies.
-constexpr int kDecSlots = 2;             // ring depth per wave: one tile in flight while one is scored
-constexpr int kDecTile = 16 * 256;       // one 16-row tile of 128 bf16 channels
+// takes 16-row tiles w, w + 8, w + 16, ... of the row range; each tile is 1 KB global_load_lds
+// copies of whole rows (non-temporal) into the wave's private ring of kDecSlots tiles, read back
+// in the MFMA operand layout. A copy's lane lands at tile row (rows per copy) * k + lane / (chunks
+// per row) and fetches a column chunk XOR-swizzled by that row, so that the operand reads of 16
+// rows hit disjoint bank groups. bf16 rows (256 B): 4 copies per tile, chunk ^ row. fp8 rows
+// (e4m3 codes, 128 B): 2 copies per tile, chunk ^ ((row >> 1) & 7); the row block's ue8m0 scale
+// words (one byte per 32 channels, one word per `rb` rows) are staged for the whole row range
+// up front, and each operand is dequantized on the way to the MFMA (exact in bf16), in the same
+// channel order as the bf16 kernel, so both forms give the same bits. The query block and the
+// head weights arrive by copies too, the scores collect in LDS and leave in one coalesced pass at
+// the end (candidate mask and -inf past visibility applied there): between the first copy and
+// the last wait a wave issues no other vector-memory operation, so its vmcnt waits count exactly
+// its own copies.
 constexpr int kIdxMaxRows = 4096;        // rows per workgroup (idx_grid's bound)
 constexpr int kDecWaves = 8;
 
-template <int HT, int NW>
+template <bool F8> struct DecKeys {
+  static constexpr int ROW = F8 ? 128 : 256;   // bytes per key row
+  static constexpr int TILE = 16 * ROW;        // one 16-row tile
+  static constexpr int CPT = TILE / 1024;      // 1 KB copies per tile
+  static constexpr int CPR = ROW / 16;         // 16-byte chunks per row
+  static constexpr int SLOTS = F8 ? 3 : 2;     // ring depth per wave: tiles in flight + the one scored
+  static constexpr int SCALES = F8 ? kIdxMaxRows * 4 : 0;   // staged scale bytes (rb = 1 at most rows)
+  __device__ static int swz(int rloc) { return F8 ? ((rloc >> 1) & 7) : (rloc & 15); }
+};
+
+template <int HT, int NW, bool F8>
 __global__ __launch_bounds__(NW * 64) void indexer_decode_kernel(
-    const bf16_t* __restrict__ q, const bf16_t* __restrict__ w_raw, float w_scale, const bf16_t* __restrict__ kcache,
-    int64_t k_bstride, const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int nb, int start_pos,
-    int ratio, int rows_per_wg) {
-  constexpr int H = HT * 16, DIM = 128, KS = 4, ROWB = DIM * 2;
-  constexpr int QCOPIES = H * ROWB / 1024;                 // 1 KB copies of the query block
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ w_raw, float w_scale, const void* __restrict__ kcache,
+    int64_t k_bstride, const uint8_t* __restrict__ kscale, int64_t ks_bstride, int ks_rb,
+    const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int nb, int start_pos, int ratio,
+    int rows_per_wg) {
+  using K = DecKeys<F8>;
+  constexpr int H = HT * 16, DIM = 128, KS = 4, QROW = DIM * 2;
+  constexpr int QCOPIES = H * QROW / 1024;                 // 1 KB copies of the query block
   constexpr int QPW = (QCOPIES + NW - 1) / NW;             // per wave (waves past the block issue none)
-  constexpr int QSC = H * ROWB > kIdxMaxRows * 4 ? H * ROWB : kIdxMaxRows * 4;
+  constexpr int QSC = H * QROW > kIdxMaxRows * 4 ? H * QROW : kIdxMaxRows * 4;
   static_assert(H * 2 % 16 == 0, "the head-weight row is whole 16-byte chunks");
-  __shared__ __align__(16) uint8_t ring[NW * kDecSlots * kDecTile];
+  __shared__ __align__(16) uint8_t ring[NW * K::SLOTS * K::TILE];
   __shared__ __align__(16) uint8_t q_lds[QSC];   // the query block; then, once every wave holds it, the scores
+  __shared__ __align__(16) uint8_t s_lds[K::SCALES > 0 ? K::SCALES : 16];
   // the head-weight row lands in the last wave's last ring slot, which no tile uses before the loop
-  const uint8_t* w_lds = ring + ((NW - 1) * kDecSlots + kDecSlots - 1) * kDecTile;
+  const uint8_t* w_lds = ring + ((NW - 1) * K::SLOTS + K::SLOTS - 1) * K::TILE;
   float* sc_lds = reinterpret_cast<float*>(q_lds);
 
   const int qi = blockIdx.y;               // b * n + s
@@ -211,20 +227,21 @@ __global__ __launch_bounds__(NW * 64) void indexer_decode_kernel(
     return;
   }
   const int nt = (vis_end - r0 + 16 * NW - 1) / (16 * NW);   // tiles per wave (the last ones clamped)
-  const uint8_t* kb = reinterpret_cast<const uint8_t*>(kcache + (int64_t)b * k_bstride);
-  const uint32_t ring_w = lds_offset(ring) + (uint32_t)(wave * kDecSlots * kDecTile);
-  auto issue = [&](int i) {                // tile i of this wave into slot i % kDecSlots: 4 copies
+  const uint8_t* kb = reinterpret_cast<const uint8_t*>(kcache) + (int64_t)b * k_bstride * (F8 ? 1 : 2);
+  const uint32_t ring_w = lds_offset(ring) + (uint32_t)(wave * K::SLOTS * K::TILE);
+  auto issue = [&](int i) {                // tile i of this wave into slot i % SLOTS
     const int ti = min(i, nt - 1);
-    const int slot = i % kDecSlots;
+    const int slot = i % K::SLOTS;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int rloc = 4 * k + (lane >> 4);
+    for (int k = 0; k < K::CPT; ++k) {
+      const int rloc = (1024 / K::ROW) * k + lane / K::CPR;
       const int row = min(r0 + 16 * (NW * ti + wave) + rloc, vis_end - 1);   // clamp: stays in the cache
-      const int col = (lane & 15) ^ rloc;
-      const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_w + (uint32_t)(slot * kDecTile + k * 1024));
-      dma16_vaddr_nt(reinterpret_cast<uint64_t>(kb + (int64_t)row * ROWB + col * 16), dst);
+      const int col = (lane % K::CPR) ^ K::swz(rloc);
+      const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_w + (uint32_t)(slot * K::TILE + k * 1024));
+      dma16_vaddr_nt(reinterpret_cast<uint64_t>(kb + (int64_t)row * K::ROW + col * 16), dst);
     }
   };
+  const int ssh = ks_rb == 32 ? 5 : 0;     // rows per scale word: 32 or 1
   {
     const uint8_t* qb = reinterpret_cast<const uint8_t*>(q + (int64_t)qi * H * DIM);
 #pragma unroll
@@ -233,19 +250,32 @@ __global__ __launch_bounds__(NW * 64) void indexer_decode_kernel(
       if (c < QCOPIES) {
         const int rloc = c * 4 + (lane >> 4);
         const int col = (lane & 15) ^ (rloc & 15);
-        dma16_vaddr(reinterpret_cast<uint64_t>(qb + rloc * ROWB + col * 16),
+        dma16_vaddr(reinterpret_cast<uint64_t>(qb + rloc * QROW + col * 16),
                     (uint32_t)__builtin_amdgcn_readfirstlane(lds_offset(q_lds) + (uint32_t)(c * 1024)));
       }
     }
     if (wave == NW - 1) {                  // the H-entry weight row: lanes past it re-read its last chunk
       const uint8_t* wb = reinterpret_cast<const uint8_t*>(w_raw + (int64_t)qi * H);
       dma16_vaddr(reinterpret_cast<uint64_t>(wb + min(lane, H * 2 / 16 - 1) * 16),
-                  (uint32_t)__builtin_amdgcn_readfirstlane(ring_w + (uint32_t)((kDecSlots - 1) * kDecTile)));
+                  (uint32_t)__builtin_amdgcn_readfirstlane(ring_w + (uint32_t)((K::SLOTS - 1) * K::TILE)));
+    }
+    if constexpr (F8) {
+      // scale words of rows [r0, vis_end): bytes [(r0 >> ssh) * 4, ((vis_end - 1 >> ssh) + 1) * 4) of the
+      // batch row, 16-byte aligned at the start (r0 is a multiple of 512); chunks past the end are
+      // clamped onto the last one, which stays inside the 16-byte-multiple batch stride
+      const uint8_t* sb = kscale + (int64_t)b * ks_bstride + (int64_t)(r0 >> ssh) * 4;
+      const int nsc = (((vis_end - 1) >> ssh) - (r0 >> ssh) + 1) * 4;
+      const int nch = (nsc + 15) / 16;
+      for (int c = wave; c * 64 < nch; c += NW) {   // uniform per wave
+        const int ch = min(c * 64 + lane, nch - 1);
+        dma16_vaddr(reinterpret_cast<uint64_t>(sb + ch * 16),
+                    (uint32_t)__builtin_amdgcn_readfirstlane(lds_offset(s_lds) + (uint32_t)(c * 1024)));
+      }
     }
   }
 #pragma unroll
-  for (int i = 0; i < kDecSlots - 1; ++i) issue(i);
-  wait_vmcnt<4 * (kDecSlots - 1)>();       // this wave's query / weight copies landed
+  for (int i = 0; i < K::SLOTS - 1; ++i) issue(i);
+  wait_vmcnt<K::CPT * (K::SLOTS - 1)>();   // this wave's query / weight / scale copies landed
   __syncthreads();                         // ... and every other wave's
   bf16x8 qa[HT][KS];
   float wv[HT][4];
@@ -253,7 +283,7 @@ __global__ __launch_bounds__(NW * 64) void indexer_decode_kernel(
   for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      qa[ht][ks] = ld_bf16x8(q_lds + (ht * 16 + l16) * ROWB + (((ks * 4 + g) ^ l16) * 16));
+      qa[ht][ks] = ld_bf16x8(q_lds + (ht * 16 + l16) * QROW + (((ks * 4 + g) ^ l16) * 16));
   {
     const bf16_t* wl = reinterpret_cast<const bf16_t*>(w_lds);
 #pragma unroll
@@ -264,15 +294,27 @@ __global__ __launch_bounds__(NW * 64) void indexer_decode_kernel(
   __syncthreads();                         // every wave holds its query operands and weights: q_lds takes
                                            // scores, the last ring slot its first tile
   for (int i = 0; i < nt; ++i) {
-    issue(i + kDecSlots - 1);              // past the last tile: a clamped re-read, so counts stay exact
-    wait_vmcnt<4 * (kDecSlots - 1)>();     // tile i landed
-    const uint8_t* rowp = ring + (wave * kDecSlots + i % kDecSlots) * kDecTile + l16 * ROWB;
+    issue(i + K::SLOTS - 1);               // past the last tile: a clamped re-read, so counts stay exact
+    wait_vmcnt<K::CPT * (K::SLOTS - 1)>(); // tile i landed
+    const uint8_t* rowp = ring + (wave * K::SLOTS + i % K::SLOTS) * K::TILE + l16 * K::ROW;
     f32x4 acc[HT];
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) acc[ht] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint32_t sw = 0u;
+    if constexpr (F8) {                    // the scale word of this lane's (clamped) row
+      const int row = min(r0 + 16 * (NW * i + wave) + l16, vis_end - 1);
+      sw = *reinterpret_cast<const uint32_t*>(s_lds + ((row >> ssh) - (r0 >> ssh)) * 4);
+    }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const bf16x8 kop = ld_bf16x8(rowp + (((ks * 4 + g) ^ l16) * 16));
+      bf16x8 kop;
+      if constexpr (F8) {                  // channels 32 ks + 8 g .. +8: half (g & 1) of chunk 2 ks + g / 2
+        const uint2 c8 = *reinterpret_cast<const uint2*>(rowp + (((2 * ks + (g >> 1)) ^ K::swz(l16)) * 16) +
+                                                         8 * (g & 1));
+        kop = dequant_e4m3x8(c8.x, c8.y, e8m0_to_float((sw >> (8 * ks)) & 255u));
+      } else {
+        kop = ld_bf16x8(rowp + (((ks * 4 + g) ^ l16) * 16));
+      }
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) acc[ht] = mfma16x16x32(qa[ht][ks], kop, acc[ht]);
     }
@@ -630,10 +672,9 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
   if (dim == 128 && (heads == 64 || heads == 32 || heads == 16) && aligned16(w_raw) && rows_per_wg <= kIdxMaxRows) {
 #define DSV41_DEC_CASE(HT_)                                                                                   \
     if (heads == HT_ * 16) {                                                                                  \
-      hipLaunchKernelGGL((indexer_decode_kernel<HT_, kDecWaves>), grid, dim3(kDecWaves * 64), 0, stream,      \
-                         (const bf16_t*)q,                                                                    \
-                         (const bf16_t*)w_raw, w_scale, (const bf16_t*)index_k, k_bstride, candidates, scores, \
-                         n, nb, start_pos, ratio, rows_per_wg);                                               \
+      hipLaunchKernelGGL((indexer_decode_kernel<HT_, kDecWaves, false>), grid, dim3(kDecWaves * 64), 0,       \
+                         stream, (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, index_k, k_bstride, nullptr, \
+                         0, 1, candidates, scores, n, nb, start_pos, ratio, rows_per_wg);                     \
       return check_launch(what);                                                                              \
     }
     DSV41_DEC_CASE(4)
@@ -683,6 +724,20 @@ extern "C" int dsv41_indexer_score_fp8(const void* q, const void* w_raw, float w
   if ((int64_t)bsz * n == 0 || nb == 0) return 0;
   int rows_per_wg = 0;
   const dim3 grid = idx_grid((int64_t)nb * bsz * n, nb, bsz * n, &rows_per_wg);
+  if ((heads == 64 || heads == 32 || heads == 16) && aligned16(w_raw) && aligned16(k_scale) &&
+      ks_bstride % 16 == 0 && rows_per_wg <= kIdxMaxRows) {
+#define DSV41_DEC8_CASE(HT_)                                                                                  \
+    if (heads == HT_ * 16) {                                                                                  \
+      hipLaunchKernelGGL((indexer_decode_kernel<HT_, kDecWaves, true>), grid, dim3(kDecWaves * 64), 0, stream, \
+                         (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, index_k, k_bstride, k_scale,         \
+                         ks_bstride, ks_rb, candidates, scores, n, nb, start_pos, ratio, rows_per_wg);        \
+      return check_launch(what);                                                                              \
+    }
+    DSV41_DEC8_CASE(4)
+    DSV41_DEC8_CASE(2)
+    DSV41_DEC8_CASE(1)
+#undef DSV41_DEC8_CASE
+  }
 #define DSV41_IDX8_CASE(HT_)                                                                                   \
   if (heads == HT_ * 16) {                                                                                     \
     launch_idx_bf16<HT_, 4, true>(grid, stream, q, w_raw, w_scale, index_k, k_bstride, k_scale, ks_bstride,  \

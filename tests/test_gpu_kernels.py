@@ -236,11 +236,15 @@ def test_indexer_score(gpu, dt, hi, di, b, n, nb, start, use_cand):
     assert np.abs(g[fin] - want[fin]).max() <= 1e-5 * max(np.abs(want[fin]).max(), 1.0)
 
 
-@pytest.mark.parametrize("b,n,h,nb,start,rb", [(16, 1, 64, 32768, 131071, 32), (3, 5, 32, 1000, 3990, 1),
-                                               (2, 40, 16, 700, 2700, 32)])
-def test_indexer_score_fp8_keys(gpu, b, n, h, nb, start, rb):
+@pytest.mark.parametrize("b,n,h,nb,start,rb,pad", [
+    (16, 1, 64, 32768, 131071, 32, False), (3, 5, 32, 1000, 3990, 1, False), (2, 40, 16, 700, 2700, 32, False),
+    (16, 1, 64, 32768, 131071, 32, True),  # 16-byte scale rows: the staged-copy decode kernel
+    (3, 5, 32, 1000, 3990, 1, True), (2, 40, 16, 700, 2700, 32, True), (2, 1, 64, 50, 199, 1, True),
+    (4, 2, 64, 9000, 35000, 1, True)])
+def test_indexer_score_fp8_keys(gpu, b, n, h, nb, start, rb, pad):
     """fp8 index keys dequantized in-kernel: bit-identical to the bf16 path on the dequantized
-    keys, and within the bf16 path's tolerance of the oracle."""
+    keys, and within the bf16 path's tolerance of the oracle. `pad` rounds the scale rows up to a
+    multiple of 16 bytes (the layout the staged-copy kernel takes; otherwise the register kernel)."""
     from dsv41 import _abi
     from dsv41.indexer import weight_scale
     rng = rng_for(f"idx8{b}{n}{nb}")
@@ -249,7 +253,8 @@ def test_indexer_score_fp8_keys(gpu, b, n, h, nb, start, rb):
     w_raw = R.cast(rng.standard_normal((b, n, h)).astype(F32), "bf16")
     codes = rng.integers(0, 256, size=(b, nb + 3, d), dtype=np.uint8)
     codes[(codes & 0x7F) == 0x7F] ^= 0x01
-    scales = rng.integers(123, 132, size=(b, -(-(nb + 3) // rb), d // 32), dtype=np.uint8)
+    nblk = -(-(nb + 3) // rb)
+    scales = rng.integers(123, 132, size=(b, (nblk + 3) // 4 * 4 if pad else nblk, d // 32), dtype=np.uint8)
     keys = R.dequant_fp8_cache(codes, scales, rb)
     scale = weight_scale(h, d, torch.bfloat16)
     got8 = _abi.indexer_score_fp8(dev(q, "bf16"), dev(w_raw, "bf16"), scale, torch.as_tensor(codes).to(gpu),
