@@ -674,7 +674,7 @@ def main():
         "hbm_frac_step": step_gbs / HBM_PEAK_GBS,
         "step_algorithmic_bytes": step_bytes,
         "kernels_us": {k: v * 1e3 for k, v in kern.items()},
-        "roofline": {"bound": "hbm", "kernel": "indexer_score (dsv41_indexer_score, bf16 MFMA)",
+        "roofline": {"bound": "hbm", "kernel": "indexer_score (dsv41_indexer_score -> indexer_decode_kernel<4, 8, false>, bf16 MFMA)",
                      "achieved": idx_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": idx_gbs / HBM_PEAK_GBS,
                      "traffic": measured_traffic(),
                      "traffic_source": TRAFFIC_FILE,
