@@ -139,6 +139,7 @@ constexpr float kRescale = 8.0f;       // lazy softmax rescaling threshold (log2
 constexpr int kStepRows = 32;          // rows per pipeline step (two 16-row MFMA tiles)
 constexpr int kMaxList = 2304;         // list entries one workgroup stages in LDS
 constexpr int kLdsBudget = 160 * 1024;
+constexpr int kPairList = 256;         // list entries of the two-per-CU decode instance (half the LDS)
 constexpr int kMaxRing = 4;            // ring slots: steps in flight + the one computed
 
 
@@ -191,13 +192,13 @@ __device__ __forceinline__ void store_out4(const MlaArgs& a, int D, int qs, bf16
   *reinterpret_cast<uint2*>(orow + d0) = st;
 }
 
-template <int D, int NW>
+template <int D, int NW, int ML, int BUDGET>
 struct MlaLds {
   static constexpr int RS = D * 2 + 16;                   // padded row stride (bytes)
   static constexpr int SLOT = kStepRows * RS;
   static constexpr int XS = NW * 2 * 64 * 16;             // partial-score exchange
-  static constexpr int FIXED = XS + kMaxList * 8 + kMaxRing * kStepRows + 256;
-  static constexpr int NS = (kLdsBudget - FIXED) / SLOT < kMaxRing ? (kLdsBudget - FIXED) / SLOT : kMaxRing;
+  static constexpr int FIXED = XS + ML * 8 + kMaxRing * kStepRows + 256;
+  static constexpr int NS = (BUDGET - FIXED) / SLOT < kMaxRing ? (BUDGET - FIXED) / SLOT : kMaxRing;
   static_assert(NS >= 2, "ring needs two slots");
 };
 
@@ -215,9 +216,12 @@ struct MlaLds {
 // arrive in the second half of its bf16 slot row ([D, 2D) data, [2D, 2D + D/32) scales -- the
 // row padding) with one copy instruction, so copy counts and waits are unchanged; after its own
 // copies land, the issuing wave dequantizes the row in place to bf16, before the step barrier.
-template <int D, int HT, int DS, bool F8>
+// PAIR: the decode instance sized for two workgroups per CU (half the LDS: at most kPairList list
+// entries, a two-slot ring), so that two independent step pipelines share each CU.
+template <int D, int HT, int DS, bool F8, bool PAIR>
 __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   constexpr int NW = HT * DS, NT = 64 * NW;
+  constexpr int ML = PAIR ? kPairList : kMaxList;
   constexpr int DSL = D / DS, KSS = DSL / 32, DTS = DSL / 16;
   static_assert(DSL % 32 == 0, "dim slice must be a multiple of 32 channels");
   constexpr int R = kStepRows;
@@ -225,11 +229,11 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   constexpr int RPW = R / NW;
   constexpr int IPR = (D / 8 + 63) / 64;
   constexpr int NL = RPW * IPR;                 // copies each wave issues per step
-  using Lds = MlaLds<D, NW>;
+  using Lds = MlaLds<D, NW, ML, PAIR ? kLdsBudget / 2 : kLdsBudget>;
   constexpr int RS = Lds::RS, SLOT = Lds::SLOT, NS = Lds::NS;
   __shared__ __align__(16) uint8_t ring[NS * SLOT];
   __shared__ __align__(16) f32x4 xs[NW][2][64];
-  __shared__ uint64_t rows[kMaxList];           // resolved row addresses, 0 = masked
+  __shared__ uint64_t rows[ML];                 // resolved row addresses, 0 = masked
   __shared__ __align__(4) uint8_t vrow[NS][R];
 
   const KvSrc& S = a.src;
@@ -249,7 +253,7 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   const int ws = (wc + a.splits - 1) / a.splits, ks = (S.k + a.splits - 1) / a.splits;
   const int w0 = min(sp * ws, wc), nw = min(w0 + ws, wc) - w0;
   const int k0 = min(sp * ks, S.k), nk = min(k0 + ks, S.k) - k0;
-  const int cnt = min(nw + nk, kMaxList);       // planner: nw + nk <= kMaxList
+  const int cnt = min(nw + nk, ML);             // planner: nw + nk <= ML
   auto entry_row = [&](int e) {                  // split entry -> row address (0 = masked)
     const int u = list_pos(S, b, a.m, qs, e < nw ? w0 + e : wc + k0 + (e - nw), wc);
     const int ci = u - S.wp - S.n_chunk;
@@ -636,14 +640,19 @@ __global__ __launch_bounds__(256) void mla_f32_kernel(MlaArgs a) {
 
 struct MlaPlan {
   bool wide;                     // 64-head workgroups of 8 waves (else 32-head, 4 waves)
+  bool pair;                     // decode instance with half the LDS, two workgroups per CU
   int hgroups, splits, per_split;
 };
 
 // Many queries (prefill): one workgroup per (query, head group) over the whole list, 64 heads
 // per workgroup when there are more than 32. Few queries (decode): (query, 32-head, split)
-// workgroups, the list split in whole 32-row steps until about 256 workgroups exist (one per
-// CU: each holds a ~160 KB LDS ring). A workgroup stages at most kMaxList list entries.
-static MlaPlan plan_bf16(int64_t units, int heads, int list_max) {
+// workgroups, the list split in whole 32-row steps until about 256 workgroups exist -- or 512,
+// two per CU, when there are already >= 128 (query, head group) units or the list is >= 1024
+// entries long (measured: bs32 / 640 rows is fastest at 4 splits, B=16 / 1152 rows and B=64 at
+// ~2 workgroups per CU). Splits of at most kPairList entries with head_dim <= 512 run the PAIR
+// instance (~77 KB of LDS, a two-slot ring), the rest one ~160 KB workgroup per CU. A workgroup
+// stages at most kMaxList list entries.
+static MlaPlan plan_bf16(int64_t units, int heads, int list_max, int dim) {
   MlaPlan p{};
   const int lm = list_max > 0 ? list_max : 1;
   const int hg32 = (heads + 31) / 32;
@@ -657,7 +666,8 @@ static MlaPlan plan_bf16(int64_t units, int heads, int list_max) {
   p.wide = false;
   p.hgroups = hg32;
   const int64_t wgs = units * p.hgroups;
-  int want = wgs < 256 ? (int)((256 + wgs - 1) / wgs) : 1;
+  const int64_t target = dim <= 512 && (wgs >= 128 || lm >= 1024) ? 512 : 256;
+  int want = wgs < target ? (int)((target + wgs - 1) / wgs) : 1;
   const int cap = (lm + kStepRows - 1) / kStepRows;
   if (want > cap) want = cap;
   if (want > 16) want = 16;
@@ -665,7 +675,8 @@ static MlaPlan plan_bf16(int64_t units, int heads, int list_max) {
   auto per = [&](int w) { return ((lm + w - 1) / w + kStepRows - 1) / kStepRows * kStepRows; };
   p.per_split = per(want);
   // a split holds ceil(window / splits) + ceil(k / splits) <= per_split + 1 entries
-  while (p.per_split + 1 > kMaxList) p.per_split = per(++want);
+  p.pair = dim <= 512 && p.per_split + 1 <= kPairList;
+  while (p.per_split + 1 > (p.pair ? kPairList : kMaxList)) p.per_split = per(++want);
   p.splits = (lm + p.per_split - 1) / p.per_split;
   return p;
 }
@@ -683,10 +694,16 @@ static bool bf16_dim_supported(int d) { return d == 64 || d == 128 || d == 256 |
 template <int D, bool F8>
 static void launch_bf16_d(const MlaArgs& a, const MlaPlan& p, int64_t units, hipStream_t stream) {
   const unsigned wgs = (unsigned)(units * p.hgroups * p.splits);
+  if constexpr (D <= 512) {                    // the planner pairs only rows of up to 512 channels
+    if (p.pair && !p.wide) {
+      hipLaunchKernelGGL((mla_bf16_kernel<D, 2, 2, F8, true>), dim3(wgs), dim3(256), 0, stream, a);
+      return;
+    }
+  }
   if (p.wide)
-    hipLaunchKernelGGL((mla_bf16_kernel<D, 4, 2, F8>), dim3(wgs), dim3(512), 0, stream, a);
+    hipLaunchKernelGGL((mla_bf16_kernel<D, 4, 2, F8, false>), dim3(wgs), dim3(512), 0, stream, a);
   else
-    hipLaunchKernelGGL((mla_bf16_kernel<D, 2, 2, F8>), dim3(wgs), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((mla_bf16_kernel<D, 2, 2, F8, false>), dim3(wgs), dim3(256), 0, stream, a);
 }
 
 // fp8_comp: the compressed source is an e4m3 cache with ue8m0 block scales (q, o and the other
@@ -708,7 +725,7 @@ static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int
   if (dtype != DSV41_BF16) return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported", what, dtype);
   DSV41_REQUIRE(bf16_dim_supported(a.dim), DSV41_E_SHAPE, "%s: bf16 path supports dim 64/128/256/512/576, got %d",
                 what, a.dim);
-  const MlaPlan p = plan_bf16(units, a.heads, list_max);
+  const MlaPlan p = plan_bf16(units, a.heads, list_max, a.dim);
   DSV41_REQUIRE(units * p.hgroups * p.splits < (1ll << 31), DSV41_E_ARG, "%s: too many workgroups", what);
   DSV41_REQUIRE(p.splits <= 64, DSV41_E_SHAPE, "%s: index list of %d entries is too long for the decode path", what,
                 list_max);
@@ -753,7 +770,7 @@ extern "C" size_t dsv41_sparse_mla_workspace_bytes(int32_t bsz, int32_t m, int32
                                                    int32_t rows_per_query, int32_t dtype) {
   if (dtype != DSV41_BF16 || bsz <= 0 || m <= 0 || heads <= 0 || dim <= 0) return 0;
   const int64_t units = (int64_t)bsz * m;
-  return workspace_for(plan_bf16(units, heads, rows_per_query), units, heads, dim);
+  return workspace_for(plan_bf16(units, heads, rows_per_query, dim), units, heads, dim);
 }
 
 extern "C" int dsv41_sparse_attn(const void* q, const void* kv, const float* sink, const int32_t* idx, void* o,
