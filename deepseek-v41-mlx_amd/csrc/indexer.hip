@@ -2,13 +2,20 @@
 //   S[b,s,t] = sum_h relu(q[b,s,h,:] . k[b,t,:]) * w[b,s,h],  t >= lens_s -> -inf,
 //   candidate-masked -> -inf, with w = round_dtype(w_raw * w_scale).
 //
-// bf16: one workgroup scores `rows_per_wg` cache rows of one query. The query's [heads x dim]
-// block is staged once in LDS and held by every wave as the MFMA A operand (heads = M); each
-// wave streams 16-row tiles of the owner's key cache straight from HBM as the B operand
-// (rows = N), four tiles in flight. Lane j ends with 4 heads x 1 row; ReLU * w and the in-lane
-// head sum run on the accumulators, two cross-lane adds finish the head reduction, and lanes
-// 0..15 store 16 consecutive fp32 scores. Rows past the query's visibility are written as
-// -inf without touching the cache (causal prefill skips about half the bytes).
+// Kernels (bf16 MFMA with fp32 accumulation unless noted; heads = MFMA M, cache rows = N; each
+// lane ends with 4 heads x 1 row, ReLU * w and the head sum run on the accumulators):
+//   indexer_decode_kernel     few queries, 128-channel bf16 or fp8 keys: key tiles move by
+//                             non-temporal LDS copies into per-wave rings (the decode path);
+//   indexer_prefill_kernel    chunked prefill: 8 queries per workgroup share 64-row key chunks
+//                             staged once in a swizzled LDS ring;
+//   indexer_score_mx_kernel   MXFP4 keys and query: block-scaled fp4 MFMA, operands loaded
+//                             straight into registers;
+//   indexer_score_bf16_kernel the register kernel for the remaining shapes (other head counts
+//                             and key widths, unaligned fp8 scale rows): keys stream straight
+//                             from HBM into VGPRs, two batches of four tiles in flight;
+//   indexer_score_f32_kernel  the fp32 parity path.
+// Rows past a query's visibility are written as -inf without touching the cache (causal
+// prefill skips about half the bytes).
 #include "mfma.h"
 
 namespace dsv41 {
