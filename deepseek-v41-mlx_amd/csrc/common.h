@@ -121,19 +121,19 @@ __device__ __forceinline__ uint32_t e2m1_code(float v) {
   return c | ((__float_as_uint(v) >> 28) & 8u);
 }
 
-// MXFP4 encoding of one 32-value block with fake_quant_fp4_ue8m0's scale and rounding
-// (fakequant.py:96-106): codes[w] holds values 8w..8w+7, value 8w+i in nibble i (so byte p
-// holds values 2p and 2p+1, the even one in the low nibble); returns the ue8m0 scale byte
-// (scale 2^(byte-127)). Decoding e2m1(code) * scale gives exactly the fake-quantized value.
-__device__ __forceinline__ uint32_t mxfp4_block(const float* v, uint32_t codes[4]) {
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+// MXFP4 encoding of N (a multiple of 8) values of one 32-value block whose absolute maximum is
+// amax (the whole block's: callers holding part of a block combine the maxima of its lanes
+// first), with fake_quant_fp4_ue8m0's scale and rounding (fakequant.py:96-106): codes[w] holds
+// values 8w..8w+7, value 8w+i in nibble i (so byte p holds values 2p and 2p+1, the even one in
+// the low nibble); returns the ue8m0 scale byte (scale 2^(byte-127)). Decoding
+// e2m1(code) * scale gives exactly the fake-quantized value.
+template <int N>
+__device__ __forceinline__ uint32_t mxfp4_encode(const float* v, float amax, uint32_t* codes) {
   amax = fmaxf(amax, (float)(6.0 * 1.1754943508222875e-38));  // 6 * 2^-126
   const float s = pow2_ceil_log2(amax * (float)(1.0 / 6.0));
   const float inv = __fdiv_rn(1.0f, s);                       // exact: s is a power of two
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
+  for (int w = 0; w < N / 8; ++w) {
     uint32_t c = 0u;
 #pragma unroll
     for (int i = 0; i < 8; ++i) c |= e2m1_code(fminf(fmaxf(v[8 * w + i] * inv, -6.0f), 6.0f)) << (4 * i);

@@ -1,7 +1,10 @@
 // Row pipelines of the attention path: RMSNorm -> rope tail -> QAT fake-quant, each stage
 // rounded to the activation dtype exactly where the reference rounds, fused into one pass
-// over HBM. One thread owns a 32-element chunk of a row (fake-quant blocks of 16/32 and rope
-// pairs never straddle chunks), so the only cross-thread step is the RMSNorm reduction.
+// over HBM. A thread owns EPT consecutive elements of a 32-element chunk of a row (fake-quant
+// blocks of 16/32 and rope pairs never straddle chunks): with EPT = 8 the 4 lanes of a chunk
+// form a block's maximum by two cross-lane steps and the row's lanes its RMSNorm sum, which
+// keeps each thread's chain short (a decode step has only a few hundred rows); EPT = 32 serves
+// norms over rows wider than 64 x 8 elements.
 //
 // Reference semantics: deepseek_v41_mlx/fakequant.py:47-119, layers.py:20-84,
 // attention.py:119-122, 157-163, indexer.py:89-104, 179-181, cache.py:61-67.
@@ -32,98 +35,102 @@ struct RowArgs {
   int64_t dst2_bstride, dst2_tstride;
 };
 
-template <typename T> __device__ __forceinline__ void load32(const T* p, float v[32]);
-template <> __device__ __forceinline__ void load32<float>(const float* p, float v[32]) {
-  const float4* q = reinterpret_cast<const float4*>(p);
+// N (a multiple of 8) consecutive elements, 16-byte aligned
+template <typename T, int N> __device__ __forceinline__ void loadn(const T* p, float* v) {
+  if constexpr (sizeof(T) == 4) {
+    const float4* q = reinterpret_cast<const float4*>(p);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float4 t = q[i];
-    v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-  }
-}
-template <> __device__ __forceinline__ void load32<bf16_t>(const bf16_t* p, float v[32]) {
-  const uint4* q = reinterpret_cast<const uint4*>(p);
+    for (int i = 0; i < N / 4; ++i) {
+      float4 t = q[i];
+      v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+  } else {
+    const uint4* q = reinterpret_cast<const uint4*>(p);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint4 t = q[i];
-    uint32_t w[4] = {t.x, t.y, t.z, t.w};
+    for (int i = 0; i < N / 8; ++i) {
+      uint4 t = q[i];
+      uint32_t w[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
-      v[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+      for (int j = 0; j < 4; ++j) {
+        v[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
+        v[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+      }
     }
   }
 }
-template <typename T> __device__ __forceinline__ void store32(T* p, const float v[32]);
-template <> __device__ __forceinline__ void store32<float>(float* p, const float v[32]) {
-  float4* q = reinterpret_cast<float4*>(p);
+template <typename T, int N> __device__ __forceinline__ void storen(T* p, const float* v) {
+  if constexpr (sizeof(T) == 4) {
+    float4* q = reinterpret_cast<float4*>(p);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) q[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-}
-template <> __device__ __forceinline__ void store32<bf16_t>(bf16_t* p, const float v[32]) {
-  uint4* q = reinterpret_cast<uint4*>(p);
+    for (int i = 0; i < N / 4; ++i) q[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+  } else {
+    uint4* q = reinterpret_cast<uint4*>(p);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t w[4];
+    for (int i = 0; i < N / 8; ++i) {
+      uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      w[j] = (uint32_t)f2bf(v[8 * i + 2 * j]) | ((uint32_t)f2bf(v[8 * i + 2 * j + 1]) << 16);
-    q[i] = make_uint4(w[0], w[1], w[2], w[3]);
+      for (int j = 0; j < 4; ++j)
+        w[j] = (uint32_t)f2bf(v[8 * i + 2 * j]) | ((uint32_t)f2bf(v[8 * i + 2 * j + 1]) << 16);
+      q[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
   }
 }
 
-// One fake-quant block of BLK values at v[0..BLK), rounded back to T.
-template <typename T, int FQ, int BLK>
+// One fake-quant block of BLK values, N of them in this thread at v[0..N): N = BLK, or N < BLK
+// with the block's other values in the BLK/N neighbouring lanes (an aligned lane group), whose
+// maxima are combined. Rounded back to T.
+template <typename T, int FQ, int BLK, int N>
 __device__ __forceinline__ void fake_quant_block(float* v) {
   float amax = 0.0f;
 #pragma unroll
-  for (int i = 0; i < BLK; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  for (int i = 0; i < N; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  if constexpr (BLK > N) amax = group_max(amax, BLK / N);
   if (FQ == FQ_FP8_UE8M0) {
     amax = fmaxf(amax, 1e-4f);
     const float s = pow2_ceil_log2(amax * (float)(1.0 / 448.0));
     const float inv = __fdiv_rn(1.0f, s);   // s is a power of two: x * (1/s) rounds as x / s does
 #pragma unroll
-    for (int i = 0; i < BLK; ++i)
+    for (int i = 0; i < N; ++i)
       v[i] = io<T>::rnd(e4m3_round(fminf(fmaxf(v[i] * inv, -448.0f), 448.0f)) * s);
   } else if (FQ == FQ_FP4_UE8M0) {
     amax = fmaxf(amax, (float)(6.0 * 1.1754943508222875e-38));  // 6 * 2^-126
     const float s = pow2_ceil_log2(amax * (float)(1.0 / 6.0));
     const float inv = __fdiv_rn(1.0f, s);   // s is a power of two: x * (1/s) rounds as x / s does
 #pragma unroll
-    for (int i = 0; i < BLK; ++i)
+    for (int i = 0; i < N; ++i)
       v[i] = io<T>::rnd(e2m1_round(fminf(fmaxf(v[i] * inv, -6.0f), 6.0f)) * s);
   } else if (FQ == FQ_FP4_E4M3) {
     amax = fmaxf(amax, 0.01171875f);                             // 6 * 2^-9
     const float s = e4m3_round(__fdiv_rn(amax, 6.0f));
 #pragma unroll
-    for (int i = 0; i < BLK; ++i)
+    for (int i = 0; i < N; ++i)
       v[i] = io<T>::rnd(e2m1_round(fminf(fmaxf(__fdiv_rn(v[i], s), -6.0f), 6.0f)) * s);
   }
 }
 
-// Row coordinates of thread gid: (row, chunk c, head h, token s, batch row b). Launches with
-// fewer than 2^32 threads (the common case) use 32-bit division, a short sequence where the
-// 64-bit one is a long software routine.
+// Row coordinates of thread gid with `upr` threads per row: (row, unit u within the row, head h,
+// token s, batch row b). Launches with fewer than 2^32 threads (the common case) use 32-bit
+// division, a short sequence where the 64-bit one is a long software routine.
 struct RowPos {
   int64_t row, b;
-  int c, h, s;
+  int u, h, s;
 };
 
 template <bool WIDE>
-__device__ __forceinline__ RowPos row_pos(const RowArgs& a) {
+__device__ __forceinline__ RowPos row_pos(const RowArgs& a, int upr) {
   RowPos p;
   if (WIDE) {
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    p.row = gid / a.cpr;
-    p.c = (int)(gid - p.row * a.cpr);
+    p.row = gid / upr;
+    p.u = (int)(gid - p.row * upr);
     p.h = (int)(p.row % a.H);
     const int64_t t = p.row / a.H;
     p.s = (int)(t % a.S);
     p.b = t / a.S;
   } else {
     const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
-    const uint32_t row = gid / (uint32_t)a.cpr;
-    p.c = (int)(gid - row * (uint32_t)a.cpr);
+    const uint32_t row = gid / (uint32_t)upr;
+    p.u = (int)(gid - row * (uint32_t)upr);
     const uint32_t t = row / (uint32_t)a.H;
     p.h = (int)(row - t * (uint32_t)a.H);
     const uint32_t bb = t / (uint32_t)a.S;
@@ -134,47 +141,52 @@ __device__ __forceinline__ RowPos row_pos(const RowArgs& a) {
   return p;
 }
 
-template <typename T, bool NORM, bool ROPE, int FQ, int BLK, bool WIDE>
+// EPT elements per thread: 32 / EPT lanes per 32-element chunk, lane `sub` of a chunk holding
+// elements sub * EPT .. +EPT of it.
+template <typename T, bool NORM, bool ROPE, int FQ, int BLK, int EPT, bool WIDE>
 __global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
-  const RowPos rp = row_pos<WIDE>(a);
+  constexpr int L = 32 / EPT;
+  static_assert(EPT % 8 == 0 && 32 % EPT == 0, "8, 16 or 32 elements per thread");
+  const RowPos rp = row_pos<WIDE>(a, a.cpr * L);
   const int64_t row = rp.row, b = rp.b;
-  const int c = rp.c, h = rp.h, s = rp.s;
-  if (row >= a.rows) return;  // whole row groups leave together (cpr divides 64 when NORM)
+  const int c = rp.u / L, sub = rp.u - (rp.u / L) * L, h = rp.h, s = rp.s;
+  const int e0 = c * 32 + sub * EPT;       // this thread's first element of the row
+  if (row >= a.rows) return;  // whole rows leave together, so every lane group stays complete
 
-  // rope factors of this chunk's pairs, requested before the row itself so the two loads
+  // rope factors of this thread's pairs, requested before the row itself so the two loads
   // overlap (a pair ahead of the tail reads the first entry and is left unrotated)
   const int first = a.dim - a.rd;
-  const bool rope = ROPE && a.rd > 0 && c * 32 + 32 > first;   // the chunk meets the rope tail
-  float cs[16], sn[16];
+  const bool rope = ROPE && a.rd > 0 && e0 + EPT > first;   // the thread meets the rope tail
+  float cs[EPT / 2], sn[EPT / 2];
   if (rope) {
     const int half = a.rd >> 1;
     const int64_t pos = (int64_t)a.pos_base + (int64_t)s * a.pos_step;
     const float* ct = a.cos_tab + pos * half;
     const float* st = a.sin_tab + pos * half;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int p = max(c * 32 + 2 * j - first, 0) >> 1;
+    for (int j = 0; j < EPT / 2; ++j) {
+      const int p = max(e0 + 2 * j - first, 0) >> 1;
       cs[j] = ct[p];
       sn[j] = st[p];
     }
   }
-  float v[32];
-  load32<T>(reinterpret_cast<const T*>(a.src) + row * a.dim + c * 32, v);
+  float v[EPT];
+  loadn<T, EPT>(reinterpret_cast<const T*>(a.src) + row * a.dim + e0, v);
 
   if (NORM) {
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) ss += v[i] * v[i];
-    ss = group_sum(ss, a.cpr);
+    for (int i = 0; i < EPT; ++i) ss += v[i] * v[i];
+    ss = group_sum(ss, a.cpr * L);
     const float inv = 1.0f / sqrtf(ss / (float)a.dim + a.eps);
-    const float* w = a.norm_w + c * 32;
+    const float* w = a.norm_w + e0;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) v[i] = io<T>::rnd(w[i] * (v[i] * inv));
+    for (int i = 0; i < EPT; ++i) v[i] = io<T>::rnd(w[i] * (v[i] * inv));
   }
   if (rope) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if (c * 32 + 2 * j >= first) {
+    for (int j = 0; j < EPT / 2; ++j) {
+      if (e0 + 2 * j >= first) {
         const float s_ = a.inverse ? -sn[j] : sn[j];
         const float xr = v[2 * j], xi = v[2 * j + 1];
         v[2 * j] = io<T>::rnd(__fsub_rn(__fmul_rn(xr, cs[j]), __fmul_rn(xi, s_)));
@@ -183,26 +195,33 @@ __global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
     }
   }
   if (FQ == FQ_FP4_MX) {
-    uint32_t cw[4];
-    const uint32_t sc = mxfp4_block(v, cw);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    if constexpr (L > 1) amax = group_max(amax, L);
+    uint32_t cw[EPT / 8];
+    const uint32_t sc = mxfp4_encode<EPT>(v, amax, cw);
     uint8_t* cdst = reinterpret_cast<uint8_t*>(a.dst) + b * a.dst_bstride + (int64_t)(a.tok_base + s) * a.dst_tstride +
-                    (int64_t)h * (a.dim / 2) + c * 16;
-    *reinterpret_cast<uint4*>(cdst) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
-    a.dst2[b * a.dst2_bstride + (int64_t)(a.tok_base + s) * a.dst2_tstride + (int64_t)h * (a.dim / 32) + c] =
-        (uint8_t)sc;
+                    (int64_t)h * (a.dim / 2) + e0 / 2;
+#pragma unroll
+    for (int w = 0; w < EPT / 8; ++w) reinterpret_cast<uint32_t*>(cdst)[w] = cw[w];
+    if (sub == 0)
+      a.dst2[b * a.dst2_bstride + (int64_t)(a.tok_base + s) * a.dst2_tstride + (int64_t)h * (a.dim / 32) + c] =
+          (uint8_t)sc;
     return;
   }
   if (FQ == FQ_FP8_PACK) {
     // fake_quant_fp8_ue8m0's scale and rounding (fake_quant_block, FQ_FP8_UE8M0), stored as codes
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    for (int i = 0; i < EPT; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    if constexpr (L > 1) amax = group_max(amax, L);
     amax = fmaxf(amax, 1e-4f);
     const float sc = pow2_ceil_log2(amax * (float)(1.0 / 448.0));
     const float inv = __fdiv_rn(1.0f, sc);   // exact: sc is a power of two
-    uint32_t cw[8];
+    uint32_t cw[EPT / 4];
 #pragma unroll
-    for (int w = 0; w < 8; ++w) {
+    for (int w = 0; w < EPT / 4; ++w) {
       uint32_t word = 0u;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -210,34 +229,43 @@ __global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
       cw[w] = word;
     }
     uint8_t* cdst = reinterpret_cast<uint8_t*>(a.dst) + b * a.dst_bstride + (int64_t)(a.tok_base + s) * a.dst_tstride +
-                    (int64_t)h * a.dim + c * 32;
-    reinterpret_cast<uint4*>(cdst)[0] = make_uint4(cw[0], cw[1], cw[2], cw[3]);
-    reinterpret_cast<uint4*>(cdst)[1] = make_uint4(cw[4], cw[5], cw[6], cw[7]);
-    a.dst2[b * a.dst2_bstride + (int64_t)(a.tok_base + s) * a.dst2_tstride + (int64_t)h * (a.dim / 32) + c] =
-        (uint8_t)((__float_as_uint(sc) >> 23) & 0xFFu);
+                    (int64_t)h * a.dim + e0;
+#pragma unroll
+    for (int w = 0; w < EPT / 8; ++w) reinterpret_cast<uint2*>(cdst)[w] = make_uint2(cw[2 * w], cw[2 * w + 1]);
+    if (sub == 0)
+      a.dst2[b * a.dst2_bstride + (int64_t)(a.tok_base + s) * a.dst2_tstride + (int64_t)h * (a.dim / 32) + c] =
+          (uint8_t)((__float_as_uint(sc) >> 23) & 0xFFu);
     return;
   }
   if (FQ != FQ_NONE) {
+    constexpr int NB = BLK < EPT ? BLK : EPT;  // this thread's values of one block
 #pragma unroll
-    for (int b0 = 0; b0 < 32; b0 += BLK) fake_quant_block<T, FQ, BLK>(v + b0);
+    for (int b0 = 0; b0 < EPT; b0 += NB) fake_quant_block<T, FQ, BLK, NB>(v + b0);
   }
   T* dst = reinterpret_cast<T*>(a.dst) + b * a.dst_bstride + (int64_t)(a.tok_base + s) * a.dst_tstride +
-           (int64_t)h * a.dim + c * 32;
-  store32<T>(dst, v);
+           (int64_t)h * a.dim + e0;
+  storen<T, EPT>(dst, v);
 }
 
-template <typename T, bool NORM, bool ROPE, int FQ, int BLK>
-static int launch_rows(const RowArgs& a, hipStream_t stream, const char* what) {
-  const int64_t threads = a.rows * a.cpr;
+template <typename T, bool NORM, bool ROPE, int FQ, int BLK, int EPT>
+static int launch_rows_ept(const RowArgs& a, hipStream_t stream, const char* what) {
+  const int64_t threads = a.rows * a.cpr * (32 / EPT);
   if (threads == 0) return 0;
   const int64_t blocks = (threads + 255) / 256;
   if (blocks * 256 <= (int64_t)UINT32_MAX)
-    hipLaunchKernelGGL((row_pipeline_kernel<T, NORM, ROPE, FQ, BLK, false>), dim3((unsigned)blocks), dim3(256),
+    hipLaunchKernelGGL((row_pipeline_kernel<T, NORM, ROPE, FQ, BLK, EPT, false>), dim3((unsigned)blocks), dim3(256),
                        0, stream, a);
   else
-    hipLaunchKernelGGL((row_pipeline_kernel<T, NORM, ROPE, FQ, BLK, true>), dim3((unsigned)blocks), dim3(256),
+    hipLaunchKernelGGL((row_pipeline_kernel<T, NORM, ROPE, FQ, BLK, EPT, true>), dim3((unsigned)blocks), dim3(256),
                        0, stream, a);
   return check_launch(what);
+}
+
+// 8 elements per thread, unless a fused norm would need more than 64 lanes for one row
+template <typename T, bool NORM, bool ROPE, int FQ, int BLK>
+static int launch_rows(const RowArgs& a, hipStream_t stream, const char* what) {
+  if (!NORM || a.cpr * 4 <= 64) return launch_rows_ept<T, NORM, ROPE, FQ, BLK, 8>(a, stream, what);
+  return launch_rows_ept<T, NORM, ROPE, FQ, BLK, 32>(a, stream, what);
 }
 
 template <bool NORM, bool ROPE, int FQ, int BLK>
