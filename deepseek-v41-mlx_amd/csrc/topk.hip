@@ -135,31 +135,108 @@ __device__ void ordered_select(SelShared& sh, KeyFn key, int count, uint32_t T, 
 // Histograms alternate between two buffers, so clearing the next one needs no extra barrier.
 // Compaction: one block scan of the packed per-thread (greater, equal) counts gives every thread
 // the number of selected positions before its own; it then walks its keys in position order.
-template <int J>
-__global__ __launch_bounds__(kSelThreads) void topk_reg_kernel(const float* __restrict__ scores,
-                                                               int32_t* __restrict__ out, int n, int nb, int k,
-                                                               int start_pos, int ratio, int offset, int vec) {
-  static_assert(J % 4 == 0, "keys are loaded as float4");
+struct RegSelShared {
+  uint32_t hist[2][2048];
+  uint32_t wsum[kSelWaves];
+  uint32_t pick[2];
+};
+
+// The selection core of the register kernels: thread t holds the keys of entries t*J .. t*J+J-1
+// (consecutive, in position order), valid for j < nvalid; 1 <= k <= the number of valid entries.
+// Finds the k-th best key T and how many T-valued entries to take, then calls emit(rank, j) for
+// each selected entry j of this thread, rank = its place among the selected in entry order (so
+// ties resolve to the lowest entries). All threads of the workgroup must call it.
+template <int J, typename Emit>
+__device__ __forceinline__ void select_top(const uint32_t (&key)[J], int nvalid, int k, RegSelShared& sh, Emit emit) {
   constexpr int NBIN = 2048;
   static_assert(NBIN == 2 * kSelThreads, "each thread owns two bins in the suffix scan");
-  __shared__ uint32_t hist[2][NBIN];
-  __shared__ uint32_t wsum[kSelWaves];
-  __shared__ uint32_t pick[2];
-  const int64_t row = blockIdx.x;
-  const float* x = scores + row * nb;
-  int32_t* o = out + row * k;
-  const int s = (int)(row % n);
-  const int lens = (start_pos + s + 1) / ratio;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int i0 = tid * J;
-  const int nvalid = min(max(nb - i0, 0), J);   // keys j < nvalid are real positions
-
-  if (k >= nb) {                                 // everything is selected, in order
-    for (int j = 0; j < nvalid; ++j) o[i0 + j] = i0 + j < lens ? i0 + j + offset : -1;
-    return;
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi) {
+    sh.hist[bi][tid] = 0u;
+    sh.hist[bi][tid + kSelThreads] = 0u;
   }
-  uint32_t key[J];
-  if (vec) {                                     // row 16-byte aligned, nb % 4 == 0
+  __syncthreads();
+
+  // exclusive prefix of the per-wave totals in wsum, for wave `wave` (all 16 reads in flight)
+  auto wave_base = [&]() {
+    uint32_t base = 0u;
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) {
+      const uint32_t v = sh.wsum[w];
+      base += w < wave ? v : 0u;
+    }
+    return base;
+  };
+
+  uint32_t prefix = 0u, pmask = 0u;
+  int kk = k;
+#pragma unroll
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const uint32_t dmask = pass == 2 ? 1023u : 2047u;
+    uint32_t* h = sh.hist[pass & 1];
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (j < nvalid && (key[j] & pmask) == prefix) atomicAdd(&h[(key[j] >> shift) & dmask], 1u);
+    __syncthreads();                             // histogram complete
+    if (pass < 2) {                              // the other buffer was last read before the previous barrier
+      sh.hist[(pass & 1) ^ 1][tid] = 0u;
+      sh.hist[(pass & 1) ^ 1][tid + kSelThreads] = 0u;
+    }
+    // suffix scan from the highest digit down: thread t owns digits 2047-2t and 2046-2t
+    const uint32_t c0 = h[NBIN - 1 - 2 * tid], c1 = h[NBIN - 2 - 2 * tid];
+    const uint32_t pair = c0 + c1;
+    const uint32_t incl = wave_incl_scan(pair, lane);
+    if (lane == 63) sh.wsum[wave] = incl;
+    __syncthreads();
+    const uint32_t above = wave_base() + incl - pair;
+    if (above < (uint32_t)kk && (uint32_t)kk <= above + c0) {
+      sh.pick[0] = (uint32_t)(NBIN - 1 - 2 * tid);
+      sh.pick[1] = above;
+    } else if (above + c0 < (uint32_t)kk && (uint32_t)kk <= above + pair) {
+      sh.pick[0] = (uint32_t)(NBIN - 2 - 2 * tid);
+      sh.pick[1] = above + c0;
+    }
+    __syncthreads();
+    prefix |= sh.pick[0] << shift;
+    pmask |= dmask << shift;
+    kk -= (int)sh.pick[1];
+  }
+  const uint32_t T = prefix;
+  const uint32_t need = (uint32_t)kk;            // keys == T to take, lowest entries first
+
+  uint32_t cg = 0u, ce = 0u;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    cg += (j < nvalid && key[j] > T) ? 1u : 0u;
+    ce += (j < nvalid && key[j] == T) ? 1u : 0u;
+  }
+  const uint32_t packed = (cg << 16) | ce;       // counts <= 32768: no carry between halves
+  const uint32_t incl = wave_incl_scan(packed, lane);
+  if (lane == 63) sh.wsum[wave] = incl;          // last read before the final pass barrier
+  __syncthreads();
+  const uint32_t excl = wave_base() + incl - packed;
+  uint32_t gt_before = excl >> 16, eq_before = excl & 0xFFFFu;
+  // branch-free walk in entry order: a key > T goes to gt_before + min(eq_before, need), a
+  // key == T to gt_before + eq_before while eq_before < need
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const bool ok = j < nvalid;
+    const bool gt = ok && key[j] > T, eq = ok && key[j] == T;
+    const bool take = gt || (eq && eq_before < need);
+    if (take) emit(gt_before + min(eq_before, need), j);
+    gt_before += gt ? 1u : 0u;
+    eq_before += eq ? 1u : 0u;
+  }
+}
+
+// J keys of entries i0 .. i0+J-1 of a score row as order keys (float4 loads when `vec`: the row
+// 16-byte aligned and i0 a multiple of 4), valid for j < nvalid.
+template <int J>
+__device__ __forceinline__ void load_keys(const float* x, int i0, int nvalid, int vec, uint32_t (&key)[J]) {
+  static_assert(J % 4 == 0, "keys are loaded as float4");
+  if (vec) {
 #pragma unroll
     for (int q = 0; q < J / 4; ++q) {
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -173,86 +250,88 @@ __global__ __launch_bounds__(kSelThreads) void topk_reg_kernel(const float* __re
 #pragma unroll
     for (int j = 0; j < J; ++j) key[j] = j < nvalid ? order_key(x[i0 + j]) : 0u;
   }
-#pragma unroll
-  for (int bi = 0; bi < 2; ++bi) {
-    hist[bi][tid] = 0u;
-    hist[bi][tid + kSelThreads] = 0u;
-  }
-  __syncthreads();
+}
 
-  // exclusive prefix of the per-wave totals in wsum, for wave `wave` (all 16 reads in flight)
-  auto wave_base = [&]() {
-    uint32_t base = 0u;
-#pragma unroll
-    for (int w = 0; w < kSelWaves; ++w) {
-      const uint32_t v = wsum[w];
-      base += w < wave ? v : 0u;
-    }
-    return base;
-  };
-
-  uint32_t prefix = 0u, pmask = 0u;
-  int kk = k;
-#pragma unroll
-  for (int pass = 0; pass < 3; ++pass) {
-    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    const uint32_t dmask = pass == 2 ? 1023u : 2047u;
-    uint32_t* h = hist[pass & 1];
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-      if (j < nvalid && (key[j] & pmask) == prefix) atomicAdd(&h[(key[j] >> shift) & dmask], 1u);
-    __syncthreads();                             // histogram complete
-    if (pass < 2) {                              // the other buffer was last read before the previous barrier
-      hist[(pass & 1) ^ 1][tid] = 0u;
-      hist[(pass & 1) ^ 1][tid + kSelThreads] = 0u;
-    }
-    // suffix scan from the highest digit down: thread t owns digits 2047-2t and 2046-2t
-    const uint32_t c0 = h[NBIN - 1 - 2 * tid], c1 = h[NBIN - 2 - 2 * tid];
-    const uint32_t pair = c0 + c1;
-    const uint32_t incl = wave_incl_scan(pair, lane);
-    if (lane == 63) wsum[wave] = incl;
-    __syncthreads();
-    const uint32_t above = wave_base() + incl - pair;
-    if (above < (uint32_t)kk && (uint32_t)kk <= above + c0) {
-      pick[0] = (uint32_t)(NBIN - 1 - 2 * tid);
-      pick[1] = above;
-    } else if (above + c0 < (uint32_t)kk && (uint32_t)kk <= above + pair) {
-      pick[0] = (uint32_t)(NBIN - 2 - 2 * tid);
-      pick[1] = above + c0;
-    }
-    __syncthreads();
-    prefix |= pick[0] << shift;
-    pmask |= dmask << shift;
-    kk -= (int)pick[1];
+template <int J>
+__global__ __launch_bounds__(kSelThreads) void topk_reg_kernel(const float* __restrict__ scores,
+                                                               int32_t* __restrict__ out, int n, int nb, int k,
+                                                               int start_pos, int ratio, int offset, int vec) {
+  __shared__ RegSelShared sh;
+  const int64_t row = blockIdx.x;
+  const float* x = scores + row * nb;
+  int32_t* o = out + row * k;
+  const int s = (int)(row % n);
+  const int lens = (start_pos + s + 1) / ratio;
+  const int i0 = threadIdx.x * J;
+  const int nvalid = min(max(nb - i0, 0), J);   // keys j < nvalid are real positions
+  if (k >= nb) {                                 // everything is selected, in order
+    for (int j = 0; j < nvalid; ++j) o[i0 + j] = i0 + j < lens ? i0 + j + offset : -1;
+    return;
   }
-  const uint32_t T = prefix;
-  const uint32_t need = (uint32_t)kk;            // keys == T to take, lowest positions first
-
-  uint32_t cg = 0u, ce = 0u;
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    cg += (j < nvalid && key[j] > T) ? 1u : 0u;
-    ce += (j < nvalid && key[j] == T) ? 1u : 0u;
-  }
-  const uint32_t packed = (cg << 16) | ce;       // counts <= 32768: no carry between halves
-  const uint32_t incl = wave_incl_scan(packed, lane);
-  if (lane == 63) wsum[wave] = incl;             // last read before the final pass barrier
-  __syncthreads();
-  const uint32_t excl = wave_base() + incl - packed;
-  uint32_t gt_before = excl >> 16, eq_before = excl & 0xFFFFu;
-  // branch-free walk in position order: a key > T goes to gt_before + min(eq_before, need), a
-  // key == T to gt_before + eq_before while eq_before < need
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
+  uint32_t key[J];
+  load_keys<J>(x, i0, nvalid, vec, key);
+  select_top<J>(key, nvalid, k, sh, [&](uint32_t rank, int j) {
     const int i = i0 + j;
-    const bool ok = j < nvalid;
-    const bool gt = ok && key[j] > T, eq = ok && key[j] == T;
-    const bool take = gt || (eq && eq_before < need);
-    const uint32_t pos = gt_before + min(eq_before, need);
-    if (take) o[pos] = i < lens ? i + offset : -1;
-    gt_before += gt ? 1u : 0u;
-    eq_before += eq ? 1u : 0u;
-  }
+    o[rank] = i < lens ? i + offset : -1;
+  });
+}
+
+// Long rows in two stages (the workspace form). Stage 1: each kTopkChunk-entry chunk of a row
+// selects its own best min(k, chunk) entries under the same order and writes them, in position
+// order, as (order key, position) at cand[row][chunk][rank] -- every entry of the row's best k
+// is among its chunk's best k, so the chunk lists hold the answer. Stage 2 selects the row's k
+// best from the concatenated lists (still in position order, so ties still resolve to the lowest
+// positions), one workgroup per row, keys in registers. Stage 1 spreads a row over
+// ceil(nb / kTopkChunk) workgroups instead of one.
+constexpr int kTopkChunk = 4096;
+
+__global__ __launch_bounds__(kSelThreads) void topk_chunk_kernel(const float* __restrict__ scores,
+                                                                 uint32_t* __restrict__ ckey,
+                                                                 int32_t* __restrict__ cpos, int nb, int k,
+                                                                 int chunks, int vec) {
+  constexpr int J = kTopkChunk / kSelThreads;
+  __shared__ RegSelShared sh;
+  const int64_t row = blockIdx.x / chunks;
+  const int ch = (int)(blockIdx.x - row * chunks);
+  const int base = ch * kTopkChunk;
+  const int count = min(kTopkChunk, nb - base);
+  const int kc = min(k, count);
+  const float* x = scores + row * nb + base;
+  const int64_t cbase = (row * chunks + ch) * (int64_t)k;
+  const int i0 = threadIdx.x * J;
+  const int nvalid = min(max(count - i0, 0), J);
+  uint32_t key[J];
+  load_keys<J>(x, i0, nvalid, vec, key);
+  select_top<J>(key, nvalid, kc, sh, [&](uint32_t rank, int j) {
+    ckey[cbase + rank] = key[j];
+    cpos[cbase + rank] = base + i0 + j;
+  });
+}
+
+template <int J>
+__global__ __launch_bounds__(kSelThreads) void topk_merge_kernel(const uint32_t* __restrict__ ckey,
+                                                                  const int32_t* __restrict__ cpos,
+                                                                  int32_t* __restrict__ out, int n, int nb, int k,
+                                                                  int chunks, int start_pos, int ratio, int offset) {
+  __shared__ RegSelShared sh;
+  const int64_t row = blockIdx.x;
+  // the lists of chunks 0..chunks-2 are full (k entries), the last one holds min(k, its count):
+  // the valid entries are the first m of the row's concatenation
+  const int m = (chunks - 1) * k + min(k, nb - (chunks - 1) * kTopkChunk);
+  const uint32_t* kr = ckey + row * (int64_t)chunks * k;
+  const int32_t* pr = cpos + row * (int64_t)chunks * k;
+  int32_t* o = out + row * k;
+  const int s = (int)(row % n);
+  const int lens = (start_pos + s + 1) / ratio;
+  const int i0 = threadIdx.x * J;
+  const int nvalid = min(max(m - i0, 0), J);
+  uint32_t key[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) key[j] = j < nvalid ? kr[i0 + j] : 0u;
+  select_top<J>(key, nvalid, k, sh, [&](uint32_t rank, int j) {
+    const int i = pr[i0 + j];
+    o[rank] = i < lens ? i + offset : -1;
+  });
 }
 
 // Rows longer than 32k scores: keys are re-read from memory in every pass.
@@ -319,9 +398,26 @@ __global__ __launch_bounds__(kSelThreads) void candidate_kernel(const float* __r
 
 using namespace dsv41;
 
-extern "C" int dsv41_topk_select(const float* scores, int32_t* out, int64_t rows, int32_t n, int32_t nb,
-                                 int32_t topk, int32_t start_pos, int32_t ratio, int32_t offset, hipStream_t stream) {
-  const char* what = "dsv41_topk_select";
+// The two-stage form for a row of nb scores: rows longer than one 16-keys-per-thread workgroup
+// holds, k at most half a chunk, and the chunk lists small enough for one register workgroup.
+static bool topk_two_stage(int nb, int k, int* chunks, int* jm) {
+  if (nb <= 16 * kSelThreads || 2 * k > kTopkChunk) return false;
+  const int c = (nb + kTopkChunk - 1) / kTopkChunk;
+  const int64_t m = (int64_t)c * k;
+  if (m > 32 * kSelThreads) return false;
+  *chunks = c;
+  *jm = m <= 4 * kSelThreads ? 4 : (m <= 8 * kSelThreads ? 8 : (m <= 16 * kSelThreads ? 16 : 32));
+  return true;
+}
+
+static size_t topk_ws_bytes(int64_t rows, int chunks, int k) {
+  const size_t list = ((size_t)rows * chunks * k * sizeof(uint32_t) + 255) & ~(size_t)255;
+  return 2 * list;                               // order keys, then positions
+}
+
+static int topk_launch(const char* what, const float* scores, int32_t* out, int64_t rows, int32_t n, int32_t nb,
+                       int32_t topk, int32_t start_pos, int32_t ratio, int32_t offset, void* workspace,
+                       size_t workspace_bytes, bool allow_two_stage, hipStream_t stream) {
   DSV41_REQUIRE(scores && out, DSV41_E_ARG, "%s: null tensor", what);
   DSV41_REQUIRE(rows >= 0 && n > 0 && nb >= 0 && topk >= 0 && start_pos >= 0 && ratio > 0, DSV41_E_ARG,
                 "%s: bad sizes", what);
@@ -331,6 +427,29 @@ extern "C" int dsv41_topk_select(const float* scores, int32_t* out, int64_t rows
   if (rows == 0 || k == 0) return 0;
   const dim3 grid((unsigned)rows), block(kSelThreads);
   const int vec = (nb % 4 == 0 && aligned16(scores)) ? 1 : 0;
+  int chunks = 0, jm = 0;
+  if (allow_two_stage && topk_two_stage(nb, k, &chunks, &jm)) {
+    const size_t need = topk_ws_bytes(rows, chunks, k);
+    DSV41_REQUIRE(workspace && workspace_bytes >= need, DSV41_E_WORKSPACE, "%s: workspace of %zu bytes needed", what,
+                  need);
+    DSV41_REQUIRE(aligned16(workspace), DSV41_E_ARG, "%s: workspace must be 16-byte aligned", what);
+    DSV41_REQUIRE(rows * chunks < (1ll << 31), DSV41_E_ARG, "%s: too many row chunks", what);
+    uint32_t* ckey = reinterpret_cast<uint32_t*>(workspace);
+    int32_t* cpos = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(workspace) + need / 2);
+    hipLaunchKernelGGL(topk_chunk_kernel, dim3((unsigned)(rows * chunks)), block, 0, stream, scores, ckey, cpos, nb, k,
+                       chunks, vec);
+    int rc = check_launch(what);
+    if (rc) return rc;
+#define DSV41_MERGE_CASE(J_)                                                                                 \
+    if (jm == J_) hipLaunchKernelGGL(topk_merge_kernel<J_>, grid, block, 0, stream, ckey, cpos, out, n, nb, k, \
+                                     chunks, start_pos, ratio, offset);
+    DSV41_MERGE_CASE(4)
+    DSV41_MERGE_CASE(8)
+    DSV41_MERGE_CASE(16)
+    DSV41_MERGE_CASE(32)
+#undef DSV41_MERGE_CASE
+    return check_launch(what);
+  }
   if (nb <= 4 * kSelThreads)
     hipLaunchKernelGGL(topk_reg_kernel<4>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset, vec);
   else if (nb <= 8 * kSelThreads)
@@ -344,6 +463,26 @@ extern "C" int dsv41_topk_select(const float* scores, int32_t* out, int64_t rows
   else
     hipLaunchKernelGGL(topk_kernel, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset);
   return check_launch(what);
+}
+
+extern "C" int dsv41_topk_select(const float* scores, int32_t* out, int64_t rows, int32_t n, int32_t nb,
+                                 int32_t topk, int32_t start_pos, int32_t ratio, int32_t offset, hipStream_t stream) {
+  return topk_launch("dsv41_topk_select", scores, out, rows, n, nb, topk, start_pos, ratio, offset, nullptr, 0, false,
+                     stream);
+}
+
+extern "C" size_t dsv41_topk_workspace_bytes(int64_t rows, int32_t nb, int32_t topk) {
+  if (rows <= 0 || nb <= 0 || topk <= 0) return 0;
+  const int k = topk < nb ? topk : nb;
+  int chunks = 0, jm = 0;
+  return topk_two_stage(nb, k, &chunks, &jm) ? topk_ws_bytes(rows, chunks, k) : 0;
+}
+
+extern "C" int dsv41_topk_select_ws(const float* scores, int32_t* out, int64_t rows, int32_t n, int32_t nb,
+                                    int32_t topk, int32_t start_pos, int32_t ratio, int32_t offset, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream) {
+  return topk_launch("dsv41_topk_select_ws", scores, out, rows, n, nb, topk, start_pos, ratio, offset, workspace,
+                     workspace_bytes, true, stream);
 }
 
 extern "C" int dsv41_candidate_blocks(const float* scores, uint8_t* keep, int64_t rows, int32_t n, int32_t nb,

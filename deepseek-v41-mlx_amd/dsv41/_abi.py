@@ -60,6 +60,8 @@ _SIGNATURES = {
     "dsv41_indexer_score_mxfp4": [_c_p, _c_p, _c_p, _f32, _c_p, _i64, _c_p, _i64, _c_p, _c_p, _i32, _i32,
                                   _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_topk_select": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_topk_workspace_bytes": [_i64, _i32, _i32],
+    "dsv41_topk_select_ws": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_candidate_blocks": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _i32, _i32, _c_p],
     "dsv41_sparse_mla_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32],
     "dsv41_sparse_attn": [_c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
@@ -82,6 +84,7 @@ _SIGNATURES = {
 }
 _RESTYPES = {
     "dsv41_sparse_mla_workspace_bytes": _sz,
+    "dsv41_topk_workspace_bytes": _sz,
     "dsv41_version": ctypes.c_char_p,
     "dsv41_last_error_string": ctypes.c_char_p,
 }
@@ -496,10 +499,16 @@ def indexer_score_mxfp4(q_mx, w_raw, w_scale, k_codes, k_scales, nb, start_pos, 
     return out
 
 
-def topk_select(scores, topk, start_pos, ratio, offset):
-    """scores [b, n, nb] fp32 -> int32 [b, n, min(topk, nb)]."""
-    name = "dsv41_topk_select"
-    _gpu(name, scores)
+def topk_workspace_bytes(rows, nb, topk) -> int:
+    return int(lib().dsv41_topk_workspace_bytes(rows, nb, topk))
+
+
+def topk_select(scores, topk, start_pos, ratio, offset, workspace=None):
+    """scores [b, n, nb] fp32 -> int32 [b, n, min(topk, nb)]. Rows longer than 16384 scores
+    (k <= 2048) are selected in two stages through a uint8 workspace of topk_workspace_bytes(...)
+    bytes, allocated when it is omitted or too small."""
+    name = "dsv41_topk_select_ws"
+    _gpu(name, scores, workspace)
     _contig(name, scores)
     if scores.dtype != torch.float32 or scores.dim() != 3:
         raise ValueError(f"{name}: scores must be fp32 [b, n, nb]")
@@ -507,8 +516,11 @@ def topk_select(scores, topk, start_pos, ratio, offset):
     k = min(topk, nb)
     out = torch.empty(b, n, k, dtype=torch.int32, device=scores.device)
     if out.numel():
-        _call(name, _ptr(scores), _ptr(out), b * n, n, nb, topk, start_pos, ratio, offset,
-              _stream(scores))
+        ws_bytes = topk_workspace_bytes(b * n, nb, topk)
+        ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else _workspace(ws_bytes,
+                                                                                                 scores.device)
+        _call(name, _ptr(scores), _ptr(out), b * n, n, nb, topk, start_pos, ratio, offset, _ptr(ws),
+              ws_bytes, _stream(scores))
     return out
 
 

@@ -233,6 +233,17 @@ int dsv41_topk_select(const float* scores, int32_t* out, int64_t rows, int32_t n
                       int32_t topk, int32_t start_pos, int32_t ratio, int32_t offset,
                       hipStream_t stream);
 
+/* The same selection with a caller-owned workspace (same reference function,
+ * deepseek_v41_mlx/indexer.py:200-204; identical results): rows longer than 16384 scores with
+ * k <= 2048 are then selected in two stages (each 4096-score chunk's best k, then the best k of
+ * those lists), spreading a row over several workgroups. The workspace is
+ * dsv41_topk_workspace_bytes(rows, nb, topk) bytes, 16-byte aligned (0: one stage, workspace
+ * may be null). */
+size_t dsv41_topk_workspace_bytes(int64_t rows, int32_t nb, int32_t topk);
+int dsv41_topk_select_ws(const float* scores, int32_t* out, int64_t rows, int32_t n, int32_t nb,
+                         int32_t topk, int32_t start_pos, int32_t ratio, int32_t offset,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* select_candidate_blocks, deepseek_v41_mlx/indexer.py:38-64: block maxima over blocks of
  * block_size (padded with -inf), the block holding position lens-1 pinned to +inf, the best
  * min(topk_blocks, n_blocks) blocks kept (ties -> lowest block) when their value is > -inf,

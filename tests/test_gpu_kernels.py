@@ -392,17 +392,30 @@ def _score_sets(rng, b, n, nb):
                                                   (1, 64, 1000, 256, 3000, 4), (2, 1, 16384, 512, 65535, 4),
                                                   (1, 2, 300, 512, 1199, 4), (1, 5, 2049, 2048, 8191, 4),
                                                   (1, 2, 32768, 2048, 131071, 4), (1, 3, 5001, 700, 20003, 4),
-                                                  (1, 1, 40000, 1000, 159999, 4), (1, 1, 20000, 5000, 79999, 4)])
+                                                  (1, 1, 40000, 1000, 159999, 4), (1, 1, 20000, 5000, 79999, 4),
+                                                  (2, 3, 16390, 512, 65559, 4), (1, 2, 20481, 64, 81923, 4)])
 def test_topk_bit_exact(gpu, b, n, nb, topk, start, r):
+    """Rows over 16384 scores with k <= 2048 take the two-stage form (chunk lists, then a merge);
+    the last two cases give it a last chunk shorter than k and rows that are not 16-byte
+    multiples. The one-stage entry point must agree bit for bit on those rows too."""
+    import ctypes
     from dsv41 import _abi
     rng = rng_for(f"topk{nb}{n}")
+    two_stage = _abi.topk_workspace_bytes(b * n, nb, topk) > 0
     for s in _score_sets(rng, b, n, nb):
         lens = R.query_lens(start, n, r)
         s = np.where(np.arange(nb)[None, None] < lens[None, :, None], s, -np.inf).astype(F32)
         off = 129
-        got = _abi.topk_select(dev(s), topk, start, r, off).cpu().numpy()
+        st = dev(s)
+        got = _abi.topk_select(st, topk, start, r, off)
         want = R.topk_indices(s, topk, lens, off)
-        assert np.array_equal(got, want), f"nb={nb} topk={topk}"
+        assert np.array_equal(got.cpu().numpy(), want), f"nb={nb} topk={topk}"
+        if two_stage:
+            one = torch.empty_like(got)
+            rc = _abi.lib().dsv41_topk_select(ctypes.c_void_p(st.data_ptr()), ctypes.c_void_p(one.data_ptr()),
+                                              b * n, n, nb, topk, start, r, off,
+                                              ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            assert rc == 0 and torch.equal(one, got)
 
 
 @pytest.mark.parametrize("b,n,nb,tb,bs,start,r", [(2, 3, 40, 3, 2, 100, 4), (1, 7, 333, 20, 8, 1200, 4),
