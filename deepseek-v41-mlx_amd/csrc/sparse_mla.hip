@@ -267,6 +267,7 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   const uint32_t ring_base = lds_offset(ring);
   const uint64_t comp8 = F8 ? reinterpret_cast<uint64_t>(S.comp) + (uint64_t)b * (uint64_t)S.comp_bstride : 0ull;
   const uint64_t scal8 = F8 ? reinterpret_cast<uint64_t>(S.comp_scale) + (uint64_t)b * (uint64_t)S.comp_scale_bstride : 0ull;
+  const int rbs = S.comp_scale_rb == 32 ? 5 : 0;   // scale row block (1 or 32) as a shift
   auto issue = [&](int t, bool direct) {
     const int slot = t % NS;
     const int mine = t * R + wave * RPW + (lane % RPW);
@@ -281,7 +282,7 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
         // lanes 0..31: the row's 512 fp8 bytes; lane 32: its 16 scale bytes
         const uint64_t ci = ent >> 1;
         const uint64_t src = lane < D / 16 ? comp8 + ci * D + (uint64_t)lane * 16u
-                                           : scal8 + (ci / (uint64_t)S.comp_scale_rb) * (D / 32);
+                                           : scal8 + (ci >> rbs) * (D / 32);
         if (lane <= D / 16) dma16_vaddr(src, dst + rr * RS + D);
       } else {
         dma_row<D>(ent, dst + rr * RS, lane);
@@ -327,21 +328,24 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   for (int t = 0; t < nsteps; ++t) {
     wait_steps<NL>(min(nsteps - 1 - t, NS - 2));
     if constexpr (F8) {
-      // this wave's own fp8 rows of step t have landed: dequantize them in place. One read of
-      // the whole row precedes the writes (a single wave converts a row), so the bf16 output
-      // may overlap the fp8 bytes it came from.
-      uint8_t* sb = ring + (t % NS) * SLOT;
+      // this wave's own fp8 rows of step t have landed: dequantize them in place. All of its
+      // rows are read before any is written (a single wave converts them), so the bf16 output
+      // may overlap the fp8 bytes it came from, and the reads go out together.
+      uint8_t* sb = ring + (t % NS) * SLOT + wave * RPW * RS;
+      uint2 c8[RPW];
+      float sc[RPW];
+      bool has[RPW];
 #pragma unroll
       for (int rr = 0; rr < RPW; ++rr) {
         const int ei = t * R + wave * RPW + rr;
-        const uint64_t ent = ei < cnt ? rows[ei] : 0ull;
-        if (ent & 1ull) {
-          uint8_t* row = sb + (wave * RPW + rr) * RS;
-          const uint2 c8 = *reinterpret_cast<const uint2*>(row + D + lane * 8);
-          const float sc = e8m0_to_float(row[2 * D + (lane >> 2)]);
-          *reinterpret_cast<bf16x8*>(row + lane * 16) = dequant_e4m3x8(c8.x, c8.y, sc);
-        }
+        has[rr] = ((ei < cnt ? rows[ei] : 0ull) & 1ull) != 0ull;
+        const uint8_t* row = sb + rr * RS;
+        c8[rr] = *reinterpret_cast<const uint2*>(row + D + lane * 8);
+        sc[rr] = e8m0_to_float(row[2 * D + (lane >> 2)]);
       }
+#pragma unroll
+      for (int rr = 0; rr < RPW; ++rr)
+        if (has[rr]) *reinterpret_cast<bf16x8*>(sb + rr * RS + lane * 16) = dequant_e4m3x8(c8[rr].x, c8[rr].y, sc[rr]);
     }
     __syncthreads();                       // step t landed; every wave is done with step t-1
     const int slot = t % NS;
