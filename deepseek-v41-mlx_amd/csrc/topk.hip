@@ -145,7 +145,8 @@ struct RegSelShared {
 // (consecutive, in position order), valid for j < nvalid; 1 <= k <= the number of valid entries.
 // Finds the k-th best key T and how many T-valued entries to take, then calls emit(rank, j) for
 // each selected entry j of this thread, rank = its place among the selected in entry order (so
-// ties resolve to the lowest entries). All threads of the workgroup must call it.
+// ties resolve to the lowest entries); j is a run-time index, so emit must not index register
+// arrays with it. All threads of the workgroup must call it.
 template <int J, typename Emit>
 __device__ __forceinline__ void select_top(const uint32_t (&key)[J], int nvalid, int k, RegSelShared& sh, Emit emit) {
   constexpr int NBIN = 2048;
@@ -217,17 +218,25 @@ __device__ __forceinline__ void select_top(const uint32_t (&key)[J], int nvalid,
   if (lane == 63) sh.wsum[wave] = incl;          // last read before the final pass barrier
   __syncthreads();
   const uint32_t excl = wave_base() + incl - packed;
-  uint32_t gt_before = excl >> 16, eq_before = excl & 0xFFFFu;
-  // branch-free walk in entry order: a key > T goes to gt_before + min(eq_before, need), a
-  // key == T to gt_before + eq_before while eq_before < need
+  const uint32_t gt_before = excl >> 16;
+  uint32_t eq_before = excl & 0xFFFFu;
+  // Every key > T is taken, and a key == T while fewer than `need` equal keys precede it; each
+  // taken entry occupies the next rank, so this thread's m-th taken entry has rank
+  // gt_before + min(eq_before, need) + m. The take mask is formed branch-free, then only its set
+  // bits are visited (a thread takes few entries).
+  const uint32_t base = gt_before + min(eq_before, need);
+  uint32_t tmask = 0u;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const bool ok = j < nvalid;
     const bool gt = ok && key[j] > T, eq = ok && key[j] == T;
-    const bool take = gt || (eq && eq_before < need);
-    if (take) emit(gt_before + min(eq_before, need), j);
-    gt_before += gt ? 1u : 0u;
+    tmask |= (gt || (eq && eq_before < need)) ? (1u << j) : 0u;
     eq_before += eq ? 1u : 0u;
+  }
+  for (uint32_t m = 0u; tmask != 0u; ++m) {
+    const int j = __builtin_ctz(tmask);
+    emit(base + m, j);
+    tmask &= tmask - 1u;
   }
 }
 
@@ -303,7 +312,7 @@ __global__ __launch_bounds__(kSelThreads) void topk_chunk_kernel(const float* __
   uint32_t key[J];
   load_keys<J>(x, i0, nvalid, vec, key);
   select_top<J>(key, nvalid, kc, sh, [&](uint32_t rank, int j) {
-    ckey[cbase + rank] = key[j];
+    ckey[cbase + rank] = order_key(x[i0 + j]);     // re-read: j is a run-time index
     cpos[cbase + rank] = base + i0 + j;
   });
 }
