@@ -368,39 +368,68 @@ __global__ __launch_bounds__(kSelThreads) void topk_kernel(const float* __restri
 
 constexpr int kMaxCandBlocks = 8192;
 
+// select_candidate_blocks on the register core: thread t holds the maxima of blocks t*J ..
+// t*J+J-1 as order keys (the pinned block (lens-1)/bs as +inf); the best min(topk_blocks, nblk)
+// blocks (ties -> lowest block) are marked, and a marked block is kept when its maximum is
+// > -inf. Each thread then writes the keep bytes of its own blocks.
+template <int J>
 __global__ __launch_bounds__(kSelThreads) void candidate_kernel(const float* __restrict__ scores,
                                                                 uint8_t* __restrict__ keep, int n, int nb,
                                                                 int topk_blocks, int bs, const int32_t* lens_v,
-                                                                int start_pos, int ratio) {
-  __shared__ SelShared sh;
-  __shared__ float bmax[kMaxCandBlocks];
-  __shared__ uint8_t bkeep[kMaxCandBlocks];
+                                                                int start_pos, int ratio, int vec8) {
+  __shared__ RegSelShared sh;
+  __shared__ uint8_t marked[kMaxCandBlocks];
   const int64_t row = blockIdx.x;
   const float* x = scores + row * nb;
   const int s = (int)(row % n);
   const int lens = lens_v ? lens_v[s] : (start_pos + s + 1) / ratio;
   const int nblk = (nb + bs - 1) / bs;
   const int last = lens > 0 ? (lens - 1) / bs : -1;  // floor((lens - 1) / bs)
-  for (int j = threadIdx.x; j < nblk; j += kSelThreads) {
+  const int j0 = threadIdx.x * J;
+  const int nvalid = min(max(nblk - j0, 0), J);
+  float bm[J];
+  uint32_t key[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
     float m = -INFINITY;
-    const int e = min(nb, (j + 1) * bs);
-    for (int t = j * bs; t < e; ++t) m = fmaxf(m, x[t]);
-    bmax[j] = j == last ? INFINITY : m;
-    bkeep[j] = 0;
+    const int blk = j0 + j;
+    if (j < nvalid) {
+      if (vec8 && blk * 8 + 8 <= nb) {                 // 8-score block, 16-byte aligned
+        const float4 u = *reinterpret_cast<const float4*>(x + blk * 8);
+        const float4 v = *reinterpret_cast<const float4*>(x + blk * 8 + 4);
+        m = fmaxf(fmaxf(fmaxf(u.x, u.y), fmaxf(u.z, u.w)), fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+      } else {
+        const int e = min(nb, (blk + 1) * bs);
+        for (int t = blk * bs; t < e; ++t) m = fmaxf(m, x[t]);
+      }
+    }
+    bm[j] = blk == last ? INFINITY : m;
+    key[j] = order_key(bm[j]);
+    if (j < nvalid) marked[blk] = 0;
   }
-  __syncthreads();
   const int kb = min(topk_blocks, nblk);
   if (kb >= nblk) {
-    for (int j = threadIdx.x; j < nblk; j += kSelThreads) bkeep[j] = bmax[j] > -INFINITY ? 1 : 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (j < nvalid) marked[j0 + j] = 1;
   } else if (kb > 0) {
-    auto key = [&](int j) { return order_key(bmax[j]); };
-    int need = 0;
-    const uint32_t T = radix_select(sh, key, nblk, kb, &need);
-    ordered_select(sh, key, nblk, T, need, [&](int j, int) { bkeep[j] = bmax[j] > -INFINITY ? 1 : 0; });
+    select_top<J>(key, nvalid, kb, sh, [&](uint32_t, int j) { marked[j0 + j] = 1; });
   }
   __syncthreads();
   uint8_t* kr = keep + row * nb;
-  for (int t = threadIdx.x; t < nb; t += kSelThreads) kr[t] = bkeep[t / bs];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    if (j >= nvalid) continue;
+    const int blk = j0 + j;
+    const uint8_t v = (marked[blk] && bm[j] > -INFINITY) ? 1 : 0;
+    if (vec8 && blk * 8 + 8 <= nb) {
+      const uint32_t w = v ? 0x01010101u : 0u;
+      *reinterpret_cast<uint2*>(kr + blk * 8) = make_uint2(w, w);
+    } else {
+      const int e = min(nb, (blk + 1) * bs);
+      for (int t = blk * bs; t < e; ++t) kr[t] = v;
+    }
+  }
 }
 
 }  // namespace dsv41
@@ -505,7 +534,15 @@ extern "C" int dsv41_candidate_blocks(const float* scores, uint8_t* keep, int64_
                 what, kMaxCandBlocks);
   DSV41_REQUIRE(rows < (1ll << 31), DSV41_E_ARG, "%s: too many rows", what);
   if (rows == 0 || nb == 0) return 0;
-  hipLaunchKernelGGL(candidate_kernel, dim3((unsigned)rows), dim3(kSelThreads), 0, stream, scores, keep, n, nb,
-                     topk_blocks, block_size, lens, start_pos, ratio);
+  const int nblk = (nb + block_size - 1) / block_size;
+  // 8-score blocks read as two float4 and written as 8 keep bytes: rows 16-byte aligned
+  const int vec8 = (block_size == 8 && nb % 4 == 0 && aligned16(scores) &&
+                    (reinterpret_cast<uintptr_t>(keep) & 7u) == 0 && nb % 8 == 0) ? 1 : 0;
+  if (nblk <= 4 * kSelThreads)
+    hipLaunchKernelGGL(candidate_kernel<4>, dim3((unsigned)rows), dim3(kSelThreads), 0, stream, scores, keep, n, nb,
+                       topk_blocks, block_size, lens, start_pos, ratio, vec8);
+  else
+    hipLaunchKernelGGL(candidate_kernel<8>, dim3((unsigned)rows), dim3(kSelThreads), 0, stream, scores, keep, n, nb,
+                       topk_blocks, block_size, lens, start_pos, ratio, vec8);
   return check_launch(what);
 }

@@ -419,7 +419,9 @@ def test_topk_bit_exact(gpu, b, n, nb, topk, start, r):
 
 
 @pytest.mark.parametrize("b,n,nb,tb,bs,start,r", [(2, 3, 40, 3, 2, 100, 4), (1, 7, 333, 20, 8, 1200, 4),
-                                                   (2, 1, 16384, 2048, 8, 65535, 4), (1, 4, 64, 100, 3, 0, 1)])
+                                                   (2, 1, 16384, 2048, 8, 65535, 4), (1, 4, 64, 100, 3, 0, 1),
+                                                   (2, 2, 32768, 1024, 8, 131071, 4),    # 4096 blocks, vector path
+                                                   (1, 3, 65536, 2048, 8, 262140, 4)])   # 8192 blocks
 def test_candidate_blocks_bit_exact(gpu, b, n, nb, tb, bs, start, r):
     from dsv41 import _abi
     from dsv41.indexer import select_candidate_blocks
