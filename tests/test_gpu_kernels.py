@@ -448,6 +448,8 @@ def test_candidate_blocks_bit_exact(gpu, b, n, nb, tb, bs, start, r):
     ("bf16", 1, 4, 4, 64, 50, 33),         # heads < 16 (masked head tile)
     ("bf16", 1, 640, 64, 512, 2000, 96),   # >= 512 queries: the prefill kernel
     ("bf16", 2, 300, 48, 128, 700, 130),   # prefill kernel, partial 64-head group
+    ("bf16", 1, 520, 64, 512, 100, 20),    # prefill kernel, one step (pipelined order's edges)
+    ("bf16", 1, 512, 64, 256, 300, 50),    # prefill kernel, two steps
     ("bf16", 1, 1, 16, 576, 41000, 40000),  # 18 splits: partials beyond the combine's register set
 ])
 def test_sparse_attn(gpu, dt, b, m, h, d, nkv, k):
