@@ -89,6 +89,24 @@ def test_contract_violations_are_reported_by_the_library():
     rc = lib.dsv41_compress_pool(fake, fake, fake, fake, fake, fake, 1, 1, 64, 1, 0, ctypes.c_float(0),
                                  1, None)
     assert rc == -1 and b"ratio" in lib.dsv41_last_error_string()
+    # two-stage top-k: the workspace is checked before any launch
+    need = _abi.topk_workspace_bytes(16, 32768, 1024)
+    rc = lib.dsv41_topk_select_ws(fake, fake, 16, 1, 32768, 1024, 131071, 4, 129, None, 0, None)
+    assert rc == -4 and b"workspace" in lib.dsv41_last_error_string()
+    rc = lib.dsv41_topk_select_ws(fake, fake, 16, 1, 32768, 1024, 131071, 4, 129, fake, need - 1, None)
+    assert rc == -4
+
+
+def test_topk_workspace_sizes():
+    """Two stages (a workspace) only for rows over 16384 scores with k <= 2048 whose chunk lists
+    fit one register workgroup: keys and positions of each 4096-score chunk's best k."""
+    from dsv41 import _abi
+    assert _abi.topk_workspace_bytes(32, 16384, 512) == 0            # one workgroup per row
+    assert _abi.topk_workspace_bytes(16, 20000, 5000) == 0           # k above half a chunk
+    assert _abi.topk_workspace_bytes(1, 4 << 20, 2048) == 0          # lists too long for one stage-2 group
+    assert _abi.topk_workspace_bytes(16, 32768, 1024) == 2 * 16 * 8 * 1024 * 4
+    assert _abi.topk_workspace_bytes(3, 16390, 512) == 2 * (((3 * 5 * 512 * 4) + 255) // 256 * 256)
+    assert _abi.topk_workspace_bytes(0, 32768, 1024) == 0
 
 
 # ------------------------------------------------------------------ host logic
