@@ -12,10 +12,10 @@
 //     V^T through the LDS transpose read ds_read_b64_tr_b16).
 // Selected rows are gathered with global_load_lds_dwordx4 (one 1 KB row per wave instruction at
 // d = 512) into LDS ring buffers, so several tiles are in flight without staging registers.
-// Decode (few queries) splits each query's index list across workgroups; a combine kernel
-// merges the partial (max, denominator, numerator) triples. The epilogue divides, rounds to bf16
-// as the reference does, then applies the inverse rope to the last rd channels
-// (attention.py:174-175).
+// Decode (few queries) splits each query's index list across workgroups (two per CU in the
+// half-LDS instance); a combine kernel merges the per-split partials (normalized bf16 numerator,
+// fp32 max and denominator). The epilogue divides, rounds to bf16 as the reference does, then
+// applies the inverse rope to the last rd channels (attention.py:174-175).
 //
 // fp32 kernel: a plain FMA implementation for the 1e-5 parity configs.
 #include "mfma.h"

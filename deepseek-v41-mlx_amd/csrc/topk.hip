@@ -5,13 +5,15 @@
 // to mx.argpartition, tests/test_parity.py:17-21), -0.0 equal to +0.0. Output positions are
 // ascending, mapped to idx + offset when idx < lens and -1 otherwise.
 //
-// One 1024-thread workgroup per score row. A 4-pass, 8-bit MSD radix select over
-// order-preserving 32-bit keys finds the k-th best key T and how many T-valued keys to keep
-// (per-wave histograms in LDS keep atomics uncontended); one ordered compaction pass then
-// writes every key > T plus the first `need` keys == T, in position order (wave ballots and
-// popcounts give each selected key its rank) -- so the output comes out sorted and ties
-// resolve to the lowest positions by construction. Rows up to 32k scores keep their keys in
-// registers for the whole selection.
+// One 1024-thread workgroup per score row. Rows of up to 32K scores (topk_reg_kernel) keep
+// their keys in registers, J consecutive positions per thread, as order-preserving 32-bit keys;
+// an MSD radix select over digits of 11, 11 and 10 bits finds the k-th best key T and how many
+// T-valued keys to take, then one block scan of per-thread (greater, equal) counts gives each
+// thread the rank of its first selection and it writes its selections in position order -- the
+// output comes out sorted and ties resolve to the lowest positions by construction. Rows over
+// 16K scores with k <= 2048 can go in two stages through a workspace (per-chunk lists of the
+// chunk's best k, then a merge); candidate blocks run the same register core over block maxima.
+// Longer rows fall back to topk_kernel (4-pass, 8-bit digits, keys re-read from memory).
 #include "common.h"
 
 namespace dsv41 {
