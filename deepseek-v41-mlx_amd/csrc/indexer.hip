@@ -17,6 +17,7 @@
 // Rows past a query's visibility are written as -inf without touching the cache (causal
 // prefill skips about half the bytes).
 #include "mfma.h"
+#include "select.h"
 
 namespace dsv41 {
 
@@ -201,12 +202,18 @@ template <bool F8> struct DecKeys {
   __device__ static int swz(int rloc) { return F8 ? ((rloc >> 1) & 7) : (rloc & 15); }
 };
 
-template <int HT, int NW, bool F8>
+// TJ > 0: the fused top-k form (decode). Instead of writing its scores, the workgroup selects
+// the best min(topk, rows) of its row range (TJ scores per thread, ties -> lowest position) and
+// writes them in position order as (order key, position) at ckey/cpos[(qi * chunks + range) *
+// topk ...]; topk_merge_launch then selects each query's topk from those lists. The range's
+// best topk contain every entry of the row's best topk, so the result is the top-k of the
+// scores exactly.
+template <int HT, int NW, bool F8, int TJ>
 __global__ __launch_bounds__(NW * 64) void indexer_decode_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ w_raw, float w_scale, const void* __restrict__ kcache,
     int64_t k_bstride, const uint8_t* __restrict__ kscale, int64_t ks_bstride, int ks_rb,
     const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int nb, int start_pos, int ratio,
-    int rows_per_wg) {
+    int rows_per_wg, int topk, uint32_t* __restrict__ ckey, int32_t* __restrict__ cpos) {
   using K = DecKeys<F8>;
   constexpr int H = HT * 16, DIM = 128, KS = 4, QROW = DIM * 2;
   constexpr int QCOPIES = H * QROW / 1024;                 // 1 KB copies of the query block
@@ -228,9 +235,17 @@ __global__ __launch_bounds__(NW * 64) void indexer_decode_kernel(
   const int r0 = blockIdx.x * rows_per_wg;
   const int r1 = min(r0 + rows_per_wg, nb);
   const int vis_end = max(r0, min(r1, lens));
-  float* out = scores + (int64_t)qi * nb;
+  float* out = TJ ? nullptr : scores + (int64_t)qi * nb;
+  const int64_t cbase = ((int64_t)qi * gridDim.x + blockIdx.x) * topk;   // this range's list (TJ > 0)
   if (vis_end <= r0) {                     // uniform: nothing visible in this row range
-    for (int t = r0 + tid; t < r1; t += NW * 64) out[t] = -INFINITY;
+    if constexpr (TJ > 0) {                // all -inf: the lowest positions are the best
+      for (int t = tid; t < min(topk, r1 - r0); t += NW * 64) {
+        ckey[cbase + t] = order_key(-INFINITY);
+        cpos[cbase + t] = r0 + t;
+      }
+    } else {
+      for (int t = r0 + tid; t < r1; t += NW * 64) out[t] = -INFINITY;
+    }
     return;
   }
   const int nt = (vis_end - r0 + 16 * NW - 1) / (16 * NW);   // tiles per wave (the last ones clamped)
@@ -336,10 +351,24 @@ __global__ __launch_bounds__(NW * 64) void indexer_decode_kernel(
   wait_vmcnt<0>();                         // no copy may land in LDS after the workgroup ends
   __syncthreads();                         // every score of the range is in LDS
   const uint8_t* cb = cand ? cand + (int64_t)qi * nb : nullptr;
-  for (int t = tid; t < r1 - r0; t += NW * 64) {
-    float v = -INFINITY;
-    if (t < vis_end - r0 && (!cb || cb[r0 + t])) v = sc_lds[t];
-    out[r0 + t] = v;
+  auto value = [&](int t) {                // the score of row r0 + t as the unfused form writes it
+    return (t < vis_end - r0 && (!cb || cb[r0 + t])) ? sc_lds[t] : -INFINITY;
+  };
+  if constexpr (TJ > 0) {
+    static_assert(TJ % 4 == 0 || TJ < 4, "keys per thread");
+    RegSelShared& sh = *reinterpret_cast<RegSelShared*>(ring);   // the ring is free past the loop
+    const int count = r1 - r0;
+    const int i0 = tid * TJ;
+    const int nvalid = min(max(count - i0, 0), TJ);
+    uint32_t key[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) key[j] = j < nvalid ? order_key(value(i0 + j)) : 0u;
+    select_top<TJ, NW * 64>(key, nvalid, min(topk, count), sh, [&](uint32_t rank, int j) {
+      ckey[cbase + rank] = order_key(value(i0 + j));             // re-read: j is a run-time index
+      cpos[cbase + rank] = r0 + i0 + j;
+    });
+  } else {
+    for (int t = tid; t < r1 - r0; t += NW * 64) out[r0 + t] = value(t);
   }
 }
 
@@ -679,9 +708,9 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
   if (dim == 128 && (heads == 64 || heads == 32 || heads == 16) && aligned16(w_raw) && rows_per_wg <= kIdxMaxRows) {
 #define DSV41_DEC_CASE(HT_)                                                                                   \
     if (heads == HT_ * 16) {                                                                                  \
-      hipLaunchKernelGGL((indexer_decode_kernel<HT_, kDecWaves, false>), grid, dim3(kDecWaves * 64), 0,       \
+      hipLaunchKernelGGL((indexer_decode_kernel<HT_, kDecWaves, false, 0>), grid, dim3(kDecWaves * 64), 0,    \
                          stream, (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, index_k, k_bstride, nullptr, \
-                         0, 1, candidates, scores, n, nb, start_pos, ratio, rows_per_wg);                     \
+                         0, 1, candidates, scores, n, nb, start_pos, ratio, rows_per_wg, 0, nullptr, nullptr); \
       return check_launch(what);                                                                              \
     }
     DSV41_DEC_CASE(4)
@@ -707,6 +736,25 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
   DSV41_IDX_CASE(4, 1)
 #undef DSV41_IDX_CASE
   return set_error(DSV41_E_SHAPE, "%s: bf16 path has no instance for heads=%d dim=%d", what, heads, dim);
+}
+
+// The fused decode form (indexer_decode_kernel with TJ > 0, then the top-k merge): shapes the
+// staged-copy decode kernel serves (bf16 keys of 128 channels, 16/32/64 heads, fewer than 8
+// queries per row or a candidate mask) with row ranges of 2048 or 4096 rows at least twice k.
+static bool idx_topk_plan(int64_t bsz, int n, int heads, int dim, int nb, int k, bool cand, int* rows_per_wg,
+                          dim3* grid, int* tj) {
+  if (dim != 128 || !(heads == 64 || heads == 32 || heads == 16)) return false;
+  if ((n >= 8 && !cand) || bsz * n >= 65536) return false;
+  *grid = idx_grid((int64_t)nb * bsz * n, nb, (int)(bsz * n), rows_per_wg);
+  if (*rows_per_wg == 2048) *tj = 4;
+  else if (*rows_per_wg == 4096) *tj = 8;
+  else return false;
+  return 2 * k <= *rows_per_wg && (int64_t)grid->x * k <= 32 * kSelThreads;
+}
+
+static size_t idx_topk_ws(int64_t rows, unsigned chunks, int k) {
+  const size_t list = ((size_t)rows * chunks * k * sizeof(uint32_t) + 255) & ~(size_t)255;
+  return 2 * list;                                 // order keys, then positions
 }
 
 extern "C" int dsv41_indexer_score_fp8(const void* q, const void* w_raw, float w_scale, const uint8_t* index_k,
@@ -735,9 +783,10 @@ extern "C" int dsv41_indexer_score_fp8(const void* q, const void* w_raw, float w
       ks_bstride % 16 == 0 && rows_per_wg <= kIdxMaxRows) {
 #define DSV41_DEC8_CASE(HT_)                                                                                  \
     if (heads == HT_ * 16) {                                                                                  \
-      hipLaunchKernelGGL((indexer_decode_kernel<HT_, kDecWaves, true>), grid, dim3(kDecWaves * 64), 0, stream, \
-                         (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, index_k, k_bstride, k_scale,         \
-                         ks_bstride, ks_rb, candidates, scores, n, nb, start_pos, ratio, rows_per_wg);        \
+      hipLaunchKernelGGL((indexer_decode_kernel<HT_, kDecWaves, true, 0>), grid, dim3(kDecWaves * 64), 0,     \
+                         stream, (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, index_k, k_bstride, k_scale, \
+                         ks_bstride, ks_rb, candidates, scores, n, nb, start_pos, ratio, rows_per_wg, 0,       \
+                         nullptr, nullptr);                                                                   \
       return check_launch(what);                                                                              \
     }
     DSV41_DEC8_CASE(4)
@@ -790,4 +839,56 @@ extern "C" int dsv41_indexer_score_mxfp4(const uint8_t* q_codes, const uint8_t* 
   DSV41_IDXMX_CASE(1)
 #undef DSV41_IDXMX_CASE
   return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
+}
+
+extern "C" size_t dsv41_indexer_topk_workspace_bytes(int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
+                                                     int32_t topk, int32_t has_candidates) {
+  if (bsz <= 0 || n <= 0 || nb <= 0 || topk <= 0 || heads <= 0 || dim <= 0) return 0;
+  const int k = topk < nb ? topk : nb;
+  int rpw = 0, tj = 0;
+  dim3 grid;
+  if (!idx_topk_plan(bsz, n, heads, dim, nb, k, has_candidates != 0, &rpw, &grid, &tj)) return 0;
+  return idx_topk_ws((int64_t)bsz * n, grid.x, k);
+}
+
+extern "C" int dsv41_indexer_topk(const void* q, const void* w_raw, float w_scale, const void* index_k,
+                                  int64_t k_bstride, const uint8_t* candidates, int32_t* out, int32_t bsz, int32_t n,
+                                  int32_t heads, int32_t dim, int32_t nb, int32_t start_pos, int32_t ratio,
+                                  int32_t topk, int32_t offset, void* workspace, size_t workspace_bytes,
+                                  hipStream_t stream) {
+  const char* what = "dsv41_indexer_topk";
+  DSV41_REQUIRE(q && w_raw && index_k && out, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(bsz >= 0 && n > 0 && heads > 0 && dim > 0 && nb >= 0 && start_pos >= 0 && ratio > 0 && topk >= 0,
+                DSV41_E_ARG, "%s: bad sizes", what);
+  DSV41_REQUIRE(k_bstride >= (int64_t)nb * dim, DSV41_E_ARG, "%s: k_bstride %lld < nb*dim", what,
+                (long long)k_bstride);
+  DSV41_REQUIRE(aligned16(q) && aligned16(index_k) && aligned16(w_raw) && k_bstride % 8 == 0, DSV41_E_ARG,
+                "%s: q, w_raw and index_k must be 16-byte aligned, k_bstride a multiple of 8", what);
+  const int k = topk < nb ? topk : nb;
+  if ((int64_t)bsz * n == 0 || nb == 0 || k == 0) return 0;
+  int rows_per_wg = 0, tj = 0;
+  dim3 grid;
+  DSV41_REQUIRE(idx_topk_plan(bsz, n, heads, dim, nb, k, candidates != nullptr, &rows_per_wg, &grid, &tj),
+                DSV41_E_SHAPE, "%s: shape not served by the fused form (dsv41_indexer_topk_workspace_bytes is 0)",
+                what);
+  const size_t need = idx_topk_ws((int64_t)bsz * n, grid.x, k);
+  DSV41_REQUIRE(workspace && workspace_bytes >= need, DSV41_E_WORKSPACE, "%s: workspace of %zu bytes needed", what,
+                need);
+  DSV41_REQUIRE(aligned16(workspace), DSV41_E_ARG, "%s: workspace must be 16-byte aligned", what);
+  uint32_t* ckey = reinterpret_cast<uint32_t*>(workspace);
+  int32_t* cpos = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(workspace) + need / 2);
+#define DSV41_FUSED_CASE(HT_, TJ_)                                                                             \
+  if (heads == HT_ * 16 && tj == TJ_) {                                                                        \
+    hipLaunchKernelGGL((indexer_decode_kernel<HT_, kDecWaves, false, TJ_>), grid, dim3(kDecWaves * 64), 0,     \
+                       stream, (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, index_k, k_bstride, nullptr, 0, 1, \
+                       candidates, nullptr, n, nb, start_pos, ratio, rows_per_wg, k, ckey, cpos);             \
+  } else
+  DSV41_FUSED_CASE(4, 4) DSV41_FUSED_CASE(4, 8) DSV41_FUSED_CASE(2, 4) DSV41_FUSED_CASE(2, 8)
+  DSV41_FUSED_CASE(1, 4) DSV41_FUSED_CASE(1, 8)
+  return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
+#undef DSV41_FUSED_CASE
+  const int rc = check_launch(what);
+  if (rc) return rc;
+  return topk_merge_launch(what, ckey, cpos, out, (int64_t)bsz * n, n, nb, k, (int)grid.x, rows_per_wg, start_pos,
+                           ratio, offset, stream);
 }

@@ -14,18 +14,9 @@
 // 16K scores with k <= 2048 can go in two stages through a workspace (per-chunk lists of the
 // chunk's best k, then a merge); candidate blocks run the same register core over block maxima.
 // Longer rows fall back to topk_kernel (4-pass, 8-bit digits, keys re-read from memory).
-#include "common.h"
+#include "select.h"
 
 namespace dsv41 {
-
-constexpr int kSelThreads = 1024;
-constexpr int kSelWaves = kSelThreads / 64;
-
-__device__ __forceinline__ uint32_t order_key(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u << 1) == 0u) u = 0u;                       // -0.0 ties with +0.0
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
 
 struct SelShared {
   uint32_t hist[kSelWaves][256];
@@ -33,18 +24,6 @@ struct SelShared {
   uint32_t wsum[kSelWaves];
   uint32_t pick[2];
 };
-
-// Inclusive scan over the 64 lanes of a wave with DPP moves (no LDS round trips): shifts by 1,
-// 2, 4, 8 within each 16-lane row, then row 15 -> row 1 and 3, lane 31 -> rows 2 and 3.
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int) {
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);   // row_shr:1
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);   // row_shr:2
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);   // row_shr:4
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);   // row_shr:8
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);  // row_bcast:15
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);  // row_bcast:31
-  return v;
-}
 
 // Finds the k-th largest key among key(0..count) (1 <= k <= count). Returns T and sets
 // *need = number of T-valued keys to take after all keys > T. All threads must call it.
@@ -137,111 +116,6 @@ __device__ void ordered_select(SelShared& sh, KeyFn key, int count, uint32_t T, 
 // Histograms alternate between two buffers, so clearing the next one needs no extra barrier.
 // Compaction: one block scan of the packed per-thread (greater, equal) counts gives every thread
 // the number of selected positions before its own; it then walks its keys in position order.
-struct RegSelShared {
-  uint32_t hist[2][2048];
-  uint32_t wsum[kSelWaves];
-  uint32_t pick[2];
-};
-
-// The selection core of the register kernels: thread t holds the keys of entries t*J .. t*J+J-1
-// (consecutive, in position order), valid for j < nvalid; 1 <= k <= the number of valid entries.
-// Finds the k-th best key T and how many T-valued entries to take, then calls emit(rank, j) for
-// each selected entry j of this thread, rank = its place among the selected in entry order (so
-// ties resolve to the lowest entries); j is a run-time index, so emit must not index register
-// arrays with it. All threads of the workgroup must call it.
-template <int J, typename Emit>
-__device__ __forceinline__ void select_top(const uint32_t (&key)[J], int nvalid, int k, RegSelShared& sh, Emit emit) {
-  constexpr int NBIN = 2048;
-  static_assert(NBIN == 2 * kSelThreads, "each thread owns two bins in the suffix scan");
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-  for (int bi = 0; bi < 2; ++bi) {
-    sh.hist[bi][tid] = 0u;
-    sh.hist[bi][tid + kSelThreads] = 0u;
-  }
-  __syncthreads();
-
-  // exclusive prefix of the per-wave totals in wsum, for wave `wave` (all 16 reads in flight)
-  auto wave_base = [&]() {
-    uint32_t base = 0u;
-#pragma unroll
-    for (int w = 0; w < kSelWaves; ++w) {
-      const uint32_t v = sh.wsum[w];
-      base += w < wave ? v : 0u;
-    }
-    return base;
-  };
-
-  uint32_t prefix = 0u, pmask = 0u;
-  int kk = k;
-#pragma unroll
-  for (int pass = 0; pass < 3; ++pass) {
-    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    const uint32_t dmask = pass == 2 ? 1023u : 2047u;
-    uint32_t* h = sh.hist[pass & 1];
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-      if (j < nvalid && (key[j] & pmask) == prefix) atomicAdd(&h[(key[j] >> shift) & dmask], 1u);
-    __syncthreads();                             // histogram complete
-    if (pass < 2) {                              // the other buffer was last read before the previous barrier
-      sh.hist[(pass & 1) ^ 1][tid] = 0u;
-      sh.hist[(pass & 1) ^ 1][tid + kSelThreads] = 0u;
-    }
-    // suffix scan from the highest digit down: thread t owns digits 2047-2t and 2046-2t
-    const uint32_t c0 = h[NBIN - 1 - 2 * tid], c1 = h[NBIN - 2 - 2 * tid];
-    const uint32_t pair = c0 + c1;
-    const uint32_t incl = wave_incl_scan(pair, lane);
-    if (lane == 63) sh.wsum[wave] = incl;
-    __syncthreads();
-    const uint32_t above = wave_base() + incl - pair;
-    if (above < (uint32_t)kk && (uint32_t)kk <= above + c0) {
-      sh.pick[0] = (uint32_t)(NBIN - 1 - 2 * tid);
-      sh.pick[1] = above;
-    } else if (above + c0 < (uint32_t)kk && (uint32_t)kk <= above + pair) {
-      sh.pick[0] = (uint32_t)(NBIN - 2 - 2 * tid);
-      sh.pick[1] = above + c0;
-    }
-    __syncthreads();
-    prefix |= sh.pick[0] << shift;
-    pmask |= dmask << shift;
-    kk -= (int)sh.pick[1];
-  }
-  const uint32_t T = prefix;
-  const uint32_t need = (uint32_t)kk;            // keys == T to take, lowest entries first
-
-  uint32_t cg = 0u, ce = 0u;
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    cg += (j < nvalid && key[j] > T) ? 1u : 0u;
-    ce += (j < nvalid && key[j] == T) ? 1u : 0u;
-  }
-  const uint32_t packed = (cg << 16) | ce;       // counts <= 32768: no carry between halves
-  const uint32_t incl = wave_incl_scan(packed, lane);
-  if (lane == 63) sh.wsum[wave] = incl;          // last read before the final pass barrier
-  __syncthreads();
-  const uint32_t excl = wave_base() + incl - packed;
-  const uint32_t gt_before = excl >> 16;
-  uint32_t eq_before = excl & 0xFFFFu;
-  // Every key > T is taken, and a key == T while fewer than `need` equal keys precede it; each
-  // taken entry occupies the next rank, so this thread's m-th taken entry has rank
-  // gt_before + min(eq_before, need) + m. The take mask is formed branch-free, then only its set
-  // bits are visited (a thread takes few entries).
-  const uint32_t base = gt_before + min(eq_before, need);
-  uint32_t tmask = 0u;
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const bool ok = j < nvalid;
-    const bool gt = ok && key[j] > T, eq = ok && key[j] == T;
-    tmask |= (gt || (eq && eq_before < need)) ? (1u << j) : 0u;
-    eq_before += eq ? 1u : 0u;
-  }
-  for (uint32_t m = 0u; tmask != 0u; ++m) {
-    const int j = __builtin_ctz(tmask);
-    emit(base + m, j);
-    tmask &= tmask - 1u;
-  }
-}
-
 // J keys of entries i0 .. i0+J-1 of a score row as order keys (float4 loads when `vec`: the row
 // 16-byte aligned and i0 a multiple of 4), valid for j < nvalid.
 template <int J>
@@ -323,12 +197,13 @@ template <int J>
 __global__ __launch_bounds__(kSelThreads) void topk_merge_kernel(const uint32_t* __restrict__ ckey,
                                                                   const int32_t* __restrict__ cpos,
                                                                   int32_t* __restrict__ out, int n, int nb, int k,
-                                                                  int chunks, int start_pos, int ratio, int offset) {
+                                                                  int chunks, int chunk, int start_pos, int ratio,
+                                                                  int offset) {
   __shared__ RegSelShared sh;
   const int64_t row = blockIdx.x;
-  // the lists of chunks 0..chunks-2 are full (k entries), the last one holds min(k, its count):
-  // the valid entries are the first m of the row's concatenation
-  const int m = (chunks - 1) * k + min(k, nb - (chunks - 1) * kTopkChunk);
+  // the lists of chunks 0..chunks-2 are full (k entries: chunk >= k), the last one holds
+  // min(k, its count): the valid entries are the first m of the row's concatenation
+  const int m = (chunks - 1) * k + min(k, nb - (chunks - 1) * chunk);
   const uint32_t* kr = ckey + row * (int64_t)chunks * k;
   const int32_t* pr = cpos + row * (int64_t)chunks * k;
   int32_t* o = out + row * k;
@@ -438,6 +313,30 @@ __global__ __launch_bounds__(kSelThreads) void candidate_kernel(const float* __r
 
 using namespace dsv41;
 
+namespace dsv41 {
+// Stage 2 of a two-stage selection over per-chunk lists of k (key, position) entries, `chunk`
+// scores per chunk (>= k); also used by the indexer's fused decode form. chunks * k <= 32768.
+int topk_merge_launch(const char* what, const uint32_t* ckey, const int32_t* cpos, int32_t* out, int64_t rows, int n,
+                      int nb, int k, int chunks, int chunk, int start_pos, int ratio, int offset, hipStream_t stream) {
+  const int64_t m = (int64_t)chunks * k;
+  DSV41_REQUIRE(m <= 32 * kSelThreads && rows < (1ll << 31), DSV41_E_SHAPE, "%s: %lld candidates per row", what,
+                (long long)m);
+  const dim3 grid((unsigned)rows), block(kSelThreads);
+#define DSV41_MERGE_CASE(J_)                                                                                  \
+  if (m <= J_ * kSelThreads) {                                                                                \
+    hipLaunchKernelGGL(topk_merge_kernel<J_>, grid, block, 0, stream, ckey, cpos, out, n, nb, k, chunks, chunk, \
+                       start_pos, ratio, offset);                                                            \
+    return check_launch(what);                                                                              \
+  }
+  DSV41_MERGE_CASE(4)
+  DSV41_MERGE_CASE(8)
+  DSV41_MERGE_CASE(16)
+  DSV41_MERGE_CASE(32)
+#undef DSV41_MERGE_CASE
+  return set_error(DSV41_E_SHAPE, "%s: too many candidates", what);
+}
+}  // namespace dsv41
+
 // The two-stage form for a row of nb scores: rows longer than one 16-keys-per-thread workgroup
 // holds, k at most half a chunk, and the chunk lists small enough for one register workgroup.
 static bool topk_two_stage(int nb, int k, int* chunks, int* jm) {
@@ -480,15 +379,8 @@ static int topk_launch(const char* what, const float* scores, int32_t* out, int6
                        chunks, vec);
     int rc = check_launch(what);
     if (rc) return rc;
-#define DSV41_MERGE_CASE(J_)                                                                                 \
-    if (jm == J_) hipLaunchKernelGGL(topk_merge_kernel<J_>, grid, block, 0, stream, ckey, cpos, out, n, nb, k, \
-                                     chunks, start_pos, ratio, offset);
-    DSV41_MERGE_CASE(4)
-    DSV41_MERGE_CASE(8)
-    DSV41_MERGE_CASE(16)
-    DSV41_MERGE_CASE(32)
-#undef DSV41_MERGE_CASE
-    return check_launch(what);
+    return topk_merge_launch(what, ckey, cpos, out, rows, n, nb, k, chunks, kTopkChunk, start_pos, ratio, offset,
+                             stream);
   }
   if (nb <= 4 * kSelThreads)
     hipLaunchKernelGGL(topk_reg_kernel<4>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset, vec);

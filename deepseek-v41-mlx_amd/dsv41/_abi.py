@@ -61,6 +61,9 @@ _SIGNATURES = {
                                   _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_topk_select": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_topk_workspace_bytes": [_i64, _i32, _i32],
+    "dsv41_indexer_topk_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32, _i32],
+    "dsv41_indexer_topk": [_c_p, _c_p, _f32, _c_p, _i64, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                           _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_topk_select_ws": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_candidate_blocks": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _i32, _i32, _c_p],
     "dsv41_sparse_mla_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32],
@@ -85,6 +88,7 @@ _SIGNATURES = {
 _RESTYPES = {
     "dsv41_sparse_mla_workspace_bytes": _sz,
     "dsv41_topk_workspace_bytes": _sz,
+    "dsv41_indexer_topk_workspace_bytes": _sz,
     "dsv41_version": ctypes.c_char_p,
     "dsv41_last_error_string": ctypes.c_char_p,
 }
@@ -419,6 +423,41 @@ def indexer_score(q, w_raw, w_scale, index_k, start_pos, ratio, candidates=None,
     cand = candidates.view(torch.uint8) if candidates is not None else None
     _call(name, _ptr(q), _ptr(w_raw), float(w_scale), _ptr(index_k), row_stride(index_k, name),
           _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, dtype_code(q, name), _stream(q))
+    return out
+
+
+def indexer_topk_workspace_bytes(b, n, heads, dim, nb, topk, has_candidates=False) -> int:
+    return int(lib().dsv41_indexer_topk_workspace_bytes(b, n, heads, dim, nb, topk, 1 if has_candidates else 0))
+
+
+def indexer_topk(q, w_raw, w_scale, index_k, start_pos, ratio, topk, offset, candidates=None, out=None,
+                 workspace=None):
+    """indexer_score followed by topk_select in one fused decode form: int32 [b, n, min(topk, nb)],
+    bit-equal to topk_select(indexer_score(...)) -- but the [b, n, nb] scores are never written:
+    each row range keeps its best topk and a merge selects from those lists. Returns None when
+    the shape is not one the fused form serves (the caller then makes the two calls)."""
+    name = "dsv41_indexer_topk"
+    _gpu(name, q, w_raw, index_k, candidates, out, workspace)
+    _contig(name, q, w_raw, candidates)
+    b, n, h, d = q.shape
+    nb = index_k.shape[1]
+    if q.dtype != torch.bfloat16 or w_raw.shape != (b, n, h) or w_raw.dtype != q.dtype:
+        raise ValueError(f"{name}: q and w_raw must be bf16, w_raw [{b}, {n}, {h}]")
+    if index_k.shape[0] < b or index_k.shape[2] != d or index_k.dtype != q.dtype:
+        raise ValueError(f"{name}: index_k {tuple(index_k.shape)} {index_k.dtype} does not match q")
+    if candidates is not None and (candidates.shape != (b, n, nb) or candidates.dtype not in (torch.uint8, torch.bool)):
+        raise ValueError(f"{name}: candidates must be bool/uint8 [{b}, {n}, {nb}]")
+    ws_bytes = indexer_topk_workspace_bytes(b, n, h, d, nb, topk, candidates is not None)
+    if ws_bytes == 0:
+        return None
+    k = min(topk, nb)
+    out = torch.empty(b, n, k, dtype=torch.int32, device=q.device) if out is None else out
+    if out.dtype != torch.int32 or tuple(out.shape) != (b, n, k) or not out.is_contiguous():
+        raise ValueError(f"{name}: out must be contiguous int32 [{b}, {n}, {k}]")
+    ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else _workspace(ws_bytes, q.device)
+    cand = candidates.view(torch.uint8) if candidates is not None else None
+    _call(name, _ptr(q), _ptr(w_raw), float(w_scale), _ptr(index_k), row_stride(index_k, name), _ptr(cand),
+          _ptr(out), b, n, h, d, nb, start_pos, ratio, topk, offset, _ptr(ws), ws_bytes, _stream(q))
     return out
 
 

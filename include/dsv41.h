@@ -225,6 +225,22 @@ int dsv41_indexer_score_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, c
                               float* scores, int32_t bsz, int32_t n, int32_t heads, int32_t dim,
                               int32_t nb, int32_t start_pos, int32_t ratio, hipStream_t stream);
 
+/* Indexer scoring followed by top-k selection, fused for decode (deepseek_v41_mlx/indexer.py:
+ * 115-144: the scores of dsv41_indexer_score, then the selection of dsv41_topk_select, with
+ * identical results): the [bsz*n, nb] scores are never written -- each workgroup's row range
+ * keeps its best k (key, position) pairs in the workspace and a merge selects each query's k.
+ * Served shapes: bf16 keys of dim 128, 16/32/64 heads, n < 8 or a candidate mask, and row ranges
+ * of 2048 or 4096 rows at least twice k; dsv41_indexer_topk_workspace_bytes returns 0 for the
+ * others (the entry point then returns DSV41_E_SHAPE). out [bsz*n, k] int32, k = min(topk, nb).
+ * The workspace is 16-byte aligned. */
+size_t dsv41_indexer_topk_workspace_bytes(int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
+                                          int32_t topk, int32_t has_candidates);
+int dsv41_indexer_topk(const void* q, const void* w_raw, float w_scale, const void* index_k,
+                       int64_t k_bstride, const uint8_t* candidates, int32_t* out, int32_t bsz,
+                       int32_t n, int32_t heads, int32_t dim, int32_t nb, int32_t start_pos,
+                       int32_t ratio, int32_t topk, int32_t offset, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+
 /* Top-k selection, deepseek_v41_mlx/indexer.py:200-204: per row of scores [bsz*n, nb],
  * the k = min(topk, nb) best positions (ties -> lowest position; -0.0 == +0.0), sorted
  * ascending, written as idx + offset when idx < lens else -1, lens = (start_pos+s+1)/ratio,

@@ -376,6 +376,30 @@ def test_indexer_score_mxfp4(gpu, b, n, h, nb, start, use_cand):
     assert np.array_equal(np.isfinite(dense), fin) and np.abs(dense[fin] - g[fin]).max() <= tol
 
 
+@pytest.mark.parametrize("b,n,h,nb,topk,start,use_cand", [
+    (32, 1, 64, 16384, 512, 65535, False),   # bs32 decode: 8 row ranges of 2048
+    (64, 1, 64, 16384, 512, 65535, False),   # 4 ranges of 4096
+    (32, 1, 32, 16384, 512, 65535, True),    # candidate-masked consumer, 32 index heads
+    (8, 4, 16, 16384, 512, 20000, False),    # causal rows: ranges past visibility list -inf entries
+])
+def test_indexer_topk_fused_equals_two_calls(gpu, b, n, h, nb, topk, start, use_cand):
+    """The fused decode form (per-range best-k lists, then a merge) returns exactly the top-k of
+    indexer_score's scores."""
+    from dsv41 import _abi
+    rng = rng_for(f"fused{b}{n}{h}{use_cand}")
+    d, r = 128, 4
+    q = dev(R.fq_fp4_ue8m0(rng.standard_normal((b, n, h, d)).astype(F32), 32, "bf16"), "bf16")
+    k = dev(R.fq_fp4_ue8m0(rng.standard_normal((b, nb, d)).astype(F32), 32, "bf16"), "bf16")
+    w = dev(rng.standard_normal((b, n, h)).astype(F32), "bf16")
+    cand = torch.as_tensor(rng.random((b, n, nb)) < 0.7).to(gpu) if use_cand else None
+    scale = R.index_weight_scale(h, d, "bf16")
+    off = 129
+    assert _abi.indexer_topk_workspace_bytes(b, n, h, d, nb, topk, use_cand) > 0
+    fused = _abi.indexer_topk(q, w, scale, k, start, r, topk, off, cand)
+    two = _abi.topk_select(_abi.indexer_score(q, w, scale, k, start, r, cand), topk, start, r, off)
+    assert torch.equal(fused, two)
+
+
 # ------------------------------------------------------------------ top-k and candidates
 
 
