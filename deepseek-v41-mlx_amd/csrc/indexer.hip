@@ -740,15 +740,15 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
 
 // The fused decode form (indexer_decode_kernel with TJ > 0, then the top-k merge): shapes the
 // staged-copy decode kernel serves (bf16 keys of 128 channels, 16/32/64 heads, fewer than 8
-// queries per row or a candidate mask) with row ranges of 2048 or 4096 rows at least twice k.
+// queries per row or a candidate mask) with row ranges of 512, 1024, 2048 or 4096 rows, at least
+// twice k.
 static bool idx_topk_plan(int64_t bsz, int n, int heads, int dim, int nb, int k, bool cand, int* rows_per_wg,
                           dim3* grid, int* tj) {
   if (dim != 128 || !(heads == 64 || heads == 32 || heads == 16)) return false;
   if ((n >= 8 && !cand) || bsz * n >= 65536) return false;
   *grid = idx_grid((int64_t)nb * bsz * n, nb, (int)(bsz * n), rows_per_wg);
-  if (*rows_per_wg == 2048) *tj = 4;
-  else if (*rows_per_wg == 4096) *tj = 8;
-  else return false;
+  *tj = *rows_per_wg / 512;                        // 512, 1024, 2048 or 4096 rows: 1, 2, 4 or 8 per thread
+  if (*tj != 1 && *tj != 2 && *tj != 4 && *tj != 8) return false;
   return 2 * k <= *rows_per_wg && (int64_t)grid->x * k <= 32 * kSelThreads;
 }
 
@@ -883,8 +883,9 @@ extern "C" int dsv41_indexer_topk(const void* q, const void* w_raw, float w_scal
                        stream, (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, index_k, k_bstride, nullptr, 0, 1, \
                        candidates, nullptr, n, nb, start_pos, ratio, rows_per_wg, k, ckey, cpos);             \
   } else
-  DSV41_FUSED_CASE(4, 4) DSV41_FUSED_CASE(4, 8) DSV41_FUSED_CASE(2, 4) DSV41_FUSED_CASE(2, 8)
-  DSV41_FUSED_CASE(1, 4) DSV41_FUSED_CASE(1, 8)
+  DSV41_FUSED_CASE(4, 1) DSV41_FUSED_CASE(4, 2) DSV41_FUSED_CASE(4, 4) DSV41_FUSED_CASE(4, 8)
+  DSV41_FUSED_CASE(2, 1) DSV41_FUSED_CASE(2, 2) DSV41_FUSED_CASE(2, 4) DSV41_FUSED_CASE(2, 8)
+  DSV41_FUSED_CASE(1, 1) DSV41_FUSED_CASE(1, 2) DSV41_FUSED_CASE(1, 4) DSV41_FUSED_CASE(1, 8)
   return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
 #undef DSV41_FUSED_CASE
   const int rc = check_launch(what);

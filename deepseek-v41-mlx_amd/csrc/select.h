@@ -30,12 +30,15 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int) {
 struct RegSelShared {
   uint32_t hist[2][2048];
   uint32_t wsum[kSelWaves];
-  uint32_t pick[2];
+  uint32_t pick[3];
 };
 
 // The selection core of the register kernels: thread t holds the keys of entries t*J .. t*J+J-1
 // (consecutive, in position order), valid for j < nvalid; 1 <= k <= the number of valid entries.
-// Finds the k-th best key T and how many T-valued entries to take, then calls emit(rank, j) for
+// Finds the k-th best key T and how many T-valued entries to take -- or, once the digit bin
+// that holds the k-th best has exactly as many entries as are still to take (after one or two of
+// the three digit passes), the resolved top bits P of every selected key: the selection is then
+// every key whose top bits are >= P, with no tie left to break -- then calls emit(rank, j) for
 // each selected entry j of this thread, rank = its place among the selected in entry order (so
 // ties resolve to the lowest entries); j is a run-time index, so emit must not index register
 // arrays with it. All threads of the workgroup must call it.
@@ -94,6 +97,7 @@ __device__ __forceinline__ void select_top(const uint32_t (&key)[J], int nvalid,
       if (above < (uint32_t)kk && (uint32_t)kk <= above + c[b]) {
         sh.pick[0] = (uint32_t)(NBIN - 1 - BPT * tid - b);
         sh.pick[1] = above;
+        sh.pick[2] = above + c[b] == (uint32_t)kk ? 1u : 0u;   // the whole bin is taken
       }
       above += c[b];
     }
@@ -101,15 +105,22 @@ __device__ __forceinline__ void select_top(const uint32_t (&key)[J], int nvalid,
     prefix |= sh.pick[0] << shift;
     pmask |= dmask << shift;
     kk -= (int)sh.pick[1];
+    // uniform: every thread read the same pick; the next pass's writes to pick follow a barrier
+    // that every thread passes after these reads
+    if (pass < 2 && sh.pick[2] != 0u) break;
   }
+  // compare the resolved top bits only (all 32 after three passes)
   const uint32_t T = prefix;
   const uint32_t need = (uint32_t)kk;            // keys == T to take, lowest entries first
+  uint32_t mk[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) mk[j] = key[j] & pmask;
 
   uint32_t cg = 0u, ce = 0u;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    cg += (j < nvalid && key[j] > T) ? 1u : 0u;
-    ce += (j < nvalid && key[j] == T) ? 1u : 0u;
+    cg += (j < nvalid && mk[j] > T) ? 1u : 0u;
+    ce += (j < nvalid && mk[j] == T) ? 1u : 0u;
   }
   const uint32_t packed = (cg << 16) | ce;       // counts <= 32768: no carry between halves
   const uint32_t incl = wave_incl_scan(packed, lane);
@@ -127,7 +138,7 @@ __device__ __forceinline__ void select_top(const uint32_t (&key)[J], int nvalid,
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const bool ok = j < nvalid;
-    const bool gt = ok && key[j] > T, eq = ok && key[j] == T;
+    const bool gt = ok && mk[j] > T, eq = ok && mk[j] == T;
     tmask |= (gt || (eq && eq_before < need)) ? (1u << j) : 0u;
     eq_before += eq ? 1u : 0u;
   }

@@ -542,18 +542,20 @@ def topk_workspace_bytes(rows, nb, topk) -> int:
     return int(lib().dsv41_topk_workspace_bytes(rows, nb, topk))
 
 
-def topk_select(scores, topk, start_pos, ratio, offset, workspace=None):
-    """scores [b, n, nb] fp32 -> int32 [b, n, min(topk, nb)]. Rows longer than 16384 scores
-    (k <= 2048) are selected in two stages through a uint8 workspace of topk_workspace_bytes(...)
-    bytes, allocated when it is omitted or too small."""
+def topk_select(scores, topk, start_pos, ratio, offset, workspace=None, out=None):
+    """scores [b, n, nb] fp32 -> int32 [b, n, min(topk, nb)] (into `out` when given). Rows longer
+    than 16384 scores (k <= 2048) are selected in two stages through a uint8 workspace of
+    topk_workspace_bytes(...) bytes, allocated when it is omitted or too small."""
     name = "dsv41_topk_select_ws"
-    _gpu(name, scores, workspace)
+    _gpu(name, scores, workspace, out)
     _contig(name, scores)
     if scores.dtype != torch.float32 or scores.dim() != 3:
         raise ValueError(f"{name}: scores must be fp32 [b, n, nb]")
     b, n, nb = scores.shape
     k = min(topk, nb)
-    out = torch.empty(b, n, k, dtype=torch.int32, device=scores.device)
+    out = torch.empty(b, n, k, dtype=torch.int32, device=scores.device) if out is None else out
+    if out.dtype != torch.int32 or tuple(out.shape) != (b, n, k) or not out.is_contiguous():
+        raise ValueError(f"{name}: out must be contiguous int32 [{b}, {n}, {k}]")
     if out.numel():
         ws_bytes = topk_workspace_bytes(b * n, nb, topk)
         ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else _workspace(ws_bytes,

@@ -12,7 +12,10 @@ on MFMA, with the visibility mask (t >= lens_s -> -inf) and, for layers after th
 source, the candidate mask applied in the same pass. The candidate source publishes its
 block mask (``select_candidate_blocks``); the top-k kernel returns the ``index_topk`` best
 positions per query in ascending order, offset into the attention's unified index space, -1
-past the visible range.
+past the visible range. Decode queries of index sources other than the candidate source, on
+bf16 keys of shapes it serves, take the fused form (dsv41_indexer_topk): the scoring kernel
+keeps each row range's best index_topk and a merge selects from those lists -- the same
+selection, without writing the scores.
 """
 
 from __future__ import annotations
@@ -125,6 +128,12 @@ class Indexer(torch.nn.Module):
                 q = _abi.rope_tail(q, rd, cos, sin, start_pos, 1)
             else:
                 _abi.index_q_prep(q, cos, sin, rd, start_pos)
+            if not self.is_candidate_source and q.dtype == torch.bfloat16:
+                # decode shapes the fused form serves: the same selection, the scores never written
+                idx = _abi.indexer_topk(q, w_raw, w_scale, index_k, start_pos, self.ratio, self.index_topk, offset,
+                                        cand)
+                if idx is not None:
+                    return idx
             scores = _abi.indexer_score(q, w_raw, w_scale, index_k, start_pos, self.ratio, cand)
         if self.is_candidate_source:
             shared.candidates = _abi.candidate_blocks(scores, self.candidate_topk_blocks,

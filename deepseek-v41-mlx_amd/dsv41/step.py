@@ -6,7 +6,11 @@ the inverse rope on the output -- i.e. attention.py:143-175 minus the projection
 cache writes and the fake-quant prologues, which are per-token elementwise work.
 
 All outputs and scratch are allocated once, so a step issues exactly three kernels (four
-when the attention splits its index list) and can be captured in a HIP graph.
+when the attention splits its index list) and can be captured in a HIP graph. Where the fused
+indexer form serves the shape (bf16 keys, 16/32/64 index heads of 128 channels, 2048 or 4096
+scored entries per workgroup), scoring and selection are dsv41_indexer_topk: the scoring kernel
+keeps each row range's best top-k and a merge kernel selects from those lists, so the
+[b, 1, nb] scores are never written; the selection is bit-equal to the two-call form.
 """
 
 from __future__ import annotations
@@ -19,7 +23,7 @@ from . import _abi
 class SparseDecodeStep:
     def __init__(self, bsz: int, heads: int, head_dim: int, rd: int, index_heads: int,
                  index_dim: int, nb: int, index_topk: int, window: int, start_pos: int,
-                 ratio: int, dtype=torch.bfloat16, device="cuda"):
+                 ratio: int, dtype=torch.bfloat16, device="cuda", fused: bool = True):
         self.bsz, self.heads, self.head_dim, self.rd = bsz, heads, head_dim, rd
         self.index_heads, self.index_dim = index_heads, index_dim
         self.nb, self.topk, self.window = nb, index_topk, window
@@ -28,7 +32,15 @@ class SparseDecodeStep:
         self.wp = min(start_pos, window)
         self.offset = self.wp + 1
         self.k = min(index_topk, nb)
+        fws = (_abi.indexer_topk_workspace_bytes(bsz, 1, index_heads, index_dim, nb, index_topk)
+               if fused and dtype == torch.bfloat16 else 0)
+        self.fused = fws > 0
+        # the scores are written only by the two-call form (fused False or a shape it does not serve)
         self.scores = torch.empty(bsz, 1, nb, dtype=torch.float32, device=device)
+        self.idx = torch.empty(bsz, 1, self.k, dtype=torch.int32, device=device)
+        self.fused_ws = torch.empty(max(fws, 1), dtype=torch.uint8, device=device)
+        tws = 0 if self.fused else _abi.topk_workspace_bytes(bsz, nb, index_topk)
+        self.topk_ws = torch.empty(max(tws, 1), dtype=torch.uint8, device=device)
         self.out = torch.empty(bsz, 1, heads, head_dim, dtype=dtype, device=device)
         rows = min(window, self.wp + 1) + self.k
         ws = _abi.mla_workspace_bytes(bsz, 1, heads, head_dim, rows, dtype)
@@ -39,9 +51,14 @@ class SparseDecodeStep:
         """q [b,1,H,D]; index_q [b,1,Hi,Di] (already roped + fake-quantized); w_raw [b,1,Hi];
         index_k / comp_kv: the owner's caches ([b, >=nb, *] views, read in place);
         win_kv [b, window, D] ring of the previous tokens; chunk_kv [b,1,D] this token's KV."""
-        _abi.indexer_score(index_q, w_raw, w_scale, index_k[:, :self.nb], self.start_pos, self.ratio,
-                           None, out=self.scores)
-        idx = _abi.topk_select(self.scores, self.topk, self.start_pos, self.ratio, self.offset)
+        keys = index_k[:, :self.nb]
+        if self.fused:
+            idx = _abi.indexer_topk(index_q, w_raw, w_scale, keys, self.start_pos, self.ratio, self.topk,
+                                    self.offset, None, out=self.idx, workspace=self.fused_ws)
+        else:
+            _abi.indexer_score(index_q, w_raw, w_scale, keys, self.start_pos, self.ratio, None, out=self.scores)
+            idx = _abi.topk_select(self.scores, self.topk, self.start_pos, self.ratio, self.offset,
+                                   workspace=self.topk_ws, out=self.idx)
         _abi.sparse_mla(q, win_kv, chunk_kv, comp_kv, self.nb, sink, idx, self.head_dim ** -0.5,
                         self.window, self.start_pos, cos, sin, self.rd, out=self.out,
                         workspace=self.workspace)
@@ -50,7 +67,7 @@ class SparseDecodeStep:
 
 class _LayerPlan:
     __slots__ = ("layer_id", "ratio", "kv_source", "index_source", "owns_k", "candidate_source",
-                 "uses_candidates", "cos", "sin", "out", "idx")
+                 "uses_candidates", "cos", "sin", "out", "idx", "fused_idx")
 
 
 class StackDecodeStep:
@@ -73,7 +90,10 @@ class StackDecodeStep:
     and ``w_scale``; kv sources add ``latent`` [b,1,D] (pre-rope); key owners add ``k_raw``
     [b,1,Di] and ``k_norm`` [Di]. Caches may be dense, carry MXFP4 index keys, or be the fp8
     variant (cache_format "fp8": fp8 compressed KV and index keys); each layer takes the kernels
-    that read and write its owners' format.
+    that read and write its owners' format. On dense bf16 keys, index sources other than the
+    candidate source score and select in the fused form (dsv41_indexer_topk) where it serves
+    the shape; the candidate source writes its scores for the block mask (kept in
+    ``candidates``).
     Outputs (``out`` per layer) and scratch are allocated once, so a step can be captured in
     a HIP graph.
     """
@@ -100,7 +120,7 @@ class StackDecodeStep:
             return tables[key]
 
         self.plan = []
-        max_rows, max_nb = 1, 1
+        max_rows, max_nb, max_fws = 1, 1, 1
         for l in range(args.n_layers):
             p = _LayerPlan()
             p.layer_id = l
@@ -113,11 +133,21 @@ class StackDecodeStep:
             p.cos, p.sin = table(p.ratio)
             p.out = torch.empty(bsz, 1, args.n_heads, args.head_dim, dtype=dtype, device=dev)
             p.idx = None                                   # an index source's last selection
+            p.fused_idx = None
             if p.ratio:
-                max_nb = max(max_nb, self.end_pos // p.ratio)
-                max_rows = max(max_rows, min(self.window, self.wp + 1) + min(args.index_topk, self.end_pos // p.ratio))
+                nb = self.end_pos // p.ratio
+                max_nb = max(max_nb, nb)
+                max_rows = max(max_rows, min(self.window, self.wp + 1) + min(args.index_topk, nb))
+                if p.index_source and not p.candidate_source and dtype == torch.bfloat16:
+                    fws = _abi.indexer_topk_workspace_bytes(bsz, 1, args.index_n_heads, args.index_head_dim, nb,
+                                                            args.index_topk, p.uses_candidates)
+                    if fws > 0:                    # bf16 keys take the fused indexer + top-k form
+                        max_fws = max(max_fws, fws)
+                        p.fused_idx = torch.empty(bsz, 1, min(args.index_topk, nb), dtype=torch.int32, device=dev)
             self.plan.append(p)
         self.scores = torch.empty(bsz * max_nb, dtype=torch.float32, device=dev)   # [b, 1, nb] per layer
+        self.fused_ws = torch.empty(max_fws, dtype=torch.uint8, device=dev)
+        self.candidates = None                             # the candidate source's last block mask
         ws = _abi.mla_workspace_bytes(bsz, 1, args.n_heads, args.head_dim, max_rows, dtype)
         self.workspace = torch.empty(max(ws, 1), dtype=torch.uint8, device=dev)
 
@@ -150,7 +180,12 @@ class StackDecodeStep:
                     keys = key_src.index_keys(b, nb)
                     c = cand if p.uses_candidates else None
                     kind = getattr(keys, "kind", None)
-                    if kind == "mxfp4":
+                    fuse = kind is None and p.fused_idx is not None
+                    if fuse:
+                        topk = p.idx = _abi.indexer_topk(x["index_q"], x["w_raw"], x["w_scale"], keys, sp, p.ratio,
+                                                         a.index_topk, self.offset, c, out=p.fused_idx,
+                                                         workspace=self.fused_ws)
+                    elif kind == "mxfp4":
                         _abi.indexer_score_mxfp4(x["index_q_mx"], x["w_raw"], x["w_scale"], keys.codes, keys.scales,
                                                  nb, sp, p.ratio, c, out=scores)
                     elif kind == "fp8":
@@ -159,9 +194,10 @@ class StackDecodeStep:
                     else:
                         _abi.indexer_score(x["index_q"], x["w_raw"], x["w_scale"], keys, sp, p.ratio, c, out=scores)
                     if p.candidate_source:
-                        cand = _abi.candidate_blocks(scores, a.candidate_topk_blocks, a.candidate_block_size,
-                                                     None, sp, p.ratio)
-                    topk = p.idx = _abi.topk_select(scores, a.index_topk, sp, p.ratio, self.offset)
+                        cand = self.candidates = _abi.candidate_blocks(scores, a.candidate_topk_blocks,
+                                                                       a.candidate_block_size, None, sp, p.ratio)
+                    if not fuse:
+                        topk = p.idx = _abi.topk_select(scores, a.index_topk, sp, p.ratio, self.offset)
                 if p.kv_source and emits and lc.comp_kv8 is not None:
                     _abi.comp_write_fp8(x["latent"], lc.comp_kv8, lc.comp_ks, nb - 1, p.ratio, p.cos, p.sin,
                                         a.rope_head_dim)

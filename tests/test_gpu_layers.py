@@ -141,7 +141,7 @@ def test_c2_decode_step(gpu):
     d = {k: v.to(gpu) for k, v in t.items()}
     cos, sin = precompute_freqs_cis(c["rd"], c["start"] + 1, 65536, 160000.0, 16.0, 32, 1, device=gpu)
     step = SparseDecodeStep(b, c["H"], c["D"], c["rd"], c["Hi"], c["Di"], c["nb"], c["K"], c["W"], c["start"],
-                            c["r"], torch.bfloat16, gpu)
+                            c["r"], torch.bfloat16, gpu, fused=False)     # two calls: the scores are kept
     ws = weight_scale(c["Hi"], c["Di"], torch.bfloat16)
     out, idx = step(d["q"], d["iq"], d["w"], ws, d["ik"], d["comp"], d["win"], d["chunk"], d["sink"], cos, sin)
     torch.cuda.synchronize()
@@ -165,3 +165,31 @@ def test_c2_decode_step(gpu):
     rc, rs = R.precompute_freqs_cis(c["rd"], c["start"] + 1, 65536, 160000.0, 16.0, 32, 1)
     want_o = R.rope_tail(o, c["rd"], rc[[c["start"]]], rs[[c["start"]]], inverse=True, dtype="bf16")
     assert rel_max_diff(to_np(out), want_o) < 2e-2
+
+
+@pytest.mark.parametrize("b,nb,K,start", [
+    (32, 16384, 512, 65535),     # bs32, 64K context: 8 row ranges of 2048 per query
+    (16, 32768, 1024, 131071),   # bs16, 128K context, top-1024: 8 ranges of 4096
+    (32, 4096, 256, 16386),      # ranges of 512, top-256; 3 tokens of the next group still open
+])
+def test_decode_step_fused_equals_two_calls(gpu, b, nb, K, start):
+    """The decode step with the fused indexer + top-k form selects exactly what indexer_score +
+    topk_select select, so its attention output is bit-equal as well."""
+    from dsv41.layers import precompute_freqs_cis
+    from dsv41.step import SparseDecodeStep
+    g = torch.Generator(gpu).manual_seed(SEED_BASE + 41)
+    H, D, Hi, Di, W, rd, r = 64, 512, 64, 128, 128, 64, 4
+    rn = lambda *s: torch.randn(*s, generator=g, device=gpu)   # noqa: E731
+    sc = 576 ** -0.5
+    q, win, chunk = (rn(b, 1, H, D) * sc).bfloat16(), (rn(b, W, D) * sc).bfloat16(), (rn(b, 1, D) * sc).bfloat16()
+    comp = (rn(b, nb, D) * sc).bfloat16()
+    iq, ik, w, sink = rn(b, 1, Hi, Di).bfloat16(), rn(b, nb, Di).bfloat16(), rn(b, 1, Hi).bfloat16(), rn(H)
+    cos, sin = precompute_freqs_cis(rd, start + 1, 65536, 160000.0, 16.0, 32, 1, device=gpu)
+    fused = SparseDecodeStep(b, H, D, rd, Hi, Di, nb, K, W, start, r, torch.bfloat16, gpu)
+    two = SparseDecodeStep(b, H, D, rd, Hi, Di, nb, K, W, start, r, torch.bfloat16, gpu, fused=False)
+    assert fused.fused and not two.fused
+    o1, i1 = fused(q, iq, w, 0.01, ik, comp, win, chunk, sink, cos, sin)
+    o2, i2 = two(q, iq, w, 0.01, ik, comp, win, chunk, sink, cos, sin)
+    torch.cuda.synchronize()
+    assert torch.equal(i1, i2)
+    assert torch.equal(o1, o2)

@@ -44,7 +44,8 @@ def _record_decode(stack, h, cache):
     layer = [0]
     orig = {n: getattr(_abi, n) for n in ("sparse_mla", "indexer_score", "comp_write", "index_key_publish",
                                           "indexer_score_mxfp4", "index_key_publish_mxfp4", "sparse_mla_fp8",
-                                          "indexer_score_fp8", "comp_write_fp8", "index_key_publish_fp8")}
+                                          "indexer_score_fp8", "comp_write_fp8", "index_key_publish_fp8",
+                                          "indexer_topk")}
 
     def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, *a, **k):
         r = recs[layer[0]]
@@ -65,6 +66,10 @@ def _record_decode(stack, h, cache):
         r["out"] = o.clone()
         layer[0] += 1
         return o
+
+    def indexer_topk(q, w_raw, w_scale, *a, **k):
+        recs[layer[0]].update(index_q=q.clone(), w_raw=w_raw.clone(), w_scale=w_scale)
+        return orig["indexer_topk"](q, w_raw, w_scale, *a, **k)
 
     def indexer_score_fp8(q, w_raw, w_scale, *a, **k):
         recs[layer[0]].update(index_q=q.clone(), w_raw=w_raw.clone(), w_scale=w_scale)
@@ -98,7 +103,7 @@ def _record_decode(stack, h, cache):
                  ("index_key_publish", index_key_publish), ("indexer_score_mxfp4", indexer_score_mxfp4),
                  ("index_key_publish_mxfp4", index_key_publish_mxfp4), ("sparse_mla_fp8", sparse_mla_fp8),
                  ("indexer_score_fp8", indexer_score_fp8), ("comp_write_fp8", comp_write_fp8),
-                 ("index_key_publish_fp8", index_key_publish_fp8)):
+                 ("index_key_publish_fp8", index_key_publish_fp8), ("indexer_topk", indexer_topk)):
         setattr(_abi, n, f)
     try:
         stack(h, cache)
@@ -219,6 +224,7 @@ def _oracle_layer_out(a, q_row, win_before, kv_row, comp_row, idx_row, sink, sta
 
 
 def test_c4_full_size_sampled_rows(gpu):
+    from dsv41 import _abi
     from dsv41.cache import ModelCache
     from dsv41.step import StackDecodeStep
     a = c4_args()
@@ -236,7 +242,11 @@ def test_c4_full_size_sampled_rows(gpu):
     nb = (sp + 1) // r
     lens = R.query_lens(sp, 1, r)
     f = lambda t: t.float().cpu().numpy()   # noqa: E731
-    got_s = to_np(step.scores[:B * nb].view(B, 1, nb))    # the last index source's (layer 36)
+    # layer 36 selects with the fused indexer + top-k form, which writes no scores: its scores
+    # come from indexer_score with the same inputs and the candidate mask layer 20 published
+    assert step.plan[36].fused_idx is not None and step.candidates is not None
+    got_s = to_np(_abi.indexer_score(ins[36]["index_q"], ins[36]["w_raw"], ins[36]["w_scale"],
+                                     cache.layers[20].index_k[:B, :nb], sp, r, step.candidates))
     idx36 = step.plan[36].idx.cpu().numpy()
     for b in rows:
         keys20 = f(cache.layers[20].index_k[b, :nb])[None]
