@@ -476,22 +476,37 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
     uint4 pv[NB];
 #pragma unroll
     for (int s = 0; s < NB; ++s) pv[s] = part(s < ns ? s : ns - 1, d);
-    float mk = kNegFloor, lk = 0.0f;
-    if (lane < ns) {
-      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (slot0 + (int64_t)lane * a.heads) * 2);
-      mk = ml.x;
-      lk = ml.y;
+    // every lane reads every split's (max, denominator) pair (the same addresses across the
+    // wave): the weights need no cross-lane exchange
+    auto ml = [&](int s) { return *reinterpret_cast<const float2*>(a.part_ml + (slot0 + (int64_t)s * a.heads) * 2); };
+    float2 mlv[NB];
+#pragma unroll
+    for (int s = 0; s < NB; ++s) mlv[s] = ml(s < ns ? s : ns - 1);
+    float M = kNegFloor;
+#pragma unroll
+    for (int s = 0; s < NB; ++s) M = s < ns ? fmaxf(M, mlv[s].x) : M;
+    for (int s = NB; s < ns; ++s) M = fmaxf(M, ml(s).x);
+    float wv[NB], den = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      wv[s] = s < ns ? mlv[s].y * exp2f(mlv[s].x - M) : 0.0f;
+      den += wv[s];
     }
-    float M = mk;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    const float wk = lane < ns ? lk * exp2f(mk - M) : 0.0f;
-    float den = wk;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o, 64);
+    for (int s = NB; s < ns; ++s) {
+      const float2 v = ml(s);
+      den += v.y * exp2f(v.x - M);
+    }
     float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     auto add = [&](int s, const uint4& v) {
-      const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), s));
+      float w;
+      if (s < NB) {
+        w = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NB; ++t) w = t == s ? wv[t] : w;
+      } else {
+        const float2 m2 = ml(s);
+        w = m2.y * exp2f(m2.x - M);
+      }
       const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {

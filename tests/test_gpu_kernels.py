@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from common import max_abs, rel_max_diff, to_np
+from common import SEED_BASE, max_abs, rel_max_diff, to_np
 from oracle import cpu_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -398,6 +398,28 @@ def test_indexer_topk_fused_equals_two_calls(gpu, b, n, h, nb, topk, start, use_
     fused = _abi.indexer_topk(q, w, scale, k, start, r, topk, off, cand)
     two = _abi.topk_select(_abi.indexer_score(q, w, scale, k, start, r, cand), topk, start, r, off)
     assert torch.equal(fused, two)
+
+
+def test_indexer_topk_shared_workspace(gpu):
+    """One workspace through a sequence of fused calls of different shapes (query counts, row
+    ranges, k, candidate masks, ranges past visibility): every call equals the two-call form."""
+    from dsv41 import _abi
+    shapes = [(32, 1, 64, 16384, 512, 65535, False), (8, 4, 16, 16384, 512, 20000, False),
+              (32, 1, 32, 16384, 512, 65535, True), (2, 1, 64, 256, 64, 1024, False),
+              (16, 1, 64, 32768, 1024, 131071, False)]
+    need = [_abi.indexer_topk_workspace_bytes(b, n, h, 128, nb, k, c) for b, n, h, nb, k, _, c in shapes]
+    assert min(need) > 0
+    ws = torch.empty(max(need), dtype=torch.uint8, device=gpu)
+    g = torch.Generator(gpu).manual_seed(SEED_BASE + 43)
+    for rep in range(2):
+        for b, n, h, nb, k, start, use_cand in shapes:
+            q = torch.randn(b, n, h, 128, generator=g, device=gpu).bfloat16()
+            keys = torch.randn(b, nb, 128, generator=g, device=gpu).bfloat16()
+            w = torch.randn(b, n, h, generator=g, device=gpu).bfloat16()
+            cand = (torch.rand(b, n, nb, generator=g, device=gpu) < 0.7) if use_cand else None
+            fused = _abi.indexer_topk(q, w, 0.01, keys, start, 4, k, 129, cand, workspace=ws)
+            two = _abi.topk_select(_abi.indexer_score(q, w, 0.01, keys, start, 4, cand), k, start, 4, 129)
+            assert torch.equal(fused, two), (rep, b, n, h, nb, k)
 
 
 # ------------------------------------------------------------------ top-k and candidates
