@@ -229,10 +229,11 @@ int dsv41_indexer_score_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, c
  * 115-144: the scores of dsv41_indexer_score, then the selection of dsv41_topk_select, with
  * identical results): the [bsz*n, nb] scores are never written -- each workgroup's row range
  * keeps its best k (key, position) pairs in the workspace and a merge selects each query's k.
- * Served shapes: bf16 keys of dim 128, 16/32/64 heads, n < 8 or a candidate mask, and row ranges
- * of 2048 or 4096 rows at least twice k; dsv41_indexer_topk_workspace_bytes returns 0 for the
- * others (the entry point then returns DSV41_E_SHAPE). out [bsz*n, k] int32, k = min(topk, nb).
- * The workspace is 16-byte aligned. */
+ * Served shapes: bf16 keys of dim 128, 16/32/64 heads, n < 8 or a candidate mask, row ranges of
+ * 512, 1024, 2048 or 4096 rows at least twice k, and at most 32768 listed pairs per query;
+ * dsv41_indexer_topk_workspace_bytes returns 0 for the others (the entry point then returns
+ * DSV41_E_SHAPE). out [bsz*n, k] int32, k = min(topk, nb). The workspace is 16-byte aligned;
+ * calls that share one must not overlap (same stream, or ordered by events). */
 size_t dsv41_indexer_topk_workspace_bytes(int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
                                           int32_t topk, int32_t has_candidates);
 int dsv41_indexer_topk(const void* q, const void* w_raw, float w_scale, const void* index_k,

@@ -95,6 +95,15 @@ def test_contract_violations_are_reported_by_the_library():
     assert rc == -4 and b"workspace" in lib.dsv41_last_error_string()
     rc = lib.dsv41_topk_select_ws(fake, fake, 16, 1, 32768, 1024, 131071, 4, 129, fake, need - 1, None)
     assert rc == -4
+    # fused indexer + top-k: unserved shapes and a missing or short workspace, before any launch
+    need = _abi.indexer_topk_workspace_bytes(32, 1, 64, 128, 16384, 512)
+    args = (fake, fake, ctypes.c_float(0.01), fake, 16384 * 128, None, fake, 32, 1)
+    rc = lib.dsv41_indexer_topk(*args, 64, 128, 16384, 65535, 4, 512, 129, None, 0, None)
+    assert rc == -4 and b"workspace" in lib.dsv41_last_error_string()
+    rc = lib.dsv41_indexer_topk(*args, 64, 128, 16384, 65535, 4, 512, 129, fake, need - 1, None)
+    assert rc == -4
+    rc = lib.dsv41_indexer_topk(*args, 48, 128, 16384, 65535, 4, 512, 129, fake, need, None)
+    assert rc == -3 and b"fused" in lib.dsv41_last_error_string()
 
 
 def test_topk_workspace_sizes():
@@ -107,6 +116,23 @@ def test_topk_workspace_sizes():
     assert _abi.topk_workspace_bytes(16, 32768, 1024) == 2 * 16 * 8 * 1024 * 4
     assert _abi.topk_workspace_bytes(3, 16390, 512) == 2 * (((3 * 5 * 512 * 4) + 255) // 256 * 256)
     assert _abi.topk_workspace_bytes(0, 32768, 1024) == 0
+
+
+def test_indexer_topk_workspace_sizes():
+    """The fused decode form serves bf16 keys of 128 channels, 16/32/64 heads, fewer than 8
+    queries per row (or a candidate mask) and row ranges of at least 2k rows: two lists (keys,
+    positions) of k entries per (query, range)."""
+    from dsv41 import _abi
+    lists = lambda rows, ranges, k: 2 * ((rows * ranges * k * 4 + 255) // 256 * 256)   # noqa: E731
+    assert _abi.indexer_topk_workspace_bytes(32, 1, 64, 128, 16384, 512) == lists(32, 8, 512)
+    assert _abi.indexer_topk_workspace_bytes(16, 1, 64, 128, 32768, 1024) == lists(16, 16, 1024)
+    assert _abi.indexer_topk_workspace_bytes(2, 1, 64, 128, 256, 64) == lists(2, 1, 64)
+    assert _abi.indexer_topk_workspace_bytes(8, 8, 64, 128, 16384, 512, True) == lists(64, 4, 512)
+    assert _abi.indexer_topk_workspace_bytes(8, 8, 64, 128, 16384, 512) == 0     # prefill-sized, no mask
+    assert _abi.indexer_topk_workspace_bytes(8, 1, 64, 128, 16384, 512) == 0     # 512-row ranges < 2k
+    assert _abi.indexer_topk_workspace_bytes(32, 1, 48, 128, 16384, 512) == 0    # head count
+    assert _abi.indexer_topk_workspace_bytes(32, 1, 64, 64, 16384, 512) == 0     # key width
+    assert _abi.indexer_topk_workspace_bytes(0, 1, 64, 128, 16384, 512) == 0
 
 
 # ------------------------------------------------------------------ host logic
