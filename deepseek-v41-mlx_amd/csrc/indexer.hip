@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) part += fmaxf(acc[ht][i], 0.0f) * wv[ht][i];
+        for (int i = 0; i < 4; ++i) part += relu_bits(acc[ht][i]) * wv[ht][i];
       part = sum_rows4(part);
       const int row = tb + l16;
       if (g == 0 && row < vis_end) {
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(NW * 64) void indexer_decode_kernel(
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
-      for (int i2 = 0; i2 < 4; ++i2) part += fmaxf(acc[ht][i2], 0.0f) * wv[ht][i2];
+      for (int i2 = 0; i2 < 4; ++i2) part += relu_bits(acc[ht][i2]) * wv[ht][i2];
     part = sum_rows4(part);
     if (g == 0) sc_lds[16 * (NW * i + wave) + l16] = part;
   }
@@ -450,7 +450,7 @@ __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
       for (int ht = 0; ht < HT; ++ht) {
         const f32x4 acc = mfma_mxfp4(qa[ht], qsa[ht], kk.k[u], sb);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) part += fmaxf(acc[i], 0.0f) * wv[ht][i];
+        for (int i = 0; i < 4; ++i) part += relu_bits(acc[i]) * wv[ht][i];
       }
       part = sum_rows4(part);
       const int row = t0 + 16 * u + l16;
@@ -600,7 +600,7 @@ __global__ __launch_bounds__(kPfThreads, 4) void indexer_prefill_kernel(
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) part += fmaxf(acc[ht][i], 0.0f) * wv[ht][i];
+        for (int i = 0; i < 4; ++i) part += relu_bits(acc[ht][i]) * wv[ht][i];
       part = sum_rows4(part);
       const int row = r0 + c * kPfChunk + kt * 16 + l16;
       if (qok && g == 0 && row < vis_end) out[row] = row < lens ? part : -INFINITY;

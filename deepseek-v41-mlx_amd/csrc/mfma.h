@@ -89,6 +89,12 @@ __device__ __forceinline__ float sum_rows4(float v) {
   return __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
 }
 
+// max(x, 0) as one integer max of the bits: a negative float has the sign bit set, so it becomes
+// +0.0, and a non-negative one passes unchanged. fmaxf(x, 0.0f) costs two v_max_f32 in IEEE mode
+// (the first quiets a signalling NaN); this differs from it only for NaN inputs and in giving +0.0
+// for -0.0. Used on MFMA accumulators in the indexer epilogues.
+__device__ __forceinline__ float relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+
 // LDS byte offset of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
