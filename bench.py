@@ -435,9 +435,21 @@ def run_fp8_decode(args, torch, device):
             scores=torch.empty(B, 1, nb, dtype=torch.float32, device=device),
             out=torch.empty(B, 1, H, D, dtype=bf, device=device),
             ws=torch.empty(max(_abi.mla_workspace_bytes(B, 1, H, D, rows, bf), 1), dtype=torch.uint8,
-                           device=device)))
+                           device=device),
+            fidx=torch.empty(B, 1, K, dtype=torch.int32, device=device),
+            fws=torch.empty(max(_abi.indexer_topk_workspace_bytes(B, 1, Hi, Di, nb, K), 1), dtype=torch.uint8,
+                            device=device)))
+    # the fused indexer + top-k form serves ranges of at least 4k rows; top-1,024 over 32,768
+    # entries at B=16 takes the two calls, as the decode steps do
+    fused_ok = _abi.indexer_topk_workspace_bytes(B, 1, Hi, Di, nb, K) > 0
     cos, sin = precompute_freqs_cis(rd, start + 1, 65536, 160000.0, 16.0, 32, 1, device=device)
     wsc = weight_scale(Hi, Di, bf)
+
+    def f_fused(d):
+        # the step's scoring + selection: the fused form over the fp8 keys
+        sel = _abi.indexer_topk_fp8(d["iq"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, K, wp + 1,
+                                    out=d["fidx"], workspace=d["fws"])
+        assert sel is not None
 
     def f_idx(d):
         _abi.indexer_score_fp8(d["iq"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, out=d["scores"])
@@ -445,14 +457,18 @@ def run_fp8_decode(args, torch, device):
     def f_topk(d):
         d["idx"] = _abi.topk_select(d["scores"], K, start, r, wp + 1)
 
-    def f_sparse(d):
-        _abi.sparse_mla_fp8(d["q"], d["win"], d["chunk"], d["comp8"], d["comp_sc"], rb, nb, d["sink"], d["idx"],
+    def f_sparse(d, key="idx"):
+        _abi.sparse_mla_fp8(d["q"], d["win"], d["chunk"], d["comp8"], d["comp_sc"], rb, nb, d["sink"], d[key],
                             D ** -0.5, W, start, cos, sin, rd, out=d["out"], workspace=d["ws"])
 
     def full(d):
-        f_idx(d)
-        f_topk(d)
-        f_sparse(d)
+        if fused_ok:
+            f_fused(d)
+            f_sparse(d, "fidx")
+        else:
+            f_idx(d)
+            f_topk(d)
+            f_sparse(d)
 
     per = len(sets)
     reps = max(1, args.steps // per)
@@ -461,7 +477,8 @@ def run_fp8_decode(args, torch, device):
         g_full.replay()
     step_ms = time_graph(g_full, reps, torch) / per
     kern, graphs = {}, [g_full]
-    for name, fn in (("indexer_score", f_idx), ("topk_select", f_topk), ("sparse_mla", f_sparse)):
+    parts = (("indexer_topk", f_fused),) if fused_ok else ()
+    for name, fn in parts + (("indexer_score", f_idx), ("topk_select", f_topk), ("sparse_mla", f_sparse)):
         gr = graph_of(fn, sets, torch)
         graphs.append(gr)
         gr.replay()
@@ -469,9 +486,10 @@ def run_fp8_decode(args, torch, device):
         log(f"[bench] fp8 {name} {kern[name] * 1e3:.2f} us")
     torch.cuda.synchronize()
     b_idx = B * (nb * Di + (nb // rb) * (Di // 32) + Hi * Di * 2 + Hi * 2 + nb * 4)
+    b_fused = b_idx - B * nb * 4 + B * K * 4           # keys, scales, q, w in; indices out
     b_topk = B * (nb * 4 + K * 4)
     b_sparse = B * (K * (D + D // 32) + (rows - K) * D * 2 + 2 * H * D * 2 + K * 4)
-    step_bytes = b_idx + b_topk + b_sparse
+    step_bytes = (b_fused if fused_ok else b_idx + b_topk) + b_sparse
     log(f"[bench] fp8-cache decode step {step_ms * 1e3:.2f} us")
     return {
         "workload": "fp8-cache decode step: B=16, 131072-token context (nb=32768), top-1024; compressed KV and "
@@ -480,6 +498,7 @@ def run_fp8_decode(args, torch, device):
         "kernels_us": {k: v * 1e3 for k, v in kern.items()},
         "step_algorithmic_bytes": step_bytes,
         "hbm_GBps_step": step_bytes / (step_ms * 1e-3) / 1e9,
+        "fused_indexer_topk": fused_ok,
         "indexer_GBps": b_idx / (kern["indexer_score"] * 1e-3) / 1e9,
         "sparse_GBps": b_sparse / (kern["sparse_mla"] * 1e-3) / 1e9,
     }

@@ -741,7 +741,7 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
 // The fused decode form (indexer_decode_kernel with TJ > 0, then the top-k merge): shapes the
 // staged-copy decode kernel serves (bf16 keys of 128 channels, 16/32/64 heads, fewer than 8
 // queries per row or a candidate mask) with row ranges of 512, 1024, 2048 or 4096 rows, at least
-// twice k.
+// four times k.
 static bool idx_topk_plan(int64_t bsz, int n, int heads, int dim, int nb, int k, bool cand, int* rows_per_wg,
                           dim3* grid, int* tj) {
   if (dim != 128 || !(heads == 64 || heads == 32 || heads == 16)) return false;
@@ -749,7 +749,9 @@ static bool idx_topk_plan(int64_t bsz, int n, int heads, int dim, int nb, int k,
   *grid = idx_grid((int64_t)nb * bsz * n, nb, (int)(bsz * n), rows_per_wg);
   *tj = *rows_per_wg / 512;                        // 512, 1024, 2048 or 4096 rows: 1, 2, 4 or 8 per thread
   if (*tj != 1 && *tj != 2 && *tj != 4 && *tj != 8) return false;
-  return 2 * k <= *rows_per_wg && (int64_t)grid->x * k <= 32 * kSelThreads;
+  // a range keeps at most a quarter of its rows: at k = rows / 2 (B = 16, 32,768 entries, top-1,024)
+  // the per-range selection and a 16,384-entry merge cost what the unfused scores write saves
+  return 4 * k <= *rows_per_wg && (int64_t)grid->x * k <= 32 * kSelThreads;
 }
 
 static size_t idx_topk_ws(int64_t rows, unsigned chunks, int k) {
@@ -888,6 +890,53 @@ extern "C" int dsv41_indexer_topk(const void* q, const void* w_raw, float w_scal
   DSV41_FUSED_CASE(1, 1) DSV41_FUSED_CASE(1, 2) DSV41_FUSED_CASE(1, 4) DSV41_FUSED_CASE(1, 8)
   return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
 #undef DSV41_FUSED_CASE
+  const int rc = check_launch(what);
+  if (rc) return rc;
+  return topk_merge_launch(what, ckey, cpos, out, (int64_t)bsz * n, n, nb, k, (int)grid.x, rows_per_wg, start_pos,
+                           ratio, offset, stream);
+}
+
+extern "C" int dsv41_indexer_topk_fp8(const void* q, const void* w_raw, float w_scale, const uint8_t* index_k,
+                                      int64_t k_bstride, const uint8_t* k_scale, int64_t ks_bstride, int32_t ks_rb,
+                                      const uint8_t* candidates, int32_t* out, int32_t bsz, int32_t n, int32_t heads,
+                                      int32_t dim, int32_t nb, int32_t start_pos, int32_t ratio, int32_t topk,
+                                      int32_t offset, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const char* what = "dsv41_indexer_topk_fp8";
+  DSV41_REQUIRE(q && w_raw && index_k && k_scale && out, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(bsz >= 0 && n > 0 && heads > 0 && dim > 0 && nb >= 0 && start_pos >= 0 && ratio > 0 && topk >= 0,
+                DSV41_E_ARG, "%s: bad sizes", what);
+  DSV41_REQUIRE(ks_rb == 1 || ks_rb == 32, DSV41_E_ARG, "%s: scale row block must be 1 or 32", what);
+  DSV41_REQUIRE(k_bstride >= (int64_t)nb * dim, DSV41_E_ARG, "%s: k_bstride too small", what);
+  DSV41_REQUIRE(ks_bstride >= (int64_t)((nb + ks_rb - 1) / ks_rb) * (dim / 32), DSV41_E_ARG,
+                "%s: ks_bstride too small", what);
+  DSV41_REQUIRE(aligned16(q) && aligned16(w_raw) && aligned16(index_k) && aligned16(k_scale) &&
+                    k_bstride % 16 == 0 && ks_bstride % 16 == 0,
+                DSV41_E_ARG, "%s: q, w_raw, index_k and k_scale must be 16-byte aligned, both strides multiples of 16",
+                what);
+  const int k = topk < nb ? topk : nb;
+  if ((int64_t)bsz * n == 0 || nb == 0 || k == 0) return 0;
+  int rows_per_wg = 0, tj = 0;
+  dim3 grid;
+  DSV41_REQUIRE(idx_topk_plan(bsz, n, heads, dim, nb, k, candidates != nullptr, &rows_per_wg, &grid, &tj),
+                DSV41_E_SHAPE, "%s: shape not served by the fused form (dsv41_indexer_topk_workspace_bytes is 0)",
+                what);
+  const size_t need = idx_topk_ws((int64_t)bsz * n, grid.x, k);
+  DSV41_REQUIRE(workspace && workspace_bytes >= need, DSV41_E_WORKSPACE, "%s: workspace of %zu bytes needed", what,
+                need);
+  DSV41_REQUIRE(aligned16(workspace), DSV41_E_ARG, "%s: workspace must be 16-byte aligned", what);
+  uint32_t* ckey = reinterpret_cast<uint32_t*>(workspace);
+  int32_t* cpos = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(workspace) + need / 2);
+#define DSV41_FUSED8_CASE(HT_, TJ_)                                                                            \
+  if (heads == HT_ * 16 && tj == TJ_) {                                                                        \
+    hipLaunchKernelGGL((indexer_decode_kernel<HT_, kDecWaves, true, TJ_>), grid, dim3(kDecWaves * 64), 0,      \
+                       stream, (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, index_k, k_bstride, k_scale,   \
+                       ks_bstride, ks_rb, candidates, nullptr, n, nb, start_pos, ratio, rows_per_wg, k, ckey, cpos); \
+  } else
+  DSV41_FUSED8_CASE(4, 1) DSV41_FUSED8_CASE(4, 2) DSV41_FUSED8_CASE(4, 4) DSV41_FUSED8_CASE(4, 8)
+  DSV41_FUSED8_CASE(2, 1) DSV41_FUSED8_CASE(2, 2) DSV41_FUSED8_CASE(2, 4) DSV41_FUSED8_CASE(2, 8)
+  DSV41_FUSED8_CASE(1, 1) DSV41_FUSED8_CASE(1, 2) DSV41_FUSED8_CASE(1, 4) DSV41_FUSED8_CASE(1, 8)
+  return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
+#undef DSV41_FUSED8_CASE
   const int rc = check_launch(what);
   if (rc) return rc;
   return topk_merge_launch(what, ckey, cpos, out, (int64_t)bsz * n, n, nb, k, (int)grid.x, rows_per_wg, start_pos,

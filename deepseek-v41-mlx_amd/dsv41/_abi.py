@@ -64,6 +64,8 @@ _SIGNATURES = {
     "dsv41_indexer_topk_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32, _i32],
     "dsv41_indexer_topk": [_c_p, _c_p, _f32, _c_p, _i64, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                            _i32, _i32, _c_p, _sz, _c_p],
+    "dsv41_indexer_topk_fp8": [_c_p, _c_p, _f32, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32, _i32, _i32, _i32,
+                               _i32, _i32, _i32, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_topk_select_ws": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_candidate_blocks": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _i32, _i32, _c_p],
     "dsv41_sparse_mla_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32],
@@ -485,6 +487,40 @@ def indexer_score_fp8(q, w_raw, w_scale, index_k8, k_scale, scale_rb, nb, start_
     cand = candidates.view(torch.uint8) if candidates is not None else None
     _call(name, _ptr(q), _ptr(w_raw), float(w_scale), _ptr(index_k8), row_stride(index_k8, name), _ptr(k_scale),
           row_stride(k_scale, name), scale_rb, _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, _stream(q))
+    return out
+
+
+def indexer_topk_fp8(q, w_raw, w_scale, index_k8, k_scale, scale_rb, nb, start_pos, ratio, topk, offset,
+                     candidates=None, out=None, workspace=None):
+    """indexer_topk over fp8 keys (the layouts of indexer_score_fp8): int32 [b, n, min(topk, nb)],
+    bit-equal to topk_select(indexer_score_fp8(...)). Returns None when the fused form does not
+    serve the shape or the layout (scales and both strides 16-byte aligned)."""
+    name = "dsv41_indexer_topk_fp8"
+    _gpu(name, q, w_raw, index_k8, k_scale, candidates, out, workspace)
+    _contig(name, q, w_raw, candidates)
+    b, n, h, d = q.shape
+    if q.dtype != torch.bfloat16 or d != 128 or w_raw.shape != (b, n, h) or w_raw.dtype != q.dtype:
+        raise ValueError(f"{name}: q must be bf16 [b, n, h, 128] and w_raw bf16 [{b}, {n}, {h}]")
+    if index_k8.dtype != torch.uint8 or index_k8.shape[0] < b or index_k8.shape[2] != d or index_k8.shape[1] < nb:
+        raise ValueError(f"{name}: fp8 keys {tuple(index_k8.shape)} {index_k8.dtype} do not match")
+    if (k_scale.dtype != torch.uint8 or k_scale.shape[0] < b or k_scale.shape[2] != d // 32
+            or k_scale.shape[1] < -(-nb // scale_rb)):
+        raise ValueError(f"{name}: key scales {tuple(k_scale.shape)} do not match")
+    if candidates is not None and (candidates.shape != (b, n, nb) or candidates.dtype not in (torch.uint8, torch.bool)):
+        raise ValueError(f"{name}: candidates must be bool/uint8 [{b}, {n}, {nb}]")
+    ks_stride = row_stride(k_scale, name)
+    ws_bytes = indexer_topk_workspace_bytes(b, n, h, d, nb, topk, candidates is not None)
+    if ws_bytes == 0 or k_scale.data_ptr() % 16 or ks_stride % 16 or index_k8.data_ptr() % 16:
+        return None
+    k = min(topk, nb)
+    out = torch.empty(b, n, k, dtype=torch.int32, device=q.device) if out is None else out
+    if out.dtype != torch.int32 or tuple(out.shape) != (b, n, k) or not out.is_contiguous():
+        raise ValueError(f"{name}: out must be contiguous int32 [{b}, {n}, {k}]")
+    ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else _workspace(ws_bytes, q.device)
+    cand = candidates.view(torch.uint8) if candidates is not None else None
+    _call(name, _ptr(q), _ptr(w_raw), float(w_scale), _ptr(index_k8), row_stride(index_k8, name), _ptr(k_scale),
+          ks_stride, scale_rb, _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, topk, offset, _ptr(ws),
+          ws_bytes, _stream(q))
     return out
 
 

@@ -90,9 +90,9 @@ class StackDecodeStep:
     and ``w_scale``; kv sources add ``latent`` [b,1,D] (pre-rope); key owners add ``k_raw``
     [b,1,Di] and ``k_norm`` [Di]. Caches may be dense, carry MXFP4 index keys, or be the fp8
     variant (cache_format "fp8": fp8 compressed KV and index keys); each layer takes the kernels
-    that read and write its owners' format. On dense bf16 keys, index sources other than the
-    candidate source score and select in the fused form (dsv41_indexer_topk) where it serves
-    the shape; the candidate source writes its scores for the block mask (kept in
+    that read and write its owners' format. On dense bf16 or fp8 keys, index sources other than
+    the candidate source score and select in the fused form (dsv41_indexer_topk(_fp8)) where it
+    serves the shape; the candidate source writes its scores for the block mask (kept in
     ``candidates``).
     Outputs (``out`` per layer) and scratch are allocated once, so a step can be captured in
     a HIP graph.
@@ -180,23 +180,29 @@ class StackDecodeStep:
                     keys = key_src.index_keys(b, nb)
                     c = cand if p.uses_candidates else None
                     kind = getattr(keys, "kind", None)
-                    fuse = kind is None and p.fused_idx is not None
-                    if fuse:
-                        topk = p.idx = _abi.indexer_topk(x["index_q"], x["w_raw"], x["w_scale"], keys, sp, p.ratio,
-                                                         a.index_topk, self.offset, c, out=p.fused_idx,
-                                                         workspace=self.fused_ws)
-                    elif kind == "mxfp4":
-                        _abi.indexer_score_mxfp4(x["index_q_mx"], x["w_raw"], x["w_scale"], keys.codes, keys.scales,
-                                                 nb, sp, p.ratio, c, out=scores)
-                    elif kind == "fp8":
-                        _abi.indexer_score_fp8(x["index_q"], x["w_raw"], x["w_scale"], keys.codes, keys.scales, 1, nb,
-                                               sp, p.ratio, c, out=scores)
+                    sel = None                     # the fused form's selection, where it serves the layer
+                    if p.fused_idx is not None and kind is None:
+                        sel = _abi.indexer_topk(x["index_q"], x["w_raw"], x["w_scale"], keys, sp, p.ratio,
+                                                a.index_topk, self.offset, c, out=p.fused_idx, workspace=self.fused_ws)
+                    elif p.fused_idx is not None and kind == "fp8":
+                        sel = _abi.indexer_topk_fp8(x["index_q"], x["w_raw"], x["w_scale"], keys.codes, keys.scales,
+                                                    1, nb, sp, p.ratio, a.index_topk, self.offset, c,
+                                                    out=p.fused_idx, workspace=self.fused_ws)
+                    if sel is not None:
+                        topk = p.idx = sel
                     else:
-                        _abi.indexer_score(x["index_q"], x["w_raw"], x["w_scale"], keys, sp, p.ratio, c, out=scores)
-                    if p.candidate_source:
-                        cand = self.candidates = _abi.candidate_blocks(scores, a.candidate_topk_blocks,
-                                                                       a.candidate_block_size, None, sp, p.ratio)
-                    if not fuse:
+                        if kind == "mxfp4":
+                            _abi.indexer_score_mxfp4(x["index_q_mx"], x["w_raw"], x["w_scale"], keys.codes,
+                                                     keys.scales, nb, sp, p.ratio, c, out=scores)
+                        elif kind == "fp8":
+                            _abi.indexer_score_fp8(x["index_q"], x["w_raw"], x["w_scale"], keys.codes, keys.scales, 1,
+                                                   nb, sp, p.ratio, c, out=scores)
+                        else:
+                            _abi.indexer_score(x["index_q"], x["w_raw"], x["w_scale"], keys, sp, p.ratio, c,
+                                               out=scores)
+                        if p.candidate_source:
+                            cand = self.candidates = _abi.candidate_blocks(scores, a.candidate_topk_blocks,
+                                                                           a.candidate_block_size, None, sp, p.ratio)
                         topk = p.idx = _abi.topk_select(scores, a.index_topk, sp, p.ratio, self.offset)
                 if p.kv_source and emits and lc.comp_kv8 is not None:
                     _abi.comp_write_fp8(x["latent"], lc.comp_kv8, lc.comp_ks, nb - 1, p.ratio, p.cos, p.sin,

@@ -230,7 +230,7 @@ int dsv41_indexer_score_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, c
  * identical results): the [bsz*n, nb] scores are never written -- each workgroup's row range
  * keeps its best k (key, position) pairs in the workspace and a merge selects each query's k.
  * Served shapes: bf16 keys of dim 128, 16/32/64 heads, n < 8 or a candidate mask, row ranges of
- * 512, 1024, 2048 or 4096 rows at least twice k, and at most 32768 listed pairs per query;
+ * 512, 1024, 2048 or 4096 rows at least four times k, and at most 32768 listed pairs per query;
  * dsv41_indexer_topk_workspace_bytes returns 0 for the others (the entry point then returns
  * DSV41_E_SHAPE). out [bsz*n, k] int32, k = min(topk, nb). The workspace is 16-byte aligned;
  * calls that share one must not overlap (same stream, or ordered by events). */
@@ -241,6 +241,17 @@ int dsv41_indexer_topk(const void* q, const void* w_raw, float w_scale, const vo
                        int32_t n, int32_t heads, int32_t dim, int32_t nb, int32_t start_pos,
                        int32_t ratio, int32_t topk, int32_t offset, void* workspace,
                        size_t workspace_bytes, hipStream_t stream);
+
+/* dsv41_indexer_topk over fp8 index keys (the layout of dsv41_indexer_score_fp8: e4m3 codes with
+ * k_bstride bytes per batch row, ue8m0 scales per 32 channels of every ks_rb = 1 or 32 rows with
+ * ks_bstride bytes per batch row): bit-equal to dsv41_indexer_score_fp8 followed by
+ * dsv41_topk_select. Served shapes and the workspace are dsv41_indexer_topk's (same size query);
+ * q, w_raw, index_k and k_scale 16-byte aligned, both strides multiples of 16 bytes. */
+int dsv41_indexer_topk_fp8(const void* q, const void* w_raw, float w_scale, const uint8_t* index_k,
+                           int64_t k_bstride, const uint8_t* k_scale, int64_t ks_bstride, int32_t ks_rb,
+                           const uint8_t* candidates, int32_t* out, int32_t bsz, int32_t n, int32_t heads,
+                           int32_t dim, int32_t nb, int32_t start_pos, int32_t ratio, int32_t topk,
+                           int32_t offset, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Top-k selection, deepseek_v41_mlx/indexer.py:200-204: per row of scores [bsz*n, nb],
  * the k = min(topk, nb) best positions (ties -> lowest position; -0.0 == +0.0), sorted

@@ -120,16 +120,17 @@ def test_topk_workspace_sizes():
 
 def test_indexer_topk_workspace_sizes():
     """The fused decode form serves bf16 keys of 128 channels, 16/32/64 heads, fewer than 8
-    queries per row (or a candidate mask) and row ranges of at least 2k rows: two lists (keys,
+    queries per row (or a candidate mask) and row ranges of at least 4k rows: two lists (keys,
     positions) of k entries per (query, range)."""
     from dsv41 import _abi
     lists = lambda rows, ranges, k: 2 * ((rows * ranges * k * 4 + 255) // 256 * 256)   # noqa: E731
     assert _abi.indexer_topk_workspace_bytes(32, 1, 64, 128, 16384, 512) == lists(32, 8, 512)
-    assert _abi.indexer_topk_workspace_bytes(16, 1, 64, 128, 32768, 1024) == lists(16, 16, 1024)
+    assert _abi.indexer_topk_workspace_bytes(16, 1, 64, 128, 32768, 512) == lists(16, 16, 512)
+    assert _abi.indexer_topk_workspace_bytes(16, 1, 64, 128, 32768, 1024) == 0   # k above a quarter of a range
     assert _abi.indexer_topk_workspace_bytes(2, 1, 64, 128, 256, 64) == lists(2, 1, 64)
     assert _abi.indexer_topk_workspace_bytes(8, 8, 64, 128, 16384, 512, True) == lists(64, 4, 512)
     assert _abi.indexer_topk_workspace_bytes(8, 8, 64, 128, 16384, 512) == 0     # prefill-sized, no mask
-    assert _abi.indexer_topk_workspace_bytes(8, 1, 64, 128, 16384, 512) == 0     # 512-row ranges < 2k
+    assert _abi.indexer_topk_workspace_bytes(8, 1, 64, 128, 16384, 512) == 0     # 512-row ranges < 4k
     assert _abi.indexer_topk_workspace_bytes(32, 1, 48, 128, 16384, 512) == 0    # head count
     assert _abi.indexer_topk_workspace_bytes(32, 1, 64, 64, 16384, 512) == 0     # key width
     assert _abi.indexer_topk_workspace_bytes(0, 1, 64, 128, 16384, 512) == 0

@@ -400,13 +400,36 @@ def test_indexer_topk_fused_equals_two_calls(gpu, b, n, h, nb, topk, start, use_
     assert torch.equal(fused, two)
 
 
+@pytest.mark.parametrize("b,n,h,nb,topk,start,rb,use_cand", [
+    (16, 1, 64, 32768, 512, 131071, 32, False),    # bs16, 128K context, scales per 32 x 32 block
+    (8, 4, 16, 16384, 512, 20000, 1, False),       # causal rows, per-row scales, ranges past visibility
+    (32, 1, 32, 16384, 512, 65535, 1, True),       # candidate-masked consumer
+])
+def test_indexer_topk_fp8_equals_two_calls(gpu, b, n, h, nb, topk, start, rb, use_cand):
+    """The fused form over fp8 keys selects exactly what indexer_score_fp8 + topk_select select."""
+    from dsv41 import _abi
+    g = torch.Generator(gpu).manual_seed(SEED_BASE + 47)
+    q = (torch.randn(b, n, h, 128, generator=g, device=gpu) * 0.3).bfloat16()
+    w = torch.randn(b, n, h, generator=g, device=gpu).bfloat16()
+    codes = torch.randint(0, 256, (b, nb, 128), generator=g, device=gpu, dtype=torch.int32)
+    codes = torch.where((codes & 0x7F) == 0x7F, codes ^ 1, codes).to(torch.uint8)     # no NaN codes
+    nblk = -(-nb // rb)
+    scales = torch.randint(123, 132, (b, (nblk + 3) // 4 * 4, 4), generator=g, device=gpu,
+                           dtype=torch.int32).to(torch.uint8)
+    cand = (torch.rand(b, n, nb, generator=g, device=gpu) < 0.7) if use_cand else None
+    fused = _abi.indexer_topk_fp8(q, w, 0.01, codes, scales, rb, nb, start, 4, topk, 129, cand)
+    assert fused is not None
+    scores = _abi.indexer_score_fp8(q, w, 0.01, codes, scales, rb, nb, start, 4, cand)
+    assert torch.equal(fused, _abi.topk_select(scores, topk, start, 4, 129))
+
+
 def test_indexer_topk_shared_workspace(gpu):
     """One workspace through a sequence of fused calls of different shapes (query counts, row
     ranges, k, candidate masks, ranges past visibility): every call equals the two-call form."""
     from dsv41 import _abi
     shapes = [(32, 1, 64, 16384, 512, 65535, False), (8, 4, 16, 16384, 512, 20000, False),
               (32, 1, 32, 16384, 512, 65535, True), (2, 1, 64, 256, 64, 1024, False),
-              (16, 1, 64, 32768, 1024, 131071, False)]
+              (16, 1, 64, 32768, 512, 131071, False)]
     need = [_abi.indexer_topk_workspace_bytes(b, n, h, 128, nb, k, c) for b, n, h, nb, k, _, c in shapes]
     assert min(need) > 0
     ws = torch.empty(max(need), dtype=torch.uint8, device=gpu)

@@ -169,8 +169,8 @@ def test_c2_decode_step(gpu):
 
 @pytest.mark.parametrize("b,nb,K,start", [
     (32, 16384, 512, 65535),     # bs32, 64K context: 8 row ranges of 2048 per query
-    (16, 32768, 1024, 131071),   # bs16, 128K context, top-1024: 8 ranges of 4096
-    (32, 4096, 256, 16386),      # ranges of 512, top-256; 3 tokens of the next group still open
+    (64, 16384, 512, 65535),     # B=64: 4 ranges of 4096
+    (32, 4096, 128, 16386),      # ranges of 512, top-128; 3 tokens of the next group still open
 ])
 def test_decode_step_fused_equals_two_calls(gpu, b, nb, K, start):
     """The decode step with the fused indexer + top-k form selects exactly what indexer_score +
