@@ -135,6 +135,16 @@ __device__ __forceinline__ bf16x8 cvt_bf16x8(const float* v) {
   return r;
 }
 
+// Two floats -> packed bf16 pair (a in the low half) with the hardware round-to-nearest-even
+// convert (v_cvt_pk_bf16_f32): the bits of f2bf for every non-NaN value, in one instruction.
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+  bf16x2 v;
+  v[0] = (__bf16)a;
+  v[1] = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // 2^x with the bare v_exp_f32 (no denormal-range fix-up). Used for softmax weights 2^(s - m) with
 // s - m <= the lazy-rescale threshold: results below 2^-126 are zero for the sum anyway.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

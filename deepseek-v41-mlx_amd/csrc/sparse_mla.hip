@@ -187,8 +187,8 @@ __device__ __forceinline__ void store_out4(const MlaArgs& a, int D, int qs, bf16
   rope_inv_pair(a, D, qs, d0, v[0], v[1], true);
   rope_inv_pair(a, D, qs, d0 + 2, v[2], v[3], true);
   uint2 st;
-  st.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-  st.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+  st.x = pack2_bf16(v[0], v[1]);
+  st.y = pack2_bf16(v[2], v[3]);
   *reinterpret_cast<uint2*>(orow + d0) = st;
 }
 
@@ -431,8 +431,8 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
       store_out4(a, D, qs, orow, d0, acc[dt], l_run);
     } else {
       uint2 st;
-      st.x = (uint32_t)f2bf(acc[dt][0] * inv) | ((uint32_t)f2bf(acc[dt][1] * inv) << 16);
-      st.y = (uint32_t)f2bf(acc[dt][2] * inv) | ((uint32_t)f2bf(acc[dt][3] * inv) << 16);
+      st.x = pack2_bf16(acc[dt][0] * inv, acc[dt][1] * inv);
+      st.y = pack2_bf16(acc[dt][2] * inv, acc[dt][3] * inv);
       *reinterpret_cast<uint2*>(a.part_o + slot_id * D + d0) = st;
     }
   }
@@ -444,10 +444,11 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
 
 // Merges split partials of one query: one wave per head, 4 heads per workgroup. Split s holds
 // (m_s, l_s, o_s) = (log2-domain max, denominator, numerator / l_s in bf16); the merged row is
-// sum_s w_s o_s / sum_s w_s with w_s = l_s 2^(m_s - M). Lane s reads split s's (m_s, l_s); the
-// weights reach every lane by readlane. NB numerator rows (splits clamped to the last one, whose
-// weight past ns is 0) are loaded together before any weight is formed; splits beyond NB are
-// streamed. Each lane covers 8 channels per 512. Splits are at most 64 (the planner's bound).
+// sum_s w_s o_s / sum_s w_s with w_s = l_s 2^(m_s - M). Every lane reads every split's
+// (m_s, l_s) (the same addresses across the wave), so the weights need no cross-lane exchange.
+// NB numerator rows and (m, l) pairs (splits clamped to the last one, whose weight past ns is 0)
+// are loaded together before any weight is formed; splits beyond NB are streamed. Each lane
+// covers 8 channels per 512.
 template <typename T, int NB>
 __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
   const int unit = blockIdx.x;
@@ -525,10 +526,10 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
       if (in_rope_tail(a, D, d + 2 * j)) rope_inv_apply(cs[j], -sn[j], v[2 * j], v[2 * j + 1]);
     if constexpr (sizeof(T) == 2) {
       uint4 st;
-      st.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-      st.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-      st.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
-      st.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+      st.x = pack2_bf16(v[0], v[1]);
+      st.y = pack2_bf16(v[2], v[3]);
+      st.z = pack2_bf16(v[4], v[5]);
+      st.w = pack2_bf16(v[6], v[7]);
       *reinterpret_cast<uint4*>(orow + d) = st;
     } else {
 #pragma unroll
