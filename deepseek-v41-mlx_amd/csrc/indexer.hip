@@ -1,4 +1,4 @@
-// Indexer scoring, deepseek_v41_mlx/indexer.py:183-198:
+// Indexer scoring, deepseek_v41_mlx/indexer.py:123-138:
 //   S[b,s,t] = sum_h relu(q[b,s,h,:] . k[b,t,:]) * w[b,s,h],  t >= lens_s -> -inf,
 //   candidate-masked -> -inf, with w = round_dtype(w_raw * w_scale).
 //

@@ -1,4 +1,4 @@
-// Top-k selection of the indexer, deepseek_v41_mlx/indexer.py:200-204, and the block-level
+// Top-k selection of the indexer, deepseek_v41_mlx/indexer.py:140-144, and the block-level
 // candidate pre-filter, indexer.py:38-64.
 //
 // Order: the k best scores, ties broken by the lowest position (the rule the reference leaves

@@ -44,7 +44,7 @@ def select_candidate_blocks(scores: torch.Tensor, lens, topk_blocks: int,
 
 def weight_scale(n_heads: int, head_dim: int, dtype) -> float:
     """head_dim**-0.5 * n_heads**-0.5 as the activation dtype holds it: a python scalar
-    multiplying an MLX array takes the array's dtype (indexer.py:183)."""
+    multiplying an MLX array takes the array's dtype (indexer.py:123)."""
     return float(torch.tensor(head_dim ** -0.5 * n_heads ** -0.5, dtype=dtype).float())
 
 

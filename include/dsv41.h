@@ -171,13 +171,13 @@ int dsv41_index_key_publish_mxfp4(const void* k_raw, uint8_t* k_codes, int64_t k
 /* ---------------------------------------------------------------- indexer --
  */
 
-/* The index-query prologue, deepseek_v41_mlx/indexer.py:179-181: in place on
+/* The index-query prologue, deepseek_v41_mlx/indexer.py:119-121: in place on
  * q [bsz, n, heads, dim], q <- fake_quant_fp4_ue8m0(rope_tail(q, positions start_pos+s), 32). */
 int dsv41_index_q_prep(void* q, const float* cos_tab, const float* sin_tab, int32_t bsz,
                        int32_t n, int32_t heads, int32_t dim, int32_t rd, int32_t start_pos,
                        int32_t dtype, hipStream_t stream);
 
-/* Indexer scoring, deepseek_v41_mlx/indexer.py:183-198:
+/* Indexer scoring, deepseek_v41_mlx/indexer.py:123-138:
  *   scores[b,s,t] = sum_h relu(q[b,s,h,:] . index_k[b,t,:]) * w[b,s,h]      (fp32)
  *   w = round_dtype(w_raw * w_scale); t >= (start_pos+s+1)/ratio -> -inf;
  *   candidates (optional, uint8 [bsz,n,nb], 0 = masked) -> -inf.
@@ -253,7 +253,7 @@ int dsv41_indexer_topk_fp8(const void* q, const void* w_raw, float w_scale, cons
                            int32_t dim, int32_t nb, int32_t start_pos, int32_t ratio, int32_t topk,
                            int32_t offset, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-/* Top-k selection, deepseek_v41_mlx/indexer.py:200-204: per row of scores [bsz*n, nb],
+/* Top-k selection, deepseek_v41_mlx/indexer.py:140-144: per row of scores [bsz*n, nb],
  * the k = min(topk, nb) best positions (ties -> lowest position; -0.0 == +0.0), sorted
  * ascending, written as idx + offset when idx < lens else -1, lens = (start_pos+s+1)/ratio,
  * s = row % n. out [bsz*n, k] int32. nb <= 1<<22. */
@@ -262,7 +262,7 @@ int dsv41_topk_select(const float* scores, int32_t* out, int64_t rows, int32_t n
                       hipStream_t stream);
 
 /* The same selection with a caller-owned workspace (same reference function,
- * deepseek_v41_mlx/indexer.py:200-204; identical results): rows longer than 16384 scores with
+ * deepseek_v41_mlx/indexer.py:140-144; identical results): rows longer than 16384 scores with
  * k <= 2048 are then selected in two stages (each 4096-score chunk's best k, then the best k of
  * those lists), spreading a row over several workgroups. The workspace is
  * dsv41_topk_workspace_bytes(rows, nb, topk) bytes, 16-byte aligned (0: one stage, workspace

@@ -319,13 +319,13 @@ def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale: float, chunk: int = 
 
 
 def query_lens(start_pos: int, n: int, ratio: int) -> np.ndarray:
-    """Visible compressed entries per query, (start_pos+s+1)//ratio (indexer.py:189-191)."""
+    """Visible compressed entries per query, (start_pos+s+1)//ratio (indexer.py:129-131)."""
     return ((start_pos + np.arange(n) + 1) // ratio).astype(np.int64)
 
 
 def indexer_scores(q, index_k, w, start_pos: int, ratio: int, candidates=None) -> np.ndarray:
     """fp32 scores S[b,s,t] = sum_h relu(q.k) * w, visibility and candidate masks
-    (indexer.py:183-198). q [b,n,hi,di], index_k [b,nb,di], w [b,n,hi] fp32."""
+    (indexer.py:123-138). q [b,n,hi,di], index_k [b,nb,di], w [b,n,hi] fp32."""
     q = np.asarray(q, F32)
     k = np.asarray(index_k, F32)
     w = np.asarray(w, F32)
@@ -355,7 +355,7 @@ def topk_order(scores, k: int) -> np.ndarray:
 
 
 def topk_indices(scores, index_topk: int, lens, offset: int) -> np.ndarray:
-    """Top-k, ascending position order, -1 past lens, + offset (indexer.py:200-204).
+    """Top-k, ascending position order, -1 past lens, + offset (indexer.py:140-144).
 
     scores [b,n,nb]; lens [n] (per query)."""
     nb = scores.shape[-1]
@@ -577,7 +577,7 @@ def publish_keys(latents, start_pos, ratio, rd, cos, sin, p, eps, dtype, cache: 
 
 def index_weight_scale(hi: int, di: int, dtype: str) -> np.float32:
     """softmax_scale * n_heads**-0.5 as the activation dtype sees it: an MLX python
-    scalar takes the array's dtype (indexer.py:183)."""
+    scalar takes the array's dtype (indexer.py:123)."""
     return cast(np.array([di ** -0.5 * hi ** -0.5], F32), dtype)[0]
 
 
