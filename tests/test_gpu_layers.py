@@ -193,3 +193,51 @@ def test_decode_step_fused_equals_two_calls(gpu, b, nb, K, start):
     torch.cuda.synchronize()
     assert torch.equal(i1, i2)
     assert torch.equal(o1, o2)
+
+
+def test_decode_step_graph_replays(gpu):
+    """The bs32 / 64K decode step (fused indexer + top-k, sparse MLA with its split combine)
+    captured in a HIP graph over two input sets: every replay, with eager work and host
+    synchronizations between replays, equals the eager step bit for bit."""
+    from dsv41.layers import precompute_freqs_cis
+    from dsv41.step import SparseDecodeStep
+    b, nb, K, start = 32, 16384, 512, 65535
+    H, D, Hi, Di, W, rd, r = 64, 512, 64, 128, 128, 64, 4
+    g = torch.Generator(gpu).manual_seed(SEED_BASE + 42)
+    rn = lambda *s: torch.randn(*s, generator=g, device=gpu)   # noqa: E731
+    sc = 576 ** -0.5
+    cos, sin = precompute_freqs_cis(rd, start + 1, 65536, 160000.0, 16.0, 32, 1, device=gpu)
+    sets, steps = [], []
+    for _ in range(2):
+        sets.append(dict(q=(rn(b, 1, H, D) * sc).bfloat16(), win=(rn(b, W, D) * sc).bfloat16(),
+                         chunk=(rn(b, 1, D) * sc).bfloat16(), comp=(rn(b, nb, D) * sc).bfloat16(),
+                         iq=rn(b, 1, Hi, Di).bfloat16(), ik=rn(b, nb, Di).bfloat16(), w=rn(b, 1, Hi).bfloat16(),
+                         sink=rn(H)))
+        steps.append(SparseDecodeStep(b, H, D, rd, Hi, Di, nb, K, W, start, r, torch.bfloat16, gpu))
+
+    def run(i):
+        d = sets[i]
+        return steps[i](d["q"], d["iq"], d["w"], 0.01, d["ik"], d["comp"], d["win"], d["chunk"], d["sink"], cos, sin)
+
+    want = [tuple(t.clone() for t in run(i)) for i in range(2)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run(0)
+        run(1)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = [run(0), run(1)]
+    for rep in range(3):
+        for st in steps:
+            st.out.zero_()
+            st.idx.fill_(-7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert steps[i].fused
+            assert torch.equal(got[i][1], want[i][1]), (rep, i)
+            assert torch.equal(got[i][0], want[i][0]), (rep, i)

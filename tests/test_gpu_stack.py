@@ -270,3 +270,42 @@ def test_c4_full_size_sampled_rows(gpu):
                                   comp20 if ratio else None, idx36[b, 0] if ratio else None, f(ins[l]["sink"]),
                                   sp, ratio)
             assert rel_max_diff(to_np(outs[l][b, 0]), o) < 2e-2, f"layer {l} row {b}"
+
+
+def test_stack_step_graph_replays(gpu):
+    """The 40-layer step captured in a HIP graph: every replay, with eager work and host
+    synchronizations between replays, reproduces the eager step bit for bit (outputs and the
+    fused top-k of the last index source). Top-128 over 4,096 entries at B=16 takes the fused
+    indexer + top-k form on every index source but the candidate source; the step's writes (ring
+    slot, owner latent and key) store the same values on every replay."""
+    from dsv41.cache import ModelCache
+    from dsv41.step import StackDecodeStep
+    a = c4_args(index_topk=128, candidate_topk_blocks=256, max_seq_len=16384)
+    B, sp = 16, 16383
+    gen = torch.Generator(device=gpu).manual_seed(SEED_BASE + 9)
+    cache = ModelCache(a, B, 16384, torch.bfloat16, gpu)
+    c4_fill_cache(cache, gen)
+    ins = c4_inputs(a, B, gen, gpu)
+    step = StackDecodeStep(a, B, sp, torch.bfloat16, gpu)
+    assert sum(p.fused_idx is not None for p in step.plan) == 7
+    want = [o.clone() for o in step(cache, ins)]
+    want_idx = step.plan[36].idx.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(cache, ins)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step(cache, ins)
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        step.plan[36].idx.fill_(-7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for l, (o, w) in enumerate(zip(outs, want)):
+            assert torch.equal(o, w), (rep, l)
+        assert torch.equal(step.plan[36].idx, want_idx), rep
