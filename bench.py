@@ -633,6 +633,48 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
     }
 
 
+def achievable_peaks(torch, device):
+    """What this box reaches, measured in the same run: a device-to-device copy (torch's copy
+    kernel) over 4 rotating 256 MiB bf16 buffers, read + write bytes per second; and a 8192^3
+    bf16 torch.matmul (hipBLASLt), flops per second. The fractions against these sit beside the
+    ones against the published peaks."""
+    n = 256 << 20
+    srcs = [torch.ones(n // 2, dtype=torch.bfloat16, device=device) for _ in range(4)]
+    dsts = [torch.empty_like(x) for x in srcs]
+    for x, y in zip(srcs, dsts):
+        y.copy_(x)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 40
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(reps):
+        dsts[i % 4].copy_(srcs[i % 4])
+    e1.record()
+    torch.cuda.synchronize()
+    copy_gbs = 2 * n * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del srcs, dsts
+    m = 8192
+    a = torch.randn(m, m, dtype=torch.bfloat16, device=device)
+    b = torch.randn(m, m, dtype=torch.bfloat16, device=device)
+    c = torch.empty(m, m, dtype=torch.bfloat16, device=device)
+    for _ in range(3):
+        torch.matmul(a, b, out=c)
+    reps = 20
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        torch.matmul(a, b, out=c)
+    e1.record()
+    torch.cuda.synchronize()
+    gemm_tf = 2 * m ** 3 * reps / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    del a, b, c
+    torch.cuda.empty_cache()
+    log(f"[bench] achievable: copy {copy_gbs:.0f} GB/s, bf16 GEMM {gemm_tf:.0f} TFLOP/s")
+    return {"hbm_copy_GBps": copy_gbs, "bf16_gemm_TFLOPs": gemm_tf,
+            "how": "torch copy over 4 rotating 256 MiB bf16 buffers (read + write bytes); 8192^3 bf16 "
+                   "torch.matmul (hipBLASLt), same run"}
+
+
 def cpu_baseline(s: Shape, sets, cos, sin, ws, seconds, torch):
     """The numpy oracle on whole batch rows of the same decode workload, until `seconds` pass."""
     import numpy as np
@@ -722,6 +764,13 @@ def main():
                                   "frac": idx_gbs / HBM_PEAK_GBS, "bytes_per_launch": s.bytes_indexer(),
                                   "avg_launch_us": kern["indexer_score"] * 1e3},
     }
+    try:
+        peaks = achievable_peaks(torch, device)
+        result["achievable"] = peaks
+        result["roofline"]["frac_of_achievable"] = fused_gbs / peaks["hbm_copy_GBps"]
+    except Exception as e:
+        peaks = None
+        result["achievable"] = {"error": repr(e)}
     if not args.no_mx:
         try:
             result["mxfp4_index_decode"] = run_mx_decode(args, torch, device)
@@ -730,6 +779,10 @@ def main():
     if not args.no_prefill:
         try:
             result["prefill"] = run_prefill(torch, device)
+            if peaks:
+                for key in ("indexer", "sparse"):
+                    result["prefill"][f"{key}_frac_of_gemm"] = (result["prefill"][f"{key}_TFLOPs"] /
+                                                                peaks["bf16_gemm_TFLOPs"])
         except Exception as e:  # report, do not hide: the decode line still prints
             result["prefill"] = {"error": repr(e)}
     if not args.no_fp8:
