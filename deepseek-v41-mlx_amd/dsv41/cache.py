@@ -19,9 +19,13 @@ stored as e4m3fn codes with one ue8m0 scale byte per 32 channels of each row (``
 fake_quant_fp8_ue8m0's formula in place of the reference's fp4 QAT at those two stores and
 dequantized in-kernel. The window ring stays in ``dtype``.
 
-All buffers are plain torch device tensors with the reference's attribute names, so callers
-that snapshot and restore them (generate.py:18-44) work unchanged. The attention kernels
-require ``dtype`` to equal the activation dtype.
+All buffers are plain torch device tensors with the reference's attribute names. The kernels
+update them in place, so a snapshot must copy: ``lc.win_kv[:]`` -- which in MLX pins the
+pre-step value (generate.py:18-44) -- is a view in torch. ``snapshot(cache)`` and
+``restore(cache, snap)`` are the torch counterparts of generate.py's ``_cache_snapshot`` /
+``_cache_restore``: they copy every buffer of every format, and restore writes back into the
+same tensors, so references to them (a captured HIP graph, a consumer's view) stay valid. The
+attention kernels require ``dtype`` to equal the activation dtype.
 """
 
 from __future__ import annotations
@@ -118,3 +122,35 @@ class ModelCache:
         self.layers = [LayerCache(bsz, args, i, self.max_seq_len, dtype, device, index_format, cache_format)
                        for i in range(args.n_layers)]
         self.engram_ids = None
+
+
+_BUFFERS = ("win_kv", "comp_kv", "index_k", "index_k4", "index_ks", "comp_kv8", "comp_ks", "index_k8", "index_k8s")
+
+
+def snapshot(cache: ModelCache):
+    """Copies of every cache buffer and the offset (generate.py:18-30 takes the same state)."""
+    layers = []
+    for lc in cache.layers:
+        bufs = {name: getattr(lc, name).clone() for name in _BUFFERS if getattr(lc, name) is not None}
+        cs = lc.comp_state
+        state = (cs.kv_state.clone(), cs.score_state.clone()) if cs is not None else None
+        layers.append((bufs, state))
+    eng = cache.engram_ids.clone() if cache.engram_ids is not None else None
+    return cache.offset, layers, eng
+
+
+def restore(cache: ModelCache, snap) -> None:
+    """Write a snapshot back (generate.py:33-44), into the same tensors."""
+    offset, layers, eng = snap
+    if len(layers) != len(cache.layers):
+        raise ValueError(f"snapshot of {len(layers)} layers for a cache of {len(cache.layers)}")
+    cache.offset = offset
+    for lc, (bufs, state) in zip(cache.layers, layers):
+        for name, t in bufs.items():
+            getattr(lc, name).copy_(t)
+        if state is not None:
+            lc.comp_state.kv_state.copy_(state[0])
+            lc.comp_state.score_state.copy_(state[1])
+    if eng is not None:
+        cache.engram_ids.copy_(eng)
+

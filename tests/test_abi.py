@@ -172,3 +172,48 @@ def test_rope_frequencies_match_oracle_restatement():
     from oracle import cpu_ref as R
     for args in [(64, 65536, 160000.0, 16.0, 32, 1), (16, 0, 10000.0, 4.0, 32, 1), (16, 64, 40000.0, 4.0, 32, 1)]:
         assert np.array_equal(yarn_inv_freqs(*args), R.yarn_freqs(*args))
+
+
+@pytest.mark.parametrize("index_format,cache_format", [("dense", "dense"), ("mxfp4", "dense"), ("dense", "fp8")])
+def test_cache_snapshot_restore(index_format, cache_format):
+    """snapshot() copies every buffer of every cache format (a torch slice would alias the
+    buffers the kernels update in place); restore() writes the copies back into the same tensors
+    and resets the offset, as generate.py:18-44 does for the reference."""
+    from common import C4_TOY, model_args
+    from dsv41.cache import ModelCache, restore, snapshot
+    a = model_args(C4_TOY)
+    cache = ModelCache(a, 2, 64, torch.float32, "cpu", index_format, cache_format)
+    g = torch.Generator().manual_seed(11)
+
+    def tensors():
+        out = []
+        for lc in cache.layers:
+            for name in ("win_kv", "comp_kv", "index_k", "index_k4", "index_ks", "comp_kv8", "comp_ks", "index_k8",
+                         "index_k8s"):
+                if getattr(lc, name) is not None:
+                    out.append(getattr(lc, name))
+            if lc.comp_state is not None:
+                out += [lc.comp_state.kv_state, lc.comp_state.score_state]
+        return out
+
+    def scramble():
+        for t in tensors():
+            if t.dtype == torch.uint8:
+                t.copy_(torch.randint(0, 256, t.shape, generator=g, dtype=torch.uint8))
+            else:
+                t.copy_(torch.randn(t.shape, generator=g))
+
+    scramble()
+    cache.offset = 7
+    want = [t.clone() for t in tensors()]
+    ptrs = [t.data_ptr() for t in tensors()]
+    snap = snapshot(cache)
+    scramble()
+    cache.offset = 9
+    assert not all(torch.equal(t, w) for t, w in zip(tensors(), want))
+    restore(cache, snap)
+    assert cache.offset == 7
+    assert [t.data_ptr() for t in tensors()] == ptrs
+    assert all(torch.equal(t, w) for t, w in zip(tensors(), want))
+    kinds = {t.dtype for t in tensors()}
+    assert (torch.uint8 in kinds) == (index_format != "dense" or cache_format != "dense")

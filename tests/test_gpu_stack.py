@@ -309,3 +309,37 @@ def test_stack_step_graph_replays(gpu):
         for l, (o, w) in enumerate(zip(outs, want)):
             assert torch.equal(o, w), (rep, l)
         assert torch.equal(step.plan[36].idx, want_idx), rep
+
+
+@pytest.mark.parametrize("cache_format", ["dense", "fp8"])
+def test_cache_snapshot_restore_replays_a_decode_step(gpu, cache_format):
+    """The torch counterpart of generate.py's snapshot / retry: after 39 prefill tokens, snapshot
+    the cache, run the decode token (it completes a group: owners write a latent and a key, every
+    layer writes its ring slot and the compressor state moves), restore, and run the same token
+    again: the same outputs, and the same cache afterwards."""
+    from dsv41.cache import restore, snapshot
+    from dsv41.model import AttentionStack
+    cfg = C4_TOY if cache_format == "dense" else dict(C4_TOY, index_head_dim=128, head_dim=512, rope_head_dim=64)
+    a = args(cfg)
+    st = AttentionStack(model_args(cfg), torch.bfloat16, gpu)
+    load_stack(st, R.make_params(a, SEED_BASE + 41, "bf16"))
+    rng = np.random.default_rng(SEED_BASE + 41)
+    b, T = 2, 40
+    h = torch.from_numpy(rng.standard_normal((b, T, a.dim)).astype(F32)).to(gpu).to(torch.bfloat16)
+    cache = st.make_cache(b, a.max_seq_len, cache_format=cache_format) if cache_format == "fp8" else \
+        st.make_cache(b, a.max_seq_len)
+    st(h[:, :T - 1], cache)
+    snap = snapshot(cache)
+    first = st(h[:, T - 1:], cache).clone()
+    after = snapshot(cache)
+    restore(cache, snap)
+    second = st(h[:, T - 1:], cache)
+    torch.cuda.synchronize()
+    assert torch.equal(first, second)
+    assert cache.offset == after[0]
+    for l, (lc, (bufs, state)) in enumerate(zip(cache.layers, after[1])):
+        for name, t in bufs.items():
+            assert torch.equal(getattr(lc, name), t), f"layer {l} {name}"
+        if state is not None:
+            assert torch.equal(lc.comp_state.kv_state, state[0]) and torch.equal(lc.comp_state.score_state,
+                                                                                 state[1]), f"layer {l} state"
