@@ -255,7 +255,8 @@ def run_mx_decode(args, torch, device):
     """The bs32 / 64K decode step with the index cache in MXFP4 (e2m1 codes + ue8m0 scales per
     32 channels, 68 bytes per key instead of 256): the packed form of the fp4 fake-quantized
     keys the indexer stores; the index query arrives in the same form from its prologue (as the
-    bf16 line's query arrives roped and quantized); scored with block-scaled fp4 MFMA.
+    bf16 line's query arrives roped and quantized); scored with block-scaled fp4 MFMA, the top-k
+    fused into the scoring as in the bf16 line.
     Everything else as the bf16 line (same shapes, 4 rotating input sets)."""
     from dsv41 import _abi
     from dsv41.indexer import weight_scale
@@ -280,6 +281,9 @@ def run_mx_decode(args, torch, device):
         d["out"] = torch.empty(s.B, 1, s.H, s.D, dtype=torch.bfloat16, device=device)
         d["ws"] = torch.empty(max(_abi.mla_workspace_bytes(s.B, 1, s.H, s.D, s.rows, torch.bfloat16), 1),
                               dtype=torch.uint8, device=device)
+        d["fidx"] = torch.empty(s.B, 1, s.K, dtype=torch.int32, device=device)
+        d["fws"] = torch.empty(max(_abi.indexer_topk_workspace_bytes(s.B, 1, s.Hi, s.Di, s.nb, s.K), 1),
+                               dtype=torch.uint8, device=device)
         sets.append(d)
     cos, sin = precompute_freqs_cis(s.rd, s.start + 1, 65536, 160000.0, 16.0, 32, 1, device=device)
     ws = weight_scale(s.Hi, s.Di, torch.bfloat16)
@@ -290,14 +294,19 @@ def run_mx_decode(args, torch, device):
     def f_topk(d):
         d["idx"] = _abi.topk_select(d["scores"], s.K, s.start, s.r, s.wp + 1)
 
-    def f_sparse(d):
-        _abi.sparse_mla(d["q"], d["win"], d["chunk"], d["comp"], s.nb, d["sink"], d["idx"], s.D ** -0.5, s.W,
+    def f_fused(d):
+        # the step's scoring + selection: the fused form over the MXFP4 query and keys
+        sel = _abi.indexer_topk_mxfp4((d["qc"], d["qs"]), d["w"], ws, d["kc"], d["ks"], s.nb, s.start, s.r, s.K,
+                                      s.wp + 1, out=d["fidx"], workspace=d["fws"])
+        assert sel is not None, "the bs32 decode shape is served by the fused form"
+
+    def f_sparse(d, key="idx"):
+        _abi.sparse_mla(d["q"], d["win"], d["chunk"], d["comp"], s.nb, d["sink"], d[key], s.D ** -0.5, s.W,
                         s.start, cos, sin, s.rd, out=d["out"], workspace=d["ws"])
 
     def full(d):
-        f_idx(d)
-        f_topk(d)
-        f_sparse(d)
+        f_fused(d)
+        f_sparse(d, "fidx")
 
     per = len(sets)
     reps = max(1, args.steps // per)
@@ -306,7 +315,8 @@ def run_mx_decode(args, torch, device):
         g_full.replay()
     step_ms = time_graph(g_full, reps, torch) / per
     kern, graphs = {}, [g_full]
-    for name, fn in (("indexer_score", f_idx), ("topk_select", f_topk), ("sparse_mla", f_sparse)):
+    for name, fn in (("indexer_topk", f_fused), ("indexer_score", f_idx), ("topk_select", f_topk),
+                     ("sparse_mla", f_sparse)):
         gr = graph_of(fn, sets, torch)
         graphs.append(gr)
         gr.replay()
@@ -314,7 +324,8 @@ def run_mx_decode(args, torch, device):
         log(f"[bench] mxfp4 {name} {kern[name] * 1e3:.2f} us")
     torch.cuda.synchronize()
     b_idx = s.B * (s.nb * (s.Di // 2 + s.Di // 32) + s.Hi * (s.Di // 2 + s.Di // 32) + s.Hi * 2 + s.nb * 4)
-    step_bytes = b_idx + s.bytes_topk() + s.bytes_sparse()
+    b_fused = b_idx - s.B * s.nb * 4 + s.B * s.K * 4     # codes, scales, q, w in; indices out
+    step_bytes = b_fused + s.bytes_sparse()
     log(f"[bench] MXFP4-index decode step {step_ms * 1e3:.2f} us")
     return {
         "workload": "bs32 / 64K decode step with an MXFP4 index cache (e2m1 codes + ue8m0 block scales, 68 B per "
@@ -323,6 +334,7 @@ def run_mx_decode(args, torch, device):
         "kernels_us": {k: v * 1e3 for k, v in kern.items()},
         "step_algorithmic_bytes": step_bytes,
         "hbm_GBps_step": step_bytes / (step_ms * 1e-3) / 1e9,
+        "indexer_topk_GBps": b_fused / (kern["indexer_topk"] * 1e-3) / 1e9,
         "indexer_bytes_per_launch": b_idx,
         "indexer_GBps": b_idx / (kern["indexer_score"] * 1e-3) / 1e9,
         "indexer_hbm_frac": b_idx / (kern["indexer_score"] * 1e-3) / 1e9 / HBM_PEAK_GBS,

@@ -398,15 +398,19 @@ template <int U> struct MxBatch {
 
 constexpr int kMxThreads = 512;  // 8 waves
 
-template <int HT>
+template <int HT, int TJ>
 __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
     const uint8_t* __restrict__ qcodes, const uint8_t* __restrict__ qscales, const bf16_t* __restrict__ w_raw,
     float w_scale,
     const uint8_t* __restrict__ kcodes, int64_t kc_bstride, const uint8_t* __restrict__ kscales, int64_t ks_bstride,
     const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int nb, int start_pos, int ratio,
-    int rows_per_wg) {
+    int rows_per_wg, int topk, uint32_t* __restrict__ ckey, int32_t* __restrict__ cpos) {
   constexpr int H = HT * 16;
   constexpr int DIM = 128;
+  // TJ > 0 (the fused top-k form): the range's scores collect in LDS and the workgroup keeps the
+  // best min(topk, rows) as (order key, position) in position order, as indexer_decode_kernel does
+  __shared__ float sc_lds[TJ > 0 ? TJ * kMxThreads : 1];
+  __shared__ __align__(16) uint8_t sel_raw[TJ > 0 ? sizeof(RegSelShared) : 16];
 
   const int qi = blockIdx.y;               // b * n + s
   const int b = qi / n, s = qi - (qi / n) * n;
@@ -416,9 +420,20 @@ __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
   const int r0 = blockIdx.x * rows_per_wg;
   const int r1 = min(r0 + rows_per_wg, nb);
   const int vis_end = max(r0, min(r1, lens));
-  float* out = scores + (int64_t)qi * nb;
-  for (int t = vis_end + tid; t < r1; t += kMxThreads) out[t] = -INFINITY;
-  if (vis_end <= r0) return;               // uniform: nothing visible in this row range
+  float* out = TJ ? nullptr : scores + (int64_t)qi * nb;
+  const int64_t cbase = ((int64_t)qi * gridDim.x + blockIdx.x) * topk;   // this range's list (TJ > 0)
+  if constexpr (TJ == 0) {
+    for (int t = vis_end + tid; t < r1; t += kMxThreads) out[t] = -INFINITY;
+  }
+  if (vis_end <= r0) {                     // uniform: nothing visible in this row range
+    if constexpr (TJ > 0) {                // all -inf: the lowest positions are the best
+      for (int t = tid; t < min(topk, r1 - r0); t += kMxThreads) {
+        ckey[cbase + t] = order_key(-INFINITY);
+        cpos[cbase + t] = r0 + t;
+      }
+    }
+    return;
+  }
 
   // lane (l16, g) of a tile loads row l16's 32-channel block g: 16 code bytes and its scale
   const uint8_t* kcb = kcodes + (int64_t)b * kc_bstride + g * 16;
@@ -454,7 +469,11 @@ __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
       }
       part = sum_rows4(part);
       const int row = t0 + 16 * u + l16;
-      if (g == 0 && row < vis_end) out[row] = kk.cf[u] ? part : -INFINITY;
+      if (g == 0 && row < vis_end) {
+        const float v = kk.cf[u] ? part : -INFINITY;
+        if constexpr (TJ > 0) sc_lds[row - r0] = v;
+        else out[row] = v;
+      }
     }
   };
   int t0 = r0 + 16 * U * wave;
@@ -477,15 +496,32 @@ __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wrow[ht * 16 + 4 * g + i]) * w_scale);
   }
-  if (t0 >= vis_end) return;
-  for (;;) {
+  bool more = t0 < vis_end;                // wave-uniform
+  while (more) {
 #pragma unroll
     for (int j = 0; j < NBUF; ++j) {
-      load(buf[(j + NBUF - 1) % NBUF], t0 + (NBUF - 1) * STRIDE);
-      compute(buf[j], t0);
-      t0 += STRIDE;
-      if (t0 >= vis_end) return;
+      if (more) {
+        load(buf[(j + NBUF - 1) % NBUF], t0 + (NBUF - 1) * STRIDE);
+        compute(buf[j], t0);
+        t0 += STRIDE;
+        more = t0 < vis_end;
+      }
     }
+  }
+  if constexpr (TJ > 0) {
+    __syncthreads();                       // every score of the range is in LDS
+    RegSelShared& sh = *reinterpret_cast<RegSelShared*>(sel_raw);
+    auto value = [&](int t) { return t < vis_end - r0 ? sc_lds[t] : -INFINITY; };
+    const int count = r1 - r0;
+    const int i0 = tid * TJ;
+    const int nvalid = min(max(count - i0, 0), TJ);
+    uint32_t key[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) key[j] = j < nvalid ? order_key(value(i0 + j)) : 0u;
+    select_top<TJ, kMxThreads>(key, nvalid, min(topk, count), sh, [&](uint32_t rank, int j) {
+      ckey[cbase + rank] = order_key(value(i0 + j));             // re-read: j is a run-time index
+      cpos[cbase + rank] = r0 + i0 + j;
+    });
   }
 }
 
@@ -831,9 +867,9 @@ extern "C" int dsv41_indexer_score_mxfp4(const uint8_t* q_codes, const uint8_t* 
   const dim3 grid = idx_grid((int64_t)nb * bsz * n, nb, bsz * n, &rows_per_wg);
 #define DSV41_IDXMX_CASE(HT_)                                                                                 \
   if (heads == HT_ * 16) {                                                                                    \
-    hipLaunchKernelGGL((indexer_score_mx_kernel<HT_>), grid, dim3(kMxThreads), 0, stream, q_codes, q_scales, \
+    hipLaunchKernelGGL((indexer_score_mx_kernel<HT_, 0>), grid, dim3(kMxThreads), 0, stream, q_codes, q_scales, \
                        (const bf16_t*)w_raw, w_scale, k_codes, kc_bstride, k_scales, ks_bstride, candidates,  \
-                       scores, n, nb, start_pos, ratio, rows_per_wg);                                        \
+                       scores, n, nb, start_pos, ratio, rows_per_wg, 0, nullptr, nullptr);                    \
     return check_launch(what);                                                                                \
   }
   DSV41_IDXMX_CASE(4)   // 64 heads
@@ -937,6 +973,53 @@ extern "C" int dsv41_indexer_topk_fp8(const void* q, const void* w_raw, float w_
   DSV41_FUSED8_CASE(1, 1) DSV41_FUSED8_CASE(1, 2) DSV41_FUSED8_CASE(1, 4) DSV41_FUSED8_CASE(1, 8)
   return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
 #undef DSV41_FUSED8_CASE
+  const int rc = check_launch(what);
+  if (rc) return rc;
+  return topk_merge_launch(what, ckey, cpos, out, (int64_t)bsz * n, n, nb, k, (int)grid.x, rows_per_wg, start_pos,
+                           ratio, offset, stream);
+}
+
+extern "C" int dsv41_indexer_topk_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
+                                        float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                                        const uint8_t* k_scales, int64_t ks_bstride, const uint8_t* candidates,
+                                        int32_t* out, int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
+                                        int32_t start_pos, int32_t ratio, int32_t topk, int32_t offset,
+                                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const char* what = "dsv41_indexer_topk_mxfp4";
+  DSV41_REQUIRE(q_codes && q_scales && w_raw && k_codes && k_scales && out, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(bsz >= 0 && n > 0 && heads > 0 && nb >= 0 && start_pos >= 0 && ratio > 0 && topk >= 0, DSV41_E_ARG,
+                "%s: bad sizes", what);
+  DSV41_REQUIRE(dim == 128, DSV41_E_SHAPE, "%s: MXFP4 index keys support dim 128, got %d", what, dim);
+  DSV41_REQUIRE(kc_bstride >= (int64_t)nb * (dim / 2) && ks_bstride >= (int64_t)nb * (dim / 32), DSV41_E_ARG,
+                "%s: batch strides too small", what);
+  DSV41_REQUIRE(aligned16(q_codes) && aligned16(k_codes) && (reinterpret_cast<uintptr_t>(k_scales) & 3u) == 0,
+                DSV41_E_ARG, "%s: q_codes and k_codes must be 16-byte aligned, k_scales 4-byte aligned", what);
+  DSV41_REQUIRE(kc_bstride % 16 == 0 && ks_bstride % 4 == 0, DSV41_E_ARG,
+                "%s: kc_bstride must be a multiple of 16 bytes, ks_bstride of 4", what);
+  const int k = topk < nb ? topk : nb;
+  if ((int64_t)bsz * n == 0 || nb == 0 || k == 0) return 0;
+  int rows_per_wg = 0, tj = 0;
+  dim3 grid;
+  DSV41_REQUIRE(idx_topk_plan(bsz, n, heads, dim, nb, k, candidates != nullptr, &rows_per_wg, &grid, &tj),
+                DSV41_E_SHAPE, "%s: shape not served by the fused form (dsv41_indexer_topk_workspace_bytes is 0)",
+                what);
+  const size_t need = idx_topk_ws((int64_t)bsz * n, grid.x, k);
+  DSV41_REQUIRE(workspace && workspace_bytes >= need, DSV41_E_WORKSPACE, "%s: workspace of %zu bytes needed", what,
+                need);
+  DSV41_REQUIRE(aligned16(workspace), DSV41_E_ARG, "%s: workspace must be 16-byte aligned", what);
+  uint32_t* ckey = reinterpret_cast<uint32_t*>(workspace);
+  int32_t* cpos = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(workspace) + need / 2);
+#define DSV41_FUSEDMX_CASE(HT_, TJ_)                                                                           \
+  if (heads == HT_ * 16 && tj == TJ_) {                                                                        \
+    hipLaunchKernelGGL((indexer_score_mx_kernel<HT_, TJ_>), grid, dim3(kMxThreads), 0, stream, q_codes,        \
+                       q_scales, (const bf16_t*)w_raw, w_scale, k_codes, kc_bstride, k_scales, ks_bstride,      \
+                       candidates, nullptr, n, nb, start_pos, ratio, rows_per_wg, k, ckey, cpos);             \
+  } else
+  DSV41_FUSEDMX_CASE(4, 1) DSV41_FUSEDMX_CASE(4, 2) DSV41_FUSEDMX_CASE(4, 4) DSV41_FUSEDMX_CASE(4, 8)
+  DSV41_FUSEDMX_CASE(2, 1) DSV41_FUSEDMX_CASE(2, 2) DSV41_FUSEDMX_CASE(2, 4) DSV41_FUSEDMX_CASE(2, 8)
+  DSV41_FUSEDMX_CASE(1, 1) DSV41_FUSEDMX_CASE(1, 2) DSV41_FUSEDMX_CASE(1, 4) DSV41_FUSEDMX_CASE(1, 8)
+  return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
+#undef DSV41_FUSEDMX_CASE
   const int rc = check_launch(what);
   if (rc) return rc;
   return topk_merge_launch(what, ckey, cpos, out, (int64_t)bsz * n, n, nb, k, (int)grid.x, rows_per_wg, start_pos,

@@ -66,6 +66,8 @@ _SIGNATURES = {
                            _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_indexer_topk_fp8": [_c_p, _c_p, _f32, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32, _i32, _i32, _i32,
                                _i32, _i32, _i32, _i32, _i32, _c_p, _sz, _c_p],
+    "dsv41_indexer_topk_mxfp4": [_c_p, _c_p, _c_p, _f32, _c_p, _i64, _c_p, _i64, _c_p, _c_p, _i32, _i32, _i32,
+                                 _i32, _i32, _i32, _i32, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_topk_select_ws": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_candidate_blocks": [_c_p, _c_p, _i64, _i32, _i32, _i32, _i32, _c_p, _i32, _i32, _c_p],
     "dsv41_sparse_mla_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32],
@@ -571,6 +573,42 @@ def indexer_score_mxfp4(q_mx, w_raw, w_scale, k_codes, k_scales, nb, start_pos, 
     _call(name, _ptr(q_codes), _ptr(q_scales), _ptr(w_raw), float(w_scale), _ptr(k_codes), row_stride(k_codes, name),
           _ptr(k_scales), row_stride(k_scales, name), _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio,
           _stream(w_raw))
+    return out
+
+
+def indexer_topk_mxfp4(q_mx, w_raw, w_scale, k_codes, k_scales, nb, start_pos, ratio, topk, offset, candidates=None,
+                       out=None, workspace=None):
+    """indexer_topk over MXFP4 query and keys (the layouts of indexer_score_mxfp4): int32
+    [b, n, min(topk, nb)], bit-equal to topk_select(indexer_score_mxfp4(...)). Returns None when
+    the fused form does not serve the shape."""
+    name = "dsv41_indexer_topk_mxfp4"
+    q_codes, q_scales = q_mx
+    _gpu(name, q_codes, q_scales, w_raw, k_codes, k_scales, candidates, out, workspace)
+    _contig(name, q_codes, q_scales, w_raw, candidates)
+    b, n, h, d2 = q_codes.shape
+    d = d2 * 2
+    if q_codes.dtype != torch.uint8 or d != 128 or q_scales.shape != (b, n, h, d // 32) or q_scales.dtype != torch.uint8:
+        raise ValueError(f"{name}: query must be uint8 codes [b, n, h, 64] with scales [b, n, h, 4]")
+    if w_raw.shape != (b, n, h) or w_raw.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: w_raw must be bf16 [{b}, {n}, {h}]")
+    if k_codes.dtype != torch.uint8 or k_codes.shape[0] < b or k_codes.shape[2] != d // 2 or k_codes.shape[1] < nb:
+        raise ValueError(f"{name}: key codes {tuple(k_codes.shape)} {k_codes.dtype} do not match")
+    if k_scales.dtype != torch.uint8 or k_scales.shape[0] < b or k_scales.shape[2] != d // 32 or k_scales.shape[1] < nb:
+        raise ValueError(f"{name}: key scales {tuple(k_scales.shape)} do not match")
+    if candidates is not None and (candidates.shape != (b, n, nb) or candidates.dtype not in (torch.uint8, torch.bool)):
+        raise ValueError(f"{name}: candidates must be bool/uint8 [{b}, {n}, {nb}]")
+    ws_bytes = indexer_topk_workspace_bytes(b, n, h, d, nb, topk, candidates is not None)
+    if ws_bytes == 0:
+        return None
+    k = min(topk, nb)
+    out = torch.empty(b, n, k, dtype=torch.int32, device=w_raw.device) if out is None else out
+    if out.dtype != torch.int32 or tuple(out.shape) != (b, n, k) or not out.is_contiguous():
+        raise ValueError(f"{name}: out must be contiguous int32 [{b}, {n}, {k}]")
+    ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else _workspace(ws_bytes, w_raw.device)
+    cand = candidates.view(torch.uint8) if candidates is not None else None
+    _call(name, _ptr(q_codes), _ptr(q_scales), _ptr(w_raw), float(w_scale), _ptr(k_codes), row_stride(k_codes, name),
+          _ptr(k_scales), row_stride(k_scales, name), _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, topk,
+          offset, _ptr(ws), ws_bytes, _stream(w_raw))
     return out
 
 

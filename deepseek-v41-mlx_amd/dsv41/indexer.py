@@ -13,7 +13,7 @@ source, the candidate mask applied in the same pass. The candidate source publis
 block mask (``select_candidate_blocks``); the top-k kernel returns the ``index_topk`` best
 positions per query in ascending order, offset into the attention's unified index space, -1
 past the visible range. Decode queries of index sources other than the candidate source, on
-bf16 or fp8 keys of shapes it serves, take the fused form (dsv41_indexer_topk(_fp8)): the scoring kernel
+keys of shapes it serves, take the fused form (dsv41_indexer_topk(_fp8, _mxfp4)): the scoring kernel
 keeps each row range's best index_topk and a merge selects from those lists -- the same
 selection, without writing the scores.
 """
@@ -114,8 +114,14 @@ class Indexer(torch.nn.Module):
             if fakequant.DISABLE:
                 raise ValueError("an MXFP4 index cache holds fp4 fake-quantized keys; QAT is disabled")
             q_mx = _abi.index_q_prep_mxfp4(q, cos, sin, rd, start_pos)
-            scores = _abi.indexer_score_mxfp4(q_mx, w_raw, w_scale, index_k.codes, index_k.scales,
-                                              index_k.codes.shape[1], start_pos, self.ratio, cand)
+            nb = index_k.codes.shape[1]
+            if not self.is_candidate_source:
+                idx = _abi.indexer_topk_mxfp4(q_mx, w_raw, w_scale, index_k.codes, index_k.scales, nb, start_pos,
+                                              self.ratio, self.index_topk, offset, cand)
+                if idx is not None:
+                    return idx
+            scores = _abi.indexer_score_mxfp4(q_mx, w_raw, w_scale, index_k.codes, index_k.scales, nb, start_pos,
+                                              self.ratio, cand)
         elif getattr(index_k, "kind", None) == "fp8":
             if fakequant.DISABLE:
                 q = _abi.rope_tail(q, rd, cos, sin, start_pos, 1)

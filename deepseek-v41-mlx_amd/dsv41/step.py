@@ -90,9 +90,9 @@ class StackDecodeStep:
     and ``w_scale``; kv sources add ``latent`` [b,1,D] (pre-rope); key owners add ``k_raw``
     [b,1,Di] and ``k_norm`` [Di]. Caches may be dense, carry MXFP4 index keys, or be the fp8
     variant (cache_format "fp8": fp8 compressed KV and index keys); each layer takes the kernels
-    that read and write its owners' format. On dense bf16 or fp8 keys, index sources other than
-    the candidate source score and select in the fused form (dsv41_indexer_topk(_fp8)) where it
-    serves the shape; the candidate source writes its scores for the block mask (kept in
+    that read and write its owners' format. On every key format, index sources other than the
+    candidate source score and select in the fused form (dsv41_indexer_topk(_fp8, _mxfp4))
+    where it serves the shape; the candidate source writes its scores for the block mask (kept in
     ``candidates``).
     Outputs (``out`` per layer) and scratch are allocated once, so a step can be captured in
     a HIP graph.
@@ -184,6 +184,10 @@ class StackDecodeStep:
                     if p.fused_idx is not None and kind is None:
                         sel = _abi.indexer_topk(x["index_q"], x["w_raw"], x["w_scale"], keys, sp, p.ratio,
                                                 a.index_topk, self.offset, c, out=p.fused_idx, workspace=self.fused_ws)
+                    elif p.fused_idx is not None and kind == "mxfp4":
+                        sel = _abi.indexer_topk_mxfp4(x["index_q_mx"], x["w_raw"], x["w_scale"], keys.codes,
+                                                      keys.scales, nb, sp, p.ratio, a.index_topk, self.offset, c,
+                                                      out=p.fused_idx, workspace=self.fused_ws)
                     elif p.fused_idx is not None and kind == "fp8":
                         sel = _abi.indexer_topk_fp8(x["index_q"], x["w_raw"], x["w_scale"], keys.codes, keys.scales,
                                                     1, nb, sp, p.ratio, a.index_topk, self.offset, c,

@@ -253,6 +253,16 @@ int dsv41_indexer_topk_fp8(const void* q, const void* w_raw, float w_scale, cons
                            int32_t dim, int32_t nb, int32_t start_pos, int32_t ratio, int32_t topk,
                            int32_t offset, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* dsv41_indexer_topk over MXFP4 query and keys (the layouts of dsv41_indexer_score_mxfp4):
+ * bit-equal to dsv41_indexer_score_mxfp4 followed by dsv41_topk_select. Served shapes and the
+ * workspace are dsv41_indexer_topk's (same size query). */
+int dsv41_indexer_topk_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
+                             float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                             const uint8_t* k_scales, int64_t ks_bstride, const uint8_t* candidates,
+                             int32_t* out, int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
+                             int32_t start_pos, int32_t ratio, int32_t topk, int32_t offset,
+                             void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Top-k selection, deepseek_v41_mlx/indexer.py:140-144: per row of scores [bsz*n, nb],
  * the k = min(topk, nb) best positions (ties -> lowest position; -0.0 == +0.0), sorted
  * ascending, written as idx + offset when idx < lens else -1, lens = (start_pos+s+1)/ratio,

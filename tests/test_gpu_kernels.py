@@ -423,6 +423,28 @@ def test_indexer_topk_fp8_equals_two_calls(gpu, b, n, h, nb, topk, start, rb, us
     assert torch.equal(fused, _abi.topk_select(scores, topk, start, 4, 129))
 
 
+@pytest.mark.parametrize("b,n,h,nb,topk,start,use_cand", [
+    (32, 1, 64, 16384, 512, 65535, False),   # bs32 decode over an MXFP4 index cache
+    (8, 4, 16, 16384, 512, 20000, False),    # causal rows, ranges past visibility
+    (32, 1, 32, 16384, 512, 65535, True),    # candidate-masked consumer
+    (2, 1, 64, 256, 64, 1024, False),        # one range
+])
+def test_indexer_topk_mxfp4_equals_two_calls(gpu, b, n, h, nb, topk, start, use_cand):
+    """The fused form over MXFP4 query and keys selects exactly what indexer_score_mxfp4 +
+    topk_select select."""
+    from dsv41 import _abi
+    g = torch.Generator(gpu).manual_seed(SEED_BASE + 48)
+    rb = lambda lo, hi, *s: torch.randint(lo, hi, s, generator=g, device=gpu, dtype=torch.int32).to(torch.uint8)  # noqa: E731
+    q_mx = (rb(0, 256, b, n, h, 64), rb(120, 132, b, n, h, 4))
+    kc, ks = rb(0, 256, b, nb, 64), rb(120, 132, b, nb, 4)
+    w = torch.randn(b, n, h, generator=g, device=gpu).bfloat16()
+    cand = (torch.rand(b, n, nb, generator=g, device=gpu) < 0.7) if use_cand else None
+    fused = _abi.indexer_topk_mxfp4(q_mx, w, 0.01, kc, ks, nb, start, 4, topk, 129, cand)
+    assert fused is not None
+    scores = _abi.indexer_score_mxfp4(q_mx, w, 0.01, kc, ks, nb, start, 4, cand)
+    assert torch.equal(fused, _abi.topk_select(scores, topk, start, 4, 129))
+
+
 def test_indexer_topk_shared_workspace(gpu):
     """One workspace through a sequence of fused calls of different shapes (query counts, row
     ranges, k, candidate masks, ranges past visibility): every call equals the two-call form."""

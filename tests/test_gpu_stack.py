@@ -45,7 +45,7 @@ def _record_decode(stack, h, cache):
     orig = {n: getattr(_abi, n) for n in ("sparse_mla", "indexer_score", "comp_write", "index_key_publish",
                                           "indexer_score_mxfp4", "index_key_publish_mxfp4", "sparse_mla_fp8",
                                           "indexer_score_fp8", "comp_write_fp8", "index_key_publish_fp8",
-                                          "indexer_topk", "indexer_topk_fp8")}
+                                          "indexer_topk", "indexer_topk_fp8", "indexer_topk_mxfp4")}
 
     def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, *a, **k):
         r = recs[layer[0]]
@@ -70,6 +70,10 @@ def _record_decode(stack, h, cache):
     def indexer_topk(q, w_raw, w_scale, *a, **k):
         recs[layer[0]].update(index_q=q.clone(), w_raw=w_raw.clone(), w_scale=w_scale)
         return orig["indexer_topk"](q, w_raw, w_scale, *a, **k)
+
+    def indexer_topk_mxfp4(q_mx, w_raw, w_scale, *a, **k):
+        recs[layer[0]].update(index_q_mx=tuple(t.clone() for t in q_mx), w_raw=w_raw.clone(), w_scale=w_scale)
+        return orig["indexer_topk_mxfp4"](q_mx, w_raw, w_scale, *a, **k)
 
     def indexer_topk_fp8(q, w_raw, w_scale, *a, **k):
         recs[layer[0]].update(index_q=q.clone(), w_raw=w_raw.clone(), w_scale=w_scale)
@@ -108,7 +112,7 @@ def _record_decode(stack, h, cache):
                  ("index_key_publish_mxfp4", index_key_publish_mxfp4), ("sparse_mla_fp8", sparse_mla_fp8),
                  ("indexer_score_fp8", indexer_score_fp8), ("comp_write_fp8", comp_write_fp8),
                  ("index_key_publish_fp8", index_key_publish_fp8), ("indexer_topk", indexer_topk),
-                 ("indexer_topk_fp8", indexer_topk_fp8)):
+                 ("indexer_topk_fp8", indexer_topk_fp8), ("indexer_topk_mxfp4", indexer_topk_mxfp4)):
         setattr(_abi, n, f)
     try:
         stack(h, cache)
