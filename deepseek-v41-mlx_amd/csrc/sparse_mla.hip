@@ -686,7 +686,7 @@ static MlaPlan plan_bf16(int64_t units, int heads, int list_max, int dim) {
   p.wide = false;
   p.hgroups = hg32;
   const int64_t wgs = units * p.hgroups;
-  const int64_t target = dim <= 512 && (wgs >= 128 || lm >= 1024) ? 512 : 256;
+  const int64_t target = dim <= 512 && wgs >= 128 ? 512 : 256;
   int want = wgs < target ? (int)((target + wgs - 1) / wgs) : 1;
   const int cap = (lm + kStepRows - 1) / kStepRows;
   if (want > cap) want = cap;
