@@ -381,6 +381,8 @@ def test_indexer_score_mxfp4(gpu, b, n, h, nb, start, use_cand):
     (64, 1, 64, 16384, 512, 65535, False),   # 4 ranges of 4096
     (32, 1, 32, 16384, 512, 65535, True),    # candidate-masked consumer, 32 index heads
     (8, 4, 16, 16384, 512, 20000, False),    # causal rows: ranges past visibility list -inf entries
+    (16, 4, 64, 16384, 512, 40000, True),    # 4 queries per row and a candidate mask: ranges of 4096
+    (3, 9, 32, 8000, 256, 30000, True),      # 9 queries per row (served with a mask), a partial last range
 ])
 def test_indexer_topk_fused_equals_two_calls(gpu, b, n, h, nb, topk, start, use_cand):
     """The fused decode form (per-range best-k lists, then a merge) returns exactly the top-k of
@@ -428,6 +430,7 @@ def test_indexer_topk_fp8_equals_two_calls(gpu, b, n, h, nb, topk, start, rb, us
     (8, 4, 16, 16384, 512, 20000, False),    # causal rows, ranges past visibility
     (32, 1, 32, 16384, 512, 65535, True),    # candidate-masked consumer
     (2, 1, 64, 256, 64, 1024, False),        # one range
+    (16, 4, 64, 16384, 512, 40000, True),    # 4 queries per row and a candidate mask
 ])
 def test_indexer_topk_mxfp4_equals_two_calls(gpu, b, n, h, nb, topk, start, use_cand):
     """The fused form over MXFP4 query and keys selects exactly what indexer_score_mxfp4 +
