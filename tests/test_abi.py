@@ -104,6 +104,19 @@ def test_contract_violations_are_reported_by_the_library():
     assert rc == -4
     rc = lib.dsv41_indexer_topk(*args, 48, 128, 16384, 65535, 4, 512, 129, fake, need, None)
     assert rc == -3 and b"fused" in lib.dsv41_last_error_string()
+    # the fp8 and MXFP4 fused entries check the same way (fp8: byte strides of codes and scales)
+    a8 = (fake, fake, ctypes.c_float(0.01), fake, 16384 * 128, fake, 16384 * 4, 1, None, fake, 32, 1)
+    rc = lib.dsv41_indexer_topk_fp8(*a8, 64, 128, 16384, 65535, 4, 512, 129, None, 0, None)
+    assert rc == -4 and b"workspace" in lib.dsv41_last_error_string()
+    rc = lib.dsv41_indexer_topk_fp8(*a8, 48, 128, 16384, 65535, 4, 512, 129, fake, need, None)
+    assert rc == -3
+    rc = lib.dsv41_indexer_topk_fp8(*a8[:7], 2, *a8[8:], 64, 128, 16384, 65535, 4, 512, 129, fake, need, None)
+    assert rc == -1 and b"row block" in lib.dsv41_last_error_string()
+    amx = (fake, fake, fake, ctypes.c_float(0.01), fake, 16384 * 64, fake, 16384 * 4, None, fake, 32, 1)
+    rc = lib.dsv41_indexer_topk_mxfp4(*amx, 64, 128, 16384, 65535, 4, 512, 129, fake, need - 1, None)
+    assert rc == -4
+    rc = lib.dsv41_indexer_topk_mxfp4(*amx, 64, 64, 16384, 65535, 4, 512, 129, fake, need, None)
+    assert rc == -3 and b"dim 128" in lib.dsv41_last_error_string()
 
 
 def test_topk_workspace_sizes():
