@@ -1,6 +1,6 @@
 """Benchmark of the DeepSeek-V4.1 sparse-attention hot path on one MI355X.
 
-Workload (BASELINE metric "sparse-MLA decode tokens/s + HBM GB/s (% peak), bs32 64K ctx;
+Workload (the headline metric, "sparse-MLA decode tokens/s + HBM GB/s (% peak), bs32 64K ctx;
 prefill TFLOP/s"): one decode step of one compressing attention layer at batch 32 and
 65,536 tokens of context, i.e. 16,384 compressed entries per sequence (ratio 4), top-512,
 64 heads x 512 (64-channel rope tail), indexer 64 heads x 128, window 128, bf16. A step is
