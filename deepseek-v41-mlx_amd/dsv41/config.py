@@ -1,179 +1,188 @@
-"""Model configuration for the attention path (the ModelArgs of deepseek_v41_mlx/config.py).
+"""Configuration of the attention path: the fields of the reference's ``ModelArgs`` that
+this package reads (deepseek_v41_mlx/config.py:28-106), loaded from either release layout.
 
-Same field names, defaults and the two JSON layouts of the release (the flat inference
-``config.json`` and the HF hub ``config.json`` with ``text_config``), config.py:28-194, so a
-reference config loads unchanged. Only the attention fields are read by this package; the
-MoE / engram / hyper-connection fields are kept so ``from_dict`` accepts every release file.
+Design:
+
+* ``_KEYS`` is one table, ``(attribute, JSON names tried in order, default)``. The first
+  JSON name that is present and not null wins. The same table serves keyword construction,
+  the flat inference ``config.json`` and the HF hub file (whose ``text_config`` is folded
+  over its top level first, config.py:137-140). YaRN settings may also arrive inside a
+  ``rope_scaling`` object (config.py:142, 179-183); ``_ROPE_SCALING`` names them.
+* Only the attention path's fields are typed attributes. Every other keyword or JSON key
+  of a release config (MoE, engram, hyper-connection, vision sizes ...) is kept verbatim in
+  ``extra`` and reachable as an attribute, so model code that reads e.g. ``args.hc_mult``
+  still runs, but nothing here interprets it.
+* The sharing topology is resolved by one walk down the layer stack
+  (``_resolve_sources``): a compressing layer reads the latest KV source at or above it,
+  whose compress ratio must equal its own, and the latest index source at or above it.
+  This is the rule of config.py:108-133, evaluated for all layers at once; lookups raise
+  ``ValueError`` for a layer the walk could not resolve.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+_TUPLE = tuple
+
+# attribute, JSON names (flat layout name last unless they coincide), default
+_KEYS = (
+    ("dim", ("hidden_size", "dim"), 5120),
+    ("n_layers", ("num_hidden_layers", "n_layers"), 40),
+    ("n_heads", ("num_attention_heads", "n_heads"), 64),
+    ("head_dim", ("head_dim",), 512),
+    ("rope_head_dim", ("qk_rope_head_dim", "rope_head_dim"), 64),
+    ("q_lora_rank", ("q_lora_rank",), 1280),
+    ("o_lora_rank", ("o_lora_rank",), 1024),
+    ("o_groups", ("o_groups",), 8),
+    ("window_size", ("sliding_window", "window_size"), 128),
+    ("norm_eps", ("rms_norm_eps", "norm_eps"), 1e-20),
+    ("compress_ratios", ("compress_ratios",), ()),
+    ("kv_source_layers", ("kv_source_layer_ids", "kv_source_layers"), ()),
+    ("index_source_layers", ("index_source_layer_ids", "index_source_layers"), ()),
+    ("compress_rope_theta", ("compress_rope_theta",), 160000.0),
+    ("candidate_source_layer", ("candidate_source_layer_id", "candidate_source_layer"), -1),
+    ("candidate_topk_blocks", ("candidate_topk_blocks",), 0),
+    ("candidate_block_size", ("candidate_block_size",), 0),
+    ("original_seq_len", ("original_seq_len",), 65536),
+    ("rope_theta", ("rope_theta",), 10000.0),
+    ("rope_factor", ("rope_factor",), 16.0),
+    ("beta_fast", ("beta_fast",), 32),
+    ("beta_slow", ("beta_slow",), 1),
+    ("max_seq_len", ("max_position_embeddings", "max_seq_len"), 1048576),
+    ("index_n_heads", ("index_n_heads",), 32),
+    ("index_head_dim", ("index_head_dim",), 128),
+    ("index_topk", ("index_topk",), 512),
+)
+
+# attribute -> its name inside a ``rope_scaling`` object, which takes precedence
+_ROPE_SCALING = {"original_seq_len": "original_max_position_embeddings",
+                 "rope_factor": "factor", "beta_fast": "beta_fast", "beta_slow": "beta_slow"}
+
+_SEQUENCE_FIELDS = {"compress_ratios", "kv_source_layers", "index_source_layers"}
+_FIELDS = {name for name, _, _ in _KEYS}
 
 
-def _get(d: dict, *names, default=None):
+def _first(d: dict, names):
     for n in names:
-        if n in d and d[n] is not None:
-            return d[n]
-    return default
+        v = d.get(n)
+        if v is not None:
+            return v
+    return None
 
 
-@dataclass
 class ModelArgs:
-    vocab_size: int = 129280
-    dim: int = 5120
-    n_layers: int = 40
-    moe_inter_dim: int = 2304
+    """Attention-path configuration; attribute names and defaults are the reference's."""
 
-    # attention (MLA): one shared head_dim KV vector per position (rope on its tail)
-    n_heads: int = 64
-    head_dim: int = 512
-    rope_head_dim: int = 64
-    q_lora_rank: int = 1280
-    o_lora_rank: int = 1024
-    o_groups: int = 8
-    window_size: int = 128
-    norm_eps: float = 1e-20
+    def __init__(self, **kw):
+        extra = {k: kw.pop(k) for k in list(kw) if k not in _FIELDS}
+        for name, _, default in _KEYS:
+            v = kw.get(name, default)
+            if name in _SEQUENCE_FIELDS:
+                v = _TUPLE(int(x) for x in (v or ()))
+            setattr(self, name, v)
+        # not typed attributes of this path; kept so a release config round-trips
+        self.extra = extra
+        self._sources = None
 
-    # MoE (unused by the attention path)
-    n_routed_experts: int = 384
-    n_shared_experts: int = 1
-    n_activated_experts: int = 6
-    score_func: str = "sqrtsoftplus"
-    gate_temp: float = 1.0
-    norm_topk_prob: bool = True
-    route_scale: float = 1.5
-    swiglu_limit: float = 10.0
+    def __getattr__(self, name):
+        # only reached for names that are not regular attributes
+        extra = self.__dict__.get("extra", {})
+        if name in extra:
+            return extra[name]
+        raise AttributeError(f"ModelArgs has no field {name!r}")
 
-    # KV compression / cross-layer sharing
-    compress_ratios: tuple = ()
-    kv_source_layers: tuple = ()
-    index_source_layers: tuple = ()
-    compress_rope_theta: float = 160000.0
+    def __repr__(self) -> str:
+        body = ", ".join(f"{n}={getattr(self, n)!r}" for n, _, _ in _KEYS)
+        return f"ModelArgs({body})"
 
-    # two-level top-k candidates; -1 disables
-    candidate_source_layer: int = -1
-    candidate_topk_blocks: int = 0
-    candidate_block_size: int = 0
+    def __eq__(self, other) -> bool:
+        return (isinstance(other, ModelArgs)
+                and all(getattr(self, n) == getattr(other, n) for n in _FIELDS)
+                and self.extra == other.extra)
 
-    # rope / YaRN
-    original_seq_len: int = 65536
-    rope_theta: float = 10000.0
-    rope_factor: float = 16.0
-    beta_fast: int = 32
-    beta_slow: int = 1
-    max_seq_len: int = 1048576
-
-    # indexer
-    index_n_heads: int = 32
-    index_head_dim: int = 128
-    index_topk: int = 512
-
-    # hyper-connections, engram, side paths (unused by the attention path)
-    hc_mult: int = 4
-    hc_sinkhorn_iters: int = 20
-    hc_eps: float = 1e-6
-    engram_layer_ids: tuple = ()
-    engram_num_embeddings: tuple = ()
-    engram_max_ngram_size: int = 4
-    engram_vocab_size: int = 0
-    engram_n_heads: int = 0
-    engram_head_dim: int = 0
-    engram_pad_id: int = 2
-    engram_compressed_vocab_size: int = 0
-    n_mtp_layers: int = 0
-    dspark_target_layer_ids: tuple = ()
-    vision_n_layers: int = 0
+    # ---------------------------------------------------------------- derived sizes
 
     @property
     def nope_head_dim(self) -> int:
         return self.head_dim - self.rope_head_dim
 
     def compress_ratio(self, layer_id: int) -> int:
-        """0 = window only, 1 = a latent per token, r > 1 = r tokens pooled (config.py:108-111)."""
-        if layer_id < len(self.compress_ratios):
-            return int(self.compress_ratios[layer_id])
-        return 0
+        """0: window only; 1: one latent per token; r > 1: r tokens pooled per latent.
+        Layers past the end of ``compress_ratios`` are window only (config.py:108-111)."""
+        r = self.compress_ratios
+        return int(r[layer_id]) if 0 <= layer_id < len(r) else 0
+
+    # ---------------------------------------------------------------- sharing topology
+
+    def _resolve_sources(self):
+        """Per layer: (kv source or an error message, index source or an error message)."""
+        if self._sources is not None:
+            return self._sources
+        kv_owners = set(self.kv_source_layers)
+        index_owners = set(self.index_source_layers)
+        depth = max([self.n_layers, len(self.compress_ratios), *(s + 1 for s in kv_owners),
+                     *(s + 1 for s in index_owners)])
+        latest_kv = latest_index = None
+        table = []
+        for layer in range(depth):
+            if layer in kv_owners:
+                latest_kv = layer
+            if layer in index_owners:
+                latest_index = layer
+            if latest_kv is None:
+                kv = f"layer {layer} compresses but no kv source layer precedes it"
+            elif self.compress_ratio(latest_kv) != self.compress_ratio(layer):
+                kv = (f"layer {layer} has compress ratio {self.compress_ratio(layer)}, but its kv "
+                      f"source {latest_kv} has ratio {self.compress_ratio(latest_kv)}")
+            else:
+                kv = latest_kv
+            idx = latest_index if latest_index is not None else (
+                f"no index source layer precedes layer {layer}")
+            table.append((kv, idx))
+        self._sources = table
+        return table
+
+    def _lookup(self, layer_id: int, which: int) -> int:
+        table = self._resolve_sources()
+        if not 0 <= layer_id < len(table):
+            raise ValueError(f"layer {layer_id} is outside the configured stack")
+        found = table[layer_id][which]
+        if isinstance(found, str):
+            raise ValueError(found)
+        return found
 
     def kv_source_for(self, layer_id: int) -> int:
-        """The most recent kv source at or above ``layer_id``; its ratio must match (config.py:113-127)."""
-        srcs = [s for s in self.kv_source_layers if s <= layer_id]
-        if not srcs:
-            raise ValueError(f"layer {layer_id} compresses but has no kv source above it")
-        src = max(srcs)
-        if self.compress_ratio(src) != self.compress_ratio(layer_id):
-            raise ValueError(
-                f"layer {layer_id} (ratio {self.compress_ratio(layer_id)}) would read "
-                f"source {src} (ratio {self.compress_ratio(src)})")
-        return src
+        """The layer whose compressed-KV cache ``layer_id`` reads: the latest kv source at or
+        above it, with an equal compress ratio (config.py:113-127)."""
+        return self._lookup(layer_id, 0)
 
     def index_source_for(self, layer_id: int) -> int:
-        """config.py:129-133."""
-        srcs = [s for s in self.index_source_layers if s <= layer_id]
-        if not srcs:
-            raise ValueError(f"layer {layer_id} has no index source above it")
-        return max(srcs)
+        """The latest index source at or above ``layer_id`` (config.py:129-133)."""
+        return self._lookup(layer_id, 1)
+
+    def __setattr__(self, name, value):
+        if name in ("compress_ratios", "kv_source_layers", "index_source_layers", "n_layers"):
+            self.__dict__["_sources"] = None
+        object.__setattr__(self, name, value)
+
+    # ---------------------------------------------------------------- release files
 
     @classmethod
-    def from_dict(cls, c: dict) -> "ModelArgs":
-        """Both release layouts (config.py:135-194)."""
-        if "text_config" in c:
-            top = dict(c)
-            tc = top.pop("text_config")
-            c = {**top, **tc}
-        rope = _get(c, "rope_scaling", default={}) or {}
-        return cls(
-            vocab_size=_get(c, "vocab_size", default=129280),
-            dim=_get(c, "hidden_size", "dim", default=5120),
-            n_layers=_get(c, "num_hidden_layers", "n_layers", default=40),
-            moe_inter_dim=_get(c, "moe_intermediate_size", "moe_inter_dim", default=2304),
-            n_heads=_get(c, "num_attention_heads", "n_heads", default=64),
-            head_dim=_get(c, "head_dim", default=512),
-            rope_head_dim=_get(c, "qk_rope_head_dim", "rope_head_dim", default=64),
-            q_lora_rank=_get(c, "q_lora_rank", default=1280),
-            o_lora_rank=_get(c, "o_lora_rank", default=1024),
-            o_groups=_get(c, "o_groups", default=8),
-            window_size=_get(c, "sliding_window", "window_size", default=128),
-            norm_eps=_get(c, "rms_norm_eps", "norm_eps", default=1e-20),
-            n_routed_experts=_get(c, "n_routed_experts", default=384),
-            n_shared_experts=_get(c, "n_shared_experts", default=1),
-            n_activated_experts=_get(c, "num_experts_per_tok", "n_activated_experts", default=6),
-            score_func=_get(c, "scoring_func", "score_func", default="sqrtsoftplus"),
-            gate_temp=_get(c, "gate_temp", default=1.0),
-            norm_topk_prob=_get(c, "norm_topk_prob", default=True),
-            route_scale=_get(c, "routed_scaling_factor", "route_scale", default=1.5),
-            swiglu_limit=_get(c, "swiglu_limit", default=0.0),
-            compress_ratios=tuple(_get(c, "compress_ratios", default=()) or ()),
-            kv_source_layers=tuple(_get(c, "kv_source_layer_ids", "kv_source_layers", default=()) or ()),
-            index_source_layers=tuple(
-                _get(c, "index_source_layer_ids", "index_source_layers", default=()) or ()),
-            compress_rope_theta=_get(c, "compress_rope_theta", default=160000.0),
-            candidate_source_layer=_get(c, "candidate_source_layer_id", "candidate_source_layer",
-                                        default=-1),
-            candidate_topk_blocks=_get(c, "candidate_topk_blocks", default=0),
-            candidate_block_size=_get(c, "candidate_block_size", default=0),
-            original_seq_len=_get(rope, "original_max_position_embeddings",
-                                  default=_get(c, "original_seq_len", default=65536)),
-            rope_theta=_get(c, "rope_theta", default=10000.0),
-            rope_factor=_get(rope, "factor", default=_get(c, "rope_factor", default=16.0)),
-            beta_fast=_get(rope, "beta_fast", default=_get(c, "beta_fast", default=32)),
-            beta_slow=_get(rope, "beta_slow", default=_get(c, "beta_slow", default=1)),
-            max_seq_len=_get(c, "max_position_embeddings", "max_seq_len", default=1048576),
-            index_n_heads=_get(c, "index_n_heads", default=32),
-            index_head_dim=_get(c, "index_head_dim", default=128),
-            index_topk=_get(c, "index_topk", default=512),
-            hc_mult=_get(c, "hc_mult", default=4),
-            hc_sinkhorn_iters=_get(c, "hc_sinkhorn_iters", default=20),
-            hc_eps=_get(c, "hc_eps", default=1e-6),
-            engram_layer_ids=tuple(_get(c, "engram_layer_ids", default=()) or ()),
-            engram_num_embeddings=tuple(_get(c, "engram_num_embeddings", default=()) or ()),
-            engram_max_ngram_size=_get(c, "engram_max_ngram_size", default=4),
-            engram_vocab_size=_get(c, "engram_vocab_size", default=0),
-            engram_n_heads=_get(c, "engram_n_heads", default=0),
-            engram_head_dim=_get(c, "engram_head_dim", default=0),
-            engram_pad_id=_get(c, "engram_pad_token_id", "engram_pad_id", default=2),
-            engram_compressed_vocab_size=_get(c, "engram_compressed_vocab_size", default=0),
-            n_mtp_layers=_get(c, "num_nextn_predict_layers", "n_mtp_layers", default=0),
-            dspark_target_layer_ids=tuple(_get(c, "dspark_target_layer_ids", default=()) or ()),
-            vision_n_layers=0,
-        )
+    def from_dict(cls, cfg: dict) -> "ModelArgs":
+        """Either release layout: the flat inference file or the hub file whose
+        ``text_config`` overrides its top level (config.py:135-194)."""
+        flat = dict(cfg)
+        nested = flat.pop("text_config", None)
+        if nested is not None:
+            flat.update(nested)
+        rope = flat.get("rope_scaling") or {}
+        kw = {}
+        claimed = {"text_config", "rope_scaling"}
+        for name, json_names, _ in _KEYS:
+            claimed.update(json_names)
+            v = rope.get(_ROPE_SCALING[name]) if name in _ROPE_SCALING else None
+            if v is None:
+                v = _first(flat, json_names)
+            if v is not None:
+                kw[name] = v
+        kw.update({k: v for k, v in flat.items() if k not in claimed and k not in _FIELDS})
+        return cls(**kw)

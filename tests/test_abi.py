@@ -178,6 +178,22 @@ def test_model_args_topology_and_both_config_layouts():
     bad = ModelArgs(compress_ratios=(2, 1), kv_source_layers=(0,))
     with pytest.raises(ValueError, match="ratio"):
         bad.kv_source_for(1)
+    # fields outside the attention path are kept verbatim and readable, never interpreted
+    a = ModelArgs.from_dict({**flat, "hc_mult": 4, "moe_inter_dim": 32})
+    assert a.hc_mult == 4 and a.moe_inter_dim == 32 and a.extra == {"hc_mult": 4, "moe_inter_dim": 32}
+    assert ModelArgs(n_routed_experts=8).n_routed_experts == 8
+    with pytest.raises(AttributeError):
+        ModelArgs().no_such_field
+    # defaults are the release's attention shape
+    d = ModelArgs()
+    assert (d.dim, d.n_heads, d.head_dim, d.rope_head_dim, d.window_size, d.index_topk) == \
+        (5120, 64, 512, 64, 128, 512)
+    # the topology is re-resolved when the sharing fields change
+    d.compress_ratios, d.kv_source_layers = (0, 4, 4), (1,)
+    assert d.kv_source_for(2) == 1
+    d.kv_source_layers = (2,)
+    with pytest.raises(ValueError):
+        d.kv_source_for(1)
 
 
 def test_rope_frequencies_match_oracle_restatement():
