@@ -134,12 +134,16 @@ def make_set(s: Shape, seed, device):
 
 
 def graph_of(fn, reps_sets, torch):
-    """Capture fn(set) for every set in order into one graph (after one eager warm call each)."""
+    """Capture fn(set) for every set in order into one graph (after one eager warm call of each
+    distinct set)."""
     st = torch.cuda.Stream()
     st.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(st):
+        seen = set()
         for d in reps_sets:
-            fn(d)
+            if id(d) not in seen:
+                seen.add(id(d))
+                fn(d)
     torch.cuda.current_stream().wait_stream(st)
     torch.cuda.synchronize()
     gr = torch.cuda.CUDAGraph()
@@ -227,13 +231,17 @@ def run_decode(args, torch, device):
             log(f"[bench] calibration copy of {args.calib_mb} MB x4 done")
         kern = {k: float("nan") for k in ("indexer_topk", "indexer_score", "topk_select", "sparse_mla")}
         return s, ms, kern, sets, cos, sin, ws, []
-    g_full = graph_of(full, sets, torch)
-    warm = max(1, args.warmup // per_replay)
+    # exactly `warmup` untimed steps, then exactly `steps` timed steps, each graph cycling through
+    # the input sets in order
+    if args.warmup > 0:
+        g_warm = graph_of(full, [sets[i % per_replay] for i in range(args.warmup)], torch)
+        g_warm.replay()
+        torch.cuda.synchronize()
+        del g_warm
+    g_full = graph_of(full, [sets[i % per_replay] for i in range(args.steps)], torch)
+    ms = time_graph(g_full, 1, torch) / args.steps
+    log(f"[bench] decode step {ms * 1e3:.2f} us ({args.steps} steps, {args.warmup} warm-up)")
     reps = max(1, args.steps // per_replay)
-    for _ in range(warm):
-        g_full.replay()
-    ms = time_graph(g_full, reps, torch) / per_replay
-    log(f"[bench] decode step {ms * 1e3:.2f} us")
 
     # per-kernel averages (each kernel alone, same rotation, graph-replayed)
     for d in sets:
@@ -747,8 +755,8 @@ def main():
         "value": s.B / (ms * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": max(1, args.steps // len(sets)) * len(sets),
-        "warmup": max(1, args.warmup // len(sets)) * len(sets),
+        "steps": args.steps,
+        "warmup": args.warmup,
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",

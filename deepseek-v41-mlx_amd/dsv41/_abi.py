@@ -154,6 +154,54 @@ def _contig(name: str, *tensors):
             raise ValueError(f"{name}: tensor of shape {tuple(t.shape)} must be contiguous")
 
 
+def _out(name: str, out, shape, dtype, device) -> torch.Tensor:
+    """The output tensor: allocated when the caller passes none, else checked for device, dtype,
+    exact shape and contiguity, so a wrong buffer raises here instead of reaching a kernel."""
+    shape = tuple(int(x) for x in shape)
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    if not isinstance(out, torch.Tensor) or out.device != torch.device(device):
+        raise ValueError(f"{name}: out must be a tensor on {device}")
+    if out.dtype != dtype or tuple(out.shape) != shape or not out.is_contiguous():
+        raise ValueError(f"{name}: out must be contiguous {dtype} {list(shape)}, "
+                         f"got {out.dtype} {list(out.shape)}")
+    return out
+
+
+def _vec(name: str, what: str, t: torch.Tensor, n: int, dtype=torch.float32) -> None:
+    """A per-channel or per-head parameter vector (norm weight, attention sink)."""
+    if t is None or t.dtype != dtype or t.numel() != n or not t.is_contiguous():
+        got = "None" if t is None else f"{t.dtype} {list(t.shape)}"
+        raise ValueError(f"{name}: {what} must be contiguous {dtype} [{n}], got {got}")
+
+
+def _tables(name: str, cos, sin, rd: int) -> None:
+    """Rope tables: fp32 [positions, rd/2], contiguous, the same shape."""
+    if (cos is None or sin is None or cos.dtype != torch.float32 or sin.dtype != torch.float32
+            or cos.dim() != 2 or cos.shape != sin.shape or cos.shape[1] * 2 != rd):
+        raise ValueError(f"{name}: rope tables must be fp32 [positions, {rd // 2}]")
+    _contig(name, cos, sin)
+
+
+def _batch(name: str, what: str, t: torch.Tensor, b: int) -> None:
+    if t.shape[0] < b:
+        raise ValueError(f"{name}: {what} holds {t.shape[0]} batch rows, the call needs {b}")
+
+
+def _ws(name: str, workspace, nbytes: int, device):
+    """A caller's uint8 workspace when it is large enough, else a fresh one (None when the
+    call needs none)."""
+    if not nbytes:
+        return None
+    if workspace is not None:
+        if (not isinstance(workspace, torch.Tensor) or workspace.dtype != torch.uint8
+                or workspace.device != torch.device(device) or not workspace.is_contiguous()):
+            raise ValueError(f"{name}: workspace must be a contiguous uint8 tensor on {device}")
+        if workspace.numel() >= nbytes:
+            return workspace
+    return _workspace(nbytes, device)
+
+
 def dtype_code(t: torch.Tensor, name: str) -> int:
     if t.dtype not in _DTYPES:
         raise ValueError(f"{name}: dtype {t.dtype} not supported (float32 or bfloat16)")
@@ -177,8 +225,7 @@ def row_stride(t: torch.Tensor, name: str) -> int:
 def _fq(name: str, x: torch.Tensor, block: int, out: torch.Tensor | None) -> torch.Tensor:
     _gpu(name, x, out)
     _contig(name, x)
-    out = torch.empty_like(x) if out is None else out
-    _contig(name, out)
+    out = _out(name, out, x.shape, x.dtype, x.device)
     cols = x.shape[-1]
     rows = x.numel() // cols if cols else 0
     _call(name, _ptr(x), _ptr(out), rows, cols, block, dtype_code(x, name), _stream(x))
@@ -216,19 +263,19 @@ def rope_tail(x, rd, cos, sin, pos_base=0, pos_step=1, inverse=False, out=None):
     """x [b, s, d] or [b, s, h, d]; rows of the tables at pos_base + s*pos_step."""
     name = "dsv41_rope_tail"
     _gpu(name, x, cos, sin, out)
-    _contig(name, x, cos, sin)
+    _contig(name, x)
     if x.dim() not in (3, 4):
         raise ValueError(f"{name}: x must be [b, s, d] or [b, s, h, d], got {tuple(x.shape)}")
     b, s = x.shape[0], x.shape[1]
     h = x.shape[2] if x.dim() == 4 else 1
     d = x.shape[-1]
-    if rd > d or cos.shape[-1] * 2 != rd:
-        raise ValueError(f"{name}: rope tables of width {cos.shape[-1]} do not match rd={rd}")
+    if rd > d or rd % 2:
+        raise ValueError(f"{name}: rd={rd} must be even and at most {d}")
+    _tables(name, cos, sin, rd)
     last = pos_base + (s - 1) * pos_step if s else 0
     if s and last >= cos.shape[0]:
         raise ValueError(f"{name}: position {last} beyond the rope table ({cos.shape[0]} rows)")
-    out = torch.empty_like(x) if out is None else out
-    _contig(name, out)
+    out = _out(name, out, x.shape, x.dtype, x.device)
     _call(name, _ptr(x), _ptr(out), b, s, h, d, rd, _ptr(cos), _ptr(sin), pos_base, pos_step,
           1 if inverse else 0, dtype_code(x, name), _stream(x))
     return out
@@ -237,11 +284,9 @@ def rope_tail(x, rd, cos, sin, pos_base=0, pos_step=1, inverse=False, out=None):
 def rmsnorm(x, weight, eps, out=None):
     name = "dsv41_rmsnorm"
     _gpu(name, x, weight, out)
-    _contig(name, x, weight)
-    if weight.dtype != torch.float32 or weight.numel() != x.shape[-1]:
-        raise ValueError(f"{name}: weight must be fp32 [{x.shape[-1]}]")
-    out = torch.empty_like(x) if out is None else out
-    _contig(name, out)
+    _contig(name, x)
+    _vec(name, "weight", weight, x.shape[-1])
+    out = _out(name, out, x.shape, x.dtype, x.device)
     d = x.shape[-1]
     _call(name, _ptr(x), _ptr(out), _ptr(weight), x.numel() // d, d, float(eps),
           dtype_code(x, name), _stream(x))
@@ -254,8 +299,10 @@ def rmsnorm(x, weight, eps, out=None):
 def kv_window_prep(kv, norm_w, cos, sin, rd, start_pos, eps):
     name = "dsv41_kv_window_prep"
     _gpu(name, kv, norm_w, cos, sin)
-    _contig(name, kv, norm_w, cos, sin)
+    _contig(name, kv)
     b, n, d = kv.shape
+    _vec(name, "norm weight", norm_w, d)
+    _tables(name, cos, sin, rd)
     if n and start_pos + n - 1 >= cos.shape[0]:
         raise ValueError(f"{name}: rope table too short")
     _call(name, _ptr(kv), _ptr(norm_w), _ptr(cos), _ptr(sin), b, n, d, rd, start_pos, float(eps),
@@ -299,8 +346,12 @@ def compress_pool(kv, score, kv_state, score_state, norm_w, ratio, start_pos, ep
         if t.dtype != torch.float32:
             raise ValueError(f"{name}: kv/score/state must be fp32")
     b, n, d = kv.shape
-    if kv_state.shape[0] < b or kv_state.shape[1:] != (ratio, d):
-        raise ValueError(f"{name}: state {tuple(kv_state.shape)} does not match [b, {ratio}, {d}]")
+    if score.shape != kv.shape:
+        raise ValueError(f"{name}: score {tuple(score.shape)} must match kv {tuple(kv.shape)}")
+    for st in (kv_state, score_state):
+        if st.dim() != 3 or st.shape[0] < b or st.shape[1:] != (ratio, d):
+            raise ValueError(f"{name}: state {tuple(st.shape)} does not match [>={b}, {ratio}, {d}]")
+    _vec(name, "norm weight", norm_w, d)
     g = (start_pos % ratio + n) // ratio
     lat = torch.empty(b, g, d, dtype=dtype, device=kv.device) if g else None
     code = _DTYPES.get(dtype)
@@ -314,10 +365,12 @@ def compress_pool(kv, score, kv_state, score_state, norm_w, ratio, start_pos, ep
 def comp_write(latents, comp_kv, g0, ratio, cos, sin, rd):
     name = "dsv41_comp_write"
     _gpu(name, latents, comp_kv, cos, sin)
-    _contig(name, latents, cos, sin)
+    _contig(name, latents)
+    _tables(name, cos, sin, rd)
     b, g, d = latents.shape
     if comp_kv.dtype != latents.dtype:
         raise ValueError(f"{name}: cache dtype {comp_kv.dtype} != latent dtype {latents.dtype}")
+    _batch(name, "the compressed cache", comp_kv, b)
     if comp_kv.shape[1] < g0 + g or comp_kv.shape[2] != d:
         raise ValueError(f"{name}: cache {tuple(comp_kv.shape)} cannot take groups {g0}..{g0 + g}")
     if g and (g0 + g - 1) * ratio >= cos.shape[0]:
@@ -329,10 +382,13 @@ def comp_write(latents, comp_kv, g0, ratio, cos, sin, rd):
 def index_key_publish(k_raw, index_k, g0, ratio, norm_w, cos, sin, rd, eps):
     name = "dsv41_index_key_publish"
     _gpu(name, k_raw, index_k, norm_w, cos, sin)
-    _contig(name, k_raw, norm_w, cos, sin)
+    _contig(name, k_raw)
+    _tables(name, cos, sin, rd)
     b, g, d = k_raw.shape
+    _vec(name, "k_norm weight", norm_w, d)
     if index_k.dtype != k_raw.dtype:
         raise ValueError(f"{name}: cache dtype {index_k.dtype} != key dtype {k_raw.dtype}")
+    _batch(name, "the index-key cache", index_k, b)
     if index_k.shape[1] < g0 + g or index_k.shape[2] != d:
         raise ValueError(f"{name}: cache {tuple(index_k.shape)} cannot take groups {g0}..{g0 + g}")
     if g and (g0 + g - 1) * ratio >= cos.shape[0]:
@@ -355,7 +411,8 @@ def comp_write_fp8(latents, codes, scales, g0, ratio, cos, sin, rd):
     [b, >=g0+g, d/32] ue8m0 (one per 32 channels of each row), values fq_fp8_ue8m0(rope(latent))."""
     name = "dsv41_comp_write_fp8"
     _gpu(name, latents, codes, scales, cos, sin)
-    _contig(name, latents, cos, sin)
+    _contig(name, latents)
+    _tables(name, cos, sin, rd)
     b, g, d = _fp8_rows(name, latents, codes, scales, g0)
     if g and (g0 + g - 1) * ratio >= cos.shape[0]:
         raise ValueError(f"{name}: rope table too short")
@@ -368,8 +425,10 @@ def index_key_publish_fp8(k_raw, codes, scales, g0, ratio, norm_w, cos, sin, rd,
     fq_fp8_ue8m0(rope(k_norm(k_raw)))."""
     name = "dsv41_index_key_publish_fp8"
     _gpu(name, k_raw, codes, scales, norm_w, cos, sin)
-    _contig(name, k_raw, norm_w, cos, sin)
+    _contig(name, k_raw)
+    _tables(name, cos, sin, rd)
     b, g, d = _fp8_rows(name, k_raw, codes, scales, g0)
+    _vec(name, "k_norm weight", norm_w, d)
     if g and (g0 + g - 1) * ratio >= cos.shape[0]:
         raise ValueError(f"{name}: rope table too short")
     _call(name, _ptr(k_raw), _ptr(codes), row_stride(codes, name), _ptr(scales), row_stride(scales, name),
@@ -382,8 +441,10 @@ def index_key_publish_mxfp4(k_raw, k_codes, k_scales, g0, ratio, norm_w, cos, si
     k_scales uint8 [b, >=g0+g, d/32] ue8m0 exponents."""
     name = "dsv41_index_key_publish_mxfp4"
     _gpu(name, k_raw, k_codes, k_scales, norm_w, cos, sin)
-    _contig(name, k_raw, norm_w, cos, sin)
+    _contig(name, k_raw)
+    _tables(name, cos, sin, rd)
     b, g, d = k_raw.shape
+    _vec(name, "k_norm weight", norm_w, d)
     if k_codes.dtype != torch.uint8 or k_codes.shape[0] < b or k_codes.shape[2] != d // 2 or k_codes.shape[1] < g0 + g:
         raise ValueError(f"{name}: code cache {tuple(k_codes.shape)} cannot take groups {g0}..{g0 + g}")
     if k_scales.dtype != torch.uint8 or k_scales.shape[0] < b or k_scales.shape[2] != d // 32 or k_scales.shape[1] < g0 + g:
@@ -401,7 +462,8 @@ def index_key_publish_mxfp4(k_raw, k_codes, k_scales, g0, ratio, norm_w, cos, si
 def index_q_prep(q, cos, sin, rd, start_pos):
     name = "dsv41_index_q_prep"
     _gpu(name, q, cos, sin)
-    _contig(name, q, cos, sin)
+    _contig(name, q)
+    _tables(name, cos, sin, rd)
     b, n, h, d = q.shape
     if n and start_pos + n - 1 >= cos.shape[0]:
         raise ValueError(f"{name}: rope table too short")
@@ -423,7 +485,7 @@ def indexer_score(q, w_raw, w_scale, index_k, start_pos, ratio, candidates=None,
         raise ValueError(f"{name}: index_k {tuple(index_k.shape)} {index_k.dtype} does not match q")
     if candidates is not None and (candidates.shape != (b, n, nb) or candidates.dtype not in (torch.uint8, torch.bool)):
         raise ValueError(f"{name}: candidates must be bool/uint8 [{b}, {n}, {nb}]")
-    out = torch.empty(b, n, nb, dtype=torch.float32, device=q.device) if out is None else out
+    out = _out(name, out, (b, n, nb), torch.float32, q.device)
     cand = candidates.view(torch.uint8) if candidates is not None else None
     _call(name, _ptr(q), _ptr(w_raw), float(w_scale), _ptr(index_k), row_stride(index_k, name),
           _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, dtype_code(q, name), _stream(q))
@@ -455,10 +517,8 @@ def indexer_topk(q, w_raw, w_scale, index_k, start_pos, ratio, topk, offset, can
     if ws_bytes == 0:
         return None
     k = min(topk, nb)
-    out = torch.empty(b, n, k, dtype=torch.int32, device=q.device) if out is None else out
-    if out.dtype != torch.int32 or tuple(out.shape) != (b, n, k) or not out.is_contiguous():
-        raise ValueError(f"{name}: out must be contiguous int32 [{b}, {n}, {k}]")
-    ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else _workspace(ws_bytes, q.device)
+    out = _out(name, out, (b, n, k), torch.int32, q.device)
+    ws = _ws(name, workspace, ws_bytes, q.device)
     cand = candidates.view(torch.uint8) if candidates is not None else None
     _call(name, _ptr(q), _ptr(w_raw), float(w_scale), _ptr(index_k), row_stride(index_k, name), _ptr(cand),
           _ptr(out), b, n, h, d, nb, start_pos, ratio, topk, offset, _ptr(ws), ws_bytes, _stream(q))
@@ -485,7 +545,7 @@ def indexer_score_fp8(q, w_raw, w_scale, index_k8, k_scale, scale_rb, nb, start_
         raise ValueError(f"{name}: key scales {tuple(k_scale.shape)} do not match")
     if candidates is not None and (candidates.shape != (b, n, nb) or candidates.dtype not in (torch.uint8, torch.bool)):
         raise ValueError(f"{name}: candidates must be bool/uint8 [{b}, {n}, {nb}]")
-    out = torch.empty(b, n, nb, dtype=torch.float32, device=q.device) if out is None else out
+    out = _out(name, out, (b, n, nb), torch.float32, q.device)
     cand = candidates.view(torch.uint8) if candidates is not None else None
     _call(name, _ptr(q), _ptr(w_raw), float(w_scale), _ptr(index_k8), row_stride(index_k8, name), _ptr(k_scale),
           row_stride(k_scale, name), scale_rb, _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, _stream(q))
@@ -515,10 +575,8 @@ def indexer_topk_fp8(q, w_raw, w_scale, index_k8, k_scale, scale_rb, nb, start_p
     if ws_bytes == 0 or k_scale.data_ptr() % 16 or ks_stride % 16 or index_k8.data_ptr() % 16:
         return None
     k = min(topk, nb)
-    out = torch.empty(b, n, k, dtype=torch.int32, device=q.device) if out is None else out
-    if out.dtype != torch.int32 or tuple(out.shape) != (b, n, k) or not out.is_contiguous():
-        raise ValueError(f"{name}: out must be contiguous int32 [{b}, {n}, {k}]")
-    ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else _workspace(ws_bytes, q.device)
+    out = _out(name, out, (b, n, k), torch.int32, q.device)
+    ws = _ws(name, workspace, ws_bytes, q.device)
     cand = candidates.view(torch.uint8) if candidates is not None else None
     _call(name, _ptr(q), _ptr(w_raw), float(w_scale), _ptr(index_k8), row_stride(index_k8, name), _ptr(k_scale),
           ks_stride, scale_rb, _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, topk, offset, _ptr(ws),
@@ -531,18 +589,16 @@ def index_q_prep_mxfp4(q, cos, sin, rd, start_pos, out=None):
     scales uint8 [b,n,h,d/32]) of fake_quant_fp4_ue8m0(rope_tail(q))."""
     name = "dsv41_index_q_prep_mxfp4"
     _gpu(name, q, cos, sin)
-    _contig(name, q, cos, sin)
+    _contig(name, q)
+    _tables(name, cos, sin, rd)
     b, n, h, d = q.shape
+    if d % 32:
+        raise ValueError(f"{name}: {d} channels is not a whole number of 32-channel blocks")
     if n and start_pos + n - 1 >= cos.shape[0]:
         raise ValueError(f"{name}: rope table too short")
-    if out is None:
-        out = (torch.empty(b, n, h, d // 2, dtype=torch.uint8, device=q.device),
-               torch.empty(b, n, h, d // 32, dtype=torch.uint8, device=q.device))
-    codes, scales = out
-    if codes.shape != (b, n, h, d // 2) or scales.shape != (b, n, h, d // 32):
-        raise ValueError(f"{name}: outputs must be [{b}, {n}, {h}, {d // 2}] and [{b}, {n}, {h}, {d // 32}] uint8")
-    _gpu(name, codes, scales)
-    _contig(name, codes, scales)
+    codes, scales = out if out is not None else (None, None)
+    codes = _out(name, codes, (b, n, h, d // 2), torch.uint8, q.device)
+    scales = _out(name, scales, (b, n, h, d // 32), torch.uint8, q.device)
     _call(name, _ptr(q), _ptr(codes), _ptr(scales), _ptr(cos), _ptr(sin), b, n, h, d, rd, start_pos,
           dtype_code(q, name), _stream(q))
     return codes, scales
@@ -568,7 +624,7 @@ def indexer_score_mxfp4(q_mx, w_raw, w_scale, k_codes, k_scales, nb, start_pos, 
         raise ValueError(f"{name}: key scales {tuple(k_scales.shape)} do not match")
     if candidates is not None and (candidates.shape != (b, n, nb) or candidates.dtype not in (torch.uint8, torch.bool)):
         raise ValueError(f"{name}: candidates must be bool/uint8 [{b}, {n}, {nb}]")
-    out = torch.empty(b, n, nb, dtype=torch.float32, device=w_raw.device) if out is None else out
+    out = _out(name, out, (b, n, nb), torch.float32, w_raw.device)
     cand = candidates.view(torch.uint8) if candidates is not None else None
     _call(name, _ptr(q_codes), _ptr(q_scales), _ptr(w_raw), float(w_scale), _ptr(k_codes), row_stride(k_codes, name),
           _ptr(k_scales), row_stride(k_scales, name), _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio,
@@ -601,10 +657,8 @@ def indexer_topk_mxfp4(q_mx, w_raw, w_scale, k_codes, k_scales, nb, start_pos, r
     if ws_bytes == 0:
         return None
     k = min(topk, nb)
-    out = torch.empty(b, n, k, dtype=torch.int32, device=w_raw.device) if out is None else out
-    if out.dtype != torch.int32 or tuple(out.shape) != (b, n, k) or not out.is_contiguous():
-        raise ValueError(f"{name}: out must be contiguous int32 [{b}, {n}, {k}]")
-    ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else _workspace(ws_bytes, w_raw.device)
+    out = _out(name, out, (b, n, k), torch.int32, w_raw.device)
+    ws = _ws(name, workspace, ws_bytes, w_raw.device)
     cand = candidates.view(torch.uint8) if candidates is not None else None
     _call(name, _ptr(q_codes), _ptr(q_scales), _ptr(w_raw), float(w_scale), _ptr(k_codes), row_stride(k_codes, name),
           _ptr(k_scales), row_stride(k_scales, name), _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, topk,
@@ -627,13 +681,10 @@ def topk_select(scores, topk, start_pos, ratio, offset, workspace=None, out=None
         raise ValueError(f"{name}: scores must be fp32 [b, n, nb]")
     b, n, nb = scores.shape
     k = min(topk, nb)
-    out = torch.empty(b, n, k, dtype=torch.int32, device=scores.device) if out is None else out
-    if out.dtype != torch.int32 or tuple(out.shape) != (b, n, k) or not out.is_contiguous():
-        raise ValueError(f"{name}: out must be contiguous int32 [{b}, {n}, {k}]")
+    out = _out(name, out, (b, n, k), torch.int32, scores.device)
     if out.numel():
         ws_bytes = topk_workspace_bytes(b * n, nb, topk)
-        ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else _workspace(ws_bytes,
-                                                                                                 scores.device)
+        ws = _ws(name, workspace, ws_bytes, scores.device)
         _call(name, _ptr(scores), _ptr(out), b * n, n, nb, topk, start_pos, ratio, offset, _ptr(ws),
               ws_bytes, _stream(scores))
     return out
@@ -699,6 +750,7 @@ def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_sca
     _gpu(name, q, win_kv, chunk_kv, comp_kv, attn_sink, idx, cos, sin, out)
     _contig(name, q, chunk_kv, attn_sink, idx)
     b, n, h, d = q.shape
+    _vec(name, "attn_sink", attn_sink, h)
     wp = min(start_pos, window)
     if chunk_kv.shape != (b, n, d) or chunk_kv.dtype != q.dtype:
         raise ValueError(f"{name}: chunk kv must be {q.dtype} [{b}, {n}, {d}]")
@@ -712,8 +764,10 @@ def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_sca
         raise ValueError(f"{name}: a window ring is needed once start_pos > 0")
     comp_bstride = 0
     if comp_kv is not None and n_comp:
-        if comp_kv.dtype != q.dtype or comp_kv.shape[2] != d or comp_kv.shape[1] < n_comp:
+        if (comp_kv.dim() != 3 or comp_kv.dtype != q.dtype or comp_kv.shape[2] != d
+                or comp_kv.shape[1] < n_comp):
             raise ValueError(f"{name}: compressed cache {tuple(comp_kv.shape)} does not match")
+        _batch(name, "the compressed cache", comp_kv, b)
         comp_bstride = row_stride(comp_kv, name)
     else:
         comp_kv, n_comp = None, 0
@@ -723,15 +777,13 @@ def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_sca
             raise ValueError(f"{name}: idx must be int32 [{b}, {n}, k]")
         k = idx.shape[2]
     if rd:
-        if cos is None or sin is None or cos.shape[-1] * 2 != rd:
-            raise ValueError(f"{name}: rope tables do not match rd={rd}")
+        _tables(name, cos, sin, rd)
         if n and start_pos + n - 1 >= cos.shape[0]:
             raise ValueError(f"{name}: rope table too short")
-    o = torch.empty_like(q) if out is None else out
+    o = _out(name, out, q.shape, q.dtype, q.device)
     rows = min(window, wp + n) + k
     ws_bytes = mla_workspace_bytes(b, n, h, d, rows, q.dtype)
-    if ws_bytes and (workspace is None or workspace.numel() < ws_bytes):
-        workspace = _workspace(ws_bytes, q.device)
+    workspace = _ws(name, workspace, ws_bytes, q.device)
     tail = (_ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, dtype_code(q, name),
             _ptr(workspace) if ws_bytes else None, ws_bytes, _stream(q))
     if write_ring:
@@ -757,6 +809,7 @@ def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, att
     b, n, h, d = q.shape
     if q.dtype != torch.bfloat16 or d != 512:
         raise ValueError(f"{name}: q must be bf16 with 512 channels")
+    _vec(name, "attn_sink", attn_sink, h)
     wp = min(start_pos, window)
     if chunk_kv.shape != (b, n, d) or chunk_kv.dtype != q.dtype:
         raise ValueError(f"{name}: chunk kv must be {q.dtype} [{b}, {n}, {d}]")
@@ -786,15 +839,13 @@ def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, att
             raise ValueError(f"{name}: idx must be int32 [{b}, {n}, k]")
         k = idx.shape[2]
     if rd:
-        if cos is None or sin is None or cos.shape[-1] * 2 != rd:
-            raise ValueError(f"{name}: rope tables do not match rd={rd}")
+        _tables(name, cos, sin, rd)
         if n and start_pos + n - 1 >= cos.shape[0]:
             raise ValueError(f"{name}: rope table too short")
-    o = torch.empty_like(q) if out is None else out
+    o = _out(name, out, q.shape, q.dtype, q.device)
     rows = min(window, wp + n) + k
     ws_bytes = mla_workspace_bytes(b, n, h, d, rows, q.dtype)
-    if ws_bytes and (workspace is None or workspace.numel() < ws_bytes):
-        workspace = _workspace(ws_bytes, q.device)
+    workspace = _ws(name, workspace, ws_bytes, q.device)
     tail = (_ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, _ptr(workspace) if ws_bytes else None,
             ws_bytes, _stream(q))
     if write_ring:

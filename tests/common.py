@@ -38,6 +38,19 @@ C4_TOY = dict(dim=64, n_layers=40, n_heads=4, head_dim=64, rope_head_dim=16, q_l
               compress_rope_theta=40000.0, original_seq_len=64, rope_factor=4.0, max_seq_len=128)
 
 
+# The release's compression ratios at toy size -- the sharing pattern of the reference test's own
+# configuration (tests/test_parity.py:77-83): window-only layers 0-1; a ratio-2 owner (2) with two
+# consumers (3, 4); a ratio-1 owner (5) that is also the candidate source (3 blocks of 2); a
+# ratio-1 consumer (6); and a ratio-1 index source without keys (7) that scores layer 5's keys
+# under layer 5's candidate mask. Window 8, so the ring wraps; top-4 of up to 40 entries.
+RELEASE_TOY = dict(dim=64, n_layers=8, n_heads=4, head_dim=64, rope_head_dim=16, q_lora_rank=32,
+                   o_lora_rank=16, o_groups=4, window_size=8, compress_ratios=(0, 0, 2, 2, 2, 1, 1, 1),
+                   kv_source_layers=(2, 5), index_source_layers=(2, 5, 7), candidate_source_layer=5,
+                   candidate_topk_blocks=3, candidate_block_size=2, index_n_heads=8, index_head_dim=32,
+                   index_topk=4, rope_theta=10000.0, compress_rope_theta=40000.0, original_seq_len=64,
+                   rope_factor=4.0, max_seq_len=128)
+
+
 def args(cfg: dict) -> R.Args:
     return R.Args(**cfg)
 

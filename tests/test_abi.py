@@ -246,3 +246,156 @@ def test_cache_snapshot_restore(index_format, cache_format):
     assert all(torch.equal(t, w) for t, w in zip(tensors(), want))
     kinds = {t.dtype for t in tensors()}
     assert (torch.uint8 in kinds) == (index_format != "dense" or cache_format != "dense")
+
+
+# ------------------------------------------------------------------ wrapper validation
+#
+# The wrappers validate every caller buffer on the host before the launch. These tests run the
+# wrappers over CPU tensors with the device check and the launch replaced by stand-ins: a valid
+# call must reach the launch, and each malformed buffer must raise ValueError before it.
+
+
+class _Launched(Exception):
+    pass
+
+
+@pytest.fixture
+def host_abi(monkeypatch):
+    from dsv41 import _abi
+    calls = []
+
+    def fake_call(name, *args):
+        calls.append(name)
+        raise _Launched(name)
+
+    monkeypatch.setattr(_abi, "_gpu", lambda name, *t: None)
+    monkeypatch.setattr(_abi, "_stream", lambda t: None)
+    monkeypatch.setattr(_abi, "_call", fake_call)
+    return _abi
+
+
+def _reaches_launch(fn):
+    with pytest.raises(_Launched):
+        fn()
+
+
+def _refused(fn, match=None):
+    with pytest.raises(ValueError, match=match):
+        fn()
+
+
+def test_validation_helpers():
+    from dsv41 import _abi
+    ok = torch.zeros(2, 3)
+    assert _abi._out("f", ok, (2, 3), torch.float32, "cpu") is ok
+    assert _abi._out("f", None, (2, 3), torch.int32, "cpu").dtype == torch.int32
+    _refused(lambda: _abi._out("f", torch.zeros(2, 2), (2, 3), torch.float32, "cpu"), "out must be")
+    _refused(lambda: _abi._out("f", torch.zeros(2, 3, dtype=torch.bfloat16), (2, 3), torch.float32, "cpu"))
+    _refused(lambda: _abi._out("f", torch.zeros(3, 2).t(), (2, 3), torch.float32, "cpu"))
+    _refused(lambda: _abi._vec("f", "sink", torch.zeros(4, dtype=torch.bfloat16), 4), "sink")
+    _refused(lambda: _abi._vec("f", "sink", torch.zeros(3), 4), "sink")
+    _refused(lambda: _abi._tables("f", torch.zeros(8, 4), torch.zeros(8, 4), 16), "rope tables")
+    _refused(lambda: _abi._batch("f", "cache", torch.zeros(1, 4, 4), 2), "batch rows")
+    assert _abi._ws("f", None, 0, "cpu") is None
+    big = torch.zeros(64, dtype=torch.uint8)
+    assert _abi._ws("f", big, 32, "cpu") is big
+    assert _abi._ws("f", big, 128, "cpu").numel() == 128       # too small: a fresh one
+    _refused(lambda: _abi._ws("f", torch.zeros(64), 32, "cpu"), "workspace")
+
+
+def test_fake_quant_rope_norm_wrappers_check_out(host_abi):
+    A = host_abi
+    x = torch.zeros(4, 64)
+    _reaches_launch(lambda: A.fq_fp8_ue8m0(x, out=torch.zeros(4, 64)))
+    _refused(lambda: A.fq_fp8_ue8m0(x, out=torch.zeros(2, 64)))
+    _refused(lambda: A.fq_fp4_e4m3(x, out=torch.zeros(4, 64, dtype=torch.bfloat16)))
+    cos = sin = torch.zeros(16, 8)
+    xr = torch.zeros(1, 4, 2, 64)
+    _reaches_launch(lambda: A.rope_tail(xr, 16, cos, sin))
+    _refused(lambda: A.rope_tail(xr, 16, cos, sin, out=torch.zeros(1, 4, 2, 32)))
+    _refused(lambda: A.rope_tail(xr, 16, cos.double(), sin.double()), "rope tables")
+    _reaches_launch(lambda: A.rmsnorm(x, torch.ones(64), 1e-6))
+    _refused(lambda: A.rmsnorm(x, torch.ones(64), 1e-6, out=torch.zeros(4, 63)))
+    _refused(lambda: A.rmsnorm(x, torch.ones(64, dtype=torch.bfloat16), 1e-6), "weight")
+
+
+def test_cache_writers_check_batch_rows_and_parameters(host_abi):
+    A = host_abi
+    cos = sin = torch.zeros(64, 8)
+    lat = torch.zeros(2, 3, 64)
+    _reaches_launch(lambda: A.comp_write(lat, torch.zeros(2, 8, 64), 0, 4, cos, sin, 16))
+    _refused(lambda: A.comp_write(lat, torch.zeros(1, 8, 64), 0, 4, cos, sin, 16), "batch rows")
+    k = torch.zeros(2, 3, 32)
+    _reaches_launch(lambda: A.index_key_publish(k, torch.zeros(2, 8, 32), 0, 4, torch.ones(32), cos, sin, 16,
+                                                1e-6))
+    _refused(lambda: A.index_key_publish(k, torch.zeros(1, 8, 32), 0, 4, torch.ones(32), cos, sin, 16, 1e-6),
+             "batch rows")
+    _refused(lambda: A.index_key_publish(k, torch.zeros(2, 8, 32), 0, 4, torch.ones(16), cos, sin, 16, 1e-6),
+             "k_norm")
+    kv = torch.zeros(2, 1, 64)
+    _reaches_launch(lambda: A.kv_window_prep(kv, torch.ones(64), cos, sin, 16, 0, 1e-6))
+    _refused(lambda: A.kv_window_prep(kv, torch.ones(64, dtype=torch.bfloat16), cos, sin, 16, 0, 1e-6),
+             "norm weight")
+    st = torch.zeros(2, 4, 64)
+    _reaches_launch(lambda: A.compress_pool(kv, kv.clone(), st, st.clone(), torch.ones(64), 4, 3, 1e-6,
+                                            torch.float32))
+    _refused(lambda: A.compress_pool(kv, kv.clone(), st, torch.zeros(2, 4, 32), torch.ones(64), 4, 3, 1e-6,
+                                     torch.float32), "state")
+    _refused(lambda: A.compress_pool(kv, kv.clone(), st, st.clone(), torch.ones(32), 4, 3, 1e-6,
+                                     torch.float32), "norm weight")
+
+
+def test_indexer_and_topk_wrappers_check_out(host_abi):
+    A = host_abi
+    q = torch.zeros(2, 1, 4, 32)
+    w = torch.zeros(2, 1, 4)
+    ik = torch.zeros(2, 16, 32)
+    _reaches_launch(lambda: A.indexer_score(q, w, 0.1, ik, 64, 4))
+    _refused(lambda: A.indexer_score(q, w, 0.1, ik, 64, 4, out=torch.zeros(2, 1, 8)))
+    _refused(lambda: A.indexer_score(q, w, 0.1, ik, 64, 4, out=torch.zeros(2, 1, 16, dtype=torch.bfloat16)))
+    s = torch.zeros(2, 1, 16)
+    _reaches_launch(lambda: A.topk_select(s, 4, 64, 4, 0))
+    _refused(lambda: A.topk_select(s, 4, 64, 4, 0, out=torch.zeros(2, 1, 3, dtype=torch.int32)))
+    _refused(lambda: A.topk_select(s, 4, 64, 4, 0, out=torch.zeros(2, 1, 4)))
+
+
+def test_sparse_mla_wrappers_check_buffers(host_abi):
+    A = host_abi
+    b, h, d, W = 2, 16, 512, 8
+    q = torch.zeros(b, 1, h, d, dtype=torch.bfloat16)
+    ring = torch.zeros(b, W, d, dtype=torch.bfloat16)
+    chunk = torch.zeros(b, 1, d, dtype=torch.bfloat16)
+    comp = torch.zeros(b, 1024, d, dtype=torch.bfloat16)
+    sink = torch.zeros(h)
+    idx = torch.zeros(b, 1, 512, dtype=torch.int32)    # long enough that the list is split
+    cos = sin = torch.zeros(128, 32)
+    assert A.mla_workspace_bytes(b, 1, h, d, W + 512, torch.bfloat16) > 0
+
+    def call(**kw):
+        args = dict(q=q, win_kv=ring, chunk_kv=chunk, comp_kv=comp, n_comp=1000, attn_sink=sink, idx=idx,
+                    softmax_scale=0.1, window=W, start_pos=64, cos=cos, sin=sin, rd=64)
+        args.update(kw)
+        return lambda: A.sparse_mla(**args)
+
+    _reaches_launch(call())
+    _reaches_launch(call(write_ring=True))
+    _refused(call(out=torch.zeros(b, 1, h, d // 2, dtype=torch.bfloat16)), "out must be")
+    _refused(call(out=torch.zeros(b, 1, h, d)), "out must be")
+    _refused(call(comp_kv=comp[:1]), "batch rows")
+    _refused(call(attn_sink=sink.to(torch.bfloat16)), "attn_sink")
+    _refused(call(attn_sink=torch.zeros(h - 1)), "attn_sink")
+    _refused(call(cos=cos[:, :16], sin=sin[:, :16]), "rope tables")
+    _refused(call(workspace=torch.zeros(1 << 20)), "workspace")
+    codes = torch.zeros(b, 1024, d, dtype=torch.uint8)
+    scales = torch.zeros(b, 32, d // 32, dtype=torch.uint8)
+
+    def call8(**kw):
+        args = dict(q=q, win_kv=ring, chunk_kv=chunk, comp8=codes, comp_scale=scales, scale_rb=32, n_comp=1000,
+                    attn_sink=sink, idx=idx, softmax_scale=0.1, window=W, start_pos=64, cos=cos, sin=sin, rd=64)
+        args.update(kw)
+        return lambda: A.sparse_mla_fp8(**args)
+
+    _reaches_launch(call8())
+    _refused(call8(out=torch.zeros(b, 1, h, d - 32, dtype=torch.bfloat16)), "out must be")
+    _refused(call8(comp8=codes[:1], comp_scale=scales[:1]), "does not match")
+    _refused(call8(attn_sink=sink.double()), "attn_sink")

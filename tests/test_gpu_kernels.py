@@ -747,3 +747,40 @@ def test_sparse_mla_decode_writes_the_ring(gpu, dt, b, h, d, window, start, n_co
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     assert torch.equal(ring_b, ring_a)
+
+
+def test_wrappers_refuse_bad_buffers_before_launch(gpu):
+    """A caller's malformed buffer raises ValueError on the host, before any kernel runs: an
+    undersized or mistyped out, a cache with fewer batch rows than the call, a bf16 sink or norm
+    weight. The same calls with correct buffers then run."""
+    from dsv41 import _abi
+    from dsv41.layers import precompute_freqs_cis
+    g = torch.Generator(gpu).manual_seed(SEED_BASE + 77)
+    rn = lambda *s: torch.randn(*s, generator=g, device=gpu)   # noqa: E731
+    b, H, D, W, nb, K, start, rd = 4, 64, 512, 128, 2048, 256, 8191, 64
+    q, chunk, win = rn(b, 1, H, D).bfloat16(), rn(b, 1, D).bfloat16(), rn(b, W, D).bfloat16()
+    comp, sink = rn(b, nb, D).bfloat16(), rn(H)
+    iq, ik, w = rn(b, 1, 64, 128).bfloat16(), rn(b, nb, 128).bfloat16(), rn(b, 1, 64).bfloat16()
+    cos, sin = precompute_freqs_cis(rd, start + 1, 65536, 160000.0, 16.0, 32, 1, device=gpu)
+    scores = _abi.indexer_score(iq, w, 0.01, ik, start, 4)
+    idx = _abi.topk_select(scores, K, start, 4, W + 1)
+    args = (q, win, chunk, comp, nb, sink, idx, D ** -0.5, W, start, cos, sin, rd)
+    with pytest.raises(ValueError, match="out must be"):
+        _abi.sparse_mla(*args, out=torch.empty(b, 1, H, D // 2, dtype=torch.bfloat16, device=gpu))
+    with pytest.raises(ValueError, match="batch rows"):
+        _abi.sparse_mla(q, win, chunk, comp[: b - 1], nb, sink, idx, D ** -0.5, W, start, cos, sin, rd)
+    with pytest.raises(ValueError, match="attn_sink"):
+        _abi.sparse_mla(q, win, chunk, comp, nb, sink.bfloat16(), idx, D ** -0.5, W, start, cos, sin, rd)
+    with pytest.raises(ValueError, match="out must be"):
+        _abi.indexer_score(iq, w, 0.01, ik, start, 4, out=torch.empty(b, 1, nb - 1, device=gpu))
+    with pytest.raises(ValueError, match="out must be"):
+        _abi.topk_select(scores, K, start, 4, W + 1, out=torch.empty(b, 1, K, dtype=torch.int64, device=gpu))
+    with pytest.raises(ValueError, match="batch rows"):
+        _abi.comp_write(rn(b, 1, D).bfloat16(), comp[: b - 1], 0, 4, cos, sin, rd)
+    with pytest.raises(ValueError, match="k_norm"):
+        _abi.index_key_publish(rn(b, 1, 128).bfloat16(), ik, 0, 4, torch.ones(128, device=gpu).bfloat16(), cos,
+                               sin, rd, 1e-6)
+    torch.cuda.synchronize()
+    o = _abi.sparse_mla(*args, out=torch.empty_like(q))
+    torch.cuda.synchronize()
+    assert torch.isfinite(o.float()).all()

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from common import C4_TOY, SEED_BASE, args, load_stack, model_args, rel_max_diff, to_np
+from common import C4_TOY, RELEASE_TOY, SEED_BASE, args, load_stack, model_args, rel_max_diff, to_np
 from oracle import cpu_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -123,22 +123,27 @@ def _record_decode(stack, h, cache):
     return recs
 
 
-@pytest.mark.parametrize("index_format", ["dense", "mxfp4", "fp8"])
-def test_stack_step_reproduces_attention_stack(gpu, index_format):
-    """Toy C4 topology in bf16: 39 prefill tokens, then the decode token at position 39, which
-    completes group 9 (owners write a latent and a key); dense or MXFP4 index caches, or the
-    fp8 cache variant (fp8 compressed KV and index keys). The packed formats use the widths
-    their kernels take (128-channel index keys; fp8 latents of 512)."""
+@pytest.mark.parametrize("topology,index_format,T", [
+    ("c4", "dense", 40), ("c4", "mxfp4", 40), ("c4", "fp8", 40),
+    ("release", "dense", 40), ("release", "dense", 39), ("release", "fp8", 40), ("release", "mxfp4", 39)])
+def test_stack_step_reproduces_attention_stack(gpu, topology, index_format, T):
+    """Toy C4 topology (ratio 4) or the release's ratios (0,0,2,2,2,1,1,1) in bf16: T-1 prefill
+    tokens, then the decode token at position T-1. At T = 40 it completes a group at every ratio
+    (owners write a latent and a key); at T = 39 the ratio-2 group stays open (its compressor
+    state carries) while the ratio-1 owner writes. Dense or MXFP4 index caches, or the fp8 cache
+    variant (fp8 compressed KV and index keys). The packed formats use the widths their kernels
+    take (128-channel index keys; fp8 latents of 512)."""
     from dsv41.model import AttentionStack
     from dsv41.step import StackDecodeStep
-    cfg = dict(C4_TOY, index_head_dim=128) if index_format == "mxfp4" else C4_TOY
+    base = C4_TOY if topology == "c4" else RELEASE_TOY
+    cfg = dict(base, index_head_dim=128) if index_format == "mxfp4" else base
     if index_format == "fp8":
-        cfg = dict(C4_TOY, index_head_dim=128, head_dim=512, rope_head_dim=64)
+        cfg = dict(base, index_head_dim=128, head_dim=512, rope_head_dim=64)
     a = args(cfg)
     st = AttentionStack(model_args(cfg), torch.bfloat16, gpu)
     load_stack(st, R.make_params(a, SEED_BASE + 40, "bf16"))
     rng = np.random.default_rng(SEED_BASE + 40)
-    b, T = 2, 40
+    b = 2
     h = torch.from_numpy(rng.standard_normal((b, T, a.dim)).astype(F32)).to(gpu).to(torch.bfloat16)
     if index_format == "fp8":
         cache = st.make_cache(b, a.max_seq_len, cache_format="fp8")
@@ -159,8 +164,12 @@ def test_stack_step_reproduces_attention_stack(gpu, index_format):
             assert (x is None) == (y is None)
             if x is not None:
                 assert torch.equal(x, y), f"layer {l} {name}"
-    # the candidate mask is live at this size: layers after 20 use it, and it drops blocks
-    assert step.plan[20].candidate_source and step.plan[24].uses_candidates
+    # the candidate mask is live at this size: layers after the source use it, and it drops blocks
+    if topology == "c4":
+        assert step.plan[20].candidate_source and step.plan[24].uses_candidates
+    else:
+        assert step.plan[5].candidate_source and step.plan[7].uses_candidates
+        assert [p.ratio for p in step.plan] == [0, 0, 2, 2, 2, 1, 1, 1]
 
 
 def c4_args(**over):

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from common import C1, TOPO, args, max_abs
+from common import C1, RELEASE_TOY, TOPO, args, max_abs, rel_max_diff
 from oracle import cpu_ref as R
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "fakequant_kat.npz")
@@ -447,11 +447,11 @@ def _stack(cfg, seed):
     return a, R.AttentionStack(a, R.make_params(a, seed))
 
 
-@pytest.mark.parametrize("cfg", [C1, TOPO], ids=["C1", "TOPO"])
+@pytest.mark.parametrize("cfg", [C1, TOPO, RELEASE_TOY], ids=["C1", "TOPO", "RELEASE"])
 def test_stack_decode_equals_prefill_tail_and_chunked_equals_single(cfg):
     a, st = _stack(cfg, 21)
     rng = np.random.default_rng(22)
-    T = 40 if cfg is TOPO else 136
+    T = 136 if cfg is C1 else 40
     h = rng.standard_normal((2, T, a.dim)).astype(F32)
     full = st(h, R.ModelCache(a, 2, a.max_seq_len))
     cache = R.ModelCache(a, 2, a.max_seq_len)
@@ -459,11 +459,12 @@ def test_stack_decode_equals_prefill_tail_and_chunked_equals_single(cfg):
     for t in range(T - 8, T):
         outs.append(st(h[:, t:t + 1], cache))
     dec = np.concatenate(outs, axis=1)
-    assert max_abs(dec, full) < 2e-5
+    # float32 reduction-order noise only (the reference test's metric and strict threshold scale)
+    assert rel_max_diff(dec, full) < 1e-5
     cache = R.ModelCache(a, 2, a.max_seq_len)
     cuts = sorted({0, 13, 14, 27, T - 9, T})
     chunks = [st(h[:, s:e], cache) for s, e in zip(cuts[:-1], cuts[1:])]
-    assert max_abs(np.concatenate(chunks, axis=1), full) < 2e-5
+    assert rel_max_diff(np.concatenate(chunks, axis=1), full) < 1e-5
 
 
 def test_topology_negative_controls_move_the_output():
