@@ -45,8 +45,10 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ w_raw, float w_scale,
     const void* __restrict__ kcache, int64_t k_bstride, const uint8_t* __restrict__ kscale, int64_t ks_bstride,
     int ks_rb, const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int nb, int start_pos, int ratio,
-    int rows_per_wg) {
+    int rows_per_wg, int heads) {
   static_assert(!F8 || KS == 4, "fp8 keys: 128 channels (four scale bytes per row block)");
+  // H = the head tiles' rows; heads <= H are real. The rows past `heads` hold a zero query and a
+  // zero weight, so each adds exactly +0 to the score.
   constexpr int H = HT * 16;
   constexpr int DIM = KS * 32;
   constexpr int QROW = DIM * 2 + 16;       // padded LDS row stride in bytes
@@ -131,12 +133,12 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
   // query's global loads go out first, then every wave's first batch (unconditional and clamped,
   // so the wait counts stay exact), then the LDS store and the barrier.
   constexpr int QN = (H * DIM / 8 + kIdxThreads - 1) / kIdxThreads;
-  const uint4* qrow = reinterpret_cast<const uint4*>(q + (int64_t)qi * H * DIM);
+  const uint4* qrow = reinterpret_cast<const uint4*>(q + (int64_t)qi * heads * DIM);
   uint4 qv[QN];
 #pragma unroll
   for (int c = 0; c < QN; ++c) {
     const int e = tid + c * kIdxThreads;
-    qv[c] = e < H * DIM / 8 ? qrow[e] : make_uint4(0u, 0u, 0u, 0u);
+    qv[c] = e < heads * DIM / 8 ? qrow[e] : make_uint4(0u, 0u, 0u, 0u);
   }
   Batch ka, kb2;
   load(ka, min(t0, vis_end - 1));
@@ -155,11 +157,14 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_score_bf16_kernel(
     for (int ks = 0; ks < KS; ++ks)
       qa[ht][ks] = ld_bf16x8(q_lds + (ht * 16 + l16) * QROW + (ks * 32 + g * 8) * 2);
   {
-    const bf16_t* wrow = w_raw + (int64_t)qi * H;
+    const bf16_t* wrow = w_raw + (int64_t)qi * heads;
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wrow[ht * 16 + 4 * g + i]) * w_scale);
+      for (int i = 0; i < 4; ++i) {
+        const int h = ht * 16 + 4 * g + i;
+        wv[ht][i] = h < heads ? round_bf16(bf2f(wrow[h]) * w_scale) : 0.0f;
+      }
   }
   if (t0 >= vis_end) return;
   for (;;) {
@@ -675,14 +680,21 @@ __global__ __launch_bounds__(256) void indexer_score_f32_kernel(
   scores[(int64_t)qi * nb + t] = v;
 }
 
+// Head tiles of the register-kernel instance for `heads` (1, 2, 4 or 8 tiles of 16; 0 if none
+// serves: more than 128 heads).
+static int head_tiles_instance(int heads) {
+  const int t = (heads + 15) / 16;
+  return t <= 1 ? 1 : t <= 2 ? 2 : t <= 4 ? 4 : t <= 8 ? 8 : 0;
+}
+
 template <int HT, int KS, bool F8>
 static void launch_idx_bf16(dim3 grid, hipStream_t stream, const void* q, const void* w_raw, float w_scale,
                             const void* index_k, int64_t k_bstride, const uint8_t* kscale, int64_t ks_bstride,
                             int ks_rb, const uint8_t* cand, float* scores, int n, int nb, int start_pos, int ratio,
-                            int rows_per_wg) {
+                            int rows_per_wg, int heads) {
   hipLaunchKernelGGL((indexer_score_bf16_kernel<HT, KS, F8>), grid, dim3(kIdxThreads), 0, stream,
                      (const bf16_t*)q, (const bf16_t*)w_raw, w_scale, index_k, k_bstride, kscale, ks_bstride, ks_rb,
-                     cand, scores, n, nb, start_pos, ratio, rows_per_wg);
+                     cand, scores, n, nb, start_pos, ratio, rows_per_wg, heads);
 }
 
 // ~256 workgroups over all rows (one per CU), in multiples of one 8-wave sweep of four tiles
@@ -754,10 +766,13 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
     DSV41_DEC_CASE(1)
 #undef DSV41_DEC_CASE
   }
+  // the register kernel serves every head count up to 128 in whole 16-head tiles (the last one
+  // padded with zero queries and weights), as the reference's kernel wrapper pads heads to 16
+  const int ht_inst = head_tiles_instance(heads);
 #define DSV41_IDX_CASE(HT_, KS_)                                                                          \
-  if (heads == HT_ * 16 && dim == KS_ * 32) {                                                                \
+  if (ht_inst == HT_ && dim == KS_ * 32) {                                                                   \
     launch_idx_bf16<HT_, KS_, false>(grid, stream, q, w_raw, w_scale, index_k, k_bstride, nullptr, 0, 1,     \
-                                     candidates, scores, n, nb, start_pos, ratio, rows_per_wg);              \
+                                     candidates, scores, n, nb, start_pos, ratio, rows_per_wg, heads);       \
     return check_launch(what);                                                                               \
   }
   DSV41_IDX_CASE(4, 4)   // 64 heads x 128
@@ -770,6 +785,8 @@ extern "C" int dsv41_indexer_score(const void* q, const void* w_raw, float w_sca
   DSV41_IDX_CASE(1, 1)
   DSV41_IDX_CASE(2, 1)
   DSV41_IDX_CASE(4, 1)
+  DSV41_IDX_CASE(8, 2)
+  DSV41_IDX_CASE(8, 1)
 #undef DSV41_IDX_CASE
   return set_error(DSV41_E_SHAPE, "%s: bf16 path has no instance for heads=%d dim=%d", what, heads, dim);
 }
@@ -832,10 +849,11 @@ extern "C" int dsv41_indexer_score_fp8(const void* q, const void* w_raw, float w
     DSV41_DEC8_CASE(1)
 #undef DSV41_DEC8_CASE
   }
+  const int ht_inst = head_tiles_instance(heads);
 #define DSV41_IDX8_CASE(HT_)                                                                                   \
-  if (heads == HT_ * 16) {                                                                                     \
+  if (ht_inst == HT_) {                                                                                        \
     launch_idx_bf16<HT_, 4, true>(grid, stream, q, w_raw, w_scale, index_k, k_bstride, k_scale, ks_bstride,  \
-                                  ks_rb, candidates, scores, n, nb, start_pos, ratio, rows_per_wg);            \
+                                  ks_rb, candidates, scores, n, nb, start_pos, ratio, rows_per_wg, heads);     \
     return check_launch(what);                                                                                 \
   }
   DSV41_IDX8_CASE(4)   // 64 heads

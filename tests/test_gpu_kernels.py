@@ -215,6 +215,9 @@ def test_index_q_prep(gpu, dt):
     ("bf16", 64, 128, 2, 1, 50, 199, False),       # decode kernel: fewer rows than one 8-wave sweep
     ("bf16", 16, 128, 3, 2, 3000, 4000, True),     # decode kernel: workgroups wholly past visibility
     ("bf16", 32, 128, 5, 1, 20000, 79999, True),   # decode kernel: 40 row ranges, candidates
+    ("bf16", 8, 32, 2, 5, 40, 30, True),           # 8 heads, one padded 16-head tile (the reference test's count)
+    ("bf16", 24, 64, 2, 1, 900, 3500, False),      # 24 heads: two tiles, the second half padding
+    ("bf16", 100, 128, 1, 2, 500, 1900, False),    # 100 heads: eight tiles, register kernel
 ])
 def test_indexer_score(gpu, dt, hi, di, b, n, nb, start, use_cand):
     from dsv41 import _abi

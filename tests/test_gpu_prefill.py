@@ -113,7 +113,9 @@ def test_c3_chunked_prefill_full_size(gpu):
     for j, s in enumerate(rows):
         w = R.cast(f(t["w"][:, s:s + 1]) * F32(ws), "bf16")
         want = R.indexer_scores(f(t["iq"][:, s:s + 1]), ik, w, prior + s, RATIO)[0, 0]
-        assert np.abs(got_s[j] - want).max() <= 1e-5 * np.abs(want).max(), f"scores row {s}"
+        vis = np.isfinite(want)                          # entries past visibility are -inf on both
+        assert np.array_equal(np.isneginf(got_s[j]), ~vis), f"visibility row {s}"
+        assert np.abs(got_s[j][vis] - want[vis]).max() <= 1e-5 * np.abs(want[vis]).max(), f"scores row {s}"
         lens_s = R.query_lens(prior + s, 1, RATIO)
         wi = R.topk_indices(got_s[j][None, None], K, lens_s, offset)[0, 0]
         assert np.array_equal(idx[0, s].cpu().numpy(), wi), f"top-k row {s}"

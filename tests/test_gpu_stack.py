@@ -136,7 +136,8 @@ def test_stack_step_reproduces_attention_stack(gpu, topology, index_format, T):
     from dsv41.model import AttentionStack
     from dsv41.step import StackDecodeStep
     base = C4_TOY if topology == "c4" else RELEASE_TOY
-    cfg = dict(base, index_head_dim=128) if index_format == "mxfp4" else base
+    # MXFP4 index caches: the fp4 MFMA kernels take 16/32/64 heads of 128 channels
+    cfg = dict(base, index_head_dim=128, index_n_heads=16) if index_format == "mxfp4" else base
     if index_format == "fp8":
         cfg = dict(base, index_head_dim=128, head_dim=512, rope_head_dim=64)
     a = args(cfg)
