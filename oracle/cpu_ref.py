@@ -32,7 +32,18 @@ Pinning status (what checks each function; see tests/test_oracle.py):
   * top-k (a13)               -- brute-force python sort on (-score, index), adversarial ties
   * sparse attention (a14)    -- float64 brute force, closed forms (single index, sink -> -inf,
                                  all masked -> 0)
-  * attention layer/stack     -- decode == tail of prefill, chunked == single forward
+  * attention layer/stack     -- DeepSeek's torch Attention / Compressor / Indexer (the reference's
+    (AttentionLayer,             docs/reference/model.py:429-789) run as an attention-only stack
+     AttentionStack,             over the same weights: tests/golden/layer_golden.npz holds its
+     publish_keys,               prefill and decode outputs, owner caches, the scores each index
+     indexer_forward,            source ranks and its selection, for three topologies (ratio 4;
+     index_weight_scale,         ratios 0/2/1 as released), fake-quant off and on; planted
+     group_positions)            composition mistakes fail it. Plus decode == tail of prefill and
+                                 chunked == single forward (the reference has no chunked path).
+  * index_weight_scale in bf16 -- the rounding of the python scalar to the activation dtype follows
+                                 MLX's weak scalar typing (an array's dtype wins); the fixtures run
+                                 in float32, where the scale is exact, so the bf16 rounding of the
+                                 scalar itself is "parity unpinned".
 """
 
 from __future__ import annotations
@@ -564,11 +575,17 @@ def compressor_forward(x, start_pos, state, p, ratio, eps, dtype):
 # ---------------------------------------------------------------------------
 
 
+def group_positions(g0: int, g: int, ratio: int) -> np.ndarray:
+    """Rope positions of compressed groups g0 .. g0+g-1: a latent stands for the first token of
+    its group, so group j rotates at position j * ratio (attention.py:157-161, indexer.py:100-102)."""
+    return (g0 + np.arange(g)) * ratio
+
+
 def publish_keys(latents, start_pos, ratio, rd, cos, sin, p, eps, dtype, cache: LayerCache):
     """Indexer.publish_keys (indexer.py:89-104)."""
     g0 = start_pos // ratio
     g = latents.shape[1]
-    pos = (g0 + np.arange(g)) * ratio
+    pos = group_positions(g0, g, ratio)
     k = rmsnorm(linear(latents, p["wk"], dtype), p["k_norm"], eps, dtype)
     k = rope_tail(k, rd, cos[pos], sin[pos], dtype=dtype)
     k = fq_fp4_ue8m0(k, 32, dtype)
@@ -692,7 +709,7 @@ class AttentionLayer:
             if latents is not None:
                 g0 = start_pos // self.ratio
                 g = latents.shape[1]
-                pos = (g0 + np.arange(g)) * self.ratio
+                pos = group_positions(g0, g, self.ratio)
                 latents = rope_tail(latents, rd, cos[pos], sin[pos], dtype=dt)
                 latents = fq_fp4_e4m3(latents, 16, dt)
                 lc.comp_kv[:bsz, g0:g0 + g] = cast(latents, lc.dtype)
