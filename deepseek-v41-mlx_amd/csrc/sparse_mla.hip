@@ -18,6 +18,8 @@
 // applies the inverse rope to the last rd channels (attention.py:174-175).
 //
 // fp32 kernel: a plain FMA implementation for the 1e-5 parity configs.
+#include <mutex>
+
 #include "mfma.h"
 
 namespace dsv41 {
@@ -865,6 +867,65 @@ extern "C" int dsv41_sparse_mla_decode(const void* q, void* win_kv, const void* 
   return sparse_mla_layer("dsv41_sparse_mla_decode", q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp, sink, idx, k,
                           o, bsz, 1, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, dtype, workspace,
                           workspace_bytes, true, stream);
+}
+
+// ------------------------------------------------------------------ allocation-free decode
+//
+// dsv41_sparse_mla_decode_noalloc keeps the split partials in `scratch`, a file-scope device array
+// (one copy per GPU, held for the life of the process), instead of a caller workspace. Host code
+// never passes the array's name to a kernel: on the host that name is a stand-in, not a device
+// address. The device address is looked up once per device, with that device current, and kept.
+
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;   // 32 MiB per GPU
+constexpr int kMaxScratchDevices = 64;
+
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's address of `scratch`, looked up on its first use on that device.
+static int scratch_of_current_device(const char* what, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error((int)e, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  DSV41_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, DSV41_E_ARG, "%s: device %d beyond the %d the scratch table holds",
+                what, dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return set_error((int)e, "%s: hipGetSymbolAddress(scratch) failed: %s", what,
+                                          hipGetErrorString(e));
+    DSV41_REQUIRE(p != nullptr, DSV41_E_ARG, "%s: scratch has no address on device %d", what, dev);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+extern "C" int dsv41_sparse_mla_decode_noalloc(const void* q, void* win_kv, const void* chunk_kv,
+                                               const void* comp_kv, int64_t comp_bstride, int32_t n_comp,
+                                               const float* sink, const int32_t* idx, int32_t k, void* o,
+                                               int32_t bsz, int32_t heads, int32_t dim, int32_t window,
+                                               int32_t start_pos, float scale, const float* cos_tab,
+                                               const float* sin_tab, int32_t rd, int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_sparse_mla_decode_noalloc";
+  const int wp = start_pos < window ? start_pos : window;
+  const int weff = window < wp + 1 ? window : wp + 1;
+  size_t need = 0;
+  if (dtype == DSV41_BF16 && bsz > 0 && heads > 0 && dim > 0 && k >= 0)
+    need = workspace_for(plan_bf16(bsz, heads, weff + k, dim), bsz, heads, dim);
+  DSV41_REQUIRE(need <= kNoAllocScratchBytes, DSV41_E_WORKSPACE,
+                "%s: this shape needs %zu bytes of split scratch, beyond the %zu-byte static buffer (use "
+                "dsv41_sparse_mla_decode with a workspace)", what, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need) {
+    int rc = scratch_of_current_device(what, &ws);
+    if (rc) return rc;
+  }
+  return sparse_mla_layer(what, q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp, sink, idx, k, o, bsz, 1, heads,
+                          dim, window, start_pos, scale, cos_tab, sin_tab, rd, dtype, ws, need, true, stream);
 }
 
 static int sparse_mla_fp8_layer(const char* what, const void* q, const void* win_kv, const void* chunk_kv,

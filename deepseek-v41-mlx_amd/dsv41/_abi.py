@@ -77,6 +77,8 @@ _SIGNATURES = {
                          _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_sparse_mla_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
                                 _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla_decode_noalloc": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
+                                        _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p],
     "dsv41_sparse_mla_fp8": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _i64, _i32, _c_p, _c_p, _i32,
                              _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p,
                              _sz, _c_p],

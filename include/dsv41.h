@@ -343,6 +343,22 @@ int dsv41_sparse_mla_decode(const void* q, void* win_kv, const void* chunk_kv,
                             float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
                             int32_t dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* dsv41_sparse_mla_decode without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference: its sparse_attn allocates its output and scratch per call.
+ * Same arguments, result and ring write as dsv41_sparse_mla_decode. The split partials live in a
+ * static 32 MiB device array inside the library, one per GPU, held until the process ends; a
+ * shape whose split scratch (dsv41_sparse_mla_workspace_bytes) exceeds 32 MiB returns
+ * DSV41_E_WORKSPACE before any launch. Nothing is allocated or freed. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (different streams, no ordering between them)
+ * race; calls ordered on one stream are safe (each call writes every partial it reads). */
+int dsv41_sparse_mla_decode_noalloc(const void* q, void* win_kv, const void* chunk_kv,
+                                    const void* comp_kv, int64_t comp_bstride, int32_t n_comp,
+                                    const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
+                                    int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
+                                    float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                                    int32_t dtype, hipStream_t stream);
+
 /* dsv41_sparse_mla with the compressed source stored as fp8: the packed, lossless form of the
  * QAT values that attention.py:157-163 writes into the cache (e4m3 code times a power-of-two
  * block scale, the ue8m0 convention of fakequant.py:83-93). comp_kv holds e4m3fn bytes
