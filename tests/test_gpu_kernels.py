@@ -787,3 +787,45 @@ def test_wrappers_refuse_bad_buffers_before_launch(gpu):
     o = _abi.sparse_mla(*args, out=torch.empty_like(q))
     torch.cuda.synchronize()
     assert torch.isfinite(o.float()).all()
+
+
+def test_sparse_mla_rows_on_both_sides_of_a_2gib_address_boundary(gpu):
+    """Regression test of a GPU memory fault met while the decode kernel was written: a 64-bit row
+    address is carried across lanes as two 32-bit halves (readlane) and rebuilt; the low half must
+    be zero-extended (lane_u64, sparse_mla.hip). Sign-extending it turned every row whose low
+    address word had bit 31 set into a wild address. Here the compressed cache is placed across a
+    multiple of 2 GiB inside one allocation, so its rows' low words have bit 31 both set and clear,
+    and the selected rows come from both sides."""
+    from dsv41 import _abi
+    from dsv41.layers import precompute_freqs_cis
+    b, H, D, W, nb, K, start, rd = 1, 64, 512, 128, 8192, 512, 32767, 64
+    row = D * 2
+    big = torch.empty((1 << 31) + (16 << 20), dtype=torch.uint8, device=gpu)
+    base = big.data_ptr()
+    off = ((1 << 31) - base % (1 << 31) - nb * row // 2) % (1 << 31)   # the boundary at the cache's midpoint
+    comp = big[off:off + nb * row].view(torch.bfloat16).view(b, nb, D)
+    cross = ((base + off) // (1 << 31) + 1) * (1 << 31)
+    assert comp.data_ptr() < cross < comp.data_ptr() + nb * row and comp.data_ptr() % 16 == 0
+    g = torch.Generator(gpu).manual_seed(SEED_BASE + 31)
+    rn = lambda *s: torch.randn(*s, generator=g, device=gpu)   # noqa: E731
+    sc = 576 ** -0.5
+    comp.copy_((rn(b, nb, D) * sc).bfloat16())
+    q, chunk, win, sink = (rn(b, 1, H, D) * sc).bfloat16(), (rn(b, 1, D) * sc).bfloat16(), \
+        (rn(b, W, D) * sc).bfloat16(), rn(H)
+    idx = _abi.topk_select(rn(b, 1, nb), K, start, 4, W + 1)
+    pos = idx[0, 0].long() - (W + 1)
+    first_after = (cross - comp.data_ptr()) // row
+    assert (pos < first_after).any() and (pos >= first_after).any()
+    cos, sin = precompute_freqs_cis(rd, start + 1, 65536, 160000.0, 16.0, 32, 1, device=gpu)
+    out = _abi.sparse_mla(q, win, chunk, comp, nb, sink, idx, D ** -0.5, W, start, cos, sin, rd)
+    torch.cuda.synchronize()
+    f = lambda x: x.float().cpu().numpy()   # noqa: E731
+    slots = (start - W + np.arange(W)) % W
+    kv_all = np.concatenate([f(win)[:, slots], f(chunk), f(comp)], axis=1)
+    widx = R.window_idx_matrix(W, 1, W)[None]
+    o = R.sparse_attn(f(q), kv_all, f(sink), np.concatenate([widx, f(idx).astype(np.int32)], -1), D ** -0.5,
+                      dtype="bf16")
+    rc, rs = R.precompute_freqs_cis(rd, start + 1, 65536, 160000.0, 16.0, 32, 1)
+    want = R.rope_tail(o, rd, rc[[start]], rs[[start]], inverse=True, dtype="bf16")
+    assert rel_max_diff(to_np(out), want) < 2e-2
+    del big
