@@ -449,6 +449,7 @@ def run_fp8_decode(args, torch, device):
             chunk=(torch.randn(B, 1, D, generator=g, device=device) * sc).to(bf),
             comp8=codes(g, B, nb, D), comp_sc=scales(g, B, nb // rb, D // 32),
             iq=(torch.randn(B, 1, Hi, Di, generator=g, device=device) * 0.3).to(bf),
+            iq_mx=(codes(g, B, 1, Hi, Di // 2), scales(g, B, 1, Hi, Di // 32)),
             ik8=codes(g, B, nb, Di), ik_sc=scales(g, B, nb // rb, Di // 32),
             w=torch.randn(B, 1, Hi, generator=g, device=device).to(bf),
             sink=torch.randn(H, generator=g, device=device),
@@ -467,11 +468,16 @@ def run_fp8_decode(args, torch, device):
 
     def f_fused(d):
         # the step's scoring + selection: the fused form over the fp8 keys
-        sel = _abi.indexer_topk_fp8(d["iq"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, K, wp + 1,
-                                    out=d["fidx"], workspace=d["fws"])
+        sel = _abi.indexer_topk_mxq_fp8(d["iq_mx"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, K, wp + 1,
+                                        out=d["fidx"], workspace=d["fws"])
         assert sel is not None
 
     def f_idx(d):
+        # the index query in MXFP4 form against the fp8 keys: block-scaled fp4 x fp8 MFMA
+        _abi.indexer_score_mxq_fp8(d["iq_mx"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, out=d["scores"])
+
+    def f_idx_dq(d):
+        # the same scores with the keys dequantized to bf16 in-kernel (VALU) for the bf16 MFMA
         _abi.indexer_score_fp8(d["iq"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, out=d["scores"])
 
     def f_topk(d):
@@ -498,14 +504,15 @@ def run_fp8_decode(args, torch, device):
     step_ms = time_graph(g_full, reps, torch) / per
     kern, graphs = {}, [g_full]
     parts = (("indexer_topk", f_fused),) if fused_ok else ()
-    for name, fn in parts + (("indexer_score", f_idx), ("topk_select", f_topk), ("sparse_mla", f_sparse)):
+    for name, fn in parts + (("indexer_score", f_idx), ("indexer_score_dequant", f_idx_dq), ("topk_select", f_topk),
+                             ("sparse_mla", f_sparse)):
         gr = graph_of(fn, sets, torch)
         graphs.append(gr)
         gr.replay()
         kern[name] = time_graph(gr, reps, torch) / per
         log(f"[bench] fp8 {name} {kern[name] * 1e3:.2f} us")
     torch.cuda.synchronize()
-    b_idx = B * (nb * Di + (nb // rb) * (Di // 32) + Hi * Di * 2 + Hi * 2 + nb * 4)
+    b_idx = B * (nb * Di + (nb // rb) * (Di // 32) + Hi * (Di // 2 + Di // 32) + Hi * 2 + nb * 4)
     b_fused = b_idx - B * nb * 4 + B * K * 4           # keys, scales, q, w in; indices out
     b_topk = B * (nb * 4 + K * 4)
     b_sparse = B * (K * (D + D // 32) + (rows - K) * D * 2 + 2 * H * D * 2 + K * 4)
@@ -513,7 +520,8 @@ def run_fp8_decode(args, torch, device):
     log(f"[bench] fp8-cache decode step {step_ms * 1e3:.2f} us")
     return {
         "workload": "fp8-cache decode step: B=16, 131072-token context (nb=32768), top-1024; compressed KV and "
-                    "index keys e4m3 with ue8m0 32x32-block scales, dequantized in-kernel; window ring bf16",
+                    "index keys e4m3 with ue8m0 32x32-block scales; index query MXFP4, scored on the block-scaled "
+                    "fp4 x fp8 MFMA; compressed rows dequantized in-kernel for the bf16 attention; window ring bf16",
         "step_us": step_ms * 1e3, "tokens_per_s": B / (step_ms * 1e-3),
         "kernels_us": {k: v * 1e3 for k, v in kern.items()},
         "step_algorithmic_bytes": step_bytes,
@@ -546,9 +554,11 @@ def c4_step_bytes(a, B, start_pos, index_format="dense"):
     and the score write; top-k score reads and index writes; the candidate mask write and
     reads; the window / latent / key writes of this token."""
     H, D, Hi, Di, W, K = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim, a.window_size, a.index_topk
-    kb = {"mxfp4": Di // 2 + Di // 32, "fp8": Di + Di // 32}.get(index_format, Di * 2)   # per index key
-    qb = Di // 2 + Di // 32 if index_format == "mxfp4" else Di * 2   # per index-query head
-    cb = D + D // 32 if index_format == "fp8" else D * 2              # per compressed KV row
+    # per index key, per index-query head, per compressed KV row; the fp8 variant's scale bytes cover
+    # 32 x 32 blocks, i.e. 1/32 byte per 32 channels of a row
+    kb = {"mxfp4": Di // 2 + Di // 32, "fp8": Di + Di / 1024}.get(index_format, Di * 2)
+    qb = Di // 2 + Di // 32 if index_format in ("mxfp4", "fp8") else Di * 2
+    cb = D + D / 1024 if index_format == "fp8" else D * 2
     wp = min(start_pos, W)
     total = 0
     for l in range(a.n_layers):
@@ -573,7 +583,7 @@ def c4_step_bytes(a, B, start_pos, index_format="dense"):
         else:
             total += B * rows * D * 2
         total += B * 2 * H * D * 2                           # q, o
-    return total
+    return int(total)
 
 
 def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=512):
@@ -595,7 +605,7 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
     sc = 576 ** -0.5
     mx = index_format == "mxfp4"
     fp8 = index_format == "fp8"
-    cache = (ModelCache(a, B, start + 1, bf, device, cache_format="fp8") if fp8
+    cache = (ModelCache(a, B, start + 1, bf, device, cache_format="fp8", fp8_block_rows=32) if fp8
              else ModelCache(a, B, start + 1, bf, device, index_format))
 
     def rbytes(lo, hi, *shape):
@@ -623,7 +633,7 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
         x = dict(q=(rn(B, 1, H, D) * sc).to(bf), kv=(rn(B, 1, D) * sc).to(bf), sink=rn(H))
         if a.compress_ratio(l) and l in a.index_source_layers:
             x.update(w_raw=rn(B, 1, Hi).to(bf), w_scale=weight_scale(Hi, Di, bf))
-            if mx:
+            if mx or fp8:                    # the query in MXFP4 form (fp8 keys: the fp4 x fp8 MFMA)
                 x["index_q_mx"] = (rbytes(0, 256, B, 1, Hi, Di // 2), rbytes(123, 132, B, 1, Hi, Di // 32))
             else:
                 x["index_q"] = _abi.fq_fp4_ue8m0(rn(B, 1, Hi, Di).to(bf))
@@ -646,8 +656,9 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
     return {
         "workload": f"{name}: 40-layer attention-only decode step (kernels only), B={B}, {start + 1}-token context "
                     f"(nb={(start + 1) // 4}), ratio 4, top-{topk}; owners 2/8/14/20, index sources 2..36, candidate "
-                    f"source 20; " + ("fp8 caches (e4m3 + ue8m0 per 32 channels of each row) for compressed KV and "
-                                      "index keys, window ring bf16" if fp8 else f"index caches {index_format}"),
+                    f"source 20; " + ("fp8 caches (e4m3 + ue8m0 per 32x32 block) for compressed KV and index keys, "
+                                      "index queries MXFP4 (fp4 x fp8 MFMA scoring), window ring bf16" if fp8
+                                      else f"index caches {index_format}"),
         "step_ms": ms, "tokens_per_s": B / (ms * 1e-3), "steps": reps,
         "step_algorithmic_bytes": nbytes, "hbm_GBps_step": gbs, "hbm_frac_step": gbs / HBM_PEAK_GBS,
     }

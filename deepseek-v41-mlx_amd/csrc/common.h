@@ -56,6 +56,11 @@ template <> struct io<bf16_t> {
 };
 
 // 2**ceil(log2(r)) from IEEE bits (the TileLang fast_round_scale, kernel.py:22-37).
+// ue8m0 scale byte -> float 2^(e-127) (e = 0 is 2^-127, a subnormal; 255 is NaN).
+__device__ __forceinline__ float e8m0_to_float(uint32_t e) {
+  return e == 0u ? __uint_as_float(0x00400000u) : (e == 255u ? __uint_as_float(0x7fc00000u) : __uint_as_float(e << 23));
+}
+
 __device__ __forceinline__ float pow2_ceil_log2(float r) {
   uint32_t b = __float_as_uint(r);
   int e = (int)((b >> 23) & 0xFFu) - 127 + ((b & 0x7FFFFFu) != 0u);

@@ -395,23 +395,47 @@ __device__ __forceinline__ f32x4 mfma_mxfp4(uint4 a, int sa, uint4 b, int sb) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, f32x4{0.f, 0.f, 0.f, 0.f}, 4, 4, 0, sa, 0, sb);
 }
 
-template <int U> struct MxBatch {
-  uint4 k[U];
+// fp8 keys: an fp4 e2m1 query (A, cbsz = 4) against e4m3 keys (B, blgp = 0). With 8-bit
+// operands the 16x16x128 instruction takes a lane group's 32 bytes as two 16-channel halves:
+// lane group g supplies channels [16g, 16g+16) in bytes 0-15 and [64+16g, 64+16g+16) in bytes
+// 16-31 (a one-wave probe on the box pinned this against a float64 reference), while its scale
+// byte is that of channel block g, like the fp4 operand's contiguous 32 channels. Products are
+// exact; the probe measured the instruction's sums within 3e-5 of max|D| of the exact sum (a
+// float32 channel-order sum of the same products was exact), so these scores are close to, not
+// bit-equal with, the dequantizing kernel's.
+__device__ __forceinline__ f32x4 mfma_q4_k8(uint4 a, int sa, uint4 b0, uint4 b1, int sb) {
+  const i32x8 av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+  const i32x8 bv = {(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, f32x4{0.f, 0.f, 0.f, 0.f}, 4, 0, 0, sa, 0, sb);
+}
+
+// 16 code bytes as a vector value: loads through it stay in registers (a struct copy of uint4
+// from memory can leave the batch in private memory)
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+__device__ __forceinline__ u32x4 ld_u32x4(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ uint4 as_uint4(u32x4 v) { return make_uint4(v[0], v[1], v[2], v[3]); }
+
+template <int U, bool KF8> struct MxBatch {
+  u32x4 k[U];
+  u32x4 k2[KF8 ? U : 1];                   // fp8 keys: the lane's second 16 code bytes
   uint32_t sc[U];
   uint32_t cf[U];
 };
 
 constexpr int kMxThreads = 512;  // 8 waves
 
-template <int HT, int TJ>
+// KF8: the keys are fp8 e4m3 rows (128 code bytes) whose ue8m0 scale word (one byte per 32
+// channels) covers 2^ks_shift rows (1 or 32); the query stays MXFP4.
+template <int HT, int TJ, bool KF8>
 __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
     const uint8_t* __restrict__ qcodes, const uint8_t* __restrict__ qscales, const bf16_t* __restrict__ w_raw,
     float w_scale,
     const uint8_t* __restrict__ kcodes, int64_t kc_bstride, const uint8_t* __restrict__ kscales, int64_t ks_bstride,
-    const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int nb, int start_pos, int ratio,
-    int rows_per_wg, int topk, uint32_t* __restrict__ ckey, int32_t* __restrict__ cpos) {
+    int ks_shift, const uint8_t* __restrict__ cand, float* __restrict__ scores, int n, int nb, int start_pos,
+    int ratio, int rows_per_wg, int topk, uint32_t* __restrict__ ckey, int32_t* __restrict__ cpos) {
   constexpr int H = HT * 16;
   constexpr int DIM = 128;
+  constexpr int KROW = KF8 ? DIM : DIM / 2;         // code bytes per key row
   // TJ > 0 (the fused top-k form): the range's scores collect in LDS and the workgroup keeps the
   // best min(topk, rows) as (order key, position) in position order, as indexer_decode_kernel does
   __shared__ float sc_lds[TJ > 0 ? TJ * kMxThreads : 1];
@@ -440,21 +464,22 @@ __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
     return;
   }
 
-  // lane (l16, g) of a tile loads row l16's 32-channel block g: 16 code bytes and its scale
+  // lane (l16, g) of a tile loads row l16's code bytes of block g (fp4: channels [32g, 32g+32);
+  // fp8: [16g, 16g+16) and [64+16g, 64+16g+16), the instruction's 8-bit layout) and the scale word
   const uint8_t* kcb = kcodes + (int64_t)b * kc_bstride + g * 16;
   const uint8_t* ksb = kscales + (int64_t)b * ks_bstride;
   const uint8_t* cb = cand ? cand + (int64_t)qi * nb : nullptr;
   constexpr int NW = kMxThreads / 64;
   constexpr int U = 4;
-  constexpr int NBUF = 2;
   constexpr int STRIDE = 16 * U * NW;
-  using Batch = MxBatch<U>;
+  using Batch = MxBatch<U, KF8>;
   auto load = [&](Batch& kk, int t0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int row = min(t0 + 16 * u + l16, vis_end - 1);   // clamp: loads stay inside the cache
-      kk.k[u] = *reinterpret_cast<const uint4*>(kcb + (int64_t)row * (DIM / 2));
-      kk.sc[u] = *reinterpret_cast<const uint32_t*>(ksb + (int64_t)row * (DIM / 32));
+      kk.k[u] = ld_u32x4(kcb + (int64_t)row * KROW);
+      if constexpr (KF8) kk.k2[u] = ld_u32x4(kcb + (int64_t)row * KROW + 64);
+      kk.sc[u] = *reinterpret_cast<const uint32_t*>(ksb + (int64_t)(row >> ks_shift) * (DIM / 32));
       kk.cf[u] = cb ? (uint32_t)cb[row] : 1u;
     }
   };
@@ -468,7 +493,9 @@ __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
       float part = 0.0f;
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) {
-        const f32x4 acc = mfma_mxfp4(qa[ht], qsa[ht], kk.k[u], sb);
+        f32x4 acc;
+        if constexpr (KF8) acc = mfma_q4_k8(qa[ht], qsa[ht], as_uint4(kk.k[u]), as_uint4(kk.k2[u]), sb);
+        else acc = mfma_mxfp4(qa[ht], qsa[ht], as_uint4(kk.k[u]), sb);
 #pragma unroll
         for (int i = 0; i < 4; ++i) part += relu_bits(acc[i]) * wv[ht][i];
       }
@@ -482,11 +509,10 @@ __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
     }
   };
   int t0 = r0 + 16 * U * wave;
-  // a ring of NBUF register batches: NBUF - 1 are in flight while one is computed; the first
-  // ones go out before the query operands are loaded
-  Batch buf[NBUF];
-#pragma unroll
-  for (int j = 0; j < NBUF - 1; ++j) load(buf[j], t0 + j * STRIDE);
+  // two register batches, named (not an array, which the compiler may keep in scratch memory):
+  // one is in flight while the other is computed; the first goes out before the query operands
+  Batch ba, bb;
+  load(ba, t0);
   // the query's A operands: lane (l16, g) of head tile ht holds head ht*16 + l16, block g
 #pragma unroll
   for (int ht = 0; ht < HT; ++ht) {
@@ -501,17 +527,14 @@ __global__ __launch_bounds__(kMxThreads) void indexer_score_mx_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) wv[ht][i] = round_bf16(bf2f(wrow[ht * 16 + 4 * g + i]) * w_scale);
   }
-  bool more = t0 < vis_end;                // wave-uniform
-  while (more) {
-#pragma unroll
-    for (int j = 0; j < NBUF; ++j) {
-      if (more) {
-        load(buf[(j + NBUF - 1) % NBUF], t0 + (NBUF - 1) * STRIDE);
-        compute(buf[j], t0);
-        t0 += STRIDE;
-        more = t0 < vis_end;
-      }
-    }
+  while (t0 < vis_end) {                   // wave-uniform
+    load(bb, t0 + STRIDE);
+    compute(ba, t0);
+    t0 += STRIDE;
+    if (t0 >= vis_end) break;
+    load(ba, t0 + STRIDE);
+    compute(bb, t0);
+    t0 += STRIDE;
   }
   if constexpr (TJ > 0) {
     __syncthreads();                       // every score of the range is in LDS
@@ -863,18 +886,23 @@ extern "C" int dsv41_indexer_score_fp8(const void* q, const void* w_raw, float w
   return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
 }
 
-extern "C" int dsv41_indexer_score_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
-                                         float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
-                                         const uint8_t* k_scales, int64_t ks_bstride, const uint8_t* candidates,
-                                         float* scores, int32_t bsz, int32_t n, int32_t heads, int32_t dim,
-                                         int32_t nb, int32_t start_pos, int32_t ratio, hipStream_t stream) {
-  const char* what = "dsv41_indexer_score_mxfp4";
+// Scoring with an MXFP4 query against MXFP4 keys (kf8 false) or fp8 e4m3 keys whose scale word
+// covers ks_rb rows (kf8 true). Strides in bytes.
+static int mx_score_entry(const char* what, bool kf8, const uint8_t* q_codes, const uint8_t* q_scales,
+                          const void* w_raw, float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                          const uint8_t* k_scales, int64_t ks_bstride, int ks_rb, const uint8_t* candidates,
+                          float* scores, int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
+                          int32_t start_pos, int32_t ratio, hipStream_t stream) {
   DSV41_REQUIRE(q_codes && q_scales && w_raw && k_codes && k_scales && scores, DSV41_E_ARG, "%s: null tensor", what);
   DSV41_REQUIRE(bsz >= 0 && n >= 0 && heads > 0 && nb >= 0 && start_pos >= 0 && ratio > 0, DSV41_E_ARG,
                 "%s: bad sizes", what);
-  DSV41_REQUIRE(dim == 128, DSV41_E_SHAPE, "%s: MXFP4 index keys support dim 128, got %d", what, dim);
-  DSV41_REQUIRE(kc_bstride >= (int64_t)nb * (dim / 2) && ks_bstride >= (int64_t)nb * (dim / 32), DSV41_E_ARG,
-                "%s: batch strides too small", what);
+  DSV41_REQUIRE(dim == 128, DSV41_E_SHAPE, "%s: MXFP4 queries and packed index keys support dim 128, got %d", what,
+                dim);
+  DSV41_REQUIRE(ks_rb == 1 || (kf8 && ks_rb == 32), DSV41_E_ARG, "%s: scale row block must be 1%s", what,
+                kf8 ? " or 32" : "");
+  const int64_t krow = kf8 ? dim : dim / 2;
+  DSV41_REQUIRE(kc_bstride >= (int64_t)nb * krow && ks_bstride >= (int64_t)((nb + ks_rb - 1) / ks_rb) * (dim / 32),
+                DSV41_E_ARG, "%s: batch strides too small", what);
   DSV41_REQUIRE((int64_t)bsz * n < 65536, DSV41_E_ARG, "%s: bsz*n must be < 65536", what);
   DSV41_REQUIRE(aligned16(q_codes) && aligned16(k_codes) && (reinterpret_cast<uintptr_t>(k_scales) & 3u) == 0,
                 DSV41_E_ARG, "%s: q_codes and k_codes must be 16-byte aligned, k_scales 4-byte aligned", what);
@@ -883,18 +911,39 @@ extern "C" int dsv41_indexer_score_mxfp4(const uint8_t* q_codes, const uint8_t* 
   if ((int64_t)bsz * n == 0 || nb == 0) return 0;
   int rows_per_wg = 0;
   const dim3 grid = idx_grid((int64_t)nb * bsz * n, nb, bsz * n, &rows_per_wg);
-#define DSV41_IDXMX_CASE(HT_)                                                                                 \
-  if (heads == HT_ * 16) {                                                                                    \
-    hipLaunchKernelGGL((indexer_score_mx_kernel<HT_, 0>), grid, dim3(kMxThreads), 0, stream, q_codes, q_scales, \
-                       (const bf16_t*)w_raw, w_scale, k_codes, kc_bstride, k_scales, ks_bstride, candidates,  \
-                       scores, n, nb, start_pos, ratio, rows_per_wg, 0, nullptr, nullptr);                    \
+  const int shift = ks_rb == 32 ? 5 : 0;
+#define DSV41_IDXMX_CASE(HT_, KF8_)                                                                           \
+  if (heads == HT_ * 16 && kf8 == KF8_) {                                                                     \
+    hipLaunchKernelGGL((indexer_score_mx_kernel<HT_, 0, KF8_>), grid, dim3(kMxThreads), 0, stream, q_codes,   \
+                       q_scales, (const bf16_t*)w_raw, w_scale, k_codes, kc_bstride, k_scales, ks_bstride,     \
+                       shift, candidates, scores, n, nb, start_pos, ratio, rows_per_wg, 0, nullptr, nullptr);  \
     return check_launch(what);                                                                                \
   }
-  DSV41_IDXMX_CASE(4)   // 64 heads
-  DSV41_IDXMX_CASE(2)   // 32 heads
-  DSV41_IDXMX_CASE(1)
+  DSV41_IDXMX_CASE(4, false) DSV41_IDXMX_CASE(2, false) DSV41_IDXMX_CASE(1, false)
+  DSV41_IDXMX_CASE(4, true) DSV41_IDXMX_CASE(2, true) DSV41_IDXMX_CASE(1, true)
 #undef DSV41_IDXMX_CASE
   return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
+}
+
+extern "C" int dsv41_indexer_score_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
+                                         float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                                         const uint8_t* k_scales, int64_t ks_bstride, const uint8_t* candidates,
+                                         float* scores, int32_t bsz, int32_t n, int32_t heads, int32_t dim,
+                                         int32_t nb, int32_t start_pos, int32_t ratio, hipStream_t stream) {
+  return mx_score_entry("dsv41_indexer_score_mxfp4", false, q_codes, q_scales, w_raw, w_scale, k_codes, kc_bstride,
+                        k_scales, ks_bstride, 1, candidates, scores, bsz, n, heads, dim, nb, start_pos, ratio,
+                        stream);
+}
+
+extern "C" int dsv41_indexer_score_mxq_fp8(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
+                                           float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                                           const uint8_t* k_scales, int64_t ks_bstride, int32_t ks_rb,
+                                           const uint8_t* candidates, float* scores, int32_t bsz, int32_t n,
+                                           int32_t heads, int32_t dim, int32_t nb, int32_t start_pos, int32_t ratio,
+                                           hipStream_t stream) {
+  return mx_score_entry("dsv41_indexer_score_mxq_fp8", true, q_codes, q_scales, w_raw, w_scale, k_codes, kc_bstride,
+                        k_scales, ks_bstride, ks_rb, candidates, scores, bsz, n, heads, dim, nb, start_pos, ratio,
+                        stream);
 }
 
 extern "C" size_t dsv41_indexer_topk_workspace_bytes(int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
@@ -997,19 +1046,22 @@ extern "C" int dsv41_indexer_topk_fp8(const void* q, const void* w_raw, float w_
                            ratio, offset, stream);
 }
 
-extern "C" int dsv41_indexer_topk_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
-                                        float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
-                                        const uint8_t* k_scales, int64_t ks_bstride, const uint8_t* candidates,
-                                        int32_t* out, int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
-                                        int32_t start_pos, int32_t ratio, int32_t topk, int32_t offset,
-                                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  const char* what = "dsv41_indexer_topk_mxfp4";
+static int mx_topk_entry(const char* what, bool kf8, const uint8_t* q_codes, const uint8_t* q_scales,
+                         const void* w_raw, float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                         const uint8_t* k_scales, int64_t ks_bstride, int ks_rb, const uint8_t* candidates,
+                         int32_t* out, int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
+                         int32_t start_pos, int32_t ratio, int32_t topk, int32_t offset, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
   DSV41_REQUIRE(q_codes && q_scales && w_raw && k_codes && k_scales && out, DSV41_E_ARG, "%s: null tensor", what);
   DSV41_REQUIRE(bsz >= 0 && n > 0 && heads > 0 && nb >= 0 && start_pos >= 0 && ratio > 0 && topk >= 0, DSV41_E_ARG,
                 "%s: bad sizes", what);
-  DSV41_REQUIRE(dim == 128, DSV41_E_SHAPE, "%s: MXFP4 index keys support dim 128, got %d", what, dim);
-  DSV41_REQUIRE(kc_bstride >= (int64_t)nb * (dim / 2) && ks_bstride >= (int64_t)nb * (dim / 32), DSV41_E_ARG,
-                "%s: batch strides too small", what);
+  DSV41_REQUIRE(dim == 128, DSV41_E_SHAPE, "%s: MXFP4 queries and packed index keys support dim 128, got %d", what,
+                dim);
+  DSV41_REQUIRE(ks_rb == 1 || (kf8 && ks_rb == 32), DSV41_E_ARG, "%s: scale row block must be 1%s", what,
+                kf8 ? " or 32" : "");
+  const int64_t krow = kf8 ? dim : dim / 2;
+  DSV41_REQUIRE(kc_bstride >= (int64_t)nb * krow && ks_bstride >= (int64_t)((nb + ks_rb - 1) / ks_rb) * (dim / 32),
+                DSV41_E_ARG, "%s: batch strides too small", what);
   DSV41_REQUIRE(aligned16(q_codes) && aligned16(k_codes) && (reinterpret_cast<uintptr_t>(k_scales) & 3u) == 0,
                 DSV41_E_ARG, "%s: q_codes and k_codes must be 16-byte aligned, k_scales 4-byte aligned", what);
   DSV41_REQUIRE(kc_bstride % 16 == 0 && ks_bstride % 4 == 0, DSV41_E_ARG,
@@ -1027,19 +1079,46 @@ extern "C" int dsv41_indexer_topk_mxfp4(const uint8_t* q_codes, const uint8_t* q
   DSV41_REQUIRE(aligned16(workspace), DSV41_E_ARG, "%s: workspace must be 16-byte aligned", what);
   uint32_t* ckey = reinterpret_cast<uint32_t*>(workspace);
   int32_t* cpos = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(workspace) + need / 2);
-#define DSV41_FUSEDMX_CASE(HT_, TJ_)                                                                           \
-  if (heads == HT_ * 16 && tj == TJ_) {                                                                        \
-    hipLaunchKernelGGL((indexer_score_mx_kernel<HT_, TJ_>), grid, dim3(kMxThreads), 0, stream, q_codes,        \
+  const int shift = ks_rb == 32 ? 5 : 0;
+#define DSV41_FUSEDMX_CASE(HT_, TJ_, KF8_)                                                                     \
+  if (heads == HT_ * 16 && tj == TJ_ && kf8 == KF8_) {                                                         \
+    hipLaunchKernelGGL((indexer_score_mx_kernel<HT_, TJ_, KF8_>), grid, dim3(kMxThreads), 0, stream, q_codes,  \
                        q_scales, (const bf16_t*)w_raw, w_scale, k_codes, kc_bstride, k_scales, ks_bstride,      \
-                       candidates, nullptr, n, nb, start_pos, ratio, rows_per_wg, k, ckey, cpos);             \
+                       shift, candidates, nullptr, n, nb, start_pos, ratio, rows_per_wg, k, ckey, cpos);      \
   } else
-  DSV41_FUSEDMX_CASE(4, 1) DSV41_FUSEDMX_CASE(4, 2) DSV41_FUSEDMX_CASE(4, 4) DSV41_FUSEDMX_CASE(4, 8)
-  DSV41_FUSEDMX_CASE(2, 1) DSV41_FUSEDMX_CASE(2, 2) DSV41_FUSEDMX_CASE(2, 4) DSV41_FUSEDMX_CASE(2, 8)
-  DSV41_FUSEDMX_CASE(1, 1) DSV41_FUSEDMX_CASE(1, 2) DSV41_FUSEDMX_CASE(1, 4) DSV41_FUSEDMX_CASE(1, 8)
+#define DSV41_FUSEDMX_HT(HT_, KF8_)                                                                            \
+  DSV41_FUSEDMX_CASE(HT_, 1, KF8_) DSV41_FUSEDMX_CASE(HT_, 2, KF8_) DSV41_FUSEDMX_CASE(HT_, 4, KF8_)           \
+  DSV41_FUSEDMX_CASE(HT_, 8, KF8_)
+  DSV41_FUSEDMX_HT(4, false) DSV41_FUSEDMX_HT(2, false) DSV41_FUSEDMX_HT(1, false)
+  DSV41_FUSEDMX_HT(4, true) DSV41_FUSEDMX_HT(2, true) DSV41_FUSEDMX_HT(1, true)
   return set_error(DSV41_E_SHAPE, "%s: no instance for heads=%d", what, heads);
+#undef DSV41_FUSEDMX_HT
 #undef DSV41_FUSEDMX_CASE
   const int rc = check_launch(what);
   if (rc) return rc;
   return topk_merge_launch(what, ckey, cpos, out, (int64_t)bsz * n, n, nb, k, (int)grid.x, rows_per_wg, start_pos,
                            ratio, offset, stream);
+}
+
+extern "C" int dsv41_indexer_topk_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
+                                        float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                                        const uint8_t* k_scales, int64_t ks_bstride, const uint8_t* candidates,
+                                        int32_t* out, int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
+                                        int32_t start_pos, int32_t ratio, int32_t topk, int32_t offset,
+                                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return mx_topk_entry("dsv41_indexer_topk_mxfp4", false, q_codes, q_scales, w_raw, w_scale, k_codes, kc_bstride,
+                       k_scales, ks_bstride, 1, candidates, out, bsz, n, heads, dim, nb, start_pos, ratio, topk,
+                       offset, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dsv41_indexer_topk_mxq_fp8(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
+                                          float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                                          const uint8_t* k_scales, int64_t ks_bstride, int32_t ks_rb,
+                                          const uint8_t* candidates, int32_t* out, int32_t bsz, int32_t n,
+                                          int32_t heads, int32_t dim, int32_t nb, int32_t start_pos, int32_t ratio,
+                                          int32_t topk, int32_t offset, void* workspace, size_t workspace_bytes,
+                                          hipStream_t stream) {
+  return mx_topk_entry("dsv41_indexer_topk_mxq_fp8", true, q_codes, q_scales, w_raw, w_scale, k_codes, kc_bstride,
+                       k_scales, ks_bstride, ks_rb, candidates, out, bsz, n, heads, dim, nb, start_pos, ratio, topk,
+                       offset, workspace, workspace_bytes, stream);
 }

@@ -149,11 +149,6 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
 // s - m <= the lazy-rescale threshold: results below 2^-126 are zero for the sum anyway.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// ue8m0 scale byte -> float 2^(e-127) (e = 0 is 2^-127, a subnormal; 255 is NaN).
-__device__ __forceinline__ float e8m0_to_float(uint32_t e) {
-  return e == 0u ? __uint_as_float(0x00400000u) : (e == 255u ? __uint_as_float(0x7fc00000u) : __uint_as_float(e << 23));
-}
-
 // 8 e4m3fn codes (two dwords) times a power-of-two scale -> MFMA operand. Exact: e4m3 values
 // scaled by 2^k are bf16-representable within bf16's exponent range. v_cvt_pk_f32_fp8 decodes
 // OCP e4m3fn on gfx950, subnormals included.

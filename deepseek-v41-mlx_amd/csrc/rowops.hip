@@ -33,6 +33,11 @@ struct RowArgs {
   // row and dst2 dim/32 scale bytes; all four strides in bytes
   uint8_t* dst2;
   int64_t dst2_bstride, dst2_tstride;
+  // FQ_FP8_PACK: one scale byte per 32 channels covers `srb` consecutive cache rows (1 or 32);
+  // with 32, a row that opens a block sets the block's scale and the block's later rows are
+  // quantized with it. Such a write runs in two launches: phase 0 the rows that open a block,
+  // phase 1 the others (which read the scales phase 0 or an earlier call stored).
+  int srb, phase;
 };
 
 // N (a multiple of 8) consecutive elements, 16-byte aligned
@@ -152,6 +157,7 @@ __global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
   const int c = rp.u / L, sub = rp.u - (rp.u / L) * L, h = rp.h, s = rp.s;
   const int e0 = c * 32 + sub * EPT;       // this thread's first element of the row
   if (row >= a.rows) return;  // whole rows leave together, so every lane group stays complete
+  if (FQ == FQ_FP8_PACK && a.srb > 1 && (((a.tok_base + s) % a.srb == 0) != (a.phase == 0))) return;
 
   // rope factors of this thread's pairs, requested before the row itself so the two loads
   // overlap (a pair ahead of the tail reads the first entry and is left unrotated)
@@ -217,7 +223,11 @@ __global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
     for (int i = 0; i < EPT; ++i) amax = fmaxf(amax, fabsf(v[i]));
     if constexpr (L > 1) amax = group_max(amax, L);
     amax = fmaxf(amax, 1e-4f);
-    const float sc = pow2_ceil_log2(amax * (float)(1.0 / 448.0));
+    const int crow = a.tok_base + s;         // the cache row written
+    uint8_t* sdst = a.dst2 + b * a.dst2_bstride + (int64_t)(a.srb > 1 ? crow / a.srb : crow) * a.dst2_tstride +
+                    (int64_t)h * (a.dim / 32) + c;
+    const bool opens = a.srb <= 1 || crow % a.srb == 0;
+    const float sc = opens ? pow2_ceil_log2(amax * (float)(1.0 / 448.0)) : e8m0_to_float(*sdst);
     const float inv = __fdiv_rn(1.0f, sc);   // exact: sc is a power of two
     uint32_t cw[EPT / 4];
 #pragma unroll
@@ -232,9 +242,7 @@ __global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
                     (int64_t)h * a.dim + e0;
 #pragma unroll
     for (int w = 0; w < EPT / 8; ++w) reinterpret_cast<uint2*>(cdst)[w] = make_uint2(cw[2 * w], cw[2 * w + 1]);
-    if (sub == 0)
-      a.dst2[b * a.dst2_bstride + (int64_t)(a.tok_base + s) * a.dst2_tstride + (int64_t)h * (a.dim / 32) + c] =
-          (uint8_t)((__float_as_uint(sc) >> 23) & 0xFFu);
+    if (sub == 0 && opens) *sdst = (uint8_t)((__float_as_uint(sc) >> 23) & 0xFFu);
     return;
   }
   if (FQ != FQ_NONE) {
@@ -544,49 +552,75 @@ extern "C" int dsv41_index_key_publish_mxfp4(const void* k_raw, uint8_t* k_codes
 }
 
 // Shared checks and set-up of the packed fp8 writers: codes [bsz, >=g0+g, dim] and scales
-// [bsz, >=g0+g, dim/32] bytes, batch strides in bytes, one scale per 32 channels of each row.
+// [bsz, >=ceil((g0+g)/scale_rb), dim/32] bytes, batch strides in bytes, one scale per 32 channels
+// of every scale_rb rows. With scale_rb = 32 a row that opens a 32-row block sets the block's
+// scale and the block's later rows are rounded with it.
 static int fp8_rows(const char* what, const void* src, uint8_t* codes, int64_t c_bstride, uint8_t* scales,
-                    int64_t s_bstride, int32_t bsz, int32_t g, int32_t dim, int32_t rd, int32_t g0, int32_t ratio,
-                    bool norm, RowArgs* a) {
+                    int64_t s_bstride, int32_t scale_rb, int32_t bsz, int32_t g, int32_t dim, int32_t rd, int32_t g0,
+                    int32_t ratio, bool norm, RowArgs* a) {
   DSV41_REQUIRE(bsz >= 0 && g >= 0 && g0 >= 0 && ratio > 0, DSV41_E_ARG, "%s: bad sizes", what);
+  DSV41_REQUIRE(scale_rb == 1 || scale_rb == 32, DSV41_E_ARG, "%s: scale row block must be 1 or 32", what);
   int rc = check_rows(what, src, codes, (int64_t)bsz * g, dim, norm);
   if (rc) return rc;
   DSV41_REQUIRE(scales, DSV41_E_ARG, "%s: null scale cache", what);
-  DSV41_REQUIRE(c_bstride >= (int64_t)(g0 + g) * dim && s_bstride >= (int64_t)(g0 + g) * (dim / 32), DSV41_E_ARG,
-                "%s: cache too small", what);
+  DSV41_REQUIRE(c_bstride >= (int64_t)(g0 + g) * dim &&
+                    s_bstride >= (int64_t)((g0 + g + scale_rb - 1) / scale_rb) * (dim / 32),
+                DSV41_E_ARG, "%s: cache too small", what);
   DSV41_REQUIRE(c_bstride % 16 == 0, DSV41_E_ARG, "%s: code batch stride must be a multiple of 16 bytes", what);
   DSV41_REQUIRE(rd > 0 && rd % 2 == 0 && rd <= dim, DSV41_E_SHAPE, "%s: bad rd %d", what, rd);
   a->src = src; a->dst = codes; a->rows = (int64_t)bsz * g; a->dim = dim; a->cpr = dim / 32;
   a->S = g; a->H = 1; a->dst_bstride = c_bstride; a->dst_tstride = dim; a->tok_base = g0;
-  a->dst2 = scales; a->dst2_bstride = s_bstride; a->dst2_tstride = dim / 32;
+  a->dst2 = scales; a->dst2_bstride = s_bstride; a->dst2_tstride = dim / 32; a->srb = scale_rb;
   a->rd = rd; a->pos_base = g0 * ratio; a->pos_step = ratio;
   return 0;
 }
 
+// The packed fp8 store of rows [g0, g0+g): one launch with per-row scales; with 32-row scale
+// blocks the rows that open a block first (they set its scale), then the others.
+template <bool NORM>
+static int fp8_store(const char* what, RowArgs a, int32_t g0, int32_t g, int32_t dtype, hipStream_t stream) {
+  if (a.srb <= 1) return dispatch_rows<NORM, true, FQ_FP8_PACK, 32>(dtype, a, stream, what);
+  const int first_open = (g0 + a.srb - 1) / a.srb, last_open = (g0 + g - 1) / a.srb;   // blocks opened here
+  const int openers = g > 0 ? last_open - first_open + 1 : 0;
+  if (openers > 0) {
+    a.phase = 0;
+    const int rc = dispatch_rows<NORM, true, FQ_FP8_PACK, 32>(dtype, a, stream, what);
+    if (rc) return rc;
+  }
+  if (g > openers) {
+    a.phase = 1;
+    return dispatch_rows<NORM, true, FQ_FP8_PACK, 32>(dtype, a, stream, what);
+  }
+  return 0;
+}
+
 extern "C" int dsv41_comp_write_fp8(const void* latents, uint8_t* codes, int64_t c_bstride, uint8_t* scales,
-                                    int64_t s_bstride, const float* cos_tab, const float* sin_tab, int32_t bsz,
-                                    int32_t g, int32_t dim, int32_t rd, int32_t g0, int32_t ratio, int32_t dtype,
-                                    hipStream_t stream) {
+                                    int64_t s_bstride, int32_t scale_rb, const float* cos_tab, const float* sin_tab,
+                                    int32_t bsz, int32_t g, int32_t dim, int32_t rd, int32_t g0, int32_t ratio,
+                                    int32_t dtype, hipStream_t stream) {
   const char* what = "dsv41_comp_write_fp8";
   RowArgs a{};
-  int rc = fp8_rows(what, latents, codes, c_bstride, scales, s_bstride, bsz, g, dim, rd, g0, ratio, false, &a);
+  int rc = fp8_rows(what, latents, codes, c_bstride, scales, s_bstride, scale_rb, bsz, g, dim, rd, g0, ratio, false,
+                    &a);
   if (rc) return rc;
   DSV41_REQUIRE(cos_tab && sin_tab, DSV41_E_ARG, "%s: null rope table", what);
   a.cos_tab = cos_tab; a.sin_tab = sin_tab;
-  return dispatch_rows<false, true, FQ_FP8_PACK, 32>(dtype, a, stream, what);
+  return fp8_store<false>(what, a, g0, g, dtype, stream);
 }
 
 extern "C" int dsv41_index_key_publish_fp8(const void* k_raw, uint8_t* codes, int64_t c_bstride, uint8_t* scales,
-                                           int64_t s_bstride, const float* norm_w, const float* cos_tab,
-                                           const float* sin_tab, int32_t bsz, int32_t g, int32_t dim, int32_t rd,
-                                           int32_t g0, int32_t ratio, float eps, int32_t dtype, hipStream_t stream) {
+                                           int64_t s_bstride, int32_t scale_rb, const float* norm_w,
+                                           const float* cos_tab, const float* sin_tab, int32_t bsz, int32_t g,
+                                           int32_t dim, int32_t rd, int32_t g0, int32_t ratio, float eps,
+                                           int32_t dtype, hipStream_t stream) {
   const char* what = "dsv41_index_key_publish_fp8";
   RowArgs a{};
-  int rc = fp8_rows(what, k_raw, codes, c_bstride, scales, s_bstride, bsz, g, dim, rd, g0, ratio, true, &a);
+  int rc = fp8_rows(what, k_raw, codes, c_bstride, scales, s_bstride, scale_rb, bsz, g, dim, rd, g0, ratio, true,
+                    &a);
   if (rc) return rc;
   DSV41_REQUIRE(norm_w && cos_tab && sin_tab, DSV41_E_ARG, "%s: null weight/table", what);
   a.norm_w = norm_w; a.eps = eps; a.cos_tab = cos_tab; a.sin_tab = sin_tab;
-  return dispatch_rows<true, true, FQ_FP8_PACK, 32>(dtype, a, stream, what);
+  return fp8_store<true>(what, a, g0, g, dtype, stream);
 }
 
 extern "C" int dsv41_index_q_prep_mxfp4(const void* q, uint8_t* q_codes, uint8_t* q_scales, const float* cos_tab,

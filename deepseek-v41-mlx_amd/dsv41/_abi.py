@@ -84,10 +84,14 @@ _SIGNATURES = {
                              _sz, _c_p],
     "dsv41_sparse_mla_fp8_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _i64, _i32, _c_p, _c_p, _i32,
                                     _c_p, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
-    "dsv41_comp_write_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-                             _c_p],
-    "dsv41_index_key_publish_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32,
-                                    _i32, _f32, _i32, _c_p],
+    "dsv41_comp_write_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32,
+                             _i32, _c_p],
+    "dsv41_index_key_publish_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32,
+                                    _i32, _i32, _f32, _i32, _c_p],
+    "dsv41_indexer_score_mxq_fp8": [_c_p, _c_p, _c_p, _f32, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32, _i32,
+                                    _i32, _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_indexer_topk_mxq_fp8": [_c_p, _c_p, _c_p, _f32, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32, _i32,
+                                   _i32, _i32, _i32, _i32, _i32, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_version": [],
     "dsv41_last_error_string": [],
 }
@@ -399,41 +403,46 @@ def index_key_publish(k_raw, index_k, g0, ratio, norm_w, cos, sin, rd, eps):
           _ptr(sin), b, g, d, rd, g0, ratio, float(eps), dtype_code(k_raw, name), _stream(k_raw))
 
 
-def _fp8_rows(name, src, codes, scales, g0):
+def _fp8_rows(name, src, codes, scales, g0, scale_rb=1):
     b, g, d = src.shape
+    if scale_rb not in (1, 32):
+        raise ValueError(f"{name}: scale_rb must be 1 or 32, got {scale_rb}")
     if codes.dtype != torch.uint8 or codes.shape[0] < b or codes.shape[2] != d or codes.shape[1] < g0 + g:
         raise ValueError(f"{name}: code cache {tuple(codes.shape)} cannot take groups {g0}..{g0 + g}")
-    if scales.dtype != torch.uint8 or scales.shape[0] < b or scales.shape[2] != d // 32 or scales.shape[1] < g0 + g:
+    nblk = -(-(g0 + g) // scale_rb)
+    if scales.dtype != torch.uint8 or scales.shape[0] < b or scales.shape[2] != d // 32 or scales.shape[1] < nblk:
         raise ValueError(f"{name}: scale cache {tuple(scales.shape)} cannot take groups {g0}..{g0 + g}")
     return b, g, d
 
 
-def comp_write_fp8(latents, codes, scales, g0, ratio, cos, sin, rd):
+def comp_write_fp8(latents, codes, scales, g0, ratio, cos, sin, rd, scale_rb=1):
     """comp_write into an fp8 cache: codes uint8 [b, >=g0+g, d] e4m3fn, scales uint8
-    [b, >=g0+g, d/32] ue8m0 (one per 32 channels of each row), values fq_fp8_ue8m0(rope(latent))."""
+    [b, >=ceil((g0+g)/scale_rb), d/32] ue8m0 (one per 32 channels of every scale_rb rows), values
+    fq_fp8_ue8m0(rope(latent)); with scale_rb 32 the row opening a block sets its scale, later rows
+    are rounded with it."""
     name = "dsv41_comp_write_fp8"
     _gpu(name, latents, codes, scales, cos, sin)
     _contig(name, latents)
     _tables(name, cos, sin, rd)
-    b, g, d = _fp8_rows(name, latents, codes, scales, g0)
+    b, g, d = _fp8_rows(name, latents, codes, scales, g0, scale_rb)
     if g and (g0 + g - 1) * ratio >= cos.shape[0]:
         raise ValueError(f"{name}: rope table too short")
-    _call(name, _ptr(latents), _ptr(codes), row_stride(codes, name), _ptr(scales), row_stride(scales, name), _ptr(cos),
-          _ptr(sin), b, g, d, rd, g0, ratio, dtype_code(latents, name), _stream(latents))
+    _call(name, _ptr(latents), _ptr(codes), row_stride(codes, name), _ptr(scales), row_stride(scales, name), scale_rb,
+          _ptr(cos), _ptr(sin), b, g, d, rd, g0, ratio, dtype_code(latents, name), _stream(latents))
 
 
-def index_key_publish_fp8(k_raw, codes, scales, g0, ratio, norm_w, cos, sin, rd, eps):
+def index_key_publish_fp8(k_raw, codes, scales, g0, ratio, norm_w, cos, sin, rd, eps, scale_rb=1):
     """index_key_publish into an fp8 index cache (layout of comp_write_fp8), values
     fq_fp8_ue8m0(rope(k_norm(k_raw)))."""
     name = "dsv41_index_key_publish_fp8"
     _gpu(name, k_raw, codes, scales, norm_w, cos, sin)
     _contig(name, k_raw)
     _tables(name, cos, sin, rd)
-    b, g, d = _fp8_rows(name, k_raw, codes, scales, g0)
+    b, g, d = _fp8_rows(name, k_raw, codes, scales, g0, scale_rb)
     _vec(name, "k_norm weight", norm_w, d)
     if g and (g0 + g - 1) * ratio >= cos.shape[0]:
         raise ValueError(f"{name}: rope table too short")
-    _call(name, _ptr(k_raw), _ptr(codes), row_stride(codes, name), _ptr(scales), row_stride(scales, name),
+    _call(name, _ptr(k_raw), _ptr(codes), row_stride(codes, name), _ptr(scales), row_stride(scales, name), scale_rb,
           _ptr(norm_w), _ptr(cos), _ptr(sin), b, g, d, rd, g0, ratio, float(eps), dtype_code(k_raw, name),
           _stream(k_raw))
 
@@ -665,6 +674,64 @@ def indexer_topk_mxfp4(q_mx, w_raw, w_scale, k_codes, k_scales, nb, start_pos, r
     _call(name, _ptr(q_codes), _ptr(q_scales), _ptr(w_raw), float(w_scale), _ptr(k_codes), row_stride(k_codes, name),
           _ptr(k_scales), row_stride(k_scales, name), _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio, topk,
           offset, _ptr(ws), ws_bytes, _stream(w_raw))
+    return out
+
+
+def _mxq_fp8_check(name, q_mx, w_raw, k_codes, k_scales, scale_rb, nb, candidates):
+    q_codes, q_scales = q_mx
+    _gpu(name, q_codes, q_scales, w_raw, k_codes, k_scales, candidates)
+    _contig(name, q_codes, q_scales, w_raw, candidates)
+    b, n, h, d2 = q_codes.shape
+    d = d2 * 2
+    if q_codes.dtype != torch.uint8 or d != 128 or q_scales.shape != (b, n, h, d // 32) or q_scales.dtype != torch.uint8:
+        raise ValueError(f"{name}: query must be uint8 codes [b, n, h, 64] with scales [b, n, h, 4]")
+    if w_raw.shape != (b, n, h) or w_raw.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: w_raw must be bf16 [{b}, {n}, {h}]")
+    if scale_rb not in (1, 32):
+        raise ValueError(f"{name}: scale_rb must be 1 or 32, got {scale_rb}")
+    if k_codes.dtype != torch.uint8 or k_codes.shape[0] < b or k_codes.shape[2] != d or k_codes.shape[1] < nb:
+        raise ValueError(f"{name}: fp8 keys {tuple(k_codes.shape)} {k_codes.dtype} do not match")
+    if (k_scales.dtype != torch.uint8 or k_scales.shape[0] < b or k_scales.shape[2] != d // 32
+            or k_scales.shape[1] < -(-nb // scale_rb)):
+        raise ValueError(f"{name}: key scales {tuple(k_scales.shape)} do not match")
+    if candidates is not None and (candidates.shape != (b, n, nb) or candidates.dtype not in (torch.uint8, torch.bool)):
+        raise ValueError(f"{name}: candidates must be bool/uint8 [{b}, {n}, {nb}]")
+    return q_codes, q_scales, b, n, h, d
+
+
+def indexer_score_mxq_fp8(q_mx, w_raw, w_scale, k_codes, k_scales, scale_rb, nb, start_pos, ratio, candidates=None,
+                          out=None):
+    """indexer_score with the query in MXFP4 form (codes uint8 [b,n,h,64], scales uint8 [b,n,h,4])
+    against fp8 keys: k_codes uint8 [b, >=nb, 128] e4m3fn, k_scales uint8 [b, >=ceil(nb/scale_rb), 4]
+    ue8m0 (one per 32 channels of every scale_rb = 1 or 32 rows); block-scaled fp4 x fp8 MFMA."""
+    name = "dsv41_indexer_score_mxq_fp8"
+    q_codes, q_scales, b, n, h, d = _mxq_fp8_check(name, q_mx, w_raw, k_codes, k_scales, scale_rb, nb, candidates)
+    out = _out(name, out, (b, n, nb), torch.float32, w_raw.device)
+    cand = candidates.view(torch.uint8) if candidates is not None else None
+    _call(name, _ptr(q_codes), _ptr(q_scales), _ptr(w_raw), float(w_scale), _ptr(k_codes), row_stride(k_codes, name),
+          _ptr(k_scales), row_stride(k_scales, name), scale_rb, _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio,
+          _stream(w_raw))
+    return out
+
+
+def indexer_topk_mxq_fp8(q_mx, w_raw, w_scale, k_codes, k_scales, scale_rb, nb, start_pos, ratio, topk, offset,
+                         candidates=None, out=None, workspace=None):
+    """indexer_topk over an MXFP4 query and fp8 keys (the layouts of indexer_score_mxq_fp8): int32
+    [b, n, min(topk, nb)], bit-equal to topk_select(indexer_score_mxq_fp8(...)). Returns None when
+    the fused form does not serve the shape."""
+    name = "dsv41_indexer_topk_mxq_fp8"
+    q_codes, q_scales, b, n, h, d = _mxq_fp8_check(name, q_mx, w_raw, k_codes, k_scales, scale_rb, nb, candidates)
+    _gpu(name, out, workspace)
+    ws_bytes = indexer_topk_workspace_bytes(b, n, h, d, nb, topk, candidates is not None)
+    if ws_bytes == 0:
+        return None
+    k = min(topk, nb)
+    out = _out(name, out, (b, n, k), torch.int32, w_raw.device)
+    ws = _ws(name, workspace, ws_bytes, w_raw.device)
+    cand = candidates.view(torch.uint8) if candidates is not None else None
+    _call(name, _ptr(q_codes), _ptr(q_scales), _ptr(w_raw), float(w_scale), _ptr(k_codes), row_stride(k_codes, name),
+          _ptr(k_scales), row_stride(k_scales, name), scale_rb, _ptr(cand), _ptr(out), b, n, h, d, nb, start_pos, ratio,
+          topk, offset, _ptr(ws), ws_bytes, _stream(w_raw))
     return out
 
 

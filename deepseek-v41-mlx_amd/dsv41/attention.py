@@ -110,7 +110,7 @@ class Attention(torch.nn.Module):
         rd = self.rope_head_dim
         if lc.comp_kv8 is not None:           # fp8 cache variant: fp8 QAT, stored packed
             _abi.comp_write_fp8(latents.to(self.dtype).contiguous(), lc.comp_kv8, lc.comp_ks, g0, self.ratio, cos,
-                                sin, rd)
+                                sin, rd, lc.fp8_rb)
             return
         lat = latents.to(lc.dtype).contiguous()
         if fakequant.DISABLE:
@@ -172,7 +172,7 @@ class Attention(torch.nn.Module):
         sel = cidx if cidx is not None and cidx.shape[-1] else None
         rdo = 0 if self._break_rope_inverse else rd
         if comp is not None and comp.dtype == torch.uint8:      # the fp8 cache variant
-            o = _abi.sparse_mla_fp8(q, lc.win_kv, kv, comp, src.comp_ks[:bsz], 1, n_comp, sink, sel,
+            o = _abi.sparse_mla_fp8(q, lc.win_kv, kv, comp, src.comp_ks[:bsz], src.fp8_rb, n_comp, sink, sel,
                                     self.softmax_scale, self.window_size, start_pos, cos, sin, rdo, write_ring=decode)
         else:
             o = _abi.sparse_mla(q, lc.win_kv, kv, comp, n_comp, sink, sel, self.softmax_scale, self.window_size,

@@ -43,10 +43,11 @@ CACHE_FORMATS = ("dense", "fp8")
 
 class PackedKeys:
     """Index keys of a packed cache as the indexer takes them: kind "mxfp4" or "fp8", the code
-    and scale views of rows [:bsz, :n]."""
+    and scale views of rows [:bsz, :n], and the rows one scale byte covers (rb: 1, or 32 for an
+    fp8 cache of 32 x 32 blocks)."""
 
-    def __init__(self, kind: str, codes: torch.Tensor, scales: torch.Tensor):
-        self.kind, self.codes, self.scales = kind, codes, scales
+    def __init__(self, kind: str, codes: torch.Tensor, scales: torch.Tensor, rb: int = 1):
+        self.kind, self.codes, self.scales, self.rb = kind, codes, scales, rb
 
     @property
     def shape(self):
@@ -55,12 +56,17 @@ class PackedKeys:
 
 class LayerCache:
     def __init__(self, bsz: int, args: ModelArgs, layer_id: int, max_seq_len: int,
-                 dtype=torch.float32, device="cuda", index_format: str = "dense", cache_format: str = "dense"):
+                 dtype=torch.float32, device="cuda", index_format: str = "dense", cache_format: str = "dense",
+                 fp8_block_rows: int = 1):
         if index_format not in INDEX_FORMATS:
             raise ValueError(f"index_format must be one of {INDEX_FORMATS}, got {index_format!r}")
         if cache_format not in CACHE_FORMATS:
             raise ValueError(f"cache_format must be one of {CACHE_FORMATS}, got {cache_format!r}")
+        if fp8_block_rows not in (1, 32):
+            raise ValueError(f"fp8_block_rows must be 1 or 32, got {fp8_block_rows}")
         fp8 = cache_format == "fp8"
+        # fp8 caches: one ue8m0 scale byte per 32 channels of every fp8_rb rows (32: 32 x 32 blocks)
+        self.fp8_rb = fp8_block_rows if fp8 else 1
         self.window = args.window_size
         self.ratio = args.compress_ratio(layer_id)
         self.is_kv_source = layer_id in args.kv_source_layers
@@ -75,9 +81,10 @@ class LayerCache:
         if self.is_kv_source:
             n_comp = max_seq_len // self.ratio
             d = args.head_dim
+            n_blk = -(-n_comp // self.fp8_rb)
             if fp8:
                 self.comp_kv8 = torch.zeros(bsz, n_comp, d, dtype=torch.uint8, device=device)
-                self.comp_ks = torch.zeros(bsz, n_comp, d // 32, dtype=torch.uint8, device=device)
+                self.comp_ks = torch.zeros(bsz, n_blk, d // 32, dtype=torch.uint8, device=device)
             else:
                 self.comp_kv = torch.zeros(bsz, n_comp, d, dtype=dtype, device=device)
             if self.ratio > 1:
@@ -86,7 +93,7 @@ class LayerCache:
                 di = args.index_head_dim
                 if fp8:
                     self.index_k8 = torch.zeros(bsz, n_comp, di, dtype=torch.uint8, device=device)
-                    self.index_k8s = torch.zeros(bsz, n_comp, di // 32, dtype=torch.uint8, device=device)
+                    self.index_k8s = torch.zeros(bsz, n_blk, di // 32, dtype=torch.uint8, device=device)
                 elif index_format == "mxfp4":
                     self.index_k4 = torch.zeros(bsz, n_comp, di // 2, dtype=torch.uint8, device=device)
                     self.index_ks = torch.zeros(bsz, n_comp, di // 32, dtype=torch.uint8, device=device)
@@ -99,7 +106,7 @@ class LayerCache:
         if self.index_k4 is not None:
             return PackedKeys("mxfp4", self.index_k4[:bsz, :n], self.index_ks[:bsz, :n])
         if self.index_k8 is not None:
-            return PackedKeys("fp8", self.index_k8[:bsz, :n], self.index_k8s[:bsz, :n])
+            return PackedKeys("fp8", self.index_k8[:bsz, :n], self.index_k8s[:bsz, :-(-n // self.fp8_rb)], self.fp8_rb)
         return self.index_k[:bsz, :n]
 
     def window_chrono(self, pos: int) -> torch.Tensor:
@@ -116,10 +123,12 @@ class LayerCache:
 
 class ModelCache:
     def __init__(self, args: ModelArgs, bsz: int = 1, max_seq_len: int | None = None,
-                 dtype=torch.float32, device="cuda", index_format: str = "dense", cache_format: str = "dense"):
+                 dtype=torch.float32, device="cuda", index_format: str = "dense", cache_format: str = "dense",
+                 fp8_block_rows: int = 1):
         self.max_seq_len = max_seq_len or min(args.max_seq_len, 4096)
         self.offset = 0
-        self.layers = [LayerCache(bsz, args, i, self.max_seq_len, dtype, device, index_format, cache_format)
+        self.layers = [LayerCache(bsz, args, i, self.max_seq_len, dtype, device, index_format, cache_format,
+                                  fp8_block_rows)
                        for i in range(args.n_layers)]
         self.engram_ids = None
 

@@ -81,7 +81,7 @@ class Indexer(torch.nn.Module):
         k_raw = self.wk(latents).contiguous()
         if cache.index_k8 is not None:
             _abi.index_key_publish_fp8(k_raw, cache.index_k8, cache.index_k8s, g0, self.ratio, self.k_norm.weight,
-                                       cos, sin, rd, self.k_norm.eps)
+                                       cos, sin, rd, self.k_norm.eps, cache.fp8_rb)
             return
         if cache.index_k4 is not None:
             if fakequant.DISABLE:
@@ -129,11 +129,11 @@ class Indexer(torch.nn.Module):
                 _abi.index_q_prep(q, cos, sin, rd, start_pos)
             nb = index_k.codes.shape[1]
             if not self.is_candidate_source and q.dtype == torch.bfloat16:
-                idx = _abi.indexer_topk_fp8(q, w_raw, w_scale, index_k.codes, index_k.scales, 1, nb, start_pos,
+                idx = _abi.indexer_topk_fp8(q, w_raw, w_scale, index_k.codes, index_k.scales, index_k.rb, nb, start_pos,
                                             self.ratio, self.index_topk, offset, cand)
                 if idx is not None:
                     return idx
-            scores = _abi.indexer_score_fp8(q, w_raw, w_scale, index_k.codes, index_k.scales, 1, nb, start_pos,
+            scores = _abi.indexer_score_fp8(q, w_raw, w_scale, index_k.codes, index_k.scales, index_k.rb, nb, start_pos,
                                             self.ratio, cand)
         else:
             if fakequant.DISABLE:

@@ -40,8 +40,9 @@ class AttentionStack(torch.nn.Module):
         self._break_sharing = False
 
     def make_cache(self, bsz: int = 1, max_seq_len: int | None = None, index_format: str = "dense",
-                   cache_format: str = "dense") -> ModelCache:
-        return ModelCache(self.args, bsz, max_seq_len, self.dtype, self.device, index_format, cache_format)
+                   cache_format: str = "dense", fp8_block_rows: int = 1) -> ModelCache:
+        return ModelCache(self.args, bsz, max_seq_len, self.dtype, self.device, index_format, cache_format,
+                          fp8_block_rows)
 
     def forward(self, h: torch.Tensor, cache: ModelCache) -> torch.Tensor:
         """h [b, n, dim] continues the sequence at cache.offset; advances the cache."""

@@ -89,11 +89,13 @@ class StackDecodeStep:
     ``index_q_mx`` (its codes and scales from dsv41_index_q_prep_mxfp4) --, ``w_raw`` [b,1,Hi]
     and ``w_scale``; kv sources add ``latent`` [b,1,D] (pre-rope); key owners add ``k_raw``
     [b,1,Di] and ``k_norm`` [Di]. Caches may be dense, carry MXFP4 index keys, or be the fp8
-    variant (cache_format "fp8": fp8 compressed KV and index keys); each layer takes the kernels
-    that read and write its owners' format. On every key format, index sources other than the
-    candidate source score and select in the fused form (dsv41_indexer_topk(_fp8, _mxfp4))
-    where it serves the shape; the candidate source writes its scores for the block mask (kept in
-    ``candidates``).
+    variant (cache_format "fp8": fp8 compressed KV and index keys, with ue8m0 scales per 32
+    channels of each row or of 32-row blocks); each layer takes the kernels that read and write
+    its owners' format. Over fp8 keys an index source given ``index_q_mx`` scores on the
+    block-scaled fp4 x fp8 MFMA (dsv41_indexer_*_mxq_fp8), else it dequantizes the keys for the
+    bf16 MFMA. On every key format, index sources other than the candidate source score and
+    select in the fused form (dsv41_indexer_topk(_fp8, _mxfp4, _mxq_fp8)) where it serves the
+    shape; the candidate source writes its scores for the block mask (kept in ``candidates``).
     Outputs (``out`` per layer) and scratch are allocated once, so a step can be captured in
     a HIP graph.
     """
@@ -168,7 +170,8 @@ class StackDecodeStep:
                     if p.owns_k:
                         if emits and lc.index_k8 is not None:
                             _abi.index_key_publish_fp8(x["k_raw"], lc.index_k8, lc.index_k8s, nb - 1, p.ratio,
-                                                       x["k_norm"], p.cos, p.sin, a.rope_head_dim, a.norm_eps)
+                                                       x["k_norm"], p.cos, p.sin, a.rope_head_dim, a.norm_eps,
+                                                       lc.fp8_rb)
                         elif emits and lc.index_k4 is not None:
                             _abi.index_key_publish_mxfp4(x["k_raw"], lc.index_k4, lc.index_ks, nb - 1, p.ratio,
                                                          x["k_norm"], p.cos, p.sin, a.rope_head_dim, a.norm_eps)
@@ -188,9 +191,13 @@ class StackDecodeStep:
                         sel = _abi.indexer_topk_mxfp4(x["index_q_mx"], x["w_raw"], x["w_scale"], keys.codes,
                                                       keys.scales, nb, sp, p.ratio, a.index_topk, self.offset, c,
                                                       out=p.fused_idx, workspace=self.fused_ws)
+                    elif p.fused_idx is not None and kind == "fp8" and "index_q_mx" in x:
+                        sel = _abi.indexer_topk_mxq_fp8(x["index_q_mx"], x["w_raw"], x["w_scale"], keys.codes,
+                                                        keys.scales, keys.rb, nb, sp, p.ratio, a.index_topk,
+                                                        self.offset, c, out=p.fused_idx, workspace=self.fused_ws)
                     elif p.fused_idx is not None and kind == "fp8":
                         sel = _abi.indexer_topk_fp8(x["index_q"], x["w_raw"], x["w_scale"], keys.codes, keys.scales,
-                                                    1, nb, sp, p.ratio, a.index_topk, self.offset, c,
+                                                    keys.rb, nb, sp, p.ratio, a.index_topk, self.offset, c,
                                                     out=p.fused_idx, workspace=self.fused_ws)
                     if sel is not None:
                         topk = p.idx = sel
@@ -198,9 +205,12 @@ class StackDecodeStep:
                         if kind == "mxfp4":
                             _abi.indexer_score_mxfp4(x["index_q_mx"], x["w_raw"], x["w_scale"], keys.codes,
                                                      keys.scales, nb, sp, p.ratio, c, out=scores)
+                        elif kind == "fp8" and "index_q_mx" in x:
+                            _abi.indexer_score_mxq_fp8(x["index_q_mx"], x["w_raw"], x["w_scale"], keys.codes,
+                                                       keys.scales, keys.rb, nb, sp, p.ratio, c, out=scores)
                         elif kind == "fp8":
-                            _abi.indexer_score_fp8(x["index_q"], x["w_raw"], x["w_scale"], keys.codes, keys.scales, 1,
-                                                   nb, sp, p.ratio, c, out=scores)
+                            _abi.indexer_score_fp8(x["index_q"], x["w_raw"], x["w_scale"], keys.codes, keys.scales,
+                                                   keys.rb, nb, sp, p.ratio, c, out=scores)
                         else:
                             _abi.indexer_score(x["index_q"], x["w_raw"], x["w_scale"], keys, sp, p.ratio, c,
                                                out=scores)
@@ -210,15 +220,15 @@ class StackDecodeStep:
                         topk = p.idx = _abi.topk_select(scores, a.index_topk, sp, p.ratio, self.offset)
                 if p.kv_source and emits and lc.comp_kv8 is not None:
                     _abi.comp_write_fp8(x["latent"], lc.comp_kv8, lc.comp_ks, nb - 1, p.ratio, p.cos, p.sin,
-                                        a.rope_head_dim)
+                                        a.rope_head_dim, lc.fp8_rb)
                 elif p.kv_source and emits:
                     _abi.comp_write(x["latent"], lc.comp_kv, nb - 1, p.ratio, p.cos, p.sin, a.rope_head_dim)
                 comp, n_comp, idx = (kv_src.comp_kv8 if kv_src.comp_kv8 is not None else kv_src.comp_kv)[:b], nb, topk
             # attention + this token's ring write in one launch
             if comp is not None and comp.dtype == torch.uint8:
-                _abi.sparse_mla_fp8(x["q"], lc.win_kv, x["kv"], comp, kv_src.comp_ks[:b], 1, n_comp, x["sink"], idx,
-                                    self.scale, self.window, sp, p.cos, p.sin, a.rope_head_dim, out=p.out,
-                                    workspace=self.workspace, write_ring=True)
+                _abi.sparse_mla_fp8(x["q"], lc.win_kv, x["kv"], comp, kv_src.comp_ks[:b], kv_src.fp8_rb, n_comp,
+                                    x["sink"], idx, self.scale, self.window, sp, p.cos, p.sin, a.rope_head_dim,
+                                    out=p.out, workspace=self.workspace, write_ring=True)
             else:
                 _abi.sparse_mla(x["q"], lc.win_kv, x["kv"], comp, n_comp, x["sink"], idx, self.scale, self.window,
                                 sp, p.cos, p.sin, a.rope_head_dim, out=p.out, workspace=self.workspace,

@@ -144,17 +144,21 @@ int dsv41_index_key_publish(const void* k_raw, void* index_k, int64_t cache_bstr
  * the index-key publish (indexer.py:89-104) with the row's values -- rope(latent), resp.
  * rope(k_norm(k_raw)), in dtype -- quantized by fake_quant_fp8_ue8m0's formula
  * (fakequant.py:83-93) and stored packed: e4m3fn codes [bsz, >=g0+g, dim] and one ue8m0 scale
- * byte per 32 channels of each row [bsz, >=g0+g, dim/32] (the scale row block 1 of
- * dsv41_sparse_mla_fp8 / dsv41_indexer_score_fp8), batch strides in bytes. This replaces the
- * reference's fp4 QAT at these two stores; decoding gives fake_quant_fp8_ue8m0(value). */
+ * byte per 32 channels of every scale_rb rows [bsz, >=ceil((g0+g)/scale_rb), dim/32] (the
+ * layout of dsv41_sparse_mla_fp8 / dsv41_indexer_score_fp8), batch strides in bytes. This
+ * replaces the reference's fp4 QAT at these two stores. scale_rb = 1: decoding gives
+ * fake_quant_fp8_ue8m0(value). scale_rb = 32 (32 x 32 blocks): a row that opens a block
+ * (row % 32 == 0) sets the block's scale by that formula and the block's later rows, in this
+ * call or later ones, are rounded with it: e4m3(clip(value / scale, +-448)) * scale. */
 int dsv41_comp_write_fp8(const void* latents, uint8_t* codes, int64_t c_bstride, uint8_t* scales,
-                         int64_t s_bstride, const float* cos_tab, const float* sin_tab, int32_t bsz,
-                         int32_t g, int32_t dim, int32_t rd, int32_t g0, int32_t ratio, int32_t dtype,
-                         hipStream_t stream);
+                         int64_t s_bstride, int32_t scale_rb, const float* cos_tab, const float* sin_tab,
+                         int32_t bsz, int32_t g, int32_t dim, int32_t rd, int32_t g0, int32_t ratio,
+                         int32_t dtype, hipStream_t stream);
 int dsv41_index_key_publish_fp8(const void* k_raw, uint8_t* codes, int64_t c_bstride, uint8_t* scales,
-                                int64_t s_bstride, const float* norm_w, const float* cos_tab,
-                                const float* sin_tab, int32_t bsz, int32_t g, int32_t dim, int32_t rd,
-                                int32_t g0, int32_t ratio, float eps, int32_t dtype, hipStream_t stream);
+                                int64_t s_bstride, int32_t scale_rb, const float* norm_w,
+                                const float* cos_tab, const float* sin_tab, int32_t bsz, int32_t g,
+                                int32_t dim, int32_t rd, int32_t g0, int32_t ratio, float eps,
+                                int32_t dtype, hipStream_t stream);
 
 /* dsv41_index_key_publish into an MXFP4 index cache, the lossless packed form of the same
  * fake_quant_fp4_ue8m0 keys (indexer.py:100-104): per 32-channel block one ue8m0 scale byte
@@ -225,6 +229,20 @@ int dsv41_indexer_score_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, c
                               float* scores, int32_t bsz, int32_t n, int32_t heads, int32_t dim,
                               int32_t nb, int32_t start_pos, int32_t ratio, hipStream_t stream);
 
+/* dsv41_indexer_score with the query in MXFP4 form (dsv41_index_q_prep_mxfp4; the index query is
+ * fp4 fake-quantized by construction, indexer.py:119-121, so the form is lossless) against fp8
+ * e4m3 keys in the layout of dsv41_indexer_score_fp8 (ue8m0 scales per 32 channels of every
+ * ks_rb = 1 or 32 rows). Each 16-head x 16-key tile is one block-scaled MFMA over the 128
+ * channels with fp4 A and fp8 B operands (exact products, fp32 sums): the scores equal
+ * dsv41_indexer_score_fp8's up to fp32 summation order, without dequantizing the keys.
+ * Heads 16, 32 or 64; dim 128. */
+int dsv41_indexer_score_mxq_fp8(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
+                                float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                                const uint8_t* k_scales, int64_t ks_bstride, int32_t ks_rb,
+                                const uint8_t* candidates, float* scores, int32_t bsz, int32_t n,
+                                int32_t heads, int32_t dim, int32_t nb, int32_t start_pos, int32_t ratio,
+                                hipStream_t stream);
+
 /* Indexer scoring followed by top-k selection, fused for decode (deepseek_v41_mlx/indexer.py:
  * 115-144: the scores of dsv41_indexer_score, then the selection of dsv41_topk_select, with
  * identical results): the [bsz*n, nb] scores are never written -- each workgroup's row range
@@ -262,6 +280,17 @@ int dsv41_indexer_topk_mxfp4(const uint8_t* q_codes, const uint8_t* q_scales, co
                              int32_t* out, int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t nb,
                              int32_t start_pos, int32_t ratio, int32_t topk, int32_t offset,
                              void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* dsv41_indexer_topk with an MXFP4 query against fp8 keys (the layouts of
+ * dsv41_indexer_score_mxq_fp8): bit-equal to dsv41_indexer_score_mxq_fp8 followed by
+ * dsv41_topk_select. Served shapes and the workspace are dsv41_indexer_topk's. */
+int dsv41_indexer_topk_mxq_fp8(const uint8_t* q_codes, const uint8_t* q_scales, const void* w_raw,
+                               float w_scale, const uint8_t* k_codes, int64_t kc_bstride,
+                               const uint8_t* k_scales, int64_t ks_bstride, int32_t ks_rb,
+                               const uint8_t* candidates, int32_t* out, int32_t bsz, int32_t n,
+                               int32_t heads, int32_t dim, int32_t nb, int32_t start_pos, int32_t ratio,
+                               int32_t topk, int32_t offset, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream);
 
 /* Top-k selection, deepseek_v41_mlx/indexer.py:140-144: per row of scores [bsz*n, nb],
  * the k = min(topk, nb) best positions (ties -> lowest position; -0.0 == +0.0), sorted

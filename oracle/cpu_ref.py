@@ -16,6 +16,8 @@ reference repository root).
 Pinning status (what checks each function; see tests/test_oracle.py):
   * bf16/e4m3 rounding        -- torch's own casts over exhaustive grids (library routines)
   * e4m3 decode / fp8 cache   -- torch's float8_e4m3fn over all 256 codes; per-element loop
+  * fp8_block_rows            -- rb = 1 equals fq_fp8_ue8m0 row by row; rb = 32: block openers
+                                 equal fq_fp8_ue8m0, later rows torch's e4m3 cast at that scale
   * MXFP4 encode / decode     -- decode(encode(x)) == fq_fp4_ue8m0(x) bit for bit (signed zeros
                                  included) on the fake-quant known-answer inputs; every code's
                                  value against the e2m1 grid definition
@@ -171,6 +173,32 @@ def fq_fp8_ue8m0(x, block: int = 32, dtype: str = "f32") -> np.ndarray:
     s = pow2_ceil_log2(amax * FP8_MAX_INV)
     q = e4m3_round(np.clip(xb / s, -FP8_MAX, FP8_MAX)) * s
     return cast(q.reshape(shape), dtype)
+
+
+def fp8_block_rows(x, row0: int, rb: int, scales_in=None):
+    """The fp8 cache variant's stored values when one ue8m0 scale covers 32 channels of every rb
+    rows (rb = 1: fq_fp8_ue8m0 per row; rb = 32: 32 x 32 blocks). x [b, g, d] are the values
+    written at cache rows row0 .. row0+g-1. A row that opens a block (row % rb == 0) sets the
+    block's scale by fake_quant_fp8_ue8m0's formula (fakequant.py:83-93); the block's later rows
+    are rounded with it: e4m3(clip(v / s, +-448)) * s. scales_in [b, blocks, d/32] holds the
+    scales of blocks opened before row0 (as powers of two). Returns (values, block scales)."""
+    x = np.asarray(x, F32)
+    b, g, d = x.shape
+    nblk = -(-(row0 + g) // rb)
+    sc = np.zeros((b, nblk, d // 32), F32)
+    if scales_in is not None:
+        prev = np.asarray(scales_in, F32)[:, :nblk]
+        sc[:, :prev.shape[1]] = prev
+    out = np.empty_like(x)
+    for j in range(g):
+        r = row0 + j
+        xb = _blockify(x[:, j], 32)                                   # [b, d/32, 32]
+        if r % rb == 0:
+            amax = np.maximum(np.abs(xb).max(axis=-1), F32(1e-4))
+            sc[:, r // rb] = pow2_ceil_log2(amax * FP8_MAX_INV)
+        s = sc[:, r // rb][..., None]
+        out[:, j] = (e4m3_round(np.clip(xb / s, -FP8_MAX, FP8_MAX)) * s).reshape(b, d)
+    return out, sc
 
 
 def fq_fp4_ue8m0(x, block: int = 32, dtype: str = "f32") -> np.ndarray:

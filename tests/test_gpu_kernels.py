@@ -829,3 +829,115 @@ def test_sparse_mla_rows_on_both_sides_of_a_2gib_address_boundary(gpu):
     want = R.rope_tail(o, rd, rc[[start]], rs[[start]], inverse=True, dtype="bf16")
     assert rel_max_diff(to_np(out), want) < 2e-2
     del big
+
+
+# ------------------------------------------------------------------ fp8 caches in 32 x 32 blocks
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_fp8_writers_with_32_row_scale_blocks(gpu, dt):
+    """The fp8 writers with one scale per 32 channels of every 32 rows: a prefill of 70 rows
+    (blocks opened at rows 0, 32, 64: two launches, openers first), then single-row appends that
+    continue block 2 and open block 3. Every stored value equals the oracle's block-row store of
+    the GPU's own roped (and normed) values: bit-exact codes and scales."""
+    from dsv41 import _abi
+    rng = rng_for("w8b" + dt)
+    rc, rs = R.precompute_freqs_cis(64, 4096, 65536, 160000.0, 16.0, 32, 1)
+    b, d, di, r = 2, 512, 128, 4
+    cos, sin = dev(rc), dev(rs)
+    codes = torch.zeros(b, 128, d, dtype=torch.uint8, device=gpu)
+    scales = torch.zeros(b, 4, d // 32, dtype=torch.uint8, device=gpu)
+    kc = torch.zeros(b, 128, di, dtype=torch.uint8, device=gpu)
+    ks = torch.zeros(b, 4, di // 32, dtype=torch.uint8, device=gpu)
+    nw = dev((1 + 0.1 * rng.standard_normal(di)).astype(F32))
+    want_v, want_k, sc_v, sc_k = [], [], None, None
+    for g0, g in ((0, 70), (70, 1), (71, 1), (95, 1), (96, 1), (97, 1)):
+        lat = dev(R.cast(rng.standard_normal((b, g, d)).astype(F32) * (1 + g0 % 7), dt), dt)
+        kr = dev(R.cast(rng.standard_normal((b, g, di)).astype(F32), dt), dt)
+        _abi.comp_write_fp8(lat, codes, scales, g0, r, cos, sin, 64, scale_rb=32)
+        _abi.index_key_publish_fp8(kr, kc, ks, g0, r, nw, cos, sin, 64, 1e-20, scale_rb=32)
+        roped = to_np(_abi.rope_tail(lat, 64, cos, sin, g0 * r, r))
+        keyed = to_np(_abi.rope_tail(_abi.rmsnorm(kr, nw, 1e-20), 64, cos, sin, g0 * r, r))
+        v, sc_v = R.fp8_block_rows(roped, g0, 32, sc_v)
+        k, sc_k = R.fp8_block_rows(keyed, g0, 32, sc_k)
+        want_v.append(v)
+        want_k.append(k)
+    torch.cuda.synchronize()
+    written = list(range(72)) + [95, 96, 97]
+    got_v = R.dequant_fp8_cache(codes.cpu().numpy()[:, :98], scales.cpu().numpy(), 32)[:, written]
+    got_k = R.dequant_fp8_cache(kc.cpu().numpy()[:, :98], ks.cpu().numpy(), 32)[:, written]
+    assert np.array_equal(got_v, np.concatenate(want_v, 1))
+    assert np.array_equal(got_k, np.concatenate(want_k, 1))
+    # the stored scale bytes are the oracle's block scales; rows never written stay zero
+    assert np.array_equal(np.ldexp(1.0, scales.cpu().numpy().astype(np.int32) - 127).astype(F32), sc_v)
+    assert not codes[:, 72:95].any() and not codes[:, 98:].any()
+
+
+def _fp8_keys(g, b, rows, rb, device, pad=True):
+    codes = torch.randint(0, 256, (b, rows, 128), generator=g, device=device, dtype=torch.int32)
+    codes = torch.where((codes & 0x7F) == 0x7F, codes ^ 1, codes).to(torch.uint8)     # no NaN codes
+    nblk = -(-rows // rb)
+    scales = torch.randint(123, 132, (b, (nblk + 3) // 4 * 4 if pad else nblk, 4), generator=g, device=device,
+                           dtype=torch.int32).to(torch.uint8)
+    return codes, scales
+
+
+@pytest.mark.parametrize("b,n,h,nb,start,rb,use_cand", [
+    (16, 1, 64, 32768, 131071, 32, False),   # the fp8 decode line: bs16, 128K context, 32 x 32 blocks
+    (16, 1, 64, 32768, 131071, 1, False),    # per-row scales
+    (3, 5, 32, 1000, 3990, 1, True),         # causal rows, candidates
+    (2, 40, 16, 700, 2700, 32, False),       # prefill-sized, most rows visible
+])
+def test_indexer_score_mxq_fp8(gpu, b, n, h, nb, start, rb, use_cand):
+    """Block-scaled MFMA with the MXFP4 query (fp4) against fp8 keys: within 1e-4 max|S| of the
+    oracle on the decoded query and keys and of the dequantizing fp8 scorer (exact) on the same
+    values -- the instruction's sums carry a few 1e-5 of relative error."""
+    from dsv41 import _abi
+    from dsv41.indexer import weight_scale
+    g = torch.Generator(gpu).manual_seed(SEED_BASE + 48 + rb + n)
+    d, r = 128, 4
+    cos, sin = (t.to(gpu) for t in (torch.ones(start + n, 32), torch.zeros(start + n, 32)))   # identity rope
+    q_raw = (torch.randn(b, n, h, d, generator=g, device=gpu) * 0.7).bfloat16()
+    q_mx = _abi.index_q_prep_mxfp4(q_raw, cos, sin, 64, start)
+    q16 = _abi.index_q_prep(q_raw.clone(), cos, sin, 64, start)                             # the same values
+    w = torch.randn(b, n, h, generator=g, device=gpu).bfloat16()
+    codes, scales = _fp8_keys(g, b, nb + 3, rb, gpu)
+    cand = (torch.rand(b, n, nb, generator=g, device=gpu) < 0.7) if use_cand else None
+    ws = weight_scale(h, d, torch.bfloat16)
+    got = _abi.indexer_score_mxq_fp8(q_mx, w, ws, codes, scales, rb, nb, start, r, cand)
+    ref8 = _abi.indexer_score_fp8(q16, w, ws, codes, scales, rb, nb, start, r, cand)
+    torch.cuda.synchronize()
+    keys = R.dequant_fp8_cache(codes.cpu().numpy(), scales.cpu().numpy(), rb)[:, :nb]
+    wv = R.cast(to_np(w) * F32(ws), "bf16")
+    want = R.indexer_scores(R.mxfp4_decode(q_mx[0].cpu().numpy(), q_mx[1].cpu().numpy()), keys, wv, start, r,
+                            cand.cpu().numpy() if use_cand else None)
+    gv, g8 = to_np(got), to_np(ref8)
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isfinite(gv), fin) and np.array_equal(np.isfinite(g8), fin)
+    scale = max(np.abs(want[fin]).max(), 1.0)
+    err = np.abs(gv[fin] - want[fin]).max() / scale
+    print(f"[mxq_fp8] max |score - exact| / max|S| = {err:.2e}", flush=True)
+    assert err <= 1e-4
+    assert np.abs(g8[fin] - want[fin]).max() <= 1e-5 * scale           # the exact path
+    assert np.abs(gv[fin] - g8[fin]).max() <= 1e-4 * scale
+
+
+@pytest.mark.parametrize("b,n,h,nb,topk,start,rb,use_cand", [
+    (16, 1, 64, 32768, 1024, 131071, 32, False),   # the C5 layer shape: top-1024 of 32K entries
+    (16, 1, 64, 32768, 512, 131071, 32, True),     # a candidate-masked consumer
+    (8, 4, 16, 16384, 512, 20000, 1, False),       # causal rows, ranges past visibility
+])
+def test_indexer_topk_mxq_fp8_equals_two_calls(gpu, b, n, h, nb, topk, start, rb, use_cand):
+    from dsv41 import _abi
+    g = torch.Generator(gpu).manual_seed(SEED_BASE + 49)
+    q_mx = (torch.randint(0, 256, (b, n, h, 64), generator=g, device=gpu, dtype=torch.int32).to(torch.uint8),
+            torch.randint(120, 130, (b, n, h, 4), generator=g, device=gpu, dtype=torch.int32).to(torch.uint8))
+    w = torch.randn(b, n, h, generator=g, device=gpu).bfloat16()
+    codes, scales = _fp8_keys(g, b, nb, rb, gpu)
+    cand = (torch.rand(b, n, nb, generator=g, device=gpu) < 0.7) if use_cand else None
+    fused = _abi.indexer_topk_mxq_fp8(q_mx, w, 0.01, codes, scales, rb, nb, start, 4, topk, 129, cand)
+    if fused is None:                                    # k above a quarter of a range: two calls
+        assert _abi.indexer_topk_workspace_bytes(b, n, h, 128, nb, topk, use_cand) == 0
+        return
+    scores = _abi.indexer_score_mxq_fp8(q_mx, w, 0.01, codes, scales, rb, nb, start, 4, cand)
+    assert torch.equal(fused, _abi.topk_select(scores, topk, start, 4, 129))

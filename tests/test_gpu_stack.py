@@ -357,3 +357,92 @@ def test_cache_snapshot_restore_replays_a_decode_step(gpu, cache_format):
         if state is not None:
             assert torch.equal(lc.comp_state.kv_state, state[0]) and torch.equal(lc.comp_state.score_state,
                                                                                  state[1]), f"layer {l} state"
+
+
+# Scores of the block-scaled fp4 x fp8 MFMA against the exact scores: the instruction sums its
+# 128 exact products to a few 1e-5 of the result's magnitude (a one-wave probe on the box), so
+# the scores carry that error; the dequantizing fp8 scorer is exact.
+MXQ_FP8_TOL = 1e-4
+
+
+def c5_fill_cache(cache, gen):
+    """fp8 caches of 32 x 32 blocks: e4m3 codes uniform over the finite codes, ue8m0 block scales
+    2^U{-4..4} (bytes 123..131); window rings N(0,1)/sqrt(576) bf16."""
+    s = 576 ** -0.5
+    for lc in cache.layers:
+        lc.win_kv.copy_(torch.randn(lc.win_kv.shape, generator=gen, device=lc.win_kv.device) * s)
+        for codes, scales in ((lc.comp_kv8, lc.comp_ks), (lc.index_k8, lc.index_k8s)):
+            if codes is None:
+                continue
+            c = torch.randint(0, 256, codes.shape, generator=gen, device=codes.device, dtype=torch.int32)
+            codes.copy_(torch.where((c & 0x7F) == 0x7F, c ^ 1, c).to(torch.uint8))
+            scales.copy_(torch.randint(123, 132, scales.shape, generator=gen, device=scales.device,
+                                       dtype=torch.int32).to(torch.uint8))
+
+
+def test_c5_fp8_block_cache_full_size_sampled_rows(gpu):
+    """The fp8 40-layer decode step as the fp8 cache variant's configuration states it: batch 16,
+    131,072-token context (32,768 compressed entries), top-1,024, compressed KV and index keys as
+    e4m3 in 32 x 32 blocks with ue8m0 scales 2^-4..2^4, dequantized in-kernel; index queries in
+    MXFP4 form, scored on the block-scaled fp4 x fp8 MFMA. Sampled rows of a window-only layer,
+    the last index source (layer 36: its queries against layer 20's keys under layer 20's
+    candidate mask, which keeps 2,048 of 4,096 blocks) and a consumer (39) against the oracle on
+    the dequantized caches: scores within 1e-5 max|S|, top-k bit-exact given them, outputs 2e-2."""
+    from dsv41 import _abi
+    from dsv41.cache import ModelCache
+    from dsv41.step import StackDecodeStep
+    a = c4_args(index_topk=1024, max_seq_len=131072)
+    B, sp, r = 16, 131071, 4
+    gen = torch.Generator(device=gpu).manual_seed(SEED_BASE + 5)
+    cache = ModelCache(a, B, 131072, torch.bfloat16, gpu, cache_format="fp8", fp8_block_rows=32)
+    c5_fill_cache(cache, gen)
+    ins = c4_inputs(a, B, gen, gpu)
+    ident = (torch.ones(sp + 1, 32, device=gpu), torch.zeros(sp + 1, 32, device=gpu))
+    for l, x in enumerate(ins):
+        if "index_q" in x:                   # the same fp4 values in MXFP4 form
+            x["index_q_mx"] = _abi.index_q_prep_mxfp4(x["index_q"], *ident, 64, sp)
+    rows = (0, 9, 15)
+    layers = (0, 36, 39)
+    win_before = {(l, b): to_np(cache.layers[l].win_kv[b]) for l in layers for b in rows}
+    step = StackDecodeStep(a, B, sp, torch.bfloat16, gpu)
+    print("[c5] 40-layer fp8 step, B=16, nb=32768", flush=True)
+    outs = step(cache, ins)
+    torch.cuda.synchronize()
+    nb = (sp + 1) // r
+    lens = R.query_lens(sp, 1, r)
+    f = lambda t: t.float().cpu().numpy()   # noqa: E731
+    l20 = cache.layers[20]
+    assert l20.fp8_rb == 32 and step.candidates is not None
+    got_s = to_np(_abi.indexer_score_mxq_fp8(ins[36]["index_q_mx"], ins[36]["w_raw"], ins[36]["w_scale"],
+                                             l20.index_k8[:B], l20.index_k8s[:B], 32, nb, sp, r, step.candidates))
+    # layer 20's scores again (the same kernel on the same inputs gives the same bits): the block
+    # mask the step applied is the oracle's selection over them, bit for bit
+    got20 = to_np(_abi.indexer_score_mxq_fp8(ins[20]["index_q_mx"], ins[20]["w_raw"], ins[20]["w_scale"],
+                                             l20.index_k8[:B], l20.index_k8s[:B], 32, nb, sp, r))
+    cand_gpu = step.candidates.cpu().numpy()
+    idx36 = step.plan[36].idx.cpu().numpy()
+    for b in rows:
+        keys20 = R.dequant_fp8_cache(l20.index_k8[b:b + 1].cpu().numpy(), l20.index_k8s[b:b + 1].cpu().numpy(),
+                                     32)[:, :nb]
+        w20 = R.cast(f(ins[20]["w_raw"][b:b + 1]) * F32(ins[20]["w_scale"]), "bf16")
+        s20 = R.indexer_scores(f(ins[20]["index_q"][b:b + 1]), keys20, w20, sp, r)
+        assert np.abs(got20[b:b + 1] - s20).max() <= MXQ_FP8_TOL * np.abs(s20).max(), f"layer 20 scores row {b}"
+        cand = R.select_candidate_blocks(got20[b:b + 1], lens, a.candidate_topk_blocks, a.candidate_block_size)
+        assert np.array_equal(cand_gpu[b:b + 1], cand), f"candidate mask row {b}"
+        assert 0 < cand.mean() < 1                           # the mask is live
+        w36 = R.cast(f(ins[36]["w_raw"][b:b + 1]) * F32(ins[36]["w_scale"]), "bf16")
+        want = R.indexer_scores(f(ins[36]["index_q"][b:b + 1]), keys20, w36, sp, r, cand)
+        fin = np.isfinite(want)
+        assert np.array_equal(np.isfinite(got_s[b:b + 1]), fin), f"mask row {b}"
+        assert np.abs(got_s[b:b + 1][fin] - want[fin]).max() <= MXQ_FP8_TOL * np.abs(want[fin]).max(), \
+            f"scores row {b}"
+        want_i = R.topk_indices(got_s[b:b + 1], a.index_topk, lens, min(sp, a.window_size) + 1)
+        assert np.array_equal(idx36[b:b + 1], want_i), f"top-k row {b}"
+        comp20 = R.dequant_fp8_cache(l20.comp_kv8[b:b + 1].cpu().numpy(), l20.comp_ks[b:b + 1].cpu().numpy(),
+                                     32)[0, :nb]
+        for l in layers:
+            ratio = a.compress_ratio(l)
+            o = _oracle_layer_out(a, f(ins[l]["q"][b, 0]), win_before[(l, b)], f(ins[l]["kv"][b]),
+                                  comp20 if ratio else None, idx36[b, 0] if ratio else None, f(ins[l]["sink"]),
+                                  sp, ratio)
+            assert rel_max_diff(to_np(outs[l][b, 0]), o) < 2e-2, f"layer {l} row {b}"

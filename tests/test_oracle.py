@@ -67,6 +67,33 @@ def test_e4m3_decode_matches_torch_on_every_code():
     assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))   # bitwise, -0 included
 
 
+def test_fp8_block_rows_store():
+    """rb = 1 is fq_fp8_ue8m0 row by row. rb = 32: a row opening a block equals fq_fp8_ue8m0 of
+    that row; the block's later rows are torch's e4m3 cast of v / s (clipped to 448) times the
+    opener's scale, also when the block was opened by an earlier call (scales_in)."""
+    rng = np.random.default_rng(12)
+    b, g, d = 2, 70, 64
+    x = (rng.standard_normal((b, g, d)) * np.exp(rng.standard_normal((b, g, 1)))).astype(F32)
+    v1, _ = R.fp8_block_rows(x, 5, 1)
+    assert np.array_equal(v1, R.fq_fp8_ue8m0(x))
+    v32, sc = R.fp8_block_rows(x, 0, 32)
+    for r in range(g):
+        opener = r - r % 32
+        s = sc[:, r // 32][:, :, None]
+        assert np.array_equal(sc[:, r // 32], R.pow2_ceil_log2(
+            np.maximum(np.abs(x[:, opener].reshape(b, -1, 32)).max(-1), F32(1e-4)) * F32(1 / 448)))
+        want = (torch.from_numpy(np.clip(x[:, r].reshape(b, -1, 32) / s, -448, 448)).to(torch.float8_e4m3fn)
+                .float().numpy() * s).reshape(b, d)
+        assert np.array_equal(v32[:, r], want), r
+        if r % 32 == 0:
+            assert np.array_equal(v32[:, r], R.fq_fp8_ue8m0(x[:, r]))
+    # a continuation call: rows 70.. of block 2 (opened at row 64 by the first call)
+    y = rng.standard_normal((b, 3, d)).astype(F32)
+    v2, sc2 = R.fp8_block_rows(y, 70, 32, sc)
+    assert np.array_equal(sc2[:, 2], sc[:, 2])
+    assert np.array_equal(v2, R.fp8_block_rows(np.concatenate([x, y], 1), 0, 32)[0][:, 70:])
+
+
 def test_fp8_cache_dequant_per_element():
     rng = np.random.default_rng(11)
     b, rows, d = 2, 70, 64
