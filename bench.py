@@ -547,18 +547,19 @@ def c4_model_args(**over):
 
 
 def c4_step_bytes(a, B, start_pos, index_format="dense"):
-    """index_format "dense", "mxfp4" (packed index keys) or "fp8" (the fp8 cache variant:
-    e4m3 + ue8m0 per 32 channels for the compressed rows and the index keys)."""
-    """Algorithmic HBM bytes of one 40-layer decode step (bf16 caches): per layer the sparse
-    MLA gather (window + top-k rows), q and o; per index source the key stream, its queries
-    and the score write; top-k score reads and index writes; the candidate mask write and
-    reads; the window / latent / key writes of this token."""
+    """Algorithmic HBM bytes of one 40-layer decode step: per layer the sparse MLA gather
+    (window + top-k rows), q and o; per index source the key stream, its queries and the score
+    write; top-k score reads and index writes; the candidate mask write and reads; the window /
+    latent / key writes of this token. index_format: "dense" (bf16 caches), "mxfp4" (packed
+    index keys), "packed" (MXFP4 index keys and fp4 compressed rows, e2m1 + e4m3 per 16
+    channels) or "fp8" (the fp8 cache variant: e4m3 + ue8m0 per 32 x 32 block for the
+    compressed rows and the index keys)."""
     H, D, Hi, Di, W, K = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim, a.window_size, a.index_topk
     # per index key, per index-query head, per compressed KV row; the fp8 variant's scale bytes cover
     # 32 x 32 blocks, i.e. 1/32 byte per 32 channels of a row
-    kb = {"mxfp4": Di // 2 + Di // 32, "fp8": Di + Di / 1024}.get(index_format, Di * 2)
-    qb = Di // 2 + Di // 32 if index_format in ("mxfp4", "fp8") else Di * 2
-    cb = D + D / 1024 if index_format == "fp8" else D * 2
+    kb = {"mxfp4": Di // 2 + Di // 32, "packed": Di // 2 + Di // 32, "fp8": Di + Di / 1024}.get(index_format, Di * 2)
+    qb = Di // 2 + Di // 32 if index_format in ("mxfp4", "packed", "fp8") else Di * 2
+    cb = {"fp8": D + D / 1024, "packed": D // 2 + D // 16}.get(index_format, D * 2)
     wp = min(start_pos, W)
     total = 0
     for l in range(a.n_layers):
@@ -592,7 +593,9 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
     writes (the token completes a group), indexer + top-k at the 8 index sources (candidate
     blocks at layer 20, applied at 24-36), sparse MLA at every layer. Caches (about 5.7 GB)
     exceed the Infinity Cache, so one input set suffices. index_format "mxfp4": the index
-    caches and index queries in packed fp4 form (codes + ue8m0 scales, random valid bytes)."""
+    caches and index queries in packed fp4 form (codes + ue8m0 scales, random valid bytes);
+    "packed": those and the compressed KV as packed fp4 rows (e2m1 + e4m3 per 16 channels);
+    "fp8": the fp8 cache variant in 32 x 32 blocks."""
     from dsv41 import _abi
     from dsv41.cache import ModelCache
     from dsv41.indexer import weight_scale
@@ -603,10 +606,16 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
     log(f"[bench] 40-layer decode B={B} start_pos={start} top-{topk} index={index_format}")
     g = torch.Generator(device=device).manual_seed(SEED + 300)
     sc = 576 ** -0.5
-    mx = index_format == "mxfp4"
+    H, D, Hi, Di = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim
+    packed = index_format == "packed"
+    mx = index_format == "mxfp4" or packed
     fp8 = index_format == "fp8"
-    cache = (ModelCache(a, B, start + 1, bf, device, cache_format="fp8", fp8_block_rows=32) if fp8
-             else ModelCache(a, B, start + 1, bf, device, index_format))
+    if fp8:
+        cache = ModelCache(a, B, start + 1, bf, device, cache_format="fp8", fp8_block_rows=32)
+    elif packed:
+        cache = ModelCache(a, B, start + 1, bf, device, "mxfp4", cache_format="fp4")
+    else:
+        cache = ModelCache(a, B, start + 1, bf, device, index_format)
 
     def rbytes(lo, hi, *shape):
         return torch.randint(lo, hi, shape, generator=g, device=device, dtype=torch.int32).to(torch.uint8)
@@ -621,12 +630,14 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
         if lc.index_k4 is not None:
             lc.index_k4.copy_(rbytes(0, 256, *lc.index_k4.shape))
             lc.index_ks.copy_(rbytes(123, 132, *lc.index_ks.shape))
+        if lc.comp_kv4 is not None:                # e2m1 codes, e4m3 scales 2^-6 .. 2^-2
+            lc.comp_kv4[..., :D // 2].copy_(rbytes(0, 256, B, lc.comp_kv4.shape[1], D // 2))
+            lc.comp_kv4[..., D // 2:].copy_(rbytes(0x08, 0x28, B, lc.comp_kv4.shape[1], D // 16))
         for codes, scales in ((lc.comp_kv8, lc.comp_ks), (lc.index_k8, lc.index_k8s)):
             if codes is not None:                  # e4m3 codes without the two NaN patterns
                 c = rbytes(0, 256, *codes.shape)
                 codes.copy_(torch.where((c & 0x7F) == 0x7F, c ^ 1, c))
                 scales.copy_(rbytes(123, 132, *scales.shape))
-    H, D, Hi, Di = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim
     rn = lambda *shape: torch.randn(*shape, generator=g, device=device)   # noqa: E731
     ins = []
     for l in range(a.n_layers):
@@ -658,6 +669,8 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
                     f"(nb={(start + 1) // 4}), ratio 4, top-{topk}; owners 2/8/14/20, index sources 2..36, candidate "
                     f"source 20; " + ("fp8 caches (e4m3 + ue8m0 per 32x32 block) for compressed KV and index keys, "
                                       "index queries MXFP4 (fp4 x fp8 MFMA scoring), window ring bf16" if fp8
+                                      else "packed caches: compressed KV e2m1 + e4m3 per 16 channels (288 B/row), "
+                                      "index keys and queries MXFP4, window ring bf16" if packed
                                       else f"index caches {index_format}"),
         "step_ms": ms, "tokens_per_s": B / (ms * 1e-3), "steps": reps,
         "step_algorithmic_bytes": nbytes, "hbm_GBps_step": gbs, "hbm_frac_step": gbs / HBM_PEAK_GBS,
@@ -832,6 +845,11 @@ def main():
                 result["c4_stack_decode_mxfp4_index"] = run_c4(args, torch, device, "mxfp4")
             except Exception as e:
                 result["c4_stack_decode_mxfp4_index"] = {"error": repr(e)}
+            torch.cuda.empty_cache()
+            try:
+                result["c4_stack_decode_packed"] = run_c4(args, torch, device, "packed")
+            except Exception as e:
+                result["c4_stack_decode_packed"] = {"error": repr(e)}
             torch.cuda.empty_cache()
         if not args.no_fp8:
             try:

@@ -162,4 +162,19 @@ __device__ __forceinline__ bf16x8 dequant_e4m3x8(uint32_t lo, uint32_t hi, float
   return cvt_bf16x8(v);
 }
 
+// 8 e2m1 codes (one dword; channel 2p in the low nibble of byte p) times an e4m3 block scale ->
+// MFMA operand. Exact: an e2m1 value times an e4m3 value has at most 6 significant bits and lies
+// inside bf16's exponent range. The e2m1 value is built from its bits: magnitude code m gives 0,
+// 0.5 (m = 1) or 2^((m >> 1) - 1) * (1 + (m & 1) / 2).
+__device__ __forceinline__ bf16x8 dequant_e2m1x8(uint32_t codes, float scale) {
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t c = (codes >> (4 * i)) & 15u, m = c & 7u;
+    const uint32_t mag = m == 0u ? 0u : (m == 1u ? 0x3F000000u : (((126u + (m >> 1)) << 23) | ((m & 1u) << 22)));
+    v[i] = __uint_as_float(mag | ((c & 8u) << 28)) * scale;
+  }
+  return cvt_bf16x8(v);
+}
+
 }  // namespace dsv41

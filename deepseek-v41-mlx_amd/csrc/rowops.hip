@@ -13,8 +13,11 @@
 namespace dsv41 {
 
 // FQ_FP4_MX: the FQ_FP4_UE8M0 values stored packed (MXFP4 codes + ue8m0 scale bytes);
-// FQ_FP8_PACK: the FQ_FP8_UE8M0 values stored packed (e4m3fn codes + ue8m0 scale bytes)
-enum FqKind { FQ_NONE = 0, FQ_FP8_UE8M0 = 1, FQ_FP4_UE8M0 = 2, FQ_FP4_E4M3 = 3, FQ_FP4_MX = 4, FQ_FP8_PACK = 5 };
+// FQ_FP8_PACK: the FQ_FP8_UE8M0 values stored packed (e4m3fn codes + ue8m0 scale bytes);
+// FQ_FP4_E4M3_PACK: the FQ_FP4_E4M3 values stored packed, one row of dim/2 e2m1 code bytes then
+// dim/16 e4m3 scale bytes
+enum FqKind { FQ_NONE = 0, FQ_FP8_UE8M0 = 1, FQ_FP4_UE8M0 = 2, FQ_FP4_E4M3 = 3, FQ_FP4_MX = 4, FQ_FP8_PACK = 5,
+              FQ_FP4_E4M3_PACK = 6 };
 
 struct RowArgs {
   const void* src;          // [rows, dim] contiguous
@@ -243,6 +246,37 @@ __global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
 #pragma unroll
     for (int w = 0; w < EPT / 8; ++w) reinterpret_cast<uint2*>(cdst)[w] = make_uint2(cw[2 * w], cw[2 * w + 1]);
     if (sub == 0 && opens) *sdst = (uint8_t)((__float_as_uint(sc) >> 23) & 0xFFu);
+    return;
+  }
+  if (FQ == FQ_FP4_E4M3_PACK) {
+    // fake_quant_fp4_e4m3's scale and rounding (fake_quant_block, FQ_FP4_E4M3) per 16 values,
+    // stored as e2m1 codes (channel 2p in the low nibble of byte p) and the block's e4m3 scale
+    constexpr int NB = EPT < 16 ? EPT : 16;  // this thread's values of one block
+    uint8_t* rowp = reinterpret_cast<uint8_t*>(a.dst) + b * a.dst_bstride + (int64_t)(a.tok_base + s) * a.dst_tstride;
+    uint32_t cw[EPT / 8];
+#pragma unroll
+    for (int w = 0; w < EPT / 8; ++w) cw[w] = 0u;
+#pragma unroll
+    for (int b0 = 0; b0 < EPT; b0 += NB) {
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) amax = fmaxf(amax, fabsf(v[b0 + i]));
+      if constexpr (NB < 16) amax = group_max(amax, 16 / NB);
+      amax = fmaxf(amax, 0.01171875f);                           // 6 * 2^-9
+      const float sc = e4m3_round(__fdiv_rn(amax, 6.0f));
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const int e = b0 + i;
+        cw[e / 8] |= e2m1_code(fminf(fmaxf(__fdiv_rn(v[e], sc), -6.0f), 6.0f)) << (4 * (e % 8));
+      }
+      if (NB == 16 || sub % (16 / NB) == 0) rowp[a.dim / 2 + (e0 + b0) / 16] = e4m3_encode(sc);
+    }
+    if constexpr (EPT == 8) {
+      *reinterpret_cast<uint32_t*>(rowp + e0 / 2) = cw[0];
+    } else {
+#pragma unroll
+      for (int w = 0; w < EPT / 8; w += 2) *reinterpret_cast<uint2*>(rowp + e0 / 2 + 4 * w) = make_uint2(cw[w], cw[w + 1]);
+    }
     return;
   }
   if (FQ != FQ_NONE) {
@@ -489,6 +523,29 @@ extern "C" int dsv41_window_idx(int32_t* out, int32_t wp, int32_t n, int32_t win
   hipLaunchKernelGGL(window_idx_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, out, wp, n,
                      window, weff);
   return check_launch(what);
+}
+
+// The compressed-cache write (attention.py:157-163) stored packed: rope(latent), then
+// fake_quant_fp4_e4m3's e2m1 codes and e4m3 scales per 16 channels, one row of dim/2 + dim/16
+// bytes per group (codes first), cache_bstride bytes per batch row.
+extern "C" int dsv41_comp_write_fp4(const void* latents, uint8_t* comp_kv4, int64_t cache_bstride,
+                                    const float* cos_tab, const float* sin_tab, int32_t bsz, int32_t g, int32_t dim,
+                                    int32_t rd, int32_t g0, int32_t ratio, int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_comp_write_fp4";
+  DSV41_REQUIRE(bsz >= 0 && g >= 0 && g0 >= 0 && ratio > 0, DSV41_E_ARG, "%s: bad sizes", what);
+  int rc = check_rows(what, latents, comp_kv4, (int64_t)bsz * g, dim, false);
+  if (rc) return rc;
+  const int64_t row = dim / 2 + dim / 16;
+  DSV41_REQUIRE(cache_bstride >= (int64_t)(g0 + g) * row, DSV41_E_ARG, "%s: cache too small", what);
+  DSV41_REQUIRE(cache_bstride % 16 == 0 && row % 16 == 0, DSV41_E_ARG,
+                "%s: rows and the batch stride must be multiples of 16 bytes", what);
+  DSV41_REQUIRE(cos_tab && sin_tab, DSV41_E_ARG, "%s: null rope table", what);
+  DSV41_REQUIRE(rd > 0 && rd % 2 == 0 && rd <= dim, DSV41_E_SHAPE, "%s: bad rd %d", what, rd);
+  RowArgs a{};
+  a.src = latents; a.dst = comp_kv4; a.rows = (int64_t)bsz * g; a.dim = dim; a.cpr = dim / 32;
+  a.S = g; a.H = 1; a.dst_bstride = cache_bstride; a.dst_tstride = row; a.tok_base = g0;
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.pos_base = g0 * ratio; a.pos_step = ratio;
+  return dispatch_rows<false, true, FQ_FP4_E4M3_PACK, 16>(dtype, a, stream, what);
 }
 
 extern "C" int dsv41_comp_write(const void* latents, void* comp_kv, int64_t cache_bstride, const float* cos_tab,

@@ -214,14 +214,21 @@ struct MlaLds {
 // Register footprint per wave: Q^T slice D/DS/8 + accumulators D/DS/4 VGPRs.
 // (__launch_bounds__'s second argument asks for 2 waves per SIMD: a 256-register budget, which
 // keeps the accumulators in VGPRs instead of AGPR copies around every MFMA block.)
-// F8: the compressed cache is fp8 (e4m3 + ue8m0 block scales). Such a row and its scale bytes
-// arrive in the second half of its bf16 slot row ([D, 2D) data, [2D, 2D + D/32) scales -- the
-// row padding) with one copy instruction, so copy counts and waits are unchanged; after its own
+// CF: the compressed cache's format. kCompFp8: e4m3 rows + ue8m0 block scales; such a row and its
+// scale bytes arrive in the second half of its bf16 slot row ([D, 2D) data, [2D, 2D + D/32)
+// scales -- the row padding) with one copy instruction. kCompFp4: packed e2m1 rows with e4m3
+// scales per 16 channels (D/2 + D/16 bytes, codes first), which arrive at the end of the bf16
+// slot row, [2D - 9D/16, 2D). Either way copy counts and waits are unchanged; after its own
 // copies land, the issuing wave dequantizes the row in place to bf16, before the step barrier.
 // PAIR: the decode instance sized for two workgroups per CU (half the LDS: at most kPairList list
 // entries, a two-slot ring), so that two independent step pipelines share each CU.
-template <int D, int HT, int DS, bool F8, bool PAIR>
+constexpr int kCompBf16 = 0, kCompFp8 = 1, kCompFp4 = 2;
+
+template <int D, int HT, int DS, int CF, bool PAIR>
 __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
+  constexpr bool F8 = CF == kCompFp8, F4 = CF == kCompFp4;
+  constexpr int F4ROW = D / 2 + D / 16;         // packed fp4 row bytes
+  constexpr int F4OFF = 2 * D - F4ROW;          // where it lands in the bf16 slot row
   constexpr int NW = HT * DS, NT = 64 * NW;
   constexpr int ML = PAIR ? kPairList : kMaxList;
   constexpr int DSL = D / DS, KSS = DSL / 32, DTS = DSL / 16;
@@ -259,15 +266,17 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   auto entry_row = [&](int e) {                  // split entry -> row address (0 = masked)
     const int u = list_pos(S, b, a.m, qs, e < nw ? w0 + e : wc + k0 + (e - nw), wc);
     const int ci = u - S.wp - S.n_chunk;
-    // F8: a compressed-cache entry is encoded as (row << 1) | 1 and addressed at issue time
-    return (F8 && u >= 0 && ci >= 0 && ci < S.n_comp) ? (((uint64_t)ci << 1) | 1ull)
-                                                       : reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, u, D));
+    // packed compressed-cache entries are encoded as (row << 1) | 1 and addressed at issue time
+    return ((F8 || F4) && u >= 0 && ci >= 0 && ci < S.n_comp)
+               ? (((uint64_t)ci << 1) | 1ull)
+               : reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, u, D));
   };
-  static_assert(!F8 || D == 512, "fp8 cache rows: 512 channels (one copy instruction with their scales)");
+  static_assert(CF == kCompBf16 || D == 512, "packed cache rows: 512 channels (one copy instruction per row)");
 
   const int nsteps = (cnt + R - 1) / R;
   const uint32_t ring_base = lds_offset(ring);
-  const uint64_t comp8 = F8 ? reinterpret_cast<uint64_t>(S.comp) + (uint64_t)b * (uint64_t)S.comp_bstride : 0ull;
+  const uint64_t comp8 =
+      (F8 || F4) ? reinterpret_cast<uint64_t>(S.comp) + (uint64_t)b * (uint64_t)S.comp_bstride : 0ull;
   const uint64_t scal8 = F8 ? reinterpret_cast<uint64_t>(S.comp_scale) + (uint64_t)b * (uint64_t)S.comp_scale_bstride : 0ull;
   const int rbs = S.comp_scale_rb == 32 ? 5 : 0;   // scale row block (1 or 32) as a shift
   auto issue = [&](int t, bool direct) {
@@ -286,6 +295,10 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
         const uint64_t src = lane < D / 16 ? comp8 + ci * D + (uint64_t)lane * 16u
                                            : scal8 + (ci >> rbs) * (D / 32);
         if (lane <= D / 16) dma16_vaddr(src, dst + rr * RS + D);
+      } else if (F4 && (ent & 1ull)) {
+        // lanes 0..F4ROW/16-1: the row's codes and scales, one contiguous packed row
+        const uint64_t src = comp8 + (ent >> 1) * F4ROW + (uint64_t)lane * 16u;
+        if (lane < F4ROW / 16) dma16_vaddr(src, dst + rr * RS + F4OFF);
       } else {
         dma_row<D>(ent, dst + rr * RS, lane);
       }
@@ -348,6 +361,24 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
 #pragma unroll
       for (int rr = 0; rr < RPW; ++rr)
         if (has[rr]) *reinterpret_cast<bf16x8*>(sb + rr * RS + lane * 16) = dequant_e4m3x8(c8[rr].x, c8[rr].y, sc[rr]);
+    } else if constexpr (F4) {
+      // the same for packed fp4 rows: lane l's 8 channels are code bytes 4l..4l+3, their scale is
+      // e4m3 byte l/2 after the codes
+      uint8_t* sb = ring + (t % NS) * SLOT + wave * RPW * RS;
+      uint32_t c4[RPW];
+      float sc[RPW];
+      bool has[RPW];
+#pragma unroll
+      for (int rr = 0; rr < RPW; ++rr) {
+        const int ei = t * R + wave * RPW + rr;
+        has[rr] = ((ei < cnt ? rows[ei] : 0ull) & 1ull) != 0ull;
+        const uint8_t* row = sb + rr * RS + F4OFF;
+        c4[rr] = *reinterpret_cast<const uint32_t*>(row + lane * 4);
+        sc[rr] = __builtin_amdgcn_cvt_f32_fp8((int)row[D / 2 + (lane >> 1)], 0);
+      }
+#pragma unroll
+      for (int rr = 0; rr < RPW; ++rr)
+        if (has[rr]) *reinterpret_cast<bf16x8*>(sb + rr * RS + lane * 16) = dequant_e2m1x8(c4[rr], sc[rr]);
     }
     __syncthreads();                       // step t landed; every wave is done with step t-1
     const int slot = t % NS;
@@ -713,25 +744,26 @@ static size_t workspace_for(const MlaPlan& p, int64_t units, int heads, int dim)
 
 static bool bf16_dim_supported(int d) { return d == 64 || d == 128 || d == 256 || d == 512 || d == 576; }
 
-template <int D, bool F8>
+template <int D, int CF>
 static void launch_bf16_d(const MlaArgs& a, const MlaPlan& p, int64_t units, hipStream_t stream) {
   const unsigned wgs = (unsigned)(units * p.hgroups * p.splits);
   if constexpr (D <= 512) {                    // the planner pairs only rows of up to 512 channels
     if (p.pair && !p.wide) {
-      hipLaunchKernelGGL((mla_bf16_kernel<D, 2, 2, F8, true>), dim3(wgs), dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((mla_bf16_kernel<D, 2, 2, CF, true>), dim3(wgs), dim3(256), 0, stream, a);
       return;
     }
   }
   if (p.wide)
-    hipLaunchKernelGGL((mla_bf16_kernel<D, 4, 2, F8, false>), dim3(wgs), dim3(512), 0, stream, a);
+    hipLaunchKernelGGL((mla_bf16_kernel<D, 4, 2, CF, false>), dim3(wgs), dim3(512), 0, stream, a);
   else
-    hipLaunchKernelGGL((mla_bf16_kernel<D, 2, 2, F8, false>), dim3(wgs), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((mla_bf16_kernel<D, 2, 2, CF, false>), dim3(wgs), dim3(256), 0, stream, a);
 }
 
-// fp8_comp: the compressed source is an e4m3 cache with ue8m0 block scales (q, o and the other
-// sources are bf16; head_dim 512).
+// comp_format: kCompFp8, the compressed source is an e4m3 cache with ue8m0 block scales; kCompFp4,
+// packed e2m1 rows with e4m3 scales per 16 channels (q, o and the other sources are bf16; head_dim
+// 512).
 static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int dtype, void* workspace,
-                   size_t workspace_bytes, hipStream_t stream, bool fp8_comp = false) {
+                   size_t workspace_bytes, hipStream_t stream, int comp_format = kCompBf16) {
   if (units == 0) return 0;
   DSV41_REQUIRE(units < (1ll << 31), DSV41_E_ARG, "%s: too many queries", what);
   if (dtype == DSV41_F32) {
@@ -763,16 +795,17 @@ static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int
     a.part_o = reinterpret_cast<bf16_t*>(workspace);
     a.part_ml = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + align256(slots * a.dim * sizeof(bf16_t)));
   }
-  if (fp8_comp) {
-    DSV41_REQUIRE(a.dim == 512, DSV41_E_SHAPE, "%s: the fp8 cache path supports dim 512, got %d", what, a.dim);
-    launch_bf16_d<512, true>(a, p, units, stream);
+  if (comp_format != kCompBf16) {
+    DSV41_REQUIRE(a.dim == 512, DSV41_E_SHAPE, "%s: the packed cache paths support dim 512, got %d", what, a.dim);
+    if (comp_format == kCompFp8) launch_bf16_d<512, kCompFp8>(a, p, units, stream);
+    else launch_bf16_d<512, kCompFp4>(a, p, units, stream);
   } else {
     switch (a.dim) {
-      case 64: launch_bf16_d<64, false>(a, p, units, stream); break;
-      case 128: launch_bf16_d<128, false>(a, p, units, stream); break;
-      case 256: launch_bf16_d<256, false>(a, p, units, stream); break;
-      case 512: launch_bf16_d<512, false>(a, p, units, stream); break;
-      default: launch_bf16_d<576, false>(a, p, units, stream); break;
+      case 64: launch_bf16_d<64, kCompBf16>(a, p, units, stream); break;
+      case 128: launch_bf16_d<128, kCompBf16>(a, p, units, stream); break;
+      case 256: launch_bf16_d<256, kCompBf16>(a, p, units, stream); break;
+      case 512: launch_bf16_d<512, kCompBf16>(a, p, units, stream); break;
+      default: launch_bf16_d<576, kCompBf16>(a, p, units, stream); break;
     }
   }
   int rc = check_launch(what);
@@ -967,7 +1000,67 @@ static int sparse_mla_fp8_layer(const char* what, const void* q, const void* win
     a.ring_w = const_cast<void*>(win_kv);
   }
   const int weff = window < wp + n ? window : wp + n;
-  return run_mla(what, a, (int64_t)bsz * n, weff + k, DSV41_BF16, workspace, workspace_bytes, stream, true);
+  return run_mla(what, a, (int64_t)bsz * n, weff + k, DSV41_BF16, workspace, workspace_bytes, stream, kCompFp8);
+}
+
+// The compressed source as packed fp4 rows: e2m1 codes then e4m3 scales per 16 channels, 288 bytes
+// per 512-channel row, comp_bstride bytes per batch row.
+static int sparse_mla_fp4_layer(const char* what, const void* q, const void* win_kv, const void* chunk_kv,
+                                const uint8_t* comp_kv4, int64_t comp_bstride, int32_t n_comp, const float* sink,
+                                const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads,
+                                int32_t dim, int32_t window, int32_t start_pos, float scale, const float* cos_tab,
+                                const float* sin_tab, int32_t rd, void* workspace, size_t workspace_bytes,
+                                bool write_ring, hipStream_t stream) {
+  const int wp = start_pos < window ? start_pos : window;
+  DSV41_REQUIRE(q && chunk_kv && sink && o && (idx || k == 0) && (win_kv || wp == 0) && (comp_kv4 || n_comp == 0),
+                DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(bsz >= 0 && n >= 0 && heads > 0 && window > 0 && start_pos >= 0 && k >= 0 && n_comp >= 0,
+                DSV41_E_ARG, "%s: bad sizes", what);
+  DSV41_REQUIRE(dim == 512, DSV41_E_SHAPE, "%s: the packed fp4 cache path supports dim 512, got %d", what, dim);
+  const int64_t row = dim / 2 + dim / 16;
+  DSV41_REQUIRE(n_comp == 0 || comp_bstride >= (int64_t)n_comp * row, DSV41_E_ARG, "%s: comp_bstride too small", what);
+  DSV41_REQUIRE(aligned16(q) && aligned16(chunk_kv) && aligned16(o) && (!win_kv || aligned16(win_kv)) &&
+                    (!comp_kv4 || aligned16(comp_kv4)),
+                DSV41_E_ARG, "%s: tensors must be 16-byte aligned", what);
+  DSV41_REQUIRE(comp_bstride % 16 == 0, DSV41_E_ARG, "%s: comp_bstride must be a multiple of 16 bytes", what);
+  DSV41_REQUIRE(rd == 0 || (cos_tab && sin_tab && rd % 2 == 0 && rd <= dim), DSV41_E_ARG, "%s: bad rope tail", what);
+  MlaArgs a{};
+  a.q = q; a.o = o; a.sink = sink;
+  a.src.ring = win_kv; a.src.ring_bstride = (int64_t)window * dim; a.src.window = window; a.src.wp = wp;
+  a.src.ring_first = (start_pos - wp) % window;
+  a.src.chunk = chunk_kv; a.src.chunk_bstride = (int64_t)n * dim; a.src.n_chunk = n;
+  a.src.comp = comp_kv4; a.src.comp_bstride = comp_bstride; a.src.n_comp = n_comp;
+  a.src.idx = idx; a.src.k = k; a.src.win_implicit = 1;
+  a.m = n; a.heads = heads; a.dim = dim; a.scale = scale;
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.start_pos = start_pos;
+  if (write_ring) {
+    DSV41_REQUIRE(n == 1 && win_kv, DSV41_E_ARG, "%s: the ring store needs one token per row and a ring", what);
+    a.ring_w = const_cast<void*>(win_kv);
+  }
+  const int weff = window < wp + n ? window : wp + n;
+  return run_mla(what, a, (int64_t)bsz * n, weff + k, DSV41_BF16, workspace, workspace_bytes, stream, kCompFp4);
+}
+
+extern "C" int dsv41_sparse_mla_fp4(const void* q, const void* win_kv, const void* chunk_kv, const uint8_t* comp_kv4,
+                                    int64_t comp_bstride, int32_t n_comp, const float* sink, const int32_t* idx,
+                                    int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads, int32_t dim,
+                                    int32_t window, int32_t start_pos, float scale, const float* cos_tab,
+                                    const float* sin_tab, int32_t rd, void* workspace, size_t workspace_bytes,
+                                    hipStream_t stream) {
+  return sparse_mla_fp4_layer("dsv41_sparse_mla_fp4", q, win_kv, chunk_kv, comp_kv4, comp_bstride, n_comp, sink, idx,
+                              k, o, bsz, n, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, workspace,
+                              workspace_bytes, false, stream);
+}
+
+extern "C" int dsv41_sparse_mla_fp4_decode(const void* q, void* win_kv, const void* chunk_kv,
+                                           const uint8_t* comp_kv4, int64_t comp_bstride, int32_t n_comp,
+                                           const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
+                                           int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
+                                           float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return sparse_mla_fp4_layer("dsv41_sparse_mla_fp4_decode", q, win_kv, chunk_kv, comp_kv4, comp_bstride, n_comp,
+                              sink, idx, k, o, bsz, 1, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd,
+                              workspace, workspace_bytes, true, stream);
 }
 
 extern "C" int dsv41_sparse_mla_fp8(const void* q, const void* win_kv, const void* chunk_kv, const uint8_t* comp_kv,

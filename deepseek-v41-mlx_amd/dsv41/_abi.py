@@ -84,6 +84,11 @@ _SIGNATURES = {
                              _sz, _c_p],
     "dsv41_sparse_mla_fp8_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _i64, _i32, _c_p, _c_p, _i32,
                                     _c_p, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
+    "dsv41_comp_write_fp4": [_c_p, _c_p, _i64, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_sparse_mla_fp4": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32,
+                             _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla_fp4_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32,
+                                    _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
     "dsv41_comp_write_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32,
                              _i32, _c_p],
     "dsv41_index_key_publish_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32,
@@ -429,6 +434,32 @@ def comp_write_fp8(latents, codes, scales, g0, ratio, cos, sin, rd, scale_rb=1):
         raise ValueError(f"{name}: rope table too short")
     _call(name, _ptr(latents), _ptr(codes), row_stride(codes, name), _ptr(scales), row_stride(scales, name), scale_rb,
           _ptr(cos), _ptr(sin), b, g, d, rd, g0, ratio, dtype_code(latents, name), _stream(latents))
+
+
+def fp4_row_bytes(d: int) -> int:
+    """Bytes of one packed fp4 compressed-cache row: d/2 code bytes, then d/16 e4m3 scales."""
+    return d // 2 + d // 16
+
+
+def comp_write_fp4(latents, comp_kv4, g0, ratio, cos, sin, rd):
+    """comp_write into a packed fp4 cache: comp_kv4 uint8 [b, >=g0+g, d/2 + d/16], per row the
+    e2m1 codes of fake_quant_fp4_e4m3(rope(latent), 16) (channel 2p in the low nibble of byte p)
+    and then one e4m3 scale byte per 16 channels. Decoding e2m1(code) * scale gives exactly the
+    values comp_write stores."""
+    name = "dsv41_comp_write_fp4"
+    _gpu(name, latents, comp_kv4, cos, sin)
+    _contig(name, latents)
+    _tables(name, cos, sin, rd)
+    b, g, d = latents.shape
+    if (comp_kv4.dtype != torch.uint8 or comp_kv4.dim() != 3 or comp_kv4.shape[2] != fp4_row_bytes(d)
+            or comp_kv4.shape[1] < g0 + g):
+        raise ValueError(f"{name}: packed cache {tuple(comp_kv4.shape)} {comp_kv4.dtype} cannot take "
+                         f"groups {g0}..{g0 + g} of {d} channels")
+    _batch(name, "the compressed cache", comp_kv4, b)
+    if g and (g0 + g - 1) * ratio >= cos.shape[0]:
+        raise ValueError(f"{name}: rope table too short")
+    _call(name, _ptr(latents), _ptr(comp_kv4), row_stride(comp_kv4, name), _ptr(cos), _ptr(sin), b, g, d, rd, g0,
+          ratio, dtype_code(latents, name), _stream(latents))
 
 
 def index_key_publish_fp8(k_raw, codes, scales, g0, ratio, norm_w, cos, sin, rd, eps, scale_rb=1):
@@ -866,14 +897,9 @@ def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_sca
     return o
 
 
-def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, attn_sink, idx, softmax_scale,
-                   window, start_pos, cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False):
-    """sparse_mla with an fp8 compressed cache: comp8 uint8 [b, >=n_comp, 512] e4m3fn codes,
-    comp_scale uint8 [b, >=ceil(n_comp / scale_rb), 16] ue8m0 exponents (one per 32 channels
-    for every scale_rb = 1 or 32 rows). q, the window ring, chunk and output are bf16.
-    write_ring (one token per row): the launch also stores chunk_kv into its ring slot."""
-    name = "dsv41_sparse_mla_fp8_decode" if write_ring else "dsv41_sparse_mla_fp8"
-    _gpu(name, q, win_kv, chunk_kv, comp8, comp_scale, attn_sink, idx, cos, sin, out)
+def _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start_pos, cos, sin, rd, write_ring):
+    """Checks shared by the packed-cache sparse_mla forms (bf16 q, ring, chunk; 512 channels):
+    returns (b, n, h, d, ring view, k)."""
     _contig(name, q, chunk_kv, attn_sink, idx)
     b, n, h, d = q.shape
     if q.dtype != torch.bfloat16 or d != 512:
@@ -890,6 +916,65 @@ def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, att
         _contig(name, ring)
     elif wp:
         raise ValueError(f"{name}: a window ring is needed once start_pos > 0")
+    k = 0
+    if idx is not None:
+        if idx.dtype != torch.int32 or idx.shape[:2] != (b, n):
+            raise ValueError(f"{name}: idx must be int32 [{b}, {n}, k]")
+        k = idx.shape[2]
+    if rd:
+        _tables(name, cos, sin, rd)
+        if n and start_pos + n - 1 >= cos.shape[0]:
+            raise ValueError(f"{name}: rope table too short")
+    if write_ring and (n != 1 or ring is None):
+        raise ValueError(f"{name}: the ring store needs one token per row and a window ring")
+    return b, n, h, d, ring, k
+
+
+def sparse_mla_fp4(q, win_kv, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softmax_scale, window, start_pos,
+                   cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False):
+    """sparse_mla with a packed fp4 compressed cache (comp_write_fp4's layout): comp_kv4 uint8
+    [b, >=n_comp, 288] rows of 512 e2m1 codes and 32 e4m3 scales. q, the window ring, chunk and
+    output are bf16; the result equals sparse_mla's on the decoded cache.
+    write_ring (one token per row): the launch also stores chunk_kv into its ring slot."""
+    name = "dsv41_sparse_mla_fp4_decode" if write_ring else "dsv41_sparse_mla_fp4"
+    _gpu(name, q, win_kv, chunk_kv, comp_kv4, attn_sink, idx, cos, sin, out)
+    b, n, h, d, ring, k = _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start_pos, cos,
+                                              sin, rd, write_ring)
+    comp_bstride = 0
+    if comp_kv4 is not None and n_comp:
+        if (comp_kv4.dtype != torch.uint8 or comp_kv4.dim() != 3 or comp_kv4.shape[2] != fp4_row_bytes(d)
+                or comp_kv4.shape[1] < n_comp):
+            raise ValueError(f"{name}: packed fp4 cache {tuple(comp_kv4.shape)} {comp_kv4.dtype} does not match")
+        _batch(name, "the compressed cache", comp_kv4, b)
+        comp_bstride = row_stride(comp_kv4, name)
+    else:
+        comp_kv4, n_comp = None, 0
+    o = _out(name, out, q.shape, q.dtype, q.device)
+    wp = min(start_pos, window)
+    ws_bytes = mla_workspace_bytes(b, n, h, d, min(window, wp + n) + k, q.dtype)
+    workspace = _ws(name, workspace, ws_bytes, q.device)
+    tail = (_ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, _ptr(workspace) if ws_bytes else None,
+            ws_bytes, _stream(q))
+    head = (_ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp_kv4), comp_bstride, n_comp, _ptr(attn_sink), _ptr(idx),
+            k, _ptr(o), b)
+    if write_ring:
+        _call(name, *head, h, d, window, start_pos, float(softmax_scale), *tail)
+    else:
+        _call(name, *head, n, h, d, window, start_pos, float(softmax_scale), *tail)
+    return o
+
+
+def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, attn_sink, idx, softmax_scale,
+                   window, start_pos, cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False):
+    """sparse_mla with an fp8 compressed cache: comp8 uint8 [b, >=n_comp, 512] e4m3fn codes,
+    comp_scale uint8 [b, >=ceil(n_comp / scale_rb), 16] ue8m0 exponents (one per 32 channels
+    for every scale_rb = 1 or 32 rows). q, the window ring, chunk and output are bf16.
+    write_ring (one token per row): the launch also stores chunk_kv into its ring slot."""
+    name = "dsv41_sparse_mla_fp8_decode" if write_ring else "dsv41_sparse_mla_fp8"
+    _gpu(name, q, win_kv, chunk_kv, comp8, comp_scale, attn_sink, idx, cos, sin, out)
+    b, n, h, d, ring, k = _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start_pos, cos,
+                                              sin, rd, write_ring)
+    wp = min(start_pos, window)
     comp_bstride = sc_bstride = 0
     if comp8 is not None and n_comp:
         if comp8.dtype != torch.uint8 or comp8.shape[2] != d or comp8.shape[1] < n_comp or comp8.shape[0] < b:
@@ -902,15 +987,6 @@ def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, att
         sc_bstride = row_stride(comp_scale, name)
     else:
         comp8, comp_scale, n_comp = None, None, 0
-    k = 0
-    if idx is not None:
-        if idx.dtype != torch.int32 or idx.shape[:2] != (b, n):
-            raise ValueError(f"{name}: idx must be int32 [{b}, {n}, k]")
-        k = idx.shape[2]
-    if rd:
-        _tables(name, cos, sin, rd)
-        if n and start_pos + n - 1 >= cos.shape[0]:
-            raise ValueError(f"{name}: rope table too short")
     o = _out(name, out, q.shape, q.dtype, q.device)
     rows = min(window, wp + n) + k
     ws_bytes = mla_workspace_bytes(b, n, h, d, rows, q.dtype)
@@ -918,8 +994,6 @@ def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, att
     tail = (_ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, _ptr(workspace) if ws_bytes else None,
             ws_bytes, _stream(q))
     if write_ring:
-        if n != 1 or ring is None:
-            raise ValueError(f"{name}: the ring store needs one token per row and a window ring")
         _call(name, _ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp8), comp_bstride, n_comp, _ptr(comp_scale),
               sc_bstride, scale_rb, _ptr(attn_sink), _ptr(idx), k, _ptr(o), b, h, d, window, start_pos,
               float(softmax_scale), *tail)

@@ -112,6 +112,9 @@ class Attention(torch.nn.Module):
             _abi.comp_write_fp8(latents.to(self.dtype).contiguous(), lc.comp_kv8, lc.comp_ks, g0, self.ratio, cos,
                                 sin, rd, lc.fp8_rb)
             return
+        if lc.comp_kv4 is not None:           # packed fp4 cache: the same fp4/e4m3 QAT, stored packed
+            _abi.comp_write_fp4(latents.to(self.dtype).contiguous(), lc.comp_kv4, g0, self.ratio, cos, sin, rd)
+            return
         lat = latents.to(lc.dtype).contiguous()
         if fakequant.DISABLE:
             lat = _abi.rope_tail(lat, rd, cos, sin, g0 * self.ratio, self.ratio)
@@ -139,7 +142,7 @@ class Attention(torch.nn.Module):
         wp = min(start_pos, self.window_size)
         offset = wp + n                     # compressed entries follow window + chunk
         cidx = None
-        comp, n_comp = None, 0
+        comp, n_comp, comp_kind = None, 0, "dense"
         if self.ratio:
             src = shared.kv_src_cache
             compress_len = end_pos // self.ratio
@@ -163,7 +166,7 @@ class Attention(torch.nn.Module):
             if latents is not None:
                 self._write_latents(latents, lc, start_pos // self.ratio, cos, sin)
             if compress_len:
-                comp, n_comp = (src.comp_kv8 if src.comp_kv8 is not None else src.comp_kv)[:bsz], compress_len
+                (comp_kind, comp), n_comp = src.comp_source(bsz), compress_len
 
         sink = torch.zeros_like(self.attn_sink) if self._break_sink else self.attn_sink
         # one-token decode: the attention launch also writes the token into the ring (the slot it
@@ -171,9 +174,12 @@ class Attention(torch.nn.Module):
         decode = n == 1
         sel = cidx if cidx is not None and cidx.shape[-1] else None
         rdo = 0 if self._break_rope_inverse else rd
-        if comp is not None and comp.dtype == torch.uint8:      # the fp8 cache variant
+        if comp_kind == "fp8":
             o = _abi.sparse_mla_fp8(q, lc.win_kv, kv, comp, src.comp_ks[:bsz], src.fp8_rb, n_comp, sink, sel,
                                     self.softmax_scale, self.window_size, start_pos, cos, sin, rdo, write_ring=decode)
+        elif comp_kind == "fp4":
+            o = _abi.sparse_mla_fp4(q, lc.win_kv, kv, comp, n_comp, sink, sel, self.softmax_scale, self.window_size,
+                                    start_pos, cos, sin, rdo, write_ring=decode)
         else:
             o = _abi.sparse_mla(q, lc.win_kv, kv, comp, n_comp, sink, sel, self.softmax_scale, self.window_size,
                                 start_pos, cos, sin, rdo, write_ring=decode)

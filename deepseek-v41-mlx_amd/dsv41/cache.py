@@ -19,6 +19,11 @@ stored as e4m3fn codes with one ue8m0 scale byte per 32 channels of each row (``
 fake_quant_fp8_ue8m0's formula in place of the reference's fp4 QAT at those two stores and
 dequantized in-kernel. The window ring stays in ``dtype``.
 
+``cache_format="fp4"`` holds the compressed KV -- fp4/e4m3 fake-quantized by construction
+(attention.py:157-163) -- losslessly packed: ``comp_kv4``, rows of d/2 bytes of e2m1 codes then
+d/16 e4m3 scale bytes (288 bytes for 512 channels; ``comp_kv`` is None). The index keys follow
+``index_format`` (MXFP4 is their lossless packed form), the window ring stays in ``dtype``.
+
 All buffers are plain torch device tensors with the reference's attribute names. The kernels
 update them in place, so a snapshot must copy: ``lc.win_kv[:]`` -- which in MLX pins the
 pre-step value (generate.py:18-44) -- is a view in torch. ``snapshot(cache)`` and
@@ -38,7 +43,7 @@ from .config import ModelArgs
 
 
 INDEX_FORMATS = ("dense", "mxfp4")
-CACHE_FORMATS = ("dense", "fp8")
+CACHE_FORMATS = ("dense", "fp8", "fp4")
 
 
 class PackedKeys:
@@ -78,6 +83,7 @@ class LayerCache:
         self.index_k4 = None
         self.index_ks = None
         self.comp_kv8 = self.comp_ks = self.index_k8 = self.index_k8s = None
+        self.comp_kv4 = None
         if self.is_kv_source:
             n_comp = max_seq_len // self.ratio
             d = args.head_dim
@@ -85,6 +91,8 @@ class LayerCache:
             if fp8:
                 self.comp_kv8 = torch.zeros(bsz, n_comp, d, dtype=torch.uint8, device=device)
                 self.comp_ks = torch.zeros(bsz, n_blk, d // 32, dtype=torch.uint8, device=device)
+            elif cache_format == "fp4":
+                self.comp_kv4 = torch.zeros(bsz, n_comp, _abi.fp4_row_bytes(d), dtype=torch.uint8, device=device)
             else:
                 self.comp_kv = torch.zeros(bsz, n_comp, d, dtype=dtype, device=device)
             if self.ratio > 1:
@@ -108,6 +116,15 @@ class LayerCache:
         if self.index_k8 is not None:
             return PackedKeys("fp8", self.index_k8[:bsz, :n], self.index_k8s[:bsz, :-(-n // self.fp8_rb)], self.fp8_rb)
         return self.index_k[:bsz, :n]
+
+    def comp_source(self, bsz: int):
+        """The compressed cache of rows [:bsz] as the attention reads it: (kind, tensor), kind
+        "dense", "fp8" (codes; the scales are ``comp_ks``) or "fp4" (packed rows)."""
+        if self.comp_kv8 is not None:
+            return "fp8", self.comp_kv8[:bsz]
+        if self.comp_kv4 is not None:
+            return "fp4", self.comp_kv4[:bsz]
+        return "dense", self.comp_kv[:bsz]
 
     def window_chrono(self, pos: int) -> torch.Tensor:
         """The ring in chronological order: positions [pos - Wp, pos), Wp = min(pos, window)."""
@@ -133,7 +150,8 @@ class ModelCache:
         self.engram_ids = None
 
 
-_BUFFERS = ("win_kv", "comp_kv", "index_k", "index_k4", "index_ks", "comp_kv8", "comp_ks", "index_k8", "index_k8s")
+_BUFFERS = ("win_kv", "comp_kv", "index_k", "index_k4", "index_ks", "comp_kv8", "comp_ks", "index_k8", "index_k8s",
+            "comp_kv4")
 
 
 def snapshot(cache: ModelCache):

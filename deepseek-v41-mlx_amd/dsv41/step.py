@@ -88,10 +88,11 @@ class StackDecodeStep:
     [b,1,Hi,Di] (roped, fake-quantized) -- or, when the key owners' caches are MXFP4,
     ``index_q_mx`` (its codes and scales from dsv41_index_q_prep_mxfp4) --, ``w_raw`` [b,1,Hi]
     and ``w_scale``; kv sources add ``latent`` [b,1,D] (pre-rope); key owners add ``k_raw``
-    [b,1,Di] and ``k_norm`` [Di]. Caches may be dense, carry MXFP4 index keys, or be the fp8
-    variant (cache_format "fp8": fp8 compressed KV and index keys, with ue8m0 scales per 32
-    channels of each row or of 32-row blocks); each layer takes the kernels that read and write
-    its owners' format. Over fp8 keys an index source given ``index_q_mx`` scores on the
+    [b,1,Di] and ``k_norm`` [Di]. Caches may be dense, carry MXFP4 index keys, hold the
+    compressed KV packed (cache_format "fp4": e2m1 codes + e4m3 scales per 16 channels), or be
+    the fp8 variant (cache_format "fp8": fp8 compressed KV and index keys, with ue8m0 scales per
+    32 channels of each row or of 32-row blocks); each layer takes the kernels that read and
+    write its owners' format. Over fp8 keys an index source given ``index_q_mx`` scores on the
     block-scaled fp4 x fp8 MFMA (dsv41_indexer_*_mxq_fp8), else it dequantizes the keys for the
     bf16 MFMA. On every key format, index sources other than the candidate source score and
     select in the fused form (dsv41_indexer_topk(_fp8, _mxfp4, _mxq_fp8)) where it serves the
@@ -160,7 +161,7 @@ class StackDecodeStep:
         for p in self.plan:
             x = inputs[p.layer_id]
             lc = cache.layers[p.layer_id]
-            comp, n_comp, idx = None, 0, None
+            comp, n_comp, idx, comp_kind = None, 0, None, "dense"
             if p.ratio:
                 nb = self.end_pos // p.ratio
                 emits = self.end_pos % p.ratio == 0       # this token completes group nb - 1
@@ -221,14 +222,20 @@ class StackDecodeStep:
                 if p.kv_source and emits and lc.comp_kv8 is not None:
                     _abi.comp_write_fp8(x["latent"], lc.comp_kv8, lc.comp_ks, nb - 1, p.ratio, p.cos, p.sin,
                                         a.rope_head_dim, lc.fp8_rb)
+                elif p.kv_source and emits and lc.comp_kv4 is not None:
+                    _abi.comp_write_fp4(x["latent"], lc.comp_kv4, nb - 1, p.ratio, p.cos, p.sin, a.rope_head_dim)
                 elif p.kv_source and emits:
                     _abi.comp_write(x["latent"], lc.comp_kv, nb - 1, p.ratio, p.cos, p.sin, a.rope_head_dim)
-                comp, n_comp, idx = (kv_src.comp_kv8 if kv_src.comp_kv8 is not None else kv_src.comp_kv)[:b], nb, topk
+                (comp_kind, comp), n_comp, idx = kv_src.comp_source(b), nb, topk
             # attention + this token's ring write in one launch
-            if comp is not None and comp.dtype == torch.uint8:
+            if comp_kind == "fp8":
                 _abi.sparse_mla_fp8(x["q"], lc.win_kv, x["kv"], comp, kv_src.comp_ks[:b], kv_src.fp8_rb, n_comp,
                                     x["sink"], idx, self.scale, self.window, sp, p.cos, p.sin, a.rope_head_dim,
                                     out=p.out, workspace=self.workspace, write_ring=True)
+            elif comp_kind == "fp4":
+                _abi.sparse_mla_fp4(x["q"], lc.win_kv, x["kv"], comp, n_comp, x["sink"], idx, self.scale, self.window,
+                                    sp, p.cos, p.sin, a.rope_head_dim, out=p.out, workspace=self.workspace,
+                                    write_ring=True)
             else:
                 _abi.sparse_mla(x["q"], lc.win_kv, x["kv"], comp, n_comp, x["sink"], idx, self.scale, self.window,
                                 sp, p.cos, p.sin, a.rope_head_dim, out=p.out, workspace=self.workspace,

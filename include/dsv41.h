@@ -132,6 +132,17 @@ int dsv41_comp_write(const void* latents, void* comp_kv, int64_t cache_bstride,
                      int32_t dim, int32_t rd, int32_t g0, int32_t ratio, int32_t dtype,
                      hipStream_t stream);
 
+/* dsv41_comp_write into a packed fp4 cache, the lossless packed form of the same
+ * fake_quant_fp4_e4m3 values (attention.py:157-163, fakequant.py:109-118): per row dim/2 bytes
+ * of e2m1 codes (byte p holds channels 2p, 2p+1, the even one in the low nibble), then one e4m3fn
+ * scale byte per 16 channels (the block's fake-quant scale) -- dim/2 + dim/16 bytes per row
+ * (288 at dim 512), comp_kv4 [bsz, >=g0+g, row] with cache_bstride bytes per batch row (both
+ * multiples of 16). Decoding e2m1(code) * scale gives exactly dsv41_comp_write's values. */
+int dsv41_comp_write_fp4(const void* latents, uint8_t* comp_kv4, int64_t cache_bstride,
+                         const float* cos_tab, const float* sin_tab, int32_t bsz, int32_t g,
+                         int32_t dim, int32_t rd, int32_t g0, int32_t ratio, int32_t dtype,
+                         hipStream_t stream);
+
 /* Indexer.publish_keys after the wk projection, deepseek_v41_mlx/indexer.py:89-104:
  * index_k[b, g0 + j] <- fake_quant_fp4_ue8m0(rope_tail(k_norm(k_raw[b, j]), (g0+j)*ratio), 32)
  * for k_raw [bsz, g, dim]; index_k has `cache_bstride` elements per batch row. */
@@ -414,6 +425,29 @@ int dsv41_sparse_mla_fp8_decode(const void* q, void* win_kv, const void* chunk_k
                                 void* o, int32_t bsz, int32_t heads, int32_t dim, int32_t window,
                                 int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab,
                                 int32_t rd, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* dsv41_sparse_mla with the compressed source in dsv41_comp_write_fp4's packed layout: 288-byte
+ * rows (512 e2m1 codes, then 32 e4m3fn scales, one per 16 channels), comp_bstride bytes per
+ * batch row (a multiple of 16). Rows are decoded to bf16 in-kernel, exactly (an e2m1 value times
+ * an e4m3 value is bf16-representable), so the result equals dsv41_sparse_mla's on the decoded
+ * cache -- the values the reference's bf16 cache holds after its fp4 QAT (attention.py:157-163).
+ * q, win_kv, chunk_kv and o are bf16; dim is 512; the workspace is sized by
+ * dsv41_sparse_mla_workspace_bytes(..., DSV41_BF16). */
+int dsv41_sparse_mla_fp4(const void* q, const void* win_kv, const void* chunk_kv,
+                         const uint8_t* comp_kv4, int64_t comp_bstride, int32_t n_comp, const float* sink,
+                         const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads,
+                         int32_t dim, int32_t window, int32_t start_pos, float scale, const float* cos_tab,
+                         const float* sin_tab, int32_t rd, void* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
+
+/* dsv41_sparse_mla_fp4 for one token per row (n = 1) that also performs the ring write of
+ * LayerCache.write_window, deepseek_v41_mlx/cache.py:61-67, as dsv41_sparse_mla_decode does. */
+int dsv41_sparse_mla_fp4_decode(const void* q, void* win_kv, const void* chunk_kv,
+                                const uint8_t* comp_kv4, int64_t comp_bstride, int32_t n_comp,
+                                const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
+                                int32_t heads, int32_t dim, int32_t window, int32_t start_pos, float scale,
+                                const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -125,6 +125,19 @@ def e4m3_decode(codes) -> np.ndarray:
     return np.where(s == 1, -v, v).astype(F32)
 
 
+def e4m3_encode(q) -> np.ndarray:
+    """e4m3fn codes (uint8) of float32 values already on the e4m3 grid (|q| <= 448): the inverse
+    of e4m3_decode on finite values."""
+    q = np.ascontiguousarray(q, dtype=F32)
+    a = np.abs(q)
+    u = a.view(np.uint32)
+    e = ((u >> 23) & 0xFF).astype(np.int32) - 127 + 7
+    normal = (e << 3) | ((u >> 20) & 7).astype(np.int32)
+    sub = np.rint(a * F32(512.0)).astype(np.int32)
+    c = np.where(a < F32(2.0 ** -6), sub, normal) | (np.signbit(q).astype(np.int32) << 7)
+    return c.astype(np.uint8)
+
+
 def dequant_fp8_cache(codes, scales, rb: int) -> np.ndarray:
     """An fp8 cache [b, rows, D] of e4m3 codes with ue8m0 block scales [b, ceil(rows/rb), D/32]
     (scale 2^(e-127) for every rb rows x 32 channels) -> float32 values."""
@@ -250,6 +263,32 @@ def fq_fp4_e4m3(x, block: int = 16, dtype: str = "f32") -> np.ndarray:
     s = e4m3_round((amax / FP4_MAX).astype(F32))
     q = e2m1_round(np.clip(xb / s, -FP4_MAX, FP4_MAX)) * s
     return cast(q.reshape(shape), dtype)
+
+
+def fp4_e4m3_encode(x, block: int = 16):
+    """Packed form of fake_quant_fp4_e4m3(x, block) over the last dim (fakequant.py:109-119):
+    per row d/2 bytes of e2m1 codes (the rounding of fq_fp4_e4m3 as a 4-bit code, sign in bit 3,
+    two per byte, the even channel in the low nibble), then one e4m3fn byte per block holding
+    the block scale s = e4m3_round(max(amax, 6 * 2^-9) / 6). Returns uint8 [..., d/2 + d/block]."""
+    xb = _blockify(x, block)
+    amax = np.maximum(np.abs(xb).max(axis=-1, keepdims=True), F32(6.0 * 2.0 ** -9))
+    s = e4m3_round((amax / FP4_MAX).astype(F32))
+    r = e2m1_round(np.clip(xb / s, -FP4_MAX, FP4_MAX))
+    mag = np.searchsorted(_E2M1_LUT, np.abs(r)).astype(np.uint8)
+    code = (mag | (np.signbit(r).astype(np.uint8) << 3)).reshape(*np.shape(x)[:-1], -1)
+    codes = (code[..., 0::2] | (code[..., 1::2] << 4)).astype(np.uint8)
+    return np.concatenate([codes, e4m3_encode(s[..., 0])], axis=-1)
+
+
+def fp4_e4m3_decode(rows, block: int = 16) -> np.ndarray:
+    """float32 values of fp4_e4m3_encode's rows: e2m1(code) * e4m3(scale byte of the block)."""
+    rows = np.asarray(rows, np.uint8)
+    d = (rows.shape[-1] * 2 * block) // (block + 2)
+    c = rows[..., :d // 2]
+    nib = np.stack([c & 15, c >> 4], axis=-1).reshape(*c.shape[:-1], -1)
+    v = _E2M1_LUT[nib & 7] * np.where(nib & 8, F32(-1.0), F32(1.0))
+    sc = e4m3_decode(rows[..., d // 2:])
+    return (v * np.repeat(sc, block, axis=-1)).astype(F32)
 
 
 # ---------------------------------------------------------------------------

@@ -203,13 +203,14 @@ def test_rope_frequencies_match_oracle_restatement():
         assert np.array_equal(yarn_inv_freqs(*args), R.yarn_freqs(*args))
 
 
-@pytest.mark.parametrize("index_format,cache_format", [("dense", "dense"), ("mxfp4", "dense"), ("dense", "fp8")])
+@pytest.mark.parametrize("index_format,cache_format", [("dense", "dense"), ("mxfp4", "dense"), ("dense", "fp8"),
+                                                       ("mxfp4", "fp4")])
 def test_cache_snapshot_restore(index_format, cache_format):
     """snapshot() copies every buffer of every cache format (a torch slice would alias the
     buffers the kernels update in place); restore() writes the copies back into the same tensors
     and resets the offset, as generate.py:18-44 does for the reference."""
     from common import C4_TOY, model_args
-    from dsv41.cache import ModelCache, restore, snapshot
+    from dsv41.cache import _BUFFERS, ModelCache, restore, snapshot
     a = model_args(C4_TOY)
     cache = ModelCache(a, 2, 64, torch.float32, "cpu", index_format, cache_format)
     g = torch.Generator().manual_seed(11)
@@ -217,8 +218,7 @@ def test_cache_snapshot_restore(index_format, cache_format):
     def tensors():
         out = []
         for lc in cache.layers:
-            for name in ("win_kv", "comp_kv", "index_k", "index_k4", "index_ks", "comp_kv8", "comp_ks", "index_k8",
-                         "index_k8s"):
+            for name in _BUFFERS:
                 if getattr(lc, name) is not None:
                     out.append(getattr(lc, name))
             if lc.comp_state is not None:
@@ -343,6 +343,14 @@ def test_cache_writers_check_batch_rows_and_parameters(host_abi):
                                      torch.float32), "state")
     _refused(lambda: A.compress_pool(kv, kv.clone(), st, st.clone(), torch.ones(32), 4, 3, 1e-6,
                                      torch.float32), "norm weight")
+    lat512 = torch.zeros(2, 3, 512)
+    _reaches_launch(lambda: A.comp_write_fp4(lat512, torch.zeros(2, 8, 288, dtype=torch.uint8), 5, 4, cos, sin, 16))
+    _refused(lambda: A.comp_write_fp4(lat512, torch.zeros(2, 7, 288, dtype=torch.uint8), 5, 4, cos, sin, 16),
+             "cannot take")
+    _refused(lambda: A.comp_write_fp4(lat512, torch.zeros(2, 8, 256, dtype=torch.uint8), 5, 4, cos, sin, 16),
+             "cannot take")
+    _refused(lambda: A.comp_write_fp4(lat512, torch.zeros(1, 8, 288, dtype=torch.uint8), 5, 4, cos, sin, 16),
+             "batch rows")
 
 
 def test_indexer_and_topk_wrappers_check_out(host_abi):
@@ -399,3 +407,19 @@ def test_sparse_mla_wrappers_check_buffers(host_abi):
     _refused(call8(out=torch.zeros(b, 1, h, d - 32, dtype=torch.bfloat16)), "out must be")
     _refused(call8(comp8=codes[:1], comp_scale=scales[:1]), "does not match")
     _refused(call8(attn_sink=sink.double()), "attn_sink")
+    packed = torch.zeros(b, 1024, 288, dtype=torch.uint8)
+
+    def call4(**kw):
+        args = dict(q=q, win_kv=ring, chunk_kv=chunk, comp_kv4=packed, n_comp=1000, attn_sink=sink, idx=idx,
+                    softmax_scale=0.1, window=W, start_pos=64, cos=cos, sin=sin, rd=64)
+        args.update(kw)
+        return lambda: A.sparse_mla_fp4(**args)
+
+    _reaches_launch(call4())
+    _reaches_launch(call4(write_ring=True))
+    _refused(call4(comp_kv4=packed[:1]), "batch rows")
+    _refused(call4(comp_kv4=torch.zeros(b, 1024, 256, dtype=torch.uint8)), "does not match")
+    _refused(call4(comp_kv4=packed[:, :999]), "does not match")
+    _refused(call4(q=q.float()), "bf16")
+    _refused(call4(chunk_kv=torch.zeros(b, 2, d, dtype=torch.bfloat16), write_ring=True), "chunk kv")
+    _refused(call4(win_kv=None, write_ring=True), "window ring")

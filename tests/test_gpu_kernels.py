@@ -694,6 +694,91 @@ def test_sparse_mla_fp8_cache_equals_bf16_on_dequantized_cache(gpu, b, n, window
     assert rel_max_diff(to_np(got8), want) < 2e-2
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_comp_write_fp4_packs_the_comp_write_values(gpu, dt):
+    """The packed fp4 writer stores the oracle's encoding of the GPU's own roped latents, byte
+    for byte; decoded, those rows are bit-equal to what the dense comp_write stores; rows outside
+    the written groups stay zero."""
+    from dsv41 import _abi
+    rng = rng_for("w4" + dt)
+    rc, rs = R.precompute_freqs_cis(64, 2048, 65536, 160000.0, 16.0, 32, 1)
+    b, g, d, g0, r = 3, 11, 512, 77, 4
+    lat = R.cast(rng.standard_normal((b, g, d)).astype(F32) * 2, dt)
+    lat[0, 0, :16] = 0.0                               # a zero block: the floor scale
+    lat[1, 2, 32:48] *= 1e-2                           # a small block: a subnormal e4m3 scale
+    row = _abi.fp4_row_bytes(d)
+    assert row == 288
+    packed = torch.zeros(b, 128, row, dtype=torch.uint8, device=gpu)
+    _abi.comp_write_fp4(dev(lat, dt), packed, g0, r, dev(rc), dev(rs), 64)
+    dense = torch.zeros(b, 128, d, dtype=DT[dt], device=gpu)
+    _abi.comp_write(dev(lat, dt), dense, g0, r, dev(rc), dev(rs), 64)
+    roped = to_np(_abi.rope_tail(dev(lat, dt), 64, dev(rc), dev(rs), g0 * r, r))
+    torch.cuda.synchronize()
+    p = packed.cpu().numpy()
+    assert np.array_equal(p[:, g0:g0 + g], R.fp4_e4m3_encode(roped))
+    got = R.fp4_e4m3_decode(p[:, g0:g0 + g])
+    assert np.array_equal(got.view(np.uint32), to_np(dense)[:, g0:g0 + g].view(np.uint32))
+    assert not p[:, :g0].any() and not p[:, g0 + g:].any()
+    assert p[0, g0, 256] == 0x01 and 0x01 < p[1, g0 + 2, 258] < 0x08     # the floor and a subnormal scale
+
+
+def _fp4_cache(rng, b, rows, d):
+    """Packed fp4 rows: uniform random code bytes and e4m3 scale bytes 2^-5 .. 2^3 (no NaN)."""
+    codes = rng.integers(0, 256, size=(b, rows, d // 2), dtype=np.uint8)
+    scales = rng.integers(0x10, 0x58, size=(b, rows, d // 16), dtype=np.uint8)
+    return np.concatenate([codes, scales], axis=-1)
+
+
+@pytest.mark.parametrize("b,n,window,start,n_comp,k", [
+    (8, 1, 128, 40000, 9000, 1000),         # decode, split index lists
+    (16, 1, 128, 131071, 4000, 1024),       # batch 16, top-1024
+    (2, 1, 128, 5, 1, 3),                   # a short ring, one compressed row
+    (1, 600, 16, 200, 150, 64),             # >= 512 queries: the 64-head plan
+])
+def test_sparse_mla_fp4_cache_equals_bf16_on_decoded_cache(gpu, b, n, window, start, n_comp, k):
+    """Packed fp4 compressed cache decoded in-kernel: bit-identical to the bf16 path on the
+    decoded cache (an e2m1 value times an e4m3 scale is exact in bf16), the decode form's ring
+    write identical too, and within the bf16 tolerance of the oracle."""
+    from dsv41 import _abi
+    rng = rng_for(f"mla4{b}{n}{start}")
+    h, d, rd = 64, 512, 64
+    rc, rs = R.precompute_freqs_cis(rd, start + n + 1, 65536, 160000.0, 16.0, 32, 1)
+    q = R.cast(rng.standard_normal((b, n, h, d)).astype(F32) * 2, "bf16")
+    win = R.cast(rng.standard_normal((b, window, d)).astype(F32), "bf16")
+    chunk = R.cast(rng.standard_normal((b, n, d)).astype(F32), "bf16")
+    rows = _fp4_cache(rng, b, n_comp + 5, d)
+    comp = R.fp4_e4m3_decode(rows)
+    assert np.array_equal(R.cast(comp, "bf16"), comp)
+    sink = rng.standard_normal(h).astype(F32)
+    wp = min(start, window)
+    lens = R.query_lens(start, n, 4)
+    cidx = np.sort(rng.integers(0, n_comp, size=(b, n, k)), axis=-1)
+    cidx = np.where(cidx < np.minimum(lens, n_comp)[None, :, None], cidx + wp + n, -1).astype(np.int32)
+    cidx[:, :, ::5] = -1
+    idx_t = torch.as_tensor(cidx).to(gpu)
+    args = (d ** -0.5, window, start, dev(rc), dev(rs), rd)
+    rows_t = torch.as_tensor(rows).to(gpu)
+    got4 = _abi.sparse_mla_fp4(dev(q, "bf16"), dev(win, "bf16"), dev(chunk, "bf16"), rows_t, n_comp, dev(sink),
+                               idx_t, *args)
+    got16 = _abi.sparse_mla(dev(q, "bf16"), dev(win, "bf16"), dev(chunk, "bf16"), dev(comp, "bf16"), n_comp,
+                            dev(sink), idx_t, *args)
+    assert torch.equal(got4, got16)
+    if n == 1:                                     # the decode form: output and ring write
+        ring4, ring16 = dev(win, "bf16"), dev(win, "bf16")
+        o4 = _abi.sparse_mla_fp4(dev(q, "bf16"), ring4, dev(chunk, "bf16"), rows_t, n_comp, dev(sink), idx_t, *args,
+                                 write_ring=True)
+        o16 = _abi.sparse_mla(dev(q, "bf16"), ring16, dev(chunk, "bf16"), dev(comp, "bf16"), n_comp, dev(sink),
+                              idx_t, *args, write_ring=True)
+        assert torch.equal(o4, o16) and torch.equal(o4, got4) and torch.equal(ring4, ring16)
+        assert torch.equal(ring4[:, start % window], dev(chunk, "bf16")[:, 0])
+    kv_all = _concat_reference(win, chunk, comp, n_comp, start, window)
+    widx = np.broadcast_to(R.window_idx_matrix(wp, n, window)[None], (b, n, min(window, wp + n)))
+    o = R.sparse_attn(q, kv_all, sink, np.concatenate([widx, cidx], axis=-1), d ** -0.5, dtype="bf16")
+    pos = start + np.arange(n)
+    want = R.rope_tail(o, rd, rc[pos], rs[pos], inverse=True, dtype="bf16")
+    assert rel_max_diff(to_np(got4), want) < 2e-2
+
+
 def test_reference_kernel_module_seam(gpu):
     """dsv41.kernel stands in for the reference model's native `kernel` module."""
     import dsv41.kernel as K

@@ -206,6 +206,49 @@ def test_mxfp4_code_values_and_nibble_order():
     assert s[0, 0] == 127 - 2
 
 
+@pytest.mark.parametrize("n", [0, 1, 2])
+def test_packed_fp4_e4m3_decodes_to_the_fake_quant_known_answers(n):
+    """The packed compressed-KV rows (e2m1 codes + e4m3 scale bytes per 16 channels) are a
+    lossless form of fake_quant_fp4_e4m3: decoding the encoding of the known-answer inputs gives
+    the known answers bit for bit, and re-encoding those gives the same bytes."""
+    d = np.load(GOLDEN)
+    x = d[f"x{n}"]
+    t = x.shape[-1] // 16 * 16
+    want = d[f"fp4_e4m3_{n}"][..., :t]
+    assert np.array_equal(R.fq_fp4_e4m3(x[..., :t], 16).view(np.uint32), want.view(np.uint32))
+    rows = R.fp4_e4m3_encode(x[..., :t])
+    assert rows.shape[-1] == t // 2 + t // 16 and rows.dtype == np.uint8
+    got = R.fp4_e4m3_decode(rows)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(R.fp4_e4m3_encode(got), rows)
+
+
+def test_e4m3_codes_against_torch_float8():
+    """e4m3_decode of every byte equals torch's float8_e4m3fn reading of it, and e4m3_encode
+    inverts it on every finite code."""
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).float().numpy()
+    got = R.e4m3_decode(codes)
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(got), fin) and fin.sum() == 254
+    assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+    assert np.array_equal(R.e4m3_encode(got[fin]), codes[fin])
+
+
+def test_packed_fp4_e4m3_layout():
+    """One 16-channel block holding 0.5, -1 and 6 (channels 0, 1, 2): amax 6 gives scale
+    e4m3(1.0) = byte 0x38; codes 1 (0.5), 8|2 (-1.0), 7 (6.0), the even channel in the low
+    nibble; a zero block takes the floor scale 6 * 2^-9 / 6 = 2^-9, the smallest e4m3 subnormal
+    (byte 0x01)."""
+    x = np.zeros((1, 32), F32)
+    x[0, :3] = (0.5, -1.0, 6.0)
+    r = R.fp4_e4m3_encode(x)[0]
+    assert r.shape == (18,)
+    assert r[0] == 0xA1 and r[1] == 0x07 and not r[2:16].any()
+    assert r[16] == 0x38 and r[17] == 0x01
+    assert np.array_equal(R.fp4_e4m3_decode(r[None])[0], x[0])
+
+
 def test_fake_quant_values_are_exact_in_bf16():
     """The QAT grids are representable in bf16, so a bf16 cache stores them losslessly."""
     rng = np.random.default_rng(4)
