@@ -551,21 +551,22 @@ def c4_step_bytes(a, B, start_pos, index_format="dense"):
     (window + top-k rows), q and o; per index source the key stream, its queries and the score
     write; top-k score reads and index writes; the candidate mask write and reads; the window /
     latent / key writes of this token. index_format: "dense" (bf16 caches), "mxfp4" (packed
-    index keys), "packed" (MXFP4 index keys and fp4 compressed rows, e2m1 + e4m3 per 16
-    channels) or "fp8" (the fp8 cache variant: e4m3 + ue8m0 per 32 x 32 block for the
-    compressed rows and the index keys)."""
+    index keys), "packed" (MXFP4 index keys, fp4 compressed rows -- e2m1 + e4m3 per 16
+    channels -- and an MXFP8 window ring) or "fp8" (the fp8 cache variant: e4m3 + ue8m0 per
+    32 x 32 block for the compressed rows and the index keys)."""
     H, D, Hi, Di, W, K = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim, a.window_size, a.index_topk
     # per index key, per index-query head, per compressed KV row; the fp8 variant's scale bytes cover
     # 32 x 32 blocks, i.e. 1/32 byte per 32 channels of a row
     kb = {"mxfp4": Di // 2 + Di // 32, "packed": Di // 2 + Di // 32, "fp8": Di + Di / 1024}.get(index_format, Di * 2)
     qb = Di // 2 + Di // 32 if index_format in ("mxfp4", "packed", "fp8") else Di * 2
     cb = {"fp8": D + D / 1024, "packed": D // 2 + D // 16}.get(index_format, D * 2)
+    wb = D + D // 32 if index_format == "packed" else D * 2  # per window-ring row
     wp = min(start_pos, W)
     total = 0
     for l in range(a.n_layers):
         r = a.compress_ratio(l)
-        rows = min(W, wp + 1)
-        total += B * D * 2                                   # window write
+        rows = min(W, wp + 1)                                # ring rows + this token's row
+        total += B * wb                                      # window write
         if r:
             nb = (start_pos + 1) // r
             k = min(K, nb)
@@ -580,9 +581,9 @@ def c4_step_bytes(a, B, start_pos, index_format="dense"):
                     total += B * nb                                         # mask read
             if l in a.kv_source_layers:
                 total += B * (D * 2 + cb) + (B * (Di * 2 + kb) if l in a.index_source_layers else 0)
-            total += B * (rows - k) * D * 2 + B * k * cb     # sparse MLA gather: window rows + selected rows
+            total += B * ((rows - k - 1) * wb + D * 2) + B * k * cb   # gather: ring, token, selected rows
         else:
-            total += B * rows * D * 2
+            total += B * ((rows - 1) * wb + D * 2)
         total += B * 2 * H * D * 2                           # q, o
     return int(total)
 
@@ -606,14 +607,14 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
     log(f"[bench] 40-layer decode B={B} start_pos={start} top-{topk} index={index_format}")
     g = torch.Generator(device=device).manual_seed(SEED + 300)
     sc = 576 ** -0.5
-    H, D, Hi, Di = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim
+    H, D, Hi, Di, W = a.n_heads, a.head_dim, a.index_n_heads, a.index_head_dim, a.window_size
     packed = index_format == "packed"
     mx = index_format == "mxfp4" or packed
     fp8 = index_format == "fp8"
     if fp8:
         cache = ModelCache(a, B, start + 1, bf, device, cache_format="fp8", fp8_block_rows=32)
     elif packed:
-        cache = ModelCache(a, B, start + 1, bf, device, "mxfp4", cache_format="fp4")
+        cache = ModelCache(a, B, start + 1, bf, device, "mxfp4", cache_format="packed")
     else:
         cache = ModelCache(a, B, start + 1, bf, device, index_format)
 
@@ -630,6 +631,10 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
         if lc.index_k4 is not None:
             lc.index_k4.copy_(rbytes(0, 256, *lc.index_k4.shape))
             lc.index_ks.copy_(rbytes(123, 132, *lc.index_ks.shape))
+        if lc.win_kv8 is not None:                 # e4m3 codes without the NaN patterns, ue8m0 2^-9 .. 2^-6
+            c = rbytes(0, 256, B, W, D)
+            lc.win_kv8[..., :D].copy_(torch.where((c & 0x7F) == 0x7F, c ^ 1, c))
+            lc.win_kv8[..., D:].copy_(rbytes(118, 122, B, W, D // 32))
         if lc.comp_kv4 is not None:                # e2m1 codes, e4m3 scales 2^-6 .. 2^-2
             lc.comp_kv4[..., :D // 2].copy_(rbytes(0, 256, B, lc.comp_kv4.shape[1], D // 2))
             lc.comp_kv4[..., D // 2:].copy_(rbytes(0x08, 0x28, B, lc.comp_kv4.shape[1], D // 16))
@@ -670,7 +675,7 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
                     f"source 20; " + ("fp8 caches (e4m3 + ue8m0 per 32x32 block) for compressed KV and index keys, "
                                       "index queries MXFP4 (fp4 x fp8 MFMA scoring), window ring bf16" if fp8
                                       else "packed caches: compressed KV e2m1 + e4m3 per 16 channels (288 B/row), "
-                                      "index keys and queries MXFP4, window ring bf16" if packed
+                                      "window ring MXFP8 (528 B/row), index keys and queries MXFP4" if packed
                                       else f"index caches {index_format}"),
         "step_ms": ms, "tokens_per_s": B / (ms * 1e-3), "steps": reps,
         "step_algorithmic_bytes": nbytes, "hbm_GBps_step": gbs, "hbm_frac_step": gbs / HBM_PEAK_GBS,

@@ -149,31 +149,33 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
 // s - m <= the lazy-rescale threshold: results below 2^-126 are zero for the sum anyway.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// 8 e4m3fn codes (two dwords) times a power-of-two scale -> MFMA operand. Exact: e4m3 values
-// scaled by 2^k are bf16-representable within bf16's exponent range. v_cvt_pk_f32_fp8 decodes
-// OCP e4m3fn on gfx950, subnormals included.
+// 8 e4m3fn codes (two dwords, channel i in byte i) times a power-of-two scale -> MFMA operand.
+// v_cvt_scalef32_pk_f32_fp8 decodes two OCP e4m3fn codes (subnormals included) and applies the
+// scale's exponent -- all of a normal power of two (2^-126 .. 2^127), which the ue8m0 scales of
+// the fp8 caches (bytes 1..254) are. Exact: e4m3 values scaled by 2^k are bf16-representable
+// within bf16's exponent range.
 __device__ __forceinline__ bf16x8 dequant_e4m3x8(uint32_t lo, uint32_t hi, float scale) {
   typedef __attribute__((ext_vector_type(2))) float f2;
-  float v[8];
-  const f2 a = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false), b = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-  const f2 c = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false), d = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-  v[0] = a[0] * scale; v[1] = a[1] * scale; v[2] = b[0] * scale; v[3] = b[1] * scale;
-  v[4] = c[0] * scale; v[5] = c[1] * scale; v[6] = d[0] * scale; v[7] = d[1] * scale;
+  const f2 a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, scale, false);
+  const f2 b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, scale, true);
+  const f2 c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, scale, false);
+  const f2 d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, scale, true);
+  const float v[8] = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
   return cvt_bf16x8(v);
 }
 
 // 8 e2m1 codes (one dword; channel 2p in the low nibble of byte p) times an e4m3 block scale ->
-// MFMA operand. Exact: an e2m1 value times an e4m3 value has at most 6 significant bits and lies
-// inside bf16's exponent range. The e2m1 value is built from its bits: magnitude code m gives 0,
-// 0.5 (m = 1) or 2^((m >> 1) - 1) * (1 + (m & 1) / 2).
+// MFMA operand. v_cvt_scalef32_pk_f32_fp4 decodes the two codes of one byte (scale 1); the e4m3
+// scale, which is not a power of two in general, is a separate multiply. Exact: an e2m1 value
+// times an e4m3 value has at most 6 significant bits and lies inside bf16's exponent range.
 __device__ __forceinline__ bf16x8 dequant_e2m1x8(uint32_t codes, float scale) {
-  float v[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t c = (codes >> (4 * i)) & 15u, m = c & 7u;
-    const uint32_t mag = m == 0u ? 0u : (m == 1u ? 0x3F000000u : (((126u + (m >> 1)) << 23) | ((m & 1u) << 22)));
-    v[i] = __uint_as_float(mag | ((c & 8u) << 28)) * scale;
-  }
+  typedef __attribute__((ext_vector_type(2))) float f2;
+  const f2 a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, 1.0f, 0);
+  const f2 b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, 1.0f, 1);
+  const f2 c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, 1.0f, 2);
+  const f2 d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(codes, 1.0f, 3);
+  const float v[8] = {a[0] * scale, a[1] * scale, b[0] * scale, b[1] * scale,
+                      c[0] * scale, c[1] * scale, d[0] * scale, d[1] * scale};
   return cvt_bf16x8(v);
 }
 

@@ -396,6 +396,39 @@ __global__ void window_write_kernel(T* win, const T* kv, int n, int dim, int win
   win[(b * window + slot) * dim + d] = kv[(b * n + (n - keep + t)) * dim + d];
 }
 
+// window_write into an MXFP8 ring (rows of dim e4m3fn codes, then dim/32 ue8m0 scale bytes):
+// 8 channels per thread, a 32-channel block per 4 consecutive lanes, quantized by
+// fake_quant_fp8_ue8m0's formula -- exact for window KV that already holds that QAT's values.
+template <typename T>
+__global__ void window_write_mxfp8_kernel(uint8_t* ring, int64_t ring_bstride, const T* kv, int n, int dim, int window,
+                                          int start_pos, int keep, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // over bsz*keep*(dim/8)
+  if (i >= total) return;                       // total is a multiple of 4: block lanes stay together
+  const int cpr = dim / 8;
+  const int64_t row = i / cpr;
+  const int c = (int)(i - row * cpr);
+  const int64_t b = row / keep;
+  const int t = (int)(row - b * keep);
+  const int slot = (int)(((int64_t)start_pos + n - keep + t) % window);
+  const T* src = kv + (b * n + (n - keep + t)) * (int64_t)dim + c * 8;
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = io<T>::ld(src + j);
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  amax = fmaxf(group_max(amax, 4), 1e-4f);
+  const float sc = pow2_ceil_log2(amax * (float)(1.0 / 448.0));
+  const float inv = __fdiv_rn(1.0f, sc);        // exact: sc is a power of two
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    w[j / 4] |= (uint32_t)e4m3_encode(e4m3_round(fminf(fmaxf(v[j] * inv, -448.0f), 448.0f))) << (8 * (j % 4));
+  uint8_t* dst = ring + b * ring_bstride + (int64_t)slot * (dim + dim / 32);
+  *reinterpret_cast<uint2*>(dst + c * 8) = make_uint2(w[0], w[1]);
+  if ((c & 3) == 0) dst[dim + c / 4] = (uint8_t)((__float_as_uint(sc) >> 23) & 0xFFu);
+}
+
 __global__ void window_idx_kernel(int32_t* out, int wp, int n, int window, int weff) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (int64_t)n * weff) return;
@@ -507,6 +540,33 @@ extern "C" int dsv41_window_write(void* win_kv, const void* kv, int32_t bsz, int
                        (const float*)kv, n, dim, window, start_pos, keep, total);
   else if (dtype == DSV41_BF16)
     hipLaunchKernelGGL(window_write_kernel<bf16_t>, dim3(blocks), dim3(256), 0, stream, (bf16_t*)win_kv,
+                       (const bf16_t*)kv, n, dim, window, start_pos, keep, total);
+  else
+    return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported", what, dtype);
+  return check_launch(what);
+}
+
+extern "C" int dsv41_window_write_mxfp8(uint8_t* win_kv8, int64_t ring_bstride, const void* kv, int32_t bsz,
+                                        int32_t n, int32_t dim, int32_t window, int32_t start_pos, int32_t dtype,
+                                        hipStream_t stream) {
+  const char* what = "dsv41_window_write_mxfp8";
+  DSV41_REQUIRE(win_kv8 && kv, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(bsz >= 0 && n >= 0 && window > 0 && start_pos >= 0, DSV41_E_ARG, "%s: bad sizes", what);
+  DSV41_REQUIRE(dim > 0 && dim % 32 == 0, DSV41_E_SHAPE, "%s: dim %d must be a positive multiple of 32", what, dim);
+  DSV41_REQUIRE(ring_bstride >= (int64_t)window * (dim + dim / 32), DSV41_E_ARG, "%s: ring too small", what);
+  DSV41_REQUIRE(ring_bstride % 8 == 0 && (dim + dim / 32) % 8 == 0, DSV41_E_ARG,
+                "%s: rows and the batch stride must be multiples of 8 bytes", what);
+  DSV41_REQUIRE((reinterpret_cast<uintptr_t>(win_kv8) & 7u) == 0 && aligned16(kv), DSV41_E_ARG,
+                "%s: misaligned tensor", what);
+  const int keep = n < window ? n : window;
+  const int64_t total = (int64_t)bsz * keep * (dim / 8);
+  if (total == 0) return 0;
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  if (dtype == DSV41_F32)
+    hipLaunchKernelGGL(window_write_mxfp8_kernel<float>, dim3(blocks), dim3(256), 0, stream, win_kv8, ring_bstride,
+                       (const float*)kv, n, dim, window, start_pos, keep, total);
+  else if (dtype == DSV41_BF16)
+    hipLaunchKernelGGL(window_write_mxfp8_kernel<bf16_t>, dim3(blocks), dim3(256), 0, stream, win_kv8, ring_bstride,
                        (const bf16_t*)kv, n, dim, window, start_pos, keep, total);
   else
     return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported", what, dtype);

@@ -46,14 +46,49 @@ struct MlaArgs {
   const float* sin_tab;
   int rd, start_pos;
   int hgroups, splits, per_split;
-  bf16_t* part_o;     // split partials: numerator / denominator, rounded to bf16 [slot][dim]
-  float* part_ml;     // split partials: (log2-domain max, denominator) [slot][2]
+  bf16_t* part_o;     // split partials: numerator / denominator, rounded to bf16, in 16 x 16 tiles
+                      // (part_tile: [unit][split][head tile][dim / 16][16 heads][16 channels])
+  float* part_ml;     // split partials: (log2-domain max, denominator) [unit][split][head][2]
   void* ring_w;       // one-token decode: also store the token's KV row in its ring slot (or null)
 };
 
 // One-token decode: copy batch row b's KV row into ring slot start_pos % window. The slot holds
 // position start_pos - window, which has just left the window, so no entry of the launch reads
 // it; one wave per batch row does the copy, at its start.
+template <typename T>
+__device__ __forceinline__ void ring_store(const MlaArgs& a, int b, int lane, int lanes);
+
+// The same store into an MXFP8 ring (rows of D e4m3fn codes, then D/32 ue8m0 scale bytes): one
+// full wave, 8 channels per lane, a 32-channel block per 4 lanes, quantized by
+// fake_quant_fp8_ue8m0's formula (fakequant.py:83-93). The window KV reaching the ring already
+// holds that QAT's values, which this encodes exactly (the block scale it finds is the QAT's own
+// or half of it, and either puts every value on the e4m3 grid).
+template <int D>
+__device__ __forceinline__ void ring_store_fp8(const MlaArgs& a, int b, int lane) {
+  static_assert(D == 512, "MXFP8 ring rows: 512 channels");
+  const KvSrc& S = a.src;
+  const bf16_t* src = reinterpret_cast<const bf16_t*>(S.chunk) + (int64_t)b * S.chunk_bstride + lane * 8;
+  uint8_t* row = reinterpret_cast<uint8_t*>(a.ring_w) + (int64_t)b * S.ring_bstride +
+                 (int64_t)(a.start_pos % S.window) * (D + D / 32);
+  float v[8];
+  const uint4 x = *reinterpret_cast<const uint4*>(src);
+  const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = bf2f((bf16_t)(xw[i / 2] >> (16 * (i % 2))));
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(group_max(amax, 4), 1e-4f);
+  const float sc = pow2_ceil_log2(amax * (float)(1.0 / 448.0));
+  const float inv = __fdiv_rn(1.0f, sc);        // exact: sc is a power of two
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    w[i / 4] |= (uint32_t)e4m3_encode(e4m3_round(fminf(fmaxf(v[i] * inv, -448.0f), 448.0f))) << (8 * (i % 4));
+  *reinterpret_cast<uint2*>(row + lane * 8) = make_uint2(w[0], w[1]);
+  if ((lane & 3) == 0) row[D + (lane >> 2)] = (uint8_t)((__float_as_uint(sc) >> 23) & 0xFFu);
+}
+
 template <typename T>
 __device__ __forceinline__ void ring_store(const MlaArgs& a, int b, int lane, int lanes) {
   const KvSrc& S = a.src;
@@ -81,6 +116,15 @@ __device__ __forceinline__ int list_pos(const KvSrc& s, int b, int m, int qs, in
   }
   if (e < s.k) return s.idx[((int64_t)b * m + qs) * s.k + e];
   return -1;
+}
+
+// Element offset of split partial (unit, split sp, head h, channel d): 16-head x 16-channel tiles
+// of 512 contiguous bytes, so the 64 lanes of one MFMA accumulator tile store one full block and
+// a combine lane's 8 channels of one head are 16 contiguous bytes.
+__device__ __forceinline__ int64_t part_tile(const MlaArgs& a, int unit, int sp, int h, int d) {
+  const int htiles = (a.heads + 15) >> 4;
+  return ((((int64_t)unit * a.splits + sp) * htiles + (h >> 4)) * (a.dim >> 4) + (d >> 4)) * 256 + (h & 15) * 16 +
+         (d & 15);
 }
 
 template <typename T>
@@ -222,13 +266,17 @@ struct MlaLds {
 // copies land, the issuing wave dequantizes the row in place to bf16, before the step barrier.
 // PAIR: the decode instance sized for two workgroups per CU (half the LDS: at most kPairList list
 // entries, a two-slot ring), so that two independent step pipelines share each CU.
-constexpr int kCompBf16 = 0, kCompFp8 = 1, kCompFp4 = 2;
+// CF | kWinFp8: the window ring is MXFP8 (rows of D e4m3 codes + D/32 ue8m0 scales, the layout
+// of ring_store_fp8); such a row lands where an fp8 compressed row does.
+constexpr int kCompBf16 = 0, kCompFp8 = 1, kCompFp4 = 2, kCompMask = 3, kWinFp8 = 4;
 
 template <int D, int HT, int DS, int CF, bool PAIR>
 __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
-  constexpr bool F8 = CF == kCompFp8, F4 = CF == kCompFp4;
+  constexpr bool F8 = (CF & kCompMask) == kCompFp8, F4 = (CF & kCompMask) == kCompFp4, W8 = (CF & kWinFp8) != 0;
+  constexpr bool PACKED = F8 || F4 || W8;
   constexpr int F4ROW = D / 2 + D / 16;         // packed fp4 row bytes
   constexpr int F4OFF = 2 * D - F4ROW;          // where it lands in the bf16 slot row
+  constexpr int W8ROW = D + D / 32;             // MXFP8 ring row bytes
   constexpr int NW = HT * DS, NT = 64 * NW;
   constexpr int ML = PAIR ? kPairList : kMaxList;
   constexpr int DSL = D / DS, KSS = DSL / 32, DTS = DSL / 16;
@@ -254,7 +302,10 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar address math
   const int ht = wave % HT, dh = wave / HT;
-  if (a.ring_w && hg == 0 && sp == 0 && wave == 0) ring_store<bf16_t>(a, b, lane, 64);
+  if (a.ring_w && hg == 0 && sp == 0 && wave == 0) {
+    if constexpr (W8) ring_store_fp8<D>(a, b, lane);
+    else ring_store<bf16_t>(a, b, lane, 64);
+  }
   const int wc = window_count(S, qs);
   // The split's entries: its share of the window rows, then its share of the index list (one
   // split takes the whole list). Window rows need no index read, so a split whose first step is
@@ -266,17 +317,20 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   auto entry_row = [&](int e) {                  // split entry -> row address (0 = masked)
     const int u = list_pos(S, b, a.m, qs, e < nw ? w0 + e : wc + k0 + (e - nw), wc);
     const int ci = u - S.wp - S.n_chunk;
-    // packed compressed-cache entries are encoded as (row << 1) | 1 and addressed at issue time
+    // packed rows are tagged and addressed at issue time: compressed (row << 2) | 1, MXFP8 ring
+    // (slot << 2) | 2; bf16 rows are 16-byte aligned addresses (tag 0), masked entries 0
+    if (W8 && u >= 0 && u < S.wp) return ((uint64_t)((S.ring_first + u) % S.window) << 2) | 2ull;
     return ((F8 || F4) && u >= 0 && ci >= 0 && ci < S.n_comp)
-               ? (((uint64_t)ci << 1) | 1ull)
+               ? (((uint64_t)ci << 2) | 1ull)
                : reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, u, D));
   };
-  static_assert(CF == kCompBf16 || D == 512, "packed cache rows: 512 channels (one copy instruction per row)");
+  static_assert(!PACKED || D == 512, "packed cache rows: 512 channels (one copy instruction per row)");
 
   const int nsteps = (cnt + R - 1) / R;
   const uint32_t ring_base = lds_offset(ring);
   const uint64_t comp8 =
       (F8 || F4) ? reinterpret_cast<uint64_t>(S.comp) + (uint64_t)b * (uint64_t)S.comp_bstride : 0ull;
+  const uint64_t ring8 = W8 ? reinterpret_cast<uint64_t>(S.ring) + (uint64_t)b * (uint64_t)S.ring_bstride : 0ull;
   const uint64_t scal8 = F8 ? reinterpret_cast<uint64_t>(S.comp_scale) + (uint64_t)b * (uint64_t)S.comp_scale_bstride : 0ull;
   const int rbs = S.comp_scale_rb == 32 ? 5 : 0;   // scale row block (1 or 32) as a shift
   auto issue = [&](int t, bool direct) {
@@ -289,16 +343,21 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
 #pragma unroll
     for (int rr = 0; rr < RPW; ++rr) {
       const uint64_t ent = lane_u64(lo, hi, rr);
-      if (F8 && (ent & 1ull)) {
+      const uint32_t tag = (uint32_t)ent & 3u;
+      if (F8 && tag == 1u) {
         // lanes 0..31: the row's 512 fp8 bytes; lane 32: its 16 scale bytes
-        const uint64_t ci = ent >> 1;
+        const uint64_t ci = ent >> 2;
         const uint64_t src = lane < D / 16 ? comp8 + ci * D + (uint64_t)lane * 16u
                                            : scal8 + (ci >> rbs) * (D / 32);
         if (lane <= D / 16) dma16_vaddr(src, dst + rr * RS + D);
-      } else if (F4 && (ent & 1ull)) {
+      } else if (F4 && tag == 1u) {
         // lanes 0..F4ROW/16-1: the row's codes and scales, one contiguous packed row
-        const uint64_t src = comp8 + (ent >> 1) * F4ROW + (uint64_t)lane * 16u;
+        const uint64_t src = comp8 + (ent >> 2) * F4ROW + (uint64_t)lane * 16u;
         if (lane < F4ROW / 16) dma16_vaddr(src, dst + rr * RS + F4OFF);
+      } else if (W8 && tag == 2u) {
+        // lanes 0..32: the ring row's 512 codes and 16 scales, contiguous, to [D, 2D + 16)
+        const uint64_t src = ring8 + (ent >> 2) * W8ROW + (uint64_t)lane * 16u;
+        if (lane <= D / 16) dma16_vaddr(src, dst + rr * RS + D);
       } else {
         dma_row<D>(ent, dst + rr * RS, lane);
       }
@@ -342,43 +401,36 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
 
   for (int t = 0; t < nsteps; ++t) {
     wait_steps<NL>(min(nsteps - 1 - t, NS - 2));
-    if constexpr (F8) {
-      // this wave's own fp8 rows of step t have landed: dequantize them in place. All of its
+    if constexpr (PACKED) {
+      // this wave's own packed rows of step t have landed: dequantize them in place. All of its
       // rows are read before any is written (a single wave converts them), so the bf16 output
-      // may overlap the fp8 bytes it came from, and the reads go out together.
+      // may overlap the bytes it came from, and the reads go out together. Lane l converts
+      // channels 8l..8l+7: fp8 rows (tag 2, or tag 1 of an fp8 compressed cache) hold their
+      // codes at [D, 2D) and the ue8m0 scale of the lane's block at 2D + l/4; fp4 rows (tag 1)
+      // hold code bytes 4l..4l+3 at F4OFF and the e4m3 scale byte l/2 after the codes.
       uint8_t* sb = ring + (t % NS) * SLOT + wave * RPW * RS;
-      uint2 c8[RPW];
+      uint2 raw[RPW];
       float sc[RPW];
-      bool has[RPW];
+      uint32_t tag[RPW];
 #pragma unroll
       for (int rr = 0; rr < RPW; ++rr) {
         const int ei = t * R + wave * RPW + rr;
-        has[rr] = ((ei < cnt ? rows[ei] : 0ull) & 1ull) != 0ull;
+        tag[rr] = (uint32_t)(ei < cnt ? rows[ei] : 0ull) & 3u;
         const uint8_t* row = sb + rr * RS;
-        c8[rr] = *reinterpret_cast<const uint2*>(row + D + lane * 8);
-        sc[rr] = e8m0_to_float(row[2 * D + (lane >> 2)]);
+        if (F4 && tag[rr] == 1u) {
+          raw[rr] = make_uint2(*reinterpret_cast<const uint32_t*>(row + F4OFF + lane * 4), 0u);
+          sc[rr] = __builtin_amdgcn_cvt_f32_fp8((int)row[F4OFF + D / 2 + (lane >> 1)], 0);
+        } else {
+          raw[rr] = *reinterpret_cast<const uint2*>(row + D + lane * 8);
+          sc[rr] = e8m0_to_float(row[2 * D + (lane >> 2)]);
+        }
       }
-#pragma unroll
-      for (int rr = 0; rr < RPW; ++rr)
-        if (has[rr]) *reinterpret_cast<bf16x8*>(sb + rr * RS + lane * 16) = dequant_e4m3x8(c8[rr].x, c8[rr].y, sc[rr]);
-    } else if constexpr (F4) {
-      // the same for packed fp4 rows: lane l's 8 channels are code bytes 4l..4l+3, their scale is
-      // e4m3 byte l/2 after the codes
-      uint8_t* sb = ring + (t % NS) * SLOT + wave * RPW * RS;
-      uint32_t c4[RPW];
-      float sc[RPW];
-      bool has[RPW];
 #pragma unroll
       for (int rr = 0; rr < RPW; ++rr) {
-        const int ei = t * R + wave * RPW + rr;
-        has[rr] = ((ei < cnt ? rows[ei] : 0ull) & 1ull) != 0ull;
-        const uint8_t* row = sb + rr * RS + F4OFF;
-        c4[rr] = *reinterpret_cast<const uint32_t*>(row + lane * 4);
-        sc[rr] = __builtin_amdgcn_cvt_f32_fp8((int)row[D / 2 + (lane >> 1)], 0);
+        bf16x8* out = reinterpret_cast<bf16x8*>(sb + rr * RS + lane * 16);
+        if (F4 && tag[rr] == 1u) *out = dequant_e2m1x8(raw[rr].x, sc[rr]);
+        else if (tag[rr] != 0u) *out = dequant_e4m3x8(raw[rr].x, raw[rr].y, sc[rr]);
       }
-#pragma unroll
-      for (int rr = 0; rr < RPW; ++rr)
-        if (has[rr]) *reinterpret_cast<bf16x8*>(sb + rr * RS + lane * 16) = dequant_e2m1x8(c4[rr], sc[rr]);
     }
     __syncthreads();                       // step t landed; every wave is done with step t-1
     const int slot = t % NS;
@@ -452,30 +504,34 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   l_run += __shfl_xor(l_run, 16, 64);      // denominator: sum of the 4 lane groups
   l_run += __shfl_xor(l_run, 32, 64);
   if (!hok) return;                        // no barrier follows
-  const int64_t slot_id = ((int64_t)unit * a.splits + sp) * a.heads + h;
-  bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + h) * D;
-  // a split's partial is stored normalized (numerator / its own denominator) in bf16; a split
-  // whose rows are all masked (denominator 0) stores zeros, which the combine weighs by 0
-  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  // The two endings are separate straight-line blocks: this code runs once per workgroup with a
+  // cold instruction cache, and one interleaved per-tile branch made it ~3,000 instructions.
+  if (a.splits > 1) {
+    // a split's partial is stored normalized (numerator / its own denominator) in bf16; a split
+    // whose rows are all masked (denominator 0) stores zeros, which the combine weighs by 0
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    bf16_t* tile0 = a.part_o + part_tile(a, unit, sp, h, dh * DSL + 4 * g);
 #pragma unroll
-  for (int dt = 0; dt < DTS; ++dt) {
-    const int d0 = dh * DSL + dt * 16 + 4 * g;
-    if (a.splits == 1) {
-      store_out4(a, D, qs, orow, d0, acc[dt], l_run);
-    } else {
+    for (int dt = 0; dt < DTS; ++dt) {
       uint2 st;
       st.x = pack2_bf16(acc[dt][0] * inv, acc[dt][1] * inv);
       st.y = pack2_bf16(acc[dt][2] * inv, acc[dt][3] * inv);
-      *reinterpret_cast<uint2*>(a.part_o + slot_id * D + d0) = st;
+      *reinterpret_cast<uint2*>(tile0 + dt * 256) = st;   // next 16-channel tile: 256 elements on
     }
+    if (dh == 0 && g == 0) {
+      const int64_t slot_id = ((int64_t)unit * a.splits + sp) * a.heads + h;
+      *reinterpret_cast<float2*>(a.part_ml + slot_id * 2) = make_float2(m_run, l_run);
+    }
+    return;
   }
-  if (a.splits > 1 && dh == 0 && g == 0) {
-    a.part_ml[slot_id * 2 + 0] = m_run;
-    a.part_ml[slot_id * 2 + 1] = l_run;
-  }
+  bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + h) * D;
+#pragma unroll
+  for (int dt = 0; dt < DTS; ++dt) store_out4(a, D, qs, orow, dh * DSL + dt * 16 + 4 * g, acc[dt], l_run);
 }
 
-// Merges split partials of one query: one wave per head, 4 heads per workgroup. Split s holds
+// Merges split partials of one query: one wave per head, 4 heads per workgroup; the workgroups
+// of a query are numbered as the attention launch numbers its tiles (xcd_tile), so they read the
+// partials on the XCD whose L2 the attention workgroups wrote them to. Split s holds
 // (m_s, l_s, o_s) = (log2-domain max, denominator, numerator / l_s in bf16); the merged row is
 // sum_s w_s o_s / sum_s w_s with w_s = l_s 2^(m_s - M). Every lane reads every split's
 // (m_s, l_s) (the same addresses across the wave), so the weights need no cross-lane exchange.
@@ -484,15 +540,17 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
 // covers 8 channels per 512.
 template <typename T, int NB>
 __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
-  const int unit = blockIdx.x;
-  const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int hq = (a.heads + 3) / 4;                          // workgroups per query
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int unit = tile / hq;
+  const int h = (tile - unit * hq) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (h >= a.heads) return;
   const int D = a.dim, qs = unit % a.m, ns = a.splits;
   const int64_t slot0 = (int64_t)unit * ns * a.heads + h;     // split s: slot0 + s * heads
   T* orow = reinterpret_cast<T*>(a.o) + ((int64_t)unit * a.heads + h) * D;
   auto part = [&](int s, int d) {
-    return *reinterpret_cast<const uint4*>(a.part_o + (slot0 + (int64_t)s * a.heads) * D + d);
+    return *reinterpret_cast<const uint4*>(a.part_o + part_tile(a, unit, s, h, d));
   };
   for (int d = 8 * lane; d < D; d += 512) {
     // the inverse-rope factors of this lane's pairs are fetched with the partials (unpredicated:
@@ -573,8 +631,8 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
 
 template <int NB>
 static void launch_combine(const MlaArgs& a, int64_t units, hipStream_t stream) {
-  hipLaunchKernelGGL((mla_combine_kernel<bf16_t, NB>), dim3((unsigned)units, (unsigned)((a.heads + 3) / 4)), dim3(256),
-                     0, stream, a);
+  hipLaunchKernelGGL((mla_combine_kernel<bf16_t, NB>), dim3((unsigned)(units * ((a.heads + 3) / 4))), dim3(256), 0,
+                     stream, a);
 }
 
 // fp32: 4 heads x 16 rows per step, plain FMA, natural-log softmax with the reference's form.
@@ -736,10 +794,15 @@ static MlaPlan plan_bf16(int64_t units, int heads, int list_max, int dim) {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Split partials: numerators in 16-head tiles (heads rounded up to 16), then (max, denominator).
+static size_t part_o_bytes(const MlaPlan& p, int64_t units, int heads, int dim) {
+  return align256((size_t)units * p.splits * ((heads + 15) / 16 * 16) * dim * sizeof(bf16_t));
+}
+
 static size_t workspace_for(const MlaPlan& p, int64_t units, int heads, int dim) {
   if (p.splits <= 1) return 0;
   const size_t slots = (size_t)units * p.splits * heads;
-  return align256(slots * dim * sizeof(bf16_t)) + align256(slots * 2 * sizeof(float));
+  return part_o_bytes(p, units, heads, dim) + align256(slots * 2 * sizeof(float));
 }
 
 static bool bf16_dim_supported(int d) { return d == 64 || d == 128 || d == 256 || d == 512 || d == 576; }
@@ -791,14 +854,15 @@ static int run_mla(const char* what, MlaArgs a, int64_t units, int list_max, int
     DSV41_REQUIRE(workspace && workspace_bytes >= need, DSV41_E_WORKSPACE, "%s: workspace of %zu bytes needed",
                   what, need);
     DSV41_REQUIRE(aligned16(workspace), DSV41_E_ARG, "%s: workspace must be 16-byte aligned", what);
-    const size_t slots = (size_t)units * p.splits * a.heads;
     a.part_o = reinterpret_cast<bf16_t*>(workspace);
-    a.part_ml = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + align256(slots * a.dim * sizeof(bf16_t)));
+    a.part_ml = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + part_o_bytes(p, units, a.heads, a.dim));
   }
   if (comp_format != kCompBf16) {
     DSV41_REQUIRE(a.dim == 512, DSV41_E_SHAPE, "%s: the packed cache paths support dim 512, got %d", what, a.dim);
     if (comp_format == kCompFp8) launch_bf16_d<512, kCompFp8>(a, p, units, stream);
-    else launch_bf16_d<512, kCompFp4>(a, p, units, stream);
+    else if (comp_format == kCompFp4) launch_bf16_d<512, kCompFp4>(a, p, units, stream);
+    else if (comp_format == (kCompFp4 | kWinFp8)) launch_bf16_d<512, kCompFp4 | kWinFp8>(a, p, units, stream);
+    else return set_error(DSV41_E_ARG, "%s: no kernel for cache format %d", what, comp_format);
   } else {
     switch (a.dim) {
       case 64: launch_bf16_d<64, kCompBf16>(a, p, units, stream); break;
@@ -1004,13 +1068,15 @@ static int sparse_mla_fp8_layer(const char* what, const void* q, const void* win
 }
 
 // The compressed source as packed fp4 rows: e2m1 codes then e4m3 scales per 16 channels, 288 bytes
-// per 512-channel row, comp_bstride bytes per batch row.
+// per 512-channel row, comp_bstride bytes per batch row. ring8_bstride > 0: the window ring is
+// MXFP8 rows (512 e4m3 codes + 16 ue8m0 scales, 528 bytes), ring8_bstride bytes per batch row;
+// else it is bf16.
 static int sparse_mla_fp4_layer(const char* what, const void* q, const void* win_kv, const void* chunk_kv,
                                 const uint8_t* comp_kv4, int64_t comp_bstride, int32_t n_comp, const float* sink,
                                 const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads,
                                 int32_t dim, int32_t window, int32_t start_pos, float scale, const float* cos_tab,
                                 const float* sin_tab, int32_t rd, void* workspace, size_t workspace_bytes,
-                                bool write_ring, hipStream_t stream) {
+                                bool write_ring, hipStream_t stream, int64_t ring8_bstride = 0) {
   const int wp = start_pos < window ? start_pos : window;
   DSV41_REQUIRE(q && chunk_kv && sink && o && (idx || k == 0) && (win_kv || wp == 0) && (comp_kv4 || n_comp == 0),
                 DSV41_E_ARG, "%s: null tensor", what);
@@ -1024,9 +1090,15 @@ static int sparse_mla_fp4_layer(const char* what, const void* q, const void* win
                 DSV41_E_ARG, "%s: tensors must be 16-byte aligned", what);
   DSV41_REQUIRE(comp_bstride % 16 == 0, DSV41_E_ARG, "%s: comp_bstride must be a multiple of 16 bytes", what);
   DSV41_REQUIRE(rd == 0 || (cos_tab && sin_tab && rd % 2 == 0 && rd <= dim), DSV41_E_ARG, "%s: bad rope tail", what);
+  const bool w8 = ring8_bstride > 0;
+  if (w8)
+    DSV41_REQUIRE(ring8_bstride >= (int64_t)window * (dim + dim / 32) && ring8_bstride % 16 == 0, DSV41_E_ARG,
+                  "%s: the ring's batch stride must hold %d rows of %d bytes and be a multiple of 16", what, window,
+                  dim + dim / 32);
   MlaArgs a{};
   a.q = q; a.o = o; a.sink = sink;
-  a.src.ring = win_kv; a.src.ring_bstride = (int64_t)window * dim; a.src.window = window; a.src.wp = wp;
+  a.src.ring = win_kv; a.src.ring_bstride = w8 ? ring8_bstride : (int64_t)window * dim; a.src.window = window;
+  a.src.wp = wp;
   a.src.ring_first = (start_pos - wp) % window;
   a.src.chunk = chunk_kv; a.src.chunk_bstride = (int64_t)n * dim; a.src.n_chunk = n;
   a.src.comp = comp_kv4; a.src.comp_bstride = comp_bstride; a.src.n_comp = n_comp;
@@ -1038,7 +1110,33 @@ static int sparse_mla_fp4_layer(const char* what, const void* q, const void* win
     a.ring_w = const_cast<void*>(win_kv);
   }
   const int weff = window < wp + n ? window : wp + n;
-  return run_mla(what, a, (int64_t)bsz * n, weff + k, DSV41_BF16, workspace, workspace_bytes, stream, kCompFp4);
+  return run_mla(what, a, (int64_t)bsz * n, weff + k, DSV41_BF16, workspace, workspace_bytes, stream,
+                 w8 ? (kCompFp4 | kWinFp8) : kCompFp4);
+}
+
+extern "C" int dsv41_sparse_mla_packed(const void* q, const uint8_t* win_kv8, int64_t ring_bstride,
+                                       const void* chunk_kv, const uint8_t* comp_kv4, int64_t comp_bstride,
+                                       int32_t n_comp, const float* sink, const int32_t* idx, int32_t k, void* o,
+                                       int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t window,
+                                       int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab,
+                                       int32_t rd, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  DSV41_REQUIRE(ring_bstride > 0, DSV41_E_ARG, "dsv41_sparse_mla_packed: ring_bstride must be positive");
+  return sparse_mla_fp4_layer("dsv41_sparse_mla_packed", q, win_kv8, chunk_kv, comp_kv4, comp_bstride, n_comp, sink,
+                              idx, k, o, bsz, n, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd,
+                              workspace, workspace_bytes, false, stream, ring_bstride);
+}
+
+extern "C" int dsv41_sparse_mla_packed_decode(const void* q, uint8_t* win_kv8, int64_t ring_bstride,
+                                              const void* chunk_kv, const uint8_t* comp_kv4, int64_t comp_bstride,
+                                              int32_t n_comp, const float* sink, const int32_t* idx, int32_t k,
+                                              void* o, int32_t bsz, int32_t heads, int32_t dim, int32_t window,
+                                              int32_t start_pos, float scale, const float* cos_tab,
+                                              const float* sin_tab, int32_t rd, void* workspace,
+                                              size_t workspace_bytes, hipStream_t stream) {
+  DSV41_REQUIRE(ring_bstride > 0, DSV41_E_ARG, "dsv41_sparse_mla_packed_decode: ring_bstride must be positive");
+  return sparse_mla_fp4_layer("dsv41_sparse_mla_packed_decode", q, win_kv8, chunk_kv, comp_kv4, comp_bstride, n_comp,
+                              sink, idx, k, o, bsz, 1, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd,
+                              workspace, workspace_bytes, true, stream, ring_bstride);
 }
 
 extern "C" int dsv41_sparse_mla_fp4(const void* q, const void* win_kv, const void* chunk_kv, const uint8_t* comp_kv4,

@@ -89,6 +89,11 @@ _SIGNATURES = {
                              _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
     "dsv41_sparse_mla_fp4_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32,
                                     _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla_packed": [_c_p, _c_p, _i64, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32,
+                                _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla_packed_decode": [_c_p, _c_p, _i64, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
+                                       _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
+    "dsv41_window_write_mxfp8": [_c_p, _i64, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_comp_write_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32,
                              _i32, _c_p],
     "dsv41_index_key_publish_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32,
@@ -434,6 +439,26 @@ def comp_write_fp8(latents, codes, scales, g0, ratio, cos, sin, rd, scale_rb=1):
         raise ValueError(f"{name}: rope table too short")
     _call(name, _ptr(latents), _ptr(codes), row_stride(codes, name), _ptr(scales), row_stride(scales, name), scale_rb,
           _ptr(cos), _ptr(sin), b, g, d, rd, g0, ratio, dtype_code(latents, name), _stream(latents))
+
+
+def mxfp8_row_bytes(d: int) -> int:
+    """Bytes of one MXFP8 window-ring row: d e4m3fn codes, then d/32 ue8m0 scales."""
+    return d + d // 32
+
+
+def window_write_mxfp8(win_kv8, kv, start_pos):
+    """window_write into an MXFP8 ring: win_kv8 uint8 [b, window, d + d/32], position p at slot
+    p % window; each row stored as fake_quant_fp8_ue8m0's codes and block scales (exact for window
+    KV that carries that QAT)."""
+    name = "dsv41_window_write_mxfp8"
+    _gpu(name, win_kv8, kv)
+    _contig(name, kv)
+    b, n, d = kv.shape
+    if win_kv8.dtype != torch.uint8 or win_kv8.dim() != 3 or win_kv8.shape[2] != mxfp8_row_bytes(d):
+        raise ValueError(f"{name}: ring {tuple(win_kv8.shape)} {win_kv8.dtype} does not hold {d}-channel MXFP8 rows")
+    _batch(name, "the window ring", win_kv8, b)
+    _call(name, _ptr(win_kv8), row_stride(win_kv8, name), _ptr(kv), b, n, d, win_kv8.shape[1], start_pos,
+          dtype_code(kv, name), _stream(kv))
 
 
 def fp4_row_bytes(d: int) -> int:
@@ -897,9 +922,10 @@ def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_sca
     return o
 
 
-def _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start_pos, cos, sin, rd, write_ring):
-    """Checks shared by the packed-cache sparse_mla forms (bf16 q, ring, chunk; 512 channels):
-    returns (b, n, h, d, ring view, k)."""
+def _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start_pos, cos, sin, rd, write_ring,
+                        ring_mxfp8=False):
+    """Checks shared by the packed-cache sparse_mla forms (bf16 q and chunk, a bf16 or MXFP8
+    ring; 512 channels): returns (b, n, h, d, ring view, k)."""
     _contig(name, q, chunk_kv, attn_sink, idx)
     b, n, h, d = q.shape
     if q.dtype != torch.bfloat16 or d != 512:
@@ -909,9 +935,10 @@ def _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start
     if chunk_kv.shape != (b, n, d) or chunk_kv.dtype != q.dtype:
         raise ValueError(f"{name}: chunk kv must be {q.dtype} [{b}, {n}, {d}]")
     ring = None
+    row, rdt = (mxfp8_row_bytes(d), torch.uint8) if ring_mxfp8 else (d, q.dtype)
     if win_kv is not None:
-        if win_kv.shape[0] < b or win_kv.shape[1:] != (window, d) or win_kv.dtype != q.dtype:
-            raise ValueError(f"{name}: window ring {tuple(win_kv.shape)} does not match")
+        if win_kv.dim() != 3 or win_kv.shape[0] < b or win_kv.shape[1:] != (window, row) or win_kv.dtype != rdt:
+            raise ValueError(f"{name}: window ring {tuple(win_kv.shape)} {win_kv.dtype} does not match")
         ring = win_kv[:b]
         _contig(name, ring)
     elif wp:
@@ -937,9 +964,27 @@ def sparse_mla_fp4(q, win_kv, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softma
     output are bf16; the result equals sparse_mla's on the decoded cache.
     write_ring (one token per row): the launch also stores chunk_kv into its ring slot."""
     name = "dsv41_sparse_mla_fp4_decode" if write_ring else "dsv41_sparse_mla_fp4"
+    return _sparse_mla_fp4_rows(name, q, win_kv, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softmax_scale, window,
+                                start_pos, cos, sin, rd, out, workspace, write_ring, False)
+
+
+def sparse_mla_packed(q, win_kv8, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softmax_scale, window, start_pos,
+                      cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False):
+    """sparse_mla over the packed cache: the window ring as MXFP8 rows (win_kv8 uint8
+    [b, window, 528]: 512 e4m3fn codes, 16 ue8m0 scales; window_write_mxfp8's layout) and the
+    compressed KV as packed fp4 rows (comp_kv4, or None for a window-only layer). q, chunk and
+    output are bf16; the result equals sparse_mla's on the decoded caches. write_ring (one token
+    per row): the launch also stores chunk_kv, MXFP8-encoded, into its ring slot."""
+    name = "dsv41_sparse_mla_packed_decode" if write_ring else "dsv41_sparse_mla_packed"
+    return _sparse_mla_fp4_rows(name, q, win_kv8, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softmax_scale, window,
+                                start_pos, cos, sin, rd, out, workspace, write_ring, True)
+
+
+def _sparse_mla_fp4_rows(name, q, win_kv, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softmax_scale, window,
+                         start_pos, cos, sin, rd, out, workspace, write_ring, ring_mxfp8):
     _gpu(name, q, win_kv, chunk_kv, comp_kv4, attn_sink, idx, cos, sin, out)
     b, n, h, d, ring, k = _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start_pos, cos,
-                                              sin, rd, write_ring)
+                                              sin, rd, write_ring, ring_mxfp8)
     comp_bstride = 0
     if comp_kv4 is not None and n_comp:
         if (comp_kv4.dtype != torch.uint8 or comp_kv4.dim() != 3 or comp_kv4.shape[2] != fp4_row_bytes(d)
@@ -955,7 +1000,13 @@ def sparse_mla_fp4(q, win_kv, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softma
     workspace = _ws(name, workspace, ws_bytes, q.device)
     tail = (_ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, _ptr(workspace) if ws_bytes else None,
             ws_bytes, _stream(q))
-    head = (_ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp_kv4), comp_bstride, n_comp, _ptr(attn_sink), _ptr(idx),
+    if ring_mxfp8:
+        if ring is None:
+            raise ValueError(f"{name}: the MXFP8 ring is required")
+        ring_part = (_ptr(ring), row_stride(ring, name))
+    else:
+        ring_part = (_ptr(ring),)
+    head = (_ptr(q), *ring_part, _ptr(chunk_kv), _ptr(comp_kv4), comp_bstride, n_comp, _ptr(attn_sink), _ptr(idx),
             k, _ptr(o), b)
     if write_ring:
         _call(name, *head, h, d, window, start_pos, float(softmax_scale), *tail)

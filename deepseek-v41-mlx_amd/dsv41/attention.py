@@ -174,7 +174,11 @@ class Attention(torch.nn.Module):
         decode = n == 1
         sel = cidx if cidx is not None and cidx.shape[-1] else None
         rdo = 0 if self._break_rope_inverse else rd
-        if comp_kind == "fp8":
+        if lc.win_kv8 is not None:          # the packed cache: MXFP8 ring, fp4 compressed rows
+            o = _abi.sparse_mla_packed(q, lc.win_kv8, kv, comp if comp_kind == "fp4" else None, n_comp, sink, sel,
+                                       self.softmax_scale, self.window_size, start_pos, cos, sin, rdo,
+                                       write_ring=decode)
+        elif comp_kind == "fp8":
             o = _abi.sparse_mla_fp8(q, lc.win_kv, kv, comp, src.comp_ks[:bsz], src.fp8_rb, n_comp, sink, sel,
                                     self.softmax_scale, self.window_size, start_pos, cos, sin, rdo, write_ring=decode)
         elif comp_kind == "fp4":

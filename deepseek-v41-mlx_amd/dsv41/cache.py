@@ -23,6 +23,10 @@ dequantized in-kernel. The window ring stays in ``dtype``.
 (attention.py:157-163) -- losslessly packed: ``comp_kv4``, rows of d/2 bytes of e2m1 codes then
 d/16 e4m3 scale bytes (288 bytes for 512 channels; ``comp_kv`` is None). The index keys follow
 ``index_format`` (MXFP4 is their lossless packed form), the window ring stays in ``dtype``.
+``cache_format="packed"`` adds the window ring in its lossless packed form: ``win_kv8``, MXFP8
+rows of d e4m3fn codes then d/32 ue8m0 scale bytes (528 bytes for 512 channels; ``win_kv`` is
+None), for window KV that carries the fp8 QAT of attention.py:120-122. The packed stores encode
+their QAT, so with the QAT switched off they quantize at the store.
 
 All buffers are plain torch device tensors with the reference's attribute names. The kernels
 update them in place, so a snapshot must copy: ``lc.win_kv[:]`` -- which in MLX pins the
@@ -43,7 +47,7 @@ from .config import ModelArgs
 
 
 INDEX_FORMATS = ("dense", "mxfp4")
-CACHE_FORMATS = ("dense", "fp8", "fp4")
+CACHE_FORMATS = ("dense", "fp8", "fp4", "packed")
 
 
 class PackedKeys:
@@ -76,7 +80,12 @@ class LayerCache:
         self.ratio = args.compress_ratio(layer_id)
         self.is_kv_source = layer_id in args.kv_source_layers
         self.dtype = dtype
-        self.win_kv = torch.zeros(bsz, self.window, args.head_dim, dtype=dtype, device=device)
+        self.win_kv = self.win_kv8 = None
+        if cache_format == "packed":
+            self.win_kv8 = torch.zeros(bsz, self.window, _abi.mxfp8_row_bytes(args.head_dim), dtype=torch.uint8,
+                                       device=device)
+        else:
+            self.win_kv = torch.zeros(bsz, self.window, args.head_dim, dtype=dtype, device=device)
         self.comp_kv = None
         self.comp_state = None
         self.index_k = None
@@ -91,7 +100,7 @@ class LayerCache:
             if fp8:
                 self.comp_kv8 = torch.zeros(bsz, n_comp, d, dtype=torch.uint8, device=device)
                 self.comp_ks = torch.zeros(bsz, n_blk, d // 32, dtype=torch.uint8, device=device)
-            elif cache_format == "fp4":
+            elif cache_format in ("fp4", "packed"):
                 self.comp_kv4 = torch.zeros(bsz, n_comp, _abi.fp4_row_bytes(d), dtype=torch.uint8, device=device)
             else:
                 self.comp_kv = torch.zeros(bsz, n_comp, d, dtype=dtype, device=device)
@@ -126,16 +135,28 @@ class LayerCache:
             return "fp4", self.comp_kv4[:bsz]
         return "dense", self.comp_kv[:bsz]
 
+    def ring(self):
+        """The window ring as the attention reads it: (kind, tensor), kind "dense" or "mxfp8"."""
+        return ("mxfp8", self.win_kv8) if self.win_kv8 is not None else ("dense", self.win_kv)
+
     def window_chrono(self, pos: int) -> torch.Tensor:
-        """The ring in chronological order: positions [pos - Wp, pos), Wp = min(pos, window)."""
+        """The ring in chronological order: positions [pos - Wp, pos), Wp = min(pos, window).
+        Rows of the packed ring come back as their uint8 MXFP8 rows."""
         w = self.window
+        if self.win_kv8 is not None:
+            wp = min(pos, w)
+            slots = (torch.arange(wp, device=self.win_kv8.device) + (pos - wp)) % w
+            return self.win_kv8[:, slots]
         wp = min(pos, w)
         slots = (torch.arange(wp, device=self.win_kv.device) + (pos - wp)) % w
         return self.win_kv[:, slots]
 
     def write_window(self, pos: int, kv: torch.Tensor) -> None:
         """Write chunk KV at positions [pos, pos+n) into the ring (cache.py:61-67)."""
-        _abi.window_write(self.win_kv, kv.to(self.dtype).contiguous(), pos)
+        if self.win_kv8 is not None:
+            _abi.window_write_mxfp8(self.win_kv8, kv.to(self.dtype).contiguous(), pos)
+        else:
+            _abi.window_write(self.win_kv, kv.to(self.dtype).contiguous(), pos)
 
 
 class ModelCache:
@@ -151,7 +172,7 @@ class ModelCache:
 
 
 _BUFFERS = ("win_kv", "comp_kv", "index_k", "index_k4", "index_ks", "comp_kv8", "comp_ks", "index_k8", "index_k8s",
-            "comp_kv4")
+            "comp_kv4", "win_kv8")
 
 
 def snapshot(cache: ModelCache):

@@ -89,8 +89,8 @@ class StackDecodeStep:
     ``index_q_mx`` (its codes and scales from dsv41_index_q_prep_mxfp4) --, ``w_raw`` [b,1,Hi]
     and ``w_scale``; kv sources add ``latent`` [b,1,D] (pre-rope); key owners add ``k_raw``
     [b,1,Di] and ``k_norm`` [Di]. Caches may be dense, carry MXFP4 index keys, hold the
-    compressed KV packed (cache_format "fp4": e2m1 codes + e4m3 scales per 16 channels), or be
-    the fp8 variant (cache_format "fp8": fp8 compressed KV and index keys, with ue8m0 scales per
+    compressed KV packed (cache_format "fp4": e2m1 codes + e4m3 scales per 16 channels) and the
+    window ring too ("packed": MXFP8 rows), or be the fp8 variant (cache_format "fp8": fp8 compressed KV and index keys, with ue8m0 scales per
     32 channels of each row or of 32-row blocks); each layer takes the kernels that read and
     write its owners' format. Over fp8 keys an index source given ``index_q_mx`` scores on the
     block-scaled fp4 x fp8 MFMA (dsv41_indexer_*_mxq_fp8), else it dequantizes the keys for the
@@ -228,7 +228,11 @@ class StackDecodeStep:
                     _abi.comp_write(x["latent"], lc.comp_kv, nb - 1, p.ratio, p.cos, p.sin, a.rope_head_dim)
                 (comp_kind, comp), n_comp, idx = kv_src.comp_source(b), nb, topk
             # attention + this token's ring write in one launch
-            if comp_kind == "fp8":
+            if lc.win_kv8 is not None:
+                _abi.sparse_mla_packed(x["q"], lc.win_kv8, x["kv"], comp if comp_kind == "fp4" else None, n_comp,
+                                       x["sink"], idx, self.scale, self.window, sp, p.cos, p.sin, a.rope_head_dim,
+                                       out=p.out, workspace=self.workspace, write_ring=True)
+            elif comp_kind == "fp8":
                 _abi.sparse_mla_fp8(x["q"], lc.win_kv, x["kv"], comp, kv_src.comp_ks[:b], kv_src.fp8_rb, n_comp,
                                     x["sink"], idx, self.scale, self.window, sp, p.cos, p.sin, a.rope_head_dim,
                                     out=p.out, workspace=self.workspace, write_ring=True)

@@ -107,6 +107,16 @@ int dsv41_kv_window_prep(void* kv, const float* norm_w, const float* cos_tab,
 int dsv41_window_write(void* win_kv, const void* kv, int32_t bsz, int32_t n, int32_t dim,
                        int32_t window, int32_t start_pos, int32_t dtype, hipStream_t stream);
 
+/* dsv41_window_write into an MXFP8 ring, the lossless packed form of the window KV's fp8 QAT
+ * (attention.py:120-122, fakequant.py:83-93): per row dim e4m3fn codes, then one ue8m0 scale
+ * byte per 32 channels (dim + dim/32 bytes; 528 at dim 512), win_kv8 [bsz, window, row] with
+ * ring_bstride bytes per batch row (a multiple of 8). Each row is stored as
+ * fake_quant_fp8_ue8m0's codes and scales, so decoding gives exactly the QAT values the window KV
+ * already holds (values that do not carry the QAT are quantized by it). */
+int dsv41_window_write_mxfp8(uint8_t* win_kv8, int64_t ring_bstride, const void* kv, int32_t bsz,
+                             int32_t n, int32_t dim, int32_t window, int32_t start_pos, int32_t dtype,
+                             hipStream_t stream);
+
 /* window_idx_matrix, deepseek_v41_mlx/attention.py:40-50: out [n, min(window, wp+n)] int32. */
 int dsv41_window_idx(int32_t* out, int32_t wp, int32_t n, int32_t window, hipStream_t stream);
 
@@ -448,6 +458,28 @@ int dsv41_sparse_mla_fp4_decode(const void* q, void* win_kv, const void* chunk_k
                                 int32_t heads, int32_t dim, int32_t window, int32_t start_pos, float scale,
                                 const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
                                 size_t workspace_bytes, hipStream_t stream);
+
+/* dsv41_sparse_mla_fp4 with the window ring also packed: win_kv8 holds MXFP8 rows in
+ * dsv41_window_write_mxfp8's layout (528 bytes at dim 512), ring_bstride bytes per batch row (> 0,
+ * a multiple of 16). Both packed sources are decoded to bf16 in-kernel, exactly, so the result
+ * equals dsv41_sparse_mla's on the decoded caches. comp_kv4 may be NULL with n_comp = 0 (a
+ * window-only layer). */
+int dsv41_sparse_mla_packed(const void* q, const uint8_t* win_kv8, int64_t ring_bstride,
+                            const void* chunk_kv, const uint8_t* comp_kv4, int64_t comp_bstride, int32_t n_comp,
+                            const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n,
+                            int32_t heads, int32_t dim, int32_t window, int32_t start_pos, float scale,
+                            const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+
+/* dsv41_sparse_mla_packed for one token per row (n = 1) that also performs the ring write of
+ * LayerCache.write_window (cache.py:61-67) into the MXFP8 ring, encoded as
+ * dsv41_window_write_mxfp8 encodes it. */
+int dsv41_sparse_mla_packed_decode(const void* q, uint8_t* win_kv8, int64_t ring_bstride,
+                                   const void* chunk_kv, const uint8_t* comp_kv4, int64_t comp_bstride,
+                                   int32_t n_comp, const float* sink, const int32_t* idx, int32_t k, void* o,
+                                   int32_t bsz, int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
+                                   float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -265,6 +265,27 @@ def fq_fp4_e4m3(x, block: int = 16, dtype: str = "f32") -> np.ndarray:
     return cast(q.reshape(shape), dtype)
 
 
+def mxfp8_encode(x):
+    """MXFP8 rows of fake_quant_fp8_ue8m0(x, 32) over the last dim (fakequant.py:83-93): d
+    e4m3fn codes of x / s, then the d/32 block scales s as ue8m0 bytes (log2(s) + 127).
+    Returns uint8 [..., d + d/32]."""
+    xb = _blockify(x, 32)
+    amax = np.maximum(np.abs(xb).max(axis=-1, keepdims=True), F32(1e-4))
+    s = pow2_ceil_log2(amax * FP8_MAX_INV)
+    q = e4m3_round(np.clip(xb / s, -FP8_MAX, FP8_MAX))
+    codes = e4m3_encode(q).reshape(*np.shape(x)[:-1], -1)
+    scales = ((s.view(np.uint32) >> 23) & 0xFF).astype(np.uint8)[..., 0]
+    return np.concatenate([codes, scales], axis=-1)
+
+
+def mxfp8_decode(rows) -> np.ndarray:
+    """float32 values of mxfp8_encode's rows: e4m3(code) * 2^(scale - 127) per 32 channels."""
+    rows = np.asarray(rows, np.uint8)
+    d = rows.shape[-1] * 32 // 33
+    sc = np.ldexp(np.ones(rows[..., d:].shape, F32), rows[..., d:].astype(np.int32) - 127).astype(F32)
+    return (e4m3_decode(rows[..., :d]) * np.repeat(sc, 32, axis=-1)).astype(F32)
+
+
 def fp4_e4m3_encode(x, block: int = 16):
     """Packed form of fake_quant_fp4_e4m3(x, block) over the last dim (fakequant.py:109-119):
     per row d/2 bytes of e2m1 codes (the rounding of fq_fp4_e4m3 as a 4-bit code, sign in bit 3,

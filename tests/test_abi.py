@@ -204,7 +204,7 @@ def test_rope_frequencies_match_oracle_restatement():
 
 
 @pytest.mark.parametrize("index_format,cache_format", [("dense", "dense"), ("mxfp4", "dense"), ("dense", "fp8"),
-                                                       ("mxfp4", "fp4")])
+                                                       ("mxfp4", "fp4"), ("mxfp4", "packed")])
 def test_cache_snapshot_restore(index_format, cache_format):
     """snapshot() copies every buffer of every cache format (a torch slice would alias the
     buffers the kernels update in place); restore() writes the copies back into the same tensors
@@ -423,3 +423,20 @@ def test_sparse_mla_wrappers_check_buffers(host_abi):
     _refused(call4(q=q.float()), "bf16")
     _refused(call4(chunk_kv=torch.zeros(b, 2, d, dtype=torch.bfloat16), write_ring=True), "chunk kv")
     _refused(call4(win_kv=None, write_ring=True), "window ring")
+    ring8 = torch.zeros(b, W, 528, dtype=torch.uint8)
+
+    def callp(**kw):
+        args = dict(q=q, win_kv8=ring8, chunk_kv=chunk, comp_kv4=packed, n_comp=1000, attn_sink=sink, idx=idx,
+                    softmax_scale=0.1, window=W, start_pos=64, cos=cos, sin=sin, rd=64)
+        args.update(kw)
+        return lambda: A.sparse_mla_packed(**args)
+
+    _reaches_launch(callp())
+    _reaches_launch(callp(write_ring=True))
+    _reaches_launch(callp(comp_kv4=None, n_comp=0, idx=None))
+    _refused(callp(win_kv8=ring), "window ring")                      # a bf16 ring is not MXFP8
+    _refused(callp(win_kv8=ring8[:, :, :512]), "window ring")
+    _refused(callp(win_kv8=None), "window ring")
+    _reaches_launch(lambda: A.window_write_mxfp8(ring8, torch.zeros(b, 3, d, dtype=torch.bfloat16), 5))
+    _refused(lambda: A.window_write_mxfp8(ring8[:1], torch.zeros(b, 3, d, dtype=torch.bfloat16), 5), "batch rows")
+    _refused(lambda: A.window_write_mxfp8(ring, torch.zeros(b, 3, d, dtype=torch.bfloat16), 5), "MXFP8")

@@ -779,6 +779,96 @@ def test_sparse_mla_fp4_cache_equals_bf16_on_decoded_cache(gpu, b, n, window, st
     assert rel_max_diff(to_np(got4), want) < 2e-2
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("n,window,start", [(21, 16, 300), (5, 128, 7), (1, 128, 131071)])
+def test_window_write_mxfp8_ring(gpu, dt, n, window, start):
+    """The MXFP8 ring write stores the oracle's MXFP8 rows of the last min(n, window) chunk rows
+    at slots p % window, byte for byte, and leaves the other slots alone; for window KV carrying
+    the fp8 QAT (the GPU's own kv_window_prep output) the rows decode to that KV exactly."""
+    from dsv41 import _abi
+    rng = rng_for(f"w8ring{dt}{n}{start}")
+    rc, rs = R.precompute_freqs_cis(64, start + n + 1, 65536, 160000.0, 16.0, 32, 1)
+    b, d = 3, 512
+    kv = R.cast(rng.standard_normal((b, n, d)).astype(F32) * 3, dt)
+    t = dev(kv, dt)
+    _abi.kv_window_prep(t, dev(np.ones(d, F32)), dev(rc), dev(rs), 64, start, 1e-20)   # carries the QAT
+    for src in (dev(kv, dt), t):
+        ring = torch.full((b, window, _abi.mxfp8_row_bytes(d)), 0x5A, dtype=torch.uint8, device=gpu)
+        _abi.window_write_mxfp8(ring, src, start)
+        torch.cuda.synchronize()
+        got, x = ring.cpu().numpy(), to_np(src)
+        keep = min(n, window)
+        want = np.full_like(got, 0x5A)
+        for j in range(n - keep, n):
+            want[:, (start + j) % window] = R.mxfp8_encode(x[:, j])
+        assert np.array_equal(got, want)
+    slots = [(start + j) % window for j in range(n - keep, n)]
+    dec = R.mxfp8_decode(got[:, slots])
+    assert np.array_equal(dec.view(np.uint32), to_np(t)[:, n - keep:].view(np.uint32))
+
+
+def _mxfp8_ring(rng, b, window, d):
+    """MXFP8 ring rows: e4m3 codes without the NaN patterns, ue8m0 scales 2^-4 .. 2^3."""
+    codes = rng.integers(0, 256, size=(b, window, d), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] ^= 0x01
+    scales = rng.integers(123, 131, size=(b, window, d // 32), dtype=np.uint8)
+    return np.concatenate([codes, scales], axis=-1)
+
+
+@pytest.mark.parametrize("b,n,window,start,n_comp,k", [
+    (8, 1, 128, 40000, 9000, 1000),         # decode, split index lists
+    (4, 1, 128, 60, 15, 15),                # ring still filling
+    (3, 1, 128, 300, 0, 0),                 # a window-only layer
+    (1, 600, 16, 200, 150, 64),             # >= 512 queries: the 64-head plan
+])
+def test_sparse_mla_packed_equals_bf16_on_decoded_caches(gpu, b, n, window, start, n_comp, k):
+    """MXFP8 window ring and packed fp4 compressed rows, both decoded in-kernel: bit-identical to
+    the bf16 path on the decoded caches; the decode form's ring store writes the token's MXFP8 row
+    and nothing else; within the bf16 tolerance of the oracle."""
+    from dsv41 import _abi
+    rng = rng_for(f"mlap{b}{n}{start}")
+    h, d, rd = 64, 512, 64
+    rc, rs = R.precompute_freqs_cis(rd, start + n + 1, 65536, 160000.0, 16.0, 32, 1)
+    q = R.cast(rng.standard_normal((b, n, h, d)).astype(F32) * 2, "bf16")
+    ring8 = _mxfp8_ring(rng, b, window, d)
+    win = R.mxfp8_decode(ring8)
+    assert np.array_equal(R.cast(win, "bf16"), win)
+    chunk = R.fq_fp8_ue8m0(R.cast(rng.standard_normal((b, n, d)).astype(F32), "bf16"), 32, "bf16")
+    rows4 = _fp4_cache(rng, b, n_comp + 5, d)
+    comp = R.fp4_e4m3_decode(rows4)
+    sink = rng.standard_normal(h).astype(F32)
+    wp = min(start, window)
+    cidx = None
+    if k:
+        lens = R.query_lens(start, n, 4)
+        cidx = np.sort(rng.integers(0, n_comp, size=(b, n, k)), axis=-1)
+        cidx = np.where(cidx < np.minimum(lens, n_comp)[None, :, None], cidx + wp + n, -1).astype(np.int32)
+        cidx[:, :, ::5] = -1
+    idx_t = torch.as_tensor(cidx).to(gpu) if k else None
+    args = (d ** -0.5, window, start, dev(rc), dev(rs), rd)
+    r8 = torch.as_tensor(ring8).to(gpu)
+    c4 = torch.as_tensor(rows4).to(gpu) if n_comp else None
+    got = _abi.sparse_mla_packed(dev(q, "bf16"), r8, dev(chunk, "bf16"), c4, n_comp, dev(sink), idx_t, *args)
+    ref = _abi.sparse_mla(dev(q, "bf16"), dev(win, "bf16"), dev(chunk, "bf16"),
+                          dev(comp, "bf16") if n_comp else None, n_comp, dev(sink), idx_t, *args)
+    assert torch.equal(got, ref)
+    if n == 1:
+        r8d = r8.clone()
+        o = _abi.sparse_mla_packed(dev(q, "bf16"), r8d, dev(chunk, "bf16"), c4, n_comp, dev(sink), idx_t, *args,
+                                   write_ring=True)
+        assert torch.equal(o, got)
+        want_ring = ring8.copy()
+        want_ring[:, start % window] = R.mxfp8_encode(chunk[:, 0])
+        assert np.array_equal(r8d.cpu().numpy(), want_ring)
+    kv_all = _concat_reference(win, chunk, comp, n_comp, start, window)
+    widx = np.broadcast_to(R.window_idx_matrix(wp, n, window)[None], (b, n, min(window, wp + n)))
+    full = np.concatenate([widx, cidx], axis=-1) if k else widx
+    o = R.sparse_attn(q, kv_all, sink, np.ascontiguousarray(full), d ** -0.5, dtype="bf16")
+    pos = start + np.arange(n)
+    want = R.rope_tail(o, rd, rc[pos], rs[pos], inverse=True, dtype="bf16")
+    assert rel_max_diff(to_np(got), want) < 2e-2
+
+
 def test_reference_kernel_module_seam(gpu):
     """dsv41.kernel stands in for the reference model's native `kernel` module."""
     import dsv41.kernel as K

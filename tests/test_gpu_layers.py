@@ -100,11 +100,13 @@ def test_topology_battery(gpu, qat, topology, qat_restore):
     assert tol(chk_g, full_o), f"chunked vs oracle {max_abs(chk_g, full_o):.3e}"
 
 
-def test_packed_fp4_cache_stack_equals_dense_cache(gpu):
-    """The release topology in bf16 (512-channel latents) over a packed fp4 compressed cache:
-    every output of a chunked prefill and the decode steps after it is bit-identical to the run
-    over the dense cache, and each owner's packed rows decode to its dense rows (the packed form
-    is lossless for the fp4/e4m3 QAT values attention.py:157-163 stores)."""
+@pytest.mark.parametrize("cache_format", ["fp4", "packed"])
+def test_packed_cache_stack_equals_dense_cache(gpu, cache_format):
+    """The release topology in bf16 (512-channel latents) over a packed fp4 compressed cache
+    ("fp4") and also an MXFP8 window ring ("packed"): every output of a chunked prefill and the
+    decode steps after it is bit-identical to the run over the dense cache, each owner's packed
+    rows decode to its dense rows and each packed ring to the dense ring (the packed forms are
+    lossless for the QAT values attention.py:120-122 and 157-163 store)."""
     cfg = dict(RELEASE_TOY, head_dim=512, rope_head_dim=64, index_head_dim=128)
     a, st, _ = _stacks(cfg, "bf16", SEED_BASE + 6, gpu)
     rng = np.random.default_rng(SEED_BASE + 6)
@@ -113,7 +115,7 @@ def test_packed_fp4_cache_stack_equals_dense_cache(gpu):
     dev = lambda x: torch.from_numpy(x).to(gpu).to(torch.bfloat16)   # noqa: E731
     splits = [(0, 17), (17, 30)] + [(t, t + 1) for t in range(30, T)]
     c16 = st.make_cache(2, a.max_seq_len)
-    c4 = st.make_cache(2, a.max_seq_len, cache_format="fp4")
+    c4 = st.make_cache(2, a.max_seq_len, cache_format=cache_format)
     o16 = _run(st, h, c16, splits, dev)
     o4 = _run(st, h, c4, splits, dev)
     assert np.array_equal(o4.view(np.uint32), o16.view(np.uint32))
@@ -122,6 +124,13 @@ def test_packed_fp4_cache_stack_equals_dense_cache(gpu):
         assert c4.layers[l].comp_kv is None and c16.layers[l].comp_kv4 is None
         got = R.fp4_e4m3_decode(c4.layers[l].comp_kv4[:, :n].cpu().numpy())
         assert np.array_equal(got.view(np.uint32), to_np(c16.layers[l].comp_kv[:, :n]).view(np.uint32)), l
+    for l, (lp, ld) in enumerate(zip(c4.layers, c16.layers)):
+        if cache_format == "packed":
+            assert lp.win_kv is None
+            got = R.mxfp8_decode(lp.win_kv8.cpu().numpy())
+            assert np.array_equal(got.view(np.uint32), to_np(ld.win_kv).view(np.uint32)), l
+        else:
+            assert lp.win_kv8 is None and torch.equal(lp.win_kv, ld.win_kv)
 
 
 def test_negative_controls_move_the_output(gpu):

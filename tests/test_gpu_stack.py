@@ -46,7 +46,7 @@ def _record_decode(stack, h, cache):
                                           "indexer_score_mxfp4", "index_key_publish_mxfp4", "sparse_mla_fp8",
                                           "indexer_score_fp8", "comp_write_fp8", "index_key_publish_fp8",
                                           "indexer_topk", "indexer_topk_fp8", "indexer_topk_mxfp4", "sparse_mla_fp4",
-                                          "comp_write_fp4")}
+                                          "comp_write_fp4", "sparse_mla_packed")}
 
     def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, *a, **k):
         r = recs[layer[0]]
@@ -72,6 +72,14 @@ def _record_decode(stack, h, cache):
         r = recs[layer[0]]
         r.update(q=q.clone(), kv=chunk_kv.clone(), sink=attn_sink.clone())
         o = orig["sparse_mla_fp4"](q, win_kv, chunk_kv, comp4, n_comp, attn_sink, idx, *a, **k)
+        r["out"] = o.clone()
+        layer[0] += 1
+        return o
+
+    def sparse_mla_packed(q, win_kv8, chunk_kv, comp4, n_comp, attn_sink, idx, *a, **k):
+        r = recs[layer[0]]
+        r.update(q=q.clone(), kv=chunk_kv.clone(), sink=attn_sink.clone())
+        o = orig["sparse_mla_packed"](q, win_kv8, chunk_kv, comp4, n_comp, attn_sink, idx, *a, **k)
         r["out"] = o.clone()
         layer[0] += 1
         return o
@@ -126,7 +134,8 @@ def _record_decode(stack, h, cache):
                  ("indexer_score_fp8", indexer_score_fp8), ("comp_write_fp8", comp_write_fp8),
                  ("index_key_publish_fp8", index_key_publish_fp8), ("indexer_topk", indexer_topk),
                  ("indexer_topk_fp8", indexer_topk_fp8), ("indexer_topk_mxfp4", indexer_topk_mxfp4),
-                 ("sparse_mla_fp4", sparse_mla_fp4), ("comp_write_fp4", comp_write_fp4)):
+                 ("sparse_mla_fp4", sparse_mla_fp4), ("comp_write_fp4", comp_write_fp4),
+                 ("sparse_mla_packed", sparse_mla_packed)):
         setattr(_abi, n, f)
     try:
         stack(h, cache)
@@ -138,25 +147,25 @@ def _record_decode(stack, h, cache):
 
 
 @pytest.mark.parametrize("topology,index_format,T", [
-    ("c4", "dense", 40), ("c4", "mxfp4", 40), ("c4", "fp8", 40), ("c4", "fp4", 40),
+    ("c4", "dense", 40), ("c4", "mxfp4", 40), ("c4", "fp8", 40), ("c4", "fp4", 40), ("c4", "packed", 40),
     ("release", "dense", 40), ("release", "dense", 39), ("release", "fp8", 40), ("release", "mxfp4", 39),
-    ("release", "fp4", 39)])
+    ("release", "fp4", 39), ("release", "packed", 40)])
 def test_stack_step_reproduces_attention_stack(gpu, topology, index_format, T):
     """Toy C4 topology (ratio 4) or the release's ratios (0,0,2,2,2,1,1,1) in bf16: T-1 prefill
     tokens, then the decode token at position T-1. At T = 40 it completes a group at every ratio
     (owners write a latent and a key); at T = 39 the ratio-2 group stays open (its compressor
     state carries) while the ratio-1 owner writes. Dense or MXFP4 index caches, the fp8 cache
-    variant (fp8 compressed KV and index keys), or the packed fp4 compressed KV with MXFP4 index
-    keys ("fp4"). The packed formats use the widths their kernels take (128-channel index keys;
-    fp8 and fp4 latents of 512)."""
+    variant (fp8 compressed KV and index keys), the packed fp4 compressed KV with MXFP4 index
+    keys ("fp4"), and that with an MXFP8 window ring ("packed"). The packed formats use the widths
+    their kernels take (128-channel index keys; fp8 and fp4 latents of 512)."""
     from dsv41.model import AttentionStack
     from dsv41.step import StackDecodeStep
     base = C4_TOY if topology == "c4" else RELEASE_TOY
     # MXFP4 index caches: the fp4 MFMA kernels take 16/32/64 heads of 128 channels
     cfg = dict(base, index_head_dim=128, index_n_heads=16) if index_format == "mxfp4" else base
-    if index_format in ("fp8", "fp4"):
+    if index_format in ("fp8", "fp4", "packed"):
         cfg = dict(base, index_head_dim=128, head_dim=512, rope_head_dim=64)
-    if index_format == "fp4":
+    if index_format in ("fp4", "packed"):
         cfg = dict(cfg, index_n_heads=16)
     a = args(cfg)
     st = AttentionStack(model_args(cfg), torch.bfloat16, gpu)
@@ -166,8 +175,8 @@ def test_stack_step_reproduces_attention_stack(gpu, topology, index_format, T):
     h = torch.from_numpy(rng.standard_normal((b, T, a.dim)).astype(F32)).to(gpu).to(torch.bfloat16)
     if index_format == "fp8":
         cache = st.make_cache(b, a.max_seq_len, cache_format="fp8")
-    elif index_format == "fp4":
-        cache = st.make_cache(b, a.max_seq_len, "mxfp4", cache_format="fp4")
+    elif index_format in ("fp4", "packed"):
+        cache = st.make_cache(b, a.max_seq_len, "mxfp4", cache_format=index_format)
     else:
         cache = st.make_cache(b, a.max_seq_len, index_format)
     st(h[:, :T - 1], cache)

@@ -223,6 +223,37 @@ def test_packed_fp4_e4m3_decodes_to_the_fake_quant_known_answers(n):
     assert np.array_equal(R.fp4_e4m3_encode(got), rows)
 
 
+@pytest.mark.parametrize("n", [0, 1, 2])
+def test_mxfp8_rows_decode_to_the_fp8_fake_quant_known_answers(n):
+    """MXFP8 ring rows (e4m3 codes + ue8m0 bytes per 32 channels) are a lossless form of
+    fake_quant_fp8_ue8m0: decoding the encoding of the known-answer inputs gives the known
+    answers bit for bit, and encoding the known answers again (what the ring store does with
+    window KV that already carries the QAT) decodes to them unchanged."""
+    d = np.load(GOLDEN)
+    x, want = d[f"x{n}"], d[f"fp8_ue8m0_{n}"]
+    rows = R.mxfp8_encode(x)
+    assert rows.shape[-1] == x.shape[-1] + x.shape[-1] // 32 and rows.dtype == np.uint8
+    assert np.array_equal(R.mxfp8_decode(rows).view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(R.mxfp8_decode(R.mxfp8_encode(want)).view(np.uint32), want.view(np.uint32))
+
+
+def test_mxfp8_reencoding_a_halved_block_scale():
+    """A block whose largest value rounds down to 224 * s under the QAT has, re-encoded, the
+    scale s / 2: its codes move one binade up and every value still decodes exactly; the
+    layout holds channel c's code at byte c and the block scale after the codes."""
+    x = np.zeros((1, 64), F32)
+    x[0, 0], x[0, 1], x[0, 5] = 228.0, -3.0, 1e-3          # block 0: s = 1, 228 -> 224
+    x[0, 32], x[0, 33] = 1.0, -0.5                          # block 1: s = 2^-8
+    q = R.fq_fp8_ue8m0(x, 32)
+    assert q[0, 0] == 224.0
+    r1, r2 = R.mxfp8_encode(x)[0], R.mxfp8_encode(q)[0]
+    assert r1[64] == 127 and r2[64] == 126                  # the scale halves on re-encoding
+    assert r1[65] == r2[65] == 127 - 8
+    assert r1[32] == 0x78 and r1[33] == 0xF0                # 256 = 2^8, -128 = -2^7
+    assert np.array_equal(R.mxfp8_decode(r2[None])[0], q[0]) and np.array_equal(R.mxfp8_decode(r1[None])[0], q[0])
+    assert r2[0] == R.e4m3_encode(np.float32(448.0)) and r1[0] == R.e4m3_encode(np.float32(224.0))
+
+
 def test_e4m3_codes_against_torch_float8():
     """e4m3_decode of every byte equals torch's float8_e4m3fn reading of it, and e4m3_encode
     inverts it on every finite code."""
