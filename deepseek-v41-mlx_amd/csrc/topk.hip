@@ -211,11 +211,18 @@ __global__ __launch_bounds__(kSelThreads) void topk_merge_kernel(const uint32_t*
   const int lens = (start_pos + s + 1) / ratio;
   const int i0 = threadIdx.x * J;
   const int nvalid = min(max(m - i0, 0), J);
+  // keys and positions are loaded together: the selection's output step then reads no memory
   uint32_t key[J];
+  int32_t pos[J];
 #pragma unroll
-  for (int j = 0; j < J; ++j) key[j] = j < nvalid ? kr[i0 + j] : 0u;
+  for (int j = 0; j < J; ++j) {
+    key[j] = j < nvalid ? kr[i0 + j] : 0u;
+    pos[j] = j < nvalid ? pr[i0 + j] : 0;
+  }
   select_top<J>(key, nvalid, k, sh, [&](uint32_t rank, int j) {
-    const int i = pr[i0 + j];
+    int32_t i = 0;
+#pragma unroll
+    for (int t = 0; t < J; ++t) i = t == j ? pos[t] : i;   // j is a run-time index
     o[rank] = i < lens ? i + offset : -1;
   });
 }
