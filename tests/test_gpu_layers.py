@@ -214,6 +214,8 @@ def test_c2_decode_step(gpu):
     (32, 16384, 512, 65535),     # bs32, 64K context: 8 row ranges of 2048 per query
     (64, 16384, 512, 65535),     # B=64: 4 ranges of 4096
     (32, 4096, 128, 16386),      # ranges of 512, top-128; 3 tokens of the next group still open
+    (16, 32768, 512, 131071),    # 16 ranges of 2048: a merge over 8,192 candidates per query
+    (256, 8192, 128, 32767),     # 512 (query, head group) units: the attention's unsplit plan
 ])
 def test_decode_step_fused_equals_two_calls(gpu, b, nb, K, start):
     """The decode step with the fused indexer + top-k form selects exactly what indexer_score +
