@@ -759,13 +759,15 @@ def cpu_baseline(s: Shape, sets, cos, sin, ws, seconds, torch):
         sc = R.indexer_scores(iq, ik, R.cast(w * np.float32(ws), "bf16"), s.start, s.r)
         idx = R.topk_indices(sc, s.K, lens, s.wp + 1)
         kv_all = np.concatenate([win[:, wslots], chunk, comp], axis=1)
+        q = R.rope_tail(q, s.rd, rc, rsn, dtype="bf16")
         o = R.sparse_attn(q, kv_all, sink, np.concatenate([widx, idx], -1), s.D ** -0.5, dtype="bf16")
         R.rope_tail(o, s.rd, rc, rsn, inverse=True, dtype="bf16")
         el += time.perf_counter() - t0
         rows += 1
     threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
     return {"value": rows / el, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{rows} batch rows of the bs32/64K decode step (indexer + top-k + sparse MLA + inverse rope), "
+            "sample": f"{rows} batch rows of the bs32/64K decode step (indexer + top-k + q rope + sparse MLA + "
+                      f"inverse rope), "
                       f"numpy float32 oracle, BLAS threads {threads}, host cpu_count {os.cpu_count()}, "
                       f"{el:.1f} s of compute (row copies to the host untimed)"}
 

@@ -147,6 +147,17 @@ __device__ __forceinline__ uint32_t mxfp4_encode(const float* v, float amax, uin
   return (__float_as_uint(s) >> 23) & 0xFFu;
 }
 
+// Rotation of the adjacent pair (x0, x1) by (c, s): x0 c - x1 s, x0 s + x1 c, each product and
+// each sum rounded to fp32 on its own as the reference's separate float32 array operations round
+// them. Contraction is off here: hipcc fuses a product into the following add by default, and a
+// fused multiply-add rounds once where this arithmetic rounds twice.
+__device__ __forceinline__ void rotate_pair(float& x0, float& x1, float c, float s) {
+#pragma clang fp contract(off)
+  const float xr = x0, xi = x1;
+  x0 = xr * c - xi * s;
+  x1 = xr * s + xi * c;
+}
+
 // ------------------------------------------------------------------ wave helpers
 
 __device__ __forceinline__ float wave_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }

@@ -196,10 +196,9 @@ __global__ __launch_bounds__(256) void row_pipeline_kernel(RowArgs a) {
 #pragma unroll
     for (int j = 0; j < EPT / 2; ++j) {
       if (e0 + 2 * j >= first) {
-        const float s_ = a.inverse ? -sn[j] : sn[j];
-        const float xr = v[2 * j], xi = v[2 * j + 1];
-        v[2 * j] = io<T>::rnd(__fsub_rn(__fmul_rn(xr, cs[j]), __fmul_rn(xi, s_)));
-        v[2 * j + 1] = io<T>::rnd(__fadd_rn(__fmul_rn(xr, s_), __fmul_rn(xi, cs[j])));
+        rotate_pair(v[2 * j], v[2 * j + 1], cs[j], a.inverse ? -sn[j] : sn[j]);
+        v[2 * j] = io<T>::rnd(v[2 * j]);
+        v[2 * j + 1] = io<T>::rnd(v[2 * j + 1]);
       }
     }
   }

@@ -45,6 +45,7 @@ struct MlaArgs {
   const float* cos_tab;
   const float* sin_tab;
   int rd, start_pos;
+  int q_rd;           // > 0: apply q's forward rope tail of this width while loading q
   int hgroups, splits, per_split;
   bf16_t* part_o;     // split partials: numerator / denominator, rounded to bf16, in 16 x 16 tiles
                       // (part_tile: [unit][split][head tile][dim / 16][16 heads][16 channels])
@@ -145,9 +146,7 @@ __device__ __forceinline__ int window_count(const KvSrc& s, int qs) {
 
 // inverse rope: rotate the adjacent pair (x0, x1) by the conjugate of (cs, sn)
 __device__ __forceinline__ void rope_inv_apply(float cs, float sn_neg, float& x0, float& x1) {
-  const float xr = x0, xi = x1;
-  x0 = __fsub_rn(__fmul_rn(xr, cs), __fmul_rn(xi, sn_neg));
-  x1 = __fadd_rn(__fmul_rn(xr, sn_neg), __fmul_rn(xi, cs));
+  rotate_pair(x0, x1, cs, sn_neg);
 }
 
 __device__ __forceinline__ bool in_rope_tail(const MlaArgs& a, int D, int d) { return a.rd > 0 && d >= D - a.rd; }
@@ -172,6 +171,29 @@ __device__ __forceinline__ void rope_inv_pair(const MlaArgs& a, int D, int qs, i
     x0 = round_bf16(x0);
     x1 = round_bf16(x1);
   }
+}
+
+// Forward rope of the query tail (rope_tail(q, rd, cos, sin), attention.py:117) applied as q is
+// loaded: the adjacent pair at channel d (even) of query qs, when d lies in the last q_rd
+// channels, turns by (cos, sin) at position start_pos + qs with dsv41_rope_tail's arithmetic
+// (rotate_pair).
+__device__ __forceinline__ void rope_q_pair(const MlaArgs& a, int D, int qs, int d, float& x0, float& x1) {
+  if (a.q_rd <= 0 || d < D - a.q_rd) return;
+  const int half = a.q_rd >> 1;
+  const int p = (d - (D - a.q_rd)) >> 1;
+  const int64_t pos = (int64_t)a.start_pos + qs;
+  rotate_pair(x0, x1, a.cos_tab[pos * half + p], a.sin_tab[pos * half + p]);
+}
+
+// The same on 8 consecutive bf16 channels c0.. of one query head (c0 a multiple of 8), each
+// rotated value rounded to bf16 (channels outside the tail convert back unchanged).
+__device__ __forceinline__ bf16x8 rope_q8(const MlaArgs& a, int D, int qs, int c0, bf16x8 x) {
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (float)x[i];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) rope_q_pair(a, D, qs, c0 + 2 * j, v[2 * j], v[2 * j + 1]);
+  return cvt_bf16x8(v);
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -371,6 +393,13 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
         reinterpret_cast<const bf16_t*>(a.q) + ((int64_t)unit * a.heads + (hok ? h : 0)) * D + dh * DSL;
 #pragma unroll
     for (int ks = 0; ks < KSS; ++ks) qb[ks] = hok ? ld_bf16x8(qrow + ks * 32 + 8 * g) : zero_bf16x8();
+    if (a.q_rd > 0 && hok) {
+#pragma unroll
+      for (int ks = 0; ks < KSS; ++ks) {
+        const int c0 = dh * DSL + ks * 32 + 8 * g;
+        if (c0 + 8 > D - a.q_rd) qb[ks] = rope_q8(a, D, qs, c0, qb[ks]);
+      }
+    }
   }
   const float sl2 = a.scale * kLog2e;
   // m_run: the exponent reference of acc and l_run, shared by the 4 lane groups of a head.
@@ -656,9 +685,16 @@ __global__ __launch_bounds__(256) void mla_f32_kernel(MlaArgs a) {
   const int wc = window_count(S, qs);
   const int L = wc + S.k;
   const float* qrow = reinterpret_cast<const float*>(a.q) + (int64_t)unit * a.heads * D;
-  for (int i = tid; i < kF32Heads * D; i += 256) {
-    const int h = hbase + i / D;
-    q_l[i] = h < a.heads ? qrow[(int64_t)h * D + i % D] : 0.0f;
+  for (int i = 2 * tid; i < kF32Heads * D; i += 512) {   // adjacent pairs: D is even
+    const int h = hbase + i / D, d = i % D;
+    float x0 = 0.0f, x1 = 0.0f;
+    if (h < a.heads) {
+      x0 = qrow[(int64_t)h * D + d];
+      x1 = qrow[(int64_t)h * D + d + 1];
+      rope_q_pair(a, D, qs, d, x0, x1);
+    }
+    q_l[i] = x0;
+    q_l[i + 1] = x1;
   }
   if (tid < kF32Heads) {
     const int h = hbase + tid;
@@ -913,8 +949,8 @@ extern "C" int dsv41_sparse_attn(const void* q, const void* kv, const float* sin
 static int sparse_mla_layer(const char* what, const void* q, const void* win_kv, const void* chunk_kv,
                             const void* comp_kv, int64_t comp_bstride, int32_t n_comp, const float* sink,
                             const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads, int32_t dim,
-                            int32_t window, int32_t start_pos, float scale, const float* cos_tab,
-                            const float* sin_tab, int32_t rd, int32_t dtype, void* workspace, size_t workspace_bytes,
+                            int32_t window, int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab,
+                            int32_t rd, int32_t q_rd, int32_t dtype, void* workspace, size_t workspace_bytes,
                             bool write_ring, hipStream_t stream) {
   const int wp = start_pos < window ? start_pos : window;
   DSV41_REQUIRE(q && chunk_kv && sink && o && (idx || k == 0) && (win_kv || wp == 0) && (comp_kv || n_comp == 0),
@@ -928,6 +964,9 @@ static int sparse_mla_layer(const char* what, const void* q, const void* win_kv,
                 DSV41_E_ARG, "%s: tensors must be 16-byte aligned", what);
   DSV41_REQUIRE(comp_bstride % 8 == 0, DSV41_E_ARG, "%s: comp_bstride must be a multiple of 8", what);
   DSV41_REQUIRE(rd == 0 || (cos_tab && sin_tab && rd % 2 == 0 && rd <= dim), DSV41_E_ARG, "%s: bad rope tail", what);
+  DSV41_REQUIRE(q_rd == 0 || (q_rd > 0 && cos_tab && sin_tab && q_rd % 2 == 0 && q_rd <= dim &&
+                              (rd == 0 || rd == q_rd)),
+                DSV41_E_ARG, "%s: bad query rope tail (q_rd %d, rd %d)", what, q_rd, rd);
   MlaArgs a{};
   a.q = q; a.o = o; a.sink = sink;
   a.src.ring = win_kv; a.src.ring_bstride = (int64_t)window * dim; a.src.window = window; a.src.wp = wp;
@@ -936,7 +975,7 @@ static int sparse_mla_layer(const char* what, const void* q, const void* win_kv,
   a.src.comp = comp_kv; a.src.comp_bstride = comp_bstride; a.src.n_comp = n_comp;
   a.src.idx = idx; a.src.k = k; a.src.win_implicit = 1;
   a.m = n; a.heads = heads; a.dim = dim; a.scale = scale;
-  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.start_pos = start_pos;
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.q_rd = q_rd; a.start_pos = start_pos;
   if (write_ring) {
     DSV41_REQUIRE(n == 1 && win_kv, DSV41_E_ARG, "%s: the ring store needs one token per row and a ring", what);
     a.ring_w = const_cast<void*>(win_kv);
@@ -949,9 +988,10 @@ extern "C" int dsv41_sparse_mla(const void* q, const void* win_kv, const void* c
                                 int64_t comp_bstride, int32_t n_comp, const float* sink, const int32_t* idx, int32_t k,
                                 void* o, int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t window,
                                 int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
-                                int32_t dtype, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                                int32_t q_rd, int32_t dtype, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream) {
   return sparse_mla_layer("dsv41_sparse_mla", q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp, sink, idx, k, o, bsz,
-                          n, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, dtype, workspace,
+                          n, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, q_rd, dtype, workspace,
                           workspace_bytes, false, stream);
 }
 
@@ -959,10 +999,10 @@ extern "C" int dsv41_sparse_mla_decode(const void* q, void* win_kv, const void* 
                                        int64_t comp_bstride, int32_t n_comp, const float* sink, const int32_t* idx,
                                        int32_t k, void* o, int32_t bsz, int32_t heads, int32_t dim, int32_t window,
                                        int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab,
-                                       int32_t rd, int32_t dtype, void* workspace, size_t workspace_bytes,
+                                       int32_t rd, int32_t q_rd, int32_t dtype, void* workspace, size_t workspace_bytes,
                                        hipStream_t stream) {
   return sparse_mla_layer("dsv41_sparse_mla_decode", q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp, sink, idx, k,
-                          o, bsz, 1, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, dtype, workspace,
+                          o, bsz, 1, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, q_rd, dtype, workspace,
                           workspace_bytes, true, stream);
 }
 
@@ -1001,12 +1041,12 @@ static int scratch_of_current_device(const char* what, void** out) {
   return 0;
 }
 
-extern "C" int dsv41_sparse_mla_decode_noalloc(const void* q, void* win_kv, const void* chunk_kv,
-                                               const void* comp_kv, int64_t comp_bstride, int32_t n_comp,
-                                               const float* sink, const int32_t* idx, int32_t k, void* o,
-                                               int32_t bsz, int32_t heads, int32_t dim, int32_t window,
-                                               int32_t start_pos, float scale, const float* cos_tab,
-                                               const float* sin_tab, int32_t rd, int32_t dtype, hipStream_t stream) {
+extern "C" int dsv41_sparse_mla_decode_noalloc(const void* q, void* win_kv, const void* chunk_kv, const void* comp_kv,
+                                               int64_t comp_bstride, int32_t n_comp, const float* sink,
+                                               const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t heads,
+                                               int32_t dim, int32_t window, int32_t start_pos, float scale,
+                                               const float* cos_tab, const float* sin_tab, int32_t rd, int32_t q_rd,
+                                               int32_t dtype, hipStream_t stream) {
   const char* what = "dsv41_sparse_mla_decode_noalloc";
   const int wp = start_pos < window ? start_pos : window;
   const int weff = window < wp + 1 ? window : wp + 1;
@@ -1021,17 +1061,17 @@ extern "C" int dsv41_sparse_mla_decode_noalloc(const void* q, void* win_kv, cons
     int rc = scratch_of_current_device(what, &ws);
     if (rc) return rc;
   }
-  return sparse_mla_layer(what, q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp, sink, idx, k, o, bsz, 1, heads,
-                          dim, window, start_pos, scale, cos_tab, sin_tab, rd, dtype, ws, need, true, stream);
+  return sparse_mla_layer(what, q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp, sink, idx, k, o, bsz, 1, heads, dim,
+                          window, start_pos, scale, cos_tab, sin_tab, rd, q_rd, dtype, ws, need, true, stream);
 }
 
 static int sparse_mla_fp8_layer(const char* what, const void* q, const void* win_kv, const void* chunk_kv,
-                                const uint8_t* comp_kv, int64_t comp_bstride, int32_t n_comp,
-                                const uint8_t* comp_scale, int64_t comp_scale_bstride, int32_t comp_scale_rb,
-                                const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n,
-                                int32_t heads, int32_t dim, int32_t window, int32_t start_pos, float scale,
-                                const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
-                                size_t workspace_bytes, bool write_ring, hipStream_t stream) {
+                                const uint8_t* comp_kv, int64_t comp_bstride, int32_t n_comp, const uint8_t* comp_scale,
+                                int64_t comp_scale_bstride, int32_t comp_scale_rb, const float* sink,
+                                const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads,
+                                int32_t dim, int32_t window, int32_t start_pos, float scale, const float* cos_tab,
+                                const float* sin_tab, int32_t rd, int32_t q_rd, void* workspace, size_t workspace_bytes,
+                                bool write_ring, hipStream_t stream) {
   const int wp = start_pos < window ? start_pos : window;
   DSV41_REQUIRE(q && chunk_kv && sink && o && (idx || k == 0) && (win_kv || wp == 0) &&
                     ((comp_kv && comp_scale) || n_comp == 0),
@@ -1049,6 +1089,9 @@ static int sparse_mla_fp8_layer(const char* what, const void* q, const void* win
   DSV41_REQUIRE(comp_bstride % 16 == 0 && comp_scale_bstride % 16 == 0, DSV41_E_ARG,
                 "%s: comp_bstride and comp_scale_bstride must be multiples of 16 bytes", what);
   DSV41_REQUIRE(rd == 0 || (cos_tab && sin_tab && rd % 2 == 0 && rd <= dim), DSV41_E_ARG, "%s: bad rope tail", what);
+  DSV41_REQUIRE(q_rd == 0 || (q_rd > 0 && cos_tab && sin_tab && q_rd % 2 == 0 && q_rd <= dim &&
+                              (rd == 0 || rd == q_rd)),
+                DSV41_E_ARG, "%s: bad query rope tail (q_rd %d, rd %d)", what, q_rd, rd);
   MlaArgs a{};
   a.q = q; a.o = o; a.sink = sink;
   a.src.ring = win_kv; a.src.ring_bstride = (int64_t)window * dim; a.src.window = window; a.src.wp = wp;
@@ -1058,7 +1101,7 @@ static int sparse_mla_fp8_layer(const char* what, const void* q, const void* win
   a.src.comp_scale = comp_scale; a.src.comp_scale_bstride = comp_scale_bstride; a.src.comp_scale_rb = comp_scale_rb;
   a.src.idx = idx; a.src.k = k; a.src.win_implicit = 1;
   a.m = n; a.heads = heads; a.dim = dim; a.scale = scale;
-  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.start_pos = start_pos;
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.q_rd = q_rd; a.start_pos = start_pos;
   if (write_ring) {
     DSV41_REQUIRE(n == 1 && win_kv, DSV41_E_ARG, "%s: the ring store needs one token per row and a ring", what);
     a.ring_w = const_cast<void*>(win_kv);
@@ -1075,7 +1118,7 @@ static int sparse_mla_fp4_layer(const char* what, const void* q, const void* win
                                 const uint8_t* comp_kv4, int64_t comp_bstride, int32_t n_comp, const float* sink,
                                 const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads,
                                 int32_t dim, int32_t window, int32_t start_pos, float scale, const float* cos_tab,
-                                const float* sin_tab, int32_t rd, void* workspace, size_t workspace_bytes,
+                                const float* sin_tab, int32_t rd, int32_t q_rd, void* workspace, size_t workspace_bytes,
                                 bool write_ring, hipStream_t stream, int64_t ring8_bstride = 0) {
   const int wp = start_pos < window ? start_pos : window;
   DSV41_REQUIRE(q && chunk_kv && sink && o && (idx || k == 0) && (win_kv || wp == 0) && (comp_kv4 || n_comp == 0),
@@ -1090,6 +1133,9 @@ static int sparse_mla_fp4_layer(const char* what, const void* q, const void* win
                 DSV41_E_ARG, "%s: tensors must be 16-byte aligned", what);
   DSV41_REQUIRE(comp_bstride % 16 == 0, DSV41_E_ARG, "%s: comp_bstride must be a multiple of 16 bytes", what);
   DSV41_REQUIRE(rd == 0 || (cos_tab && sin_tab && rd % 2 == 0 && rd <= dim), DSV41_E_ARG, "%s: bad rope tail", what);
+  DSV41_REQUIRE(q_rd == 0 || (q_rd > 0 && cos_tab && sin_tab && q_rd % 2 == 0 && q_rd <= dim &&
+                              (rd == 0 || rd == q_rd)),
+                DSV41_E_ARG, "%s: bad query rope tail (q_rd %d, rd %d)", what, q_rd, rd);
   const bool w8 = ring8_bstride > 0;
   if (w8)
     DSV41_REQUIRE(ring8_bstride >= (int64_t)window * (dim + dim / 32) && ring8_bstride % 16 == 0, DSV41_E_ARG,
@@ -1104,7 +1150,7 @@ static int sparse_mla_fp4_layer(const char* what, const void* q, const void* win
   a.src.comp = comp_kv4; a.src.comp_bstride = comp_bstride; a.src.n_comp = n_comp;
   a.src.idx = idx; a.src.k = k; a.src.win_implicit = 1;
   a.m = n; a.heads = heads; a.dim = dim; a.scale = scale;
-  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.start_pos = start_pos;
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.rd = rd; a.q_rd = q_rd; a.start_pos = start_pos;
   if (write_ring) {
     DSV41_REQUIRE(n == 1 && win_kv, DSV41_E_ARG, "%s: the ring store needs one token per row and a ring", what);
     a.ring_w = const_cast<void*>(win_kv);
@@ -1119,23 +1165,24 @@ extern "C" int dsv41_sparse_mla_packed(const void* q, const uint8_t* win_kv8, in
                                        int32_t n_comp, const float* sink, const int32_t* idx, int32_t k, void* o,
                                        int32_t bsz, int32_t n, int32_t heads, int32_t dim, int32_t window,
                                        int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab,
-                                       int32_t rd, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                                       int32_t rd, int32_t q_rd, void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream) {
   DSV41_REQUIRE(ring_bstride > 0, DSV41_E_ARG, "dsv41_sparse_mla_packed: ring_bstride must be positive");
   return sparse_mla_fp4_layer("dsv41_sparse_mla_packed", q, win_kv8, chunk_kv, comp_kv4, comp_bstride, n_comp, sink,
-                              idx, k, o, bsz, n, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd,
+                              idx, k, o, bsz, n, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, q_rd,
                               workspace, workspace_bytes, false, stream, ring_bstride);
 }
 
 extern "C" int dsv41_sparse_mla_packed_decode(const void* q, uint8_t* win_kv8, int64_t ring_bstride,
                                               const void* chunk_kv, const uint8_t* comp_kv4, int64_t comp_bstride,
-                                              int32_t n_comp, const float* sink, const int32_t* idx, int32_t k,
-                                              void* o, int32_t bsz, int32_t heads, int32_t dim, int32_t window,
+                                              int32_t n_comp, const float* sink, const int32_t* idx, int32_t k, void* o,
+                                              int32_t bsz, int32_t heads, int32_t dim, int32_t window,
                                               int32_t start_pos, float scale, const float* cos_tab,
-                                              const float* sin_tab, int32_t rd, void* workspace,
+                                              const float* sin_tab, int32_t rd, int32_t q_rd, void* workspace,
                                               size_t workspace_bytes, hipStream_t stream) {
   DSV41_REQUIRE(ring_bstride > 0, DSV41_E_ARG, "dsv41_sparse_mla_packed_decode: ring_bstride must be positive");
   return sparse_mla_fp4_layer("dsv41_sparse_mla_packed_decode", q, win_kv8, chunk_kv, comp_kv4, comp_bstride, n_comp,
-                              sink, idx, k, o, bsz, 1, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd,
+                              sink, idx, k, o, bsz, 1, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, q_rd,
                               workspace, workspace_bytes, true, stream, ring_bstride);
 }
 
@@ -1143,21 +1190,21 @@ extern "C" int dsv41_sparse_mla_fp4(const void* q, const void* win_kv, const voi
                                     int64_t comp_bstride, int32_t n_comp, const float* sink, const int32_t* idx,
                                     int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads, int32_t dim,
                                     int32_t window, int32_t start_pos, float scale, const float* cos_tab,
-                                    const float* sin_tab, int32_t rd, void* workspace, size_t workspace_bytes,
-                                    hipStream_t stream) {
-  return sparse_mla_fp4_layer("dsv41_sparse_mla_fp4", q, win_kv, chunk_kv, comp_kv4, comp_bstride, n_comp, sink, idx,
-                              k, o, bsz, n, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, workspace,
+                                    const float* sin_tab, int32_t rd, int32_t q_rd, void* workspace,
+                                    size_t workspace_bytes, hipStream_t stream) {
+  return sparse_mla_fp4_layer("dsv41_sparse_mla_fp4", q, win_kv, chunk_kv, comp_kv4, comp_bstride, n_comp, sink, idx, k,
+                              o, bsz, n, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, q_rd, workspace,
                               workspace_bytes, false, stream);
 }
 
-extern "C" int dsv41_sparse_mla_fp4_decode(const void* q, void* win_kv, const void* chunk_kv,
-                                           const uint8_t* comp_kv4, int64_t comp_bstride, int32_t n_comp,
-                                           const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
-                                           int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
-                                           float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
-                                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  return sparse_mla_fp4_layer("dsv41_sparse_mla_fp4_decode", q, win_kv, chunk_kv, comp_kv4, comp_bstride, n_comp,
-                              sink, idx, k, o, bsz, 1, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd,
+extern "C" int dsv41_sparse_mla_fp4_decode(const void* q, void* win_kv, const void* chunk_kv, const uint8_t* comp_kv4,
+                                           int64_t comp_bstride, int32_t n_comp, const float* sink, const int32_t* idx,
+                                           int32_t k, void* o, int32_t bsz, int32_t heads, int32_t dim, int32_t window,
+                                           int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab,
+                                           int32_t rd, int32_t q_rd, void* workspace, size_t workspace_bytes,
+                                           hipStream_t stream) {
+  return sparse_mla_fp4_layer("dsv41_sparse_mla_fp4_decode", q, win_kv, chunk_kv, comp_kv4, comp_bstride, n_comp, sink,
+                              idx, k, o, bsz, 1, heads, dim, window, start_pos, scale, cos_tab, sin_tab, rd, q_rd,
                               workspace, workspace_bytes, true, stream);
 }
 
@@ -1165,12 +1212,12 @@ extern "C" int dsv41_sparse_mla_fp8(const void* q, const void* win_kv, const voi
                                     int64_t comp_bstride, int32_t n_comp, const uint8_t* comp_scale,
                                     int64_t comp_scale_bstride, int32_t comp_scale_rb, const float* sink,
                                     const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads,
-                                    int32_t dim, int32_t window, int32_t start_pos, float scale,
-                                    const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
+                                    int32_t dim, int32_t window, int32_t start_pos, float scale, const float* cos_tab,
+                                    const float* sin_tab, int32_t rd, int32_t q_rd, void* workspace,
                                     size_t workspace_bytes, hipStream_t stream) {
   return sparse_mla_fp8_layer("dsv41_sparse_mla_fp8", q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp, comp_scale,
-                              comp_scale_bstride, comp_scale_rb, sink, idx, k, o, bsz, n, heads, dim, window,
-                              start_pos, scale, cos_tab, sin_tab, rd, workspace, workspace_bytes, false, stream);
+                              comp_scale_bstride, comp_scale_rb, sink, idx, k, o, bsz, n, heads, dim, window, start_pos,
+                              scale, cos_tab, sin_tab, rd, q_rd, workspace, workspace_bytes, false, stream);
 }
 
 extern "C" int dsv41_sparse_mla_fp8_decode(const void* q, void* win_kv, const void* chunk_kv, const uint8_t* comp_kv,
@@ -1178,9 +1225,10 @@ extern "C" int dsv41_sparse_mla_fp8_decode(const void* q, void* win_kv, const vo
                                            int64_t comp_scale_bstride, int32_t comp_scale_rb, const float* sink,
                                            const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t heads,
                                            int32_t dim, int32_t window, int32_t start_pos, float scale,
-                                           const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
-                                           size_t workspace_bytes, hipStream_t stream) {
+                                           const float* cos_tab, const float* sin_tab, int32_t rd, int32_t q_rd,
+                                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
   return sparse_mla_fp8_layer("dsv41_sparse_mla_fp8_decode", q, win_kv, chunk_kv, comp_kv, comp_bstride, n_comp,
                               comp_scale, comp_scale_bstride, comp_scale_rb, sink, idx, k, o, bsz, 1, heads, dim,
-                              window, start_pos, scale, cos_tab, sin_tab, rd, workspace, workspace_bytes, true, stream);
+                              window, start_pos, scale, cos_tab, sin_tab, rd, q_rd, workspace, workspace_bytes, true,
+                              stream);
 }

@@ -73,26 +73,25 @@ _SIGNATURES = {
     "dsv41_sparse_mla_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32],
     "dsv41_sparse_attn": [_c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                           _i32, _c_p, _sz, _c_p],
-    "dsv41_sparse_mla": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
-                         _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
-    "dsv41_sparse_mla_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
-                                _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
-    "dsv41_sparse_mla_decode_noalloc": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
-                                        _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p],
-    "dsv41_sparse_mla_fp8": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _i64, _i32, _c_p, _c_p, _i32,
-                             _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p,
-                             _sz, _c_p],
-    "dsv41_sparse_mla_fp8_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _i64, _i32, _c_p, _c_p, _i32,
-                                    _c_p, _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32,
+                         _i32, _f32, _c_p, _c_p, _i32, _i32, _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32,
+                                _i32, _f32, _c_p, _c_p, _i32, _i32, _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla_decode_noalloc": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32,
+                                        _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _i32, _c_p],
+    "dsv41_sparse_mla_fp8": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
+                             _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla_fp8_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p,
+                                    _i32, _i32, _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_comp_write_fp4": [_c_p, _c_p, _i64, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
-    "dsv41_sparse_mla_fp4": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32,
-                             _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
+    "dsv41_sparse_mla_fp4": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32,
+                             _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_sparse_mla_fp4_decode": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32,
-                                    _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
+                                    _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_sparse_mla_packed": [_c_p, _c_p, _i64, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32,
-                                _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
+                                _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_sparse_mla_packed_decode": [_c_p, _c_p, _i64, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
-                                       _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _c_p, _sz, _c_p],
+                                       _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_window_write_mxfp8": [_c_p, _i64, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_comp_write_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32,
                              _i32, _c_p],
@@ -197,6 +196,19 @@ def _tables(name: str, cos, sin, rd: int) -> None:
             or cos.dim() != 2 or cos.shape != sin.shape or cos.shape[1] * 2 != rd):
         raise ValueError(f"{name}: rope tables must be fp32 [positions, {rd // 2}]")
     _contig(name, cos, sin)
+
+
+def _attn_tables(name: str, cos, sin, rd: int, q_rd: int, start_pos: int, n: int) -> None:
+    """The rope tables of a sparse_mla form: rd (the output's inverse rope) and q_rd (q's forward
+    rope, applied as q loads) share one table, so nonzero widths must agree; positions
+    start_pos .. start_pos + n - 1 must be in it."""
+    if rd < 0 or q_rd < 0 or (rd and q_rd and rd != q_rd):
+        raise ValueError(f"{name}: rd {rd} and q_rd {q_rd} must be 0 or one shared rope width")
+    w = rd or q_rd
+    if w:
+        _tables(name, cos, sin, w)
+        if n and start_pos + n - 1 >= cos.shape[0]:
+            raise ValueError(f"{name}: rope table too short")
 
 
 def _batch(name: str, what: str, t: torch.Tensor, b: int) -> None:
@@ -865,12 +877,14 @@ def sparse_attn(q, kv, attn_sink, topk_idxs, softmax_scale):
 
 
 def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_scale, window,
-               start_pos, cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False):
+               start_pos, cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False, q_rd=0):
     """The layer form: window ring + this chunk's KV + the owner's compressed cache, all read
     in place. comp_kv: [b, >=n_comp, d] view (or None); idx [b, n, k] int32 or None.
     workspace: a uint8 scratch tensor of at least mla_workspace_bytes(...) bytes, allocated
     when it is omitted or too small. write_ring (one token per row): the same launch also
-    stores chunk_kv into its ring slot, as LayerCache.write_window would afterwards."""
+    stores chunk_kv into its ring slot, as LayerCache.write_window would afterwards.
+    rd: width of the inverse rope on the output; q_rd > 0: q is given before its rope and the
+    launch applies rope_tail(q, q_rd, cos, sin) at positions start_pos + s as it loads q."""
     name = "dsv41_sparse_mla_decode" if write_ring else "dsv41_sparse_mla"
     _gpu(name, q, win_kv, chunk_kv, comp_kv, attn_sink, idx, cos, sin, out)
     _contig(name, q, chunk_kv, attn_sink, idx)
@@ -901,15 +915,12 @@ def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_sca
         if idx.dtype != torch.int32 or idx.shape[:2] != (b, n):
             raise ValueError(f"{name}: idx must be int32 [{b}, {n}, k]")
         k = idx.shape[2]
-    if rd:
-        _tables(name, cos, sin, rd)
-        if n and start_pos + n - 1 >= cos.shape[0]:
-            raise ValueError(f"{name}: rope table too short")
+    _attn_tables(name, cos, sin, rd, q_rd, start_pos, n)
     o = _out(name, out, q.shape, q.dtype, q.device)
     rows = min(window, wp + n) + k
     ws_bytes = mla_workspace_bytes(b, n, h, d, rows, q.dtype)
     workspace = _ws(name, workspace, ws_bytes, q.device)
-    tail = (_ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, dtype_code(q, name),
+    tail = (_ptr(cos) if rd or q_rd else None, _ptr(sin) if rd or q_rd else None, rd, q_rd, dtype_code(q, name),
             _ptr(workspace) if ws_bytes else None, ws_bytes, _stream(q))
     if write_ring:
         if n != 1 or ring is None:
@@ -922,8 +933,8 @@ def sparse_mla(q, win_kv, chunk_kv, comp_kv, n_comp, attn_sink, idx, softmax_sca
     return o
 
 
-def _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start_pos, cos, sin, rd, write_ring,
-                        ring_mxfp8=False):
+def _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start_pos, cos, sin, rd, q_rd,
+                        write_ring, ring_mxfp8=False):
     """Checks shared by the packed-cache sparse_mla forms (bf16 q and chunk, a bf16 or MXFP8
     ring; 512 channels): returns (b, n, h, d, ring view, k)."""
     _contig(name, q, chunk_kv, attn_sink, idx)
@@ -948,28 +959,25 @@ def _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start
         if idx.dtype != torch.int32 or idx.shape[:2] != (b, n):
             raise ValueError(f"{name}: idx must be int32 [{b}, {n}, k]")
         k = idx.shape[2]
-    if rd:
-        _tables(name, cos, sin, rd)
-        if n and start_pos + n - 1 >= cos.shape[0]:
-            raise ValueError(f"{name}: rope table too short")
+    _attn_tables(name, cos, sin, rd, q_rd, start_pos, n)
     if write_ring and (n != 1 or ring is None):
         raise ValueError(f"{name}: the ring store needs one token per row and a window ring")
     return b, n, h, d, ring, k
 
 
 def sparse_mla_fp4(q, win_kv, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softmax_scale, window, start_pos,
-                   cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False):
+                   cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False, q_rd=0):
     """sparse_mla with a packed fp4 compressed cache (comp_write_fp4's layout): comp_kv4 uint8
     [b, >=n_comp, 288] rows of 512 e2m1 codes and 32 e4m3 scales. q, the window ring, chunk and
     output are bf16; the result equals sparse_mla's on the decoded cache.
     write_ring (one token per row): the launch also stores chunk_kv into its ring slot."""
     name = "dsv41_sparse_mla_fp4_decode" if write_ring else "dsv41_sparse_mla_fp4"
     return _sparse_mla_fp4_rows(name, q, win_kv, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softmax_scale, window,
-                                start_pos, cos, sin, rd, out, workspace, write_ring, False)
+                                start_pos, cos, sin, rd, q_rd, out, workspace, write_ring, False)
 
 
 def sparse_mla_packed(q, win_kv8, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softmax_scale, window, start_pos,
-                      cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False):
+                      cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False, q_rd=0):
     """sparse_mla over the packed cache: the window ring as MXFP8 rows (win_kv8 uint8
     [b, window, 528]: 512 e4m3fn codes, 16 ue8m0 scales; window_write_mxfp8's layout) and the
     compressed KV as packed fp4 rows (comp_kv4, or None for a window-only layer). q, chunk and
@@ -977,14 +985,14 @@ def sparse_mla_packed(q, win_kv8, chunk_kv, comp_kv4, n_comp, attn_sink, idx, so
     per row): the launch also stores chunk_kv, MXFP8-encoded, into its ring slot."""
     name = "dsv41_sparse_mla_packed_decode" if write_ring else "dsv41_sparse_mla_packed"
     return _sparse_mla_fp4_rows(name, q, win_kv8, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softmax_scale, window,
-                                start_pos, cos, sin, rd, out, workspace, write_ring, True)
+                                start_pos, cos, sin, rd, q_rd, out, workspace, write_ring, True)
 
 
 def _sparse_mla_fp4_rows(name, q, win_kv, chunk_kv, comp_kv4, n_comp, attn_sink, idx, softmax_scale, window,
-                         start_pos, cos, sin, rd, out, workspace, write_ring, ring_mxfp8):
+                         start_pos, cos, sin, rd, q_rd, out, workspace, write_ring, ring_mxfp8):
     _gpu(name, q, win_kv, chunk_kv, comp_kv4, attn_sink, idx, cos, sin, out)
     b, n, h, d, ring, k = _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start_pos, cos,
-                                              sin, rd, write_ring, ring_mxfp8)
+                                              sin, rd, q_rd, write_ring, ring_mxfp8)
     comp_bstride = 0
     if comp_kv4 is not None and n_comp:
         if (comp_kv4.dtype != torch.uint8 or comp_kv4.dim() != 3 or comp_kv4.shape[2] != fp4_row_bytes(d)
@@ -998,8 +1006,8 @@ def _sparse_mla_fp4_rows(name, q, win_kv, chunk_kv, comp_kv4, n_comp, attn_sink,
     wp = min(start_pos, window)
     ws_bytes = mla_workspace_bytes(b, n, h, d, min(window, wp + n) + k, q.dtype)
     workspace = _ws(name, workspace, ws_bytes, q.device)
-    tail = (_ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, _ptr(workspace) if ws_bytes else None,
-            ws_bytes, _stream(q))
+    tail = (_ptr(cos) if rd or q_rd else None, _ptr(sin) if rd or q_rd else None, rd, q_rd,
+            _ptr(workspace) if ws_bytes else None, ws_bytes, _stream(q))
     if ring_mxfp8:
         if ring is None:
             raise ValueError(f"{name}: the MXFP8 ring is required")
@@ -1016,7 +1024,7 @@ def _sparse_mla_fp4_rows(name, q, win_kv, chunk_kv, comp_kv4, n_comp, attn_sink,
 
 
 def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, attn_sink, idx, softmax_scale,
-                   window, start_pos, cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False):
+                   window, start_pos, cos=None, sin=None, rd=0, out=None, workspace=None, write_ring=False, q_rd=0):
     """sparse_mla with an fp8 compressed cache: comp8 uint8 [b, >=n_comp, 512] e4m3fn codes,
     comp_scale uint8 [b, >=ceil(n_comp / scale_rb), 16] ue8m0 exponents (one per 32 channels
     for every scale_rb = 1 or 32 rows). q, the window ring, chunk and output are bf16.
@@ -1024,7 +1032,7 @@ def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, att
     name = "dsv41_sparse_mla_fp8_decode" if write_ring else "dsv41_sparse_mla_fp8"
     _gpu(name, q, win_kv, chunk_kv, comp8, comp_scale, attn_sink, idx, cos, sin, out)
     b, n, h, d, ring, k = _packed_mla_sources(name, q, win_kv, chunk_kv, attn_sink, idx, window, start_pos, cos,
-                                              sin, rd, write_ring)
+                                              sin, rd, q_rd, write_ring)
     wp = min(start_pos, window)
     comp_bstride = sc_bstride = 0
     if comp8 is not None and n_comp:
@@ -1042,8 +1050,8 @@ def sparse_mla_fp8(q, win_kv, chunk_kv, comp8, comp_scale, scale_rb, n_comp, att
     rows = min(window, wp + n) + k
     ws_bytes = mla_workspace_bytes(b, n, h, d, rows, q.dtype)
     workspace = _ws(name, workspace, ws_bytes, q.device)
-    tail = (_ptr(cos) if rd else None, _ptr(sin) if rd else None, rd, _ptr(workspace) if ws_bytes else None,
-            ws_bytes, _stream(q))
+    tail = (_ptr(cos) if rd or q_rd else None, _ptr(sin) if rd or q_rd else None, rd, q_rd,
+            _ptr(workspace) if ws_bytes else None, ws_bytes, _stream(q))
     if write_ring:
         _call(name, _ptr(q), _ptr(ring), _ptr(chunk_kv), _ptr(comp8), comp_bstride, n_comp, _ptr(comp_scale),
               sc_bstride, scale_rb, _ptr(attn_sink), _ptr(idx), k, _ptr(o), b, h, d, window, start_pos,

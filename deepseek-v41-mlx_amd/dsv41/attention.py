@@ -3,7 +3,8 @@
 The projections (wq_a, wq_b, wkv, the compressor / indexer projections, wo_a, wo_b) are torch
 GEMMs; everything between them runs in HIP kernels:
 
-  q      : q_norm (RMSNorm kernel) ... rope tail (in place)
+  q      : q_norm (RMSNorm kernel); q's rope tail is applied by the attention launch as it
+           loads q (no separate pass over q)
   kv     : kv_norm -> rope -> fp8 fake-quant, one fused kernel, in place
   owner  : compressor pooling kernel; index keys published into its own index_k; latents
            roped + fp4/e4m3 fake-quantized straight into its comp_kv (no staging copy)
@@ -130,10 +131,9 @@ class Attention(torch.nn.Module):
         cos, sin = self._freqs(end_pos)
         x = x.contiguous()
 
-        # queries
+        # queries: q's rope tail (attention.py:117) is applied by the attention launch as it loads q
         qr = self.q_norm(self.wq_a(x))
         q = self.wq_b(qr).view(bsz, n, self.n_heads, self.head_dim).contiguous()
-        _abi.rope_tail(q, rd, cos, sin, start_pos, 1, out=q)
 
         # this chunk's window KV
         kv = self._kv_prologue(self.wkv(x).contiguous(), cos, sin, start_pos)
@@ -177,16 +177,17 @@ class Attention(torch.nn.Module):
         if lc.win_kv8 is not None:          # the packed cache: MXFP8 ring, fp4 compressed rows
             o = _abi.sparse_mla_packed(q, lc.win_kv8, kv, comp if comp_kind == "fp4" else None, n_comp, sink, sel,
                                        self.softmax_scale, self.window_size, start_pos, cos, sin, rdo,
-                                       write_ring=decode)
+                                       write_ring=decode, q_rd=rd)
         elif comp_kind == "fp8":
             o = _abi.sparse_mla_fp8(q, lc.win_kv, kv, comp, src.comp_ks[:bsz], src.fp8_rb, n_comp, sink, sel,
-                                    self.softmax_scale, self.window_size, start_pos, cos, sin, rdo, write_ring=decode)
+                                    self.softmax_scale, self.window_size, start_pos, cos, sin, rdo, write_ring=decode,
+                                    q_rd=rd)
         elif comp_kind == "fp4":
             o = _abi.sparse_mla_fp4(q, lc.win_kv, kv, comp, n_comp, sink, sel, self.softmax_scale, self.window_size,
-                                    start_pos, cos, sin, rdo, write_ring=decode)
+                                    start_pos, cos, sin, rdo, write_ring=decode, q_rd=rd)
         else:
             o = _abi.sparse_mla(q, lc.win_kv, kv, comp, n_comp, sink, sel, self.softmax_scale, self.window_size,
-                                start_pos, cos, sin, rdo, write_ring=decode)
+                                start_pos, cos, sin, rdo, write_ring=decode, q_rd=rd)
         if not decode:
             lc.write_window(start_pos, kv)
 

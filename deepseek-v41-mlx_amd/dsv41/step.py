@@ -2,8 +2,9 @@
 
 One step = indexer scoring of every visible compressed entry (MFMA) -> top-k selection ->
 sparse MLA over the window ring, this token's KV and the selected compressed entries, with
-the inverse rope on the output -- i.e. attention.py:143-175 minus the projections, the
-cache writes and the fake-quant prologues, which are per-token elementwise work.
+q's rope tail applied as the attention loads q and the inverse rope on the output -- i.e.
+attention.py:117 and 143-175 minus the projections, the cache writes and the fake-quant
+prologues, which are per-token elementwise work.
 
 All outputs and scratch are allocated once, so a step issues exactly three kernels (four
 when the attention splits its index list) and can be captured in a HIP graph. Where the fused
@@ -48,7 +49,8 @@ class SparseDecodeStep:
 
     def __call__(self, q, index_q, w_raw, w_scale, index_k, comp_kv, win_kv, chunk_kv, sink,
                  cos, sin):
-        """q [b,1,H,D]; index_q [b,1,Hi,Di] (already roped + fake-quantized); w_raw [b,1,Hi];
+        """q [b,1,H,D] as wq_b gives it (the attention launch applies its rope tail);
+        index_q [b,1,Hi,Di] (already roped + fake-quantized); w_raw [b,1,Hi];
         index_k / comp_kv: the owner's caches ([b, >=nb, *] views, read in place);
         win_kv [b, window, D] ring of the previous tokens; chunk_kv [b,1,D] this token's KV."""
         keys = index_k[:, :self.nb]
@@ -61,7 +63,7 @@ class SparseDecodeStep:
                                    workspace=self.topk_ws, out=self.idx)
         _abi.sparse_mla(q, win_kv, chunk_kv, comp_kv, self.nb, sink, idx, self.head_dim ** -0.5,
                         self.window, self.start_pos, cos, sin, self.rd, out=self.out,
-                        workspace=self.workspace)
+                        workspace=self.workspace, q_rd=self.rd)
         return self.out, idx
 
 
@@ -83,15 +85,17 @@ class StackDecodeStep:
     follows the layer loop of model.py:141-154: the most recent kv source, key owner, top-k
     selection and candidate mask are handed down the stack.
 
-    ``inputs[l]`` holds layer l's per-token tensors: ``q`` [b,1,H,D] (roped), ``kv`` [b,1,D]
+    ``inputs[l]`` holds layer l's per-token tensors: ``q`` [b,1,H,D] (wq_b's output: the
+    attention launch applies its rope tail), ``kv`` [b,1,D]
     (the window KV after its prologue), ``sink`` [H]; index sources add ``index_q``
     [b,1,Hi,Di] (roped, fake-quantized) -- or, when the key owners' caches are MXFP4,
     ``index_q_mx`` (its codes and scales from dsv41_index_q_prep_mxfp4) --, ``w_raw`` [b,1,Hi]
     and ``w_scale``; kv sources add ``latent`` [b,1,D] (pre-rope); key owners add ``k_raw``
     [b,1,Di] and ``k_norm`` [Di]. Caches may be dense, carry MXFP4 index keys, hold the
     compressed KV packed (cache_format "fp4": e2m1 codes + e4m3 scales per 16 channels) and the
-    window ring too ("packed": MXFP8 rows), or be the fp8 variant (cache_format "fp8": fp8 compressed KV and index keys, with ue8m0 scales per
-    32 channels of each row or of 32-row blocks); each layer takes the kernels that read and
+    window ring too ("packed": MXFP8 rows), or be the fp8 variant (cache_format "fp8": fp8
+    compressed KV and index keys, with ue8m0 scales per 32 channels of each row or of 32-row
+    blocks); each layer takes the kernels that read and
     write its owners' format. Over fp8 keys an index source given ``index_q_mx`` scores on the
     block-scaled fp4 x fp8 MFMA (dsv41_indexer_*_mxq_fp8), else it dequantizes the keys for the
     bf16 MFMA. On every key format, index sources other than the candidate source score and
@@ -231,17 +235,17 @@ class StackDecodeStep:
             if lc.win_kv8 is not None:
                 _abi.sparse_mla_packed(x["q"], lc.win_kv8, x["kv"], comp if comp_kind == "fp4" else None, n_comp,
                                        x["sink"], idx, self.scale, self.window, sp, p.cos, p.sin, a.rope_head_dim,
-                                       out=p.out, workspace=self.workspace, write_ring=True)
+                                       out=p.out, workspace=self.workspace, write_ring=True, q_rd=a.rope_head_dim)
             elif comp_kind == "fp8":
                 _abi.sparse_mla_fp8(x["q"], lc.win_kv, x["kv"], comp, kv_src.comp_ks[:b], kv_src.fp8_rb, n_comp,
                                     x["sink"], idx, self.scale, self.window, sp, p.cos, p.sin, a.rope_head_dim,
-                                    out=p.out, workspace=self.workspace, write_ring=True)
+                                    out=p.out, workspace=self.workspace, write_ring=True, q_rd=a.rope_head_dim)
             elif comp_kind == "fp4":
                 _abi.sparse_mla_fp4(x["q"], lc.win_kv, x["kv"], comp, n_comp, x["sink"], idx, self.scale, self.window,
                                     sp, p.cos, p.sin, a.rope_head_dim, out=p.out, workspace=self.workspace,
-                                    write_ring=True)
+                                    write_ring=True, q_rd=a.rope_head_dim)
             else:
                 _abi.sparse_mla(x["q"], lc.win_kv, x["kv"], comp, n_comp, x["sink"], idx, self.scale, self.window,
                                 sp, p.cos, p.sin, a.rope_head_dim, out=p.out, workspace=self.workspace,
-                                write_ring=True)
+                                write_ring=True, q_rd=a.rope_head_dim)
         return [p.out for p in self.plan]

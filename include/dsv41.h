@@ -371,13 +371,18 @@ int dsv41_sparse_attn(const void* q, const void* kv, const float* sink, const in
  * [max(wp+s-window+1, 0), wp+s] (window_idx_matrix, attention.py:40-50) plus idx[b,s,:]
  * (the indexer's output, already offset by wp + n; -1 masked; may be NULL with k = 0).
  * Output o [bsz,n,heads,dim] gets the inverse rope on its last rd channels at position
- * start_pos + s when rd > 0 (attention.py:174-175). win_kv [bsz,window,dim], chunk
- * [bsz,n,dim], comp with comp_bstride elements per batch row. dtype F32 or BF16. */
+ * start_pos + s when rd > 0 (attention.py:174-175). q_rd > 0: q is wq_b's output before
+ * its rope, and the launch applies the forward rope of attention.py:117 (rope_tail, inverse
+ * false) to q's last q_rd channels as it loads q, at position start_pos + s, rounding each
+ * rotated value to q's dtype as dsv41_rope_tail does (q itself is not written); q_rd = 0: q
+ * arrives roped. cos_tab/sin_tab are [positions, w/2] for w = the nonzero of rd and q_rd (equal
+ * when both are). win_kv [bsz,window,dim], chunk [bsz,n,dim], comp with comp_bstride elements
+ * per batch row. dtype F32 or BF16. Every dsv41_sparse_mla_* form below takes rd and q_rd so. */
 int dsv41_sparse_mla(const void* q, const void* win_kv, const void* chunk_kv,
                      const void* comp_kv, int64_t comp_bstride, int32_t n_comp,
                      const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
                      int32_t n, int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
-                     float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                     float scale, const float* cos_tab, const float* sin_tab, int32_t rd, int32_t q_rd,
                      int32_t dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* One-token decode form of dsv41_sparse_mla (n = 1) that also performs the ring write of
@@ -390,7 +395,7 @@ int dsv41_sparse_mla_decode(const void* q, void* win_kv, const void* chunk_kv,
                             const void* comp_kv, int64_t comp_bstride, int32_t n_comp,
                             const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
                             int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
-                            float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                            float scale, const float* cos_tab, const float* sin_tab, int32_t rd, int32_t q_rd,
                             int32_t dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* dsv41_sparse_mla_decode without a workspace argument, for callers that cannot allocate device
@@ -406,7 +411,7 @@ int dsv41_sparse_mla_decode_noalloc(const void* q, void* win_kv, const void* chu
                                     const void* comp_kv, int64_t comp_bstride, int32_t n_comp,
                                     const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
                                     int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
-                                    float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                                    float scale, const float* cos_tab, const float* sin_tab, int32_t rd, int32_t q_rd,
                                     int32_t dtype, hipStream_t stream);
 
 /* dsv41_sparse_mla with the compressed source stored as fp8: the packed, lossless form of the
@@ -423,7 +428,7 @@ int dsv41_sparse_mla_fp8(const void* q, const void* win_kv, const void* chunk_kv
                          const uint8_t* comp_scale, int64_t comp_scale_bstride, int32_t comp_scale_rb,
                          const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
                          int32_t n, int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
-                         float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                         float scale, const float* cos_tab, const float* sin_tab, int32_t rd, int32_t q_rd,
                          void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* dsv41_sparse_mla_fp8 for one token per row (n = 1) that also performs the ring write of
@@ -434,7 +439,7 @@ int dsv41_sparse_mla_fp8_decode(const void* q, void* win_kv, const void* chunk_k
                                 int32_t comp_scale_rb, const float* sink, const int32_t* idx, int32_t k,
                                 void* o, int32_t bsz, int32_t heads, int32_t dim, int32_t window,
                                 int32_t start_pos, float scale, const float* cos_tab, const float* sin_tab,
-                                int32_t rd, void* workspace, size_t workspace_bytes, hipStream_t stream);
+                                int32_t rd, int32_t q_rd, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* dsv41_sparse_mla with the compressed source in dsv41_comp_write_fp4's packed layout: 288-byte
  * rows (512 e2m1 codes, then 32 e4m3fn scales, one per 16 channels), comp_bstride bytes per
@@ -447,7 +452,7 @@ int dsv41_sparse_mla_fp4(const void* q, const void* win_kv, const void* chunk_kv
                          const uint8_t* comp_kv4, int64_t comp_bstride, int32_t n_comp, const float* sink,
                          const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n, int32_t heads,
                          int32_t dim, int32_t window, int32_t start_pos, float scale, const float* cos_tab,
-                         const float* sin_tab, int32_t rd, void* workspace, size_t workspace_bytes,
+                         const float* sin_tab, int32_t rd, int32_t q_rd, void* workspace, size_t workspace_bytes,
                          hipStream_t stream);
 
 /* dsv41_sparse_mla_fp4 for one token per row (n = 1) that also performs the ring write of
@@ -456,7 +461,7 @@ int dsv41_sparse_mla_fp4_decode(const void* q, void* win_kv, const void* chunk_k
                                 const uint8_t* comp_kv4, int64_t comp_bstride, int32_t n_comp,
                                 const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz,
                                 int32_t heads, int32_t dim, int32_t window, int32_t start_pos, float scale,
-                                const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
+                                const float* cos_tab, const float* sin_tab, int32_t rd, int32_t q_rd, void* workspace,
                                 size_t workspace_bytes, hipStream_t stream);
 
 /* dsv41_sparse_mla_fp4 with the window ring also packed: win_kv8 holds MXFP8 rows in
@@ -468,7 +473,7 @@ int dsv41_sparse_mla_packed(const void* q, const uint8_t* win_kv8, int64_t ring_
                             const void* chunk_kv, const uint8_t* comp_kv4, int64_t comp_bstride, int32_t n_comp,
                             const float* sink, const int32_t* idx, int32_t k, void* o, int32_t bsz, int32_t n,
                             int32_t heads, int32_t dim, int32_t window, int32_t start_pos, float scale,
-                            const float* cos_tab, const float* sin_tab, int32_t rd, void* workspace,
+                            const float* cos_tab, const float* sin_tab, int32_t rd, int32_t q_rd, void* workspace,
                             size_t workspace_bytes, hipStream_t stream);
 
 /* dsv41_sparse_mla_packed for one token per row (n = 1) that also performs the ring write of
@@ -478,7 +483,7 @@ int dsv41_sparse_mla_packed_decode(const void* q, uint8_t* win_kv8, int64_t ring
                                    const void* chunk_kv, const uint8_t* comp_kv4, int64_t comp_bstride,
                                    int32_t n_comp, const float* sink, const int32_t* idx, int32_t k, void* o,
                                    int32_t bsz, int32_t heads, int32_t dim, int32_t window, int32_t start_pos,
-                                   float scale, const float* cos_tab, const float* sin_tab, int32_t rd,
+                                   float scale, const float* cos_tab, const float* sin_tab, int32_t rd, int32_t q_rd,
                                    void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus

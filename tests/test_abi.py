@@ -266,6 +266,8 @@ def host_abi(monkeypatch):
 
     def fake_call(name, *args):
         calls.append(name)
+        # the wrapper passes exactly the arguments the C declaration takes
+        assert len(args) == len(_abi._SIGNATURES[name]), (name, len(args), len(_abi._SIGNATURES[name]))
         raise _Launched(name)
 
     monkeypatch.setattr(_abi, "_gpu", lambda name, *t: None)
@@ -393,6 +395,11 @@ def test_sparse_mla_wrappers_check_buffers(host_abi):
     _refused(call(attn_sink=sink.to(torch.bfloat16)), "attn_sink")
     _refused(call(attn_sink=torch.zeros(h - 1)), "attn_sink")
     _refused(call(cos=cos[:, :16], sin=sin[:, :16]), "rope tables")
+    _reaches_launch(call(q_rd=64))                # q's rope tail in the launch, one table for both
+    _reaches_launch(call(rd=0, q_rd=64))
+    _refused(call(q_rd=32), "one shared rope width")
+    _refused(call(rd=0, q_rd=64, cos=None, sin=None), "rope tables")
+    _refused(call(q_rd=64, start_pos=200), "rope table too short")
     _refused(call(workspace=torch.zeros(1 << 20)), "workspace")
     codes = torch.zeros(b, 1024, d, dtype=torch.uint8)
     scales = torch.zeros(b, 32, d // 32, dtype=torch.uint8)
@@ -404,6 +411,7 @@ def test_sparse_mla_wrappers_check_buffers(host_abi):
         return lambda: A.sparse_mla_fp8(**args)
 
     _reaches_launch(call8())
+    _reaches_launch(call8(q_rd=64, write_ring=True))
     _refused(call8(out=torch.zeros(b, 1, h, d - 32, dtype=torch.bfloat16)), "out must be")
     _refused(call8(comp8=codes[:1], comp_scale=scales[:1]), "does not match")
     _refused(call8(attn_sink=sink.double()), "attn_sink")
@@ -417,6 +425,8 @@ def test_sparse_mla_wrappers_check_buffers(host_abi):
 
     _reaches_launch(call4())
     _reaches_launch(call4(write_ring=True))
+    _reaches_launch(call4(write_ring=True, q_rd=64))
+    _refused(call4(q_rd=-2), "one shared rope width")
     _refused(call4(comp_kv4=packed[:1]), "batch rows")
     _refused(call4(comp_kv4=torch.zeros(b, 1024, 256, dtype=torch.uint8)), "does not match")
     _refused(call4(comp_kv4=packed[:, :999]), "does not match")
@@ -433,6 +443,7 @@ def test_sparse_mla_wrappers_check_buffers(host_abi):
 
     _reaches_launch(callp())
     _reaches_launch(callp(write_ring=True))
+    _reaches_launch(callp(write_ring=True, q_rd=64))
     _reaches_launch(callp(comp_kv4=None, n_comp=0, idx=None))
     _refused(callp(win_kv8=ring), "window ring")                      # a bf16 ring is not MXFP8
     _refused(callp(win_kv8=ring8[:, :, :512]), "window ring")

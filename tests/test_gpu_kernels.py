@@ -97,10 +97,8 @@ def test_rope_tail_and_rmsnorm(gpu, dt):
         got = to_np(_abi.rope_tail(dev(x, dt), 64, cos, sin, 100, 3, inverse))
         pos = 100 + 3 * np.arange(37)
         want = R.rope_tail(x, 64, rc[pos], rs[pos], inverse, dt)
-        if dt == "f32":
-            assert max_abs(got, want) < 1e-5
-        else:
-            assert rel_max_diff(got, want) < 1e-2
+        # bit-exact: products and sums rounded separately, as the reference's float32 ops do
+        assert np.array_equal(got, want), f"rope_tail {dt} inverse={inverse}"
     w = (1 + 0.1 * rng.standard_normal(1280)).astype(F32)
     y = R.cast(rng.standard_normal((33, 1280)).astype(F32) * 4, dt)
     got = to_np(_abi.rmsnorm(dev(y, dt), dev(w), 1e-20))
@@ -867,6 +865,70 @@ def test_sparse_mla_packed_equals_bf16_on_decoded_caches(gpu, b, n, window, star
     pos = start + np.arange(n)
     want = R.rope_tail(o, rd, rc[pos], rs[pos], inverse=True, dtype="bf16")
     assert rel_max_diff(to_np(got), want) < 2e-2
+
+
+@pytest.mark.parametrize("form,dt,b,n,h,d,window,start,n_comp,k,rdo", [
+    ("dense", "f32", 1, 1, 4, 64, 128, 143, 36, 16, 16),     # C1 decode, the fp32 kernel
+    ("dense", "f32", 2, 20, 4, 64, 8, 30, 12, 4, 0),         # a chunk, no inverse rope (the hook)
+    ("dense", "bf16", 32, 1, 64, 512, 128, 16383, 4096, 512, 64),   # bs32 decode: split lists
+    ("dense", "bf16", 1, 600, 64, 512, 16, 200, 150, 64, 64),       # >= 512 queries: the 64-head plan
+    ("dense", "bf16", 2, 1, 64, 512, 128, 5, 0, 0, 0),       # window only, no inverse rope
+    ("fp8", "bf16", 8, 1, 64, 512, 128, 40000, 9000, 1000, 64),
+    ("fp4", "bf16", 8, 1, 64, 512, 128, 40000, 9000, 1000, 64),
+    ("packed", "bf16", 8, 1, 64, 512, 128, 40000, 9000, 1000, 64),
+    ("packed", "bf16", 1, 600, 64, 512, 16, 200, 150, 64, 64),
+])
+def test_sparse_mla_q_rope_in_launch(gpu, form, dt, b, n, h, d, window, start, n_comp, k, rdo):
+    """q_rd: the launch applies q's forward rope tail (attention.py:117) as it loads q. Bit-equal
+    to dsv41_rope_tail on q followed by the same call without it, on every cache form and plan
+    (whatever rd the output's inverse rope uses); q itself is left as given; and the roped q
+    equals the oracle's rope_tail."""
+    from dsv41 import _abi
+    rng = rng_for(f"mlaqr{form}{dt}{b}{n}{start}")
+    rd = 16 if d == 64 else 64
+    rc, rs = R.precompute_freqs_cis(rd, start + n + 1, 65536, 160000.0, 16.0, 32, 1)
+    q = R.cast(rng.standard_normal((b, n, h, d)).astype(F32) * 2, dt)
+    chunk = R.cast(rng.standard_normal((b, n, d)).astype(F32), dt)
+    sink = rng.standard_normal(h).astype(F32)
+    wp = min(start, window)
+    cidx = None
+    if k:
+        lens = R.query_lens(start, n, 4)
+        cidx = np.sort(rng.integers(0, n_comp, size=(b, n, k)), axis=-1)
+        cidx = np.where(cidx < np.minimum(lens, n_comp)[None, :, None], cidx + wp + n, -1).astype(np.int32)
+    idx_t = torch.as_tensor(cidx).to(gpu) if k else None
+    cos, sin = dev(rc), dev(rs)
+    if form == "dense":
+        win = dev(R.cast(rng.standard_normal((b, window, d)).astype(F32), dt), dt)
+        comp = dev(R.cast(rng.standard_normal((b, n_comp + 7, d)).astype(F32), dt), dt) if n_comp else None
+        call = lambda qq, **kw: _abi.sparse_mla(qq, win, dev(chunk, dt), comp, n_comp, dev(sink), idx_t,  # noqa: E731
+                                                d ** -0.5, window, start, cos, sin, rdo, **kw)
+    elif form == "fp8":
+        codes, scales = _fp8_cache(rng, b, n_comp + 5, d, 32)
+        win = dev(R.cast(rng.standard_normal((b, window, d)).astype(F32), dt), dt)
+        c8, s8 = torch.as_tensor(codes).to(gpu), torch.as_tensor(scales).to(gpu)
+        call = lambda qq, **kw: _abi.sparse_mla_fp8(qq, win, dev(chunk, dt), c8, s8, 32, n_comp,  # noqa: E731
+                                                    dev(sink), idx_t, d ** -0.5, window, start, cos, sin, rdo, **kw)
+    elif form == "fp4":
+        win = dev(R.cast(rng.standard_normal((b, window, d)).astype(F32), dt), dt)
+        c4 = torch.as_tensor(_fp4_cache(rng, b, n_comp + 5, d)).to(gpu)
+        call = lambda qq, **kw: _abi.sparse_mla_fp4(qq, win, dev(chunk, dt), c4, n_comp, dev(sink), idx_t,  # noqa: E731
+                                                    d ** -0.5, window, start, cos, sin, rdo, **kw)
+    else:
+        r8 = torch.as_tensor(_mxfp8_ring(rng, b, window, d)).to(gpu)
+        c4 = torch.as_tensor(_fp4_cache(rng, b, n_comp + 5, d)).to(gpu)
+        call = lambda qq, **kw: _abi.sparse_mla_packed(qq, r8, dev(chunk, dt), c4, n_comp, dev(sink),  # noqa: E731
+                                                       idx_t, d ** -0.5, window, start, cos, sin, rdo, **kw)
+    q_dev = dev(q, dt)
+    q_keep = q_dev.clone()
+    got = call(q_dev, q_rd=rd)
+    roped = _abi.rope_tail(q_dev.clone(), rd, cos, sin, start, 1)
+    want = call(roped)
+    torch.cuda.synchronize()
+    assert torch.equal(q_dev, q_keep), "q must be left as given"
+    assert torch.equal(got, want), "in-launch q rope differs from rope_tail + attention"
+    pos = start + np.arange(n)
+    assert np.array_equal(to_np(roped), R.rope_tail(q, rd, rc[pos], rs[pos], dtype=dt))
 
 
 def test_reference_kernel_module_seam(gpu):

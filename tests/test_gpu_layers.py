@@ -203,9 +203,9 @@ def test_c2_decode_step(gpu):
     slots = (c["start"] - wp + np.arange(wp)) % c["W"]
     kv_all = np.concatenate([f(t["win"])[:, slots], f(t["chunk"]), f(t["comp"])], axis=1)
     widx = np.broadcast_to(R.window_idx_matrix(wp, 1, c["W"])[None], (b, 1, min(c["W"], wp + 1)))
-    o = R.sparse_attn(f(t["q"]), kv_all, f(t["sink"]), np.concatenate([widx, want_i], -1), c["D"] ** -0.5,
-                      dtype="bf16")
     rc, rs = R.precompute_freqs_cis(c["rd"], c["start"] + 1, 65536, 160000.0, 16.0, 32, 1)
+    qr = R.rope_tail(f(t["q"]), c["rd"], rc[[c["start"]]], rs[[c["start"]]], dtype="bf16")   # q's rope, in-launch
+    o = R.sparse_attn(qr, kv_all, f(t["sink"]), np.concatenate([widx, want_i], -1), c["D"] ** -0.5, dtype="bf16")
     want_o = R.rope_tail(o, c["rd"], rc[[c["start"]]], rs[[c["start"]]], inverse=True, dtype="bf16")
     assert rel_max_diff(to_np(out), want_o) < 2e-2
 

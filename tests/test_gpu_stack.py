@@ -253,8 +253,9 @@ def c4_fill_cache(cache, gen):
 
 
 def _oracle_layer_out(a, q_row, win_before, kv_row, comp_row, idx_row, sink, start_pos, ratio):
-    """Oracle attention output of one batch row: concat(window chrono, chunk, comp), then the
-    inverse rope of the layer's table."""
+    """Oracle attention output of one batch row: q's rope tail (the step applies it as the
+    attention loads q), attention over concat(window chrono, chunk, comp), then the inverse rope
+    of the layer's table."""
     W = a.window_size
     wp = min(start_pos, W)
     slots = (start_pos - wp + np.arange(wp)) % W
@@ -264,10 +265,11 @@ def _oracle_layer_out(a, q_row, win_before, kv_row, comp_row, idx_row, sink, sta
     kv_all = np.concatenate(parts, axis=0)[None]
     widx = R.window_idx_matrix(wp, 1, W)[None]
     full = widx if idx_row is None else np.concatenate([widx, idx_row[None, None]], -1)
-    o = R.sparse_attn(q_row[None, None], kv_all, sink, full, a.head_dim ** -0.5, dtype="bf16")
     orig, theta = (a.original_seq_len, a.compress_rope_theta) if ratio else (0, a.rope_theta)
     rc, rs = R.precompute_freqs_cis(a.rope_head_dim, start_pos + 1, orig, theta, a.rope_factor, a.beta_fast,
                                     a.beta_slow)
+    q = R.rope_tail(q_row[None, None], a.rope_head_dim, rc[[start_pos]], rs[[start_pos]], dtype="bf16")
+    o = R.sparse_attn(q, kv_all, sink, full, a.head_dim ** -0.5, dtype="bf16")
     return R.rope_tail(o, a.rope_head_dim, rc[[start_pos]], rs[[start_pos]], inverse=True, dtype="bf16")[0, 0]
 
 

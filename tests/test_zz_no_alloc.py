@@ -38,7 +38,7 @@ def _decode(name, t, start, cos, sin, ring, out, workspace=None):
     b, nb, k = t["comp"].shape[0], t["comp"].shape[1], t["idx"].shape[-1]
     p = lambda x: ctypes.c_void_p(x.data_ptr())   # noqa: E731
     args = [p(t["q"]), p(ring), p(t["chunk"]), p(t["comp"]), nb * D, nb, p(t["sink"]), p(t["idx"]), k, p(out), b, H, D,
-            W, start, ctypes.c_float(D ** -0.5), p(cos), p(sin), RD, _abi.BF16]
+            W, start, ctypes.c_float(D ** -0.5), p(cos), p(sin), RD, 0, _abi.BF16]
     if workspace is not None:
         args += [p(workspace), workspace.numel()]
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -76,5 +76,6 @@ def test_noalloc_refuses_shapes_beyond_the_static_buffer(gpu):
     assert _abi.mla_workspace_bytes(b, 1, H, D, W + k, torch.bfloat16) > 32 << 20
     fake = ctypes.c_void_p(256)            # never dereferenced: refused before any launch
     rc = lib.dsv41_sparse_mla_decode_noalloc(fake, fake, fake, fake, 16384 * D, 16384, fake, fake, k, fake, b, H, D,
-                                             W, 65535, ctypes.c_float(D ** -0.5), fake, fake, RD, _abi.BF16, None)
+                                             W, 65535, ctypes.c_float(D ** -0.5), fake, fake, RD, 0, _abi.BF16,
+                                             None)
     assert rc == -4 and b"static" in lib.dsv41_last_error_string()
