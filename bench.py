@@ -50,6 +50,7 @@ def parse():
     p.add_argument("--no-fp8", action="store_true", help="skip the fp8-cache decode line")
     p.add_argument("--no-c4", action="store_true", help="skip the 40-layer decode line")
     p.add_argument("--no-mx", action="store_true", help="skip the MXFP4-index decode line")
+    p.add_argument("--no-wo-a", action="store_true", help="skip the grouped output-LoRA line")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--eager", action="store_true",
                    help="launch the decode kernels without HIP graphs (for counter-collecting profilers)")
@@ -413,6 +414,50 @@ def run_prefill(torch, device):
         "flops_note": f"indexer 2*Hi*Di*sum(lens)={fl_idx:.3e} (causal), sparse 4*n*H*(W+K)*D={fl_sparse:.3e}",
         "rows_per_query": rows_sparse,
     }
+
+
+def run_wo_a(torch, device):
+    """The grouped block-diagonal output LoRA (attention.py:176-179) at the release's shape:
+    8 groups, d = 64 * 512 / 8 = 4096 channels per group, rank 1024 (wo_a 64 MiB of bf16). Rows =
+    the decode batch (32, 64) or a prefill chunk (8192). dsv41_wo_a_grouped reads the attention
+    output and the weight in place; beside it, in the same run, torch.bmm (hipBLASLt) on operands
+    copied once into its layout ([G, rows, d] x [G, d, r], contiguous) -- the copy not timed."""
+    from dsv41 import _abi
+    G, R, d = 8, 1024, 4096
+    g = torch.Generator(device=device).manual_seed(SEED + 300)
+    bf = torch.bfloat16
+    w = (torch.randn(G * R, d, generator=g, device=device) * 0.02).to(bf)
+    wT = w.view(G, R, d).transpose(1, 2).contiguous()
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3     # us
+
+    out = {"workload": "grouped wo_a: 8 groups x (4096 -> 1024), bf16 in, fp32 sums, bf16 out", "lines": {}}
+    for rows in (32, 64, 8192):
+        o = torch.randn(rows, G * d, generator=g, device=device).to(bf)
+        y = torch.empty(rows, G * R, dtype=bf, device=device)
+        reps = 50 if rows <= 64 else 10
+        us = timed(lambda: _abi.wo_a_grouped(o, w, G, out=y), reps)
+        ob = o.view(rows, G, d).transpose(0, 1).contiguous()
+        us_bmm = timed(lambda: torch.bmm(ob, wT), reps)
+        nbytes = (G * R * d + rows * G * d + rows * G * R) * 2
+        flops = 2.0 * rows * G * R * d
+        line = {"us": us, "GBps": nbytes / us / 1e3, "hbm_frac": nbytes / us / 1e3 / HBM_PEAK_GBS,
+                "TFLOPs": flops / us / 1e6, "mfma_frac": flops / us / 1e6 / BF16_PEAK_TFLOPS,
+                "algorithmic_bytes": nbytes, "flops": flops, "hipblaslt_bmm_pre_transposed_us": us_bmm}
+        out["lines"][str(rows)] = line
+        log(f"[bench] wo_a rows={rows}: {us:.1f} us ({line['GBps']:.0f} GB/s, {line['TFLOPs']:.0f} TFLOP/s), "
+            f"hipBLASLt bmm on transposed copies {us_bmm:.1f} us")
+        del o, y, ob
+    return out
 
 
 def run_fp8_decode(args, torch, device):
@@ -849,6 +894,12 @@ def main():
                                                                 peaks["bf16_gemm_TFLOPs"])
         except Exception as e:  # report, do not hide: the decode line still prints
             result["prefill"] = {"error": repr(e)}
+    if not args.no_wo_a and not args.eager:
+        try:
+            result["output_lora"] = run_wo_a(torch, device)
+        except Exception as e:
+            result["output_lora"] = {"error": repr(e)}
+        torch.cuda.empty_cache()
     if not args.no_fp8 and not args.eager:
         try:
             result["fp8_cache_decode"] = run_fp8_decode(args, torch, device)

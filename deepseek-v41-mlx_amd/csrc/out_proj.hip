@@ -1,0 +1,367 @@
+// The grouped block-diagonal output LoRA of Attention.__call__ (attention.py:176-179):
+//
+//   out[m, g*r + j] = sum_k o[m, g*d + k] * wo_a[g*r + j, k]
+//
+// o is the attention output [rows, groups*d] (bf16, inverse rope applied), wo_a the Linear weight
+// [groups*r, d] (bf16, unquantized), out [rows, groups*r]. The reference computes the einsum on
+// fp32 copies of both and casts the result to the activation dtype before wo_b. Here every
+// product of two bf16 values is exact in the MFMA and the sums are fp32 (the MFMA's own
+// accumulation, then a fixed-order sum of per-wave partials), so the result differs from the
+// reference's only in the order of the fp32 additions; the bf16 output is the fp32 value rounded
+// to nearest even once, as astype does.
+//
+// Launch shapes (bf16 o and wo_a with d a multiple of 512 and r of 128 -- the release's 4096 and
+// 1024 -- take the MFMA kernels; other shapes and fp32 activations take a plain fp32 kernel):
+//   few rows (decode, <= 128): the kernel streams wo_a from HBM once. A workgroup owns 32
+//     weight rows of one group and all query rows; its four waves split the d channels four ways
+//     (each a quarter of the contraction, loads double-buffered in registers) and their partial
+//     sums meet in LDS in a fixed order. groups * r / 32 workgroups (256 for 8 x 1024), the
+//     group index fastest so that one group's workgroups share an XCD and its L2 copy of o.
+//   many rows (prefill): 128 x 128 output tiles (weight rows x query rows) over 64-channel
+//     steps, both operand tiles copied global -> LDS (global_load_lds_dwordx4, double-buffered)
+//     in an XOR-swizzled layout that the MFMA fragment reads take without bank conflicts; four
+//     waves of 64 x 64 each.
+#include "mfma.h"
+
+namespace dsv41 {
+
+struct WoaArgs {
+  const bf16_t* o;     // [rows, groups * d]
+  const bf16_t* w;     // [groups * r, d]
+  void* out;           // [rows, groups * r], bf16 or fp32
+  int rows, groups, d, r;
+};
+
+// ------------------------------------------------------------------ any shape
+
+// One thread per output: the d products of one row of o and one weight row, summed in fp32 in
+// channel order (products of bf16 values are exact; fp32 ones round). For the shapes and dtypes
+// the MFMA kernels do not take (small test configurations, fp32 activations).
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void wo_a_plain_kernel(const TI* o, const TI* w, TO* out, int rows, int groups,
+                                                          int d, int r) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;      // over rows * groups * r
+  if (i >= (int64_t)rows * groups * r) return;
+  const int64_t gr = (int64_t)groups * r;
+  const int64_t m = i / gr;
+  const int gj = (int)(i - m * gr), grp = gj / r;
+  const TI* op = o + m * groups * d + (int64_t)grp * d;
+  const TI* wp = w + (int64_t)gj * d;
+  float acc = 0.0f;
+  for (int k = 0; k < d; ++k) acc += io<TI>::ld(op + k) * io<TI>::ld(wp + k);
+  io<TO>::st(out + i, acc);
+}
+
+// Four consecutive outputs of one query row.
+template <typename TO>
+__device__ __forceinline__ void store4(TO* p, f32x4 v);
+template <>
+__device__ __forceinline__ void store4<bf16_t>(bf16_t* p, f32x4 v) {
+  uint2 s;
+  s.x = pack2_bf16(v[0], v[1]);
+  s.y = pack2_bf16(v[2], v[3]);
+  *reinterpret_cast<uint2*>(p) = s;
+}
+template <>
+__device__ __forceinline__ void store4<float>(float* p, f32x4 v) {
+  *reinterpret_cast<f32x4*>(p) = v;
+}
+
+// ------------------------------------------------------------------ few rows
+
+constexpr int kSkRows = 32;   // weight rows per workgroup
+
+// MT 16-row tiles of query rows. The MFMA's A operand is a 16-row weight tile and its B operand
+// a 16-row query tile, so lane (l16, g) receives out[query 16 mt + l16][weight rows 4g .. 4g + 3]:
+// four consecutive outputs of one row.
+template <int MT, typename TO>
+__global__ __launch_bounds__(256) void wo_a_rows_kernel(WoaArgs a) {
+  constexpr int U = MT <= 4 ? 4 : 2;     // 32-channel steps per load batch
+  constexpr int CH = 32 * U;
+  __shared__ __align__(16) f32x4 red[4][MT * 2][64];
+  const int grp = blockIdx.x % a.groups, rt = blockIdx.x / a.groups;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+  const int kw = a.d >> 2, k0 = wave * kw;        // this wave's quarter of the channels
+  const bf16_t* w0 = a.w + ((int64_t)grp * a.r + rt * kSkRows + l16) * a.d + k0 + 8 * g;
+  const bf16_t* w1 = w0 + 16 * (int64_t)a.d;
+  const bf16_t* op[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = min(16 * mt + l16, a.rows - 1);   // rows past the end repeat the last (not stored)
+    op[mt] = a.o + (int64_t)m * a.groups * a.d + (int64_t)grp * a.d + k0 + 8 * g;
+  }
+  f32x4 acc[MT][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 wa[2][U][2], ob[2][U][MT];
+  auto load = [&](bf16x8 (&wv)[U][2], bf16x8 (&ov)[U][MT], int k) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      wv[u][0] = ld_bf16x8(w0 + k + 32 * u);
+      wv[u][1] = ld_bf16x8(w1 + k + 32 * u);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) ov[u][mt] = ld_bf16x8(op[mt] + k + 32 * u);
+    }
+  };
+  auto mma = [&](const bf16x8 (&wv)[U][2], const bf16x8 (&ov)[U][MT]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[mt][0] = mfma16x16x32(wv[u][0], ov[u][mt], acc[mt][0]);
+        acc[mt][1] = mfma16x16x32(wv[u][1], ov[u][mt], acc[mt][1]);
+      }
+  };
+  // Two register buffers: the next batch is in flight while this one multiplies. Every path
+  // issues the same loads (the batch after the last re-reads the last), so the compiler's
+  // wait counts stay exact.
+  const int steps = kw / CH;
+  load(wa[0], ob[0], 0);
+  int s = 0;
+  for (; s + 2 <= steps; s += 2) {
+    load(wa[1], ob[1], (s + 1) * CH);
+    mma(wa[0], ob[0]);
+    load(wa[0], ob[0], min(s + 2, steps - 1) * CH);
+    mma(wa[1], ob[1]);
+  }
+  if (s < steps) mma(wa[0], ob[0]);
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    red[wave][mt * 2][lane] = acc[mt][0];
+    red[wave][mt * 2 + 1][lane] = acc[mt][1];
+  }
+  __syncthreads();
+  const int64_t ostride = (int64_t)a.groups * a.r;
+  TO* out = reinterpret_cast<TO*>(a.out);
+  for (int tile = wave; tile < MT * 2; tile += 4) {
+    const int mt = tile >> 1, t = tile & 1;
+    const int m = 16 * mt + l16;
+    f32x4 v = red[0][tile][lane];
+#pragma unroll
+    for (int p = 1; p < 4; ++p) {
+      const f32x4 q = red[p][tile][lane];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = v[e] + q[e];
+    }
+    if (m < a.rows) store4<TO>(out + m * ostride + (int64_t)grp * a.r + rt * kSkRows + 16 * t + 4 * g, v);
+  }
+}
+
+// ------------------------------------------------------------------ many rows
+
+constexpr int kTileR = 128;   // weight rows of the smallest output tile (r is a multiple of it)
+
+// 16-byte chunk c of tile row `row` (rows of BK bf16: BK / 8 chunks) sits at slot c ^ swz(row).
+// A fragment read takes one chunk of 16 consecutive rows; with these slots no two of those lanes
+// share a bank, whether the banks serve 8 lanes of 16 bytes (128 bytes) per cycle or 16 lanes
+// (256 bytes).
+template <int BK>
+__device__ __forceinline__ int tile_swz(int row) {
+  if constexpr (BK == 64) return (row & 7) ^ ((row >> 3) & 1);
+  else return ((row >> 1) & 3) ^ ((row >> 3) & 1);
+}
+
+// Output tile of 32 WR weight rows x 32 WM query rows: a 2 x 2 grid of waves, each 16 WR x 16 WM
+// (WR x WM MFMA tiles). BK channels per step; NS steps of both operand tiles in LDS at once
+// (NS - 1 in flight while one is multiplied).
+template <int WR, int WM, int BK, int NS>
+struct TileCfg {
+  static constexpr int TR = 32 * WR, TM = 32 * WM;
+  static constexpr int RB = BK * 2;                 // bytes per tile row
+  static constexpr int CPR = BK / 8;                // 16-byte chunks per row
+  static constexpr int RPI = 1024 / RB;             // rows per copy instruction
+  static constexpr int NW = TR * RB / 4096, NO = TM * RB / 4096;   // copies per wave per step
+  static constexpr int STAGE = (TR + TM) * RB;
+  static constexpr int LDS = NS * STAGE;
+  static_assert(BK == 32 || BK == 64, "32- or 64-channel steps");
+  static_assert(NW * 4096 == TR * RB && NO * 4096 == TM * RB, "whole copy instructions per wave");
+};
+
+template <int N>
+__device__ __forceinline__ void wait_copies(int pending) {
+  // at most `pending` later steps of per_step copies each may stay in flight
+  if constexpr (N >= 3) {
+    if (pending >= 3) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * N) : "memory");
+      return;
+    }
+  }
+  if constexpr (N >= 2) {
+    if (pending == 2) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * N) : "memory");
+      return;
+    }
+  }
+  if (pending >= 1) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+    return;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+template <int WR, int WM, int BK, int NS, typename TO>
+__global__ __launch_bounds__(256, (TileCfg<WR, WM, BK, NS>::LDS <= 80 * 1024) ? 2 : 1) void wo_a_tiles_kernel(
+    WoaArgs a) {
+  using C = TileCfg<WR, WM, BK, NS>;
+  __shared__ __align__(16) uint8_t lds[C::LDS];   // NS x [weight tile][query tile]
+  const int mtiles = (a.rows + C::TM - 1) / C::TM, rtiles = a.r / C::TR;
+  // consecutive tiles on one XCD, the weight tile fastest: the rtiles workgroups that read one
+  // query tile share that XCD's L2
+  const int total = (int)gridDim.x;
+  const int tile = total % 8 ? (int)blockIdx.x : ((int)blockIdx.x % 8) * (total / 8) + (int)blockIdx.x / 8;
+  const int rt = tile % rtiles, mt = (tile / rtiles) % mtiles, grp = tile / (rtiles * mtiles);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+  const int wr = (wave & 1) * 16 * WR, wm = (wave >> 1) * 16 * WM;   // this wave's block
+
+  // copy sources: wave w fills rows [w TR/4, (w+1) TR/4) of the weight tile and [w TM/4, ..) of
+  // the query tile, RPI rows per instruction; lane l writes slot l % CPR of row l / CPR of its
+  // instruction's rows, i.e. chunk slot ^ swz(row) of that row
+  uint64_t wsrc[C::NW], osrc[C::NO];
+#pragma unroll
+  for (int j = 0; j < C::NW; ++j) {
+    const int row = wave * (C::TR / 4) + j * C::RPI + lane / C::CPR;
+    const int chunk = (lane % C::CPR) ^ tile_swz<BK>(row);
+    wsrc[j] = reinterpret_cast<uint64_t>(a.w + ((int64_t)grp * a.r + rt * C::TR + row) * a.d + 8 * chunk);
+  }
+#pragma unroll
+  for (int j = 0; j < C::NO; ++j) {
+    const int row = wave * (C::TM / 4) + j * C::RPI + lane / C::CPR;
+    const int chunk = (lane % C::CPR) ^ tile_swz<BK>(row);
+    const int64_t orow = min(mt * C::TM + row, a.rows - 1);   // rows past the end: not stored
+    osrc[j] = reinterpret_cast<uint64_t>(a.o + orow * a.groups * a.d + (int64_t)grp * a.d + 8 * chunk);
+  }
+  const uint32_t lds0 = lds_offset(lds);
+  auto issue = [&](int buf, int k) {
+    const uint32_t wdst = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(lds0 + (uint32_t)(buf * C::STAGE) + (uint32_t)(wave * (C::TR / 4) * C::RB)));   // wave-uniform: M0
+    const uint32_t odst = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(lds0 + (uint32_t)(buf * C::STAGE + C::TR * C::RB) + (uint32_t)(wave * (C::TM / 4) * C::RB)));
+    const uint64_t kb = (uint64_t)k * 2;
+#pragma unroll
+    for (int j = 0; j < C::NW; ++j) dma16_vaddr(wsrc[j] + kb, wdst + j * 1024);
+#pragma unroll
+    for (int j = 0; j < C::NO; ++j) dma16_vaddr(osrc[j] + kb, odst + j * 1024);
+  };
+  auto frag = [&](const uint8_t* t, int row, int chunk) {
+    return as_bf16x8(*reinterpret_cast<const uint4*>(t + row * C::RB + ((chunk ^ tile_swz<BK>(row)) << 4)));
+  };
+
+  f32x4 acc[WR][WM];
+#pragma unroll
+  for (int i = 0; i < WR; ++i)
+#pragma unroll
+    for (int j = 0; j < WM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // One barrier per step: after it, step kt is in LDS for every wave and every wave is done with
+  // step kt - 1, whose buffer then takes step kt + NS - 1.
+  const int nk = a.d / BK;
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p)
+    if (p < nk) issue(p, p * BK);
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_copies<C::NW + C::NO>(min(NS - 2, nk - 1 - kt));   // this wave's copies of step kt landed
+    __syncthreads();
+    if (kt + NS - 1 < nk) issue((kt + NS - 1) % NS, (kt + NS - 1) * BK);
+    const uint8_t* wt = lds + (kt % NS) * C::STAGE;
+    const uint8_t* qt = wt + C::TR * C::RB;
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      bf16x8 af[WR], bf[WM];
+#pragma unroll
+      for (int i = 0; i < WR; ++i) af[i] = frag(wt, wr + 16 * i + l16, 4 * ks + g);
+#pragma unroll
+      for (int j = 0; j < WM; ++j) bf[j] = frag(qt, wm + 16 * j + l16, 4 * ks + g);
+#pragma unroll
+      for (int i = 0; i < WR; ++i)
+#pragma unroll
+        for (int j = 0; j < WM; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
+    }
+  }
+
+  const int64_t ostride = (int64_t)a.groups * a.r;
+  TO* out = reinterpret_cast<TO*>(a.out);
+#pragma unroll
+  for (int j = 0; j < WM; ++j) {
+    const int m = mt * C::TM + wm + 16 * j + l16;
+    if (m >= a.rows) continue;
+#pragma unroll
+    for (int i = 0; i < WR; ++i)
+      store4<TO>(out + m * ostride + (int64_t)grp * a.r + rt * C::TR + wr + 16 * i + 4 * g, acc[i][j]);
+  }
+}
+
+template <int WR, int WM, int BK, int NS, typename TO>
+static void launch_tiles(const WoaArgs& a, hipStream_t stream) {
+  using C = TileCfg<WR, WM, BK, NS>;
+  const int64_t tiles = (int64_t)a.groups * (a.r / C::TR) * ((a.rows + C::TM - 1) / C::TM);
+  hipLaunchKernelGGL((wo_a_tiles_kernel<WR, WM, BK, NS, TO>), dim3((unsigned)tiles), dim3(256), 0, stream, a);
+}
+
+template <typename TO>
+static void launch_wo_a(const WoaArgs& a, hipStream_t stream) {
+  if (a.rows <= 128) {
+    const dim3 grid((unsigned)(a.groups * (a.r / kSkRows)));
+    switch ((a.rows + 15) / 16) {
+      case 1: hipLaunchKernelGGL((wo_a_rows_kernel<1, TO>), grid, dim3(256), 0, stream, a); break;
+      case 2: hipLaunchKernelGGL((wo_a_rows_kernel<2, TO>), grid, dim3(256), 0, stream, a); break;
+      case 3: hipLaunchKernelGGL((wo_a_rows_kernel<3, TO>), grid, dim3(256), 0, stream, a); break;
+      case 4: hipLaunchKernelGGL((wo_a_rows_kernel<4, TO>), grid, dim3(256), 0, stream, a); break;
+      case 5: hipLaunchKernelGGL((wo_a_rows_kernel<5, TO>), grid, dim3(256), 0, stream, a); break;
+      case 6: hipLaunchKernelGGL((wo_a_rows_kernel<6, TO>), grid, dim3(256), 0, stream, a); break;
+      case 7: hipLaunchKernelGGL((wo_a_rows_kernel<7, TO>), grid, dim3(256), 0, stream, a); break;
+      default: hipLaunchKernelGGL((wo_a_rows_kernel<8, TO>), grid, dim3(256), 0, stream, a); break;
+    }
+    return;
+  }
+  launch_tiles<4, 4, 64, 2, TO>(a, stream);
+}
+
+}  // namespace dsv41
+
+using namespace dsv41;
+
+template <typename TI>
+static int launch_wo_a_plain(const void* o, const void* w, void* out, int rows, int groups, int d, int r,
+                             int out_dtype, hipStream_t stream) {
+  const int64_t n = (int64_t)rows * groups * r;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  const TI* oi = static_cast<const TI*>(o);
+  const TI* wi = static_cast<const TI*>(w);
+  if (out_dtype == DSV41_BF16)
+    hipLaunchKernelGGL((wo_a_plain_kernel<TI, bf16_t>), grid, dim3(256), 0, stream, oi, wi,
+                       static_cast<bf16_t*>(out), rows, groups, d, r);
+  else
+    hipLaunchKernelGGL((wo_a_plain_kernel<TI, float>), grid, dim3(256), 0, stream, oi, wi, static_cast<float*>(out),
+                       rows, groups, d, r);
+  return 0;
+}
+
+extern "C" int dsv41_wo_a_grouped(const void* o, const void* wo_a, void* out, int32_t rows, int32_t groups,
+                                  int32_t d, int32_t r, int32_t dtype, int32_t out_dtype, hipStream_t stream) {
+  const char* what = "dsv41_wo_a_grouped";
+  DSV41_REQUIRE(o && wo_a && out, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(rows >= 0 && groups > 0 && d > 0 && r > 0, DSV41_E_ARG, "%s: bad sizes", what);
+  DSV41_REQUIRE(dtype == DSV41_BF16 || dtype == DSV41_F32, DSV41_E_DTYPE, "%s: dtype %d not supported (BF16 or F32)",
+                what, dtype);
+  DSV41_REQUIRE(out_dtype == DSV41_BF16 || out_dtype == DSV41_F32, DSV41_E_DTYPE,
+                "%s: out dtype %d not supported (BF16 or F32)", what, out_dtype);
+  DSV41_REQUIRE(aligned16(o) && aligned16(wo_a) && aligned16(out), DSV41_E_ARG, "%s: tensors must be 16-byte aligned",
+                what);
+  DSV41_REQUIRE((int64_t)groups * r * d < (1ll << 40) && (int64_t)rows * groups * (d > r ? d : r) < (1ll << 40),
+                DSV41_E_ARG, "%s: tensors too large", what);
+  if (rows == 0) return 0;
+  const bool mfma = dtype == DSV41_BF16 && d % 512 == 0 && r % kTileR == 0;   // every tile shape's multiples
+  if (!mfma) {
+    DSV41_REQUIRE(((int64_t)rows * groups * r + 255) / 256 < (1ll << 32), DSV41_E_ARG, "%s: too many outputs", what);
+    if (dtype == DSV41_BF16) launch_wo_a_plain<bf16_t>(o, wo_a, out, rows, groups, d, r, out_dtype, stream);
+    else launch_wo_a_plain<float>(o, wo_a, out, rows, groups, d, r, out_dtype, stream);
+    return check_launch(what);
+  }
+  DSV41_REQUIRE((int64_t)groups * (r / kTileR) * ((rows + 127) / 128) < (1ll << 31), DSV41_E_ARG,
+                "%s: too many tiles", what);
+  WoaArgs a{static_cast<const bf16_t*>(o), static_cast<const bf16_t*>(wo_a), out, rows, groups, d, r};
+  if (out_dtype == DSV41_BF16) launch_wo_a<bf16_t>(a, stream);
+  else launch_wo_a<float>(a, stream);
+  return check_launch(what);
+}

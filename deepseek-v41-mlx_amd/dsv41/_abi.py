@@ -93,6 +93,7 @@ _SIGNATURES = {
     "dsv41_sparse_mla_packed_decode": [_c_p, _c_p, _i64, _c_p, _c_p, _i64, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32,
                                        _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_window_write_mxfp8": [_c_p, _i64, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_wo_a_grouped": [_c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_comp_write_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32,
                              _i32, _c_p],
     "dsv41_index_key_publish_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32,
@@ -476,6 +477,31 @@ def window_write_mxfp8(win_kv8, kv, start_pos):
 def fp4_row_bytes(d: int) -> int:
     """Bytes of one packed fp4 compressed-cache row: d/2 code bytes, then d/16 e4m3 scales."""
     return d // 2 + d // 16
+
+
+def wo_a_grouped(o, wo_a, groups, out=None, out_dtype=None):
+    """The grouped block-diagonal output LoRA (attention.py:176-179): o [..., groups*d] (the
+    attention output; its leading dims are the rows), wo_a [groups*r, d] (the Linear weight,
+    read in place), both bf16 or both float32. Returns [..., groups*r] in out_dtype (o's dtype
+    by default, the reference's cast of its fp32 einsum; float32 gives the einsum itself)."""
+    name = "dsv41_wo_a_grouped"
+    _gpu(name, o, wo_a, out)
+    _contig(name, o, wo_a)
+    if o.dtype != wo_a.dtype:
+        raise ValueError(f"{name}: o {o.dtype} and wo_a {wo_a.dtype} must share a dtype")
+    if groups <= 0 or wo_a.dim() != 2 or wo_a.shape[0] % groups:
+        raise ValueError(f"{name}: wo_a {tuple(wo_a.shape)} is not [groups * r, d] for {groups} groups")
+    d, r = wo_a.shape[1], wo_a.shape[0] // groups
+    if o.dim() < 1 or o.shape[-1] != groups * d:
+        raise ValueError(f"{name}: o's last dim must be groups * d = {groups * d}, got {tuple(o.shape)}")
+    out_dtype = o.dtype if out_dtype is None else out_dtype
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"{name}: out_dtype must be bf16 or float32")
+    rows = o.numel() // (groups * d)
+    out = _out(name, out, (*o.shape[:-1], groups * r), out_dtype, o.device)
+    _call(name, _ptr(o), _ptr(wo_a), _ptr(out), rows, groups, d, r, dtype_code(o, name), dtype_code(out, name),
+          _stream(o))
+    return out
 
 
 def comp_write_fp4(latents, comp_kv4, g0, ratio, cos, sin, rd):

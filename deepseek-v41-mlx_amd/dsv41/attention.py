@@ -1,7 +1,7 @@
 """One V4.1 attention layer (deepseek_v41_mlx/attention.py:53-179) on the GPU.
 
-The projections (wq_a, wq_b, wkv, the compressor / indexer projections, wo_a, wo_b) are torch
-GEMMs; everything between them runs in HIP kernels:
+The dense projections (wq_a, wq_b, wkv, the compressor / indexer projections, wo_b) are torch
+GEMMs; everything between them, and the grouped block-diagonal wo_a, runs in HIP kernels:
 
   q      : q_norm (RMSNorm kernel); q's rope tail is applied by the attention launch as it
            loads q (no separate pass over q)
@@ -13,6 +13,8 @@ GEMMs; everything between them runs in HIP kernels:
            most recent owner's comp_kv in place -- the reference's concatenation of the three
            (attention.py:127, 165-168) never happens -- and applies the inverse rope to the
            output tail before storing it.
+  output : the grouped wo_a (dsv41_wo_a_grouped: exact products, fp32 sums, one rounding to
+           x's dtype), reading the attention output and wo_a's weight in place; then wo_b.
 The window ring is written after the attention kernel has read the previous window, which
 is equivalent to the reference's write-before-concatenate order because the concatenated
 copy held the old ring contents.
@@ -191,9 +193,6 @@ class Attention(torch.nn.Module):
         if not decode:
             lc.write_window(start_pos, kv)
 
-        # grouped block-diagonal wo_a in fp32, then wo_b (attention.py:176-179)
-        G, R = self.n_groups, self.o_lora_rank
-        og = o.view(bsz * n, G, -1).float().transpose(0, 1)                      # [G, bn, d]
-        wa = self.wo_a.weight.float().view(G, R, -1).transpose(1, 2).contiguous()  # [G, d, R]
-        oa = torch.matmul(og.contiguous(), wa).transpose(0, 1).reshape(bsz, n, G * R)
-        return self.wo_b(oa.to(x.dtype))
+        # grouped block-diagonal wo_a, fp32 sums cast to x's dtype, then wo_b (attention.py:176-179)
+        oa = _abi.wo_a_grouped(o.view(bsz, n, -1), self.wo_a.weight, self.n_groups, out_dtype=x.dtype)
+        return self.wo_b(oa)

@@ -486,6 +486,19 @@ int dsv41_sparse_mla_packed_decode(const void* q, uint8_t* win_kv8, int64_t ring
                                    float scale, const float* cos_tab, const float* sin_tab, int32_t rd, int32_t q_rd,
                                    void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* The grouped block-diagonal output LoRA of Attention.__call__, deepseek_v41_mlx/attention.py:
+ * 176-179 (DeepSeek's docs/reference/model.py:783-787): o viewed as [rows, groups, d], wo_a's
+ * weight as [groups, r, d], einsum "bsgd,grd->bsgr" in fp32, cast to the activation dtype:
+ *   out[m, g*r + j] = sum_k o[m, g*d + k] * wo_a[g*r + j, k].
+ * o [rows, groups*d] (the attention output) and wo_a [groups*r, d] (nn.Linear's weight,
+ * unquantized) in dtype (BF16 or F32); out [rows, groups*r] in out_dtype: BF16 (the fp32 sum
+ * rounded to nearest even once, as astype does) or F32. Sums are fp32 in a fixed order:
+ * deterministic, equal to the reference up to the order of fp32 additions (bf16 products are
+ * exact). bf16 with d a multiple of 512 and r of 128 (the release's 4096 and 1024) runs on MFMA;
+ * any other shape, and fp32, on a plain fp32 kernel. */
+int dsv41_wo_a_grouped(const void* o, const void* wo_a, void* out, int32_t rows, int32_t groups,
+                       int32_t d, int32_t r, int32_t dtype, int32_t out_dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

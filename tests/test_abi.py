@@ -444,6 +444,15 @@ def test_sparse_mla_wrappers_check_buffers(host_abi):
     _reaches_launch(callp())
     _reaches_launch(callp(write_ring=True))
     _reaches_launch(callp(write_ring=True, q_rd=64))
+    o = torch.zeros(3, 1, 8 * 512, dtype=torch.bfloat16)
+    wa = torch.zeros(8 * 128, 512, dtype=torch.bfloat16)
+    _reaches_launch(lambda: A.wo_a_grouped(o, wa, 8))
+    _reaches_launch(lambda: A.wo_a_grouped(o, wa, 8, out=torch.zeros(3, 1, 1024), out_dtype=torch.float32))
+    _refused(lambda: A.wo_a_grouped(o, wa, 8, out=torch.zeros(3, 1, 1024)), "out must be")   # bf16 by default
+    _refused(lambda: A.wo_a_grouped(o, wa.float(), 8), "share a dtype")
+    _refused(lambda: A.wo_a_grouped(o, wa, 3), "groups")
+    _refused(lambda: A.wo_a_grouped(o[..., :-8].contiguous(), wa, 8), "last dim")
+    _refused(lambda: A.wo_a_grouped(o, wa, 8, out=torch.zeros(3, 1, 1000, dtype=torch.bfloat16)), "out must be")
     _reaches_launch(callp(comp_kv4=None, n_comp=0, idx=None))
     _refused(callp(win_kv8=ring), "window ring")                      # a bf16 ring is not MXFP8
     _refused(callp(win_kv8=ring8[:, :, :512]), "window ring")

@@ -1178,3 +1178,47 @@ def test_indexer_topk_mxq_fp8_equals_two_calls(gpu, b, n, h, nb, topk, start, rb
         return
     scores = _abi.indexer_score_mxq_fp8(q_mx, w, 0.01, codes, scales, rb, nb, start, 4, cand)
     assert torch.equal(fused, _abi.topk_select(scores, topk, start, 4, 129))
+
+
+# ------------------------------------------------------------------ grouped output LoRA
+
+
+@pytest.mark.parametrize("rows,groups,d,r,dt", [
+    (1, 8, 4096, 1024, "bf16"),       # the release's output LoRA, one decode row
+    (32, 8, 4096, 1024, "bf16"),      # bs32 decode
+    (37, 8, 4096, 1024, "bf16"),      # a partial 16-row tile
+    (64, 8, 4096, 1024, "bf16"),
+    (100, 2, 512, 128, "bf16"),       # the 8-tile row kernel, a partial tile
+    (128, 8, 4096, 1024, "bf16"),
+    (129, 8, 4096, 1024, "bf16"),     # the tiled kernel, one row in the second row tile
+    (700, 4, 1024, 256, "bf16"),
+    (2048, 8, 4096, 1024, "bf16"),    # a prefill chunk
+    (9, 2, 128, 16, "bf16"),          # a test configuration's shape: the plain kernel
+    (9, 2, 128, 16, "f32"),
+    (40, 8, 512, 128, "f32"),         # fp32 activations: the plain kernel
+])
+def test_wo_a_grouped(gpu, rows, groups, d, r, dt):
+    """dsv41_wo_a_grouped = the reference's einsum("bsgd,grd->bsgr") on fp32 copies, cast back
+    (attention.py:176-179). Against a float64 product of the same values: every fp32 output
+    within 2e-5 of sum_k |o_k w_k| (fp32 sums; bf16 products are exact); the bf16 output is the
+    fp32 output rounded once, bit for bit; repeated calls are bit-identical."""
+    from dsv41 import _abi
+    g = torch.Generator(device=gpu).manual_seed(SEED_BASE + rows + d)
+    tdt = DT[dt]
+    o = torch.randn(rows, groups * d, generator=g, device=gpu).to(tdt)
+    w = (torch.randn(groups * r, d, generator=g, device=gpu) * 0.02).to(tdt)
+    got32 = _abi.wo_a_grouped(o, w, groups, out_dtype=torch.float32)
+    got = _abi.wo_a_grouped(o, w, groups)
+    again = _abi.wo_a_grouped(o, w, groups)
+    torch.cuda.synchronize()
+    assert got.dtype == tdt and got.shape == (rows, groups * r)
+    o64 = o.double().view(rows, groups, d).transpose(0, 1).contiguous()    # [G, rows, d]
+    w64 = w.double().view(groups, r, d).transpose(1, 2).contiguous()       # [G, d, r]
+    ref = torch.bmm(o64, w64).transpose(0, 1).reshape(rows, groups * r)
+    mag = torch.bmm(o64.abs(), w64.abs()).transpose(0, 1).reshape(rows, groups * r)
+    err = ((got32.double() - ref).abs() / mag.clamp_min(1e-30)).max().item()
+    assert err < 2e-5, f"fp32 sums off by {err:.2e} of sum |o w|"
+    assert torch.equal(got, got32.to(tdt)), "the output is the fp32 result rounded once"
+    assert torch.equal(got, again), "repeated calls differ"
+    if dt == "bf16":                   # and so mostly equal to the float64 result rounded once
+        assert (got != ref.to(tdt)).float().mean().item() < 2e-3
