@@ -89,11 +89,13 @@ def test_contract_violations_are_reported_by_the_library():
     rc = lib.dsv41_compress_pool(fake, fake, fake, fake, fake, fake, 1, 1, 64, 1, 0, ctypes.c_float(0),
                                  1, None)
     assert rc == -1 and b"ratio" in lib.dsv41_last_error_string()
-    # two-stage top-k: the workspace is checked before any launch
-    need = _abi.topk_workspace_bytes(16, 32768, 1024)
-    rc = lib.dsv41_topk_select_ws(fake, fake, 16, 1, 32768, 1024, 131071, 4, 129, None, 0, None)
+    # two-stage top-k: the workspace is checked before any launch (the shape must take that form,
+    # or the call below would launch on the fake pointers)
+    need = _abi.topk_workspace_bytes(16, 32768, 512)
+    assert need > 0
+    rc = lib.dsv41_topk_select_ws(fake, fake, 16, 1, 32768, 512, 131071, 4, 129, None, 0, None)
     assert rc == -4 and b"workspace" in lib.dsv41_last_error_string()
-    rc = lib.dsv41_topk_select_ws(fake, fake, 16, 1, 32768, 1024, 131071, 4, 129, fake, need - 1, None)
+    rc = lib.dsv41_topk_select_ws(fake, fake, 16, 1, 32768, 512, 131071, 4, 129, fake, need - 1, None)
     assert rc == -4
     # fused indexer + top-k: unserved shapes and a missing or short workspace, before any launch
     need = _abi.indexer_topk_workspace_bytes(32, 1, 64, 128, 16384, 512)
@@ -121,12 +123,15 @@ def test_contract_violations_are_reported_by_the_library():
 
 def test_topk_workspace_sizes():
     """Two stages (a workspace) only for rows over 16384 scores with k <= 2048 whose chunk lists
-    fit one register workgroup: keys and positions of each 4096-score chunk's best k."""
+    fit one register workgroup: keys and positions of each 4096-score chunk's best k. With k a
+    quarter of a chunk or more, rows one 32-keys-per-thread workgroup holds stay one stage."""
     from dsv41 import _abi
     assert _abi.topk_workspace_bytes(32, 16384, 512) == 0            # one workgroup per row
     assert _abi.topk_workspace_bytes(16, 20000, 5000) == 0           # k above half a chunk
     assert _abi.topk_workspace_bytes(1, 4 << 20, 2048) == 0          # lists too long for one stage-2 group
-    assert _abi.topk_workspace_bytes(16, 32768, 1024) == 2 * 16 * 8 * 1024 * 4
+    assert _abi.topk_workspace_bytes(16, 32768, 1024) == 0           # k = chunk / 4, row <= 32K: one stage
+    assert _abi.topk_workspace_bytes(1, 40000, 1024) == 2 * ((10 * 1024 * 4 + 255) // 256 * 256)   # row > 32K
+    assert _abi.topk_workspace_bytes(16, 32768, 512) == 2 * 16 * 8 * 512 * 4
     assert _abi.topk_workspace_bytes(3, 16390, 512) == 2 * (((3 * 5 * 512 * 4) + 255) // 256 * 256)
     assert _abi.topk_workspace_bytes(0, 32768, 1024) == 0
 
