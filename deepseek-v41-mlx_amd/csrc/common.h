@@ -57,8 +57,11 @@ template <> struct io<bf16_t> {
 
 // 2**ceil(log2(r)) from IEEE bits (the TileLang fast_round_scale, kernel.py:22-37).
 // ue8m0 scale byte -> float 2^(e-127) (e = 0 is 2^-127, a subnormal; 255 is NaN).
+// e << 23 is the float 2^(e-127) for 1 <= e <= 254; e = 0 and e = 255 differ from it in bit 22 only
+// (0x00400000, 0x7fc00000), so the special cases are one select and the whole conversion has no
+// branch.
 __device__ __forceinline__ float e8m0_to_float(uint32_t e) {
-  return e == 0u ? __uint_as_float(0x00400000u) : (e == 255u ? __uint_as_float(0x7fc00000u) : __uint_as_float(e << 23));
+  return __uint_as_float((e << 23) | ((e == 0u || e == 255u) ? 0x00400000u : 0u));
 }
 
 __device__ __forceinline__ float pow2_ceil_log2(float r) {

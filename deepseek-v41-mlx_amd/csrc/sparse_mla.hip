@@ -187,7 +187,9 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
     const int slot = t % NS;
     const int mine = t * R + wave * RPW + (lane % RPW);
     const uint64_t mp = mine < cnt ? (direct ? entry_row(mine) : rows[mine]) : 0ull;
-    if (lane < RPW) vrow[slot][wave * RPW + lane] = mp != 0ull ? 1 : 0;
+    // the row's kind for the masking (nonzero = a row) and the dequantization: 0 masked, 1 bf16,
+    // 2 packed compressed (tag 1), 3 MXFP8 ring (tag 2)
+    if (lane < RPW) vrow[slot][wave * RPW + lane] = mp != 0ull ? (uint8_t)(1u + ((uint32_t)mp & 3u)) : 0;
     const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
     const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_base + (uint32_t)(slot * SLOT + wave * RPW * RS));
 #pragma unroll
@@ -261,32 +263,34 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
     if constexpr (PACKED) {
       // this wave's own packed rows of step t have landed: dequantize them in place. All of its
       // rows are read before any is written (a single wave converts them), so the bf16 output
-      // may overlap the bytes it came from, and the reads go out together. Lane l converts
-      // channels 8l..8l+7: fp8 rows (tag 2, or tag 1 of an fp8 compressed cache) hold their
-      // codes at [D, 2D) and the ue8m0 scale of the lane's block at 2D + l/4; fp4 rows (tag 1)
-      // hold code bytes 4l..4l+3 at F4OFF and the e4m3 scale byte l/2 after the codes.
+      // may overlap the bytes it came from. Lane l converts channels 8l..8l+7: fp8 rows (kind 3,
+      // or kind 2 of an fp8 compressed cache) hold their codes at [D, 2D) and the ue8m0 scale of
+      // the lane's block at 2D + l/4; fp4 rows (kind 2) hold code bytes 4l..4l+3 at F4OFF and the
+      // e4m3 scale byte l/2 after the codes. The kinds come from one LDS read per 4 rows as
+      // wave-uniform values, so the loads of all rows go out together with no branch between
+      // them (a per-row conditional read serialized them: ~1 us per step).
       uint8_t* sb = ring + (t % NS) * SLOT + wave * RPW * RS;
+      const uint32_t* kw = reinterpret_cast<const uint32_t*>(&vrow[t % NS][wave * RPW]);
+      uint32_t kinds[RPW / 4];
+#pragma unroll
+      for (int w4 = 0; w4 < RPW / 4; ++w4) kinds[w4] = (uint32_t)__builtin_amdgcn_readfirstlane((int)kw[w4]);
       uint2 raw[RPW];
       float sc[RPW];
-      uint32_t tag[RPW];
 #pragma unroll
       for (int rr = 0; rr < RPW; ++rr) {
-        const int ei = t * R + wave * RPW + rr;
-        tag[rr] = (uint32_t)(ei < cnt ? rows[ei] : 0ull) & 3u;
+        const uint32_t kind = (kinds[rr / 4] >> (8 * (rr % 4))) & 0xFFu;
+        const bool f4row = F4 && kind == 2u;
         const uint8_t* row = sb + rr * RS;
-        if (F4 && tag[rr] == 1u) {
-          raw[rr] = make_uint2(*reinterpret_cast<const uint32_t*>(row + F4OFF + lane * 4), 0u);
-          sc[rr] = __builtin_amdgcn_cvt_f32_fp8((int)row[F4OFF + D / 2 + (lane >> 1)], 0);
-        } else {
-          raw[rr] = *reinterpret_cast<const uint2*>(row + D + lane * 8);
-          sc[rr] = e8m0_to_float(row[2 * D + (lane >> 2)]);
-        }
+        raw[rr] = *reinterpret_cast<const uint2*>(row + (f4row ? F4OFF + lane * 4 : D + lane * 8));
+        const uint32_t sbyte = row[f4row ? F4OFF + D / 2 + (lane >> 1) : 2 * D + (lane >> 2)];
+        sc[rr] = f4row ? __builtin_amdgcn_cvt_f32_fp8((int)sbyte, 0) : e8m0_to_float(sbyte);
       }
 #pragma unroll
       for (int rr = 0; rr < RPW; ++rr) {
+        const uint32_t kind = (kinds[rr / 4] >> (8 * (rr % 4))) & 0xFFu;
         bf16x8* out = reinterpret_cast<bf16x8*>(sb + rr * RS + lane * 16);
-        if (F4 && tag[rr] == 1u) *out = dequant_e2m1x8(raw[rr].x, sc[rr]);
-        else if (tag[rr] != 0u) *out = dequant_e4m3x8(raw[rr].x, raw[rr].y, sc[rr]);
+        if (F4 && kind == 2u) *out = dequant_e2m1x8(raw[rr].x, sc[rr]);
+        else if (kind >= 2u) *out = dequant_e4m3x8(raw[rr].x, raw[rr].y, sc[rr]);
       }
     }
     __syncthreads();                       // step t landed; every wave is done with step t-1
