@@ -894,7 +894,7 @@ def main():
                                                                 peaks["bf16_gemm_TFLOPs"])
         except Exception as e:  # report, do not hide: the decode line still prints
             result["prefill"] = {"error": repr(e)}
-    if not args.no_wo_a and not args.eager:
+    if not args.no_wo_a:                  # event-timed, so it also runs in the eager counter passes
         try:
             result["output_lora"] = run_wo_a(torch, device)
         except Exception as e:
