@@ -120,13 +120,143 @@ struct MlaLds {
 // of ring_store_fp8); such a row lands where an fp8 compressed row does.
 constexpr int kCompBf16 = 0, kCompFp8 = 1, kCompFp4 = 2, kCompMask = 3, kWinFp8 = 4;
 
+template <int CF>
+struct CacheFmt {
+  static constexpr bool F8 = (CF & kCompMask) == kCompFp8, F4 = (CF & kCompMask) == kCompFp4;
+  static constexpr bool W8 = (CF & kWinFp8) != 0, PACKED = F8 || F4 || W8;
+  static constexpr int F4ROW = 512 / 2 + 512 / 16;   // packed fp4 row bytes (D = 512)
+  static constexpr int F4OFF = 2 * 512 - F4ROW;      // where it lands in the bf16 slot row
+  static constexpr int W8ROW = 512 + 512 / 32;       // MXFP8 ring row bytes
+};
+
+// Unified position u of batch row b -> what a copy needs: a 16-byte aligned bf16 row address
+// (tag 0), a packed compressed row (row << 2) | 1, an MXFP8 ring slot (slot << 2) | 2, or 0
+// (masked; the zero row is gathered).
+template <int D, int CF>
+__device__ __forceinline__ uint64_t row_entry(const KvSrc& S, int b, int u) {
+  using F = CacheFmt<CF>;
+  const int ci = u - S.wp - S.n_chunk;
+  if (F::W8 && u >= 0 && u < S.wp) return ((uint64_t)((S.ring_first + u) % S.window) << 2) | 2ull;
+  return ((F::F8 || F::F4) && u >= 0 && ci >= 0 && ci < S.n_comp)
+             ? (((uint64_t)ci << 2) | 1ull)
+             : reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, u, D));
+}
+
+// Batch row b's bases of the packed sources (0 where the format has none).
+struct PackedBase {
+  uint64_t comp8, ring8, scal8;
+  int rbs;   // scale row block (1 or 32) as a shift
+};
+template <int CF>
+__device__ __forceinline__ PackedBase packed_base(const KvSrc& S, int b) {
+  using F = CacheFmt<CF>;
+  PackedBase p;
+  p.comp8 = (F::F8 || F::F4) ? reinterpret_cast<uint64_t>(S.comp) + (uint64_t)b * (uint64_t)S.comp_bstride : 0ull;
+  p.ring8 = F::W8 ? reinterpret_cast<uint64_t>(S.ring) + (uint64_t)b * (uint64_t)S.ring_bstride : 0ull;
+  p.scal8 = F::F8 ? reinterpret_cast<uint64_t>(S.comp_scale) + (uint64_t)b * (uint64_t)S.comp_scale_bstride : 0ull;
+  p.rbs = S.comp_scale_rb == 32 ? 5 : 0;
+  return p;
+}
+
+// Layout of a staged row in LDS. Padded (mla_bf16_kernel): rows of 2D + 16 bytes, the bf16
+// channels in order, packed bytes from D on (fp8 and MXFP8 scales in the padding). Swizzled
+// (mla_roles_kernel): rows of 2D bytes, 16-byte chunk c of a bf16 row at chunk c ^ row_swz(r) (r:
+// the row's index in its step), packed bytes ending at 2D.
+template <int D, bool SWZ>
+struct RowLayout {
+  static constexpr int RS = SWZ ? 2 * D : 2 * D + 16;
+  static constexpr int P8 = SWZ ? D - 16 : D;   // fp8 / MXFP8 codes, then their 16 scale bytes
+};
+
+// Chunk permutation of the swizzled layout, within each 256-byte group: row r's chunks are XORed
+// with the 4 x 4 transpose of r mod 16. A K fragment read (rows 0..15 of a tile, the same chunk)
+// then touches 16 different chunks of a group, and a transposed V read (4 rows r, r + 1, r + 2,
+// r + 3 with r % 4 == 0, 64 contiguous bytes each, per 32 lanes) 4 different 64-byte quarters:
+// neither has bank conflicts with 32 or with 64 four-byte banks (the padded layout's transposed
+// reads conflict 2- to 4-way).
+__device__ __forceinline__ int row_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// One wave copies RPW rows into LDS rows dst + rr * RS (lane rr < RPW holds row rr's entry; in
+// the swizzled layout row rr is row r0 + rr of its step) and records each row's kind for the
+// masking and the dequantization: 0 masked, 1 bf16, 2 packed compressed (tag 1), 3 MXFP8 ring
+// (tag 2). Every row is whole copy instructions, the same count for every kind, so a step's copies
+// are counted by vmcnt alone.
+template <int D, int CF, int RPW, bool SWZ>
+__device__ __forceinline__ void gather_rows(uint64_t mp, uint8_t* kind, uint32_t dst, int lane, const PackedBase& pb,
+                                            int r0) {
+  using F = CacheFmt<CF>;
+  constexpr int RS = RowLayout<D, SWZ>::RS, P8 = RowLayout<D, SWZ>::P8;
+  static_assert(!SWZ || D == 512, "swizzled rows: 512 channels");
+  if (lane < RPW) kind[lane] = mp != 0ull ? (uint8_t)(1u + ((uint32_t)mp & 3u)) : 0;
+  const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    const uint64_t ent = lane_u64(lo, hi, rr);
+    const uint32_t tag = (uint32_t)ent & 3u;
+    if (F::F8 && tag == 1u) {
+      // lanes 0..31: the row's 512 fp8 bytes; lane 32: its 16 scale bytes
+      const uint64_t ci = ent >> 2;
+      const uint64_t src = lane < D / 16 ? pb.comp8 + ci * D + (uint64_t)lane * 16u
+                                         : pb.scal8 + (ci >> pb.rbs) * (D / 32);
+      if (lane <= D / 16) dma16_vaddr(src, dst + rr * RS + P8);
+    } else if (F::F4 && tag == 1u) {
+      // lanes 0..F4ROW/16-1: the row's codes and scales, one contiguous packed row
+      const uint64_t src = pb.comp8 + (ent >> 2) * F::F4ROW + (uint64_t)lane * 16u;
+      if (lane < F::F4ROW / 16) dma16_vaddr(src, dst + rr * RS + F::F4OFF);
+    } else if (F::W8 && tag == 2u) {
+      // lanes 0..32: the ring row's 512 codes and 16 scales, contiguous, to [P8, P8 + 528)
+      const uint64_t src = pb.ring8 + (ent >> 2) * F::W8ROW + (uint64_t)lane * 16u;
+      if (lane <= D / 16) dma16_vaddr(src, dst + rr * RS + P8);
+    } else if constexpr (SWZ) {
+      // lane l lands chunk l of the LDS row: it fetches chunk l ^ row_swz(r)
+      dma16_sgpr(ent ? ent : reinterpret_cast<uint64_t>(g_zero_row), (uint32_t)(lane ^ row_swz(r0 + rr)) * 16u,
+                 dst + rr * RS);
+    } else {
+      dma_row<D>(ent, dst + rr * RS, lane);
+    }
+  }
+}
+
+// A wave's own packed rows of a step have landed (sb: its first row, kind: their kinds):
+// dequantize them in place. All of its rows are read before any is written (a single wave
+// converts them), so the bf16 output may overlap the bytes it came from. Lane l converts channels
+// 8l..8l+7 (its chunk, at chunk l ^ row_swz(r0 + rr) in the swizzled layout): fp8 rows (kind 3,
+// or kind 2 of an fp8 compressed cache) hold their codes at [P8, P8 + D) and the ue8m0 scale of
+// the lane's block at P8 + D + l/4; fp4 rows (kind 2) hold code bytes 4l..4l+3 at F4OFF and the
+// e4m3 scale byte l/2 after the codes. The kinds come from one LDS read per 4 rows as
+// wave-uniform values, so the loads of all rows go out together with no branch between them (a
+// per-row conditional read serialized them: ~1 us per step).
+template <int D, int CF, int RPW, bool SWZ>
+__device__ __forceinline__ void dequant_rows(uint8_t* sb, const uint8_t* kind, int lane, int r0) {
+  using F = CacheFmt<CF>;
+  constexpr int RS = RowLayout<D, SWZ>::RS, P8 = RowLayout<D, SWZ>::P8;
+  const uint32_t* kw = reinterpret_cast<const uint32_t*>(kind);
+  uint32_t kinds[RPW / 4];
+#pragma unroll
+  for (int w4 = 0; w4 < RPW / 4; ++w4) kinds[w4] = (uint32_t)__builtin_amdgcn_readfirstlane((int)kw[w4]);
+  uint2 raw[RPW];
+  float sc[RPW];
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    const uint32_t k = (kinds[rr / 4] >> (8 * (rr % 4))) & 0xFFu;
+    const bool f4row = F::F4 && k == 2u;
+    const uint8_t* row = sb + rr * RS;
+    raw[rr] = *reinterpret_cast<const uint2*>(row + (f4row ? F::F4OFF + lane * 4 : P8 + lane * 8));
+    const uint32_t sbyte = row[f4row ? F::F4OFF + D / 2 + (lane >> 1) : P8 + D + (lane >> 2)];
+    sc[rr] = f4row ? __builtin_amdgcn_cvt_f32_fp8((int)sbyte, 0) : e8m0_to_float(sbyte);
+  }
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    const uint32_t k = (kinds[rr / 4] >> (8 * (rr % 4))) & 0xFFu;
+    bf16x8* out = reinterpret_cast<bf16x8*>(sb + rr * RS + (SWZ ? lane ^ row_swz(r0 + rr) : lane) * 16);
+    if (F::F4 && k == 2u) *out = dequant_e2m1x8(raw[rr].x, sc[rr]);
+    else if (k >= 2u) *out = dequant_e4m3x8(raw[rr].x, raw[rr].y, sc[rr]);
+  }
+}
+
 template <int D, int HT, int DS, int CF, bool PAIR>
 __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
-  constexpr bool F8 = (CF & kCompMask) == kCompFp8, F4 = (CF & kCompMask) == kCompFp4, W8 = (CF & kWinFp8) != 0;
-  constexpr bool PACKED = F8 || F4 || W8;
-  constexpr int F4ROW = D / 2 + D / 16;         // packed fp4 row bytes
-  constexpr int F4OFF = 2 * D - F4ROW;          // where it lands in the bf16 slot row
-  constexpr int W8ROW = D + D / 32;             // MXFP8 ring row bytes
+  constexpr bool W8 = CacheFmt<CF>::W8, PACKED = CacheFmt<CF>::PACKED;
   constexpr int NW = HT * DS, NT = 64 * NW;
   constexpr int ML = PAIR ? kPairList : kMaxList;
   constexpr int DSL = D / DS, KSS = DSL / 32, DTS = DSL / 16;
@@ -138,6 +268,7 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   constexpr int NL = RPW * IPR;                 // copies each wave issues per step
   using Lds = MlaLds<D, NW, ML, PAIR ? kLdsBudget / 2 : kLdsBudget>;
   constexpr int RS = Lds::RS, SLOT = Lds::SLOT, NS = Lds::NS;
+  static_assert(RS == RowLayout<D, false>::RS, "padded row layout");
   __shared__ __align__(16) uint8_t ring[NS * SLOT];
   __shared__ __align__(16) f32x4 xs[NW][2][64];
   __shared__ uint64_t rows[ML];                 // resolved row addresses, 0 = masked
@@ -164,56 +295,20 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   const int w0 = min(sp * ws, wc), nw = min(w0 + ws, wc) - w0;
   const int k0 = min(sp * ks, S.k), nk = min(k0 + ks, S.k) - k0;
   const int cnt = min(nw + nk, ML);             // planner: nw + nk <= ML
-  auto entry_row = [&](int e) {                  // split entry -> row address (0 = masked)
-    const int u = list_pos(S, b, a.m, qs, e < nw ? w0 + e : wc + k0 + (e - nw), wc);
-    const int ci = u - S.wp - S.n_chunk;
-    // packed rows are tagged and addressed at issue time: compressed (row << 2) | 1, MXFP8 ring
-    // (slot << 2) | 2; bf16 rows are 16-byte aligned addresses (tag 0), masked entries 0
-    if (W8 && u >= 0 && u < S.wp) return ((uint64_t)((S.ring_first + u) % S.window) << 2) | 2ull;
-    return ((F8 || F4) && u >= 0 && ci >= 0 && ci < S.n_comp)
-               ? (((uint64_t)ci << 2) | 1ull)
-               : reinterpret_cast<uint64_t>(row_ptr<bf16_t>(S, b, u, D));
+  auto entry_row = [&](int e) {                  // split entry -> copy entry (0 = masked)
+    return row_entry<D, CF>(S, b, list_pos(S, b, a.m, qs, e < nw ? w0 + e : wc + k0 + (e - nw), wc));
   };
   static_assert(!PACKED || D == 512, "packed cache rows: 512 channels (one copy instruction per row)");
 
   const int nsteps = (cnt + R - 1) / R;
   const uint32_t ring_base = lds_offset(ring);
-  const uint64_t comp8 =
-      (F8 || F4) ? reinterpret_cast<uint64_t>(S.comp) + (uint64_t)b * (uint64_t)S.comp_bstride : 0ull;
-  const uint64_t ring8 = W8 ? reinterpret_cast<uint64_t>(S.ring) + (uint64_t)b * (uint64_t)S.ring_bstride : 0ull;
-  const uint64_t scal8 = F8 ? reinterpret_cast<uint64_t>(S.comp_scale) + (uint64_t)b * (uint64_t)S.comp_scale_bstride : 0ull;
-  const int rbs = S.comp_scale_rb == 32 ? 5 : 0;   // scale row block (1 or 32) as a shift
+  const PackedBase pbase = packed_base<CF>(S, b);
   auto issue = [&](int t, bool direct) {
     const int slot = t % NS;
     const int mine = t * R + wave * RPW + (lane % RPW);
     const uint64_t mp = mine < cnt ? (direct ? entry_row(mine) : rows[mine]) : 0ull;
-    // the row's kind for the masking (nonzero = a row) and the dequantization: 0 masked, 1 bf16,
-    // 2 packed compressed (tag 1), 3 MXFP8 ring (tag 2)
-    if (lane < RPW) vrow[slot][wave * RPW + lane] = mp != 0ull ? (uint8_t)(1u + ((uint32_t)mp & 3u)) : 0;
-    const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
     const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_base + (uint32_t)(slot * SLOT + wave * RPW * RS));
-#pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      const uint64_t ent = lane_u64(lo, hi, rr);
-      const uint32_t tag = (uint32_t)ent & 3u;
-      if (F8 && tag == 1u) {
-        // lanes 0..31: the row's 512 fp8 bytes; lane 32: its 16 scale bytes
-        const uint64_t ci = ent >> 2;
-        const uint64_t src = lane < D / 16 ? comp8 + ci * D + (uint64_t)lane * 16u
-                                           : scal8 + (ci >> rbs) * (D / 32);
-        if (lane <= D / 16) dma16_vaddr(src, dst + rr * RS + D);
-      } else if (F4 && tag == 1u) {
-        // lanes 0..F4ROW/16-1: the row's codes and scales, one contiguous packed row
-        const uint64_t src = comp8 + (ent >> 2) * F4ROW + (uint64_t)lane * 16u;
-        if (lane < F4ROW / 16) dma16_vaddr(src, dst + rr * RS + F4OFF);
-      } else if (W8 && tag == 2u) {
-        // lanes 0..32: the ring row's 512 codes and 16 scales, contiguous, to [D, 2D + 16)
-        const uint64_t src = ring8 + (ent >> 2) * W8ROW + (uint64_t)lane * 16u;
-        if (lane <= D / 16) dma16_vaddr(src, dst + rr * RS + D);
-      } else {
-        dma_row<D>(ent, dst + rr * RS, lane);
-      }
-    }
+    gather_rows<D, CF, RPW, false>(mp, &vrow[slot][wave * RPW], dst, lane, pbase, 0);
   };
   const int h = hg * (HT * 16) + ht * 16 + l16;
   const bool hok = h < a.heads;
@@ -260,39 +355,8 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
 
   for (int t = 0; t < nsteps; ++t) {
     wait_steps<NL>(min(nsteps - 1 - t, NS - 2));
-    if constexpr (PACKED) {
-      // this wave's own packed rows of step t have landed: dequantize them in place. All of its
-      // rows are read before any is written (a single wave converts them), so the bf16 output
-      // may overlap the bytes it came from. Lane l converts channels 8l..8l+7: fp8 rows (kind 3,
-      // or kind 2 of an fp8 compressed cache) hold their codes at [D, 2D) and the ue8m0 scale of
-      // the lane's block at 2D + l/4; fp4 rows (kind 2) hold code bytes 4l..4l+3 at F4OFF and the
-      // e4m3 scale byte l/2 after the codes. The kinds come from one LDS read per 4 rows as
-      // wave-uniform values, so the loads of all rows go out together with no branch between
-      // them (a per-row conditional read serialized them: ~1 us per step).
-      uint8_t* sb = ring + (t % NS) * SLOT + wave * RPW * RS;
-      const uint32_t* kw = reinterpret_cast<const uint32_t*>(&vrow[t % NS][wave * RPW]);
-      uint32_t kinds[RPW / 4];
-#pragma unroll
-      for (int w4 = 0; w4 < RPW / 4; ++w4) kinds[w4] = (uint32_t)__builtin_amdgcn_readfirstlane((int)kw[w4]);
-      uint2 raw[RPW];
-      float sc[RPW];
-#pragma unroll
-      for (int rr = 0; rr < RPW; ++rr) {
-        const uint32_t kind = (kinds[rr / 4] >> (8 * (rr % 4))) & 0xFFu;
-        const bool f4row = F4 && kind == 2u;
-        const uint8_t* row = sb + rr * RS;
-        raw[rr] = *reinterpret_cast<const uint2*>(row + (f4row ? F4OFF + lane * 4 : D + lane * 8));
-        const uint32_t sbyte = row[f4row ? F4OFF + D / 2 + (lane >> 1) : 2 * D + (lane >> 2)];
-        sc[rr] = f4row ? __builtin_amdgcn_cvt_f32_fp8((int)sbyte, 0) : e8m0_to_float(sbyte);
-      }
-#pragma unroll
-      for (int rr = 0; rr < RPW; ++rr) {
-        const uint32_t kind = (kinds[rr / 4] >> (8 * (rr % 4))) & 0xFFu;
-        bf16x8* out = reinterpret_cast<bf16x8*>(sb + rr * RS + lane * 16);
-        if (F4 && kind == 2u) *out = dequant_e2m1x8(raw[rr].x, sc[rr]);
-        else if (kind >= 2u) *out = dequant_e4m3x8(raw[rr].x, raw[rr].y, sc[rr]);
-      }
-    }
+    if constexpr (PACKED)   // this wave's own packed rows of step t have landed
+      dequant_rows<D, CF, RPW, false>(ring + (t % NS) * SLOT + wave * RPW * RS, &vrow[t % NS][wave * RPW], lane, 0);
     __syncthreads();                       // step t landed; every wave is done with step t-1
     const int slot = t % NS;
     const uint8_t* buf = ring + slot * SLOT;
@@ -388,6 +452,226 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + h) * D;
 #pragma unroll
   for (int dt = 0; dt < DTS; ++dt) store_out4(a, D, qs, orow, dh * DSL + dt * 16 + 4 * g, acc[dt], l_run);
+}
+
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Sparse MLA for many queries with two wave roles (chunked prefill: rows of 512 channels, 64
+// heads per workgroup, the whole list in one workgroup). In mla_bf16_kernel every wave runs
+// the same serial step (QK, score exchange, softmax, PV) in lockstep with the other wave on its
+// SIMD, so the MFMA pipe idles through the exchange and the softmax. Here each SIMD holds one
+// wave of each role:
+//   score waves 0-3, 16 heads each over all 512 channels: S^T = K Q^T of step t (Q^T in VGPRs),
+//     masking, the running max and denominator with lazy rescaling, P rounded to bf16 into LDS
+//     as P^T [head][row], and the step's rescale factor per head (1 when the max did not move);
+//   value waves 4-7, 32 heads x 256 channels each (v_mfma_f32_32x32x16_bf16): O^T = alpha O^T +
+//     V^T P^T for step t - 1, with V^T through the LDS transpose read.
+// One barrier per step: past it, step t's rows are in LDS for the score waves and step t-1's P
+// for the value waves, and the ring slot of step t-2 takes the copies of step t+2. A gathered row
+// is read from LDS four times for QK and twice for PV (mla_bf16_kernel: four and four, plus
+// the partial-score exchange), 204 KB per 32-row step instead of 288 KB.
+// Lane layouts of the 32x32x16 MFMA: lane l supplies A[l % 32][k] and B[k][l % 32] for
+// k = 8 (l / 32) .. + 7, and receives D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32] in accumulator
+// register i.
+// Copies, the in-place dequantization of packed rows (CF), masking, sink, lazy rescaling,
+// rounding and the inverse rope are mla_bf16_kernel's; only the order of the fp32 additions in S
+// and O differs.
+constexpr int kRolesSlots = 4;          // ring: the score step, the value step, two in flight
+
+template <int CF>
+__global__ __launch_bounds__(512, 1) void mla_roles_kernel(MlaArgs a) {
+  constexpr int D = 512, R = kStepRows, NT = 512, NS = kRolesSlots;
+  constexpr int RS = RowLayout<D, true>::RS, SLOT = R * RS;
+  constexpr int VR = R / 4;                       // rows each value wave copies per step
+  constexpr int KSS = D / 32, DH = D / 2;
+  __shared__ __align__(16) uint8_t ring[NS * SLOT];
+  __shared__ uint64_t rows[kMaxList];             // resolved row entries, 0 = masked
+  __shared__ __align__(16) uint8_t pbuf[2][64][R * 2];   // P^T of a step: [head][row] bf16
+  __shared__ float abuf[2][64];                   // the step's rescale factor per head
+  __shared__ float lbuf[64];                      // denominators
+  __shared__ __align__(4) uint8_t vrow[NS][R];
+  static_assert(sizeof(ring) + sizeof(rows) + sizeof(pbuf) + sizeof(abuf) + sizeof(lbuf) + sizeof(vrow) <=
+                    kLdsBudget,
+                "LDS budget");
+
+  const KvSrc& S = a.src;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);   // (unit, head group), head group fastest
+  const int hg = tile % a.hgroups, unit = tile / a.hgroups;
+  const int b = unit / a.m, qs = unit - (unit / a.m) * a.m;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (a.ring_w && hg == 0 && wave == 0) {
+    if constexpr (CacheFmt<CF>::W8) ring_store_fp8<D>(a, b, lane);
+    else ring_store<bf16_t>(a, b, lane, 64);
+  }
+  const int wc = window_count(S, qs);
+  const int cnt = min(wc + S.k, kMaxList);      // planner: the list fits
+  const int nsteps = (cnt + R - 1) / R;
+  for (int e = tid; e < cnt; e += NT) rows[e] = row_entry<D, CF>(S, b, list_pos(S, b, a.m, qs, e, wc));
+
+  if (wave < 4) {
+    // ---- score wave: heads ht * 16 + l16 of the group, all 512 channels
+    const int ht = wave;
+    const int hl = ht * 16 + l16;
+    const int h = hg * 64 + hl;
+    bf16x8 qb[KSS];
+    const bf16_t* qrow = reinterpret_cast<const bf16_t*>(a.q) + ((int64_t)unit * a.heads + h) * D;
+#pragma unroll
+    for (int ks = 0; ks < KSS; ++ks) qb[ks] = ld_bf16x8(qrow + ks * 32 + 8 * g);
+    if (a.q_rd > 0) {
+#pragma unroll
+      for (int ks = 0; ks < KSS; ++ks) {
+        const int c0 = ks * 32 + 8 * g;
+        if (c0 + 8 > D - a.q_rd) qb[ks] = rope_q8(a, D, qs, c0, qb[ks]);
+      }
+    }
+    const float sl2 = a.scale * kLog2e;
+    // m_run: the exponent reference shared by the head's 4 lane groups; l_run: this lane's share
+    // of the denominator (its own rows), the sink seeded in lane group 0
+    const float s2 = a.sink[h] * kLog2e;
+    float m_run = fmaxf(s2, kNegFloor);
+    float l_run = g == 0 ? exp2f(s2 - m_run) : 0.0f;
+    // K fragment of k-step ks, row tile rt: row rt * 16 + l16, logical chunk 4 ks + g, stored at
+    // chunk 4 ks ^ (g ^ row_swz(l16)): 256 (ks / 4) bytes on from the row plus a per-lane offset
+    // for each ks % 4
+    const int xk = g ^ row_swz(l16);
+    const int ko[4] = {16 * xk, 16 * (4 ^ xk), 16 * (8 ^ xk), 16 * (12 ^ xk)};
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);    // q, sink and list loads done
+    __syncthreads();                              // rows[] complete
+    for (int t = 0; t <= nsteps; ++t) {
+      __syncthreads();                            // step t landed; step t-1's P was taken
+      if (t == nsteps) break;
+      const int slot = t % NS;
+      const uint8_t* buf = ring + slot * SLOT;
+      f32x4 sq[2][2];
+      sq[0][0] = sq[0][1] = sq[1][0] = sq[1][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KSS; ++ks)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          sq[rt][ks & 1] = mfma16x16x32(ld_bf16x8(buf + (rt * 16 + l16) * RS + 256 * (ks >> 2) + ko[ks & 3]),
+                                        qb[ks], sq[rt][ks & 1]);
+      const f32x4 sacc[2] = {sq[0][0] + sq[0][1], sq[1][0] + sq[1][1]};
+      const uint32_t v0 = *reinterpret_cast<const uint32_t*>(&vrow[slot][4 * g]);
+      const uint32_t v1 = *reinterpret_cast<const uint32_t*>(&vrow[slot][16 + 4 * g]);
+      float p[8];
+      float tmax = kNegFloor;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool ok = (((rt ? v1 : v0) >> (8 * i)) & 0xFFu) != 0u;
+          const float l2 = sacc[rt][i] * sl2;
+          p[rt * 4 + i] = ok ? l2 : -INFINITY;
+          if (ok) tmax = fmaxf(tmax, l2);
+        }
+      float alpha = 1.0f;
+      if (__any(tmax > m_run + kRescale)) {
+        float gmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        gmax = fmaxf(gmax, __shfl_xor(gmax, 32, 64));
+        const bool grow = gmax > m_run + kRescale;
+        alpha = grow ? fast_exp2(m_run - gmax) : 1.0f;
+        l_run *= alpha;
+        m_run = grow ? gmax : m_run;
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p[e] = fast_exp2(p[e] - m_run);
+        l_run += p[e];
+      }
+      // rows 16 rt + 4 g .. + 3 of head hl
+      uint8_t* pt = &pbuf[t & 1][hl][0];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+        *reinterpret_cast<uint2*>(pt + (16 * rt + 4 * g) * 2) =
+            make_uint2(pack2_bf16(p[4 * rt], p[4 * rt + 1]), pack2_bf16(p[4 * rt + 2], p[4 * rt + 3]));
+      if (g == 0) abuf[t & 1][hl] = alpha;
+    }
+    l_run += __shfl_xor(l_run, 16, 64);           // denominator: sum of the 4 lane groups
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (g == 0) lbuf[hl] = l_run;
+    __syncthreads();                              // denominators to the value waves
+    return;
+  }
+
+  // ---- value wave: heads hp * 32 + l32 of the group, channels cb0 .. cb0 + 255; it also copies
+  // rows 8 vw .. 8 vw + 7 of every step (the score waves' path is the longer one)
+  const int vw = wave - 4, hp = vw & 1, cb0 = (vw >> 1) * DH;
+  const int l32 = lane & 31, hi = lane >> 5, q4 = lane >> 4, r16 = lane & 15;
+  const int hl = hp * 32 + l32;
+  const uint32_t ring_base = lds_offset(ring);
+  const PackedBase pbase = packed_base<CF>(S, b);
+  auto entry_of = [&](int t) -> uint64_t {
+    const int mine = t * R + vw * VR + (lane % VR);
+    return mine < cnt ? rows[mine] : 0ull;
+  };
+  auto issue = [&](int t, uint64_t mp) {
+    const int slot = t % NS;
+    const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_base + (uint32_t)(slot * SLOT + vw * VR * RS));
+    gather_rows<D, CF, VR, true>(mp, &vrow[slot][vw * VR], dst, lane, pbase, vw * VR);
+  };
+  // V^T fragments: the 16-lane group q4 reads channels 16 (q4 & 1) + (0..15) of a 32-channel tile
+  // ct, rows 16 kk + vrb (lo) and 16 kk + vrb + 4 (hi), 8 bytes each. Logical chunk 4 ct + j of
+  // such a row (j = 2 (q4 & 1) + (r16 & 3) / 2, counted from channel cb0) sits at chunk
+  // 4 ct ^ (j ^ row_swz(row)): 256 (ct / 4) bytes on plus a per-lane offset for each ct % 4.
+  const int vrb = 8 * (q4 >> 1) + (r16 >> 2);
+  const int jv = 2 * (q4 & 1) + ((r16 & 3) >> 1);
+  const int xl = jv ^ row_swz(vrb), xh = jv ^ row_swz(vrb + 4), e8 = 8 * (r16 & 1);
+  const int vlo[4] = {16 * xl + e8, 16 * (4 ^ xl) + e8, 16 * (8 ^ xl) + e8, 16 * (12 ^ xl) + e8};
+  const int vhi[4] = {16 * xh + e8, 16 * (4 ^ xh) + e8, 16 * (8 ^ xh) + e8, 16 * (12 ^ xh) + e8};
+  f32x16 acc[DH / 32];
+#pragma unroll
+  for (int ct = 0; ct < DH / 32; ++ct)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[ct][i] = 0.0f;
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();                                // rows[] complete
+  for (int t = 0; t < NS - 2 && t < nsteps; ++t) issue(t, entry_of(t));
+  for (int t = 0; t <= nsteps; ++t) {
+    const uint64_t mp = t + NS - 2 < nsteps ? entry_of(t + NS - 2) : 0ull;
+    if (t < nsteps) {
+      wait_steps<VR>(min(NS - 3, nsteps - 1 - t));   // this wave's rows of step t landed
+      if constexpr (CacheFmt<CF>::PACKED)
+        dequant_rows<D, CF, VR, true>(ring + (t % NS) * SLOT + vw * VR * RS, &vrow[t % NS][vw * VR], lane, vw * VR);
+    }
+    __syncthreads();                              // step t-1's P and rescale factors are in LDS
+    if (t + NS - 2 < nsteps) issue(t + NS - 2, mp);   // into step t-2's slot
+    if (t == 0) continue;
+    const int s = t - 1;
+    const float alpha = abuf[s & 1][hl];
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int ct = 0; ct < DH / 32; ++ct) acc[ct] *= alpha;
+    }
+    // P^T as the B operand of two 16-row k-steps: rows 16 kk + 8 hi .. + 7 of head hl
+    const uint8_t* pt = &pbuf[s & 1][hl][0];
+    const bf16x8 pb0 = ld_bf16x8(pt + (8 * hi) * 2), pb1 = ld_bf16x8(pt + (16 + 8 * hi) * 2);
+    const uint8_t* buf = ring + (s % NS) * SLOT + 2 * cb0;
+#pragma unroll
+    for (int ct = 0; ct < DH / 32; ++ct) {
+      const uint8_t* col = buf + 256 * (ct >> 2);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const i16x4 lo4 = lds_read_tr16(col + (16 * kk + vrb) * RS + vlo[ct & 3]);
+        const i16x4 hi4 = lds_read_tr16(col + (16 * kk + vrb + 4) * RS + vhi[ct & 3]);
+        acc[ct] = mfma32x32x16(join_bf16x8(lo4, hi4), kk ? pb1 : pb0, acc[ct]);
+      }
+    }
+  }
+  __syncthreads();                                // denominators written
+  const float den = lbuf[hl];
+  bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + hg * 64 + hl) * D;
+  // accumulator register i of tile ct: channel cb0 + 32 ct + 8 (i / 4) + 4 hi + i % 4
+#pragma unroll
+  for (int ct = 0; ct < DH / 32; ++ct)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      store_out4(a, D, qs, orow, cb0 + 32 * ct + 8 * j + 4 * hi,
+                 f32x4{acc[ct][4 * j], acc[ct][4 * j + 1], acc[ct][4 * j + 2], acc[ct][4 * j + 3]}, den);
 }
 
 // Merges split partials of one query: one wave per head, 4 heads per workgroup; the workgroups
@@ -684,7 +968,9 @@ static void launch_bf16_d(const MlaArgs& a, const MlaPlan& p, int64_t units, hip
       return;
     }
   }
-  if (p.wide)
+  if (D == 512 && p.wide && a.heads % 64 == 0)
+    hipLaunchKernelGGL(mla_roles_kernel<CF>, dim3(wgs), dim3(512), 0, stream, a);
+  else if (p.wide)
     hipLaunchKernelGGL((mla_bf16_kernel<D, 4, 2, CF, false>), dim3(wgs), dim3(512), 0, stream, a);
   else
     hipLaunchKernelGGL((mla_bf16_kernel<D, 2, 2, CF, false>), dim3(wgs), dim3(256), 0, stream, a);
