@@ -168,13 +168,15 @@ struct RowLayout {
   static constexpr int P8 = SWZ ? D - 16 : D;   // fp8 / MXFP8 codes, then their 16 scale bytes
 };
 
-// Chunk permutation of the swizzled layout, within each 256-byte group: row r's chunks are XORed
-// with the 4 x 4 transpose of r mod 16. A K fragment read (rows 0..15 of a tile, the same chunk)
-// then touches 16 different chunks of a group, and a transposed V read (4 rows r, r + 1, r + 2,
-// r + 3 with r % 4 == 0, 64 contiguous bytes each, per 32 lanes) 4 different 64-byte quarters:
-// neither has bank conflicts with 32 or with 64 four-byte banks (the padded layout's transposed
-// reads conflict 2- to 4-way).
-__device__ __forceinline__ int row_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+// Chunk permutation of the swizzled layout, within each 256-byte group: row r's chunk c sits at
+// c ^ row_swz(r). Bank-conflict counters over several layouts (measured on the two-role kernel):
+// the transposed V reads (8 bytes per lane, rows r..r+3 and 64 bytes of each per 32 lanes) are
+// conflict-free when row_swz / 4 takes 4 values over such rows, as here; the padded 1,040-byte rows
+// and a plain XOR with r % 8 left them 2-way. The K fragment reads (16 bytes per lane, 16 rows at
+// one chunk) counted 4 conflict cycles per instruction under every row-major layout tried, this
+// one included; only lanes reading one contiguous 1 KB in lane order avoided that, which the
+// transposed reads then pay for. Padding the P rows to 80 bytes removed their conflicts.
+__device__ __forceinline__ int row_swz(int r) { return ((r & 3) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
 
 // One wave copies RPW rows into LDS rows dst + rr * RS (lane rr < RPW holds row rr's entry; in
 // the swizzled layout row rr is row r0 + rr of its step) and records each row's kind for the
@@ -490,7 +492,8 @@ __global__ __launch_bounds__(512, 1) void mla_roles_kernel(MlaArgs a) {
   constexpr int KSS = D / 32, DH = D / 2;
   __shared__ __align__(16) uint8_t ring[NS * SLOT];
   __shared__ uint64_t rows[kMaxList];             // resolved row entries, 0 = masked
-  __shared__ __align__(16) uint8_t pbuf[2][64][R * 2];   // P^T of a step: [head][row] bf16
+  __shared__ __align__(16) uint8_t pbuf[2][64][R * 2 + 16];   // P^T: [head][row] bf16, rows padded
+                                                  // to 80 bytes against bank conflicts
   __shared__ float abuf[2][64];                   // the step's rescale factor per head
   __shared__ float lbuf[64];                      // denominators
   __shared__ __align__(4) uint8_t vrow[NS][R];
