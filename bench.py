@@ -445,9 +445,14 @@ def run_wo_a(torch, device):
         o = torch.randn(rows, G * d, generator=g, device=device).to(bf)
         y = torch.empty(rows, G * R, dtype=bf, device=device)
         reps = 50 if rows <= 64 else 10
-        us = timed(lambda: _abi.wo_a_grouped(o, w, G, out=y), reps)
         ob = o.view(rows, G, d).transpose(0, 1).contiguous()
-        us_bmm = timed(lambda: torch.bmm(ob, wT), reps)
+        ours = lambda: _abi.wo_a_grouped(o, w, G, out=y)   # noqa: E731
+        lib = lambda: torch.bmm(ob, wT)                      # noqa: E731
+        # the engine clock ramps up under the first heavy launches: warm both, then time each
+        # twice, alternating, and keep the faster pass of each
+        timed(ours, reps), timed(lib, reps)
+        us, us_bmm = timed(ours, reps), timed(lib, reps)
+        us, us_bmm = min(us, timed(ours, reps)), min(us_bmm, timed(lib, reps))
         nbytes = (G * R * d + rows * G * d + rows * G * R) * 2
         flops = 2.0 * rows * G * R * d
         line = {"us": us, "GBps": nbytes / us / 1e3, "hbm_frac": nbytes / us / 1e3 / HBM_PEAK_GBS,

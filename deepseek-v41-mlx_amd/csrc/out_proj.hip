@@ -17,10 +17,11 @@
 //     (each a quarter of the contraction, loads double-buffered in registers) and their partial
 //     sums meet in LDS in a fixed order. groups * r / 32 workgroups (256 for 8 x 1024), the
 //     group index fastest so that one group's workgroups share an XCD and its L2 copy of o.
-//   many rows (prefill): 128 x 128 output tiles (weight rows x query rows) over 64-channel
+//   many rows (prefill): 256 x 256 output tiles (weight rows x query rows) over 64-channel
 //     steps, both operand tiles copied global -> LDS (global_load_lds_dwordx4, double-buffered)
-//     in an XOR-swizzled layout that the MFMA fragment reads take without bank conflicts; four
-//     waves of 64 x 64 each.
+//     in an XOR-swizzled layout that the MFMA fragment reads take without bank conflicts; eight
+//     waves of 128 x 64 each, two per SIMD (128 x 128 tiles of four 64 x 64 waves when r is not
+//     a multiple of 256).
 #include "mfma.h"
 
 namespace dsv41 {
@@ -151,6 +152,7 @@ __global__ __launch_bounds__(256) void wo_a_rows_kernel(WoaArgs a) {
 // ------------------------------------------------------------------ many rows
 
 constexpr int kTileR = 128;   // weight rows of the smallest output tile (r is a multiple of it)
+constexpr int kWideR = 256;   // weight rows of the large tile
 
 // 16-byte chunk c of tile row `row` (rows of BK bf16: BK / 8 chunks) sits at slot c ^ swz(row).
 // A fragment read takes one chunk of 16 consecutive rows; with these slots no two of those lanes
@@ -162,20 +164,21 @@ __device__ __forceinline__ int tile_swz(int row) {
   else return ((row >> 1) & 3) ^ ((row >> 3) & 1);
 }
 
-// Output tile of 32 WR weight rows x 32 WM query rows: a 2 x 2 grid of waves, each 16 WR x 16 WM
-// (WR x WM MFMA tiles). BK channels per step; NS steps of both operand tiles in LDS at once
-// (NS - 1 in flight while one is multiplied).
-template <int WR, int WM, int BK, int NS>
+// Output tile of 16 WR GR weight rows x 16 WM GM query rows: a GR x GM grid of waves, each
+// 16 WR x 16 WM (WR x WM MFMA tiles). BK channels per step; NS steps of both operand tiles in LDS
+// at once (NS - 1 in flight while one is multiplied).
+template <int WR, int WM, int GR, int GM, int BK, int NS>
 struct TileCfg {
-  static constexpr int TR = 32 * WR, TM = 32 * WM;
+  static constexpr int NWV = GR * GM, NT = 64 * NWV;
+  static constexpr int TR = 16 * WR * GR, TM = 16 * WM * GM;
   static constexpr int RB = BK * 2;                 // bytes per tile row
   static constexpr int CPR = BK / 8;                // 16-byte chunks per row
   static constexpr int RPI = 1024 / RB;             // rows per copy instruction
-  static constexpr int NW = TR * RB / 4096, NO = TM * RB / 4096;   // copies per wave per step
+  static constexpr int NW = TR * RB / (1024 * NWV), NO = TM * RB / (1024 * NWV);   // copies per wave per step
   static constexpr int STAGE = (TR + TM) * RB;
   static constexpr int LDS = NS * STAGE;
   static_assert(BK == 32 || BK == 64, "32- or 64-channel steps");
-  static_assert(NW * 4096 == TR * RB && NO * 4096 == TM * RB, "whole copy instructions per wave");
+  static_assert(NW * 1024 * NWV == TR * RB && NO * 1024 * NWV == TM * RB, "whole copy instructions per wave");
 };
 
 template <int N>
@@ -200,10 +203,10 @@ __device__ __forceinline__ void wait_copies(int pending) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <int WR, int WM, int BK, int NS, typename TO>
-__global__ __launch_bounds__(256, (TileCfg<WR, WM, BK, NS>::LDS <= 80 * 1024) ? 2 : 1) void wo_a_tiles_kernel(
+template <int WR, int WM, int GR, int GM, int BK, int NS, typename TO>
+__global__ __launch_bounds__(64 * GR * GM, (TileCfg<WR, WM, GR, GM, BK, NS>::LDS <= 80 * 1024) ? 2 : 1) void wo_a_tiles_kernel(
     WoaArgs a) {
-  using C = TileCfg<WR, WM, BK, NS>;
+  using C = TileCfg<WR, WM, GR, GM, BK, NS>;
   __shared__ __align__(16) uint8_t lds[C::LDS];   // NS x [weight tile][query tile]
   const int mtiles = (a.rows + C::TM - 1) / C::TM, rtiles = a.r / C::TR;
   // consecutive tiles on one XCD, the weight tile fastest: the rtiles workgroups that read one
@@ -212,21 +215,21 @@ __global__ __launch_bounds__(256, (TileCfg<WR, WM, BK, NS>::LDS <= 80 * 1024) ? 
   const int tile = total % 8 ? (int)blockIdx.x : ((int)blockIdx.x % 8) * (total / 8) + (int)blockIdx.x / 8;
   const int rt = tile % rtiles, mt = (tile / rtiles) % mtiles, grp = tile / (rtiles * mtiles);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
-  const int wr = (wave & 1) * 16 * WR, wm = (wave >> 1) * 16 * WM;   // this wave's block
+  const int wr = (wave % GR) * 16 * WR, wm = (wave / GR) * 16 * WM;   // this wave's block
 
-  // copy sources: wave w fills rows [w TR/4, (w+1) TR/4) of the weight tile and [w TM/4, ..) of
-  // the query tile, RPI rows per instruction; lane l writes slot l % CPR of row l / CPR of its
+  // copy sources: wave w fills rows [w TR/NWV, (w+1) TR/NWV) of the weight tile and [w TM/NWV, ..)
+  // of the query tile, RPI rows per instruction; lane l writes slot l % CPR of row l / CPR of its
   // instruction's rows, i.e. chunk slot ^ swz(row) of that row
   uint64_t wsrc[C::NW], osrc[C::NO];
 #pragma unroll
   for (int j = 0; j < C::NW; ++j) {
-    const int row = wave * (C::TR / 4) + j * C::RPI + lane / C::CPR;
+    const int row = wave * (C::TR / C::NWV) + j * C::RPI + lane / C::CPR;
     const int chunk = (lane % C::CPR) ^ tile_swz<BK>(row);
     wsrc[j] = reinterpret_cast<uint64_t>(a.w + ((int64_t)grp * a.r + rt * C::TR + row) * a.d + 8 * chunk);
   }
 #pragma unroll
   for (int j = 0; j < C::NO; ++j) {
-    const int row = wave * (C::TM / 4) + j * C::RPI + lane / C::CPR;
+    const int row = wave * (C::TM / C::NWV) + j * C::RPI + lane / C::CPR;
     const int chunk = (lane % C::CPR) ^ tile_swz<BK>(row);
     const int64_t orow = min(mt * C::TM + row, a.rows - 1);   // rows past the end: not stored
     osrc[j] = reinterpret_cast<uint64_t>(a.o + orow * a.groups * a.d + (int64_t)grp * a.d + 8 * chunk);
@@ -234,9 +237,9 @@ __global__ __launch_bounds__(256, (TileCfg<WR, WM, BK, NS>::LDS <= 80 * 1024) ? 
   const uint32_t lds0 = lds_offset(lds);
   auto issue = [&](int buf, int k) {
     const uint32_t wdst = (uint32_t)__builtin_amdgcn_readfirstlane(
-        (int)(lds0 + (uint32_t)(buf * C::STAGE) + (uint32_t)(wave * (C::TR / 4) * C::RB)));   // wave-uniform: M0
+        (int)(lds0 + (uint32_t)(buf * C::STAGE) + (uint32_t)(wave * (C::TR / C::NWV) * C::RB)));   // wave-uniform: M0
     const uint32_t odst = (uint32_t)__builtin_amdgcn_readfirstlane(
-        (int)(lds0 + (uint32_t)(buf * C::STAGE + C::TR * C::RB) + (uint32_t)(wave * (C::TM / 4) * C::RB)));
+        (int)(lds0 + (uint32_t)(buf * C::STAGE + C::TR * C::RB) + (uint32_t)(wave * (C::TM / C::NWV) * C::RB)));
     const uint64_t kb = (uint64_t)k * 2;
 #pragma unroll
     for (int j = 0; j < C::NW; ++j) dma16_vaddr(wsrc[j] + kb, wdst + j * 1024);
@@ -291,11 +294,11 @@ __global__ __launch_bounds__(256, (TileCfg<WR, WM, BK, NS>::LDS <= 80 * 1024) ? 
   }
 }
 
-template <int WR, int WM, int BK, int NS, typename TO>
+template <int WR, int WM, int GR, int GM, int BK, int NS, typename TO>
 static void launch_tiles(const WoaArgs& a, hipStream_t stream) {
-  using C = TileCfg<WR, WM, BK, NS>;
+  using C = TileCfg<WR, WM, GR, GM, BK, NS>;
   const int64_t tiles = (int64_t)a.groups * (a.r / C::TR) * ((a.rows + C::TM - 1) / C::TM);
-  hipLaunchKernelGGL((wo_a_tiles_kernel<WR, WM, BK, NS, TO>), dim3((unsigned)tiles), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((wo_a_tiles_kernel<WR, WM, GR, GM, BK, NS, TO>), dim3((unsigned)tiles), dim3(C::NT), 0, stream, a);
 }
 
 template <typename TO>
@@ -314,7 +317,8 @@ static void launch_wo_a(const WoaArgs& a, hipStream_t stream) {
     }
     return;
   }
-  launch_tiles<4, 4, 64, 2, TO>(a, stream);
+  if (a.r % kWideR == 0) launch_tiles<8, 4, 2, 4, 64, 2, TO>(a, stream);
+  else launch_tiles<4, 4, 2, 2, 64, 2, TO>(a, stream);
 }
 
 }  // namespace dsv41

@@ -1192,8 +1192,10 @@ def test_indexer_topk_mxq_fp8_equals_two_calls(gpu, b, n, h, nb, topk, start, rb
     (64, 8, 4096, 1024, "bf16"),
     (100, 2, 512, 128, "bf16"),       # the 8-tile row kernel, a partial tile
     (128, 8, 4096, 1024, "bf16"),
-    (129, 8, 4096, 1024, "bf16"),     # the tiled kernel, one row in the second row tile
+    (129, 8, 4096, 1024, "bf16"),     # the tiled kernel, a partial 256-row query tile
+    (257, 8, 4096, 1024, "bf16"),     # one row in the second 256-row query tile
     (700, 4, 1024, 256, "bf16"),
+    (300, 2, 512, 384, "bf16"),       # r not a multiple of 256: the 128 x 128 tiles
     (2048, 8, 4096, 1024, "bf16"),    # a prefill chunk
     (9, 2, 128, 16, "bf16"),          # a test configuration's shape: the plain kernel
     (9, 2, 128, 16, "f32"),
