@@ -580,6 +580,8 @@ def _concat_reference(win, chunk, comp, n_comp, start, window):
     ("bf16", 2, 1, 64, 512, 128, 5, 0, 0),        # window only, ring still filling
     ("bf16", 1, 600, 64, 512, 16, 200, 150, 64),  # >= 512 queries: the 64-head two-role prefill kernel
     ("bf16", 2, 300, 96, 512, 128, 1000, 300, 128),   # 96 heads: its second workgroup has one idle tile
+    ("bf16", 2, 300, 64, 512, 128, 1000, 300, 128),   # two batch rows through the two-role kernel
+    ("bf16", 1, 520, 128, 512, 128, 3000, 700, 96),   # 128 heads: two head groups per query
 ])
 def test_sparse_mla_in_place_sources(gpu, dt, b, n, h, d, window, start, n_comp, k):
     from dsv41 import _abi
