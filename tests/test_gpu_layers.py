@@ -210,6 +210,53 @@ def test_c2_decode_step(gpu):
     assert rel_max_diff(to_np(out), want_o) < 2e-2
 
 
+def test_bs32_ctx64k_decode_step_sampled_rows(gpu):
+    """The bench's decode workload at full size (batch 32, 65,536 tokens -> 16,384 compressed
+    entries, top-512, window 128), through the fused step the bench times: sampled batch rows
+    against the oracle -- scores (two-call form) within 1e-5 of max |S|, the fused selection
+    bit-exact to the oracle's top-k of the GPU scores, attention within 2e-2."""
+    from dsv41.indexer import weight_scale
+    from dsv41.layers import precompute_freqs_cis
+    from dsv41.step import SparseDecodeStep
+    b, nb, start, K = 32, 16384, 65536, 512
+    H, D, Hi, Di, W, rd, r = 64, 512, 64, 128, 128, 64, 4
+    g = torch.Generator(gpu).manual_seed(SEED_BASE + 64)
+    rn = lambda *s: torch.randn(*s, generator=g, device=gpu)   # noqa: E731
+    sc = 576 ** -0.5
+    # index queries and keys on the e2m1 grid times 1/4, as the fp4 index cache holds them
+    grid = torch.tensor([0, .5, 1, 1.5, 2, 3, 4, 6, 0, -.5, -1, -1.5, -2, -3, -4, -6], device=gpu) * 0.25
+    fp4 = lambda *s: grid[torch.randint(0, 16, s, generator=g, device=gpu)].bfloat16()   # noqa: E731
+    q, win, chunk = (rn(b, 1, H, D) * sc).bfloat16(), (rn(b, W, D) * sc).bfloat16(), (rn(b, 1, D) * sc).bfloat16()
+    comp = (rn(b, nb, D) * sc).bfloat16()
+    iq, ik = fp4(b, 1, Hi, Di), fp4(b, nb, Di)
+    w, sink = rn(b, 1, Hi).bfloat16(), rn(H)
+    cos, sin = precompute_freqs_cis(rd, start + 1, 65536, 160000.0, 16.0, 32, 1, device=gpu)
+    ws = weight_scale(Hi, Di, torch.bfloat16)
+    fused = SparseDecodeStep(b, H, D, rd, Hi, Di, nb, K, W, start, r, torch.bfloat16, gpu)
+    two = SparseDecodeStep(b, H, D, rd, Hi, Di, nb, K, W, start, r, torch.bfloat16, gpu, fused=False)
+    assert fused.fused
+    out, idx = fused(q, iq, w, ws, ik, comp, win, chunk, sink, cos, sin)
+    two(q, iq, w, ws, ik, comp, win, chunk, sink, cos, sin)
+    torch.cuda.synchronize()
+    rows = [0, 13, 31]
+    f = lambda x: x[rows].float().cpu().numpy()   # noqa: E731
+    wq = R.cast(f(w) * np.float32(ws), "bf16")
+    want_s = R.indexer_scores(f(iq), f(ik), wq, start, r)
+    got_s = to_np(two.scores)[rows]
+    assert np.abs(got_s - want_s).max() <= 1e-5 * np.abs(want_s).max()
+    wp = min(start, W)
+    want_i = R.topk_indices(got_s, K, R.query_lens(start, 1, r), wp + 1)
+    assert np.array_equal(idx.cpu().numpy()[rows], want_i)
+    slots = (start - wp + np.arange(wp)) % W
+    kv_all = np.concatenate([f(win)[:, slots], f(chunk), f(comp)], axis=1)
+    widx = np.broadcast_to(R.window_idx_matrix(wp, 1, W)[None], (len(rows), 1, min(W, wp + 1)))
+    rc, rs = R.precompute_freqs_cis(rd, start + 1, 65536, 160000.0, 16.0, 32, 1)
+    qr = R.rope_tail(f(q), rd, rc[[start]], rs[[start]], dtype="bf16")
+    o = R.sparse_attn(qr, kv_all, sink.cpu().numpy(), np.concatenate([widx, want_i], -1), D ** -0.5, dtype="bf16")
+    want_o = R.rope_tail(o, rd, rc[[start]], rs[[start]], inverse=True, dtype="bf16")
+    assert rel_max_diff(to_np(out)[rows], want_o) < 2e-2
+
+
 @pytest.mark.parametrize("b,nb,K,start", [
     (32, 16384, 512, 65535),     # bs32, 64K context: 8 row ranges of 2048 per query
     (64, 16384, 512, 65535),     # B=64: 4 ranges of 4096
