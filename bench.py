@@ -231,7 +231,7 @@ def run_decode(args, torch, device):
             torch.cuda.synchronize()
             log(f"[bench] calibration copy of {args.calib_mb} MB x4 done")
         kern = {k: float("nan") for k in ("indexer_topk", "indexer_score", "topk_select", "sparse_mla")}
-        return s, ms, kern, sets, cos, sin, ws, []
+        return s, ms, kern, sets, cos, sin, ws, [], []
     # exactly `warmup` untimed steps, then exactly `steps` timed steps, each graph cycling through
     # the input sets in order
     if args.warmup > 0:
@@ -241,7 +241,11 @@ def run_decode(args, torch, device):
         del g_warm
     g_full = graph_of(full, [sets[i % per_replay] for i in range(args.steps)], torch)
     ms = time_graph(g_full, 1, torch) / args.steps
-    log(f"[bench] decode step {ms * 1e3:.2f} us ({args.steps} steps, {args.warmup} warm-up)")
+    # the timed replay is this graph's first: later replays of the same graph, beside it, show
+    # how much of the figure is the graph's first-launch cost
+    later = [time_graph(g_full, 1, torch) / args.steps for _ in range(4)]
+    log(f"[bench] decode step {ms * 1e3:.2f} us ({args.steps} steps, {args.warmup} warm-up); later replays "
+        + " ".join(f"{x * 1e3:.2f}" for x in later) + " us")
     reps = max(1, args.steps // per_replay)
 
     # per-kernel averages (each kernel alone, same rotation, graph-replayed)
@@ -257,7 +261,7 @@ def run_decode(args, torch, device):
         kern[name] = time_graph(gr, reps, torch) / per_replay
         log(f"[bench] {name} {kern[name] * 1e3:.2f} us")
     torch.cuda.synchronize()
-    return s, ms, kern, sets, cos, sin, ws, graphs
+    return s, ms, kern, sets, cos, sin, ws, graphs, later
 
 
 def run_mx_decode(args, torch, device):
@@ -498,7 +502,7 @@ def run_fp8_decode(args, torch, device):
             win=(torch.randn(B, W, D, generator=g, device=device) * sc).to(bf),
             chunk=(torch.randn(B, 1, D, generator=g, device=device) * sc).to(bf),
             comp8=codes(g, B, nb, D), comp_sc=scales(g, B, nb // rb, D // 32),
-            iq=(torch.randn(B, 1, Hi, Di, generator=g, device=device) * 0.3).to(bf),
+            iq=_abi.fq_fp4_ue8m0(torch.randn(B, 1, Hi, Di, generator=g, device=device).to(bf)),
             iq_mx=(codes(g, B, 1, Hi, Di // 2), scales(g, B, 1, Hi, Di // 32)),
             ik8=codes(g, B, nb, Di), ik_sc=scales(g, B, nb // rb, Di // 32),
             w=torch.randn(B, 1, Hi, generator=g, device=device).to(bf),
@@ -517,18 +521,19 @@ def run_fp8_decode(args, torch, device):
     wsc = weight_scale(Hi, Di, bf)
 
     def f_fused(d):
-        # the step's scoring + selection: the fused form over the fp8 keys
-        sel = _abi.indexer_topk_mxq_fp8(d["iq_mx"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, K, wp + 1,
-                                        out=d["fidx"], workspace=d["fws"])
+        # the step's scoring + selection: the fused form over the fp8 keys (exact scores)
+        sel = _abi.indexer_topk_fp8(d["iq"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, K, wp + 1,
+                                    out=d["fidx"], workspace=d["fws"])
         assert sel is not None
 
     def f_idx(d):
-        # the index query in MXFP4 form against the fp8 keys: block-scaled fp4 x fp8 MFMA
-        _abi.indexer_score_mxq_fp8(d["iq_mx"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, out=d["scores"])
-
-    def f_idx_dq(d):
-        # the same scores with the keys dequantized to bf16 in-kernel (VALU) for the bf16 MFMA
+        # the step's scores: keys dequantized in-kernel for the bf16 MFMA, exact products, fp32 sums
         _abi.indexer_score_fp8(d["iq"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, out=d["scores"])
+
+    def f_idx_mxq(d):
+        # opt-in: the index query in MXFP4 form against the fp8 keys on the block-scaled fp4 x fp8
+        # MFMA (its sums carry a few 1e-5 of max |S|, so its selection may swap near-ties)
+        _abi.indexer_score_mxq_fp8(d["iq_mx"], d["w"], wsc, d["ik8"], d["ik_sc"], rb, nb, start, r, out=d["scores"])
 
     def f_topk(d):
         d["idx"] = _abi.topk_select(d["scores"], K, start, r, wp + 1)
@@ -554,15 +559,15 @@ def run_fp8_decode(args, torch, device):
     step_ms = time_graph(g_full, reps, torch) / per
     kern, graphs = {}, [g_full]
     parts = (("indexer_topk", f_fused),) if fused_ok else ()
-    for name, fn in parts + (("indexer_score", f_idx), ("indexer_score_dequant", f_idx_dq), ("topk_select", f_topk),
-                             ("sparse_mla", f_sparse)):
+    for name, fn in parts + (("indexer_score", f_idx), ("indexer_score_mxq_opt_in", f_idx_mxq),
+                             ("topk_select", f_topk), ("sparse_mla", f_sparse)):
         gr = graph_of(fn, sets, torch)
         graphs.append(gr)
         gr.replay()
         kern[name] = time_graph(gr, reps, torch) / per
         log(f"[bench] fp8 {name} {kern[name] * 1e3:.2f} us")
     torch.cuda.synchronize()
-    b_idx = B * (nb * Di + (nb // rb) * (Di // 32) + Hi * (Di // 2 + Di // 32) + Hi * 2 + nb * 4)
+    b_idx = B * (nb * Di + (nb // rb) * (Di // 32) + Hi * Di * 2 + Hi * 2 + nb * 4)
     b_fused = b_idx - B * nb * 4 + B * K * 4           # keys, scales, q, w in; indices out
     b_topk = B * (nb * 4 + K * 4)
     b_sparse = B * (K * (D + D // 32) + (rows - K) * D * 2 + 2 * H * D * 2 + K * 4)
@@ -570,8 +575,9 @@ def run_fp8_decode(args, torch, device):
     log(f"[bench] fp8-cache decode step {step_ms * 1e3:.2f} us")
     return {
         "workload": "fp8-cache decode step: B=16, 131072-token context (nb=32768), top-1024; compressed KV and "
-                    "index keys e4m3 with ue8m0 32x32-block scales; index query MXFP4, scored on the block-scaled "
-                    "fp4 x fp8 MFMA; compressed rows dequantized in-kernel for the bf16 attention; window ring bf16",
+                    "index keys e4m3 with ue8m0 32x32-block scales, dequantized in-kernel (exact index scores: bf16 "
+                    "query on the fp4 grid, bf16 MFMA, fp32 sums); window ring bf16. indexer_score_mxq_opt_in: the "
+                    "MXFP4 query on the block-scaled fp4 x fp8 MFMA, timed alone",
         "step_us": step_ms * 1e3, "tokens_per_s": B / (step_ms * 1e-3),
         "kernels_us": {k: v * 1e3 for k, v in kern.items()},
         "step_algorithmic_bytes": step_bytes,
@@ -596,7 +602,7 @@ def c4_model_args(**over):
     return ModelArgs(**cfg)
 
 
-def c4_step_bytes(a, B, start_pos, index_format="dense"):
+def c4_step_bytes(a, B, start_pos, index_format="dense", mx_query=None):
     """Algorithmic HBM bytes of one 40-layer decode step: per layer the sparse MLA gather
     (window + top-k rows), q and o; per index source the key stream, its queries and the score
     write; top-k score reads and index writes; the candidate mask write and reads; the window /
@@ -608,7 +614,9 @@ def c4_step_bytes(a, B, start_pos, index_format="dense"):
     # per index key, per index-query head, per compressed KV row; the fp8 variant's scale bytes cover
     # 32 x 32 blocks, i.e. 1/32 byte per 32 channels of a row
     kb = {"mxfp4": Di // 2 + Di // 32, "packed": Di // 2 + Di // 32, "fp8": Di + Di / 1024}.get(index_format, Di * 2)
-    qb = Di // 2 + Di // 32 if index_format in ("mxfp4", "packed", "fp8") else Di * 2
+    if mx_query is None:
+        mx_query = index_format in ("mxfp4", "packed")
+    qb = Di // 2 + Di // 32 if mx_query else Di * 2
     cb = {"fp8": D + D / 1024, "packed": D // 2 + D // 16}.get(index_format, D * 2)
     wb = D + D // 32 if index_format == "packed" else D * 2  # per window-ring row
     wp = min(start_pos, W)
@@ -638,7 +646,7 @@ def c4_step_bytes(a, B, start_pos, index_format="dense"):
     return int(total)
 
 
-def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=512):
+def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=512, mxq=False):
     """C4: one decode token through the 40-layer stack at batch 64 and 65,536 tokens of context
     (16,384 compressed entries per sequence), kernels only: window writes, owner latent / key
     writes (the token completes a group), indexer + top-k at the 8 index sources (candidate
@@ -646,7 +654,9 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
     exceed the Infinity Cache, so one input set suffices. index_format "mxfp4": the index
     caches and index queries in packed fp4 form (codes + ue8m0 scales, random valid bytes);
     "packed": those and the compressed KV as packed fp4 rows (e2m1 + e4m3 per 16 channels);
-    "fp8": the fp8 cache variant in 32 x 32 blocks."""
+    "fp8": the fp8 cache variant in 32 x 32 blocks, scored exactly (bf16 index queries on the fp4
+    grid against keys dequantized in-kernel), or with mxq on the block-scaled fp4 x fp8 MFMA
+    (MXFP4 queries; opt-in, its sums are not the exact scores)."""
     from dsv41 import _abi
     from dsv41.cache import ModelCache
     from dsv41.indexer import weight_scale
@@ -699,7 +709,7 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
         x = dict(q=(rn(B, 1, H, D) * sc).to(bf), kv=(rn(B, 1, D) * sc).to(bf), sink=rn(H))
         if a.compress_ratio(l) and l in a.index_source_layers:
             x.update(w_raw=rn(B, 1, Hi).to(bf), w_scale=weight_scale(Hi, Di, bf))
-            if mx or fp8:                    # the query in MXFP4 form (fp8 keys: the fp4 x fp8 MFMA)
+            if mx or (fp8 and mxq):          # the query in MXFP4 form (fp8 keys: the fp4 x fp8 MFMA)
                 x["index_q_mx"] = (rbytes(0, 256, B, 1, Hi, Di // 2), rbytes(123, 132, B, 1, Hi, Di // 32))
             else:
                 x["index_q"] = _abi.fq_fp4_ue8m0(rn(B, 1, Hi, Di).to(bf))
@@ -726,7 +736,7 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
         for _ in range(max(1, args.warmup // 4)):
             gr.replay()
         ms = time_graph(gr, reps, torch)
-    nbytes = c4_step_bytes(a, B, start, index_format)
+    nbytes = c4_step_bytes(a, B, start, index_format, mx_query=mx or (fp8 and mxq))
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] C4 step {ms:.3f} ms, {B / (ms * 1e-3):.0f} tokens/s, {gbs:.0f} GB/s")
     name = "C5" if fp8 else "C4"
@@ -734,7 +744,9 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
         "workload": f"{name}: 40-layer attention-only decode step (kernels only), B={B}, {start + 1}-token context "
                     f"(nb={(start + 1) // 4}), ratio 4, top-{topk}; owners 2/8/14/20, index sources 2..36, candidate "
                     f"source 20; " + ("fp8 caches (e4m3 + ue8m0 per 32x32 block) for compressed KV and index keys, "
-                                      "index queries MXFP4 (fp4 x fp8 MFMA scoring), window ring bf16" if fp8
+                                      + ("index queries MXFP4 (fp4 x fp8 MFMA scoring, opt-in)" if mxq else
+                                         "exact index scores (keys dequantized in-kernel)") + ", window ring bf16"
+                                      if fp8
                                       else "packed caches: compressed KV e2m1 + e4m3 per 16 channels (288 B/row), "
                                       "window ring MXFP8 (528 B/row), index keys and queries MXFP4" if packed
                                       else f"index caches {index_format}"),
@@ -836,7 +848,7 @@ def main():
     from dsv41 import _abi
     _abi.lib()
 
-    s, ms, kern, sets, cos, sin, ws, _graphs = run_decode(args, torch, device)
+    s, ms, kern, sets, cos, sin, ws, _graphs, later = run_decode(args, torch, device)
     # the step runs the fused indexer + top-k form and the sparse MLA (with its split combine)
     step_bytes = s.bytes_indexer_topk() + s.bytes_sparse()
     step_gbs = step_bytes / (ms * 1e-3) / 1e9
@@ -850,6 +862,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "ms_per_step_later_replays": later,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -933,6 +946,13 @@ def main():
             except Exception as e:
                 result["c5_stack_decode_fp8"] = {"error": repr(e)}
             torch.cuda.empty_cache()
+            if not args.no_mx:
+                try:
+                    result["c5_stack_decode_fp8_mxq_opt_in"] = run_c4(args, torch, device, "fp8", B=16, start=131071,
+                                                                      topk=1024, mxq=True)
+                except Exception as e:
+                    result["c5_stack_decode_fp8_mxq_opt_in"] = {"error": repr(e)}
+                torch.cuda.empty_cache()
     if not args.no_cpu:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(s, sets, cos, sin, ws, args.cpu_seconds, torch)

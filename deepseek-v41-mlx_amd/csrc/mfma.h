@@ -145,6 +145,11 @@ __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// The two bf16 values of a packed pair (low half first), widened exactly and summed in fp32.
+__device__ __forceinline__ float sum_bf16x2(uint32_t u) {
+  return __uint_as_float(u << 16) + __uint_as_float(u & 0xFFFF0000u);
+}
+
 // 2^x with the bare v_exp_f32 (no denormal-range fix-up). Used for softmax weights 2^(s - m) with
 // s - m <= the lazy-rescale threshold: results below 2^-126 are zero for the sum anyway.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -414,11 +414,15 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
       m_run = grow ? gmax : m_run;
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      p[e] = fast_exp2(p[e] - m_run);
-      l_run += p[e];
-    }
+    for (int e = 0; e < 8; ++e) p[e] = fast_exp2(p[e] - m_run);
     const bf16x8 pb = cvt_bf16x8(p);
+    // the denominator sums the weights as the PV product takes them (rounded to bf16), so every
+    // output is a normalized average of its rows: the rounding moves weight between rows but
+    // never scales a head's output
+    {
+      const uint4 pu = __builtin_bit_cast(uint4, pb);
+      l_run += (sum_bf16x2(pu.x) + sum_bf16x2(pu.y)) + (sum_bf16x2(pu.z) + sum_bf16x2(pu.w));
+    }
 #pragma unroll
     for (int dt = 0; dt < DTS; ++dt) {
       const uint8_t* col = buf + (dh * DSL + dt * 16 + 4 * (l16 & 3)) * 2;
@@ -582,16 +586,16 @@ __global__ __launch_bounds__(512, 1) void mla_roles_kernel(MlaArgs a) {
         m_run = grow ? gmax : m_run;
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        p[e] = fast_exp2(p[e] - m_run);
-        l_run += p[e];
-      }
-      // rows 16 rt + 4 g .. + 3 of head hl
+      for (int e = 0; e < 8; ++e) p[e] = fast_exp2(p[e] - m_run);
+      // rows 16 rt + 4 g .. + 3 of head hl; the denominator sums the weights as the value waves
+      // take them (rounded to bf16), so every output is a normalized average of its rows
       uint8_t* pt = &pbuf[t & 1][hl][0];
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-        *reinterpret_cast<uint2*>(pt + (16 * rt + 4 * g) * 2) =
-            make_uint2(pack2_bf16(p[4 * rt], p[4 * rt + 1]), pack2_bf16(p[4 * rt + 2], p[4 * rt + 3]));
+      for (int rt = 0; rt < 2; ++rt) {
+        const uint32_t w0 = pack2_bf16(p[4 * rt], p[4 * rt + 1]), w1 = pack2_bf16(p[4 * rt + 2], p[4 * rt + 3]);
+        *reinterpret_cast<uint2*>(pt + (16 * rt + 4 * g) * 2) = make_uint2(w0, w1);
+        l_run += sum_bf16x2(w0) + sum_bf16x2(w1);
+      }
       if (g == 0) abuf[t & 1][hl] = alpha;
     }
     l_run += __shfl_xor(l_run, 16, 64);           // denominator: sum of the 4 lane groups

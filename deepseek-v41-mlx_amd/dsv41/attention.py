@@ -19,6 +19,13 @@ The window ring is written after the attention kernel has read the previous wind
 is equivalent to the reference's write-before-concatenate order because the concatenated
 copy held the old ring contents.
 
+Caches held in another dtype than the activations (the reference's default: fp32 caches under a
+bf16 model, cache.py:29, 72) are converted at every cache boundary, as the reference converts
+them (attention.py:127, 163, 166; cache.py:67): stores compute in the activation dtype and
+convert on the store, reads convert the visible rows to the activation dtype first. That costs
+one copy of the visible cache per call; keeping the cache in the activation dtype reads it in
+place.
+
 The forward is chunk-general: prefill, chunked prefill and 1-token decode share one path.
 """
 
@@ -31,6 +38,11 @@ from .compressor import Compressor
 from .config import ModelArgs
 from .indexer import Indexer
 from .layers import RMSNorm, yarn_inv_freqs
+
+
+# multiply-adds from which fp32 activations take the batched GEMM for wo_a (the release shape
+# 8 x (4096 -> 1024) from two rows on)
+_WO_A_FP32_GEMM_MACS = 1 << 26
 
 
 def window_idx_matrix(wp: int, n: int, window: int, device="cuda") -> torch.Tensor:
@@ -118,12 +130,20 @@ class Attention(torch.nn.Module):
         if lc.comp_kv4 is not None:           # packed fp4 cache: the same fp4/e4m3 QAT, stored packed
             _abi.comp_write_fp4(latents.to(self.dtype).contiguous(), lc.comp_kv4, g0, self.ratio, cos, sin, rd)
             return
-        lat = latents.to(lc.dtype).contiguous()
+        lat = latents.contiguous()
         if fakequant.DISABLE:
             lat = _abi.rope_tail(lat, rd, cos, sin, g0 * self.ratio, self.ratio)
             lc.comp_kv[:lat.shape[0], g0:g0 + lat.shape[1]] = lat
             return
-        _abi.comp_write(lat, lc.comp_kv, g0, self.ratio, cos, sin, rd)
+        if lc.comp_kv.dtype == lat.dtype:
+            _abi.comp_write(lat, lc.comp_kv, g0, self.ratio, cos, sin, rd)
+            return
+        # a cache in another dtype: rope + QAT in the latents' dtype, converted on the store
+        # (attention.py:158-163); tables shifted so group j sits at position (g0 + j) * ratio
+        staged = torch.empty_like(lat)
+        p0 = g0 * self.ratio
+        _abi.comp_write(lat, staged, 0, self.ratio, cos[p0:], sin[p0:], rd)
+        lc.comp_kv[:lat.shape[0], g0:g0 + lat.shape[1]] = staged
 
     def forward(self, x: torch.Tensor, start_pos: int, cache, shared) -> torch.Tensor:
         """x [b, n, dim] (post attn_norm), absolute positions [start_pos, start_pos + n)."""
@@ -161,6 +181,8 @@ class Attention(torch.nn.Module):
                     cidx = torch.zeros(bsz, n, 0, dtype=torch.int32, device=x.device)
                 else:
                     index_k = shared.index_src_cache.index_keys(bsz, compress_len)
+                    if isinstance(index_k, torch.Tensor) and index_k.dtype != x.dtype:
+                        index_k = index_k.to(x.dtype)   # indexer.py:125 reads the keys converted
                     cidx = self.indexer(x, qr, start_pos, offset, cos, sin, index_k, shared)
                 shared.topk_idxs = cidx
             else:
@@ -169,11 +191,17 @@ class Attention(torch.nn.Module):
                 self._write_latents(latents, lc, start_pos // self.ratio, cos, sin)
             if compress_len:
                 (comp_kind, comp), n_comp = src.comp_source(bsz), compress_len
+                if comp_kind == "dense" and comp.dtype != x.dtype:
+                    comp = comp[:, :n_comp].to(x.dtype)     # attention.py:166
 
         sink = torch.zeros_like(self.attn_sink) if self._break_sink else self.attn_sink
         # one-token decode: the attention launch also writes the token into the ring (the slot it
         # takes is outside the token's window); a chunk writes its ring after the attention
-        decode = n == 1
+        # (a ring held in another dtype is read converted, attention.py:127, and written after)
+        ring = lc.win_kv
+        if ring is not None and ring.dtype != x.dtype:
+            ring = ring[:bsz].to(x.dtype)
+        decode = n == 1 and ring is lc.win_kv
         sel = cidx if cidx is not None and cidx.shape[-1] else None
         rdo = 0 if self._break_rope_inverse else rd
         if lc.win_kv8 is not None:          # the packed cache: MXFP8 ring, fp4 compressed rows
@@ -181,18 +209,29 @@ class Attention(torch.nn.Module):
                                        self.softmax_scale, self.window_size, start_pos, cos, sin, rdo,
                                        write_ring=decode, q_rd=rd)
         elif comp_kind == "fp8":
-            o = _abi.sparse_mla_fp8(q, lc.win_kv, kv, comp, src.comp_ks[:bsz], src.fp8_rb, n_comp, sink, sel,
+            o = _abi.sparse_mla_fp8(q, ring, kv, comp, src.comp_ks[:bsz], src.fp8_rb, n_comp, sink, sel,
                                     self.softmax_scale, self.window_size, start_pos, cos, sin, rdo, write_ring=decode,
                                     q_rd=rd)
         elif comp_kind == "fp4":
-            o = _abi.sparse_mla_fp4(q, lc.win_kv, kv, comp, n_comp, sink, sel, self.softmax_scale, self.window_size,
+            o = _abi.sparse_mla_fp4(q, ring, kv, comp, n_comp, sink, sel, self.softmax_scale, self.window_size,
                                     start_pos, cos, sin, rdo, write_ring=decode, q_rd=rd)
         else:
-            o = _abi.sparse_mla(q, lc.win_kv, kv, comp, n_comp, sink, sel, self.softmax_scale, self.window_size,
+            o = _abi.sparse_mla(q, ring, kv, comp, n_comp, sink, sel, self.softmax_scale, self.window_size,
                                 start_pos, cos, sin, rdo, write_ring=decode, q_rd=rd)
         if not decode:
             lc.write_window(start_pos, kv)
 
         # grouped block-diagonal wo_a, fp32 sums cast to x's dtype, then wo_b (attention.py:176-179)
-        oa = _abi.wo_a_grouped(o.view(bsz, n, -1), self.wo_a.weight, self.n_groups, out_dtype=x.dtype)
-        return self.wo_b(oa)
+        return self.wo_b(self._wo_a(o.view(bsz, n, -1), x.dtype))
+
+    def _wo_a(self, o, out_dtype):
+        g, r = self.n_groups, self.o_lora_rank
+        d = o.shape[-1] // g
+        rows = o.numel() // o.shape[-1]
+        if o.dtype == torch.float32 and rows * o.shape[-1] * r >= _WO_A_FP32_GEMM_MACS:
+            # fp32 activations at GEMM-sized shapes: one fp32 GEMM per group (the grouped kernel's
+            # fp32 form is a one-thread-per-output loop, meant for small shapes)
+            og = o.reshape(rows, g, d).transpose(0, 1).contiguous()                  # [g, rows, d]
+            wg = self.wo_a.weight.view(g, r, d).transpose(1, 2).contiguous()         # [g, d, r]
+            return torch.bmm(og, wg).transpose(0, 1).reshape(*o.shape[:-1], g * r).to(out_dtype)
+        return _abi.wo_a_grouped(o, self.wo_a.weight, g, out_dtype=out_dtype)

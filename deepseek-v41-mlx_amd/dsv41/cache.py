@@ -33,12 +33,16 @@ update them in place, so a snapshot must copy: ``lc.win_kv[:]`` -- which in MLX 
 pre-step value (generate.py:18-44) -- is a view in torch. ``snapshot(cache)`` and
 ``restore(cache, snap)`` are the torch counterparts of generate.py's ``_cache_snapshot`` /
 ``_cache_restore``: they copy every buffer of every format, and restore writes back into the
-same tensors, so references to them (a captured HIP graph, a consumer's view) stay valid. The
-attention kernels require ``dtype`` to equal the activation dtype.
+same tensors, so references to them (a captured HIP graph, a consumer's view) stay valid.
+
+``dtype`` defaults to fp32, the reference's default (cache.py:29, 72). The attention layer
+converts at every boundary of a cache held in another dtype than its activations, as the
+reference does (attention.py:127, 163, 166); a cache in the activation dtype is read in place.
 """
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import _abi
@@ -168,7 +172,9 @@ class ModelCache:
         self.layers = [LayerCache(bsz, args, i, self.max_seq_len, dtype, device, index_format, cache_format,
                                   fp8_block_rows)
                        for i in range(args.n_layers)]
-        self.engram_ids = None
+        # token ids the engram hasher reads back (cache.py:77-78); host memory, as there
+        self.engram_ids = (np.zeros((bsz, self.max_seq_len), dtype=np.int64)
+                           if args.engram_layer_ids else None)
 
 
 _BUFFERS = ("win_kv", "comp_kv", "index_k", "index_k4", "index_ks", "comp_kv8", "comp_ks", "index_k8", "index_k8s",
@@ -183,7 +189,7 @@ def snapshot(cache: ModelCache):
         cs = lc.comp_state
         state = (cs.kv_state.clone(), cs.score_state.clone()) if cs is not None else None
         layers.append((bufs, state))
-    eng = cache.engram_ids.clone() if cache.engram_ids is not None else None
+    eng = cache.engram_ids.copy() if cache.engram_ids is not None else None
     return cache.offset, layers, eng
 
 
@@ -200,5 +206,5 @@ def restore(cache: ModelCache, snap) -> None:
             lc.comp_state.kv_state.copy_(state[0])
             lc.comp_state.score_state.copy_(state[1])
     if eng is not None:
-        cache.engram_ids.copy_(eng)
+        cache.engram_ids[...] = eng
 

@@ -1,17 +1,22 @@
-"""Configuration of the attention path: the fields of the reference's ``ModelArgs`` that
-this package reads (deepseek_v41_mlx/config.py:28-106), loaded from either release layout.
+"""Configuration of the attention path: the reference's ``ModelArgs``
+(deepseek_v41_mlx/config.py:28-106), loaded from either release layout.
 
 Design:
 
-* ``_KEYS`` is one table, ``(attribute, JSON names tried in order, default)``. The first
-  JSON name that is present and not null wins. The same table serves keyword construction,
-  the flat inference ``config.json`` and the HF hub file (whose ``text_config`` is folded
-  over its top level first, config.py:137-140). YaRN settings may also arrive inside a
-  ``rope_scaling`` object (config.py:142, 179-183); ``_ROPE_SCALING`` names them.
-* Only the attention path's fields are typed attributes. Every other keyword or JSON key
-  of a release config (MoE, engram, hyper-connection, vision sizes ...) is kept verbatim in
-  ``extra`` and reachable as an attribute, so model code that reads e.g. ``args.hc_mult``
-  still runs, but nothing here interprets it.
+* ``_KEYS`` is one table, ``(attribute, JSON names tried in order, default)``, holding every
+  attribute the reference defines (config.py:30-102) with its default and the JSON names its
+  ``from_dict`` reads (config.py:146-191). The first JSON name that is present and not null
+  wins. The same table serves keyword construction, the flat inference ``config.json`` and the
+  HF hub file (whose ``text_config`` is folded over its top level first, config.py:137-140).
+  YaRN settings may also arrive inside a ``rope_scaling`` object (config.py:142, 179-183);
+  ``_ROPE_SCALING`` names them. Two fields differ between the two routes, as in the reference:
+  a file without ``swiglu_limit`` gives 0.0 (the keyword default is 10.0), and a file never
+  sets ``vision_n_layers`` (text-only runtime).
+* Only the attention path's fields are read here. The MoE, hyper-connection, engram and
+  side-path fields are pass-through entries: they carry the reference's names, defaults and
+  JSON aliases so model code that reads e.g. ``args.hc_mult`` or ``args.n_activated_experts``
+  runs, but nothing here interprets them. Keys outside the table (vision sizes, tokenizer ids
+  ...) are kept verbatim in ``extra`` and reachable as attributes.
 * The sharing topology is resolved by one walk down the layer stack
   (``_resolve_sources``): a compressing layer reads the latest KV source at or above it,
   whose compress ratio must equal its own, and the latest index source at or above it.
@@ -51,13 +56,44 @@ _KEYS = (
     ("index_n_heads", ("index_n_heads",), 32),
     ("index_head_dim", ("index_head_dim",), 128),
     ("index_topk", ("index_topk",), 512),
+    # pass-through: read by model code outside the attention path, never interpreted here
+    ("vocab_size", ("vocab_size",), 129280),
+    ("moe_inter_dim", ("moe_intermediate_size", "moe_inter_dim"), 2304),
+    ("n_routed_experts", ("n_routed_experts",), 384),
+    ("n_shared_experts", ("n_shared_experts",), 1),
+    ("n_activated_experts", ("num_experts_per_tok", "n_activated_experts"), 6),
+    ("score_func", ("scoring_func", "score_func"), "sqrtsoftplus"),
+    ("gate_temp", ("gate_temp",), 1.0),
+    ("norm_topk_prob", ("norm_topk_prob",), True),
+    ("route_scale", ("routed_scaling_factor", "route_scale"), 1.5),
+    ("swiglu_limit", ("swiglu_limit",), 10.0),
+    ("hc_mult", ("hc_mult",), 4),
+    ("hc_sinkhorn_iters", ("hc_sinkhorn_iters",), 20),
+    ("hc_eps", ("hc_eps",), 1e-6),
+    ("engram_layer_ids", ("engram_layer_ids",), ()),
+    ("engram_num_embeddings", ("engram_num_embeddings",), ()),
+    ("engram_max_ngram_size", ("engram_max_ngram_size",), 4),
+    ("engram_vocab_size", ("engram_vocab_size",), 0),
+    ("engram_n_heads", ("engram_n_heads",), 0),
+    ("engram_head_dim", ("engram_head_dim",), 0),
+    ("engram_pad_id", ("engram_pad_token_id", "engram_pad_id"), 2),
+    ("engram_compressed_vocab_size", ("engram_compressed_vocab_size",), 0),
+    ("n_mtp_layers", ("num_nextn_predict_layers", "n_mtp_layers"), 0),
+    ("dspark_target_layer_ids", ("dspark_target_layer_ids",), ()),
+    ("vision_n_layers", ("vision_n_layers",), 0),
 )
+
+# a release file that omits these gets a different value than keyword construction
+# (config.py:162, 193): the file route's default, and a field the file route never sets
+_FILE_DEFAULTS = {"swiglu_limit": 0.0}
+_FILE_FIXED = {"vision_n_layers": 0}
 
 # attribute -> its name inside a ``rope_scaling`` object, which takes precedence
 _ROPE_SCALING = {"original_seq_len": "original_max_position_embeddings",
                  "rope_factor": "factor", "beta_fast": "beta_fast", "beta_slow": "beta_slow"}
 
 _SEQUENCE_FIELDS = {"compress_ratios", "kv_source_layers", "index_source_layers"}
+_TUPLE_FIELDS = {"engram_layer_ids", "engram_num_embeddings", "dspark_target_layer_ids"}
 _FIELDS = {name for name, _, _ in _KEYS}
 
 
@@ -78,6 +114,8 @@ class ModelArgs:
             v = kw.get(name, default)
             if name in _SEQUENCE_FIELDS:
                 v = _TUPLE(int(x) for x in (v or ()))
+            elif name in _TUPLE_FIELDS:
+                v = _TUPLE(v or ())
             setattr(self, name, v)
         # not typed attributes of this path; kept so a release config round-trips
         self.extra = extra
@@ -179,10 +217,20 @@ class ModelArgs:
         claimed = {"text_config", "rope_scaling"}
         for name, json_names, _ in _KEYS:
             claimed.update(json_names)
+            if name in _FILE_FIXED:
+                kw[name] = _FILE_FIXED[name]
+                continue
             v = rope.get(_ROPE_SCALING[name]) if name in _ROPE_SCALING else None
             if v is None:
                 v = _first(flat, json_names)
+            if v is None:
+                v = _FILE_DEFAULTS.get(name)
             if v is not None:
                 kw[name] = v
         kw.update({k: v for k, v in flat.items() if k not in claimed and k not in _FIELDS})
         return cls(**kw)
+
+    @property
+    def raw(self) -> dict:
+        """The model type tag of the reference's config (config.py:196-198)."""
+        return {"model_type": "deepseek_v41"}

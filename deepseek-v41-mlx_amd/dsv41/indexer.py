@@ -94,8 +94,17 @@ class Indexer(torch.nn.Module):
             k = _abi.rope_tail(k, rd, cos, sin, g0 * self.ratio, self.ratio)
             cache.index_k[:k.shape[0], g0:g0 + k.shape[1]] = k
             return
-        _abi.index_key_publish(k_raw, cache.index_k, g0, self.ratio, self.k_norm.weight, cos, sin,
-                               rd, self.k_norm.eps)
+        if cache.index_k.dtype == k_raw.dtype:
+            _abi.index_key_publish(k_raw, cache.index_k, g0, self.ratio, self.k_norm.weight, cos, sin,
+                                   rd, self.k_norm.eps)
+            return
+        # a cache in another dtype: norm, rope and QAT in the keys' dtype, converted on the store
+        # (indexer.py:104); tables shifted so group j sits at position (g0 + j) * ratio
+        staged = torch.empty_like(k_raw)
+        p0 = g0 * self.ratio
+        _abi.index_key_publish(k_raw, staged, 0, self.ratio, self.k_norm.weight, cos[p0:], sin[p0:], rd,
+                               self.k_norm.eps)
+        cache.index_k[:k_raw.shape[0], g0:g0 + k_raw.shape[1]] = staged
 
     def forward(self, x: torch.Tensor, qr: torch.Tensor, start_pos: int, offset: int,
                 cos, sin, index_k: torch.Tensor, shared) -> torch.Tensor:

@@ -39,10 +39,13 @@ class AttentionStack(torch.nn.Module):
         # test hook (negative control), model.py:111-112, 145-152
         self._break_sharing = False
 
-    def make_cache(self, bsz: int = 1, max_seq_len: int | None = None, index_format: str = "dense",
+    def make_cache(self, bsz: int = 1, max_seq_len: int | None = None, dtype=None, *, index_format: str = "dense",
                    cache_format: str = "dense", fp8_block_rows: int = 1) -> ModelCache:
-        return ModelCache(self.args, bsz, max_seq_len, self.dtype, self.device, index_format, cache_format,
-                          fp8_block_rows)
+        """The reference's Model.make_cache (model.py:117-119) takes the cache dtype, fp32 by
+        default; here it defaults to the stack's own dtype, whose caches the kernels read in
+        place. Any other dtype is converted at each cache boundary, as the reference does."""
+        return ModelCache(self.args, bsz, max_seq_len, self.dtype if dtype is None else dtype, self.device,
+                          index_format, cache_format, fp8_block_rows)
 
     def forward(self, h: torch.Tensor, cache: ModelCache) -> torch.Tensor:
         """h [b, n, dim] continues the sequence at cache.offset; advances the cache."""

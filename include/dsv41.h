@@ -12,7 +12,9 @@
  *     violation (bad size, dtype, null pointer, unsupported shape), or a positive
  *     hipError_t from the launch; dsv41_last_error_string() then describes it
  *     (thread-local, valid until the next call on the same thread);
- *   - calls are stateless and reentrant.
+ *   - calls are stateless and reentrant, with one exception: dsv41_sparse_mla_decode_noalloc
+ *     keeps its split partials in one process-wide static device array per GPU, so its calls
+ *     on one GPU must be ordered on one stream (overlapping calls race on that array).
  *
  * Reference citations name files of the reference repository (thedracle/deepseek-v41-mlx):
  * the MLX modules under deepseek_v41_mlx/ and DeepSeek's TileLang kernels in

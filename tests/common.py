@@ -109,3 +109,74 @@ def load_stack(stack, params: list) -> None:
 def model_args(cfg: dict):
     from dsv41.config import ModelArgs
     return ModelArgs(**cfg)
+
+
+# ---------------------------------------------------------------- bf16 attention check
+
+# bf16 attention outputs are held to the 2e-2 relative gate, and to two per-head bounds at the
+# kernels' own error level (bf16 rounding of the softmax weights fed to the PV product and of the
+# output), which a sink in the wrong place, a dropped list row or a shifted window exceed even
+# where they stay inside 2e-2 of max |o|:
+#   * per-head scale: alpha_h = <got_h, want_h> / <want_h, want_h>, over every query and channel
+#     of head h, within ATTN_ALPHA of 1 -- a sink that enters a head's denominator wrongly
+#     scales that head's whole output. The kernels normalize by the sum of the bf16 weights they
+#     multiply, so rounding only moves weight between rows; where one row dominates a head that
+#     moves the fit by up to one bf16 half-ulp, 2^-8, the bound (over many rows it averages out:
+#     ~2e-4 at 640 rows);
+#   * per-head max error within ATTN_HEAD_REL of that head's own max |want_h|.
+ATTN_ALPHA = 2.0 ** -8
+ATTN_HEAD_REL = 1.5e-2
+
+
+def attn_metrics(got, want):
+    """(max |got - want| / max |want|, max_h |alpha_h - 1|, max_h per-head relative max error)
+    over arrays [..., heads, channels]."""
+    g = np.asarray(got, np.float64)
+    w = np.asarray(want, np.float64)
+    h = g.shape[-2]
+    g2 = np.moveaxis(g, -2, 0).reshape(h, -1)
+    w2 = np.moveaxis(w, -2, 0).reshape(h, -1)
+    ww = (w2 * w2).sum(1)
+    live = ww > 0
+    alpha = np.where(live, (g2 * w2).sum(1) / np.where(live, ww, 1.0), 1.0)
+    head_max = np.abs(w2).max(1)
+    err = np.abs(g2 - w2).max(1)
+    head_err = np.where(live, err / np.where(live, head_max, 1.0), err)
+    return rel_max_diff(g, w), float(np.abs(alpha - 1).max()), float(head_err.max())
+
+
+def attn_close(got, want) -> bool:
+    rel, a, e = attn_metrics(got, want)
+    return rel < 2e-2 and a <= ATTN_ALPHA and e <= ATTN_HEAD_REL
+
+
+def assert_attn_close(got, want, what=""):
+    rel, a, e = attn_metrics(got, want)
+    assert rel < 2e-2 and a <= ATTN_ALPHA and e <= ATTN_HEAD_REL, \
+        f"{what} rel {rel:.3e} |alpha-1| {a:.3e} head err {e:.3e}"
+
+
+def attn_controls(idx, sink, window_rows=0):
+    """Planted mistakes for the bf16 attention check, as changed oracle inputs: (name, idx, sink).
+    idx [b, m, k] with the window rows first (window_rows of them) when window_rows > 0.
+
+    * the sink zeroed;
+    * the sink counted once per split of two (its weight doubled: sink + ln 2);
+    * the last valid list row of every query dropped;
+    * the window read one row early: its rows' indices minus one (the oldest row that has just
+      left the window in, the newest row out)."""
+    idx = np.asarray(idx)
+    yield "sink zeroed", idx, np.zeros_like(sink)
+    yield "sink once per split", idx, (sink + np.log(2.0)).astype(np.float32)
+    dropped = idx.copy()
+    valid = dropped >= 0
+    last = dropped.shape[-1] - 1 - np.argmax(valid[..., ::-1], axis=-1)
+    has = valid.any(-1)
+    bi, mi = np.nonzero(has)
+    dropped[bi, mi, last[bi, mi]] = -1
+    yield "one list row dropped", dropped, sink
+    if window_rows:
+        shifted = idx.copy()
+        win = shifted[..., :window_rows]
+        shifted[..., :window_rows] = np.where(win >= 0, win - 1, -1)
+        yield "window shifted by one", shifted, sink

@@ -183,9 +183,10 @@ def test_model_args_topology_and_both_config_layouts():
     bad = ModelArgs(compress_ratios=(2, 1), kv_source_layers=(0,))
     with pytest.raises(ValueError, match="ratio"):
         bad.kv_source_for(1)
-    # fields outside the attention path are kept verbatim and readable, never interpreted
-    a = ModelArgs.from_dict({**flat, "hc_mult": 4, "moe_inter_dim": 32})
-    assert a.hc_mult == 4 and a.moe_inter_dim == 32 and a.extra == {"hc_mult": 4, "moe_inter_dim": 32}
+    # fields outside the attention path are read by their reference names, never interpreted;
+    # keys outside the reference's table are kept verbatim
+    a = ModelArgs.from_dict({**flat, "hc_mult": 3, "moe_inter_dim": 32, "vision_dim": 9})
+    assert a.hc_mult == 3 and a.moe_inter_dim == 32 and a.extra == {"vision_dim": 9} and a.vision_dim == 9
     assert ModelArgs(n_routed_experts=8).n_routed_experts == 8
     with pytest.raises(AttributeError):
         ModelArgs().no_such_field
@@ -199,6 +200,80 @@ def test_model_args_topology_and_both_config_layouts():
     d.kv_source_layers = (2,)
     with pytest.raises(ValueError):
         d.kv_source_for(1)
+
+
+# every attribute of the reference's ModelArgs (deepseek_v41_mlx/config.py:30-102) with the value
+# its from_dict gives for the two release files (config.py:136-193, read by hand): both layouts
+# describe the same model, so one table serves both
+_RELEASE_ATTRS = {
+    "vocab_size": 129280, "dim": 5120, "n_layers": 40, "moe_inter_dim": 2304, "n_heads": 64, "head_dim": 512,
+    "rope_head_dim": 64, "q_lora_rank": 1280, "o_lora_rank": 1024, "o_groups": 8, "window_size": 128,
+    "norm_eps": 1e-20, "n_routed_experts": 384, "n_shared_experts": 1, "n_activated_experts": 6,
+    "score_func": "sqrtsoftplus", "gate_temp": 1.0, "norm_topk_prob": True, "route_scale": 1.5,
+    "swiglu_limit": 10.0, "kv_source_layers": (2, 8, 14, 20),
+    "index_source_layers": (2, 8, 14, 20, 24, 28, 32, 36), "compress_rope_theta": 160000,
+    "candidate_source_layer": 20, "candidate_topk_blocks": 2048, "candidate_block_size": 8,
+    "original_seq_len": 65536, "rope_theta": 10000, "rope_factor": 16, "beta_fast": 32, "beta_slow": 1,
+    "max_seq_len": 1048576, "index_n_heads": 32, "index_head_dim": 128, "index_topk": 512, "hc_mult": 4,
+    "hc_sinkhorn_iters": 20, "hc_eps": 1e-6, "engram_layer_ids": (1, 14),
+    "engram_num_embeddings": (384006168, 384016682), "engram_max_ngram_size": 4, "engram_vocab_size": 16000000,
+    "engram_n_heads": 8, "engram_head_dim": 256, "engram_pad_id": 2, "engram_compressed_vocab_size": 99092,
+    "n_mtp_layers": 3, "dspark_target_layer_ids": (37, 38, 39), "vision_n_layers": 0,
+}
+
+# keyword construction: the dataclass defaults of config.py:30-102
+_DEFAULT_ATTRS = {
+    "vocab_size": 129280, "dim": 5120, "n_layers": 40, "moe_inter_dim": 2304, "n_heads": 64, "head_dim": 512,
+    "rope_head_dim": 64, "q_lora_rank": 1280, "o_lora_rank": 1024, "o_groups": 8, "window_size": 128,
+    "norm_eps": 1e-20, "n_routed_experts": 384, "n_shared_experts": 1, "n_activated_experts": 6,
+    "score_func": "sqrtsoftplus", "gate_temp": 1.0, "norm_topk_prob": True, "route_scale": 1.5,
+    "swiglu_limit": 10.0, "compress_ratios": (), "kv_source_layers": (), "index_source_layers": (),
+    "compress_rope_theta": 160000.0, "candidate_source_layer": -1, "candidate_topk_blocks": 0,
+    "candidate_block_size": 0, "original_seq_len": 65536, "rope_theta": 10000.0, "rope_factor": 16.0,
+    "beta_fast": 32, "beta_slow": 1, "max_seq_len": 1048576, "index_n_heads": 32, "index_head_dim": 128,
+    "index_topk": 512, "hc_mult": 4, "hc_sinkhorn_iters": 20, "hc_eps": 1e-6, "engram_layer_ids": (),
+    "engram_num_embeddings": (), "engram_max_ngram_size": 4, "engram_vocab_size": 0, "engram_n_heads": 0,
+    "engram_head_dim": 0, "engram_pad_id": 2, "engram_compressed_vocab_size": 0, "n_mtp_layers": 0,
+    "dspark_target_layer_ids": (), "vision_n_layers": 0,
+}
+
+
+def test_model_args_release_files_expose_every_reference_attribute():
+    """Both release layouts (the flat inference config.json and the hub file, stored verbatim in
+    tests/golden/release_configs.json) give every attribute the reference's ModelArgs defines, with
+    the values its from_dict gives, and keyword construction gives the dataclass defaults."""
+    import json
+    from dsv41.config import ModelArgs
+    with open(os.path.join(os.path.dirname(__file__), "golden", "release_configs.json")) as f:
+        files = json.load(f)
+    assert set(_RELEASE_ATTRS) | {"compress_ratios"} == set(_DEFAULT_ATTRS)
+    for layout in ("flat", "hub"):
+        a = ModelArgs.from_dict(files[layout])
+        for name, want in _RELEASE_ATTRS.items():
+            got = getattr(a, name)
+            assert got == want and type(got) is type(want), (layout, name, got, want)
+        assert len(a.compress_ratios) == 43 and a.compress_ratios[:4] == (0, 0, 2, 2)
+        assert [a.kv_source_for(i) for i in (2, 7, 21, 39)] == [2, 2, 20, 20]
+        assert a.raw == {"model_type": "deepseek_v41"}
+    d = ModelArgs()
+    for name, want in _DEFAULT_ATTRS.items():
+        assert getattr(d, name) == want, (name, getattr(d, name), want)
+    # the two routes differ where the reference's differ (config.py:162, 193)
+    assert ModelArgs.from_dict({}).swiglu_limit == 0.0 and ModelArgs().swiglu_limit == 10.0
+    assert ModelArgs.from_dict({"vision_n_layers": 32}).vision_n_layers == 0
+    # every hub alias is read (values away from the defaults, so a dropped alias cannot pass)
+    hub = {"text_config": {"moe_intermediate_size": 7, "num_experts_per_tok": 9, "scoring_func": "softmax",
+                           "routed_scaling_factor": 2.5, "engram_pad_token_id": 5, "num_nextn_predict_layers": 1,
+                           "hidden_size": 64, "num_hidden_layers": 3, "num_attention_heads": 4,
+                           "qk_rope_head_dim": 16, "sliding_window": 32, "rms_norm_eps": 1e-6,
+                           "kv_source_layer_ids": [1], "index_source_layer_ids": [1],
+                           "candidate_source_layer_id": 2, "max_position_embeddings": 4096}}
+    a = ModelArgs.from_dict(hub)
+    assert (a.moe_inter_dim, a.n_activated_experts, a.score_func, a.route_scale, a.engram_pad_id,
+            a.n_mtp_layers) == (7, 9, "softmax", 2.5, 5, 1)
+    assert (a.dim, a.n_layers, a.n_heads, a.rope_head_dim, a.window_size, a.norm_eps, a.kv_source_layers,
+            a.index_source_layers, a.candidate_source_layer, a.max_seq_len) == \
+        (64, 3, 4, 16, 32, 1e-6, (1,), (1,), 2, 4096)
 
 
 def test_rope_frequencies_match_oracle_restatement():

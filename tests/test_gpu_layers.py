@@ -8,7 +8,7 @@
   tests/test_parity.py:736-760 (broken sink / rope inverse / sharing must move the output).
 * C2 (bf16, batch 32, 4096 compressed entries, top-512, 64 heads x 512): the decode step --
   scores within 1e-5 of the float32 contraction, top-k bit-exact given those scores,
-  attention output within 2e-2 relative.
+  attention output within the bf16 attention check (2e-2 relative plus per-head bounds).
 """
 
 from __future__ import annotations
@@ -17,7 +17,8 @@ import numpy as np
 import pytest
 import torch
 
-from common import C1, RELEASE_TOY, SEED_BASE, TOPO, args, load_stack, max_abs, model_args, rel_max_diff, to_np
+from common import (C1, RELEASE_TOY, SEED_BASE, TOPO, args, assert_attn_close, load_stack, max_abs, model_args,
+                    rel_max_diff, to_np)
 from oracle import cpu_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -133,6 +134,44 @@ def test_packed_cache_stack_equals_dense_cache(gpu, cache_format):
             assert lp.win_kv8 is None and torch.equal(lp.win_kv, ld.win_kv)
 
 
+@pytest.mark.parametrize("topology", ["topo", "release"])
+@pytest.mark.parametrize("qat", [False, True], ids=["qat-off", "qat-on"])
+def test_bf16_stack_over_default_fp32_cache(gpu, topology, qat, qat_restore):
+    """The reference's default cache dtype under a bf16 model: ModelCache(args, bsz, max_seq_len)
+    holds fp32 buffers (cache.py:29, 72; stream.py:71 builds it so) and the layer converts at
+    every cache boundary (attention.py:127, 163, 166; cache.py:67). A chunked prefill with odd
+    cuts and decode steps past the ring wrap give outputs bit-identical to the run over bf16
+    caches, and every fp32 buffer holds the bf16 run's values exactly (a bf16 value widens
+    exactly, so both runs read the same numbers)."""
+    from dsv41.cache import ModelCache
+    _qat(qat)
+    cfg = TOPO if topology == "topo" else RELEASE_TOY
+    a, st, _ = _stacks(cfg, "bf16", SEED_BASE + 7, gpu)
+    rng = np.random.default_rng(SEED_BASE + 7)
+    T = 40
+    h = rng.standard_normal((2, T, a.dim)).astype(F32)
+    dev = lambda x: torch.from_numpy(x).to(gpu).to(torch.bfloat16)   # noqa: E731
+    splits = [(0, 13), (13, 27)] + [(t, t + 1) for t in range(27, T)]
+    c32 = ModelCache(model_args(cfg), 2, a.max_seq_len, device=gpu)
+    c16 = st.make_cache(2, a.max_seq_len)
+    assert c32.layers[0].win_kv.dtype == torch.float32 and c16.layers[0].win_kv.dtype == torch.bfloat16
+    o16 = _run(st, h, c16, splits, dev)
+    o32 = _run(st, h, c32, splits, dev)
+    assert np.array_equal(o32.view(np.uint32), o16.view(np.uint32))
+    checked = 0
+    for l, (w, n) in enumerate(zip(c32.layers, c16.layers)):
+        for name in ("win_kv", "comp_kv", "index_k"):
+            x, y = getattr(w, name), getattr(n, name)
+            assert (x is None) == (y is None), (l, name)
+            if x is not None:
+                assert x.dtype == torch.float32 and torch.equal(x, y.float()), (l, name)
+                checked += 1
+        if w.comp_state is not None:
+            assert torch.equal(w.comp_state.kv_state, n.comp_state.kv_state)
+            assert torch.equal(w.comp_state.score_state, n.comp_state.score_state)
+    assert checked >= len(c32.layers) + 2 * len(a.kv_source_layers) - 1
+
+
 def test_negative_controls_move_the_output(gpu):
     a, st, _ = _stacks(TOPO, "f32", SEED_BASE + 4, gpu)
     rng = np.random.default_rng(SEED_BASE + 4)
@@ -207,14 +246,14 @@ def test_c2_decode_step(gpu):
     qr = R.rope_tail(f(t["q"]), c["rd"], rc[[c["start"]]], rs[[c["start"]]], dtype="bf16")   # q's rope, in-launch
     o = R.sparse_attn(qr, kv_all, f(t["sink"]), np.concatenate([widx, want_i], -1), c["D"] ** -0.5, dtype="bf16")
     want_o = R.rope_tail(o, c["rd"], rc[[c["start"]]], rs[[c["start"]]], inverse=True, dtype="bf16")
-    assert rel_max_diff(to_np(out), want_o) < 2e-2
+    assert_attn_close(to_np(out), want_o)
 
 
 def test_bs32_ctx64k_decode_step_sampled_rows(gpu):
     """The bench's decode workload at full size (batch 32, 65,536 tokens -> 16,384 compressed
     entries, top-512, window 128), through the fused step the bench times: sampled batch rows
     against the oracle -- scores (two-call form) within 1e-5 of max |S|, the fused selection
-    bit-exact to the oracle's top-k of the GPU scores, attention within 2e-2."""
+    bit-exact to the oracle's top-k of the GPU scores, attention within the bf16 attention check."""
     from dsv41.indexer import weight_scale
     from dsv41.layers import precompute_freqs_cis
     from dsv41.step import SparseDecodeStep
@@ -254,7 +293,7 @@ def test_bs32_ctx64k_decode_step_sampled_rows(gpu):
     qr = R.rope_tail(f(q), rd, rc[[start]], rs[[start]], dtype="bf16")
     o = R.sparse_attn(qr, kv_all, sink.cpu().numpy(), np.concatenate([widx, want_i], -1), D ** -0.5, dtype="bf16")
     want_o = R.rope_tail(o, rd, rc[[start]], rs[[start]], inverse=True, dtype="bf16")
-    assert rel_max_diff(to_np(out)[rows], want_o) < 2e-2
+    assert_attn_close(to_np(out)[rows], want_o)
 
 
 @pytest.mark.parametrize("b,nb,K,start", [

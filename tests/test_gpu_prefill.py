@@ -5,7 +5,7 @@ size-independent properties on every row.
 * C3: B=1, an 8,192-token chunk after 32,768 tokens (nb = 10,240 compressed entries at ratio 4),
   64 heads x 512 (rope 64), indexer 64 x 128, top-2,048, window 128: 2,176-entry lists per
   query. Sampled rows: scores within 1e-5 of max |S|, top-k bit-exact given those scores,
-  attention output within 2e-2 relative. Every row: the selection is a valid top-2,048 of its
+  attention output within the bf16 attention check (2e-2 relative plus per-head bounds). Every row: the selection is a valid top-2,048 of its
   scores (no unselected visible score above a selected one), ascending, offset, in range.
 * The longest list one prefill workgroup stages: 512 queries whose lists hold exactly 2,304
   entries (128 window rows + top-2,176), some of them masked (-1).
@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from common import SEED_BASE, rel_max_diff, to_np
+from common import SEED_BASE, assert_attn_close, to_np
 from oracle import cpu_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -122,8 +122,7 @@ def test_c3_chunked_prefill_full_size(gpu):
         want_i.append(wi)
     want_o = _oracle_rows(t, rows, want_i, n, prior)
     for s in rows:
-        d = rel_max_diff(to_np(out[0, s]), want_o[s])
-        assert d < 2e-2, f"output row {s}: rel {d:.3e}"
+        assert_attn_close(to_np(out[0, s]), want_o[s], f"output row {s}")
 
 
 def test_prefill_lists_at_the_workgroup_limit(gpu):
@@ -156,5 +155,4 @@ def test_prefill_lists_at_the_workgroup_limit(gpu):
     rows = (0, 1, 255, 510, 511)
     want_o = _oracle_rows(t, rows, [idx[0, s].cpu().numpy() for s in rows], n, prior)
     for s in rows:
-        d = rel_max_diff(to_np(out[0, s]), want_o[s])
-        assert d < 2e-2, f"output row {s}: rel {d:.3e}"
+        assert_attn_close(to_np(out[0, s]), want_o[s], f"output row {s}")

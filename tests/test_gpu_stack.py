@@ -7,7 +7,7 @@
   64 x 128, top-512, 40 layers): sampled rows of a window-only layer, the last index source
   (layer 36: its own queries against layer 20's keys under layer 20's candidate mask) and a
   consumer (layer 39) against the oracle -- scores within 1e-5 of max |S|, top-k bit-exact
-  given those scores, outputs within 2e-2 relative.
+  given those scores, outputs within the bf16 attention check (2e-2 relative plus per-head bounds).
 """
 
 from __future__ import annotations
@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from common import C4_TOY, RELEASE_TOY, SEED_BASE, args, load_stack, model_args, rel_max_diff, to_np
+from common import C4_TOY, RELEASE_TOY, SEED_BASE, args, assert_attn_close, load_stack, model_args, to_np
 from oracle import cpu_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -176,9 +176,9 @@ def test_stack_step_reproduces_attention_stack(gpu, topology, index_format, T):
     if index_format == "fp8":
         cache = st.make_cache(b, a.max_seq_len, cache_format="fp8")
     elif index_format in ("fp4", "packed"):
-        cache = st.make_cache(b, a.max_seq_len, "mxfp4", cache_format=index_format)
+        cache = st.make_cache(b, a.max_seq_len, index_format="mxfp4", cache_format=index_format)
     else:
-        cache = st.make_cache(b, a.max_seq_len, index_format)
+        cache = st.make_cache(b, a.max_seq_len, index_format=index_format)
     st(h[:, :T - 1], cache)
     before = _clone_cache(cache)
     recs = _record_decode(st, h[:, T - 1:], cache)
@@ -314,7 +314,7 @@ def test_c4_full_size_sampled_rows(gpu):
             o = _oracle_layer_out(a, f(ins[l]["q"][b, 0]), win_before[(l, b)], f(ins[l]["kv"][b]),
                                   comp20 if ratio else None, idx36[b, 0] if ratio else None, f(ins[l]["sink"]),
                                   sp, ratio)
-            assert rel_max_diff(to_np(outs[l][b, 0]), o) < 2e-2, f"layer {l} row {b}"
+            assert_attn_close(to_np(outs[l][b, 0]), o, f"layer {l} row {b}")
 
 
 def test_stack_step_graph_replays(gpu):
@@ -411,14 +411,23 @@ def c5_fill_cache(cache, gen):
                                        dtype=torch.int32).to(torch.uint8))
 
 
-def test_c5_fp8_block_cache_full_size_sampled_rows(gpu):
+@pytest.mark.parametrize("scorer", ["exact", "mxq"])
+def test_c5_fp8_block_cache_full_size_sampled_rows(gpu, scorer):
     """The fp8 40-layer decode step as the fp8 cache variant's configuration states it: batch 16,
     131,072-token context (32,768 compressed entries), top-1,024, compressed KV and index keys as
-    e4m3 in 32 x 32 blocks with ue8m0 scales 2^-4..2^4, dequantized in-kernel; index queries in
-    MXFP4 form, scored on the block-scaled fp4 x fp8 MFMA. Sampled rows of a window-only layer,
-    the last index source (layer 36: its queries against layer 20's keys under layer 20's
-    candidate mask, which keeps 2,048 of 4,096 blocks) and a consumer (39) against the oracle on
-    the dequantized caches: scores within 1e-5 max|S|, top-k bit-exact given them, outputs 2e-2."""
+    e4m3 in 32 x 32 blocks with ue8m0 scales 2^-4..2^4, dequantized in-kernel. Sampled rows of a
+    window-only layer, the candidate source (layer 20), the last index source (layer 36: its
+    queries against layer 20's keys under layer 20's candidate mask, which keeps 2,048 of 4,096
+    blocks) and a consumer (39) against the oracle on the dequantized caches.
+
+    scorer "exact" (the default form: bf16 queries, keys dequantized in-kernel, exact products,
+    fp32 sums): scores within 1e-5 max|S|, and the candidate mask and the top-k of layers 20 and
+    36 bit-exact against the oracle's selection over the oracle's own fp32 scores (indexer.py:
+    134-144), outputs within the bf16 attention check.
+    scorer "mxq" (opt-in: MXFP4 queries on the block-scaled fp4 x fp8 MFMA, whose sums carry a few
+    1e-5 max|S|): scores within MXQ_FP8_TOL max|S|, the selection bit-exact given its own scores,
+    and against the exact scores it may differ only by swaps among entries within that error of
+    the k-th score."""
     from dsv41 import _abi
     from dsv41.cache import ModelCache
     from dsv41.step import StackDecodeStep
@@ -429,46 +438,77 @@ def test_c5_fp8_block_cache_full_size_sampled_rows(gpu):
     c5_fill_cache(cache, gen)
     ins = c4_inputs(a, B, gen, gpu)
     ident = (torch.ones(sp + 1, 32, device=gpu), torch.zeros(sp + 1, 32, device=gpu))
-    for l, x in enumerate(ins):
-        if "index_q" in x:                   # the same fp4 values in MXFP4 form
-            x["index_q_mx"] = _abi.index_q_prep_mxfp4(x["index_q"], *ident, 64, sp)
+    if scorer == "mxq":
+        for l, x in enumerate(ins):
+            if "index_q" in x:                   # the same fp4 values in MXFP4 form
+                x["index_q_mx"] = _abi.index_q_prep_mxfp4(x["index_q"], *ident, 64, sp)
     rows = (0, 9, 15)
     layers = (0, 36, 39)
     win_before = {(l, b): to_np(cache.layers[l].win_kv[b]) for l in layers for b in rows}
     step = StackDecodeStep(a, B, sp, torch.bfloat16, gpu)
-    print("[c5] 40-layer fp8 step, B=16, nb=32768", flush=True)
+    print(f"[c5] 40-layer fp8 step, B=16, nb=32768, scorer {scorer}", flush=True)
     outs = step(cache, ins)
     torch.cuda.synchronize()
     nb = (sp + 1) // r
     lens = R.query_lens(sp, 1, r)
+    off = min(sp, a.window_size) + 1
+    K = a.index_topk
     f = lambda t: t.float().cpu().numpy()   # noqa: E731
     l20 = cache.layers[20]
     assert l20.fp8_rb == 32 and step.candidates is not None
-    got_s = to_np(_abi.indexer_score_mxq_fp8(ins[36]["index_q_mx"], ins[36]["w_raw"], ins[36]["w_scale"],
-                                             l20.index_k8[:B], l20.index_k8s[:B], 32, nb, sp, r, step.candidates))
-    # layer 20's scores again (the same kernel on the same inputs gives the same bits): the block
-    # mask the step applied is the oracle's selection over them, bit for bit
-    got20 = to_np(_abi.indexer_score_mxq_fp8(ins[20]["index_q_mx"], ins[20]["w_raw"], ins[20]["w_scale"],
-                                             l20.index_k8[:B], l20.index_k8s[:B], 32, nb, sp, r))
+    if scorer == "mxq":
+        tol = MXQ_FP8_TOL
+        score = lambda l, cand=None: to_np(_abi.indexer_score_mxq_fp8(   # noqa: E731
+            ins[l]["index_q_mx"], ins[l]["w_raw"], ins[l]["w_scale"], l20.index_k8[:B], l20.index_k8s[:B], 32, nb,
+            sp, r, cand))
+    else:
+        tol = 1e-5
+        score = lambda l, cand=None: to_np(_abi.indexer_score_fp8(   # noqa: E731
+            ins[l]["index_q"], ins[l]["w_raw"], ins[l]["w_scale"], l20.index_k8[:B], l20.index_k8s[:B], 32, nb, sp,
+            r, cand))
+    # the scores the step's kernels formed (the same kernel on the same inputs gives the same bits)
+    got20 = score(20)
+    got_s = score(36, step.candidates)
     cand_gpu = step.candidates.cpu().numpy()
+    idx20 = step.plan[20].idx.cpu().numpy()
     idx36 = step.plan[36].idx.cpu().numpy()
+    swaps = 0
     for b in rows:
         keys20 = R.dequant_fp8_cache(l20.index_k8[b:b + 1].cpu().numpy(), l20.index_k8s[b:b + 1].cpu().numpy(),
                                      32)[:, :nb]
         w20 = R.cast(f(ins[20]["w_raw"][b:b + 1]) * F32(ins[20]["w_scale"]), "bf16")
         s20 = R.indexer_scores(f(ins[20]["index_q"][b:b + 1]), keys20, w20, sp, r)
-        assert np.abs(got20[b:b + 1] - s20).max() <= MXQ_FP8_TOL * np.abs(s20).max(), f"layer 20 scores row {b}"
-        cand = R.select_candidate_blocks(got20[b:b + 1], lens, a.candidate_topk_blocks, a.candidate_block_size)
-        assert np.array_equal(cand_gpu[b:b + 1], cand), f"candidate mask row {b}"
-        assert 0 < cand.mean() < 1                           # the mask is live
+        assert np.abs(got20[b:b + 1] - s20).max() <= tol * np.abs(s20).max(), f"layer 20 scores row {b}"
+        # given the GPU's own scores the selection is always bit-exact
+        cand_own = R.select_candidate_blocks(got20[b:b + 1], lens, a.candidate_topk_blocks, a.candidate_block_size)
+        assert np.array_equal(cand_gpu[b:b + 1], cand_own), f"candidate mask row {b}"
+        assert np.array_equal(idx20[b:b + 1], R.topk_indices(got20[b:b + 1], K, lens, off)), f"layer 20 top-k {b}"
+        assert 0 < cand_own.mean() < 1                           # the mask is live
+        cand = R.select_candidate_blocks(s20, lens, a.candidate_topk_blocks, a.candidate_block_size)
         w36 = R.cast(f(ins[36]["w_raw"][b:b + 1]) * F32(ins[36]["w_scale"]), "bf16")
         want = R.indexer_scores(f(ins[36]["index_q"][b:b + 1]), keys20, w36, sp, r, cand)
         fin = np.isfinite(want)
-        assert np.array_equal(np.isfinite(got_s[b:b + 1]), fin), f"mask row {b}"
-        assert np.abs(got_s[b:b + 1][fin] - want[fin]).max() <= MXQ_FP8_TOL * np.abs(want[fin]).max(), \
-            f"scores row {b}"
-        want_i = R.topk_indices(got_s[b:b + 1], a.index_topk, lens, min(sp, a.window_size) + 1)
-        assert np.array_equal(idx36[b:b + 1], want_i), f"top-k row {b}"
+        if scorer == "exact":
+            # the reference's rule on the oracle's exact fp32 scores, bit for bit
+            assert np.array_equal(cand_gpu[b:b + 1], cand), f"candidate mask vs exact scores row {b}"
+            assert np.array_equal(idx20[b:b + 1], R.topk_indices(s20, K, lens, off)), f"layer 20 exact top-k {b}"
+        assert np.array_equal(np.isfinite(got_s[b:b + 1]), np.isfinite(R.indexer_scores(
+            f(ins[36]["index_q"][b:b + 1]), keys20, w36, sp, r, cand_own))), f"mask row {b}"
+        if np.array_equal(cand_own, cand):
+            assert np.abs(got_s[b:b + 1][fin] - want[fin]).max() <= tol * np.abs(want[fin]).max(), f"scores row {b}"
+        assert np.array_equal(idx36[b:b + 1], R.topk_indices(got_s[b:b + 1], K, lens, off)), f"top-k row {b}"
+        want_i = R.topk_indices(want, K, lens, off)
+        if scorer == "exact":
+            assert np.array_equal(idx36[b:b + 1], want_i), f"layer 36 exact top-k row {b}"
+        else:
+            got_pos = idx36[b, 0][idx36[b, 0] >= 0] - off
+            want_pos = want_i[0, 0][want_i[0, 0] >= 0] - off
+            diff = np.setxor1d(got_pos, want_pos)
+            if diff.size:
+                kth = np.sort(want[0, 0][fin[0, 0]])[::-1][K - 1]
+                band = tol * np.abs(want[fin]).max()
+                assert np.all(np.abs(want[0, 0][diff] - kth) <= 2 * band), f"layer 36 swaps beyond the error, row {b}"
+            swaps += diff.size // 2
         comp20 = R.dequant_fp8_cache(l20.comp_kv8[b:b + 1].cpu().numpy(), l20.comp_ks[b:b + 1].cpu().numpy(),
                                      32)[0, :nb]
         for l in layers:
@@ -476,4 +516,5 @@ def test_c5_fp8_block_cache_full_size_sampled_rows(gpu):
             o = _oracle_layer_out(a, f(ins[l]["q"][b, 0]), win_before[(l, b)], f(ins[l]["kv"][b]),
                                   comp20 if ratio else None, idx36[b, 0] if ratio else None, f(ins[l]["sink"]),
                                   sp, ratio)
-            assert rel_max_diff(to_np(outs[l][b, 0]), o) < 2e-2, f"layer {l} row {b}"
+            assert_attn_close(to_np(outs[l][b, 0]), o, f"layer {l} row {b}")
+    print(f"[c5] scorer {scorer}: {swaps} top-k swaps against the exact scores over {len(rows)} rows", flush=True)

@@ -711,3 +711,27 @@ def test_planted_composition_mistakes_fail_the_reference_comparison(monkeypatch,
         m = _oracle_vs_golden(name, "off")
         assert (not m["picks_equal"] or max(m["prefill"], m["decode"], m["cache"], m["scores"]) > 1e-3), \
             (name, which, m)
+
+
+@pytest.mark.parametrize("b,m,rows,window_rows", [(4, 1, 640, 128), (1, 24, 256, 128)])
+def test_bf16_attention_check_rejects_planted_mistakes_on_the_oracle(b, m, rows, window_rows):
+    """The bf16 attention check of the GPU tests (tests/common.py) rejects the oracle recomputed
+    with each planted mistake (sink zeroed, sink counted once per split, one list row dropped,
+    window read one row early) against the oracle itself, at the release data scale (q and KV
+    N(0,1)/sqrt(576), sinks N(0,1), 64 heads x 512), and accepts the oracle's own bf16 output
+    against its fp32 output. (On the GPU test's data the sink mistakes stay inside 2e-2 of
+    max |o|; the per-head bounds are what reject them there.)"""
+    from common import attn_close, attn_controls
+    rng = np.random.default_rng(99 + m)
+    h, d = 64, 512
+    s = 576 ** -0.5
+    q = R.cast(rng.standard_normal((b, m, h, d)).astype(np.float32) * s, "bf16")
+    kv = R.cast(rng.standard_normal((b, rows + 64, d)).astype(np.float32) * s, "bf16")
+    sink = rng.standard_normal(h).astype(np.float32)
+    idx = np.stack([np.stack([rng.permutation(rows + 64)[:rows] for _ in range(m)]) for _ in range(b)])
+    idx[..., :window_rows] = np.sort(idx[..., :window_rows], axis=-1)
+    idx = idx.astype(np.int32)
+    want = R.sparse_attn(q, kv, sink, idx, d ** -0.5)
+    assert attn_close(R.sparse_attn(q, kv, sink, idx, d ** -0.5, dtype="bf16"), want)
+    for name, ix, sk in attn_controls(idx, sink, window_rows):
+        assert not attn_close(R.sparse_attn(q, kv, sk, ix, d ** -0.5), want), name
