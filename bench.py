@@ -51,6 +51,7 @@ def parse():
     p.add_argument("--no-c4", action="store_true", help="skip the 40-layer decode line")
     p.add_argument("--no-mx", action="store_true", help="skip the MXFP4-index decode line")
     p.add_argument("--no-wo-a", action="store_true", help="skip the grouped output-LoRA line")
+    p.add_argument("--no-token", action="store_true", help="skip the caller-path decode token line")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--eager", action="store_true",
                    help="launch the decode kernels without HIP graphs (for counter-collecting profilers)")
@@ -444,7 +445,10 @@ def run_wo_a(torch, device):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps * 1e3     # us
 
-    out = {"workload": "grouped wo_a: 8 groups x (4096 -> 1024), bf16 in, fp32 sums, bf16 out", "lines": {}}
+    out = {"workload": "grouped wo_a: 8 groups x (4096 -> 1024), bf16 in, fp32 sums, bf16 out; then wo_b "
+                       "(8192 -> 5120, torch linear = hipBLASLt)", "lines": {}}
+    dim = 5120
+    wb = (torch.randn(dim, G * R, generator=g, device=device) * 0.02).to(bf)
     for rows in (32, 64, 8192):
         o = torch.randn(rows, G * d, generator=g, device=device).to(bf)
         y = torch.empty(rows, G * R, dtype=bf, device=device)
@@ -452,19 +456,33 @@ def run_wo_a(torch, device):
         ob = o.view(rows, G, d).transpose(0, 1).contiguous()
         ours = lambda: _abi.wo_a_grouped(o, w, G, out=y)   # noqa: E731
         lib = lambda: torch.bmm(ob, wT)                      # noqa: E731
-        # the engine clock ramps up under the first heavy launches: warm both, then time each
-        # twice, alternating, and keep the faster pass of each
-        timed(ours, reps), timed(lib, reps)
-        us, us_bmm = timed(ours, reps), timed(lib, reps)
-        us, us_bmm = min(us, timed(ours, reps)), min(us_bmm, timed(lib, reps))
+        lin_b = lambda: torch.nn.functional.linear(y, wb)    # noqa: E731
+        both = lambda: torch.nn.functional.linear(_abi.wo_a_grouped(o, w, G, out=y), wb)   # noqa: E731
+        # the engine clock ramps up under the first heavy launches: warm every form, then time
+        # each twice, alternating, and keep the faster pass of each
+        fns = (ours, lib, lin_b, both)
+        for fn in fns:
+            timed(fn, reps)
+        t = [timed(fn, reps) for fn in fns]
+        t = [min(x, timed(fn, reps)) for x, fn in zip(t, fns)]
+        us, us_bmm, us_b, us_ab = t
+        b_bytes = (dim * G * R + rows * G * R + rows * dim) * 2
+        b_flops = 2.0 * rows * dim * G * R
         nbytes = (G * R * d + rows * G * d + rows * G * R) * 2
         flops = 2.0 * rows * G * R * d
         line = {"us": us, "GBps": nbytes / us / 1e3, "hbm_frac": nbytes / us / 1e3 / HBM_PEAK_GBS,
                 "TFLOPs": flops / us / 1e6, "mfma_frac": flops / us / 1e6 / BF16_PEAK_TFLOPS,
-                "algorithmic_bytes": nbytes, "flops": flops, "hipblaslt_bmm_pre_transposed_us": us_bmm}
+                "algorithmic_bytes": nbytes, "flops": flops, "hipblaslt_bmm_pre_transposed_us": us_bmm,
+                # wo_b as the attention runs it (torch linear: hipBLASLt), alone and after wo_a; a
+                # fused pair would save at most the intermediate's write and read
+                "wo_b_us": us_b, "wo_b_GBps": b_bytes / us_b / 1e3, "wo_b_hbm_frac": b_bytes / us_b / 1e3 / HBM_PEAK_GBS,
+                "wo_b_TFLOPs": b_flops / us_b / 1e6, "wo_b_mfma_frac": b_flops / us_b / 1e6 / BF16_PEAK_TFLOPS,
+                "wo_b_algorithmic_bytes": b_bytes, "wo_a_then_wo_b_us": us_ab,
+                "intermediate_bytes_frac": 2 * rows * G * R * 2 / (nbytes + b_bytes)}
         out["lines"][str(rows)] = line
         log(f"[bench] wo_a rows={rows}: {us:.1f} us ({line['GBps']:.0f} GB/s, {line['TFLOPs']:.0f} TFLOP/s), "
-            f"hipBLASLt bmm on transposed copies {us_bmm:.1f} us")
+            f"hipBLASLt bmm on transposed copies {us_bmm:.1f} us; wo_b {us_b:.1f} us "
+            f"({line['wo_b_GBps']:.0f} GB/s), wo_a then wo_b {us_ab:.1f} us")
         del o, y, ob
     return out
 
@@ -646,6 +664,44 @@ def c4_step_bytes(a, B, start_pos, index_format="dense", mx_query=None):
     return int(total)
 
 
+def c4_fill(cache, g, device, torch):
+    """Random rows in every buffer of a stack cache, whatever its format: dense rows N(0, 1/576),
+    index keys on the fp4 grid, packed codes without the NaN patterns and scales in the ranges
+    the kernels meet in use."""
+    from dsv41 import _abi
+    sc = 576 ** -0.5
+
+    def rbytes(lo, hi, *shape):
+        return torch.randint(lo, hi, shape, generator=g, device=device, dtype=torch.int32).to(torch.uint8)
+
+    for lc in cache.layers:
+        for t in (lc.win_kv, lc.comp_kv):
+            if t is not None:
+                t.copy_(torch.randn(t.shape, generator=g, device=device) * sc)
+        if lc.index_k is not None:
+            lc.index_k.copy_(torch.randn(lc.index_k.shape, generator=g, device=device))
+            _abi.fq_fp4_ue8m0(lc.index_k, out=lc.index_k)
+        if lc.index_k4 is not None:
+            lc.index_k4.copy_(rbytes(0, 256, *lc.index_k4.shape))
+            lc.index_ks.copy_(rbytes(123, 132, *lc.index_ks.shape))
+        if lc.win_kv8 is not None:                 # e4m3 codes without the NaN patterns, ue8m0 2^-9 .. 2^-6
+            B, W, R = lc.win_kv8.shape             # rows of D codes then D / 32 scale bytes
+            D = R * 32 // 33
+            c = rbytes(0, 256, B, W, D)
+            lc.win_kv8[..., :D].copy_(torch.where((c & 0x7F) == 0x7F, c ^ 1, c))
+            lc.win_kv8[..., D:].copy_(rbytes(118, 122, B, W, D // 32))
+        if lc.comp_kv4 is not None:                # e2m1 codes, e4m3 scales 2^-6 .. 2^-2
+            B, n, R = lc.comp_kv4.shape            # rows of D / 2 code bytes then D / 16 scale bytes
+            D = R * 16 // 9
+            lc.comp_kv4[..., :D // 2].copy_(rbytes(0, 256, B, n, D // 2))
+            lc.comp_kv4[..., D // 2:].copy_(rbytes(0x08, 0x28, B, n, D // 16))
+        for codes, scales in ((lc.comp_kv8, lc.comp_ks), (lc.index_k8, lc.index_k8s)):
+            if codes is not None:                  # e4m3 codes without the two NaN patterns
+                c = rbytes(0, 256, *codes.shape)
+                codes.copy_(torch.where((c & 0x7F) == 0x7F, c ^ 1, c))
+                scales.copy_(rbytes(123, 132, *scales.shape))
+
+
 def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=512, mxq=False):
     """C4: one decode token through the 40-layer stack at batch 64 and 65,536 tokens of context
     (16,384 compressed entries per sequence), kernels only: window writes, owner latent / key
@@ -681,28 +737,7 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
     def rbytes(lo, hi, *shape):
         return torch.randint(lo, hi, shape, generator=g, device=device, dtype=torch.int32).to(torch.uint8)
 
-    for lc in cache.layers:
-        for t in (lc.win_kv, lc.comp_kv):
-            if t is not None:
-                t.copy_(torch.randn(t.shape, generator=g, device=device) * sc)
-        if lc.index_k is not None:
-            lc.index_k.copy_(torch.randn(lc.index_k.shape, generator=g, device=device))
-            _abi.fq_fp4_ue8m0(lc.index_k, out=lc.index_k)
-        if lc.index_k4 is not None:
-            lc.index_k4.copy_(rbytes(0, 256, *lc.index_k4.shape))
-            lc.index_ks.copy_(rbytes(123, 132, *lc.index_ks.shape))
-        if lc.win_kv8 is not None:                 # e4m3 codes without the NaN patterns, ue8m0 2^-9 .. 2^-6
-            c = rbytes(0, 256, B, W, D)
-            lc.win_kv8[..., :D].copy_(torch.where((c & 0x7F) == 0x7F, c ^ 1, c))
-            lc.win_kv8[..., D:].copy_(rbytes(118, 122, B, W, D // 32))
-        if lc.comp_kv4 is not None:                # e2m1 codes, e4m3 scales 2^-6 .. 2^-2
-            lc.comp_kv4[..., :D // 2].copy_(rbytes(0, 256, B, lc.comp_kv4.shape[1], D // 2))
-            lc.comp_kv4[..., D // 2:].copy_(rbytes(0x08, 0x28, B, lc.comp_kv4.shape[1], D // 16))
-        for codes, scales in ((lc.comp_kv8, lc.comp_ks), (lc.index_k8, lc.index_k8s)):
-            if codes is not None:                  # e4m3 codes without the two NaN patterns
-                c = rbytes(0, 256, *codes.shape)
-                codes.copy_(torch.where((c & 0x7F) == 0x7F, c ^ 1, c))
-                scales.copy_(rbytes(123, 132, *scales.shape))
+    c4_fill(cache, g, device, torch)
     rn = lambda *shape: torch.randn(*shape, generator=g, device=device)   # noqa: E731
     ins = []
     for l in range(a.n_layers):
@@ -752,6 +787,66 @@ def run_c4(args, torch, device, index_format="dense", B=64, start=65535, topk=51
                                       else f"index caches {index_format}"),
         "step_ms": ms, "tokens_per_s": B / (ms * 1e-3), "steps": reps,
         "step_algorithmic_bytes": nbytes, "hbm_GBps_step": gbs, "hbm_frac_step": gbs / HBM_PEAK_GBS,
+    }
+
+
+def run_token(args, torch, device, B=64, start=65535):
+    """One decode token as callers run it: AttentionStack.forward, i.e. model.py:141-154's layer
+    loop with attention.py:106-179 in every layer (q and kv projections with their norms, the
+    window-KV prologue, compressor and indexer at their layers, top-k, sparse MLA, grouped wo_a,
+    wo_b, the residual add), MoE and hyper-connections as identity. 40 layers with C4's sharing
+    layout at the release's widths (dim 5120, q LoRA 1280, 64 x 512 heads, indexer 64 x 128,
+    8 x 1024 output LoRA), bf16 weights (torch's default init) and bf16 caches of random rows,
+    B=64 at 65,536 tokens of context. The token is timed eagerly (Python issuing every launch, as
+    the reference's generate loop runs it) and replayed from one HIP graph captured at position
+    65,535; every call rewrites that position's ring slot, latent and key."""
+    from dsv41.model import AttentionStack
+
+    a = c4_model_args(max_seq_len=start + 1)
+    bf = torch.bfloat16
+    log(f"[bench] decode token through AttentionStack: B={B} start_pos={start}, release widths")
+    torch.manual_seed(SEED + 400)
+    stack = AttentionStack(a, bf, device)
+    g = torch.Generator(device=device).manual_seed(SEED + 401)
+    for attn in stack.layers:
+        attn.attn_sink.copy_(torch.randn(a.n_heads, generator=g, device=device))
+    cache = stack.make_cache(B, start + 1)
+    c4_fill(cache, g, device, torch)
+    h = torch.randn(B, 1, a.dim, generator=g, device=device).to(bf)
+
+    def token(_):
+        cache.offset = start
+        return stack(h, cache)
+
+    reps = max(4, args.steps // 20)
+    for _ in range(2):
+        token(None)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        token(None)
+    e1.record()
+    torch.cuda.synchronize()
+    eager_ms = e0.elapsed_time(e1) / reps
+    gr = graph_of(token, [None], torch)
+    for _ in range(2):
+        gr.replay()
+    ms = time_graph(gr, reps, torch)
+    weight_bytes = sum(p.numel() * p.element_size() for p in stack.parameters())
+    cache_bytes = c4_step_bytes(a, B, start)
+    nbytes = weight_bytes + cache_bytes
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] decode token {ms:.3f} ms graph-replayed, {eager_ms:.3f} ms eager, {gbs:.0f} GB/s")
+    del gr, stack, cache
+    return {
+        "workload": f"one decode token through AttentionStack (40 layers, C4 sharing layout, release widths: "
+                    f"dim {a.dim}, q LoRA {a.q_lora_rank}, {a.n_heads} x {a.head_dim} heads, indexer "
+                    f"{a.index_n_heads} x {a.index_head_dim}, wo_a {a.o_groups} x {a.o_lora_rank}), B={B}, "
+                    f"{start + 1}-token context, bf16 weights and caches; projections are torch GEMMs",
+        "token_ms": ms, "token_ms_eager": eager_ms, "tokens_per_s": B / (ms * 1e-3), "steps": reps,
+        "weight_bytes": weight_bytes, "cache_algorithmic_bytes": cache_bytes,
+        "token_algorithmic_bytes": nbytes, "hbm_GBps_token": gbs, "hbm_frac_token": gbs / HBM_PEAK_GBS,
     }
 
 
@@ -953,6 +1048,12 @@ def main():
                 except Exception as e:
                     result["c5_stack_decode_fp8_mxq_opt_in"] = {"error": repr(e)}
                 torch.cuda.empty_cache()
+    if not args.no_token and not args.eager:
+        try:
+            result["decode_token_stack"] = run_token(args, torch, device)
+        except Exception as e:
+            result["decode_token_stack"] = {"error": repr(e)}
+        torch.cuda.empty_cache()
     if not args.no_cpu:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(s, sets, cos, sin, ws, args.cpu_seconds, torch)

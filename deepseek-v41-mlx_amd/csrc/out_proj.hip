@@ -6,22 +6,22 @@
 // [groups*r, d] (bf16, unquantized), out [rows, groups*r]. The reference computes the einsum on
 // fp32 copies of both and casts the result to the activation dtype before wo_b. Here every
 // product of two bf16 values is exact in the MFMA and the sums are fp32 (the MFMA's own
-// accumulation, then a fixed-order sum of per-wave partials), so the result differs from the
-// reference's only in the order of the fp32 additions; the bf16 output is the fp32 value rounded
-// to nearest even once, as astype does.
+// accumulation over the channels in order), so the result differs from the reference's only in the
+// order of the fp32 additions; the bf16 output is the fp32 value rounded to nearest even once, as
+// astype does.
 //
 // Launch shapes (bf16 o and wo_a with d a multiple of 512 and r of 128 -- the release's 4096 and
-// 1024 -- take the MFMA kernels; other shapes and fp32 activations take a plain fp32 kernel):
-//   few rows (decode, <= 128): the kernel streams wo_a from HBM once. A workgroup owns 32
-//     weight rows of one group and all query rows; its four waves split the d channels four ways
-//     (each a quarter of the contraction, loads double-buffered in registers) and their partial
-//     sums meet in LDS in a fixed order. groups * r / 32 workgroups (256 for 8 x 1024), the
-//     group index fastest so that one group's workgroups share an XCD and its L2 copy of o.
-//   many rows (prefill): 256 x 256 output tiles (weight rows x query rows) over 64-channel
-//     steps, both operand tiles copied global -> LDS (global_load_lds_dwordx4, double-buffered)
-//     in an XOR-swizzled layout that the MFMA fragment reads take without bank conflicts; eight
-//     waves of 128 x 64 each, two per SIMD (128 x 128 tiles of four 64 x 64 waves when r is not
-//     a multiple of 256).
+// 1024 -- take the MFMA kernel; other shapes and fp32 activations take a plain fp32 kernel). Both
+// operand tiles are copied global -> LDS (global_load_lds_dwordx4) over 64-channel steps in an
+// XOR-swizzled layout that the MFMA fragment reads take without bank conflicts:
+//   decode (rows <= 128): the weight is streamed from HBM once. A workgroup owns 32 weight rows
+//     of one group and every query row (32-row tiles); its four waves each own a 16 x 32 or
+//     16 x 16 block of the output, and the copies run eight steps ahead (a 64-128 KB ring), which
+//     is what keeps enough of the stream in flight: 256 workgroups for 8 x 1024, one per CU, the
+//     workgroups of one group on one XCD so that they share its L2 copy of o.
+//   prefill: 256 x 256 output tiles (weight rows x query rows), double-buffered; eight waves of
+//     128 x 64 each, two per SIMD (128 x 128 tiles of four 64 x 64 waves when r is not a
+//     multiple of 256).
 #include "mfma.h"
 
 namespace dsv41 {
@@ -68,88 +68,7 @@ __device__ __forceinline__ void store4<float>(float* p, f32x4 v) {
   *reinterpret_cast<f32x4*>(p) = v;
 }
 
-// ------------------------------------------------------------------ few rows
-
-constexpr int kSkRows = 32;   // weight rows per workgroup
-
-// MT 16-row tiles of query rows. The MFMA's A operand is a 16-row weight tile and its B operand
-// a 16-row query tile, so lane (l16, g) receives out[query 16 mt + l16][weight rows 4g .. 4g + 3]:
-// four consecutive outputs of one row.
-template <int MT, typename TO>
-__global__ __launch_bounds__(256) void wo_a_rows_kernel(WoaArgs a) {
-  constexpr int U = MT <= 4 ? 4 : 2;     // 32-channel steps per load batch
-  constexpr int CH = 32 * U;
-  __shared__ __align__(16) f32x4 red[4][MT * 2][64];
-  const int grp = blockIdx.x % a.groups, rt = blockIdx.x / a.groups;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
-  const int kw = a.d >> 2, k0 = wave * kw;        // this wave's quarter of the channels
-  const bf16_t* w0 = a.w + ((int64_t)grp * a.r + rt * kSkRows + l16) * a.d + k0 + 8 * g;
-  const bf16_t* w1 = w0 + 16 * (int64_t)a.d;
-  const bf16_t* op[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = min(16 * mt + l16, a.rows - 1);   // rows past the end repeat the last (not stored)
-    op[mt] = a.o + (int64_t)m * a.groups * a.d + (int64_t)grp * a.d + k0 + 8 * g;
-  }
-  f32x4 acc[MT][2];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  bf16x8 wa[2][U][2], ob[2][U][MT];
-  auto load = [&](bf16x8 (&wv)[U][2], bf16x8 (&ov)[U][MT], int k) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      wv[u][0] = ld_bf16x8(w0 + k + 32 * u);
-      wv[u][1] = ld_bf16x8(w1 + k + 32 * u);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) ov[u][mt] = ld_bf16x8(op[mt] + k + 32 * u);
-    }
-  };
-  auto mma = [&](const bf16x8 (&wv)[U][2], const bf16x8 (&ov)[U][MT]) {
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        acc[mt][0] = mfma16x16x32(wv[u][0], ov[u][mt], acc[mt][0]);
-        acc[mt][1] = mfma16x16x32(wv[u][1], ov[u][mt], acc[mt][1]);
-      }
-  };
-  // Two register buffers: the next batch is in flight while this one multiplies. Every path
-  // issues the same loads (the batch after the last re-reads the last), so the compiler's
-  // wait counts stay exact.
-  const int steps = kw / CH;
-  load(wa[0], ob[0], 0);
-  int s = 0;
-  for (; s + 2 <= steps; s += 2) {
-    load(wa[1], ob[1], (s + 1) * CH);
-    mma(wa[0], ob[0]);
-    load(wa[0], ob[0], min(s + 2, steps - 1) * CH);
-    mma(wa[1], ob[1]);
-  }
-  if (s < steps) mma(wa[0], ob[0]);
-
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    red[wave][mt * 2][lane] = acc[mt][0];
-    red[wave][mt * 2 + 1][lane] = acc[mt][1];
-  }
-  __syncthreads();
-  const int64_t ostride = (int64_t)a.groups * a.r;
-  TO* out = reinterpret_cast<TO*>(a.out);
-  for (int tile = wave; tile < MT * 2; tile += 4) {
-    const int mt = tile >> 1, t = tile & 1;
-    const int m = 16 * mt + l16;
-    f32x4 v = red[0][tile][lane];
-#pragma unroll
-    for (int p = 1; p < 4; ++p) {
-      const f32x4 q = red[p][tile][lane];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = v[e] + q[e];
-    }
-    if (m < a.rows) store4<TO>(out + m * ostride + (int64_t)grp * a.r + rt * kSkRows + 16 * t + 4 * g, v);
-  }
-}
-
-// ------------------------------------------------------------------ many rows
+// ------------------------------------------------------------------ tiled (every row count)
 
 constexpr int kTileR = 128;   // weight rows of the smallest output tile (r is a multiple of it)
 constexpr int kWideR = 256;   // weight rows of the large tile
@@ -180,6 +99,22 @@ struct TileCfg {
   static_assert(BK == 32 || BK == 64, "32- or 64-channel steps");
   static_assert(NW * 1024 * NWV == TR * RB && NO * 1024 * NWV == TM * RB, "whole copy instructions per wave");
 };
+
+// The same for deep rings: at most `pending` (clamped to P) later steps of N copies each may
+// stay in flight; N * P stays within the 6-bit vmcnt field.
+template <int N, int P>
+__device__ __forceinline__ void wait_copies_deep(int pending) {
+  static_assert(N * P <= 63, "vmcnt holds 6 bits");
+  if constexpr (P > 0) {
+    if (pending >= P) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N * P) : "memory");
+      return;
+    }
+    wait_copies_deep<N, P - 1>(pending);
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+}
 
 template <int N>
 __device__ __forceinline__ void wait_copies(int pending) {
@@ -263,7 +198,8 @@ __global__ __launch_bounds__(64 * GR * GM, (TileCfg<WR, WM, GR, GM, BK, NS>::LDS
   for (int p = 0; p < NS - 1; ++p)
     if (p < nk) issue(p, p * BK);
   for (int kt = 0; kt < nk; ++kt) {
-    wait_copies<C::NW + C::NO>(min(NS - 2, nk - 1 - kt));   // this wave's copies of step kt landed
+    if constexpr (NS <= 4) wait_copies<C::NW + C::NO>(min(NS - 2, nk - 1 - kt));   // this wave's copies of step kt landed
+    else wait_copies_deep<C::NW + C::NO, NS - 2>(min(NS - 2, nk - 1 - kt));
     __syncthreads();
     if (kt + NS - 1 < nk) issue((kt + NS - 1) % NS, (kt + NS - 1) * BK);
     const uint8_t* wt = lds + (kt % NS) * C::STAGE;
@@ -303,17 +239,14 @@ static void launch_tiles(const WoaArgs& a, hipStream_t stream) {
 
 template <typename TO>
 static void launch_wo_a(const WoaArgs& a, hipStream_t stream) {
+  // decode: 32 weight rows x every query row per workgroup (groups * r / 32 workgroups), an
+  // eight-stage copy ring (four at 128 rows, whose stage is 20 KB)
   if (a.rows <= 128) {
-    const dim3 grid((unsigned)(a.groups * (a.r / kSkRows)));
-    switch ((a.rows + 15) / 16) {
-      case 1: hipLaunchKernelGGL((wo_a_rows_kernel<1, TO>), grid, dim3(256), 0, stream, a); break;
-      case 2: hipLaunchKernelGGL((wo_a_rows_kernel<2, TO>), grid, dim3(256), 0, stream, a); break;
-      case 3: hipLaunchKernelGGL((wo_a_rows_kernel<3, TO>), grid, dim3(256), 0, stream, a); break;
-      case 4: hipLaunchKernelGGL((wo_a_rows_kernel<4, TO>), grid, dim3(256), 0, stream, a); break;
-      case 5: hipLaunchKernelGGL((wo_a_rows_kernel<5, TO>), grid, dim3(256), 0, stream, a); break;
-      case 6: hipLaunchKernelGGL((wo_a_rows_kernel<6, TO>), grid, dim3(256), 0, stream, a); break;
-      case 7: hipLaunchKernelGGL((wo_a_rows_kernel<7, TO>), grid, dim3(256), 0, stream, a); break;
-      default: hipLaunchKernelGGL((wo_a_rows_kernel<8, TO>), grid, dim3(256), 0, stream, a); break;
+    switch ((a.rows + 31) / 32) {
+      case 1: launch_tiles<1, 1, 2, 2, 64, 8, TO>(a, stream); break;
+      case 2: launch_tiles<1, 2, 2, 2, 64, 8, TO>(a, stream); break;
+      case 3: launch_tiles<1, 3, 2, 2, 64, 8, TO>(a, stream); break;
+      default: launch_tiles<1, 4, 2, 2, 64, 4, TO>(a, stream); break;
     }
     return;
   }

@@ -1248,7 +1248,9 @@ def test_indexer_topk_mxq_fp8_equals_two_calls(gpu, b, n, h, nb, topk, start, rb
     (32, 8, 4096, 1024, "bf16"),      # bs32 decode
     (37, 8, 4096, 1024, "bf16"),      # a partial 16-row tile
     (64, 8, 4096, 1024, "bf16"),
-    (100, 2, 512, 128, "bf16"),       # the 8-tile row kernel, a partial tile
+    (70, 8, 4096, 1024, "bf16"),      # three 32-row query tiles, a partial one
+    (100, 2, 512, 128, "bf16"),       # four 32-row query tiles, a partial one
+    (64, 1, 5120, 1280, "bf16"),      # one group: a dense projection's shape
     (128, 8, 4096, 1024, "bf16"),
     (129, 8, 4096, 1024, "bf16"),     # the tiled kernel, a partial 256-row query tile
     (257, 8, 4096, 1024, "bf16"),     # one row in the second 256-row query tile
