@@ -155,18 +155,18 @@ __device__ __forceinline__ float sum_bf16x2(uint32_t u) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // 8 e4m3fn codes (two dwords, channel i in byte i) times a power-of-two scale -> MFMA operand.
-// v_cvt_scalef32_pk_f32_fp8 decodes two OCP e4m3fn codes (subnormals included) and applies the
+// v_cvt_scalef32_pk_bf16_fp8 decodes two OCP e4m3fn codes (subnormals included), applies the
 // scale's exponent -- all of a normal power of two (2^-126 .. 2^127), which the ue8m0 scales of
-// the fp8 caches (bytes 1..254) are. Exact: e4m3 values scaled by 2^k are bf16-representable
-// within bf16's exponent range.
+// the fp8 caches (bytes 1..254) are -- and packs the two bf16 results: one instruction per two
+// channels (decoding to fp32 and packing separately took two). Exact: e4m3 values scaled by 2^k
+// are bf16-representable within bf16's exponent range.
 __device__ __forceinline__ bf16x8 dequant_e4m3x8(uint32_t lo, uint32_t hi, float scale) {
-  typedef __attribute__((ext_vector_type(2))) float f2;
-  const f2 a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, scale, false);
-  const f2 b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, scale, true);
-  const f2 c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, scale, false);
-  const f2 d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, scale, true);
-  const float v[8] = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-  return cvt_bf16x8(v);
+  typedef __attribute__((ext_vector_type(2))) __bf16 b2;
+  const b2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, scale, false);
+  const b2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, scale, true);
+  const b2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, scale, false);
+  const b2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, scale, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
 // 8 e2m1 codes (one dword; channel 2p in the low nibble of byte p) times an e4m3 block scale ->

@@ -256,6 +256,67 @@ __device__ __forceinline__ void dequant_rows(uint8_t* sb, const uint8_t* kind, i
   }
 }
 
+// Global address space: plain loads through such pointers are global_load (vmcnt only), where a
+// generic pointer's flat_load would also hold lgkmcnt and so every LDS wait behind it.
+#define GLOBAL __attribute__((address_space(1)))
+
+// The register path of the two-slot decode ring (mla_bf16_kernel with NS = 2) for packed rows:
+// instead of copying a packed row into LDS, reading it back and writing its bf16 form (~2x the
+// LDS traffic of a bf16 row), lane l loads the row's bytes for channels 8l..8l+7 and their scale
+// byte into registers when the step is issued; bf16 rows keep their LDS copies. raw/sb hold the
+// wave's RPW rows of the next step, valid for the rows whose kind is 2 or 3.
+template <int D, int CF, int RPW>
+__device__ __forceinline__ void gather_rows_reg(uint64_t mp, uint8_t* kind, uint32_t dst, int lane, const PackedBase& pb,
+                                                uint2 (&raw)[RPW], uint32_t (&sb)[RPW]) {
+  using F = CacheFmt<CF>;
+  constexpr int RS = RowLayout<D, false>::RS;
+  static_assert(D == 512, "packed rows: 512 channels, 8 per lane");
+  if (lane < RPW) kind[lane] = mp != 0ull ? (uint8_t)(1u + ((uint32_t)mp & 3u)) : 0;
+  const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    const uint64_t ent = lane_u64(lo, hi, rr);
+    const uint32_t tag = (uint32_t)ent & 3u;
+    if (F::F8 && tag == 1u) {           // e4m3 codes 8l..8l+7 and the ue8m0 scale of block l/4
+      const uint64_t ci = ent >> 2;
+      const uint64_t v = *reinterpret_cast<const GLOBAL uint64_t*>(pb.comp8 + ci * D + (uint64_t)lane * 8u);
+      raw[rr] = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+      sb[rr] = *reinterpret_cast<const GLOBAL uint8_t*>(pb.scal8 + (ci >> pb.rbs) * (D / 32) + (uint64_t)(lane >> 2));
+    } else if (F::F4 && tag == 1u) {    // e2m1 code bytes 4l..4l+3 and the e4m3 scale of block l/2
+      const uint64_t row = pb.comp8 + (ent >> 2) * F::F4ROW;
+      raw[rr].x = *reinterpret_cast<const GLOBAL uint32_t*>(row + (uint64_t)lane * 4u);
+      sb[rr] = *reinterpret_cast<const GLOBAL uint8_t*>(row + D / 2 + (uint64_t)(lane >> 1));
+    } else if (F::W8 && tag == 2u) {    // MXFP8 ring row: codes, then 16 ue8m0 scales
+      const uint64_t row = pb.ring8 + (ent >> 2) * F::W8ROW;
+      const uint64_t v = *reinterpret_cast<const GLOBAL uint64_t*>(row + (uint64_t)lane * 8u);
+      raw[rr] = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+      sb[rr] = *reinterpret_cast<const GLOBAL uint8_t*>(row + D + (uint64_t)(lane >> 2));
+    } else {
+      dma_row<D>(ent, dst + rr * RS, lane);
+    }
+  }
+}
+
+// The step's loads have landed: this wave writes its packed rows to LDS as bf16 (lane l: its
+// 16-byte chunk of each row). The kinds come back as wave-uniform words, as in dequant_rows.
+template <int D, int CF, int RPW>
+__device__ __forceinline__ void store_rows_reg(uint8_t* sbase, const uint8_t* kind, int lane, const uint2 (&raw)[RPW],
+                                               const uint32_t (&sb)[RPW]) {
+  using F = CacheFmt<CF>;
+  constexpr int RS = RowLayout<D, false>::RS;
+  const uint32_t* kw = reinterpret_cast<const uint32_t*>(kind);
+  uint32_t kinds[RPW / 4];
+#pragma unroll
+  for (int w4 = 0; w4 < RPW / 4; ++w4) kinds[w4] = (uint32_t)__builtin_amdgcn_readfirstlane((int)kw[w4]);
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    const uint32_t k = (kinds[rr / 4] >> (8 * (rr % 4))) & 0xFFu;
+    bf16x8* out = reinterpret_cast<bf16x8*>(sbase + rr * RS + lane * 16);
+    if (F::F4 && k == 2u) *out = dequant_e2m1x8(raw[rr].x, __builtin_amdgcn_cvt_f32_fp8((int)sb[rr], 0));
+    else if (k >= 2u) *out = dequant_e4m3x8(raw[rr].x, raw[rr].y, e8m0_to_float(sb[rr]));
+  }
+}
+
 template <int D, int HT, int DS, int CF, bool PAIR>
 __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   constexpr bool W8 = CacheFmt<CF>::W8, PACKED = CacheFmt<CF>::PACKED;
@@ -305,12 +366,18 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   const int nsteps = (cnt + R - 1) / R;
   const uint32_t ring_base = lds_offset(ring);
   const PackedBase pbase = packed_base<CF>(S, b);
+  // packed rows through registers: with two slots every step waits for all its loads (vmcnt 0),
+  // so plain loads and the bf16 rows' LDS copies need no separate counts
+  constexpr bool REG = PACKED && NS == 2;
+  uint2 praw[RPW];
+  uint32_t psb[RPW];
   auto issue = [&](int t, bool direct) {
     const int slot = t % NS;
     const int mine = t * R + wave * RPW + (lane % RPW);
     const uint64_t mp = mine < cnt ? (direct ? entry_row(mine) : rows[mine]) : 0ull;
     const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_base + (uint32_t)(slot * SLOT + wave * RPW * RS));
-    gather_rows<D, CF, RPW, false>(mp, &vrow[slot][wave * RPW], dst, lane, pbase, 0);
+    if constexpr (REG) gather_rows_reg<D, CF, RPW>(mp, &vrow[slot][wave * RPW], dst, lane, pbase, praw, psb);
+    else gather_rows<D, CF, RPW, false>(mp, &vrow[slot][wave * RPW], dst, lane, pbase, 0);
   };
   const int h = hg * (HT * 16) + ht * 16 + l16;
   const bool hok = h < a.heads;
@@ -356,8 +423,13 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   for (int t = early ? 1 : 0; t < nsteps && t < NS - 1; ++t) issue(t, false);
 
   for (int t = 0; t < nsteps; ++t) {
-    wait_steps<NL>(min(nsteps - 1 - t, NS - 2));
-    if constexpr (PACKED)   // this wave's own packed rows of step t have landed
+    // REG: the same wait (two slots: vmcnt 0) as the builtin, so that the wait-count pass knows
+    // the row registers have landed and adds no waits of its own where the next step reloads them
+    if constexpr (REG) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    else wait_steps<NL>(min(nsteps - 1 - t, NS - 2));
+    if constexpr (REG)   // this wave's packed rows of step t are in registers
+      store_rows_reg<D, CF, RPW>(ring + (t % NS) * SLOT + wave * RPW * RS, &vrow[t % NS][wave * RPW], lane, praw, psb);
+    else if constexpr (PACKED)   // this wave's own packed rows of step t have landed
       dequant_rows<D, CF, RPW, false>(ring + (t % NS) * SLOT + wave * RPW * RS, &vrow[t % NS][wave * RPW], lane, 0);
     __syncthreads();                       // step t landed; every wave is done with step t-1
     const int slot = t % NS;
