@@ -88,12 +88,14 @@ __device__ __forceinline__ void dma_row(uint64_t p, uint32_t dst, int lane) {
   }
 }
 
+constexpr int kRopeRowPairs = 128;   // q rope pairs (rd / 2) staged in LDS by the decode kernel
+
 template <int D, int NW, int ML, int BUDGET>
 struct MlaLds {
   static constexpr int RS = D * 2 + 16;                   // padded row stride (bytes)
   static constexpr int SLOT = kStepRows * RS;
   static constexpr int XS = NW * 2 * 64 * 16;             // partial-score exchange
-  static constexpr int FIXED = XS + ML * 8 + kMaxRing * kStepRows + 256;
+  static constexpr int FIXED = XS + ML * 8 + kMaxRing * kStepRows + 2 * kRopeRowPairs * 4 + 256;
   static constexpr int NS = (BUDGET - FIXED) / SLOT < kMaxRing ? (BUDGET - FIXED) / SLOT : kMaxRing;
   static_assert(NS >= 2, "ring needs two slots");
 };
@@ -336,6 +338,7 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   __shared__ __align__(16) f32x4 xs[NW][2][64];
   __shared__ uint64_t rows[ML];                 // resolved row addresses, 0 = masked
   __shared__ __align__(4) uint8_t vrow[NS][R];
+  __shared__ float rope_cs[2][kRopeRowPairs];   // the query position's (cos, sin) row of the q rope
 
   const KvSrc& S = a.src;
   const int tile = xcd_tile(blockIdx.x, gridDim.x);   // (unit, split, head group), head group fastest
@@ -387,12 +390,21 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
         reinterpret_cast<const bf16_t*>(a.q) + ((int64_t)unit * a.heads + (hok ? h : 0)) * D + dh * DSL;
 #pragma unroll
     for (int ks = 0; ks < KSS; ++ks) qb[ks] = hok ? ld_bf16x8(qrow + ks * 32 + 8 * g) : zero_bf16x8();
-    if (a.q_rd > 0 && hok) {
+  }
+  // the q rope's table row goes out with the other prologue loads, one pair per thread, into LDS;
+  // the rotation waits for the list barrier below (reading the table per pair inside the
+  // rotation made one dependent round trip per pair, several us with the table out of cache)
+  const bool rope_lds = a.q_rd > 0 && (a.q_rd >> 1) <= kRopeRowPairs;
+  if (rope_lds && tid < (a.q_rd >> 1)) {
+    const int64_t row = ((int64_t)a.start_pos + qs) * (a.q_rd >> 1);
+    rope_cs[0][tid] = a.cos_tab[row + tid];
+    rope_cs[1][tid] = a.sin_tab[row + tid];
+  }
+  if (a.q_rd > 0 && !rope_lds && hok) {
 #pragma unroll
-      for (int ks = 0; ks < KSS; ++ks) {
-        const int c0 = dh * DSL + ks * 32 + 8 * g;
-        if (c0 + 8 > D - a.q_rd) qb[ks] = rope_q8(a, D, qs, c0, qb[ks]);
-      }
+    for (int ks = 0; ks < KSS; ++ks) {
+      const int c0 = dh * DSL + ks * 32 + 8 * g;
+      if (c0 + 8 > D - a.q_rd) qb[ks] = rope_q8(a, D, qs, c0, qb[ks]);
     }
   }
   const float sl2 = a.scale * kLog2e;
@@ -418,7 +430,32 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   // wait the compiler can see, it waits for the query registers at their first use inside the
   // loop -- vmcnt(0) at every step, which also drains the copies in flight.
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  __syncthreads();                         // rows[] complete
+  __syncthreads();                         // rows[] and the rope row complete
+  if (rope_lds && hok) {
+    const int t0 = D - a.q_rd;             // first channel of the rope tail
+#pragma unroll
+    for (int ks = 0; ks < KSS; ++ks) {
+      const int c0 = dh * DSL + ks * 32 + 8 * g;
+      if (dh * DSL + ks * 32 + 32 > t0) {  // wave-uniform: the chunk reaches into the tail
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (float)qb[ks][i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = c0 + 2 * j;
+          const int pr = max(d - t0, 0) >> 1;
+          const float cs = rope_cs[0][pr], sn = rope_cs[1][pr];
+          float x0 = v[2 * j], x1 = v[2 * j + 1];
+          rotate_pair(x0, x1, cs, sn);
+          if (d >= t0) {
+            v[2 * j] = x0;
+            v[2 * j + 1] = x1;
+          }
+        }
+        qb[ks] = cvt_bf16x8(v);
+      }
+    }
+  }
 
   for (int t = early ? 1 : 0; t < nsteps && t < NS - 1; ++t) issue(t, false);
 
