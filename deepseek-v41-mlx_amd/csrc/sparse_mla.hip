@@ -275,26 +275,48 @@ __device__ __forceinline__ void gather_rows_reg(uint64_t mp, uint8_t* kind, uint
   static_assert(D == 512, "packed rows: 512 channels, 8 per lane");
   if (lane < RPW) kind[lane] = mp != 0ull ? (uint8_t)(1u + ((uint32_t)mp & 3u)) : 0;
   const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
+  const uint64_t zero = reinterpret_cast<uint64_t>(g_zero_row);
 #pragma unroll
   for (int rr = 0; rr < RPW; ++rr) {
     const uint64_t ent = lane_u64(lo, hi, rr);
     const uint32_t tag = (uint32_t)ent & 3u;
-    if (F::F8 && tag == 1u) {           // e4m3 codes 8l..8l+7 and the ue8m0 scale of block l/4
-      const uint64_t ci = ent >> 2;
-      const uint64_t v = *reinterpret_cast<const GLOBAL uint64_t*>(pb.comp8 + ci * D + (uint64_t)lane * 8u);
+    const uint64_t idx = ent >> 2;
+    if constexpr (F::W8) {
+      // With an MXFP8 ring every row issues the same two loads into the same registers (a bf16
+      // row reads the zero row and ignores it), from wave-uniform selects: with per-format
+      // branches around the loads the compiler merged their registers after them and waited for
+      // each load right where it was issued (3 us per 32-row step at B = 64). The scale comes as
+      // the dword holding its byte (every scale base is 16-byte aligned): a byte load's
+      // zero-extension consumed it at once.
+      const bool is_c = (F::F8 || F::F4) && tag == 1u, is_w = tag == 2u, packed = is_c || is_w;
+      constexpr uint64_t CROW = F::F4 ? (uint64_t)F::F4ROW : (uint64_t)D;
+      const uint64_t cbase = is_c ? pb.comp8 + idx * CROW : (is_w ? pb.ring8 + idx * F::W8ROW : zero);
+      const uint64_t sbase = is_c ? (F::F8 ? pb.scal8 + (idx >> pb.rbs) * (D / 32) : pb.comp8 + idx * CROW + D / 2)
+                                  : (is_w ? pb.ring8 + idx * F::W8ROW + D : zero);
+      // codes: fp4 lanes read bytes 4l.. (8 bytes, the last 4 unused), fp8 lanes 8l..; scales:
+      // fp4 block l/2 (16 channels), fp8 block l/4 (32 channels)
+      const uint32_t coff = !packed ? 0u : (F::F4 && is_c ? (uint32_t)lane * 4u : (uint32_t)lane * 8u);
+      const uint32_t soff = !packed ? 0u : (F::F4 && is_c ? (uint32_t)(lane >> 1) : (uint32_t)(lane >> 2));
+      const uint64_t v = *reinterpret_cast<const GLOBAL uint64_t*>(cbase + coff);
       raw[rr] = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
-      sb[rr] = *reinterpret_cast<const GLOBAL uint8_t*>(pb.scal8 + (ci >> pb.rbs) * (D / 32) + (uint64_t)(lane >> 2));
-    } else if (F::F4 && tag == 1u) {    // e2m1 code bytes 4l..4l+3 and the e4m3 scale of block l/2
-      const uint64_t row = pb.comp8 + (ent >> 2) * F::F4ROW;
-      raw[rr].x = *reinterpret_cast<const GLOBAL uint32_t*>(row + (uint64_t)lane * 4u);
-      sb[rr] = *reinterpret_cast<const GLOBAL uint8_t*>(row + D / 2 + (uint64_t)(lane >> 1));
-    } else if (F::W8 && tag == 2u) {    // MXFP8 ring row: codes, then 16 ue8m0 scales
-      const uint64_t row = pb.ring8 + (ent >> 2) * F::W8ROW;
-      const uint64_t v = *reinterpret_cast<const GLOBAL uint64_t*>(row + (uint64_t)lane * 8u);
-      raw[rr] = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
-      sb[rr] = *reinterpret_cast<const GLOBAL uint8_t*>(row + D + (uint64_t)(lane >> 2));
+      sb[rr] = *reinterpret_cast<const GLOBAL uint32_t*>((sbase + soff) & ~3ull);
+      if (!packed) dma_row<D>(ent, dst + rr * RS, lane);
     } else {
-      dma_row<D>(ent, dst + rr * RS, lane);
+      // compressed fp8 or fp4 rows, bf16 ring: one branch per kind (measured faster than the
+      // selects above here: the bf16 window rows issue no dummy loads), the scale byte itself
+      if (tag == 1u) {
+        if constexpr (F::F8) {
+          const uint64_t v = *reinterpret_cast<const GLOBAL uint64_t*>(pb.comp8 + idx * D + (uint64_t)lane * 8u);
+          raw[rr] = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+          sb[rr] = *reinterpret_cast<const GLOBAL uint8_t*>(pb.scal8 + (idx >> pb.rbs) * (D / 32) + (uint64_t)(lane >> 2));
+        } else {
+          const uint64_t row = pb.comp8 + idx * F::F4ROW;
+          raw[rr].x = *reinterpret_cast<const GLOBAL uint32_t*>(row + (uint64_t)lane * 4u);
+          sb[rr] = *reinterpret_cast<const GLOBAL uint8_t*>(row + D / 2 + (uint64_t)(lane >> 1));
+        }
+      } else {
+        dma_row<D>(ent, dst + rr * RS, lane);
+      }
     }
   }
 }
@@ -314,8 +336,12 @@ __device__ __forceinline__ void store_rows_reg(uint8_t* sbase, const uint8_t* ki
   for (int rr = 0; rr < RPW; ++rr) {
     const uint32_t k = (kinds[rr / 4] >> (8 * (rr % 4))) & 0xFFu;
     bf16x8* out = reinterpret_cast<bf16x8*>(sbase + rr * RS + lane * 16);
-    if (F::F4 && k == 2u) *out = dequant_e2m1x8(raw[rr].x, __builtin_amdgcn_cvt_f32_fp8((int)sb[rr], 0));
-    else if (k >= 2u) *out = dequant_e4m3x8(raw[rr].x, raw[rr].y, e8m0_to_float(sb[rr]));
+    // with an MXFP8 ring sb holds the dword around the scale byte, otherwise the byte itself
+    const int fsh = F::W8 ? 8 * ((lane >> 1) & 3) : 0, esh = F::W8 ? 8 * ((lane >> 2) & 3) : 0;
+    if (F::F4 && k == 2u)
+      *out = dequant_e2m1x8(raw[rr].x, __builtin_amdgcn_cvt_f32_fp8((int)((sb[rr] >> fsh) & 0xFFu), 0));
+    else if (k >= 2u)
+      *out = dequant_e4m3x8(raw[rr].x, raw[rr].y, e8m0_to_float((sb[rr] >> esh) & 0xFFu));
   }
 }
 
