@@ -371,6 +371,81 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* x, T* y, const fl
   for (int i = threadIdx.x; i < dim; i += 256) io<T>::st(y + i, w[i] * (io<T>::ld(x + i) * inv));
 }
 
+// Rows held in registers: one workgroup per row, thread t holding 16-byte chunks t, t + 256, ...
+// (at most C of them), so the row is read once with full-width loads and scaled from registers.
+// ADD: the residual add of a block first -- h <- cast(h + delta), stored back -- and the norm of
+// the rounded sum, as the two separate ops compute it. The sum of squares is fp32, per thread,
+// then the wave's xor tree and the four waves in a fixed order.
+template <typename T, int C, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(T* x, const T* delta, T* y, const float* w, int dim,
+                                                           float eps) {
+  constexpr int E = 16 / (int)sizeof(T);       // elements per chunk
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int nch = dim / E;
+  uint4* xr = reinterpret_cast<uint4*>(x + row * dim);
+  float v[C][E];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int ch = threadIdx.x + 256 * c;
+    if (ch < nch) {
+      const uint4 u = xr[ch];
+      const T* e = reinterpret_cast<const T*>(&u);
+#pragma unroll
+      for (int i = 0; i < E; ++i) v[c][i] = io<T>::ld(e + i);
+      if constexpr (ADD) {
+        const uint4 du = reinterpret_cast<const uint4*>(delta + row * dim)[ch];
+        const T* de = reinterpret_cast<const T*>(&du);
+        uint4 out;
+        T* oe = reinterpret_cast<T*>(&out);
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          v[c][i] = io<T>::rnd(v[c][i] + io<T>::ld(de + i));
+          io<T>::st(oe + i, v[c][i]);
+        }
+        xr[ch] = out;
+      }
+#pragma unroll
+      for (int i = 0; i < E; ++i) ss += v[c][i] * v[c][i];
+    }
+  }
+  ss = group_sum(ss, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.0f / sqrtf(tot / (float)dim + eps);
+  uint4* yr = reinterpret_cast<uint4*>(y + row * dim);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int ch = threadIdx.x + 256 * c;
+    if (ch < nch) {
+      uint4 out;
+      T* oe = reinterpret_cast<T*>(&out);
+#pragma unroll
+      for (int i = 0; i < E; ++i) io<T>::st(oe + i, w[ch * E + i] * (v[c][i] * inv));
+      yr[ch] = out;
+    }
+  }
+}
+
+template <typename T, bool ADD>
+static bool launch_rows_norm(T* x, const T* delta, T* y, const float* w, int64_t rows, int dim, float eps,
+                             hipStream_t stream) {
+  constexpr int E = 16 / (int)sizeof(T);
+  if (dim % E || !aligned16(x) || !aligned16(y) || (ADD && !aligned16(delta))) return false;
+  const int per = (dim / E + 255) / 256;     // chunks per thread
+  const dim3 grid((unsigned)rows), block(256);
+  switch (per) {
+    case 1: hipLaunchKernelGGL((rmsnorm_rows_kernel<T, 1, ADD>), grid, block, 0, stream, x, delta, y, w, dim, eps); break;
+    case 2: hipLaunchKernelGGL((rmsnorm_rows_kernel<T, 2, ADD>), grid, block, 0, stream, x, delta, y, w, dim, eps); break;
+    case 3: hipLaunchKernelGGL((rmsnorm_rows_kernel<T, 3, ADD>), grid, block, 0, stream, x, delta, y, w, dim, eps); break;
+    case 4: hipLaunchKernelGGL((rmsnorm_rows_kernel<T, 4, ADD>), grid, block, 0, stream, x, delta, y, w, dim, eps); break;
+    default: return false;
+  }
+  return true;
+}
+
 // ------------------------------------------------------------------ rope table, ring, window idx
 
 __global__ void rope_table_kernel(float* cs, float* sn, const float* freqs, int seqlen, int half) {
@@ -497,14 +572,40 @@ extern "C" int dsv41_rmsnorm(const void* x, void* y, const float* weight, int64_
   DSV41_REQUIRE(rows >= 0 && dim > 0, DSV41_E_ARG, "%s: bad sizes", what);
   if (rows == 0) return 0;
   DSV41_REQUIRE(rows < (1ll << 31), DSV41_E_ARG, "%s: too many rows", what);
+  // rows of up to 4 chunks of 16 bytes per thread take the register kernel (bf16 up to 8,192
+  // channels, fp32 up to 4,096); others the strided one
+  if (dtype == DSV41_F32) {
+    if (!launch_rows_norm<float, false>((float*)const_cast<void*>(x), nullptr, (float*)y, weight, rows, dim, eps, stream))
+      hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3((unsigned)rows), dim3(256), 0, stream, (const float*)x,
+                         (float*)y, weight, dim, eps);
+  } else if (dtype == DSV41_BF16) {
+    if (!launch_rows_norm<bf16_t, false>((bf16_t*)const_cast<void*>(x), nullptr, (bf16_t*)y, weight, rows, dim, eps,
+                                         stream))
+      hipLaunchKernelGGL(rmsnorm_kernel<bf16_t>, dim3((unsigned)rows), dim3(256), 0, stream, (const bf16_t*)x,
+                         (bf16_t*)y, weight, dim, eps);
+  } else {
+    return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported", what, dtype);
+  }
+  return check_launch(what);
+}
+
+extern "C" int dsv41_add_rmsnorm(void* h, const void* delta, void* y, const float* weight, int64_t rows, int32_t dim,
+                                 float eps, int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_add_rmsnorm";
+  DSV41_REQUIRE(h && delta && y && weight, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(rows >= 0 && dim > 0, DSV41_E_ARG, "%s: bad sizes", what);
+  if (rows == 0) return 0;
+  DSV41_REQUIRE(rows < (1ll << 31), DSV41_E_ARG, "%s: too many rows", what);
+  DSV41_REQUIRE(h != y && delta != y, DSV41_E_ARG, "%s: the output must not alias h or delta", what);
+  bool ok;
   if (dtype == DSV41_F32)
-    hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3((unsigned)rows), dim3(256), 0, stream, (const float*)x,
-                       (float*)y, weight, dim, eps);
+    ok = launch_rows_norm<float, true>((float*)h, (const float*)delta, (float*)y, weight, rows, dim, eps, stream);
   else if (dtype == DSV41_BF16)
-    hipLaunchKernelGGL(rmsnorm_kernel<bf16_t>, dim3((unsigned)rows), dim3(256), 0, stream, (const bf16_t*)x,
-                       (bf16_t*)y, weight, dim, eps);
+    ok = launch_rows_norm<bf16_t, true>((bf16_t*)h, (const bf16_t*)delta, (bf16_t*)y, weight, rows, dim, eps, stream);
   else
     return set_error(DSV41_E_DTYPE, "%s: dtype %d not supported", what, dtype);
+  DSV41_REQUIRE(ok, DSV41_E_SHAPE, "%s: rows of %d elements (16-byte aligned, at most 1,024 16-byte chunks) required",
+                what, dim);
   return check_launch(what);
 }
 

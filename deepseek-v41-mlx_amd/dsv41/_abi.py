@@ -38,6 +38,7 @@ _SIGNATURES = {
     "dsv41_rope_tail": [_c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _c_p, _c_p, _i32, _i32, _i32,
                         _i32, _c_p],
     "dsv41_rmsnorm": [_c_p, _c_p, _c_p, _i64, _i32, _f32, _i32, _c_p],
+    "dsv41_add_rmsnorm": [_c_p, _c_p, _c_p, _c_p, _i64, _i32, _f32, _i32, _c_p],
     "dsv41_kv_window_prep": [_c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _f32, _i32,
                              _c_p],
     "dsv41_window_write": [_c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
@@ -319,6 +320,22 @@ def rmsnorm(x, weight, eps, out=None):
     d = x.shape[-1]
     _call(name, _ptr(x), _ptr(out), _ptr(weight), x.numel() // d, d, float(eps),
           dtype_code(x, name), _stream(x))
+    return out
+
+
+def add_rmsnorm(h, delta, weight, eps, out=None):
+    """h <- cast(h + delta) in place, then rmsnorm(h): the residual add of one block and the next
+    block's attn_norm (model.py:141-154 with layers.py:20-33) in one pass over the rows."""
+    name = "dsv41_add_rmsnorm"
+    _gpu(name, h, delta, weight, out)
+    _contig(name, h, delta)
+    if delta.shape != h.shape or delta.dtype != h.dtype:
+        raise ValueError(f"{name}: delta {tuple(delta.shape)} {delta.dtype} must match h {tuple(h.shape)} {h.dtype}")
+    _vec(name, "weight", weight, h.shape[-1])
+    out = _out(name, out, h.shape, h.dtype, h.device)
+    d = h.shape[-1]
+    _call(name, _ptr(h), _ptr(delta), _ptr(out), _ptr(weight), h.numel() // d, d, float(eps),
+          dtype_code(h, name), _stream(h))
     return out
 
 

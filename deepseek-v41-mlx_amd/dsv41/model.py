@@ -11,10 +11,17 @@ from __future__ import annotations
 
 import torch
 
+from . import _abi
 from .attention import Attention
 from .cache import ModelCache
 from .config import ModelArgs
 from .layers import RMSNorm
+
+
+def _fused_norm_ok(h: torch.Tensor) -> bool:
+    """dsv41_add_rmsnorm's row shapes: whole 16-byte chunks, at most 1,024 of them per row."""
+    per = 16 // h.element_size()
+    return h.shape[-1] % per == 0 and h.shape[-1] // per <= 1024 and h.data_ptr() % 16 == 0
 
 
 class SharedState:
@@ -51,6 +58,11 @@ class AttentionStack(torch.nn.Module):
         """h [b, n, dim] continues the sequence at cache.offset; advances the cache."""
         start_pos = cache.offset
         shared = SharedState()
+        # each block's residual add is fused with the next block's attn_norm (dsv41_add_rmsnorm):
+        # the same two ops, bit for bit, in one pass over h, which is updated in place (a copy of
+        # the caller's tensor)
+        h = h.contiguous().clone()
+        delta = None
         for attn, norm in zip(self.layers, self.norms):
             use = shared
             if self._break_sharing and not attn.is_kv_source and attn.ratio:
@@ -59,6 +71,15 @@ class AttentionStack(torch.nn.Module):
                 use.index_src_cache = shared.index_src_cache
                 use.topk_idxs = (torch.full_like(shared.topk_idxs, -1)
                                  if shared.topk_idxs is not None else None)
-            h = h + attn(norm(h), start_pos, cache, use)
+            if delta is None:
+                x = norm(h)
+            elif _fused_norm_ok(h):
+                x = _abi.add_rmsnorm(h, delta.contiguous(), norm.weight, norm.eps)
+            else:
+                h.add_(delta)
+                x = norm(h)
+            delta = attn(x, start_pos, cache, use)
+        if delta is not None:
+            h = h + delta
         cache.offset = start_pos + h.shape[1]
         return h

@@ -94,6 +94,14 @@ int dsv41_rope_tail(const void* x, void* y, int32_t bsz, int32_t seqlen, int32_t
 int dsv41_rmsnorm(const void* x, void* y, const float* weight, int64_t rows, int32_t dim,
                   float eps, int32_t dtype, hipStream_t stream);
 
+/* The residual add of one block and the next block's attn_norm, deepseek_v41_mlx/model.py:141-154
+ * (h = h + attn(attn_norm(h)), MoE and hyper-connections as identity) with the RMSNorm of
+ * layers.py:20-33: h <- cast(h + delta) in place, then y = rmsnorm(h, weight) as dsv41_rmsnorm
+ * computes it. Rows of `dim` elements, dim a multiple of 8 (bf16) or 4 (fp32), at most 8,192 bf16
+ * or 4,096 fp32 channels, 16-byte aligned; y must not alias h or delta. */
+int dsv41_add_rmsnorm(void* h, const void* delta, void* y, const float* weight, int64_t rows,
+                      int32_t dim, float eps, int32_t dtype, hipStream_t stream);
+
 /* ---------------------------------------------------------------- window KV --
  */
 

@@ -399,6 +399,10 @@ def test_fake_quant_rope_norm_wrappers_check_out(host_abi):
     _reaches_launch(lambda: A.rmsnorm(x, torch.ones(64), 1e-6))
     _refused(lambda: A.rmsnorm(x, torch.ones(64), 1e-6, out=torch.zeros(4, 63)))
     _refused(lambda: A.rmsnorm(x, torch.ones(64, dtype=torch.bfloat16), 1e-6), "weight")
+    _reaches_launch(lambda: A.add_rmsnorm(x, torch.zeros(4, 64), torch.ones(64), 1e-6))
+    _refused(lambda: A.add_rmsnorm(x, torch.zeros(4, 32), torch.ones(64), 1e-6), "delta")
+    _refused(lambda: A.add_rmsnorm(x, torch.zeros(4, 64, dtype=torch.bfloat16), torch.ones(64), 1e-6), "delta")
+    _refused(lambda: A.add_rmsnorm(x, torch.zeros(4, 64), torch.ones(64), 1e-6, out=torch.zeros(4, 63)))
 
 
 def test_cache_writers_check_batch_rows_and_parameters(host_abi):

@@ -108,6 +108,36 @@ def test_rope_tail_and_rmsnorm(gpu, dt):
     assert (max_abs(got, want) < 1e-5) if dt == "f32" else (rel_max_diff(got, want) < 1e-2)
 
 
+@pytest.mark.parametrize("dt,dim", [("bf16", 5120), ("bf16", 8192), ("bf16", 1280), ("bf16", 64), ("bf16", 1000),
+                                    ("f32", 4096), ("f32", 1280), ("f32", 5120)])
+def test_rmsnorm_rows_and_fused_residual_add(gpu, dt, dim):
+    """dsv41_rmsnorm against the oracle over every launch form (rows held in registers for up to
+    1,024 16-byte chunks; the strided kernel for 1,000 bf16 and 5,120 fp32 channels), in place
+    too; dsv41_add_rmsnorm (the block's residual add and the next attn_norm) bit for bit equal to
+    torch's add followed by dsv41_rmsnorm, h updated in place, on the shapes it takes."""
+    from dsv41 import _abi
+    rng = rng_for(f"norm{dt}{dim}")
+    w = (1 + 0.1 * rng.standard_normal(dim)).astype(F32)
+    for rows in (1, 33, 64):
+        y = R.cast(rng.standard_normal((rows, dim)).astype(F32) * 4, dt)
+        got = to_np(_abi.rmsnorm(dev(y, dt), dev(w), 1e-20))
+        want = R.rmsnorm(y, w, 1e-20, dt)
+        assert (max_abs(got, want) < 1e-5) if dt == "f32" else (rel_max_diff(got, want) < 1e-2), rows
+        x = dev(y, dt)
+        assert torch.equal(_abi.rmsnorm(x, dev(w), 1e-20, out=x), dev(got, dt)), "in place"
+        per = 16 // (4 if dt == "f32" else 2)
+        if dim % per or dim // per > 1024:
+            continue
+        h = dev(y, dt)
+        delta = dev(R.cast(rng.standard_normal((rows, dim)).astype(F32), dt), dt)
+        h_want = h + delta
+        n_want = _abi.rmsnorm(h_want, dev(w), 1e-20)
+        n_got = _abi.add_rmsnorm(h, delta, dev(w), 1e-20)
+        torch.cuda.synchronize()
+        assert torch.equal(h, h_want), "h + delta"
+        assert torch.equal(n_got, n_want), "norm of the sum"
+
+
 # ------------------------------------------------------------------ fused window / cache writes
 
 
