@@ -10,7 +10,7 @@
 // order of the fp32 additions; the bf16 output is the fp32 value rounded to nearest even once, as
 // astype does.
 //
-// Launch shapes (bf16 o and wo_a with d a multiple of 512 and r of 128 -- the release's 4096 and
+// Launch shapes (bf16 o and wo_a with d a multiple of 64 and r of 128 -- the release's 4096 and
 // 1024 -- take the MFMA kernel; other shapes and fp32 activations take a plain fp32 kernel). Both
 // operand tiles are copied global -> LDS (global_load_lds_dwordx4) over 64-channel steps in an
 // XOR-swizzled layout that the MFMA fragment reads take without bank conflicts:
@@ -288,7 +288,7 @@ extern "C" int dsv41_wo_a_grouped(const void* o, const void* wo_a, void* out, in
   DSV41_REQUIRE((int64_t)groups * r * d < (1ll << 40) && (int64_t)rows * groups * (d > r ? d : r) < (1ll << 40),
                 DSV41_E_ARG, "%s: tensors too large", what);
   if (rows == 0) return 0;
-  const bool mfma = dtype == DSV41_BF16 && d % 512 == 0 && r % kTileR == 0;   // every tile shape's multiples
+  const bool mfma = dtype == DSV41_BF16 && d % 64 == 0 && r % kTileR == 0;   // every tile shape's multiples
   if (!mfma) {
     DSV41_REQUIRE(((int64_t)rows * groups * r + 255) / 256 < (1ll << 32), DSV41_E_ARG, "%s: too many outputs", what);
     if (dtype == DSV41_BF16) launch_wo_a_plain<bf16_t>(o, wo_a, out, rows, groups, d, r, out_dtype, stream);

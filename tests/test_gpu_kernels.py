@@ -1281,6 +1281,7 @@ def test_indexer_topk_mxq_fp8_equals_two_calls(gpu, b, n, h, nb, topk, start, rb
     (70, 8, 4096, 1024, "bf16"),      # three 32-row query tiles, a partial one
     (100, 2, 512, 128, "bf16"),       # four 32-row query tiles, a partial one
     (64, 1, 5120, 1280, "bf16"),      # one group: a dense projection's shape
+    (32, 1, 1280, 8192, "bf16"),      # the indexer's query projection at decode (d not a multiple of 512)
     (128, 8, 4096, 1024, "bf16"),
     (129, 8, 4096, 1024, "bf16"),     # the tiled kernel, a partial 256-row query tile
     (257, 8, 4096, 1024, "bf16"),     # one row in the second 256-row query tile
