@@ -28,9 +28,10 @@ namespace dsv41 {
 
 struct WoaArgs {
   const bf16_t* o;     // [rows, groups * d]
-  const bf16_t* w;     // [groups * r, d]
+  const bf16_t* w;     // [groups * r, d]; split: [r, groups * d]
   void* out;           // [rows, groups * r], bf16 or fp32
   int rows, groups, d, r;
+  int split;           // 1: one dense weight whose contraction is cut into `groups` ranges of d
 };
 
 // ------------------------------------------------------------------ any shape
@@ -160,7 +161,10 @@ __global__ __launch_bounds__(64 * GR * GM, (TileCfg<WR, WM, GR, GM, BK, NS>::LDS
   for (int j = 0; j < C::NW; ++j) {
     const int row = wave * (C::TR / C::NWV) + j * C::RPI + lane / C::CPR;
     const int chunk = (lane % C::CPR) ^ tile_swz<BK>(row);
-    wsrc[j] = reinterpret_cast<uint64_t>(a.w + ((int64_t)grp * a.r + rt * C::TR + row) * a.d + 8 * chunk);
+    // grouped: group grp's weight rows; split: range grp of every weight row (row stride groups * d)
+    const int64_t wrow = a.split ? (int64_t)(rt * C::TR + row) * ((int64_t)a.groups * a.d) + (int64_t)grp * a.d
+                                 : ((int64_t)grp * a.r + rt * C::TR + row) * a.d;
+    wsrc[j] = reinterpret_cast<uint64_t>(a.w + wrow + 8 * chunk);
   }
 #pragma unroll
   for (int j = 0; j < C::NO; ++j) {
@@ -297,8 +301,66 @@ extern "C" int dsv41_wo_a_grouped(const void* o, const void* wo_a, void* out, in
   }
   DSV41_REQUIRE((int64_t)groups * (r / kTileR) * ((rows + 127) / 128) < (1ll << 31), DSV41_E_ARG,
                 "%s: too many tiles", what);
-  WoaArgs a{static_cast<const bf16_t*>(o), static_cast<const bf16_t*>(wo_a), out, rows, groups, d, r};
+  WoaArgs a{static_cast<const bf16_t*>(o), static_cast<const bf16_t*>(wo_a), out, rows, groups, d, r, 0};
   if (out_dtype == DSV41_BF16) launch_wo_a<bf16_t>(a, stream);
   else launch_wo_a<float>(a, stream);
+  return check_launch(what);
+}
+
+// ------------------------------------------------------------------ split-contraction rows
+
+namespace dsv41 {
+// y[m, j] = sum over the ranges s (in order) of part[m, s * n + j], rounded to bf16 once; four
+// consecutive outputs per thread.
+__global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restrict__ part, bf16_t* __restrict__ y,
+                                                            int rows, int n, int splits) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;   // over rows * n
+  if (i >= (int64_t)rows * n) return;
+  const int64_t m = i / n;
+  const int j = (int)(i - m * n);
+  const float* p = part + m * (int64_t)splits * n + j;
+  f32x4 acc = *reinterpret_cast<const f32x4*>(p);
+  for (int sidx = 1; sidx < splits; ++sidx) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p + (int64_t)sidx * n);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = acc[e] + v[e];
+  }
+  uint2 st;
+  st.x = pack2_bf16(acc[0], acc[1]);
+  st.y = pack2_bf16(acc[2], acc[3]);
+  *reinterpret_cast<uint2*>(y + i) = st;
+}
+}  // namespace dsv41
+
+extern "C" size_t dsv41_linear_rows_workspace_bytes(int32_t rows, int32_t n, int32_t splits) {
+  if (rows <= 0 || n <= 0 || splits <= 1) return 0;
+  return (size_t)rows * (size_t)splits * (size_t)n * sizeof(float);
+}
+
+extern "C" int dsv41_linear_rows(const void* x, const void* w, void* y, void* workspace, size_t workspace_bytes,
+                                 int32_t rows, int32_t k, int32_t n, int32_t splits, int32_t dtype,
+                                 hipStream_t stream) {
+  const char* what = "dsv41_linear_rows";
+  DSV41_REQUIRE(x && w && y, DSV41_E_ARG, "%s: null tensor", what);
+  DSV41_REQUIRE(dtype == DSV41_BF16, DSV41_E_DTYPE, "%s: bf16 only (dtype %d)", what, dtype);
+  DSV41_REQUIRE(rows >= 0 && rows <= 128 && k > 0 && n > 0, DSV41_E_ARG, "%s: rows %d (at most 128), k %d, n %d", what,
+                rows, k, n);
+  DSV41_REQUIRE(splits >= 1 && splits <= 64 && k % (64 * splits) == 0, DSV41_E_SHAPE,
+                "%s: k = %d must split into %d ranges of whole 64-channel steps", what, k, splits);
+  DSV41_REQUIRE(n % 32 == 0, DSV41_E_SHAPE, "%s: n = %d must be a multiple of 32", what, n);
+  DSV41_REQUIRE(aligned16(x) && aligned16(w) && aligned16(y), DSV41_E_ARG, "%s: tensors must be 16-byte aligned", what);
+  if (rows == 0) return 0;
+  const size_t need = dsv41_linear_rows_workspace_bytes(rows, n, splits);
+  DSV41_REQUIRE(workspace_bytes >= need && (need == 0 || (workspace && aligned16(workspace))), DSV41_E_WORKSPACE,
+                "%s: workspace of %zu bytes needed, %zu given", what, need, workspace_bytes);
+  WoaArgs a{static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(w), splits > 1 ? workspace : y, rows, splits,
+            k / splits, n, 1};
+  if (splits > 1) launch_wo_a<float>(a, stream);
+  else launch_wo_a<bf16_t>(a, stream);
+  int rc = check_launch(what);
+  if (rc || splits <= 1) return rc;
+  const int64_t quads = ((int64_t)rows * n) / 4;
+  hipLaunchKernelGGL(linear_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const float*>(workspace), static_cast<bf16_t*>(y), rows, n, splits);
   return check_launch(what);
 }

@@ -95,6 +95,8 @@ _SIGNATURES = {
                                        _i32, _i32, _i32, _f32, _c_p, _c_p, _i32, _i32, _c_p, _sz, _c_p],
     "dsv41_window_write_mxfp8": [_c_p, _i64, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_wo_a_grouped": [_c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_linear_rows_workspace_bytes": [_i32, _i32, _i32],
+    "dsv41_linear_rows": [_c_p, _c_p, _c_p, _c_p, _sz, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_comp_write_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32,
                              _i32, _c_p],
     "dsv41_index_key_publish_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32,
@@ -108,6 +110,7 @@ _SIGNATURES = {
 }
 _RESTYPES = {
     "dsv41_sparse_mla_workspace_bytes": _sz,
+    "dsv41_linear_rows_workspace_bytes": _sz,
     "dsv41_topk_workspace_bytes": _sz,
     "dsv41_indexer_topk_workspace_bytes": _sz,
     "dsv41_version": ctypes.c_char_p,
@@ -520,6 +523,40 @@ def wo_a_grouped(o, wo_a, groups, out=None, out_dtype=None):
           _stream(o))
     return out
 
+
+def linear_rows_splits(k: int, n: int) -> int:
+    """Contraction ranges for dsv41_linear_rows: the most ranges (of whole 64-channel steps, at
+    most 64) that keep the n / 32 x ranges workgroups within one wave of the chip (256: one
+    workgroup per CU; a 320-workgroup wq_a ran a second round of 64 and took 9.0 us)."""
+    tiles = max(n // 32, 1)
+    best = 1
+    for s in range(1, 65):
+        if k % (64 * s) == 0 and tiles * s <= 256:
+            best = s
+    return best
+
+
+def linear_rows(x, w, splits=None, out=None, workspace=None):
+    """y = x @ w^T for decode row counts (at most 128 rows of x [..., k]; w [n, k] the Linear
+    weight, read in place), bf16: the projections of attention.py:114-116 on the decode tile
+    kernel with the contraction split over `splits` ranges (linear_rows_splits by default)."""
+    name = "dsv41_linear_rows"
+    _gpu(name, x, w, out)
+    _contig(name, x, w)
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: x and w must be bfloat16")
+    if w.dim() != 2 or x.shape[-1] != w.shape[1]:
+        raise ValueError(f"{name}: x {tuple(x.shape)} and w {tuple(w.shape)} do not contract")
+    n, k = w.shape
+    rows = x.numel() // k
+    if splits is None:
+        splits = linear_rows_splits(k, n)
+    out = _out(name, out, (*x.shape[:-1], n), torch.bfloat16, x.device)
+    need = lib().dsv41_linear_rows_workspace_bytes(rows, n, splits)
+    ws = _ws(name, workspace, need, x.device)
+    _call(name, _ptr(x), _ptr(w), _ptr(out), _ptr(ws) if ws is not None else None, need, rows, k, n, splits,
+          dtype_code(x, name), _stream(x))
+    return out
 
 def comp_write_fp4(latents, comp_kv4, g0, ratio, cos, sin, rd):
     """comp_write into a packed fp4 cache: comp_kv4 uint8 [b, >=g0+g, d/2 + d/16], per row the

@@ -1,7 +1,8 @@
 """One V4.1 attention layer (deepseek_v41_mlx/attention.py:53-179) on the GPU.
 
-The dense projections (wq_a, wq_b, wkv, the compressor / indexer projections, wo_b) are torch
-GEMMs; everything between them, and the grouped block-diagonal wo_a, runs in HIP kernels:
+The dense projections (wq_b, the compressor projections, wo_b) are torch GEMMs; at decode row
+counts wq_a, wkv and the indexer's wq_b run on dsv41_linear_rows (layers.decode_linear).
+Everything between them, and the grouped block-diagonal wo_a, runs in HIP kernels:
 
   q      : q_norm (RMSNorm kernel); q's rope tail is applied by the attention launch as it
            loads q (no separate pass over q)
@@ -37,7 +38,7 @@ from . import _abi, fakequant
 from .compressor import Compressor
 from .config import ModelArgs
 from .indexer import Indexer
-from .layers import RMSNorm, yarn_inv_freqs
+from .layers import RMSNorm, decode_linear, yarn_inv_freqs
 
 
 # multiply-adds from which fp32 activations take the batched GEMM for wo_a (the release shape
@@ -154,11 +155,11 @@ class Attention(torch.nn.Module):
         x = x.contiguous()
 
         # queries: q's rope tail (attention.py:117) is applied by the attention launch as it loads q
-        qr = self.q_norm(self.wq_a(x))
+        qr = self.q_norm(decode_linear(self.wq_a, x))
         q = self.wq_b(qr).view(bsz, n, self.n_heads, self.head_dim).contiguous()
 
         # this chunk's window KV
-        kv = self._kv_prologue(self.wkv(x).contiguous(), cos, sin, start_pos)
+        kv = self._kv_prologue(decode_linear(self.wkv, x).contiguous(), cos, sin, start_pos)
 
         lc = cache.layers[self.layer_id]
         wp = min(start_pos, self.window_size)

@@ -25,7 +25,7 @@ import torch
 
 from . import _abi, fakequant
 from .config import ModelArgs
-from .layers import RMSNorm
+from .layers import RMSNorm, decode_linear
 
 
 def _lens_tensor(lens, device) -> torch.Tensor:
@@ -41,21 +41,6 @@ def select_candidate_blocks(scores: torch.Tensor, lens, topk_blocks: int,
     return _abi.candidate_blocks(scores.float().contiguous(), topk_blocks, block_size,
                                  _lens_tensor(lens, scores.device))
 
-
-# Decode rows (at most 128) of bf16 activations: the index-query projection wq_b (q_lora -> Hi * Di,
-# 20 MiB of weight at the release shape) runs on dsv41_wo_a_grouped with one group -- its weight
-# streamed once through an eight-stage LDS copy ring: 8.8-9.2 us at 32-64 rows against
-# 18.2-18.4 us for torch's linear (hipBLASLt), with the same exact bf16 products and fp32 sums.
-_DECODE_PROJ_ROWS = 128
-
-
-def _decode_proj(lin: torch.nn.Linear, x: torch.Tensor) -> torch.Tensor:
-    w = lin.weight
-    rows = x.numel() // x.shape[-1]
-    if (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.is_cuda and rows <= _DECODE_PROJ_ROWS
-            and w.shape[1] % 64 == 0 and w.shape[0] % 128 == 0):
-        return _abi.wo_a_grouped(x.contiguous(), w, 1)
-    return lin(x)
 
 def weight_scale(n_heads: int, head_dim: int, dtype) -> float:
     """head_dim**-0.5 * n_heads**-0.5 as the activation dtype holds it: a python scalar
@@ -128,7 +113,8 @@ class Indexer(torch.nn.Module):
         Returns [b, n, min(index_topk, nb)] int32 indices, -1 masked."""
         bsz, n, _ = x.shape
         rd = self.rope_head_dim
-        q = _decode_proj(self.wq_b, qr).view(bsz, n, self.n_heads, self.head_dim).contiguous()
+        # decode rows: dsv41_linear_rows (8.8-9.2 us at 32-64 rows against 18.2-18.4 us for torch's linear)
+        q = decode_linear(self.wq_b, qr).view(bsz, n, self.n_heads, self.head_dim).contiguous()
         w_raw = self.weights_proj(x).contiguous()
         w_scale = weight_scale(self.n_heads, self.head_dim, x.dtype)
         cand = None

@@ -29,6 +29,22 @@ class RMSNorm(torch.nn.Module):
         return _abi.rmsnorm(x.contiguous(), self.weight, self.eps)
 
 
+# Decode row counts (at most 128 rows of bf16 activations): the projections that take
+# decode_linear run on dsv41_linear_rows -- the weight streamed once through the decode tile
+# kernel's LDS copy ring, the contraction split so that small outputs still fill the chip --
+# instead of torch's linear, whose library kernels for these shapes run ~17 us even for a 5 MB
+# weight. Other shapes, dtypes and row counts take torch's linear.
+DECODE_ROWS = 128
+
+
+def decode_linear(lin: torch.nn.Linear, x: torch.Tensor) -> torch.Tensor:
+    w = lin.weight
+    rows = x.numel() // x.shape[-1]
+    if (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.is_cuda and lin.bias is None
+            and rows <= DECODE_ROWS and w.shape[1] % 64 == 0 and w.shape[0] % 32 == 0):
+        return _abi.linear_rows(x.contiguous(), w)
+    return lin(x)
+
 def yarn_inv_freqs(dim: int, original_seq_len: int, base: float, factor: float,
                    beta_fast: int, beta_slow: int) -> np.ndarray:
     """[dim/2] fp32 inverse frequencies; ``original_seq_len == 0`` disables YaRN (layers.py:36-52)."""

@@ -504,10 +504,24 @@ int dsv41_sparse_mla_packed_decode(const void* q, uint8_t* win_kv8, int64_t ring
  * unquantized) in dtype (BF16 or F32); out [rows, groups*r] in out_dtype: BF16 (the fp32 sum
  * rounded to nearest even once, as astype does) or F32. Sums are fp32 in a fixed order:
  * deterministic, equal to the reference up to the order of fp32 additions (bf16 products are
- * exact). bf16 with d a multiple of 512 and r of 128 (the release's 4096 and 1024) runs on MFMA;
+ * exact). bf16 with d a multiple of 64 and r of 128 (the release's 4096 and 1024) runs on MFMA;
  * any other shape, and fp32, on a plain fp32 kernel. */
 int dsv41_wo_a_grouped(const void* o, const void* wo_a, void* out, int32_t rows, int32_t groups,
                        int32_t d, int32_t r, int32_t dtype, int32_t out_dtype, hipStream_t stream);
+
+/* The dense projections of Attention.__call__ at decode row counts, deepseek_v41_mlx/attention.py:
+ * 114-116 (wq_a and wkv on the block input: nn.Linear, y = x @ w^T): x [rows, k] and the Linear
+ * weight w [n, k] as they lie, bf16, y [rows, n] bf16 (fp32 sums rounded once). For rows <= 128
+ * the weight is streamed once by the decode tile kernel of dsv41_wo_a_grouped, with the
+ * contraction cut into `splits` ranges so that n / 32 x splits workgroups fill the chip; each
+ * range's fp32 partial goes to `workspace` ([rows, splits * n] floats,
+ * dsv41_linear_rows_workspace_bytes; none for splits == 1) and a second kernel sums them in
+ * range order: deterministic, equal to the reference up to the order of fp32 additions.
+ * k a multiple of 64 * splits, n of 32, splits <= 64. */
+size_t dsv41_linear_rows_workspace_bytes(int32_t rows, int32_t n, int32_t splits);
+int dsv41_linear_rows(const void* x, const void* w, void* y, void* workspace, size_t workspace_bytes,
+                      int32_t rows, int32_t k, int32_t n, int32_t splits, int32_t dtype,
+                      hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -403,6 +403,10 @@ def test_fake_quant_rope_norm_wrappers_check_out(host_abi):
     _refused(lambda: A.add_rmsnorm(x, torch.zeros(4, 32), torch.ones(64), 1e-6), "delta")
     _refused(lambda: A.add_rmsnorm(x, torch.zeros(4, 64, dtype=torch.bfloat16), torch.ones(64), 1e-6), "delta")
     _refused(lambda: A.add_rmsnorm(x, torch.zeros(4, 64), torch.ones(64), 1e-6, out=torch.zeros(4, 63)))
+    xb = torch.zeros(4, 128, dtype=torch.bfloat16)
+    _reaches_launch(lambda: A.linear_rows(xb, torch.zeros(64, 128, dtype=torch.bfloat16)))
+    _refused(lambda: A.linear_rows(xb, torch.zeros(64, 96, dtype=torch.bfloat16)), "contract")
+    _refused(lambda: A.linear_rows(xb.float(), torch.zeros(64, 128)), "bfloat16")
 
 
 def test_cache_writers_check_batch_rows_and_parameters(host_abi):

@@ -1319,6 +1319,35 @@ def test_wo_a_grouped(gpu, rows, groups, d, r, dt):
         assert (got != ref.to(tdt)).float().mean().item() < 2e-3
 
 
+@pytest.mark.parametrize("rows,k,n,splits", [
+    (64, 5120, 1280, None),       # wq_a at the C4 batch (8 contraction ranges)
+    (32, 5120, 512, None),        # wkv at bs32 (16 ranges)
+    (1, 5120, 1792, None),        # one decode row, wq_a + wkv's width
+    (100, 1280, 8192, None),      # the indexer's wq_b, a partial 32-row query tile (one range)
+    (64, 5120, 1280, 1),          # no split: the kernel stores bf16 itself
+    (37, 640, 96, 5),             # odd row count, n a multiple of 32 only
+])
+def test_linear_rows(gpu, rows, k, n, splits):
+    """dsv41_linear_rows = nn.Linear (x @ w^T) at decode rows: against a float64 product of the
+    same values every output within one bf16 step of the exact sum (bf16 products are exact,
+    fp32 sums per contraction range, then the ranges in order, rounded once), most outputs equal
+    to the float64 result rounded once; repeat calls bit-identical."""
+    from dsv41 import _abi
+    g = torch.Generator(device=gpu).manual_seed(SEED_BASE + rows + k + n)
+    x = torch.randn(rows, k, generator=g, device=gpu).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g, device=gpu) * 0.02).to(torch.bfloat16)
+    got = _abi.linear_rows(x, w, splits)
+    again = _abi.linear_rows(x, w, splits)
+    torch.cuda.synchronize()
+    assert got.shape == (rows, n) and got.dtype == torch.bfloat16
+    assert torch.equal(got, again), "repeated calls differ"
+    ref = x.double() @ w.double().t()
+    mag = x.double().abs() @ w.double().abs().t()
+    err = ((got.double() - ref).abs() - ref.abs() * 2.0 ** -8).clamp_min(0) / mag.clamp_min(1e-30)
+    assert err.max().item() < 2e-5, f"beyond one bf16 rounding: {err.max().item():.2e} of sum |x w|"
+    assert (got != ref.to(torch.bfloat16)).float().mean().item() < 2e-3
+
+
 @pytest.mark.parametrize("rows", [1, 4, 300])
 def test_attention_wo_a_fp32_at_release_shape(gpu, rows):
     """An fp32 layer at the release's output-LoRA shape (8 groups x (4096 -> 1024)) takes one fp32
