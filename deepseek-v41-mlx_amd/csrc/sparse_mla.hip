@@ -609,12 +609,13 @@ __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
 //   score waves 0-3, 16 heads each over all 512 channels: S^T = K Q^T of step t (Q^T in VGPRs),
 //     masking, the running max and denominator with lazy rescaling, P rounded to bf16 into LDS
 //     as P^T [head][row], and the step's rescale factor per head (1 when the max did not move);
-//   value waves 4-7, 32 heads x 256 channels each (v_mfma_f32_32x32x16_bf16): O^T = alpha O^T +
-//     V^T P^T for step t - 1, with V^T through the LDS transpose read.
+//   value waves 4-7, all 64 heads x 128 channels each (v_mfma_f32_32x32x16_bf16, two 32-head
+//     blocks per V^T fragment): O^T = alpha O^T + V^T P^T for step t - 1, with V^T through the
+//     LDS transpose read.
 // One barrier per step: past it, step t's rows are in LDS for the score waves and step t-1's P
 // for the value waves, and the ring slot of step t-2 takes the copies of step t+2. A gathered row
-// is read from LDS four times for QK and twice for PV (mla_bf16_kernel: four and four, plus
-// the partial-score exchange), 204 KB per 32-row step instead of 288 KB.
+// is read from LDS four times for QK and once for PV (mla_bf16_kernel: four and four, plus
+// the partial-score exchange).
 // Lane layouts of the 32x32x16 MFMA: lane l supplies A[l % 32][k] and B[k][l % 32] for
 // k = 8 (l / 32) .. + 7, and receives D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32] in accumulator
 // register i.
@@ -628,7 +629,7 @@ __global__ __launch_bounds__(512, 1) void mla_roles_kernel(MlaArgs a) {
   constexpr int D = 512, R = kStepRows, NT = 512, NS = kRolesSlots;
   constexpr int RS = RowLayout<D, true>::RS, SLOT = R * RS;
   constexpr int VR = R / 4;                       // rows each value wave copies per step
-  constexpr int KSS = D / 32, DH = D / 2;
+  constexpr int KSS = D / 32;
   __shared__ __align__(16) uint8_t ring[NS * SLOT];
   __shared__ uint64_t rows[kMaxList];             // resolved row entries, 0 = masked
   __shared__ __align__(16) uint8_t pbuf[2][64][R * 2 + 16];   // P^T: [head][row] bf16, rows padded
@@ -740,11 +741,14 @@ __global__ __launch_bounds__(512, 1) void mla_roles_kernel(MlaArgs a) {
     return;
   }
 
-  // ---- value wave: heads hp * 32 + l32 of the group, channels cb0 .. cb0 + 255; it also copies
-  // rows 8 vw .. 8 vw + 7 of every step (the score waves' path is the longer one)
-  const int vw = wave - 4, hp = vw & 1, cb0 = (vw >> 1) * DH;
+  // ---- value wave: all 64 heads of the group (two 32-head blocks hb, head hb * 32 + l32),
+  // channels cb0 .. cb0 + 127; it also copies rows 8 vw .. 8 vw + 7 of every step (the score
+  // waves' path is the longer one). Each V^T fragment feeds both head blocks, so a staged row is
+  // read once for PV (four waves of 32 heads x 256 channels read it twice: 64 KB of LDS reads per
+  // 32-row step instead of 32 KB, against 16 KB of P^T reads instead of 8).
+  constexpr int DQ = D / 4;                       // channels per value wave
+  const int vw = wave - 4, cb0 = vw * DQ;
   const int l32 = lane & 31, hi = lane >> 5, q4 = lane >> 4, r16 = lane & 15;
-  const int hl = hp * 32 + l32;
   const uint32_t ring_base = lds_offset(ring);
   const PackedBase pbase = packed_base<CF>(S, b);
   auto entry_of = [&](int t) -> uint64_t {
@@ -765,11 +769,13 @@ __global__ __launch_bounds__(512, 1) void mla_roles_kernel(MlaArgs a) {
   const int xl = jv ^ row_swz(vrb), xh = jv ^ row_swz(vrb + 4), e8 = 8 * (r16 & 1);
   const int vlo[4] = {16 * xl + e8, 16 * (4 ^ xl) + e8, 16 * (8 ^ xl) + e8, 16 * (12 ^ xl) + e8};
   const int vhi[4] = {16 * xh + e8, 16 * (4 ^ xh) + e8, 16 * (8 ^ xh) + e8, 16 * (12 ^ xh) + e8};
-  f32x16 acc[DH / 32];
+  f32x16 acc[DQ / 32][2];
 #pragma unroll
-  for (int ct = 0; ct < DH / 32; ++ct)
+  for (int ct = 0; ct < DQ / 32; ++ct)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[ct][i] = 0.0f;
+    for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[ct][hb][i] = 0.0f;
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();                                // rows[] complete
   for (int t = 0; t < NS - 2 && t < nsteps; ++t) issue(t, entry_of(t));
@@ -784,36 +790,53 @@ __global__ __launch_bounds__(512, 1) void mla_roles_kernel(MlaArgs a) {
     if (t + NS - 2 < nsteps) issue(t + NS - 2, mp);   // into step t-2's slot
     if (t == 0) continue;
     const int s = t - 1;
-    const float alpha = abuf[s & 1][hl];
-    if (__any(alpha != 1.0f)) {
 #pragma unroll
-      for (int ct = 0; ct < DH / 32; ++ct) acc[ct] *= alpha;
+    for (int hb = 0; hb < 2; ++hb) {
+      const float alpha = abuf[s & 1][hb * 32 + l32];
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int ct = 0; ct < DQ / 32; ++ct) acc[ct][hb] *= alpha;
+      }
     }
-    // P^T as the B operand of two 16-row k-steps: rows 16 kk + 8 hi .. + 7 of head hl
-    const uint8_t* pt = &pbuf[s & 1][hl][0];
-    const bf16x8 pb0 = ld_bf16x8(pt + (8 * hi) * 2), pb1 = ld_bf16x8(pt + (16 + 8 * hi) * 2);
+    // P^T as the B operand of two 16-row k-steps per head block: rows 16 kk + 8 hi .. + 7 of head
+    // hb * 32 + l32
+    bf16x8 pbk[2][2];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      const uint8_t* pt = &pbuf[s & 1][hb * 32 + l32][0];
+      pbk[hb][0] = ld_bf16x8(pt + (8 * hi) * 2);
+      pbk[hb][1] = ld_bf16x8(pt + (16 + 8 * hi) * 2);
+    }
     const uint8_t* buf = ring + (s % NS) * SLOT + 2 * cb0;
 #pragma unroll
-    for (int ct = 0; ct < DH / 32; ++ct) {
+    for (int ct = 0; ct < DQ / 32; ++ct) {
       const uint8_t* col = buf + 256 * (ct >> 2);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const i16x4 lo4 = lds_read_tr16(col + (16 * kk + vrb) * RS + vlo[ct & 3]);
         const i16x4 hi4 = lds_read_tr16(col + (16 * kk + vrb + 4) * RS + vhi[ct & 3]);
-        acc[ct] = mfma32x32x16(join_bf16x8(lo4, hi4), kk ? pb1 : pb0, acc[ct]);
+        const bf16x8 vt = join_bf16x8(lo4, hi4);
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) acc[ct][hb] = mfma32x32x16(vt, pbk[hb][kk], acc[ct][hb]);
       }
     }
   }
   __syncthreads();                                // denominators written
-  const float den = lbuf[hl];
-  bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + hg * 64 + hl) * D;
-  // accumulator register i of tile ct: channel cb0 + 32 ct + 8 (i / 4) + 4 hi + i % 4
+  // accumulator register i of tile (ct, hb): channel cb0 + 32 ct + 8 (i / 4) + 4 hi + i % 4 of
+  // head hb * 32 + l32
 #pragma unroll
-  for (int ct = 0; ct < DH / 32; ++ct)
+  for (int hb = 0; hb < 2; ++hb) {
+    const int hl = hb * 32 + l32;
+    const float den = lbuf[hl];
+    bf16_t* orow = reinterpret_cast<bf16_t*>(a.o) + ((int64_t)unit * a.heads + hg * 64 + hl) * D;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      store_out4(a, D, qs, orow, cb0 + 32 * ct + 8 * j + 4 * hi,
-                 f32x4{acc[ct][4 * j], acc[ct][4 * j + 1], acc[ct][4 * j + 2], acc[ct][4 * j + 3]}, den);
+    for (int ct = 0; ct < DQ / 32; ++ct)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        store_out4(a, D, qs, orow, cb0 + 32 * ct + 8 * j + 4 * hi,
+                   f32x4{acc[ct][hb][4 * j], acc[ct][hb][4 * j + 1], acc[ct][hb][4 * j + 2], acc[ct][hb][4 * j + 3]},
+                   den);
+  }
 }
 
 // Merges split partials of one query: one wave per head, 4 heads per workgroup; the workgroups
