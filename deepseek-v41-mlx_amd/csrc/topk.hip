@@ -346,12 +346,12 @@ int topk_merge_launch(const char* what, const uint32_t* ckey, const int32_t* cpo
 
 // The two-stage form for a row of nb scores: rows longer than one 16-keys-per-thread workgroup
 // holds, k at most half a chunk, and the chunk lists small enough for one register workgroup.
-// With k a quarter of a chunk or more, a row that one 32-keys-per-thread workgroup holds selects
-// faster in one stage (16 rows of 32,768 scores, k = 1,024: 17.5 against 19.4 us; at k = 512 the
-// two stages win, 13.4 against 17.4 us).
+// For 16 rows of 32,768 scores and k = 1,024 one 32-keys-per-thread workgroup per row is faster
+// on scores already in cache (17.5-19.3 against 19.4-20.2 us), but inside a decode step, reading
+// the scores the scoring kernel has just written, the two stages spread that read over 8
+// workgroups per row and win: the 40-layer fp8 step took 1.163-1.166 ms against 1.190-1.195 ms.
 static bool topk_two_stage(int nb, int k, int* chunks, int* jm) {
   if (nb <= 16 * kSelThreads || 2 * k > kTopkChunk) return false;
-  if (4 * k >= kTopkChunk && nb <= 32 * kSelThreads) return false;
   const int c = (nb + kTopkChunk - 1) / kTopkChunk;
   const int64_t m = (int64_t)c * k;
   if (m > 32 * kSelThreads) return false;
