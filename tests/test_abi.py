@@ -123,13 +123,12 @@ def test_contract_violations_are_reported_by_the_library():
 
 def test_topk_workspace_sizes():
     """Two stages (a workspace) only for rows over 16384 scores with k <= 2048 whose chunk lists
-    fit one register workgroup: keys and positions of each 4096-score chunk's best k. With k a
-    quarter of a chunk or more, rows one 32-keys-per-thread workgroup holds stay one stage."""
+    fit one register workgroup: keys and positions of each 4096-score chunk's best k."""
     from dsv41 import _abi
     assert _abi.topk_workspace_bytes(32, 16384, 512) == 0            # one workgroup per row
     assert _abi.topk_workspace_bytes(16, 20000, 5000) == 0           # k above half a chunk
     assert _abi.topk_workspace_bytes(1, 4 << 20, 2048) == 0          # lists too long for one stage-2 group
-    assert _abi.topk_workspace_bytes(16, 32768, 1024) == 0           # k = chunk / 4, row <= 32K: one stage
+    assert _abi.topk_workspace_bytes(16, 32768, 1024) == 2 * 16 * 8 * 1024 * 4   # k = chunk / 4: two stages too
     assert _abi.topk_workspace_bytes(1, 40000, 1024) == 2 * ((10 * 1024 * 4 + 255) // 256 * 256)   # row > 32K
     assert _abi.topk_workspace_bytes(16, 32768, 512) == 2 * 16 * 8 * 512 * 4
     assert _abi.topk_workspace_bytes(3, 16390, 512) == 2 * (((3 * 5 * 512 * 4) + 255) // 256 * 256)
@@ -407,6 +406,10 @@ def test_fake_quant_rope_norm_wrappers_check_out(host_abi):
     _reaches_launch(lambda: A.linear_rows(xb, torch.zeros(64, 128, dtype=torch.bfloat16)))
     _refused(lambda: A.linear_rows(xb, torch.zeros(64, 96, dtype=torch.bfloat16)), "contract")
     _refused(lambda: A.linear_rows(xb.float(), torch.zeros(64, 128)), "bfloat16")
+    wa, wb = torch.zeros(64, 128, dtype=torch.bfloat16), torch.zeros(32, 128, dtype=torch.bfloat16)
+    _reaches_launch(lambda: A.linear_rows_pair(xb, wa, wb))
+    _refused(lambda: A.linear_rows_pair(xb, wa, torch.zeros(32, 96, dtype=torch.bfloat16)), "contract")
+    _refused(lambda: A.linear_rows_pair(xb, wa, wb.float()), "bfloat16")
 
 
 def test_cache_writers_check_batch_rows_and_parameters(host_abi):
