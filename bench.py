@@ -843,7 +843,9 @@ def run_token(args, torch, device, B=64, start=65535):
         "workload": f"one decode token through AttentionStack (40 layers, C4 sharing layout, release widths: "
                     f"dim {a.dim}, q LoRA {a.q_lora_rank}, {a.n_heads} x {a.head_dim} heads, indexer "
                     f"{a.index_n_heads} x {a.index_head_dim}, wo_a {a.o_groups} x {a.o_lora_rank}), B={B}, "
-                    f"{start + 1}-token context, bf16 weights and caches; projections are torch GEMMs",
+                    f"{start + 1}-token context, bf16 weights and caches; wq_a + wkv, wq_b, wo_b and the "
+                    f"indexer's wq_b and weights_proj on dsv41_linear_rows(_pair), the compressor's fp32 "
+                    f"projections torch GEMMs",
         "token_ms": ms, "token_ms_eager": eager_ms, "tokens_per_s": B / (ms * 1e-3), "steps": reps,
         "weight_bytes": weight_bytes, "cache_algorithmic_bytes": cache_bytes,
         "token_algorithmic_bytes": nbytes, "hbm_GBps_token": gbs, "hbm_frac_token": gbs / HBM_PEAK_GBS,

@@ -32,6 +32,8 @@ struct WoaArgs {
   void* out;           // [rows, groups * r], bf16 or fp32
   int rows, groups, d, r;
   int split;           // 1: one dense weight whose contraction is cut into `groups` ranges of d
+  const bf16_t* w1;    // split only: weight rows [r0, r) come from w1 [r - r0, groups * d]
+  int r0;              // (two weights applied to the same rows; r0 a multiple of the tile's rows)
 };
 
 // ------------------------------------------------------------------ any shape
@@ -161,10 +163,14 @@ __global__ __launch_bounds__(64 * GR * GM, (TileCfg<WR, WM, GR, GM, BK, NS>::LDS
   for (int j = 0; j < C::NW; ++j) {
     const int row = wave * (C::TR / C::NWV) + j * C::RPI + lane / C::CPR;
     const int chunk = (lane % C::CPR) ^ tile_swz<BK>(row);
-    // grouped: group grp's weight rows; split: range grp of every weight row (row stride groups * d)
-    const int64_t wrow = a.split ? (int64_t)(rt * C::TR + row) * ((int64_t)a.groups * a.d) + (int64_t)grp * a.d
-                                 : ((int64_t)grp * a.r + rt * C::TR + row) * a.d;
-    wsrc[j] = reinterpret_cast<uint64_t>(a.w + wrow + 8 * chunk);
+    // grouped: group grp's weight rows; split: range grp of every weight row (row stride groups * d),
+    // rows from r0 on in w1 when it is given
+    const int wr_all = rt * C::TR + row;
+    const bool second = a.w1 != nullptr && wr_all >= a.r0;
+    const bf16_t* wbase = second ? a.w1 : a.w;
+    const int64_t wrow = a.split ? (int64_t)(second ? wr_all - a.r0 : wr_all) * ((int64_t)a.groups * a.d) + (int64_t)grp * a.d
+                                 : ((int64_t)grp * a.r + wr_all) * a.d;
+    wsrc[j] = reinterpret_cast<uint64_t>(wbase + wrow + 8 * chunk);
   }
 #pragma unroll
   for (int j = 0; j < C::NO; ++j) {
@@ -241,14 +247,32 @@ static void launch_tiles(const WoaArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((wo_a_tiles_kernel<WR, WM, GR, GM, BK, NS, TO>), dim3((unsigned)tiles), dim3(C::NT), 0, stream, a);
 }
 
+// Split contraction at 33-64 query rows: 128-row weight tiles where each range is long (>= 1024
+// channels) and the tiles fill the chip once (128-256 workgroups). A 32-row tile reads the 64 query
+// rows from L2 for every 32 weight rows it streams, twice the weight's bytes; a 128-row one half of
+// them (measured at 64 rows: wq_b 1280 -> 32768 19.1 us against 21.5 for hipBLASLt, wo_b
+// 8192 -> 5120 in 4 ranges 25.5 against 29.0; 32-row tiles 32.8 us for wo_b).
+__host__ __device__ inline bool wide_split_tiles(int rows, int d, int n, int ranges) {
+  const int64_t t = (int64_t)(n / 128) * ranges;
+  return rows > 32 && rows <= 64 && n % 128 == 0 && d >= 1024 && t >= 128 && t <= 256;
+}
+
 template <typename TO>
 static void launch_wo_a(const WoaArgs& a, hipStream_t stream) {
   // decode: 32 weight rows x every query row per workgroup (groups * r / 32 workgroups), an
   // eight-stage copy ring (four at 128 rows, whose stage is 20 KB)
   if (a.rows <= 128) {
+    const int64_t tiles = (int64_t)a.groups * (a.r / 32);
+    if (a.split && wide_split_tiles(a.rows, a.d, a.r, a.groups) && (a.w1 == nullptr || a.r0 % 128 == 0)) {
+      launch_tiles<4, 2, 2, 2, 64, 4, TO>(a, stream);   // 128 weight rows x 64 query rows, 96 KB
+      return;
+    }
     switch ((a.rows + 31) / 32) {
       case 1: launch_tiles<1, 1, 2, 2, 64, 8, TO>(a, stream); break;
-      case 2: launch_tiles<1, 2, 2, 2, 64, 8, TO>(a, stream); break;
+      case 2:
+        if (tiles > 256) launch_tiles<1, 2, 2, 2, 64, 6, TO>(a, stream);   // 72 KB: two per CU
+        else launch_tiles<1, 2, 2, 2, 64, 8, TO>(a, stream);
+        break;
       case 3: launch_tiles<1, 3, 2, 2, 64, 8, TO>(a, stream); break;
       default: launch_tiles<1, 4, 2, 2, 64, 4, TO>(a, stream); break;
     }
@@ -311,13 +335,16 @@ extern "C" int dsv41_wo_a_grouped(const void* o, const void* wo_a, void* out, in
 
 namespace dsv41 {
 // y[m, j] = sum over the ranges s (in order) of part[m, s * n + j], rounded to bf16 once; four
-// consecutive outputs per thread.
+// consecutive outputs per thread. With y1, columns j >= n0 go to y1 [rows, n - n0] and the rest to
+// y [rows, n0] (n0 a multiple of 4).
 __global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restrict__ part, bf16_t* __restrict__ y,
-                                                            int rows, int n, int splits) {
+                                                            bf16_t* __restrict__ y1, int rows, int n, int n0,
+                                                            int splits) {
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;   // over rows * n
   if (i >= (int64_t)rows * n) return;
   const int64_t m = i / n;
   const int j = (int)(i - m * n);
+  bf16_t* dst = y1 == nullptr ? y + i : (j < n0 ? y + m * n0 + j : y1 + m * (n - n0) + (j - n0));
   const float* p = part + m * (int64_t)splits * n + j;
   f32x4 acc = *reinterpret_cast<const f32x4*>(p);
   for (int sidx = 1; sidx < splits; ++sidx) {
@@ -328,7 +355,7 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restr
   uint2 st;
   st.x = pack2_bf16(acc[0], acc[1]);
   st.y = pack2_bf16(acc[2], acc[3]);
-  *reinterpret_cast<uint2*>(y + i) = st;
+  *reinterpret_cast<uint2*>(dst) = st;
 }
 }  // namespace dsv41
 
@@ -337,30 +364,52 @@ extern "C" size_t dsv41_linear_rows_workspace_bytes(int32_t rows, int32_t n, int
   return (size_t)rows * (size_t)splits * (size_t)n * sizeof(float);
 }
 
-extern "C" int dsv41_linear_rows(const void* x, const void* w, void* y, void* workspace, size_t workspace_bytes,
-                                 int32_t rows, int32_t k, int32_t n, int32_t splits, int32_t dtype,
-                                 hipStream_t stream) {
-  const char* what = "dsv41_linear_rows";
-  DSV41_REQUIRE(x && w && y, DSV41_E_ARG, "%s: null tensor", what);
+// y = x w^T (or, with w1, y = x w^T and y1 = x w1^T in one launch) at decode row counts; n is the
+// total width n0 + n1 of the two outputs.
+static int run_linear_rows(const char* what, const void* x, const void* w, const void* w1, void* y, void* y1,
+                           void* workspace, size_t workspace_bytes, int32_t rows, int32_t k, int32_t n0, int32_t n1,
+                           int32_t splits, int32_t dtype, hipStream_t stream) {
+  const bool pair = w1 != nullptr;
+  DSV41_REQUIRE(x && w && y && (!pair || y1), DSV41_E_ARG, "%s: null tensor", what);
   DSV41_REQUIRE(dtype == DSV41_BF16, DSV41_E_DTYPE, "%s: bf16 only (dtype %d)", what, dtype);
-  DSV41_REQUIRE(rows >= 0 && rows <= 128 && k > 0 && n > 0, DSV41_E_ARG, "%s: rows %d (at most 128), k %d, n %d", what,
-                rows, k, n);
+  DSV41_REQUIRE(rows >= 0 && rows <= 128 && k > 0 && n0 > 0 && n1 >= 0 && (int64_t)n0 + n1 < (1 << 30), DSV41_E_ARG,
+                "%s: rows %d (at most 128), k %d, n %d + %d", what, rows, k, n0, n1);
   DSV41_REQUIRE(splits >= 1 && splits <= 64 && k % (64 * splits) == 0, DSV41_E_SHAPE,
                 "%s: k = %d must split into %d ranges of whole 64-channel steps", what, k, splits);
-  DSV41_REQUIRE(n % 32 == 0, DSV41_E_SHAPE, "%s: n = %d must be a multiple of 32", what, n);
-  DSV41_REQUIRE(aligned16(x) && aligned16(w) && aligned16(y), DSV41_E_ARG, "%s: tensors must be 16-byte aligned", what);
+  DSV41_REQUIRE(!pair || splits >= 2, DSV41_E_SHAPE, "%s: two weights need at least 2 contraction ranges", what);
+  DSV41_REQUIRE(n0 % 32 == 0 && n1 % 32 == 0, DSV41_E_SHAPE, "%s: n = %d (+ %d) must be multiples of 32", what, n0,
+                n1);
+  DSV41_REQUIRE(aligned16(x) && aligned16(w) && aligned16(y) && (!pair || (aligned16(w1) && aligned16(y1))),
+                DSV41_E_ARG, "%s: tensors must be 16-byte aligned", what);
   if (rows == 0) return 0;
+  const int n = n0 + n1;
   const size_t need = dsv41_linear_rows_workspace_bytes(rows, n, splits);
   DSV41_REQUIRE(workspace_bytes >= need && (need == 0 || (workspace && aligned16(workspace))), DSV41_E_WORKSPACE,
                 "%s: workspace of %zu bytes needed, %zu given", what, need, workspace_bytes);
   WoaArgs a{static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(w), splits > 1 ? workspace : y, rows, splits,
-            k / splits, n, 1};
+            k / splits, n, 1, static_cast<const bf16_t*>(w1), n0};
   if (splits > 1) launch_wo_a<float>(a, stream);
   else launch_wo_a<bf16_t>(a, stream);
   int rc = check_launch(what);
   if (rc || splits <= 1) return rc;
   const int64_t quads = ((int64_t)rows * n) / 4;
   hipLaunchKernelGGL(linear_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
-                     static_cast<const float*>(workspace), static_cast<bf16_t*>(y), rows, n, splits);
+                     static_cast<const float*>(workspace), static_cast<bf16_t*>(y), static_cast<bf16_t*>(y1), rows,
+                     n, n0, splits);
   return check_launch(what);
+}
+
+extern "C" int dsv41_linear_rows(const void* x, const void* w, void* y, void* workspace, size_t workspace_bytes,
+                                 int32_t rows, int32_t k, int32_t n, int32_t splits, int32_t dtype,
+                                 hipStream_t stream) {
+  return run_linear_rows("dsv41_linear_rows", x, w, nullptr, y, nullptr, workspace, workspace_bytes, rows, k, n, 0,
+                         splits, dtype, stream);
+}
+
+extern "C" int dsv41_linear_rows_pair(const void* x, const void* w0, const void* w1, void* y0, void* y1,
+                                      void* workspace, size_t workspace_bytes, int32_t rows, int32_t k, int32_t n0,
+                                      int32_t n1, int32_t splits, int32_t dtype, hipStream_t stream) {
+  const char* what = "dsv41_linear_rows_pair";
+  DSV41_REQUIRE(w1 != nullptr && n1 > 0, DSV41_E_ARG, "%s: the second weight is missing", what);
+  return run_linear_rows(what, x, w0, w1, y0, y1, workspace, workspace_bytes, rows, k, n0, n1, splits, dtype, stream);
 }

@@ -97,6 +97,7 @@ _SIGNATURES = {
     "dsv41_wo_a_grouped": [_c_p, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_linear_rows_workspace_bytes": [_i32, _i32, _i32],
     "dsv41_linear_rows": [_c_p, _c_p, _c_p, _c_p, _sz, _i32, _i32, _i32, _i32, _i32, _c_p],
+    "dsv41_linear_rows_pair": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _sz, _i32, _i32, _i32, _i32, _i32, _i32, _c_p],
     "dsv41_comp_write_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _i32, _i32, _i32, _i32, _i32, _i32,
                              _i32, _c_p],
     "dsv41_index_key_publish_fp8": [_c_p, _c_p, _i64, _c_p, _i64, _i32, _c_p, _c_p, _c_p, _i32, _i32, _i32, _i32,
@@ -524,10 +525,22 @@ def wo_a_grouped(o, wo_a, groups, out=None, out_dtype=None):
     return out
 
 
-def linear_rows_splits(k: int, n: int) -> int:
-    """Contraction ranges for dsv41_linear_rows: the most ranges (of whole 64-channel steps, at
-    most 64) that keep the n / 32 x ranges workgroups within one wave of the chip (256: one
-    workgroup per CU; a 320-workgroup wq_a ran a second round of 64 and took 9.0 us)."""
+def linear_rows_wide(rows: int, k: int, n: int, splits: int) -> bool:
+    """Whether dsv41_linear_rows takes its 128-row weight tiles for this call (the kernel's own rule,
+    out_proj.hip wide_split_tiles): 33-64 rows, n a multiple of 128, each contraction range at
+    least 1024 channels, and n / 128 x splits between 128 and 256 workgroups."""
+    t = (n // 128) * splits
+    return 32 < rows <= 64 and n % 128 == 0 and k // splits >= 1024 and 128 <= t <= 256
+
+
+def linear_rows_splits(k: int, n: int, rows: int = 64) -> int:
+    """Contraction ranges for dsv41_linear_rows (whole 64-channel steps, at most 64). At 33-64 rows
+    the most ranges that give the 128-row tiles (linear_rows_wide) when some do; otherwise the most
+    that keep the n / 32 x ranges workgroups within one wave of the chip (256: one workgroup per
+    CU; a 320-workgroup wq_a ran a second round of 64 and took 9.0 us)."""
+    wide = [s for s in range(1, 65) if k % (64 * s) == 0 and linear_rows_wide(rows, k, n, s)]
+    if wide:
+        return max(wide)
     tiles = max(n // 32, 1)
     best = 1
     for s in range(1, 65):
@@ -536,27 +549,52 @@ def linear_rows_splits(k: int, n: int) -> int:
     return best
 
 
+def _linear_args(name, x, *ws):
+    _gpu(name, x, *ws)
+    _contig(name, x, *ws)
+    if x.dtype != torch.bfloat16 or any(w.dtype != torch.bfloat16 for w in ws):
+        raise ValueError(f"{name}: x and w must be bfloat16")
+    for w in ws:
+        if w.dim() != 2 or x.shape[-1] != w.shape[1]:
+            raise ValueError(f"{name}: x {tuple(x.shape)} and w {tuple(w.shape)} do not contract")
+    return ws[0].shape[1], x.numel() // ws[0].shape[1]
+
+
 def linear_rows(x, w, splits=None, out=None, workspace=None):
     """y = x @ w^T for decode row counts (at most 128 rows of x [..., k]; w [n, k] the Linear
-    weight, read in place), bf16: the projections of attention.py:114-116 on the decode tile
-    kernel with the contraction split over `splits` ranges (linear_rows_splits by default)."""
+    weight, read in place), bf16: the projections of attention.py:114-116 and :179 on the decode
+    tile kernel with the contraction split over `splits` ranges (linear_rows_splits by default)."""
     name = "dsv41_linear_rows"
-    _gpu(name, x, w, out)
-    _contig(name, x, w)
-    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
-        raise ValueError(f"{name}: x and w must be bfloat16")
-    if w.dim() != 2 or x.shape[-1] != w.shape[1]:
-        raise ValueError(f"{name}: x {tuple(x.shape)} and w {tuple(w.shape)} do not contract")
-    n, k = w.shape
-    rows = x.numel() // k
+    k, rows = _linear_args(name, x, w)
+    n = w.shape[0]
     if splits is None:
-        splits = linear_rows_splits(k, n)
+        splits = linear_rows_splits(k, n, rows)
     out = _out(name, out, (*x.shape[:-1], n), torch.bfloat16, x.device)
     need = lib().dsv41_linear_rows_workspace_bytes(rows, n, splits)
     ws = _ws(name, workspace, need, x.device)
     _call(name, _ptr(x), _ptr(w), _ptr(out), _ptr(ws) if ws is not None else None, need, rows, k, n, splits,
           dtype_code(x, name), _stream(x))
     return out
+
+
+def linear_rows_pair(x, w0, w1, splits=None, out0=None, out1=None, workspace=None):
+    """(x @ w0^T, x @ w1^T) in one launch for decode row counts -- wq_a(x) and wkv(x) of
+    attention.py:114/:116 -- each weight read in place; every output equals linear_rows on its
+    own weight with the same ranges (linear_rows_splits over the stacked width by default, at
+    least 2)."""
+    name = "dsv41_linear_rows_pair"
+    k, rows = _linear_args(name, x, w0, w1)
+    n0, n1 = w0.shape[0], w1.shape[0]
+    if splits is None:
+        splits = max(linear_rows_splits(k, n0 + n1, rows), 2)
+    out0 = _out(name, out0, (*x.shape[:-1], n0), torch.bfloat16, x.device)
+    out1 = _out(name, out1, (*x.shape[:-1], n1), torch.bfloat16, x.device)
+    need = lib().dsv41_linear_rows_workspace_bytes(rows, n0 + n1, splits)
+    ws = _ws(name, workspace, need, x.device)
+    _call(name, _ptr(x), _ptr(w0), _ptr(w1), _ptr(out0), _ptr(out1), _ptr(ws) if ws is not None else None, need,
+          rows, k, n0, n1, splits, dtype_code(x, name), _stream(x))
+    return out0, out1
+
 
 def comp_write_fp4(latents, comp_kv4, g0, ratio, cos, sin, rd):
     """comp_write into a packed fp4 cache: comp_kv4 uint8 [b, >=g0+g, d/2 + d/16], per row the

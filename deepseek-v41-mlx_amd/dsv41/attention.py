@@ -1,7 +1,10 @@
 """One V4.1 attention layer (deepseek_v41_mlx/attention.py:53-179) on the GPU.
 
-The dense projections (wq_b, the compressor projections, wo_b) are torch GEMMs; at decode row
-counts wq_a, wkv and the indexer's wq_b run on dsv41_linear_rows (layers.decode_linear).
+The compressor projections are torch GEMMs, and so are the other projections outside decode row
+counts. At decode row counts wq_a and wkv run in one dsv41_linear_rows_pair launch, the indexer's
+wq_b and weights_proj on dsv41_linear_rows, and wq_b and wo_b on dsv41_linear_rows where its
+128-row tiles apply (33-64 rows at the release's widths); otherwise they stay torch GEMMs
+(layers.decode_linear).
 Everything between them, and the grouped block-diagonal wo_a, runs in HIP kernels:
 
   q      : q_norm (RMSNorm kernel); q's rope tail is applied by the attention launch as it
@@ -38,7 +41,7 @@ from . import _abi, fakequant
 from .compressor import Compressor
 from .config import ModelArgs
 from .indexer import Indexer
-from .layers import RMSNorm, decode_linear, yarn_inv_freqs
+from .layers import RMSNorm, decode_linear, decode_linear_pair, yarn_inv_freqs
 
 
 # multiply-adds from which fp32 activations take the batched GEMM for wo_a (the release shape
@@ -154,12 +157,14 @@ class Attention(torch.nn.Module):
         cos, sin = self._freqs(end_pos)
         x = x.contiguous()
 
+        # wq_a and wkv read the same rows: one launch at decode row counts
+        qa, kv_raw = decode_linear_pair(self.wq_a, self.wkv, x)
         # queries: q's rope tail (attention.py:117) is applied by the attention launch as it loads q
-        qr = self.q_norm(decode_linear(self.wq_a, x))
-        q = self.wq_b(qr).view(bsz, n, self.n_heads, self.head_dim).contiguous()
+        qr = self.q_norm(qa)
+        q = decode_linear(self.wq_b, qr, wide_only=True).view(bsz, n, self.n_heads, self.head_dim).contiguous()
 
         # this chunk's window KV
-        kv = self._kv_prologue(decode_linear(self.wkv, x).contiguous(), cos, sin, start_pos)
+        kv = self._kv_prologue(kv_raw.contiguous(), cos, sin, start_pos)
 
         lc = cache.layers[self.layer_id]
         wp = min(start_pos, self.window_size)
@@ -223,7 +228,9 @@ class Attention(torch.nn.Module):
             lc.write_window(start_pos, kv)
 
         # grouped block-diagonal wo_a, fp32 sums cast to x's dtype, then wo_b (attention.py:176-179)
-        return self.wo_b(self._wo_a(o.view(bsz, n, -1), x.dtype))
+        # wo_b at 33-64 rows: 128-row tiles over 4 contraction ranges and their reduce (24.4 + 4.5
+        # us at 64 rows against 28.9 us for the library; the 40-layer token 5.748 against 5.78 ms)
+        return decode_linear(self.wo_b, self._wo_a(o.view(bsz, n, -1), x.dtype), wide_only=True)
 
     def _wo_a(self, o, out_dtype):
         g, r = self.n_groups, self.o_lora_rank

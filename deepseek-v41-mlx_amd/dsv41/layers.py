@@ -37,13 +37,35 @@ class RMSNorm(torch.nn.Module):
 DECODE_ROWS = 128
 
 
-def decode_linear(lin: torch.nn.Linear, x: torch.Tensor) -> torch.Tensor:
+def _decode_ok(lin: torch.nn.Linear, x: torch.Tensor) -> bool:
     w = lin.weight
-    rows = x.numel() // x.shape[-1]
-    if (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.is_cuda and lin.bias is None
-            and rows <= DECODE_ROWS and w.shape[1] % 64 == 0 and w.shape[0] % 32 == 0):
-        return _abi.linear_rows(x.contiguous(), w)
+    return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.is_cuda and lin.bias is None
+            and x.numel() // x.shape[-1] <= DECODE_ROWS and w.dim() == 2 and w.is_contiguous()
+            and w.shape[1] % 64 == 0 and w.shape[0] % 32 == 0)
+
+
+def decode_linear(lin: torch.nn.Linear, x: torch.Tensor, wide_only: bool = False) -> torch.Tensor:
+    """lin(x) on dsv41_linear_rows at decode row counts, else torch's linear. wide_only: only where
+    the 128-row tiles apply (the large projections wq_b and wo_b, 84 MB each at the release's
+    widths, where the 32-row tiles lose to the library: wo_b 32.8 against 29.0 us at 64 rows)."""
+    if _decode_ok(lin, x):
+        k, n = lin.weight.shape[1], lin.weight.shape[0]
+        rows = x.numel() // k
+        splits = _abi.linear_rows_splits(k, n, rows)
+        if not wide_only or _abi.linear_rows_wide(rows, k, n, splits):
+            return _abi.linear_rows(x.contiguous(), lin.weight, splits)
     return lin(x)
+
+
+def decode_linear_pair(lin0: torch.nn.Linear, lin1: torch.nn.Linear, x: torch.Tensor):
+    """(lin0(x), lin1(x)) in one dsv41_linear_rows_pair launch at decode row counts (wq_a and wkv of
+    attention.py:114/:116: 10.9 us at 64 rows against 10.2 + 8.4 us for the two calls), else the two
+    decode_linear calls."""
+    k = x.shape[-1]
+    if (_decode_ok(lin0, x) and _decode_ok(lin1, x) and lin0.weight.shape[1] == lin1.weight.shape[1]
+            and k % 128 == 0):
+        return _abi.linear_rows_pair(x.contiguous(), lin0.weight, lin1.weight)
+    return decode_linear(lin0, x), decode_linear(lin1, x)
 
 def yarn_inv_freqs(dim: int, original_seq_len: int, base: float, factor: float,
                    beta_fast: int, beta_slow: int) -> np.ndarray:

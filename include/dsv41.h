@@ -510,10 +510,11 @@ int dsv41_wo_a_grouped(const void* o, const void* wo_a, void* out, int32_t rows,
                        int32_t d, int32_t r, int32_t dtype, int32_t out_dtype, hipStream_t stream);
 
 /* The dense projections of Attention.__call__ at decode row counts, deepseek_v41_mlx/attention.py:
- * 114-116 (wq_a and wkv on the block input: nn.Linear, y = x @ w^T): x [rows, k] and the Linear
+ * 114-116 and 179 (wq_a, wq_b, wkv and wo_b: nn.Linear, y = x @ w^T): x [rows, k] and the Linear
  * weight w [n, k] as they lie, bf16, y [rows, n] bf16 (fp32 sums rounded once). For rows <= 128
  * the weight is streamed once by the decode tile kernel of dsv41_wo_a_grouped, with the
- * contraction cut into `splits` ranges so that n / 32 x splits workgroups fill the chip; each
+ * contraction cut into `splits` ranges so that the workgroups fill the chip (n / 32 x splits; at
+ * 33-64 rows n / 128 x splits when each range holds >= 1024 channels and that gives 128-256); each
  * range's fp32 partial goes to `workspace` ([rows, splits * n] floats,
  * dsv41_linear_rows_workspace_bytes; none for splits == 1) and a second kernel sums them in
  * range order: deterministic, equal to the reference up to the order of fp32 additions.
@@ -522,6 +523,15 @@ size_t dsv41_linear_rows_workspace_bytes(int32_t rows, int32_t n, int32_t splits
 int dsv41_linear_rows(const void* x, const void* w, void* y, void* workspace, size_t workspace_bytes,
                       int32_t rows, int32_t k, int32_t n, int32_t splits, int32_t dtype,
                       hipStream_t stream);
+
+/* Two projections of the same rows in one launch, deepseek_v41_mlx/attention.py:114 and :116
+ * (wq_a(x) and wkv(x)): y0 = x @ w0^T [rows, n0] and y1 = x @ w1^T [rows, n1], each weight as it
+ * lies. The same arithmetic and order of additions as dsv41_linear_rows over the two weights
+ * stacked, so each output equals that call's on its own weight when the split is the same.
+ * splits >= 2; the workspace is dsv41_linear_rows_workspace_bytes(rows, n0 + n1, splits). */
+int dsv41_linear_rows_pair(const void* x, const void* w0, const void* w1, void* y0, void* y1,
+                           void* workspace, size_t workspace_bytes, int32_t rows, int32_t k, int32_t n0,
+                           int32_t n1, int32_t splits, int32_t dtype, hipStream_t stream);
 
 #ifdef __cplusplus
 }

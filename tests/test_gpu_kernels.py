@@ -1326,6 +1326,10 @@ def test_wo_a_grouped(gpu, rows, groups, d, r, dt):
     (100, 1280, 8192, None),      # the indexer's wq_b, a partial 32-row query tile (one range)
     (64, 5120, 1280, 1),          # no split: the kernel stores bf16 itself
     (37, 640, 96, 5),             # odd row count, n a multiple of 32 only
+    (64, 8192, 5120, None),       # wo_b at the C4 batch: 128-row tiles, 4 ranges
+    (48, 1280, 32768, None),      # wq_b at 48 rows: 128-row tiles, one range, partial query tile
+    (64, 2048, 16384, 2),         # 128-row tiles over 2 ranges
+    (64, 5120, 64, None),         # the indexer's weights_proj: 2 tiles x 40 ranges
 ])
 def test_linear_rows(gpu, rows, k, n, splits):
     """dsv41_linear_rows = nn.Linear (x @ w^T) at decode rows: against a float64 product of the
@@ -1346,6 +1350,36 @@ def test_linear_rows(gpu, rows, k, n, splits):
     err = ((got.double() - ref).abs() - ref.abs() * 2.0 ** -8).clamp_min(0) / mag.clamp_min(1e-30)
     assert err.max().item() < 2e-5, f"beyond one bf16 rounding: {err.max().item():.2e} of sum |x w|"
     assert (got != ref.to(torch.bfloat16)).float().mean().item() < 2e-3
+
+
+@pytest.mark.parametrize("rows,k,n0,n1,splits", [
+    (64, 5120, 1280, 512, None),  # wq_a + wkv at the C4 batch (4 ranges)
+    (1, 5120, 1280, 512, None),   # one decode row
+    (37, 640, 96, 64, 5),         # odd row count, widths multiples of 32 only
+    (64, 2048, 8192, 8192, 2),    # 128-row tiles, the boundary between the weights on a tile edge
+    (64, 2048, 8160, 8224, 2),    # a boundary inside a 128-row tile: 32-row tiles instead
+])
+def test_linear_rows_pair(gpu, rows, k, n0, n1, splits):
+    """dsv41_linear_rows_pair (wq_a(x), wkv(x) in one launch): each output bit-identical to
+    dsv41_linear_rows on its own weight with the same ranges, and within one bf16 step of a float64
+    product of the same values."""
+    from dsv41 import _abi
+    g = torch.Generator(device=gpu).manual_seed(SEED_BASE + 11 * rows + k + n0 + 3 * n1)
+    x = torch.randn(rows, k, generator=g, device=gpu).to(torch.bfloat16)
+    w0 = (torch.randn(n0, k, generator=g, device=gpu) * 0.02).to(torch.bfloat16)
+    w1 = (torch.randn(n1, k, generator=g, device=gpu) * 0.02).to(torch.bfloat16)
+    if splits is None:
+        splits = max(_abi.linear_rows_splits(k, n0 + n1, rows), 2)
+    y0, y1 = _abi.linear_rows_pair(x, w0, w1, splits)
+    torch.cuda.synchronize()
+    assert y0.shape == (rows, n0) and y1.shape == (rows, n1)
+    assert torch.equal(y0, _abi.linear_rows(x, w0, splits)), "first output differs from the single call"
+    assert torch.equal(y1, _abi.linear_rows(x, w1, splits)), "second output differs from the single call"
+    for got, w in ((y0, w0), (y1, w1)):
+        ref = x.double() @ w.double().t()
+        mag = x.double().abs() @ w.double().abs().t()
+        err = ((got.double() - ref).abs() - ref.abs() * 2.0 ** -8).clamp_min(0) / mag.clamp_min(1e-30)
+        assert err.max().item() < 2e-5
 
 
 @pytest.mark.parametrize("rows", [1, 4, 300])
