@@ -267,20 +267,52 @@ __device__ __forceinline__ void dequant_rows(uint8_t* sb, const uint8_t* kind, i
 // LDS traffic of a bf16 row), lane l loads the row's bytes for channels 8l..8l+7 and their scale
 // byte into registers when the step is issued; bf16 rows keep their LDS copies. raw/sb hold the
 // wave's RPW rows of the next step, valid for the rows whose kind is 2 or 3.
+//
+// With an MXFP8 ring a list entry is resolved once, by the prologue's parallel pass (reg_row),
+// into the row's code address with the entry's tag in its two low bits (every packed row starts
+// 4-byte aligned) and its scale address; a bf16 or masked entry keeps its entry (tag 0) and gets
+// the zero row as its scale address. A step then spends a few scalar instructions per row:
+// resolving tags and row addresses at issue took ~590 scalar instructions per wave and step, and
+// the CU's waves share one scalar unit (packed C4 1.572-1.580 -> 1.486-1.496 ms). With a bf16
+// ring the per-kind branches below stay cheaper than the second LDS array (C5 1.180-1.182 against
+// 1.193-1.196 ms), so there the entries stay as they are and ms is unused.
+struct RegRow {
+  uint64_t c, s;
+};
+template <int D, int CF>
+__device__ __forceinline__ RegRow reg_row(uint64_t ent, const PackedBase& pb) {
+  using F = CacheFmt<CF>;
+  const uint32_t tag = (uint32_t)ent & 3u;
+  const uint64_t idx = ent >> 2;
+  RegRow r{ent, reinterpret_cast<uint64_t>(g_zero_row)};
+  if ((F::F8 || F::F4) && tag == 1u) {
+    constexpr uint64_t CROW = F::F4 ? (uint64_t)F::F4ROW : (uint64_t)D;
+    const uint64_t row = pb.comp8 + idx * CROW;
+    r.c = row | 1u;
+    r.s = F::F8 ? pb.scal8 + (idx >> pb.rbs) * (D / 32) : row + D / 2;
+  } else if (F::W8 && tag == 2u) {
+    const uint64_t row = pb.ring8 + idx * F::W8ROW;
+    r.c = row | 2u;
+    r.s = row + D;
+  }
+  return r;
+}
+
 template <int D, int CF, int RPW>
-__device__ __forceinline__ void gather_rows_reg(uint64_t mp, uint8_t* kind, uint32_t dst, int lane, const PackedBase& pb,
-                                                uint2 (&raw)[RPW], uint32_t (&sb)[RPW]) {
+__device__ __forceinline__ void gather_rows_reg(uint64_t mc, uint64_t ms, uint8_t* kind, uint32_t dst, int lane,
+                                                const PackedBase& pb, uint2 (&raw)[RPW], uint32_t (&sb)[RPW]) {
   using F = CacheFmt<CF>;
   constexpr int RS = RowLayout<D, false>::RS;
   static_assert(D == 512, "packed rows: 512 channels, 8 per lane");
-  if (lane < RPW) kind[lane] = mp != 0ull ? (uint8_t)(1u + ((uint32_t)mp & 3u)) : 0;
-  const uint32_t lo = (uint32_t)mp, hi = (uint32_t)(mp >> 32);
+  static_assert(F::F4ROW % 4 == 0 && F::W8ROW % 4 == 0, "packed rows start 4-byte aligned: the tag fits below");
+  if (lane < RPW) kind[lane] = mc != 0ull ? (uint8_t)(1u + ((uint32_t)mc & 3u)) : 0;
+  const uint32_t clo = (uint32_t)mc, chi = (uint32_t)(mc >> 32), slo = (uint32_t)ms, shi = (uint32_t)(ms >> 32);
   const uint64_t zero = reinterpret_cast<uint64_t>(g_zero_row);
 #pragma unroll
   for (int rr = 0; rr < RPW; ++rr) {
-    const uint64_t ent = lane_u64(lo, hi, rr);
+    const uint64_t ent = lane_u64(clo, chi, rr);
+    const uint64_t sadr = lane_u64(slo, shi, rr);
     const uint32_t tag = (uint32_t)ent & 3u;
-    const uint64_t idx = ent >> 2;
     if constexpr (F::W8) {
       // With an MXFP8 ring every row issues the same two loads into the same registers (a bf16
       // row reads the zero row and ignores it), from wave-uniform selects: with per-format
@@ -288,22 +320,22 @@ __device__ __forceinline__ void gather_rows_reg(uint64_t mp, uint8_t* kind, uint
       // each load right where it was issued (3 us per 32-row step at B = 64). The scale comes as
       // the dword holding its byte (every scale base is 16-byte aligned): a byte load's
       // zero-extension consumed it at once.
-      const bool is_c = (F::F8 || F::F4) && tag == 1u, is_w = tag == 2u, packed = is_c || is_w;
-      constexpr uint64_t CROW = F::F4 ? (uint64_t)F::F4ROW : (uint64_t)D;
-      const uint64_t cbase = is_c ? pb.comp8 + idx * CROW : (is_w ? pb.ring8 + idx * F::W8ROW : zero);
-      const uint64_t sbase = is_c ? (F::F8 ? pb.scal8 + (idx >> pb.rbs) * (D / 32) : pb.comp8 + idx * CROW + D / 2)
-                                  : (is_w ? pb.ring8 + idx * F::W8ROW + D : zero);
+      const bool packed = tag != 0u, c4 = F::F4 && tag == 1u;
+      const uint64_t cbase = packed ? ent & ~3ull : zero;
       // codes: fp4 lanes read bytes 4l.. (8 bytes, the last 4 unused), fp8 lanes 8l..; scales:
       // fp4 block l/2 (16 channels), fp8 block l/4 (32 channels)
-      const uint32_t coff = !packed ? 0u : (F::F4 && is_c ? (uint32_t)lane * 4u : (uint32_t)lane * 8u);
-      const uint32_t soff = !packed ? 0u : (F::F4 && is_c ? (uint32_t)(lane >> 1) : (uint32_t)(lane >> 2));
+      const uint32_t coff = !packed ? 0u : (c4 ? (uint32_t)lane * 4u : (uint32_t)lane * 8u);
+      const uint32_t soff = !packed ? 0u : (c4 ? (uint32_t)(lane >> 1) : (uint32_t)(lane >> 2));
       const uint64_t v = *reinterpret_cast<const GLOBAL uint64_t*>(cbase + coff);
       raw[rr] = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
-      sb[rr] = *reinterpret_cast<const GLOBAL uint32_t*>((sbase + soff) & ~3ull);
+      sb[rr] = *reinterpret_cast<const GLOBAL uint32_t*>((sadr + soff) & ~3ull);
       if (!packed) dma_row<D>(ent, dst + rr * RS, lane);
     } else {
-      // compressed fp8 or fp4 rows, bf16 ring: one branch per kind (measured faster than the
-      // selects above here: the bf16 window rows issue no dummy loads), the scale byte itself
+      // compressed fp8 or fp4 rows, bf16 ring (entries as list_pos gives them): one branch per
+      // kind (measured faster than the selects above here: the bf16 window rows issue no dummy
+      // loads), the scale byte itself
+      (void)sadr;
+      const uint64_t idx = ent >> 2;
       if (tag == 1u) {
         if constexpr (F::F8) {
           const uint64_t v = *reinterpret_cast<const GLOBAL uint64_t*>(pb.comp8 + idx * D + (uint64_t)lane * 8u);
@@ -362,9 +394,17 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   static_assert(RS == RowLayout<D, false>::RS, "padded row layout");
   __shared__ __align__(16) uint8_t ring[NS * SLOT];
   __shared__ __align__(16) f32x4 xs[NW][2][64];
-  __shared__ uint64_t rows[ML];                 // resolved row addresses, 0 = masked
+  // packed rows through registers: with two slots every step waits for all its loads (vmcnt 0),
+  // so plain loads and the bf16 rows' LDS copies need no separate counts
+  constexpr bool REG = PACKED && NS == 2;
+  constexpr bool PRE = REG && W8;               // entries resolved to row addresses (reg_row)
+  __shared__ uint64_t rows[ML];                 // resolved row addresses, 0 = masked (PRE: reg_row's .c)
+  __shared__ uint64_t rows_s[PRE ? ML : 1];     // PRE: each entry's scale address (reg_row's .s)
   __shared__ __align__(4) uint8_t vrow[NS][R];
   __shared__ float rope_cs[2][kRopeRowPairs];   // the query position's (cos, sin) row of the q rope
+  static_assert(sizeof(ring) + sizeof(xs) + sizeof(rows) + sizeof(rows_s) + sizeof(vrow) + sizeof(rope_cs) <=
+                    (PAIR ? kLdsBudget / 2 : kLdsBudget),
+                "LDS budget (PAIR: two workgroups per CU)");
 
   const KvSrc& S = a.src;
   const int tile = xcd_tile(blockIdx.x, gridDim.x);   // (unit, split, head group), head group fastest
@@ -395,18 +435,23 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   const int nsteps = (cnt + R - 1) / R;
   const uint32_t ring_base = lds_offset(ring);
   const PackedBase pbase = packed_base<CF>(S, b);
-  // packed rows through registers: with two slots every step waits for all its loads (vmcnt 0),
-  // so plain loads and the bf16 rows' LDS copies need no separate counts
-  constexpr bool REG = PACKED && NS == 2;
   uint2 praw[RPW];
   uint32_t psb[RPW];
   auto issue = [&](int t, bool direct) {
     const int slot = t % NS;
     const int mine = t * R + wave * RPW + (lane % RPW);
-    const uint64_t mp = mine < cnt ? (direct ? entry_row(mine) : rows[mine]) : 0ull;
     const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane(ring_base + (uint32_t)(slot * SLOT + wave * RPW * RS));
-    if constexpr (REG) gather_rows_reg<D, CF, RPW>(mp, &vrow[slot][wave * RPW], dst, lane, pbase, praw, psb);
-    else gather_rows<D, CF, RPW, false>(mp, &vrow[slot][wave * RPW], dst, lane, pbase, 0);
+    if constexpr (PRE) {
+      RegRow rr{0ull, reinterpret_cast<uint64_t>(g_zero_row)};
+      if (mine < cnt) rr = direct ? reg_row<D, CF>(entry_row(mine), pbase) : RegRow{rows[mine], rows_s[mine]};
+      gather_rows_reg<D, CF, RPW>(rr.c, rr.s, &vrow[slot][wave * RPW], dst, lane, pbase, praw, psb);
+    } else if constexpr (REG) {
+      const uint64_t mp = mine < cnt ? (direct ? entry_row(mine) : rows[mine]) : 0ull;
+      gather_rows_reg<D, CF, RPW>(mp, 0ull, &vrow[slot][wave * RPW], dst, lane, pbase, praw, psb);
+    } else {
+      const uint64_t mp = mine < cnt ? (direct ? entry_row(mine) : rows[mine]) : 0ull;
+      gather_rows<D, CF, RPW, false>(mp, &vrow[slot][wave * RPW], dst, lane, pbase, 0);
+    }
   };
   const int h = hg * (HT * 16) + ht * 16 + l16;
   const bool hok = h < a.heads;
@@ -447,7 +492,15 @@ __global__ __launch_bounds__(64 * HT * DS, 2) void mla_bf16_kernel(MlaArgs a) {
   if (early) issue(0, true);
   // resolve the split's list once (segment, ring slot, batch row): no global reads are left
   // inside the copy pipeline and a step spends a few instructions per row
-  for (int e = tid; e < cnt; e += NT) rows[e] = entry_row(e);
+  for (int e = tid; e < cnt; e += NT) {
+    if constexpr (PRE) {
+      const RegRow rr = reg_row<D, CF>(entry_row(e), pbase);
+      rows[e] = rr.c;
+      rows_s[e] = rr.s;
+    } else {
+      rows[e] = entry_row(e);
+    }
+  }
 
   f32x4 acc[DTS];
 #pragma unroll
