@@ -247,14 +247,25 @@ static void launch_tiles(const WoaArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((wo_a_tiles_kernel<WR, WM, GR, GM, BK, NS, TO>), dim3((unsigned)tiles), dim3(C::NT), 0, stream, a);
 }
 
-// Split contraction at 33-64 query rows: 128-row weight tiles where each range is long (>= 1024
-// channels) and the tiles fill the chip once (128-256 workgroups). A 32-row tile reads the 64 query
-// rows from L2 for every 32 weight rows it streams, twice the weight's bytes; a 128-row one half of
-// them (measured at 64 rows: wq_b 1280 -> 32768 19.1 us against 21.5 for hipBLASLt, wo_b
-// 8192 -> 5120 in 4 ranges 25.5 against 29.0; 32-row tiles 32.8 us for wo_b).
-__host__ __device__ inline bool wide_split_tiles(int rows, int d, int n, int ranges) {
-  const int64_t t = (int64_t)(n / 128) * ranges;
-  return rows > 32 && rows <= 64 && n % 128 == 0 && d >= 1024 && t >= 128 && t <= 256;
+// Split contraction at 33-64 query rows: 128- or 160-row weight tiles where each range is long
+// (>= 1024 channels) and the tiles fill the chip once (128-256 workgroups; of the two, the one with
+// more workgroups). A 32-row tile reads the 64 query rows from L2 for every 32 weight rows it
+// streams, twice the weight's bytes; a 128-row one half of them (measured at 64 rows: wq_b
+// 1280 -> 32768 19.1 us against 21.5 for hipBLASLt; wo_b 8192 -> 5120 in 4 ranges on 128-row tiles
+// 26.5 us, 160 workgroups, and in 8 ranges on 160-row tiles 23.4-23.8 us, 256 workgroups, against
+// 29.6-30.1 for hipBLASLt; 32-row tiles 32.8 us). Returns the tile's weight rows, 0 for none.
+__host__ __device__ inline int wide_split_tile(int rows, int d, int n, int ranges) {
+  if (rows <= 32 || rows > 64 || d < 1024) return 0;
+  int best = 0;
+  int64_t best_t = 0;
+  for (int tr = 128; tr <= 160; tr += 32) {
+    const int64_t t = (int64_t)(n / tr) * ranges;
+    if (n % tr == 0 && t >= 128 && t <= 256 && t > best_t) {
+      best = tr;
+      best_t = t;
+    }
+  }
+  return best;
 }
 
 template <typename TO>
@@ -263,8 +274,10 @@ static void launch_wo_a(const WoaArgs& a, hipStream_t stream) {
   // eight-stage copy ring (four at 128 rows, whose stage is 20 KB)
   if (a.rows <= 128) {
     const int64_t tiles = (int64_t)a.groups * (a.r / 32);
-    if (a.split && wide_split_tiles(a.rows, a.d, a.r, a.groups) && (a.w1 == nullptr || a.r0 % 128 == 0)) {
-      launch_tiles<4, 2, 2, 2, 64, 4, TO>(a, stream);   // 128 weight rows x 64 query rows, 96 KB
+    const int wide = a.split ? wide_split_tile(a.rows, a.d, a.r, a.groups) : 0;
+    if (wide && (a.w1 == nullptr || a.r0 % wide == 0)) {
+      if (wide == 160) launch_tiles<5, 2, 2, 2, 64, 4, TO>(a, stream);   // 160 x 64 tiles, 112 KB
+      else launch_tiles<4, 2, 2, 2, 64, 4, TO>(a, stream);               // 128 x 64 tiles, 96 KB
       return;
     }
     switch ((a.rows + 31) / 32) {

@@ -525,22 +525,35 @@ def wo_a_grouped(o, wo_a, groups, out=None, out_dtype=None):
     return out
 
 
+def linear_rows_wide_tile(rows: int, k: int, n: int, splits: int) -> int:
+    """The weight rows of dsv41_linear_rows's wide tiles for this call, 0 when it takes the 32-row
+    ones (the kernel's own rule, out_proj.hip wide_split_tile): 33-64 rows, each contraction range
+    at least 1024 channels, and of 128- and 160-row tiles dividing n the one whose n / tile x splits
+    workgroups is largest within 128-256."""
+    if not 32 < rows <= 64 or k // splits < 1024:
+        return 0
+    best, best_t = 0, 0
+    for tr in (128, 160):
+        t = (n // tr) * splits
+        if n % tr == 0 and 128 <= t <= 256 and t > best_t:
+            best, best_t = tr, t
+    return best
+
+
 def linear_rows_wide(rows: int, k: int, n: int, splits: int) -> bool:
-    """Whether dsv41_linear_rows takes its 128-row weight tiles for this call (the kernel's own rule,
-    out_proj.hip wide_split_tiles): 33-64 rows, n a multiple of 128, each contraction range at
-    least 1024 channels, and n / 128 x splits between 128 and 256 workgroups."""
-    t = (n // 128) * splits
-    return 32 < rows <= 64 and n % 128 == 0 and k // splits >= 1024 and 128 <= t <= 256
+    """Whether dsv41_linear_rows takes its wide (128- or 160-row) weight tiles for this call."""
+    return linear_rows_wide_tile(rows, k, n, splits) != 0
 
 
 def linear_rows_splits(k: int, n: int, rows: int = 64) -> int:
     """Contraction ranges for dsv41_linear_rows (whole 64-channel steps, at most 64). At 33-64 rows
-    the most ranges that give the 128-row tiles (linear_rows_wide) when some do; otherwise the most
+    the ranges whose wide tiles (linear_rows_wide) make the most workgroups when some do; otherwise the most
     that keep the n / 32 x ranges workgroups within one wave of the chip (256: one workgroup per
     CU; a 320-workgroup wq_a ran a second round of 64 and took 9.0 us)."""
-    wide = [s for s in range(1, 65) if k % (64 * s) == 0 and linear_rows_wide(rows, k, n, s)]
+    wide = [((n // linear_rows_wide_tile(rows, k, n, s)) * s, s) for s in range(1, 65)
+            if k % (64 * s) == 0 and linear_rows_wide(rows, k, n, s)]
     if wide:
-        return max(wide)
+        return max(wide)[1]                    # the most workgroups, then the most ranges
     tiles = max(n // 32, 1)
     best = 1
     for s in range(1, 65):

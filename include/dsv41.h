@@ -514,7 +514,8 @@ int dsv41_wo_a_grouped(const void* o, const void* wo_a, void* out, int32_t rows,
  * weight w [n, k] as they lie, bf16, y [rows, n] bf16 (fp32 sums rounded once). For rows <= 128
  * the weight is streamed once by the decode tile kernel of dsv41_wo_a_grouped, with the
  * contraction cut into `splits` ranges so that the workgroups fill the chip (n / 32 x splits; at
- * 33-64 rows n / 128 x splits when each range holds >= 1024 channels and that gives 128-256); each
+ * 33-64 rows n / 128 or n / 160 x splits when each range holds >= 1024 channels and that gives
+ * 128-256); each
  * range's fp32 partial goes to `workspace` ([rows, splits * n] floats,
  * dsv41_linear_rows_workspace_bytes; none for splits == 1) and a second kernel sums them in
  * range order: deterministic, equal to the reference up to the order of fp32 additions.

@@ -1326,7 +1326,8 @@ def test_wo_a_grouped(gpu, rows, groups, d, r, dt):
     (100, 1280, 8192, None),      # the indexer's wq_b, a partial 32-row query tile (one range)
     (64, 5120, 1280, 1),          # no split: the kernel stores bf16 itself
     (37, 640, 96, 5),             # odd row count, n a multiple of 32 only
-    (64, 8192, 5120, None),       # wo_b at the C4 batch: 128-row tiles, 4 ranges
+    (64, 8192, 5120, None),       # wo_b at the C4 batch: 160-row tiles, 8 ranges (256 workgroups)
+    (40, 8192, 5120, 4),          # the same on 128-row tiles (4 ranges: 160 workgroups), 40 rows
     (48, 1280, 32768, None),      # wq_b at 48 rows: 128-row tiles, one range, partial query tile
     (64, 2048, 16384, 2),         # 128-row tiles over 2 ranges
     (64, 5120, 64, None),         # the indexer's weights_proj: 2 tiles x 40 ranges
