@@ -426,13 +426,27 @@ def run_wo_a(torch, device):
     8 groups, d = 64 * 512 / 8 = 4096 channels per group, rank 1024 (wo_a 64 MiB of bf16). Rows =
     the decode batch (32, 64) or a prefill chunk (8192). dsv41_wo_a_grouped reads the attention
     output and the weight in place; beside it, in the same run, torch.bmm (hipBLASLt) on operands
-    copied once into its layout ([G, rows, d] x [G, d, r], contiguous) -- the copy not timed."""
+    copied once into its layout ([G, rows, d] x [G, d, r], contiguous) -- the copy not timed. Then
+    wo_b (8192 -> 5120) as torch's linear and, where the attention takes it (33-64 rows), on
+    dsv41_linear_rows. Every form rotates over 4 weight sets (592 MB of wo_a and wo_b weights,
+    beyond the 256 MB Infinity Cache), so the decode rows' weights stream from HBM."""
     from dsv41 import _abi
     G, R, d = 8, 1024, 4096
+    NSET = 4
     g = torch.Generator(device=device).manual_seed(SEED + 300)
     bf = torch.bfloat16
-    w = (torch.randn(G * R, d, generator=g, device=device) * 0.02).to(bf)
-    wT = w.view(G, R, d).transpose(1, 2).contiguous()
+    dim = 5120
+    w = [(torch.randn(G * R, d, generator=g, device=device) * 0.02).to(bf) for _ in range(NSET)]
+    wT = [x.view(G, R, d).transpose(1, 2).contiguous() for x in w]
+    wb = [(torch.randn(dim, G * R, generator=g, device=device) * 0.02).to(bf) for _ in range(NSET)]
+
+    def rot():
+        i = [0]
+
+        def nxt():
+            i[0] = (i[0] + 1) % NSET
+            return i[0]
+        return nxt
 
     def timed(fn, reps):
         fn()
@@ -446,26 +460,37 @@ def run_wo_a(torch, device):
         return e0.elapsed_time(e1) / reps * 1e3     # us
 
     out = {"workload": "grouped wo_a: 8 groups x (4096 -> 1024), bf16 in, fp32 sums, bf16 out; then wo_b "
-                       "(8192 -> 5120, torch linear = hipBLASLt)", "lines": {}}
-    dim = 5120
-    wb = (torch.randn(dim, G * R, generator=g, device=device) * 0.02).to(bf)
+                       "(8192 -> 5120) as torch linear (hipBLASLt) and, at 33-64 rows, on dsv41_linear_rows as the "
+                       "attention runs it; 4 rotating weight sets (592 MB)", "lines": {}}
     for rows in (32, 64, 8192):
         o = torch.randn(rows, G * d, generator=g, device=device).to(bf)
         y = torch.empty(rows, G * R, dtype=bf, device=device)
-        reps = 50 if rows <= 64 else 10
+        reps = 48 if rows <= 64 else 8
         ob = o.view(rows, G, d).transpose(0, 1).contiguous()
-        ours = lambda: _abi.wo_a_grouped(o, w, G, out=y)   # noqa: E731
-        lib = lambda: torch.bmm(ob, wT)                      # noqa: E731
-        lin_b = lambda: torch.nn.functional.linear(y, wb)    # noqa: E731
-        both = lambda: torch.nn.functional.linear(_abi.wo_a_grouped(o, w, G, out=y), wb)   # noqa: E731
+        splits = _abi.linear_rows_splits(G * R, dim, rows)
+        decode_b = _abi.linear_rows_wide(rows, G * R, dim, splits)
+        ra, rl, rb, rd, rab = rot(), rot(), rot(), rot(), rot()
+        ours = lambda: _abi.wo_a_grouped(o, w[ra()], G, out=y)   # noqa: E731
+        lib = lambda: torch.bmm(ob, wT[rl()])                     # noqa: E731
+        lin_b = lambda: torch.nn.functional.linear(y, wb[rb()])   # noqa: E731
+        dec_b = lambda: _abi.linear_rows(y, wb[rd()], splits)     # noqa: E731
+
+        def both():
+            i = rab()
+            ya = _abi.wo_a_grouped(o, w[i], G, out=y)
+            return _abi.linear_rows(ya, wb[i], splits) if decode_b else torch.nn.functional.linear(ya, wb[i])
         # the engine clock ramps up under the first heavy launches: warm every form, then time
         # each twice, alternating, and keep the faster pass of each
-        fns = (ours, lib, lin_b, both)
+        fns = (ours, lib, lin_b, dec_b, both) if decode_b else (ours, lib, lin_b, both)
         for fn in fns:
             timed(fn, reps)
         t = [timed(fn, reps) for fn in fns]
         t = [min(x, timed(fn, reps)) for x, fn in zip(t, fns)]
-        us, us_bmm, us_b, us_ab = t
+        if decode_b:
+            us, us_bmm, us_b, us_db, us_ab = t
+        else:
+            us, us_bmm, us_b, us_ab = t
+            us_db = None
         b_bytes = (dim * G * R + rows * G * R + rows * dim) * 2
         b_flops = 2.0 * rows * dim * G * R
         nbytes = (G * R * d + rows * G * d + rows * G * R) * 2
@@ -473,16 +498,21 @@ def run_wo_a(torch, device):
         line = {"us": us, "GBps": nbytes / us / 1e3, "hbm_frac": nbytes / us / 1e3 / HBM_PEAK_GBS,
                 "TFLOPs": flops / us / 1e6, "mfma_frac": flops / us / 1e6 / BF16_PEAK_TFLOPS,
                 "algorithmic_bytes": nbytes, "flops": flops, "hipblaslt_bmm_pre_transposed_us": us_bmm,
-                # wo_b as the attention runs it (torch linear: hipBLASLt), alone and after wo_a; a
-                # fused pair would save at most the intermediate's write and read
-                "wo_b_us": us_b, "wo_b_GBps": b_bytes / us_b / 1e3, "wo_b_hbm_frac": b_bytes / us_b / 1e3 / HBM_PEAK_GBS,
-                "wo_b_TFLOPs": b_flops / us_b / 1e6, "wo_b_mfma_frac": b_flops / us_b / 1e6 / BF16_PEAK_TFLOPS,
+                # wo_b alone (torch linear, and dsv41_linear_rows where the attention takes it) and
+                # after wo_a as the attention runs the pair; a fused pair would save at most the
+                # intermediate's write and read
+                "wo_b_torch_us": us_b, "wo_b_decode_us": us_db,
+                "wo_b_us": us_db if decode_b else us_b,
                 "wo_b_algorithmic_bytes": b_bytes, "wo_a_then_wo_b_us": us_ab,
                 "intermediate_bytes_frac": 2 * rows * G * R * 2 / (nbytes + b_bytes)}
+        ub = line["wo_b_us"]
+        line.update({"wo_b_GBps": b_bytes / ub / 1e3, "wo_b_hbm_frac": b_bytes / ub / 1e3 / HBM_PEAK_GBS,
+                     "wo_b_TFLOPs": b_flops / ub / 1e6, "wo_b_mfma_frac": b_flops / ub / 1e6 / BF16_PEAK_TFLOPS})
         out["lines"][str(rows)] = line
+        dec = f", on dsv41_linear_rows {us_db:.1f} us" if decode_b else ""
         log(f"[bench] wo_a rows={rows}: {us:.1f} us ({line['GBps']:.0f} GB/s, {line['TFLOPs']:.0f} TFLOP/s), "
-            f"hipBLASLt bmm on transposed copies {us_bmm:.1f} us; wo_b {us_b:.1f} us "
-            f"({line['wo_b_GBps']:.0f} GB/s), wo_a then wo_b {us_ab:.1f} us")
+            f"hipBLASLt bmm on transposed copies {us_bmm:.1f} us; wo_b torch {us_b:.1f} us{dec}; "
+            f"wo_a then wo_b {us_ab:.1f} us")
         del o, y, ob
     return out
 
