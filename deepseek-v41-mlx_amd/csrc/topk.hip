@@ -167,19 +167,21 @@ __global__ __launch_bounds__(kSelThreads) void topk_reg_kernel(const float* __re
 // is among its chunk's best k, so the chunk lists hold the answer. Stage 2 selects the row's k
 // best from the concatenated lists (still in position order, so ties still resolve to the lowest
 // positions), one workgroup per row, keys in registers. Stage 1 spreads a row over
-// ceil(nb / kTopkChunk) workgroups instead of one.
+// ceil(nb / chunk) workgroups instead of one; chunks are kTopkChunk entries, or twice that where
+// k is above an eighth of kTopkChunk (the lists then stay at 4,096 entries per 32K-score row).
 constexpr int kTopkChunk = 4096;
 
+template <int J>   // chunk = J * kSelThreads entries
 __global__ __launch_bounds__(kSelThreads) void topk_chunk_kernel(const float* __restrict__ scores,
                                                                  uint32_t* __restrict__ ckey,
                                                                  int32_t* __restrict__ cpos, int nb, int k,
                                                                  int chunks, int vec) {
-  constexpr int J = kTopkChunk / kSelThreads;
+  constexpr int CH = J * kSelThreads;
   __shared__ RegSelShared sh;
   const int64_t row = blockIdx.x / chunks;
   const int ch = (int)(blockIdx.x - row * chunks);
-  const int base = ch * kTopkChunk;
-  const int count = min(kTopkChunk, nb - base);
+  const int base = ch * CH;
+  const int count = min(CH, nb - base);
   const int kc = min(k, count);
   const float* x = scores + row * nb + base;
   const int64_t cbase = (row * chunks + ch) * (int64_t)k;
@@ -350,12 +352,15 @@ int topk_merge_launch(const char* what, const uint32_t* ckey, const int32_t* cpo
 // on scores already in cache (17.5-19.3 against 19.4-20.2 us), but inside a decode step, reading
 // the scores the scoring kernel has just written, the two stages spread that read over 8
 // workgroups per row and win: the 40-layer fp8 step took 1.163-1.166 ms against 1.190-1.195 ms.
-static bool topk_two_stage(int nb, int k, int* chunks, int* jm) {
+static bool topk_two_stage(int nb, int k, int* chunks, int* jm, int* chunk) {
   if (nb <= 16 * kSelThreads || 2 * k > kTopkChunk) return false;
-  const int c = (nb + kTopkChunk - 1) / kTopkChunk;
+  // lists of more than 4,096 entries per row with 4,096-entry chunks: 8,192-entry chunks halve them
+  const int ch = (int64_t)((nb + kTopkChunk - 1) / kTopkChunk) * k > 4 * kSelThreads ? 2 * kTopkChunk : kTopkChunk;
+  const int c = (nb + ch - 1) / ch;
   const int64_t m = (int64_t)c * k;
   if (m > 32 * kSelThreads) return false;
   *chunks = c;
+  *chunk = ch;
   *jm = m <= 4 * kSelThreads ? 4 : (m <= 8 * kSelThreads ? 8 : (m <= 16 * kSelThreads ? 16 : 32));
   return true;
 }
@@ -377,8 +382,8 @@ static int topk_launch(const char* what, const float* scores, int32_t* out, int6
   if (rows == 0 || k == 0) return 0;
   const dim3 grid((unsigned)rows), block(kSelThreads);
   const int vec = (nb % 4 == 0 && aligned16(scores)) ? 1 : 0;
-  int chunks = 0, jm = 0;
-  if (allow_two_stage && topk_two_stage(nb, k, &chunks, &jm)) {
+  int chunks = 0, jm = 0, chunk = 0;
+  if (allow_two_stage && topk_two_stage(nb, k, &chunks, &jm, &chunk)) {
     const size_t need = topk_ws_bytes(rows, chunks, k);
     DSV41_REQUIRE(workspace && workspace_bytes >= need, DSV41_E_WORKSPACE, "%s: workspace of %zu bytes needed", what,
                   need);
@@ -386,12 +391,15 @@ static int topk_launch(const char* what, const float* scores, int32_t* out, int6
     DSV41_REQUIRE(rows * chunks < (1ll << 31), DSV41_E_ARG, "%s: too many row chunks", what);
     uint32_t* ckey = reinterpret_cast<uint32_t*>(workspace);
     int32_t* cpos = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(workspace) + need / 2);
-    hipLaunchKernelGGL(topk_chunk_kernel, dim3((unsigned)(rows * chunks)), block, 0, stream, scores, ckey, cpos, nb, k,
-                       chunks, vec);
+    if (chunk == kTopkChunk)
+      hipLaunchKernelGGL(topk_chunk_kernel<kTopkChunk / kSelThreads>, dim3((unsigned)(rows * chunks)), block, 0, stream,
+                         scores, ckey, cpos, nb, k, chunks, vec);
+    else
+      hipLaunchKernelGGL(topk_chunk_kernel<2 * kTopkChunk / kSelThreads>, dim3((unsigned)(rows * chunks)), block, 0,
+                         stream, scores, ckey, cpos, nb, k, chunks, vec);
     int rc = check_launch(what);
     if (rc) return rc;
-    return topk_merge_launch(what, ckey, cpos, out, rows, n, nb, k, chunks, kTopkChunk, start_pos, ratio, offset,
-                             stream);
+    return topk_merge_launch(what, ckey, cpos, out, rows, n, nb, k, chunks, chunk, start_pos, ratio, offset, stream);
   }
   if (nb <= 4 * kSelThreads)
     hipLaunchKernelGGL(topk_reg_kernel<4>, grid, block, 0, stream, scores, out, n, nb, k, start_pos, ratio, offset, vec);
@@ -417,8 +425,8 @@ extern "C" int dsv41_topk_select(const float* scores, int32_t* out, int64_t rows
 extern "C" size_t dsv41_topk_workspace_bytes(int64_t rows, int32_t nb, int32_t topk) {
   if (rows <= 0 || nb <= 0 || topk <= 0) return 0;
   const int k = topk < nb ? topk : nb;
-  int chunks = 0, jm = 0;
-  return topk_two_stage(nb, k, &chunks, &jm) ? topk_ws_bytes(rows, chunks, k) : 0;
+  int chunks = 0, jm = 0, chunk = 0;
+  return topk_two_stage(nb, k, &chunks, &jm, &chunk) ? topk_ws_bytes(rows, chunks, k) : 0;
 }
 
 extern "C" int dsv41_topk_select_ws(const float* scores, int32_t* out, int64_t rows, int32_t n, int32_t nb,

@@ -128,8 +128,9 @@ def test_topk_workspace_sizes():
     assert _abi.topk_workspace_bytes(32, 16384, 512) == 0            # one workgroup per row
     assert _abi.topk_workspace_bytes(16, 20000, 5000) == 0           # k above half a chunk
     assert _abi.topk_workspace_bytes(1, 4 << 20, 2048) == 0          # lists too long for one stage-2 group
-    assert _abi.topk_workspace_bytes(16, 32768, 1024) == 2 * 16 * 8 * 1024 * 4   # k = chunk / 4: two stages too
-    assert _abi.topk_workspace_bytes(1, 40000, 1024) == 2 * ((10 * 1024 * 4 + 255) // 256 * 256)   # row > 32K
+    # k above an eighth of a 4,096-entry chunk: 8,192-entry chunks (4 lists of 1,024 per 32K row)
+    assert _abi.topk_workspace_bytes(16, 32768, 1024) == 2 * 16 * 4 * 1024 * 4
+    assert _abi.topk_workspace_bytes(1, 40000, 1024) == 2 * ((5 * 1024 * 4 + 255) // 256 * 256)   # row > 32K
     assert _abi.topk_workspace_bytes(16, 32768, 512) == 2 * 16 * 8 * 512 * 4
     assert _abi.topk_workspace_bytes(3, 16390, 512) == 2 * (((3 * 5 * 512 * 4) + 255) // 256 * 256)
     assert _abi.topk_workspace_bytes(0, 32768, 1024) == 0

@@ -520,11 +520,13 @@ def _score_sets(rng, b, n, nb):
                                                   (1, 2, 300, 512, 1199, 4), (1, 5, 2049, 2048, 8191, 4),
                                                   (1, 2, 32768, 2048, 131071, 4), (1, 3, 5001, 700, 20003, 4),
                                                   (1, 1, 40000, 1000, 159999, 4), (1, 1, 20000, 5000, 79999, 4),
-                                                  (2, 3, 16390, 512, 65559, 4), (1, 2, 20481, 64, 81923, 4)])
+                                                  (2, 3, 16390, 512, 65559, 4), (1, 2, 20481, 64, 81923, 4),
+                                                  (16, 1, 32768, 1024, 131071, 4)])
 def test_topk_bit_exact(gpu, b, n, nb, topk, start, r):
     """Rows over 16384 scores with k <= 2048 take the two-stage form (chunk lists, then a merge);
-    the last two cases give it a last chunk shorter than k and rows that are not 16-byte
-    multiples. The one-stage entry point must agree bit for bit on those rows too."""
+    (2, 3, 16390, ...) and (1, 2, 20481, ...) give it a last chunk shorter than k and rows that are
+    not 16-byte multiples; k above 512 takes 8,192-entry chunks (the 32,768 / 40,000 rows, C5's
+    16 x 32,768 at k = 1,024). The one-stage entry point must agree bit for bit on those rows too."""
     import ctypes
     from dsv41 import _abi
     rng = rng_for(f"topk{nb}{n}")
