@@ -393,18 +393,26 @@ def run_prefill(torch, device):
         _abi.sparse_mla(q, win, chunk, comp, nb, sink, idx_holder["idx"], D ** -0.5, W, prior, cos, sin, rd,
                         out=out)
 
-    res = {}
-    for name, fn in (("indexer_score", f_idx), ("topk_select", f_topk), ("sparse_mla", f_sparse)):
-        fn()
+    def timed(fn, reps=3):
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 3
         e0.record()
         for _ in range(reps):
             fn()
         e1.record()
         torch.cuda.synchronize()
-        res[name] = e0.elapsed_time(e1) / reps
+        return e0.elapsed_time(e1) / reps
+
+    # the engine clock ramps up under the first heavy launches: warm every form (in the pipeline's
+    # order, each reading the previous one's output), then time each twice, alternating, and keep
+    # the faster pass of each
+    fns = (("indexer_score", f_idx), ("topk_select", f_topk), ("sparse_mla", f_sparse))
+    for _, fn in fns:
+        fn()
+    res = {name: timed(fn) for name, fn in fns}
+    for name, fn in fns:
+        res[name] = min(res[name], timed(fn))
+    for name, _ in fns:
         log(f"[bench] prefill {name} {res[name]:.3f} ms")
     rows_sparse = min(W, W + n) + K   # window rows listed per query (<= W valid) + top-k
     fl_idx = 2.0 * Hi * Di * vis
