@@ -892,110 +892,112 @@ __global__ __launch_bounds__(512, 1) void mla_roles_kernel(MlaArgs a) {
   }
 }
 
-// Merges split partials of one query: one wave per head, 4 heads per workgroup; the workgroups
-// of a query are numbered as the attention launch numbers its tiles (xcd_tile), so they read the
-// partials on the XCD whose L2 the attention workgroups wrote them to. Split s holds
-// (m_s, l_s, o_s) = (log2-domain max, denominator, numerator / l_s in bf16); the merged row is
-// sum_s w_s o_s / sum_s w_s with w_s = l_s 2^(m_s - M). Every lane reads every split's
-// (m_s, l_s) (the same addresses across the wave), so the weights need no cross-lane exchange.
-// NB numerator rows and (m, l) pairs (splits clamped to the last one, whose weight past ns is 0)
-// are loaded together before any weight is formed; splits beyond NB are streamed. Each lane
-// covers 8 channels per 512.
+// Merges split partials of one query. The partials lie in 16-head x 16-channel tiles of 512
+// contiguous bytes (part_tile), and the merge reads them in that order: a wave takes two
+// neighbouring channel tiles of one 16-head tile, lane l the 8 channels (l & 1) * 8 .. + 7 of head
+// (l & 31) / 2 in tile l / 32, so each split's read is 1 KB contiguous per wave. (One head per
+// wave read 32-byte pieces 512 bytes apart.) The workgroups of a query are numbered as the
+// attention launch numbers its tiles (xcd_tile), so they read the partials on the XCD whose L2 the
+// attention workgroups wrote them to. Split s holds (m_s, l_s, o_s) = (log2-domain max,
+// denominator, numerator / l_s in bf16); the merged row is sum_s w_s o_s / sum_s w_s with
+// w_s = l_s 2^(m_s - M). NB numerator chunks and (m, l) pairs (splits clamped to the last one,
+// whose weight past ns is 0) are loaded together before any weight is formed; splits beyond NB
+// are streamed.
 template <typename T, int NB>
 __global__ __launch_bounds__(256) void mla_combine_kernel(MlaArgs a) {
-  const int hq = (a.heads + 3) / 4;                          // workgroups per query
+  const int D = a.dim, ns = a.splits;
+  const int htiles = (a.heads + 15) >> 4, dpairs = D >> 5;
+  const int wpu = (htiles * dpairs + 3) >> 2;                  // workgroups per query
   const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  const int unit = tile / hq;
-  const int h = (tile - unit * hq) * 4 + (threadIdx.x >> 6);
+  const int unit = tile / wpu;
   const int lane = threadIdx.x & 63;
+  const int idx = (tile - unit * wpu) * 4 + (threadIdx.x >> 6);   // (head tile, channel-tile pair)
+  if (idx >= htiles * dpairs) return;
+  const int ht = idx / dpairs, dp = idx - ht * dpairs;
+  const int h = ht * 16 + ((lane & 31) >> 1);
+  const int d = (2 * dp + (lane >> 5)) * 16 + (lane & 1) * 8;
   if (h >= a.heads) return;
-  const int D = a.dim, qs = unit % a.m, ns = a.splits;
+  const int qs = unit % a.m;
   const int64_t slot0 = (int64_t)unit * ns * a.heads + h;     // split s: slot0 + s * heads
   T* orow = reinterpret_cast<T*>(a.o) + ((int64_t)unit * a.heads + h) * D;
-  auto part = [&](int s, int d) {
-    return *reinterpret_cast<const uint4*>(a.part_o + part_tile(a, unit, s, h, d));
-  };
-  for (int d = 8 * lane; d < D; d += 512) {
-    // the inverse-rope factors of this lane's pairs are fetched with the partials (unpredicated:
-    // a pair outside the tail reads the table's first pair of its row and ignores it)
-    float cs[4] = {0.f, 0.f, 0.f, 0.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
-    if (a.rd > 0) {
-      const int64_t row = ((int64_t)a.start_pos + qs) * (a.rd >> 1);
+  auto part = [&](int s) { return *reinterpret_cast<const uint4*>(a.part_o + part_tile(a, unit, s, h, d)); };
+  // the inverse-rope factors of this lane's pairs are fetched with the partials (unpredicated:
+  // a pair outside the tail reads the table's first pair of its row and ignores it)
+  float cs[4] = {0.f, 0.f, 0.f, 0.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
+  if (a.rd > 0) {
+    const int64_t row = ((int64_t)a.start_pos + qs) * (a.rd >> 1);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int p = max(d + 2 * j - (D - a.rd), 0) >> 1;
-        cs[j] = a.cos_tab[row + p];
-        sn[j] = a.sin_tab[row + p];
-      }
+    for (int j = 0; j < 4; ++j) {
+      const int p = max(d + 2 * j - (D - a.rd), 0) >> 1;
+      cs[j] = a.cos_tab[row + p];
+      sn[j] = a.sin_tab[row + p];
     }
-    uint4 pv[NB];
+  }
+  uint4 pv[NB];
 #pragma unroll
-    for (int s = 0; s < NB; ++s) pv[s] = part(s < ns ? s : ns - 1, d);
-    // every lane reads every split's (max, denominator) pair (the same addresses across the
-    // wave): the weights need no cross-lane exchange
-    auto ml = [&](int s) { return *reinterpret_cast<const float2*>(a.part_ml + (slot0 + (int64_t)s * a.heads) * 2); };
-    float2 mlv[NB];
+  for (int s = 0; s < NB; ++s) pv[s] = part(s < ns ? s : ns - 1);
+  auto ml = [&](int s) { return *reinterpret_cast<const float2*>(a.part_ml + (slot0 + (int64_t)s * a.heads) * 2); };
+  float2 mlv[NB];
 #pragma unroll
-    for (int s = 0; s < NB; ++s) mlv[s] = ml(s < ns ? s : ns - 1);
-    float M = kNegFloor;
+  for (int s = 0; s < NB; ++s) mlv[s] = ml(s < ns ? s : ns - 1);
+  float M = kNegFloor;
 #pragma unroll
-    for (int s = 0; s < NB; ++s) M = s < ns ? fmaxf(M, mlv[s].x) : M;
-    for (int s = NB; s < ns; ++s) M = fmaxf(M, ml(s).x);
-    float wv[NB], den = 0.0f;
+  for (int s = 0; s < NB; ++s) M = s < ns ? fmaxf(M, mlv[s].x) : M;
+  for (int s = NB; s < ns; ++s) M = fmaxf(M, ml(s).x);
+  float wv[NB], den = 0.0f;
 #pragma unroll
-    for (int s = 0; s < NB; ++s) {
-      wv[s] = s < ns ? mlv[s].y * exp2f(mlv[s].x - M) : 0.0f;
-      den += wv[s];
-    }
-    for (int s = NB; s < ns; ++s) {
-      const float2 v = ml(s);
-      den += v.y * exp2f(v.x - M);
-    }
-    float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    auto add = [&](int s, const uint4& v) {
-      float w;
-      if (s < NB) {
-        w = 0.0f;
+  for (int s = 0; s < NB; ++s) {
+    wv[s] = s < ns ? mlv[s].y * exp2f(mlv[s].x - M) : 0.0f;
+    den += wv[s];
+  }
+  for (int s = NB; s < ns; ++s) {
+    const float2 v = ml(s);
+    den += v.y * exp2f(v.x - M);
+  }
+  float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  auto add = [&](int s, const uint4& v) {
+    float w;
+    if (s < NB) {
+      w = 0.0f;
 #pragma unroll
-        for (int t = 0; t < NB; ++t) w = t == s ? wv[t] : w;
-      } else {
-        const float2 m2 = ml(s);
-        w = m2.y * exp2f(m2.x - M);
-      }
-      const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[2 * i] += w * __uint_as_float(wd[i] << 16);
-        x[2 * i + 1] += w * __uint_as_float(wd[i] & 0xFFFF0000u);
-      }
-    };
-#pragma unroll
-    for (int s = 0; s < NB; ++s) add(s, pv[s]);
-    for (int s = NB; s < ns; ++s) add(s, part(s, d));
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = io<T>::rnd(x[i] / den);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (in_rope_tail(a, D, d + 2 * j)) rope_inv_apply(cs[j], -sn[j], v[2 * j], v[2 * j + 1]);
-    if constexpr (sizeof(T) == 2) {
-      uint4 st;
-      st.x = pack2_bf16(v[0], v[1]);
-      st.y = pack2_bf16(v[2], v[3]);
-      st.z = pack2_bf16(v[4], v[5]);
-      st.w = pack2_bf16(v[6], v[7]);
-      *reinterpret_cast<uint4*>(orow + d) = st;
+      for (int t = 0; t < NB; ++t) w = t == s ? wv[t] : w;
     } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) io<T>::st(orow + d + i, v[i]);
+      const float2 m2 = ml(s);
+      w = m2.y * exp2f(m2.x - M);
     }
+    const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] += w * __uint_as_float(wd[i] << 16);
+      x[2 * i + 1] += w * __uint_as_float(wd[i] & 0xFFFF0000u);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < NB; ++s) add(s, pv[s]);
+  for (int s = NB; s < ns; ++s) add(s, part(s));
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = io<T>::rnd(x[i] / den);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (in_rope_tail(a, D, d + 2 * j)) rope_inv_apply(cs[j], -sn[j], v[2 * j], v[2 * j + 1]);
+  if constexpr (sizeof(T) == 2) {
+    uint4 st;
+    st.x = pack2_bf16(v[0], v[1]);
+    st.y = pack2_bf16(v[2], v[3]);
+    st.z = pack2_bf16(v[4], v[5]);
+    st.w = pack2_bf16(v[6], v[7]);
+    *reinterpret_cast<uint4*>(orow + d) = st;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) io<T>::st(orow + d + i, v[i]);
   }
 }
 
 template <int NB>
 static void launch_combine(const MlaArgs& a, int64_t units, hipStream_t stream) {
-  hipLaunchKernelGGL((mla_combine_kernel<bf16_t, NB>), dim3((unsigned)(units * ((a.heads + 3) / 4))), dim3(256), 0,
-                     stream, a);
+  const int wpu = (((a.heads + 15) >> 4) * (a.dim >> 5) + 3) >> 2;   // workgroups per query
+  hipLaunchKernelGGL((mla_combine_kernel<bf16_t, NB>), dim3((unsigned)(units * wpu)), dim3(256), 0, stream, a);
 }
 
 // fp32: 4 heads x 16 rows per step, plain FMA, natural-log softmax with the reference's form.
