@@ -248,17 +248,17 @@ def run_decode(args, torch, device):
         kern = {k: float("nan") for k in ("indexer_topk", "indexer_score", "topk_select", "sparse_mla")}
         return s, ms, kern, sets, cos, sin, ws, [], []
     # exactly `warmup` untimed steps, then exactly `steps` timed steps, each graph cycling through
-    # the input sets in order
-    if args.warmup > 0:
-        g_warm = graph_of(full, [sets[i % per_replay] for i in range(args.warmup)], torch)
-        g_warm.replay()
-        torch.cuda.synchronize()
-        del g_warm
+    # the input sets in order. Both graphs are captured first (the timed one uploaded, no step
+    # run), so the warm-up steps run right before the timed ones: a capture between them leaves
+    # the GPU idle for tens of milliseconds, and the timed replay would start at a lower engine
+    # clock. Later replays of the same graph, beside it, show what first-launch cost is left.
+    g_warm = graph_of(full, [sets[i % per_replay] for i in range(args.warmup)], torch) if args.warmup > 0 else None
     g_full = graph_of(full, [sets[i % per_replay] for i in range(args.steps)], torch)
-    # uploaded before its one timed replay (no step runs); later replays of the same graph, beside
-    # it, show what first-launch cost is left in the figure
     up = upload_graph(g_full, torch)
+    if g_warm is not None:
+        g_warm.replay()
     ms = time_graph(g_full, 1, torch) / args.steps
+    del g_warm
     later = [time_graph(g_full, 1, torch) / args.steps for _ in range(4)]
     log(f"[bench] decode step {ms * 1e3:.2f} us ({args.steps} steps, {args.warmup} warm-up, graph upload "
         f"{'ok' if up == 0 else f'status {up}'}); later replays "
