@@ -612,6 +612,8 @@ def _concat_reference(win, chunk, comp, n_comp, start, window):
     ("bf16", 32, 1, 64, 512, 128, 16383, 4096, 512),
     ("bf16", 1, 40, 64, 512, 16, 100, 35, 24),
     ("bf16", 2, 1, 64, 512, 128, 5, 0, 0),        # window only, ring still filling
+    ("bf16", 3, 1, 64, 512, 128, 0, 0, 0),        # the first token: an empty ring, its own row and the sink
+    ("f32", 2, 1, 4, 64, 8, 0, 0, 0),
     ("bf16", 1, 600, 64, 512, 16, 200, 150, 64),  # >= 512 queries: the 64-head two-role prefill kernel
     ("bf16", 2, 300, 96, 512, 128, 1000, 300, 128),   # 96 heads: its second workgroup has one idle tile
     ("bf16", 2, 300, 64, 512, 128, 1000, 300, 128),   # two batch rows through the two-role kernel
